@@ -1,0 +1,545 @@
+// gfx950 kernels and the C ABI of libcugo_hip.so (declared in include/cugo_hip.h).
+//
+// Every row kernel works on tiles of 64 games with one 64-lane wavefront per
+// workgroup.  The tile's 248-byte rows move between HBM and LDS with coalesced 8-byte
+// accesses (consecutive lanes touch consecutive words, also for gathered rows, whose
+// 31 words are contiguous), and each lane then runs one game in registers.  The
+// observation is the widest output (2,880 + 179 bytes per row): lanes first build a
+// compact per-row feature record in LDS, then the wavefront writes the feature rows as
+// consecutive float4 stores and the legal-mask rows as consecutive 32-bit words, so
+// every output byte is written once, in order.
+#include <hip/hip_runtime.h>
+
+#include "engine.h"
+#include "../../include/cugo_hip.h"
+
+namespace cugo_amd {
+
+constexpr int kTile = 64;
+constexpr int kTileWords = kTile * kRowWords;  // 1,984
+
+// log2f(1 + p) / 12 clamped to 1 for p < 4095 (torch50.h:405-408), generated at build
+// time with the host C library's log2f, so the values are the reference engine's own.
+__constant__ float c_stop_bits[kStopBitsTable] = {
+#include "stop_bits.inc"
+};
+
+__device__ inline i64 tile_base() { return (i64)blockIdx.x * kTile; }
+
+__device__ inline int tile_count(i64 base, i64 n) {
+  const i64 left = n - base;
+  return left < kTile ? (int)left : kTile;
+}
+
+__device__ inline bool valid_id(i64 id, i64 env_count) { return id >= 0 && id < env_count; }
+
+// Loads the tile's rows into LDS; src row r is `ids[r]` (gathered, zero row when the id
+// is invalid) or base + r (contiguous) when ids_lds is null.
+__device__ inline void stage_in(u64* lds, const u64* states, const i64* ids_lds, i64 base,
+                                int count, i64 env_count) {
+  const int words = count * kRowWords;
+  if (ids_lds == nullptr) {
+    const u64* src = states + base * kRowWords;
+    for (int j = threadIdx.x; j < words; j += kTile) lds[j] = src[j];
+  } else {
+    for (int j = threadIdx.x; j < words; j += kTile) {
+      const int r = j / kRowWords;
+      const int k = j - r * kRowWords;
+      const i64 id = ids_lds[r];
+      lds[j] = valid_id(id, env_count) ? states[id * kRowWords + k] : 0ull;
+    }
+  }
+}
+
+// Stores the tile's rows from LDS: to dst rows base + r (contiguous) or, when ids_lds
+// is given, to rows ids[r] with a valid id (scatter, in place).
+__device__ inline void stage_out(const u64* lds, u64* dst, const i64* ids_lds, i64 base,
+                                 int count, i64 env_count) {
+  const int words = count * kRowWords;
+  if (ids_lds == nullptr) {
+    u64* out = dst + base * kRowWords;
+    for (int j = threadIdx.x; j < words; j += kTile) out[j] = lds[j];
+  } else {
+    for (int j = threadIdx.x; j < words; j += kTile) {
+      const int r = j / kRowWords;
+      const int k = j - r * kRowWords;
+      const i64 id = ids_lds[r];
+      if (valid_id(id, env_count)) dst[id * kRowWords + k] = lds[j];
+    }
+  }
+}
+
+__device__ inline u16 clamp_action(i64 raw) {  // torch50_ext.cu:96-99
+  return raw >= 0 && raw < kActionCount ? (u16)raw : kInvalidAction16;
+}
+
+// ------------------------------------------------------------------- create ----
+__global__ __launch_bounds__(kTile) void create_kernel(const i64* seeds, const i64* first,
+                                                       i64 n, u64* states) {
+  __shared__ u64 rows[kTileWords];
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int lane = threadIdx.x;
+  if (lane < count) {
+    const Env e = create_env((u64)seeds[base + lane], (u32)(first[base + lane] & 1));
+    pack_row(e, rows + lane * kRowWords);
+  }
+  __syncthreads();
+  stage_out(rows, states, nullptr, base, count, 0);
+}
+
+// ------------------------------------------------------------------ observe ----
+struct FeatTile {
+  u64 w[kTile][kFeatWords];
+  float d[kTile][kFeatDense];
+  u64 legal[kTile][3];
+};
+
+template <bool kIndexed>
+__global__ __launch_bounds__(kTile) void observe_kernel(const u64* states, i64 env_count,
+                                                        const i64* ids, i64 n, float* features,
+                                                        u8* legal, u8* player, u8* done,
+                                                        i16* status) {
+  __shared__ u64 rows[kTileWords];
+  __shared__ i64 tile_ids[kTile];
+  __shared__ FeatTile ft;
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int lane = threadIdx.x;
+  if (kIndexed && lane < count) tile_ids[lane] = ids[base + lane];
+  __syncthreads();
+  stage_in(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
+  __syncthreads();
+  if (lane < count) {
+    const i64 i = base + lane;
+    const bool ok = !kIndexed || valid_id(tile_ids[lane], env_count);
+    FeatRow fr;
+    if (ok) {
+      const Env e = unpack_row(rows + lane * kRowWords);
+      const Packet pk = make_packet(e);
+      feature_row(pk, c_stop_bits, fr);
+      ft.legal[lane][0] = pk.head.legal.w0;
+      ft.legal[lane][1] = pk.head.legal.w1;
+      ft.legal[lane][2] = pk.head.legal.w2;
+      player[i] = pk.head.player;
+      done[i] = e.done != 0;
+      status[i] = (i16)pk.head.status;
+    } else {  // torch50_ext.cu:71-87
+      for (int k = 0; k < kFeatWords; ++k) fr.w[k] = 0;
+      for (int k = 0; k < kFeatDense; ++k) fr.d[k] = 0.0f;
+      ft.legal[lane][0] = ft.legal[lane][1] = ft.legal[lane][2] = 0;
+      player[i] = 0;
+      done[i] = 1;
+      status[i] = CUGO_INVALID_INDEX_STATUS;
+    }
+    for (int k = 0; k < kFeatWords; ++k) ft.w[lane][k] = fr.w[k];
+    for (int k = 0; k < kFeatDense; ++k) ft.d[lane][k] = fr.d[k];
+  }
+  __syncthreads();
+  // Features: count rows x 180 float4, consecutive lanes -> consecutive float4.
+  float4* fout = reinterpret_cast<float4*>(features + base * kFeatureCount);
+  const int quads = count * (kFeatureCount / 4);
+  for (int q = lane; q < quads; q += kTile) {
+    const int r = q / (kFeatureCount / 4);
+    const u32 f = (u32)(q - r * (kFeatureCount / 4)) * 4u;
+    float4 v;
+    v.x = feature_at(ft.w[r], ft.d[r], f);
+    v.y = feature_at(ft.w[r], ft.d[r], f + 1);
+    v.z = feature_at(ft.w[r], ft.d[r], f + 2);
+    v.w = feature_at(ft.w[r], ft.d[r], f + 3);
+    fout[q] = v;
+  }
+  // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0).
+  u8* lout = legal + base * kActionCount;
+  const int bytes = count * kActionCount;
+  const int full = bytes / 4;
+  for (int w = lane; w < full; w += kTile) {
+    u32 packed = 0;
+    for (int b = 0; b < 4; ++b) {
+      const int at = w * 4 + b;
+      const int r = at / kActionCount;
+      const int a = at - r * kActionCount;
+      const u64 word = ft.legal[r][a >> 6];
+      packed |= (u32)((word >> (a & 63)) & 1u) << (8 * b);
+    }
+    reinterpret_cast<u32*>(lout)[w] = packed;
+  }
+  for (int at = full * 4 + lane; at < bytes; at += kTile) {
+    const int r = at / kActionCount;
+    const int a = at - r * kActionCount;
+    lout[at] = (u8)((ft.legal[r][a >> 6] >> (a & 63)) & 1u);
+  }
+}
+
+// --------------------------------------------------------------------- step ----
+// kMode: 0 = step (contiguous, in place), 1 = step_indexed (gather/scatter in place),
+// 2 = branch_indexed (gather from parents, children written contiguously).
+template <int kMode, bool kEvents>
+__global__ __launch_bounds__(kTile) void step_kernel(u64* states, i64 env_count, const i64* ids,
+                                                     const i64* actions, i64 n, u64* children,
+                                                     float* reward, u8* done, u8* nagari,
+                                                     i16* status, u8* committed, i64* events) {
+  __shared__ u64 rows[kTileWords];
+  __shared__ i64 tile_ids[kTile];
+  __shared__ i64 ev[kTile * kEventWords];
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int lane = threadIdx.x;
+  constexpr bool kIndexed = kMode != 0;
+  if (kIndexed && lane < count) tile_ids[lane] = ids[base + lane];
+  __syncthreads();
+  stage_in(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
+  __syncthreads();
+  if (lane < count) {
+    const i64 i = base + lane;
+    const bool ok = !kIndexed || valid_id(tile_ids[lane], env_count);
+    u64* row = rows + lane * kRowWords;
+    i64* evr = ev + lane * kEventWords;
+    if (ok) {
+      Env e = unpack_row(row);
+      const StepOut so = torch_step(e, clamp_action(actions[i]));
+      if (kEvents) {
+        if (so.committed) {
+          // make_torch_event50 against the untouched row still in LDS
+          Env before;
+          before.hand0 = row[0]; before.hand1 = row[1]; before.stock = row[3];
+          before.cap0 = row[4]; before.cap1 = row[5]; before.rev0 = row[22];
+          before.rev1 = row[23];
+          make_event(before, e, evr);
+        } else {
+          for (int k = 0; k < kEventWords; ++k) evr[k] = 0;
+        }
+      }
+      pack_row(e, row);
+      reward[i] = (float)so.reward0;
+      done[i] = so.done;
+      nagari[i] = so.nagari;
+      status[i] = (i16)so.status;
+      committed[i] = so.committed;
+    } else {  // torch50_ext.cu:108-118
+      if (kEvents) for (int k = 0; k < kEventWords; ++k) evr[k] = 0;
+      if (kMode == 2) for (int k = 0; k < kRowWords; ++k) row[k] = 0;
+      reward[i] = 0.0f;
+      done[i] = 1;
+      nagari[i] = 0;
+      status[i] = CUGO_INVALID_INDEX_STATUS;
+      committed[i] = 0;
+    }
+  }
+  __syncthreads();
+  if (kMode == 0) stage_out(rows, states, nullptr, base, count, env_count);
+  else if (kMode == 1) stage_out(rows, states, tile_ids, base, count, env_count);
+  else stage_out(rows, children, nullptr, base, count, env_count);
+  if (kEvents) {
+    i64* eout = events + base * kEventWords;
+    for (int j = lane; j < count * kEventWords; j += kTile) eout[j] = ev[j];
+  }
+}
+
+// -------------------------------------------------------------------- small ----
+__global__ __launch_bounds__(256) void start_kernel(const u64* states, i64 n, i64* out) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const u64* w = states + i * kRowWords;
+  Env e;
+  e.hand0 = w[0]; e.hand1 = w[1]; e.floor = w[2]; e.cap0 = w[4]; e.cap1 = w[5];
+  e.mission = w[10]; e.neutral = (u16)w[11]; e.actor = (u8)(w[9] >> 16);
+  e.mtype = (u8)(w[18] >> 40); e.mmult = (u8)(w[18] >> 48); e.mm0 = (u8)(w[18] >> 56);
+  e.mm1 = (u8)w[19];
+  i64 o[kStartWords];
+  pack_start(e, o);
+  for (int k = 0; k < kStartWords; ++k) out[i * kStartWords + k] = o[k];
+}
+
+// One 8-byte word per lane: word j of the output is word j % 31 of row j / 31.
+__global__ __launch_bounds__(256) void clone_kernel(const u64* states, i64 env_count,
+                                                    const i64* ids, i64 n, u64* children) {
+  const i64 words = n * kRowWords;
+  for (i64 j = (i64)blockIdx.x * blockDim.x + threadIdx.x; j < words;
+       j += (i64)gridDim.x * blockDim.x) {
+    const i64 r = j / kRowWords;
+    const i64 k = j - r * kRowWords;
+    const i64 id = ids[r];
+    children[j] = valid_id(id, env_count) ? states[id * kRowWords + k] : 0ull;
+  }
+}
+
+__global__ __launch_bounds__(256) void hands_kernel(const u64* states, i64 env_count,
+                                                    const i64* ids, i64 n, i64* hands) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const i64 id = ids[i];
+  const bool ok = valid_id(id, env_count);
+  hands[2 * i] = ok ? (i64)states[id * kRowWords + 0] : 0;
+  hands[2 * i + 1] = ok ? (i64)states[id * kRowWords + 1] : 0;
+}
+
+__global__ __launch_bounds__(256) void stock_kernel(const u64* states, i64 env_count,
+                                                    const i64* ids, i64 n, i64* stock) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const i64 id = ids[i];
+  u64 packed = ~0ull;
+  if (valid_id(id, env_count)) {
+    Env e;
+    e.stock = states[id * kRowWords + 3];
+    e.rng = states[id * kRowWords + 6];
+    packed = peek_stock(e);
+  }
+  stock[i] = (i64)packed;
+}
+
+// ------------------------------------------------------- random-policy driver ----
+__device__ inline u64 xorshift64(u64& x) {
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  return x;
+}
+
+__device__ inline u64 sampler_seed(u64 seed) {
+  u64 s = seed;
+  const u64 v = sm_next(s);
+  return v != 0 ? v : 1ull;
+}
+
+// Tile of 64 mask rows staged in LDS as bytes; lane r scans its row.
+__global__ __launch_bounds__(kTile) void sample_kernel(const u8* legal, i64 n, u64* sampler,
+                                                       i64* actions) {
+  __shared__ u32 masks[kTile * kActionCount / 4];
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int lane = threadIdx.x;
+  const u8* src = legal + base * kActionCount;
+  const int bytes = count * kActionCount;
+  const int full = bytes / 4;
+  for (int w = lane; w < full; w += kTile) masks[w] = reinterpret_cast<const u32*>(src)[w];
+  u8* mb = reinterpret_cast<u8*>(masks);
+  for (int at = full * 4 + lane; at < bytes; at += kTile) mb[at] = src[at];
+  __syncthreads();
+  if (lane >= count) return;
+  const u8* row = mb + lane * kActionCount;
+  u32 total = 0;
+  for (int a = 0; a < kActionCount; ++a) total += row[a] != 0;
+  const i64 i = base + lane;
+  if (total == 0) { actions[i] = -1; return; }
+  u64 x = sampler[i];
+  u32 pick = (u32)(xorshift64(x) % total);
+  sampler[i] = x;
+  int chosen = -1;
+  for (int a = 0; a < kActionCount; ++a) {
+    if (row[a] != 0) {
+      if (pick == 0) { chosen = a; break; }
+      --pick;
+    }
+  }
+  actions[i] = chosen;
+}
+
+__global__ __launch_bounds__(kTile) void reset_kernel(u64* states, const u8* done, i64 n,
+                                                      u64 base_seed, u32* generation,
+                                                      u64* sampler,
+                                                      unsigned long long* completed) {
+  __shared__ u64 rows[kTileWords];
+  __shared__ int flags[kTile];
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int lane = threadIdx.x;
+  const bool reset = lane < count && done[base + lane] != 0;
+  flags[lane] = reset;
+  if (reset) {
+    const i64 i = base + lane;
+    const u32 gen = generation[i] + 1u;
+    generation[i] = gen;
+    const u64 seed = base_seed + (u64)i + (u64)n * gen;
+    const Env e = create_env(seed, (u32)(i & 1));
+    pack_row(e, rows + lane * kRowWords);
+    sampler[i] = sampler_seed(seed);
+  }
+  const u64 ballot = __ballot(reset);
+  if (lane == 0 && ballot != 0) atomicAdd(completed, (unsigned long long)__popcll(ballot));
+  __syncthreads();
+  u64* out = states + base * kRowWords;
+  for (int j = lane; j < count * kRowWords; j += kTile)
+    if (flags[j / kRowWords]) out[j] = rows[j];
+}
+
+__global__ __launch_bounds__(256) void seed_kernel(i64 n, u64 base_seed, const u32* generation,
+                                                   u64* sampler) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const u64 gen = generation != nullptr ? generation[i] : 0u;
+  sampler[i] = sampler_seed(base_seed + (u64)i + (u64)n * gen);
+}
+
+}  // namespace cugo_amd
+
+// ===================================================================== C ABI ====
+using namespace cugo_amd;
+
+namespace {
+inline unsigned tiles(int64_t n) { return (unsigned)((n + kTile - 1) / kTile); }
+inline unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
+inline int launched() { return (int)hipGetLastError(); }
+constexpr int kBadArgument = -22;
+}  // namespace
+
+extern "C" {
+
+int cugo_version(void) { return (1 << 16) | 0; }
+
+int cugo_create(const int64_t* seeds, const int64_t* first, int64_t n, uint8_t* states,
+                hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!seeds || !first || !states))) return kBadArgument;
+  if (n == 0) return 0;
+  create_kernel<<<tiles(n), kTile, 0, stream>>>(seeds, first, n,
+                                                reinterpret_cast<u64*>(states));
+  return launched();
+}
+
+int cugo_observe(const uint8_t* states, int64_t n, float* features, uint8_t* legal,
+                 uint8_t* player, uint8_t* done, int16_t* status, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!states || !features || !legal || !player || !done || !status)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  observe_kernel<false><<<tiles(n), kTile, 0, stream>>>(
+      reinterpret_cast<const u64*>(states), n, nullptr, n, features, legal, player, done,
+      status);
+  return launched();
+}
+
+int cugo_observe_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids,
+                         int64_t n, float* features, uint8_t* legal, uint8_t* player,
+                         uint8_t* done, int16_t* status, hipStream_t stream) {
+  if (n < 0 || env_count < 0 ||
+      (n > 0 && (!ids || !features || !legal || !player || !done || !status)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  observe_kernel<true><<<tiles(n), kTile, 0, stream>>>(
+      reinterpret_cast<const u64*>(states), env_count, ids, n, features, legal, player, done,
+      status);
+  return launched();
+}
+
+int cugo_step(uint8_t* states, const int64_t* actions, int64_t n, float* reward, uint8_t* done,
+              uint8_t* nagari, int16_t* status, uint8_t* committed, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!states || !actions || !reward || !done || !nagari || !status ||
+                          !committed)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  step_kernel<0, false><<<tiles(n), kTile, 0, stream>>>(
+      reinterpret_cast<u64*>(states), n, nullptr, actions, n, nullptr, reward, done, nagari,
+      status, committed, nullptr);
+  return launched();
+}
+
+int cugo_step_indexed(uint8_t* states, int64_t env_count, const int64_t* ids,
+                      const int64_t* actions, int64_t n, float* reward, uint8_t* done,
+                      uint8_t* nagari, int16_t* status, uint8_t* committed,
+                      hipStream_t stream) {
+  if (n < 0 || env_count < 0 ||
+      (n > 0 && (!ids || !actions || !reward || !done || !nagari || !status || !committed)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  step_kernel<1, false><<<tiles(n), kTile, 0, stream>>>(
+      reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
+      nagari, status, committed, nullptr);
+  return launched();
+}
+
+int cugo_step_events_indexed(uint8_t* states, int64_t env_count, const int64_t* ids,
+                             const int64_t* actions, int64_t n, float* reward, uint8_t* done,
+                             uint8_t* nagari, int16_t* status, uint8_t* committed,
+                             int64_t* events, hipStream_t stream) {
+  if (n < 0 || env_count < 0 ||
+      (n > 0 && (!ids || !actions || !reward || !done || !nagari || !status || !committed ||
+                 !events)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  step_kernel<1, true><<<tiles(n), kTile, 0, stream>>>(
+      reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
+      nagari, status, committed, events);
+  return launched();
+}
+
+int cugo_start(const uint8_t* states, int64_t n, int64_t* out, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!states || !out))) return kBadArgument;
+  if (n == 0) return 0;
+  start_kernel<<<blocks256(n), 256, 0, stream>>>(reinterpret_cast<const u64*>(states), n, out);
+  return launched();
+}
+
+int cugo_clone_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids, int64_t n,
+                       uint8_t* children, hipStream_t stream) {
+  if (n < 0 || env_count < 0 || (n > 0 && (!ids || !children))) return kBadArgument;
+  if (n == 0) return 0;
+  const int64_t words = n * kRowWords;
+  int64_t grid = (words + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  clone_kernel<<<(unsigned)grid, 256, 0, stream>>>(reinterpret_cast<const u64*>(states),
+                                                   env_count, ids, n,
+                                                   reinterpret_cast<u64*>(children));
+  return launched();
+}
+
+int cugo_branch_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids,
+                        const int64_t* actions, int64_t n, uint8_t* children, float* reward,
+                        uint8_t* done, uint8_t* nagari, int16_t* status, uint8_t* committed,
+                        hipStream_t stream) {
+  if (n < 0 || env_count < 0 ||
+      (n > 0 && (!ids || !actions || !children || !reward || !done || !nagari || !status ||
+                 !committed)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  step_kernel<2, false><<<tiles(n), kTile, 0, stream>>>(
+      const_cast<u64*>(reinterpret_cast<const u64*>(states)), env_count, ids, actions, n,
+      reinterpret_cast<u64*>(children), reward, done, nagari, status, committed, nullptr);
+  return launched();
+}
+
+int cugo_hands_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids, int64_t n,
+                       int64_t* hands, hipStream_t stream) {
+  if (n < 0 || env_count < 0 || (n > 0 && (!ids || !hands))) return kBadArgument;
+  if (n == 0) return 0;
+  hands_kernel<<<blocks256(n), 256, 0, stream>>>(reinterpret_cast<const u64*>(states),
+                                                 env_count, ids, n, hands);
+  return launched();
+}
+
+int cugo_stock_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids, int64_t n,
+                       int64_t* stock, hipStream_t stream) {
+  if (n < 0 || env_count < 0 || (n > 0 && (!ids || !stock))) return kBadArgument;
+  if (n == 0) return 0;
+  stock_kernel<<<blocks256(n), 256, 0, stream>>>(reinterpret_cast<const u64*>(states),
+                                                 env_count, ids, n, stock);
+  return launched();
+}
+
+int cugo_sample_uniform(const uint8_t* legal, int64_t n, uint64_t* sampler, int64_t* actions,
+                        hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!legal || !sampler || !actions))) return kBadArgument;
+  if (n == 0) return 0;
+  sample_kernel<<<tiles(n), kTile, 0, stream>>>(legal, n, sampler, actions);
+  return launched();
+}
+
+int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
+                    uint32_t* generation, uint64_t* sampler, unsigned long long* completed,
+                    hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!states || !done || !generation || !sampler || !completed)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  reset_kernel<<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<u64*>(states), done, n,
+                                               base_seed, generation, sampler, completed);
+  return launched();
+}
+
+int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation,
+                       uint64_t* sampler, hipStream_t stream) {
+  if (n < 0 || (n > 0 && !sampler)) return kBadArgument;
+  if (n == 0) return 0;
+  seed_kernel<<<blocks256(n), 256, 0, stream>>>(n, base_seed, generation, sampler);
+  return launched();
+}
+
+}  // extern "C"

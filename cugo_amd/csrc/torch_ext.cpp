@@ -1,0 +1,307 @@
+// PyTorch-ROCm extension `cugo_torch50_ext`: the reference module's operations
+// (python/csrc/torch50_ext.cpp:36-72) over the C ABI of libcugo_hip.so.
+//
+// Each operation checks its tensors like the reference (torch50_ext.cu:26-51, same
+// messages), allocates the outputs with torch::empty on the states' device, and calls
+// the C ABI on the current HIP stream.  Nothing here synchronises, so the operations
+// can be captured in HIP graphs.
+#include <torch/extension.h>
+
+// PyTorch-ROCm keeps torch's device type "cuda" for HIP devices; these are its native
+// HIP guard and stream accessors for that device type.
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <cstdint>
+#include <vector>
+
+#include "../../include/cugo_hip.h"
+
+namespace {
+
+void check_1d(const torch::Tensor& t, at::ScalarType dtype, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK(t.dim() == 1, name, " must be one-dimensional");
+  TORCH_CHECK(t.scalar_type() == dtype, name, " has the wrong dtype");
+}
+
+void check_states(const torch::Tensor& s) {
+  TORCH_CHECK(s.is_cuda(), "states must be a CUDA tensor");
+  TORCH_CHECK(s.is_contiguous(), "states must be contiguous");
+  TORCH_CHECK(s.scalar_type() == at::kByte, "states must have dtype torch.uint8");
+  TORCH_CHECK(s.dim() == 2, "states must have shape [N, STATE_BYTES]");
+  TORCH_CHECK(s.size(1) == CUGO_STATE_BYTES, "states second dimension must equal STATE_BYTES");
+  TORCH_CHECK(reinterpret_cast<std::uintptr_t>(s.data_ptr()) % 8 == 0,
+              "states must be 8-byte aligned");
+}
+
+void check_same_device(const torch::Tensor& a, const torch::Tensor& b, const char* an,
+                       const char* bn) {
+  TORCH_CHECK(a.device() == b.device(), an, " and ", bn, " must be on the same CUDA device");
+}
+
+void check_call(int rc, const char* op) {
+  TORCH_CHECK(rc == 0, "cugo_hip ", op, " failed with code ", rc);
+}
+
+hipStream_t stream() { return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream(); }
+
+using DeviceGuard = c10::hip::HIPGuardMasqueradingAsCUDA;
+
+torch::TensorOptions on(const torch::Tensor& t, at::ScalarType dtype) {
+  return torch::TensorOptions().device(t.device()).dtype(dtype);
+}
+
+std::vector<torch::Tensor> observation_outputs(int64_t n, const torch::Tensor& like) {
+  return {torch::empty({n, CUGO_FEATURE_COUNT}, on(like, at::kFloat)),
+          torch::empty({n, CUGO_ACTION_COUNT}, on(like, at::kBool)),
+          torch::empty({n}, on(like, at::kByte)), torch::empty({n}, on(like, at::kBool)),
+          torch::empty({n}, on(like, at::kShort))};
+}
+
+std::vector<torch::Tensor> step_outputs(int64_t n, const torch::Tensor& like) {
+  return {torch::empty({n}, on(like, at::kFloat)), torch::empty({n}, on(like, at::kBool)),
+          torch::empty({n}, on(like, at::kBool)), torch::empty({n}, on(like, at::kShort)),
+          torch::empty({n}, on(like, at::kBool))};
+}
+
+uint8_t* u8p(const torch::Tensor& t) { return reinterpret_cast<uint8_t*>(t.data_ptr()); }
+
+torch::Tensor create(torch::Tensor seeds, torch::Tensor first) {
+  check_1d(seeds, at::kLong, "seeds");
+  check_1d(first, at::kLong, "first_players");
+  TORCH_CHECK(seeds.numel() == first.numel(),
+              "seeds and first_players must have the same length");
+  check_same_device(seeds, first, "seeds", "first_players");
+  const DeviceGuard guard(seeds.device());
+  const int64_t n = seeds.numel();
+  auto states = torch::empty({n, CUGO_STATE_BYTES}, on(seeds, at::kByte));
+  check_call(cugo_create(seeds.data_ptr<int64_t>(), first.data_ptr<int64_t>(), n, u8p(states),
+                         stream()),
+             "create");
+  return states;
+}
+
+std::vector<torch::Tensor> observe(torch::Tensor states) {
+  check_states(states);
+  const DeviceGuard guard(states.device());
+  const int64_t n = states.size(0);
+  auto o = observation_outputs(n, states);
+  check_call(cugo_observe(u8p(states), n, o[0].data_ptr<float>(), u8p(o[1]), u8p(o[2]),
+                          u8p(o[3]), o[4].data_ptr<int16_t>(), stream()),
+             "observe");
+  return o;
+}
+
+std::vector<torch::Tensor> observe_indexed(torch::Tensor states, torch::Tensor ids) {
+  check_states(states);
+  check_1d(ids, at::kLong, "env_ids");
+  check_same_device(states, ids, "states", "env_ids");
+  const DeviceGuard guard(states.device());
+  const int64_t n = ids.numel();
+  auto o = observation_outputs(n, states);
+  check_call(cugo_observe_indexed(u8p(states), states.size(0), ids.data_ptr<int64_t>(), n,
+                                  o[0].data_ptr<float>(), u8p(o[1]), u8p(o[2]), u8p(o[3]),
+                                  o[4].data_ptr<int16_t>(), stream()),
+             "observe_indexed");
+  return o;
+}
+
+std::vector<torch::Tensor> step(torch::Tensor states, torch::Tensor actions) {
+  check_states(states);
+  check_1d(actions, at::kLong, "actions");
+  TORCH_CHECK(states.size(0) == actions.numel(),
+              "states and actions must have the same batch size");
+  check_same_device(states, actions, "states", "actions");
+  const DeviceGuard guard(states.device());
+  const int64_t n = states.size(0);
+  auto o = step_outputs(n, states);
+  check_call(cugo_step(u8p(states), actions.data_ptr<int64_t>(), n, o[0].data_ptr<float>(),
+                       u8p(o[1]), u8p(o[2]), o[3].data_ptr<int16_t>(), u8p(o[4]), stream()),
+             "step");
+  return o;
+}
+
+void check_indexed_actions(const torch::Tensor& states, const torch::Tensor& ids,
+                           const torch::Tensor& actions) {
+  check_states(states);
+  check_1d(ids, at::kLong, "env_ids");
+  check_1d(actions, at::kLong, "actions");
+  TORCH_CHECK(ids.numel() == actions.numel(), "env_ids and actions must have the same length");
+  check_same_device(states, ids, "states", "env_ids");
+  check_same_device(states, actions, "states", "actions");
+}
+
+std::vector<torch::Tensor> step_indexed(torch::Tensor states, torch::Tensor ids,
+                                        torch::Tensor actions) {
+  check_indexed_actions(states, ids, actions);
+  const DeviceGuard guard(states.device());
+  const int64_t n = ids.numel();
+  auto o = step_outputs(n, states);
+  check_call(cugo_step_indexed(u8p(states), states.size(0), ids.data_ptr<int64_t>(),
+                               actions.data_ptr<int64_t>(), n, o[0].data_ptr<float>(),
+                               u8p(o[1]), u8p(o[2]), o[3].data_ptr<int16_t>(), u8p(o[4]),
+                               stream()),
+             "step_indexed");
+  return o;
+}
+
+std::vector<torch::Tensor> step_events_indexed(torch::Tensor states, torch::Tensor ids,
+                                               torch::Tensor actions) {
+  check_indexed_actions(states, ids, actions);
+  const DeviceGuard guard(states.device());
+  const int64_t n = ids.numel();
+  auto o = step_outputs(n, states);
+  auto events = torch::empty({n, CUGO_EVENT_WORDS}, on(states, at::kLong));
+  check_call(cugo_step_events_indexed(u8p(states), states.size(0), ids.data_ptr<int64_t>(),
+                                      actions.data_ptr<int64_t>(), n, o[0].data_ptr<float>(),
+                                      u8p(o[1]), u8p(o[2]), o[3].data_ptr<int16_t>(), u8p(o[4]),
+                                      events.data_ptr<int64_t>(), stream()),
+             "step_events_indexed");
+  o.push_back(events);
+  return o;
+}
+
+torch::Tensor start(torch::Tensor states) {
+  check_states(states);
+  const DeviceGuard guard(states.device());
+  const int64_t n = states.size(0);
+  auto out = torch::empty({n, CUGO_START_WORDS}, on(states, at::kLong));
+  check_call(cugo_start(u8p(states), n, out.data_ptr<int64_t>(), stream()), "start");
+  return out;
+}
+
+torch::Tensor clone_indexed(torch::Tensor states, torch::Tensor ids) {
+  check_states(states);
+  check_1d(ids, at::kLong, "env_ids");
+  check_same_device(states, ids, "states", "env_ids");
+  const DeviceGuard guard(states.device());
+  const int64_t n = ids.numel();
+  auto children = torch::empty({n, CUGO_STATE_BYTES}, on(states, at::kByte));
+  check_call(cugo_clone_indexed(u8p(states), states.size(0), ids.data_ptr<int64_t>(), n,
+                                u8p(children), stream()),
+             "clone_indexed");
+  return children;
+}
+
+std::vector<torch::Tensor> branch_indexed(torch::Tensor states, torch::Tensor ids,
+                                          torch::Tensor actions) {
+  check_indexed_actions(states, ids, actions);
+  const DeviceGuard guard(states.device());
+  const int64_t n = ids.numel();
+  auto children = torch::empty({n, CUGO_STATE_BYTES}, on(states, at::kByte));
+  auto o = step_outputs(n, states);
+  check_call(cugo_branch_indexed(u8p(states), states.size(0), ids.data_ptr<int64_t>(),
+                                 actions.data_ptr<int64_t>(), n, u8p(children),
+                                 o[0].data_ptr<float>(), u8p(o[1]), u8p(o[2]),
+                                 o[3].data_ptr<int16_t>(), u8p(o[4]), stream()),
+             "branch_indexed");
+  return {children, o[0], o[1], o[2], o[3], o[4]};
+}
+
+torch::Tensor hands_indexed(torch::Tensor states, torch::Tensor ids) {
+  check_states(states);
+  check_1d(ids, at::kLong, "env_ids");
+  check_same_device(states, ids, "states", "env_ids");
+  const DeviceGuard guard(states.device());
+  const int64_t n = ids.numel();
+  auto hands = torch::empty({n, 2}, on(states, at::kLong));
+  check_call(cugo_hands_indexed(u8p(states), states.size(0), ids.data_ptr<int64_t>(), n,
+                                hands.data_ptr<int64_t>(), stream()),
+             "hands_indexed");
+  return hands;
+}
+
+torch::Tensor stock_indexed(torch::Tensor states, torch::Tensor ids) {
+  check_states(states);
+  check_1d(ids, at::kLong, "env_ids");
+  check_same_device(states, ids, "states", "env_ids");
+  const DeviceGuard guard(states.device());
+  const int64_t n = ids.numel();
+  auto stock = torch::empty({n}, on(states, at::kLong));
+  check_call(cugo_stock_indexed(u8p(states), states.size(0), ids.data_ptr<int64_t>(), n,
+                                stock.data_ptr<int64_t>(), stream()),
+             "stock_indexed");
+  return stock;
+}
+
+// Random-policy driver operations (not in the reference module; used by the
+// throughput harness).  sampler: uint64 [N] (int64 tensor), generation: int32 [N],
+// completed: int64 [1] counter.
+torch::Tensor sample_uniform(torch::Tensor legal, torch::Tensor sampler) {
+  TORCH_CHECK(legal.is_cuda() && legal.is_contiguous() && legal.dim() == 2 &&
+                  legal.size(1) == CUGO_ACTION_COUNT && legal.scalar_type() == at::kBool,
+              "legal must be a contiguous CUDA bool [N, ACTION_COUNT] tensor");
+  check_1d(sampler, at::kLong, "sampler");
+  TORCH_CHECK(sampler.numel() == legal.size(0), "sampler and legal must have the same length");
+  check_same_device(legal, sampler, "legal", "sampler");
+  const DeviceGuard guard(legal.device());
+  const int64_t n = legal.size(0);
+  auto actions = torch::empty({n}, on(legal, at::kLong));
+  check_call(cugo_sample_uniform(u8p(legal), n, reinterpret_cast<uint64_t*>(sampler.data_ptr()),
+                                 actions.data_ptr<int64_t>(), stream()),
+             "sample_uniform");
+  return actions;
+}
+
+void reset_done(torch::Tensor states, torch::Tensor done, int64_t base_seed,
+                torch::Tensor generation, torch::Tensor sampler, torch::Tensor completed) {
+  check_states(states);
+  const int64_t n = states.size(0);
+  check_1d(done, at::kBool, "done");
+  check_1d(generation, at::kInt, "generation");
+  check_1d(sampler, at::kLong, "sampler");
+  check_1d(completed, at::kLong, "completed");
+  TORCH_CHECK(done.numel() == n && generation.numel() == n && sampler.numel() == n,
+              "done, generation and sampler must have one entry per state row");
+  TORCH_CHECK(completed.numel() >= 1, "completed must hold one counter");
+  const DeviceGuard guard(states.device());
+  check_call(cugo_reset_done(u8p(states), u8p(done), n, static_cast<uint64_t>(base_seed),
+                             reinterpret_cast<uint32_t*>(generation.data_ptr()),
+                             reinterpret_cast<uint64_t*>(sampler.data_ptr()),
+                             reinterpret_cast<unsigned long long*>(completed.data_ptr()),
+                             stream()),
+             "reset_done");
+}
+
+torch::Tensor seed_samplers(int64_t n, int64_t base_seed, torch::Tensor generation) {
+  check_1d(generation, at::kInt, "generation");
+  TORCH_CHECK(generation.numel() == n, "generation must have n entries");
+  const DeviceGuard guard(generation.device());
+  auto sampler = torch::empty({n}, on(generation, at::kLong));
+  check_call(cugo_seed_samplers(n, static_cast<uint64_t>(base_seed),
+                                reinterpret_cast<const uint32_t*>(generation.data_ptr()),
+                                reinterpret_cast<uint64_t*>(sampler.data_ptr()), stream()),
+             "seed_samplers");
+  return sampler;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "Cugo Shin Matgo batch environment on gfx950 (HIP)";
+  m.def("create", &create, "Create a GPU-resident batch of 248-byte game rows");
+  m.def("observe", &observe, "Encode features and legal masks on the current stream");
+  m.def("observe_indexed", &observe_indexed, "Encode only selected rows");
+  m.def("step", &step, "Apply unified actions to every row in place");
+  m.def("step_indexed", &step_indexed, "Apply unified actions to selected rows in place");
+  m.def("clone_indexed", &clone_indexed, "Clone selected rows");
+  m.def("branch_indexed", &branch_indexed, "Clone selected rows and step the clones");
+  m.def("hands_indexed", &hands_indexed, "[N, 2] int64 hand masks of both players");
+  m.def("stock_indexed", &stock_indexed, "[N] int64: the next 8 stock draws, one per byte");
+  m.def("step_events_indexed", &step_events_indexed,
+        "step_indexed plus [N, EVENT_WORDS] int64 event records");
+  m.def("start", &start, "[N, START_WORDS] int64 opening records");
+  m.def("sample_uniform", &sample_uniform, "Uniform legal action per row (xorshift64)");
+  m.def("reset_done", &reset_done, "Re-create finished rows with their next seed");
+  m.def("seed_samplers", &seed_samplers, "Per-row sampler state from the row seeds");
+  m.attr("FEATURE_COUNT") = pybind11::int_(CUGO_FEATURE_COUNT);
+  m.attr("ACTION_COUNT") = pybind11::int_(CUGO_ACTION_COUNT);
+  m.attr("PRIMARY_ACTION_COUNT") = pybind11::int_(CUGO_PRIMARY_ACTION_COUNT);
+  m.attr("CHOICE_ACTION_BEGIN") = pybind11::int_(CUGO_CHOICE_ACTION_BEGIN);
+  m.attr("EVENT_WORDS") = pybind11::int_(CUGO_EVENT_WORDS);
+  m.attr("START_WORDS") = pybind11::int_(CUGO_START_WORDS);
+  m.attr("STATE_BYTES") = pybind11::int_(CUGO_STATE_BYTES);
+  m.attr("STATUS_OK") = pybind11::int_(CUGO_STATUS_OK);
+}

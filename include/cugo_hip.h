@@ -1,0 +1,121 @@
+/*
+ * cugo_hip.h - C ABI of the gfx950 Shin Matgo batch engine (libcugo_hip.so).
+ *
+ * One entry point per operation of the reference PyTorch extension
+ * (python/csrc/torch50_ext.cpp:36-59, host wrappers python/csrc/torch50_ext.cu:406-686).
+ * The C ABI takes plain device pointers, element counts and a hipStream_t; it allocates
+ * nothing and never synchronises, so every call is an asynchronous launch on `stream`
+ * and is safe inside HIP graph capture.  Shape/dtype/device checks stay with the
+ * caller (the PyTorch extension raises the reference's RuntimeErrors,
+ * torch50_ext.cu:26-51); per-row problems go to the `status` outputs exactly as in
+ * the reference (-1 for an env id outside [0, env_count), ActionStatus50 0..9 otherwise,
+ * include/cugo/game/rollout50.h:33-44).
+ *
+ * Layout contract (identical to the reference TorchEnv50, torch50.h:108-121):
+ *   states   uint8 [n, CUGO_STATE_BYTES] rows, 8-byte aligned, row i = game i
+ *   features float [n, CUGO_FEATURE_COUNT]      legal    uint8 (0/1) [n, CUGO_ACTION_COUNT]
+ *   events   int64 [n, CUGO_EVENT_WORDS]         start    int64 [n, CUGO_START_WORDS]
+ *   bool outputs are one byte 0/1 (torch.bool).
+ * Padding bytes of every row the library writes are zero.
+ *
+ * Return value: 0 (hipSuccess) or the hipError_t of the launch; a negative value for
+ * an invalid argument (negative count, null pointer with a non-zero count).
+ */
+#ifndef CUGO_HIP_H_
+#define CUGO_HIP_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CUGO_FEATURE_COUNT 720        /* torch50.h:55 */
+#define CUGO_ACTION_COUNT 179         /* torch50.h:22 */
+#define CUGO_PRIMARY_ACTION_COUNT 127 /* torch50.h:16 */
+#define CUGO_CHOICE_ACTION_BEGIN 127  /* torch50.h:17 */
+#define CUGO_EVENT_WORDS 9            /* torch50.h:628 */
+#define CUGO_START_WORDS 8            /* torch50.h:629 */
+#define CUGO_STATE_BYTES 248          /* sizeof(TorchEnv50) */
+#define CUGO_STATUS_OK 0              /* ActionStatus50::kOk */
+#define CUGO_INVALID_INDEX_STATUS (-1) /* torch50_ext.cu:24 */
+
+/* Library/ABI version (major << 16 | minor). */
+int cugo_version(void);
+
+/* create(seeds, first_players) -> states (torch50_ext.cu:131-141, 406-427). */
+int cugo_create(const int64_t* seeds, const int64_t* first_players, int64_t n,
+                uint8_t* states, hipStream_t stream);
+
+/* observe(states) (torch50_ext.cu:143-158, 429-446). */
+int cugo_observe(const uint8_t* states, int64_t n, float* features, uint8_t* legal,
+                 uint8_t* player, uint8_t* done, int16_t* status, hipStream_t stream);
+
+/* observe_indexed(states, env_ids) (torch50_ext.cu:160-184, 448-472). */
+int cugo_observe_indexed(const uint8_t* states, int64_t env_count, const int64_t* env_ids,
+                         int64_t n, float* features, uint8_t* legal, uint8_t* player,
+                         uint8_t* done, int16_t* status, hipStream_t stream);
+
+/* step(states, actions), in place (torch50_ext.cu:186-200, 474-497). */
+int cugo_step(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
+              uint8_t* done, uint8_t* nagari, int16_t* status, uint8_t* committed,
+              hipStream_t stream);
+
+/* step_indexed(states, env_ids, actions), in place (torch50_ext.cu:202-225, 499-528). */
+int cugo_step_indexed(uint8_t* states, int64_t env_count, const int64_t* env_ids,
+                      const int64_t* actions, int64_t n, float* reward, uint8_t* done,
+                      uint8_t* nagari, int16_t* status, uint8_t* committed,
+                      hipStream_t stream);
+
+/* step_events_indexed(states, env_ids, actions) (torch50_ext.cu:227-262, 554-588). */
+int cugo_step_events_indexed(uint8_t* states, int64_t env_count, const int64_t* env_ids,
+                             const int64_t* actions, int64_t n, float* reward, uint8_t* done,
+                             uint8_t* nagari, int16_t* status, uint8_t* committed,
+                             int64_t* events, hipStream_t stream);
+
+/* start(states) (torch50_ext.cu:264-269, 590-605). */
+int cugo_start(const uint8_t* states, int64_t n, int64_t* out, hipStream_t stream);
+
+/* clone_indexed(states, env_ids) -> children (torch50_ext.cu:271-286, 607-629). */
+int cugo_clone_indexed(const uint8_t* states, int64_t env_count, const int64_t* env_ids,
+                       int64_t n, uint8_t* children, hipStream_t stream);
+
+/* branch_indexed(states, env_ids, actions) -> children + step outputs; parents are
+ * read only (torch50_ext.cu:288-314, 631-662). */
+int cugo_branch_indexed(const uint8_t* states, int64_t env_count, const int64_t* env_ids,
+                        const int64_t* actions, int64_t n, uint8_t* children, float* reward,
+                        uint8_t* done, uint8_t* nagari, int16_t* status, uint8_t* committed,
+                        hipStream_t stream);
+
+/* hands_indexed(states, env_ids) -> int64 [n, 2] (torch50_ext.cu:316-334, 664-686). */
+int cugo_hands_indexed(const uint8_t* states, int64_t env_count, const int64_t* env_ids,
+                       int64_t n, int64_t* hands, hipStream_t stream);
+
+/* stock_indexed(states, env_ids) -> int64 [n] (torch50_ext.cu:336-363, 530-552). */
+int cugo_stock_indexed(const uint8_t* states, int64_t env_count, const int64_t* env_ids,
+                       int64_t n, int64_t* stock, hipStream_t stream);
+
+/*
+ * Random-policy driver pieces (no counterpart in the reference extension; the
+ * reference's own smoke harness samples in Python, python/torch50_smoke.py:33-36).
+ *   cugo_sample_uniform: action[i] = legal list of row i [xorshift64(sampler[i]) % count],
+ *     -1 when the row has no legal action; sampler words advance in place.
+ *   cugo_reset_done: every row with done[i] != 0 is re-created from
+ *     seed = base_seed + i + batch * (++generation[i]) with first = i & 1, and its
+ *     sampler re-seeded from the same seed; completed[0] += number of rows reset.
+ */
+int cugo_sample_uniform(const uint8_t* legal, int64_t n, uint64_t* sampler, int64_t* actions,
+                        hipStream_t stream);
+int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
+                    uint32_t* generation, uint64_t* sampler, unsigned long long* completed,
+                    hipStream_t stream);
+/* sampler[i] = SplitMix64(base_seed + i + batch * generation[i]).next(), never 0. */
+int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation,
+                       uint64_t* sampler, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUGO_HIP_H_ */

@@ -1,0 +1,90 @@
+"""Writes the golden fixtures under tests/golden/ from the reference engine build.
+
+    python tests/golden/make_golden.py
+
+Runs the reference's own header-only engine (oracle/_ref/libcugo_ref.so, built by
+`make -C oracle ref` from the reference checkout) and stores inputs and expected
+outputs as .npz data:
+
+  c1_random_policy.npz  4,096 random-policy games (seed = 0x243F6A8885A308D3 + i,
+                        first = i & 1, sampler xorshift64 seeded by SplitMix64(seed)):
+                        per-game FNV-1a digest of every decision record, decision count
+                        and exact final reward of player 0; plus the full records of
+                        games 0..15 (first 64 decisions).
+  rows.npz              created rows and start records of games 0..255; mid-game rows
+                        (incl. pending floor choices) with their observations, hands,
+                        stock peeks and the step results of a fixed action list.
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parents[1]))
+
+from oracle.ref import SEED_BASE, RefEngine, sample_actions, splitmix_first  # noqa: E402
+
+
+def c1(ref: RefEngine) -> None:
+    digest, steps, reward, records, total = ref.play_random(SEED_BASE, 4096, threads=8,
+                                                            record_games=16, record_cap=64)
+    np.savez_compressed(HERE / "c1_random_policy.npz", digest=digest, steps=steps,
+                        final_reward=reward, records=records, total=np.int64(total))
+    print(f"c1: games=4096 decisions={total} mean={total / 4096:.2f}")
+
+
+def rows(ref: RefEngine) -> None:
+    n = 256
+    idx = np.arange(n, dtype=np.int64)
+    seeds = (np.uint64(SEED_BASE) + idx.astype(np.uint64)).view(np.int64)
+    first = idx & 1
+    created = ref.create(seeds, first)
+    start = ref.start(created)
+    # Play every game forward by a seed-dependent number of random decisions and keep
+    # the intermediate rows: a mix of primary, Go/Stop, Gukjin, pending floor-choice and
+    # finished states.
+    states = created.copy()
+    sampler = np.array([splitmix_first(int(s) & (2**64 - 1)) for s in seeds], dtype=np.uint64)
+    keep = []
+    for step in range(40):
+        _, legal, _, done, _ = ref.observe(states)
+        actions = sample_actions(legal, sampler, ~done)
+        ref.step(states, actions)
+        if step % 4 == 3:
+            keep.append(states.copy())
+    mid = np.concatenate(keep, axis=0)
+    obs = ref.observe(mid)
+    ids = np.arange(mid.shape[0], dtype=np.int64)
+    hands = ref.hands(mid, ids)
+    stock = ref.stock(mid, ids)
+    # A fixed action list over every row: first legal action, and out-of-range ones.
+    legal = obs[1]
+    first_legal = np.where(legal.any(axis=1), legal.argmax(axis=1), -1).astype(np.int64)
+    wild = (ids * 37) % 183 - 2
+    stepped = mid.copy()
+    out_first = ref.step(stepped, first_legal, events=True)
+    stepped_wild = mid.copy()
+    out_wild = ref.step(stepped_wild, wild, events=True)
+    np.savez_compressed(
+        HERE / "rows.npz", seeds=seeds, first=first, created=created, start=start, mid=mid,
+        features=obs[0], legal=obs[1], player=obs[2], done=obs[3], status=obs[4], hands=hands,
+        stock=stock, first_legal=first_legal, after_first=stepped,
+        first_out=np.stack([o.astype(np.float64) for o in out_first[:5]]),
+        first_events=out_first[5], wild=wild, after_wild=stepped_wild,
+        wild_out=np.stack([o.astype(np.float64) for o in out_wild[:5]]), wild_events=out_wild[5])
+    pending = int((mid[:, 219] != 0).sum())
+    print(f"rows: created={n} mid={mid.shape[0]} pending={pending} done={int(obs[3].sum())}")
+
+
+def main() -> None:
+    ref = RefEngine()
+    c1(ref)
+    rows(ref)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,76 @@
+"""CPU: the product libraries load and export their declared interface (no GPU calls)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+
+from tests.conftest import REPO
+
+
+def declared_symbols() -> list[str]:
+    text = (REPO / "include" / "cugo_hip.h").read_text()
+    return sorted(set(re.findall(r"\bint\s+(cugo_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(REPO / "cugo_amd" / "libcugo_hip.so"))
+    names = declared_symbols()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(lib, name), name
+    lib.cugo_version.restype = ctypes.c_int
+    assert lib.cugo_version() >> 16 == 1
+
+
+def test_abi_rejects_bad_arguments_without_launching():
+    lib = ctypes.CDLL(str(REPO / "cugo_amd" / "libcugo_hip.so"))
+    lib.cugo_create.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                ctypes.c_void_p, ctypes.c_void_p]
+    assert lib.cugo_create(None, None, -1, None, None) < 0
+    assert lib.cugo_create(None, None, 5, None, None) < 0
+    assert lib.cugo_create(None, None, 0, None, None) == 0
+
+
+def test_extension_module_constants():
+    from cugo_amd import _cugo_torch50_hip as m
+
+    assert (m.FEATURE_COUNT, m.ACTION_COUNT, m.PRIMARY_ACTION_COUNT, m.CHOICE_ACTION_BEGIN,
+            m.EVENT_WORDS, m.START_WORDS, m.STATE_BYTES, m.STATUS_OK) == (
+                720, 179, 127, 127, 9, 8, 248, 0)
+    for op in ("create", "observe", "observe_indexed", "step", "step_indexed", "clone_indexed",
+               "branch_indexed", "hands_indexed", "stock_indexed", "step_events_indexed",
+               "start"):
+        assert callable(getattr(m, op))
+
+
+def test_stop_points_table_is_the_host_log2f():
+    """The baked table equals this host's libm log2f(1 + p) / 12 (torch50.h:405-408)."""
+    text = (REPO / "cugo_amd" / "csrc" / "stop_bits.inc").read_text()
+    values = [float.fromhex(t.strip().rstrip("f")) for t in text.replace("\n", " ").split(",")
+              if t.strip()]
+    assert len(values) == 4095
+    libm = ctypes.CDLL("libm.so.6")
+    libm.log2f.restype = ctypes.c_float
+    libm.log2f.argtypes = [ctypes.c_float]
+    for p in range(0, 4095, 7):
+        bits = np.float32(libm.log2f(np.float32(1.0) + np.float32(p))) / np.float32(12.0)
+        expect = min(np.float32(bits), np.float32(1.0))
+        assert np.float32(values[p]) == expect, p
+    assert values[0] == 0.0 and values[4094] < 1.0
+
+
+def test_load_extension_fails_loudly_without_gpu(monkeypatch):
+    import torch
+
+    import cugo_amd
+
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    try:
+        cugo_amd.load_extension()
+    except RuntimeError as exc:
+        assert "not available" in str(exc)
+    else:
+        raise AssertionError("load_extension must raise without a GPU")

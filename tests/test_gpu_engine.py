@@ -1,0 +1,291 @@
+"""GPU parity: every operation of the HIP extension against the reference engine.
+
+The checker is the reference's own C++ engine (oracle/_ref, driven through
+oracle/ref.py) on the same inputs; integer, byte and mask outputs must be identical and
+float features/rewards bit-identical (compared as raw 32-bit patterns).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.ref import (PADDING, SEED_BASE, fnv_update, FNV_OFFSET, sample_actions,
+                        splitmix_first, step_record)
+from tests.conftest import GOLDEN, announce
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def f32_bits(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def c1_seeds(n: int, base: int = SEED_BASE):
+    idx = np.arange(n, dtype=np.uint64)
+    seeds = (np.uint64(base) + idx).view(np.int64)
+    return seeds, (np.arange(n, dtype=np.int64) & 1)
+
+
+def assert_observe_equal(gpu_out, ref_out, label: str) -> None:
+    f, legal, player, done, status = (to_np(t) for t in gpu_out)
+    rf, rlegal, rplayer, rdone, rstatus = ref_out
+    bad = np.nonzero((f32_bits(f) != f32_bits(rf)).any(axis=1))[0]
+    assert bad.size == 0, f"{label}: features differ in rows {bad[:8]}"
+    assert np.array_equal(legal, rlegal), f"{label}: legal masks differ"
+    assert np.array_equal(player, rplayer), f"{label}: players differ"
+    assert np.array_equal(done, rdone), f"{label}: done differs"
+    assert np.array_equal(status, rstatus), f"{label}: status differs"
+
+
+def assert_step_equal(gpu_out, ref_out, label: str) -> None:
+    names = ("reward", "done", "nagari", "status", "committed", "events")
+    for name, g, r in zip(names, gpu_out, ref_out):
+        g = to_np(g)
+        if name == "reward":
+            assert np.array_equal(f32_bits(g), f32_bits(r)), f"{label}: reward differs"
+        else:
+            assert np.array_equal(g, r), f"{label}: {name} differs"
+
+
+def test_create_and_start(ext, ref):
+    announce("create_and_start")
+    seeds, first = c1_seeds(4096)
+    rng = np.random.default_rng(7)
+    seeds = np.concatenate([seeds, rng.integers(-2**63, 2**63 - 1, 4033, dtype=np.int64)])
+    first = np.concatenate([first, rng.integers(0, 5, 4033, dtype=np.int64)])
+    states = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(first).to(DEV))
+    rows = to_np(states)
+    expect = ref.create(seeds, first)
+    assert np.array_equal(rows, expect)
+    assert np.array_equal(to_np(ext.start(states)), ref.start(expect))
+    golden = np.load(GOLDEN / "rows.npz")
+    g = ext.create(torch.from_numpy(golden["seeds"]).to(DEV),
+                   torch.from_numpy(golden["first"]).to(DEV))
+    assert np.array_equal(to_np(g), golden["created"])
+    assert np.array_equal(to_np(ext.start(g)), golden["start"])
+
+
+def test_random_policy_games_match_reference(ext, ref):
+    """The C1 protocol: 4,096 games to the end in lockstep with the reference; every
+    observation, step output, event record and row byte compared, and the per-game
+    digests checked against the golden fixture."""
+    announce("random_policy_lockstep_c1")
+    n = 4096
+    seeds, first = c1_seeds(n)
+    states = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(first).to(DEV))
+    host = ref.create(seeds, first)
+    sampler = np.array([splitmix_first(int(s) & (2**64 - 1)) for s in seeds], dtype=np.uint64)
+    digest = np.full(n, FNV_OFFSET, dtype=np.uint64)
+    steps = np.zeros(n, dtype=np.int32)
+    ids = torch.arange(n, device=DEV)
+    for step in range(128):
+        obs = ext.observe(states)
+        robs = ref.observe(host)
+        assert_observe_equal(obs, robs, f"observe step {step}")
+        active = ~robs[3]
+        if not active.any():
+            break
+        assert robs[1][active].any(axis=1).all(), "active game without a legal action"
+        actions = sample_actions(robs[1], sampler, active)
+        out = ext.step_events_indexed(states, ids, torch.from_numpy(actions).to(DEV))
+        rout = ref.step(host, actions, events=True)
+        assert_step_equal(out, rout, f"step {step}")
+        assert np.array_equal(to_np(states), host), f"rows differ after step {step}"
+        rec = step_record(robs[0], robs[1], robs[2], robs[3], robs[4], actions, *rout)
+        digest[active] = fnv_update(digest[active], rec[active])
+        steps[active] += 1
+    golden = np.load(GOLDEN / "c1_random_policy.npz")
+    assert np.array_equal(steps, golden["steps"])
+    assert np.array_equal(digest, golden["digest"])
+    rewards = np.array([ref.reward0(r) for r in host], dtype=np.int64)
+    assert np.array_equal(rewards, golden["final_reward"])
+
+
+def test_wild_actions_and_indexed_rows(ext, ref):
+    """Out-of-range and illegal actions, invalid/duplicate ids, odd batch sizes."""
+    announce("wild_actions_indexed")
+    rng = np.random.default_rng(11)
+    n = 1000  # not a multiple of 64
+    seeds = rng.integers(-2**63, 2**63 - 1, n, dtype=np.int64)
+    first = rng.integers(0, 2, n, dtype=np.int64)
+    states = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(first).to(DEV))
+    host = ref.create(seeds, first)
+    sampler = np.array([splitmix_first(int(s) & (2**64 - 1)) for s in seeds], dtype=np.uint64)
+    for step in range(60):
+        ids = rng.permutation(n)[: rng.integers(1, n)].astype(np.int64)
+        obs_ids = np.concatenate([ids, [-1, n, n + 5, ids[0], ids[0]]]).astype(np.int64)
+        obs = ext.observe_indexed(states, torch.from_numpy(obs_ids).to(DEV))
+        assert_observe_equal(obs, ref.observe(host, obs_ids), f"observe_indexed {step}")
+        _, legal, _, done, _ = ref.observe(host, ids)
+        actions = sample_actions(legal, sampler[ids], ~done)
+        wild = rng.random(ids.size) < 0.15
+        actions[wild] = rng.integers(-3, 185, int(wild.sum()))
+        step_ids = np.concatenate([ids, [-7, n]]).astype(np.int64)
+        step_actions = np.concatenate([actions, [0, 1]]).astype(np.int64)
+        if step % 2:
+            out = ext.step_indexed(states, torch.from_numpy(step_ids).to(DEV),
+                                   torch.from_numpy(step_actions).to(DEV))
+            rout = ref.step(host, step_actions, ids=step_ids)
+        else:
+            out = ext.step_events_indexed(states, torch.from_numpy(step_ids).to(DEV),
+                                          torch.from_numpy(step_actions).to(DEV))
+            rout = ref.step(host, step_actions, ids=step_ids, events=True)
+        assert_step_equal(out, rout, f"step_indexed {step}")
+        assert np.array_equal(to_np(states), host), f"rows differ after indexed step {step}"
+
+
+def test_full_batch_step_matches(ext, ref):
+    announce("full_batch_step")
+    golden = np.load(GOLDEN / "rows.npz")
+    mid = golden["mid"]
+    for name, actions in (("first", golden["first_legal"]), ("wild", golden["wild"])):
+        states = torch.from_numpy(mid.copy()).to(DEV)
+        out = ext.step(states, torch.from_numpy(actions).to(DEV))
+        host = mid.copy()
+        rout = ref.step(host, actions)
+        assert_step_equal(out, rout, f"step {name}")
+        assert np.array_equal(to_np(states), host)
+        assert np.array_equal(host, golden[f"after_{name}"])
+
+
+def test_golden_rows_observe_hands_stock(ext):
+    announce("golden_rows")
+    golden = np.load(GOLDEN / "rows.npz")
+    states = torch.from_numpy(golden["mid"]).to(DEV)
+    f, legal, player, done, status = (to_np(t) for t in ext.observe(states))
+    assert np.array_equal(f32_bits(f), f32_bits(golden["features"]))
+    assert np.array_equal(legal, golden["legal"])
+    assert np.array_equal(player, golden["player"])
+    assert np.array_equal(done, golden["done"])
+    assert np.array_equal(status, golden["status"])
+    ids = torch.arange(states.shape[0], device=DEV)
+    assert np.array_equal(to_np(ext.hands_indexed(states, ids)), golden["hands"])
+    assert np.array_equal(to_np(ext.stock_indexed(states, ids)), golden["stock"])
+
+
+def test_branch_and_clone(ext, ref):
+    announce("branch_clone")
+    golden = np.load(GOLDEN / "rows.npz")
+    parents_np = golden["mid"]
+    parents = torch.from_numpy(parents_np).to(DEV)
+    snapshot = parents.clone()
+    m = parents_np.shape[0]
+    rng = np.random.default_rng(3)
+    ids = np.concatenate([rng.integers(0, m, 5000), [-1, m, m + 3]]).astype(np.int64)
+    actions = rng.integers(-2, 181, ids.size).astype(np.int64)
+    legal = golden["legal"]
+    pick = rng.random(ids.size) < 0.7
+    for k in np.nonzero(pick & (ids >= 0) & (ids < m))[0]:
+        choices = np.nonzero(legal[ids[k]])[0]
+        if choices.size:
+            actions[k] = choices[k % choices.size]
+    tid, tact = torch.from_numpy(ids).to(DEV), torch.from_numpy(actions).to(DEV)
+    out = ext.branch_indexed(parents, tid, tact)
+    rout = ref.branch(parents_np, ids, actions)
+    assert np.array_equal(to_np(out[0]), rout[0]), "children differ"
+    assert_step_equal(out[1:], rout[1:], "branch outputs")
+    assert torch.equal(parents, snapshot), "parents changed"
+    clones = ext.clone_indexed(parents, tid)
+    assert np.array_equal(to_np(clones), ref.clone(parents_np, ids))
+    # branch == clone + step on valid parents (branch50_smoke.py:113-115)
+    valid = torch.from_numpy((ids >= 0) & (ids < m)).to(DEV)
+    split = ext.step(clones, tact)
+    assert torch.equal(out[0][valid], clones[valid])
+    for a, b in zip(out[1:], split):
+        assert torch.equal(a[valid], b[valid])
+
+
+def test_empty_batches(ext):
+    announce("empty_batches")
+    states = ext.create(torch.zeros(4, dtype=torch.long, device=DEV),
+                        torch.zeros(4, dtype=torch.long, device=DEV))
+    empty = torch.empty(0, dtype=torch.long, device=DEV)
+    assert tuple(ext.clone_indexed(states, empty).shape) == (0, 248)
+    br = ext.branch_indexed(states, empty, empty)
+    assert tuple(br[0].shape) == (0, 248) and all(t.numel() == 0 for t in br[1:])
+    assert ext.observe_indexed(states, empty)[0].shape == (0, 720)
+    assert ext.create(empty, empty).shape == (0, 248)
+    ev = ext.step_events_indexed(states, empty, empty)
+    assert tuple(ev[5].shape) == (0, 9)
+
+
+def test_shape_errors_raise(ext):
+    announce("shape_errors")
+    states = ext.create(torch.zeros(4, dtype=torch.long, device=DEV),
+                        torch.zeros(4, dtype=torch.long, device=DEV))
+    with pytest.raises(RuntimeError, match="states second dimension"):
+        ext.observe(torch.zeros(4, 100, dtype=torch.uint8, device=DEV))
+    with pytest.raises(RuntimeError, match="same batch size"):
+        ext.step(states, torch.zeros(3, dtype=torch.long, device=DEV))
+    with pytest.raises(RuntimeError, match="wrong dtype"):
+        ext.step(states, torch.zeros(4, dtype=torch.int32, device=DEV))
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ext.observe(states.cpu())
+
+
+def test_driver_sample_and_reset(ext, ref):
+    """The random-policy driver kernels: GPU sampler == numpy sampler; reset_done
+    re-creates exactly the finished rows from their next seed."""
+    announce("driver_sample_reset")
+    n = 3000
+    base = 0x1234567
+    gen = torch.zeros(n, dtype=torch.int32, device=DEV)
+    sampler = ext.seed_samplers(n, base, gen)
+    host_sampler = np.array([splitmix_first(base + i) for i in range(n)], dtype=np.uint64)
+    assert np.array_equal(to_np(sampler).view(np.uint64), host_sampler)
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    states = ext.create(torch.from_numpy(seeds).to(DEV),
+                        torch.from_numpy(np.arange(n) & 1).to(DEV))
+    completed = torch.zeros(1, dtype=torch.long, device=DEV)
+    for _ in range(30):
+        _, legal, _, done, _ = ext.observe(states)
+        actions = ext.sample_uniform(legal, sampler)
+        expect = sample_actions(to_np(legal), host_sampler, np.ones(n, dtype=bool))
+        assert np.array_equal(to_np(actions), expect)
+        _, sdone, _, _, _ = ext.step(states, actions)
+        before = to_np(gen).copy()
+        ext.reset_done(states, sdone, base, gen, sampler, completed)
+        reset = to_np(sdone)
+        after = to_np(gen)
+        assert np.array_equal(after, before + reset)
+        rows = to_np(states)
+        for k, i in enumerate(np.nonzero(reset)[0]):
+            seed = (base + int(i) + n * int(after[i])) & (2**64 - 1)
+            host_sampler[i] = splitmix_first(seed)
+            if k < 8:
+                expect_row = ref.create(np.array([seed], dtype=np.uint64).view(np.int64),
+                                        np.array([i & 1]))
+                assert np.array_equal(rows[i], expect_row[0])
+    assert int(completed.item()) == int(to_np(gen).sum())
+
+
+def test_repeatable(ext):
+    announce("repeatable")
+    golden = np.load(GOLDEN / "rows.npz")
+    a = torch.from_numpy(golden["mid"]).to(DEV)
+    b = a.clone()
+    acts = torch.from_numpy(golden["first_legal"]).to(DEV)
+    oa, ob = ext.step(a, acts), ext.step(b, acts)
+    assert torch.equal(a, b)
+    for x, y in zip(oa, ob):
+        assert torch.equal(x, y)
+    f1 = ext.observe(a)[0]
+    f2 = ext.observe(a)[0]
+    assert torch.equal(f1, f2)
+
+
+def test_padding_bytes_zero(ext):
+    announce("padding_zero")
+    seeds, first = c1_seeds(512)
+    states = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(first).to(DEV))
+    rows = to_np(states)
+    for lo, hi in PADDING:
+        assert not rows[:, lo:hi].any()
