@@ -1,0 +1,215 @@
+"""Throughput of the gfx950 Shin Matgo engine on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--no-cpu] [--no-branch]
+
+Workload (timed, one JSON line on stdout): random-policy self-play on B = 65,536
+GPU-resident games.  One step = observe (720 features + 179-way mask for every game)
+-> uniform legal sample (per-game xorshift64) -> step -> re-create finished games with
+their next seed.  `value` = complete games per second over K steps.  Games are dealt
+from seed = 0x243F6A8885A308D3 + i (+ B per later game of row i), first = i & 1.
+
+Also reported (not timed into `value`):
+  roofline      the observe kernel (the widest), bytes per row = 248 read + 3,063 written,
+                timed with HIP events on the stream it runs on
+  branch        4,096 roots (3-15 seeded random decisions deep) x 256 children:
+                branch_indexed (clone + step) and the observation of all children
+  cpu_baseline  the reference engine (oracle/_ref) on this host's cores, same protocol,
+                bounded sample
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+SEED_BASE = 0x243F6A8885A308D3
+HBM_PEAK_GBS = 8000.0
+OBSERVE_BYTES_PER_ROW = 248 + 720 * 4 + 179 + 1 + 1 + 2  # 3,311
+STEP_BYTES_PER_ROW = 248 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # 513
+BRANCH_BYTES_PER_CHILD = 8 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # parent reads hit L2: 273
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=100)
+    p.add_argument("--batch", type=int, default=65536)
+    p.add_argument("--branch-iters", type=int, default=20)
+    p.add_argument("--no-branch", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+def random_policy(ext, torch, batch: int, steps: int, warmup: int) -> dict:
+    dev = torch.device("cuda")
+    idx = torch.arange(batch, dtype=torch.int64, device=dev)
+    states = ext.create(idx + SEED_BASE, idx & 1)
+    gen = torch.zeros(batch, dtype=torch.int32, device=dev)
+    sampler = ext.seed_samplers(batch, SEED_BASE, gen)
+    completed = torch.zeros(1, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def one_step(events=None):
+        if events is not None:
+            events[0].record(stream)
+        _, legal, _, _, _ = ext.observe(states)
+        if events is not None:
+            events[1].record(stream)
+        actions = ext.sample_uniform(legal, sampler)
+        _, done, _, _, _ = ext.step(states, actions)
+        ext.reset_done(states, done, SEED_BASE, gen, sampler, completed)
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    start_games = int(completed.item())
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        one_step(pairs[k])
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - t0
+    games = int(completed.item()) - start_games
+    observe_ms = sum(a.elapsed_time(b) for a, b in pairs) / steps
+    return {"seconds": seconds, "games": games, "observe_ms": observe_ms}
+
+
+def branch_workload(ext, torch, iters: int) -> dict:
+    """4,096 roots from seeded random play of 3-15 decisions; child k of a root takes
+    legal[k] while k < count, then legal[xorshift % count]."""
+    import numpy as np
+
+    dev = torch.device("cuda")
+    roots_n, fan = 4096, 256
+    idx = torch.arange(roots_n, dtype=torch.int64, device=dev)
+    base = SEED_BASE + 0x5EED
+    roots = ext.create(idx + base, idx & 1)
+    gen = torch.zeros(roots_n, dtype=torch.int32, device=dev)
+    sampler = ext.seed_samplers(roots_n, base, gen)
+    depth = 3 + (sampler.cpu().numpy().view(np.uint64) % np.uint64(13)).astype(np.int64)
+    depth_t = torch.from_numpy(depth).to(dev)
+    for d in range(15):
+        _, legal, _, done, _ = ext.observe(roots)
+        actions = ext.sample_uniform(legal, sampler)
+        actions = torch.where(depth_t > d, actions, torch.full_like(actions, -1))
+        ext.step_indexed(roots, idx[depth_t > d], actions[depth_t > d])
+    # keep live roots (a root may have finished early); refill from live ones
+    _, legal, _, done, status = ext.observe(roots)
+    live = torch.nonzero(~done & (status == 0)).flatten()
+    roots = roots.index_select(0, live).contiguous()
+    legal = legal.index_select(0, live)
+    n_live = roots.shape[0]
+    parent = (torch.arange(roots_n * fan, device=dev) // fan) % n_live
+    k = torch.arange(roots_n * fan, device=dev) % fan
+    lg = legal.index_select(0, parent)
+    counts = lg.sum(1)
+    x = (torch.arange(roots_n * fan, device=dev) * 0x9E3779B97F4A7C15 + 1) & ((1 << 62) - 1)
+    pick = torch.where(k < counts, k, x % counts)
+    actions = torch.argmax((lg.cumsum(1) > pick[:, None]).to(torch.int8), dim=1)
+    parent, actions = parent.contiguous(), actions.contiguous()
+    children = ext.branch_indexed(roots, parent, actions)[0]
+    ext.observe(children)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    stream = torch.cuda.current_stream()
+    ev[0].record(stream)
+    for _ in range(iters):
+        children = ext.branch_indexed(roots, parent, actions)[0]
+    ev[1].record(stream)
+    for _ in range(iters):
+        ext.observe(children)
+    ev[2].record(stream)
+    torch.cuda.synchronize()
+    branch_ms = ev[0].elapsed_time(ev[1]) / iters
+    observe_ms = ev[1].elapsed_time(ev[2]) / iters
+    n = roots_n * fan
+    return {
+        "children": n,
+        "live_roots": int(n_live),
+        "branch_ms": round(branch_ms, 4),
+        "branches_per_s": n / (branch_ms * 1e-3),
+        "branch_gbs": n * BRANCH_BYTES_PER_CHILD / (branch_ms * 1e-3) / 1e9,
+        "observe_children_ms": round(observe_ms, 4),
+        "branch_observe_per_s": n / ((branch_ms + observe_ms) * 1e-3),
+    }
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The reference engine (oracle/_ref) on the host cores, same random-policy protocol
+    (observe + sample + step_events per decision), growing the sample to ~`seconds`."""
+    from oracle.ref import SEED_BASE as base, RefEngine
+
+    ref = RefEngine()
+    threads = min(os.cpu_count() or 1, 16)
+    n = 4096
+    while True:
+        t0 = time.perf_counter()
+        _, _, _, _, decisions = ref.play_random(base + 10**9, n, threads=threads, outputs=False)
+        dt = time.perf_counter() - t0
+        if dt >= seconds or n >= 1 << 24:
+            break
+        n = int(n * min(8.0, max(1.5, seconds / max(dt, 1e-3))))
+    return {"value": n / dt, "unit": "games/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} random-policy games ({decisions} decisions) in {dt:.1f} s",
+            "steps_per_s": decisions / dt}
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
+                          "n_gpus": args.gpus}), flush=True)
+        sys.exit(2)
+    import torch
+
+    from cugo_amd import load_extension
+
+    ext = load_extension()
+    rp = random_policy(ext, torch, args.batch, args.steps, args.warmup)
+    games_per_s = rp["games"] / rp["seconds"]
+    ms_per_step = 1000.0 * rp["seconds"] / args.steps
+    observe_gbs = args.batch * OBSERVE_BYTES_PER_ROW / (rp["observe_ms"] * 1e-3) / 1e9
+    result = {
+        "metric": "complete games/sec (random-policy self-play, B=65536 resident games)",
+        "value": round(games_per_s, 1),
+        "unit": "games/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic",
+        "config": {"workload": "random-policy self-play: observe -> sample -> step -> reset",
+                   "batch": args.batch, "seed_base": hex(SEED_BASE),
+                   "policy": "uniform legal action, per-game xorshift64"},
+        "steps_per_s": round(args.batch * args.steps / rp["seconds"], 1),
+        "games_timed": rp["games"],
+        "roofline": {"kernel": "observe_kernel", "bound": "hbm",
+                     "achieved": round(observe_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(observe_gbs / HBM_PEAK_GBS, 4),
+                     "bytes_per_row": OBSERVE_BYTES_PER_ROW,
+                     "avg_launch_ms": round(rp["observe_ms"], 4), "traffic": None},
+    }
+    if not args.no_branch:
+        result["branch"] = branch_workload(ext, torch, args.branch_iters)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -17,7 +17,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#define CG_HD __host__ __device__ inline
+#define CG_HD __host__ __device__ __forceinline__
 
 namespace cugo_amd {
 
@@ -332,24 +332,48 @@ CG_HD void pack_row(const Env& e, u64* w) {
   w[30] = e.nagari;
 }
 
-// Per-player field access (player bit 0 selects).
-CG_HD u64 hand_of(const Env& e, u32 p) { return (p & 1u) ? e.hand1 : e.hand0; }
-CG_HD void set_hand(Env& e, u32 p, u64 v) { if (p & 1u) e.hand1 = v; else e.hand0 = v; }
-CG_HD u64 cap_of(const Env& e, u32 p) { return (p & 1u) ? e.cap1 : e.cap0; }
-CG_HD void set_cap(Env& e, u32 p, u64 v) { if (p & 1u) e.cap1 = v; else e.cap0 = v; }
-CG_HD u8 go_of(const Env& e, u32 p) { return (p & 1u) ? e.go1 : e.go0; }
-CG_HD u8 lgo_of(const Env& e, u32 p) { return (p & 1u) ? e.lgo1 : e.lgo0; }
-CG_HD u16 shaken_of(const Env& e, u32 p) { return (p & 1u) ? e.shaken1 : e.shaken0; }
-CG_HD u16 sh4_of(const Env& e, u32 p) { return (p & 1u) ? e.sh4_1 : e.sh4_0; }
-CG_HD u8 bombs_of(const Env& e, u32 p) { return (p & 1u) ? e.bombs1 : e.bombs0; }
-CG_HD u8 cred_of(const Env& e, u32 p) { return (p & 1u) ? e.cred1 : e.cred0; }
-CG_HD void set_cred(Env& e, u32 p, u8 v) { if (p & 1u) e.cred1 = v; else e.cred0 = v; }
-CG_HD u8 pcount_of(const Env& e, u32 p) { return (p & 1u) ? e.pcount1 : e.pcount0; }
-CG_HD u8 streak_of(const Env& e, u32 p) { return (p & 1u) ? e.streak1 : e.streak0; }
-CG_HD u8 mm_of(const Env& e, u32 p) { return (p & 1u) ? e.mm1 : e.mm0; }
-CG_HD void set_mm(Env& e, u32 p, u8 v) { if (p & 1u) e.mm1 = v; else e.mm0 = v; }
-CG_HD u64 held_of(const Env& e, u32 p) { return (p & 1u) ? e.held1 : e.held0; }
-CG_HD u64 rev_of(const Env& e, u32 p) { return (p & 1u) ? e.rev1 : e.rev0; }
+// Per-player field access (player bit 0 selects).  Both fields are read and combined
+// arithmetically: a conditional read of one of two adjacent fields would be folded by
+// the optimiser into a read at a computed offset, which pins the whole Env in private
+// (scratch) memory instead of registers.
+template <class T>
+CG_HD T pick(T v0, T v1, u32 p) {
+  const T m = (T)(0 - (T)(p & 1u));
+  return (T)((v0 & (T)~m) | (v1 & m));
+}
+CG_HD u64 hand_of(const Env& e, u32 p) { return pick<u64>(e.hand0, e.hand1, p); }
+CG_HD void set_hand(Env& e, u32 p, u64 v) {
+  const u64 a = e.hand0, b = e.hand1;
+  e.hand0 = pick<u64>(v, a, p);
+  e.hand1 = pick<u64>(b, v, p);
+}
+CG_HD u64 cap_of(const Env& e, u32 p) { return pick<u64>(e.cap0, e.cap1, p); }
+CG_HD void set_cap(Env& e, u32 p, u64 v) {
+  const u64 a = e.cap0, b = e.cap1;
+  e.cap0 = pick<u64>(v, a, p);
+  e.cap1 = pick<u64>(b, v, p);
+}
+CG_HD u8 go_of(const Env& e, u32 p) { return pick<u8>(e.go0, e.go1, p); }
+CG_HD u8 lgo_of(const Env& e, u32 p) { return pick<u8>(e.lgo0, e.lgo1, p); }
+CG_HD u16 shaken_of(const Env& e, u32 p) { return pick<u16>(e.shaken0, e.shaken1, p); }
+CG_HD u16 sh4_of(const Env& e, u32 p) { return pick<u16>(e.sh4_0, e.sh4_1, p); }
+CG_HD u8 bombs_of(const Env& e, u32 p) { return pick<u8>(e.bombs0, e.bombs1, p); }
+CG_HD u8 cred_of(const Env& e, u32 p) { return pick<u8>(e.cred0, e.cred1, p); }
+CG_HD void set_cred(Env& e, u32 p, u8 v) {
+  const u8 a = e.cred0, b = e.cred1;
+  e.cred0 = pick<u8>(v, a, p);
+  e.cred1 = pick<u8>(b, v, p);
+}
+CG_HD u8 pcount_of(const Env& e, u32 p) { return pick<u8>(e.pcount0, e.pcount1, p); }
+CG_HD u8 streak_of(const Env& e, u32 p) { return pick<u8>(e.streak0, e.streak1, p); }
+CG_HD u8 mm_of(const Env& e, u32 p) { return pick<u8>(e.mm0, e.mm1, p); }
+CG_HD void set_mm(Env& e, u32 p, u8 v) {
+  const u8 a = e.mm0, b = e.mm1;
+  e.mm0 = pick<u8>(v, a, p);
+  e.mm1 = pick<u8>(b, v, p);
+}
+CG_HD u64 held_of(const Env& e, u32 p) { return pick<u64>(e.held0, e.held1, p); }
+CG_HD u64 rev_of(const Env& e, u32 p) { return pick<u64>(e.rev0, e.rev1, p); }
 
 // -------------------------------------------------------------------- turn50 ----
 CG_HD u64 active_hand(const Env& e) { return hand_of(e, e.actor); }
@@ -2049,6 +2073,45 @@ CG_HD float feature_at(const u64* w, const float* d, u32 f) {
   if (f < 710) { const u32 g = f - 560; return bit_feature(w[17 + g / 50], g % 50); }
   if (f < 712) return d[54 + (f - 710)];
   return 0.0f;
+}
+
+
+// Per-row dword record read by the GPU feature writer: the 20 bit-plane words as 40
+// dwords (low half first), the 56 dense floats, then one float 0.0 for the padding
+// features.  feature_source(f) names feature f's dword in that record and, for a bit
+// feature, the bit: (dword << 8) | (bit << 1) | 1; a float feature is (dword << 8).
+constexpr int kFeatRecord = 2 * kFeatWords + kFeatDense + 1;  // 97 used dwords
+constexpr int kFeatRecordStride = 98;                          // keeps u64 words aligned
+
+CG_HD void feature_record(const FeatRow& r, u32* rec) {
+  for (int k = 0; k < kFeatWords; ++k) {
+    rec[2 * k] = (u32)r.w[k];
+    rec[2 * k + 1] = (u32)(r.w[k] >> 32);
+  }
+  for (int k = 0; k < kFeatDense; ++k) rec[2 * kFeatWords + k] = __builtin_bit_cast(u32, r.d[k]);
+  rec[2 * kFeatWords + kFeatDense] = 0u;
+}
+
+CG_HD u32 feature_source(u32 f) {
+  u32 word, b;
+  if (f < 300) { word = f / 50; b = f % 50; }
+  else if (f < 396) { const u32 g = f - 300; word = 6 + g / 12; b = g % 12; }
+  else if (f < 446) { word = 14; b = f - 396; }
+  else if (f < 479) return (u32)(2 * kFeatWords + (f - 446)) << 8;
+  else if (f < 491) { word = 15; b = f - 479; }
+  else if (f < 496) return (u32)(2 * kFeatWords + 33 + (f - 491)) << 8;
+  else if (f < 544) { word = 16; b = f - 496; }
+  else if (f < 560) return (u32)(2 * kFeatWords + 38 + (f - 544)) << 8;
+  else if (f < 710) { const u32 g = f - 560; word = 17 + g / 50; b = g % 50; }
+  else if (f < 712) return (u32)(2 * kFeatWords + 54 + (f - 710)) << 8;
+  else return (u32)(2 * kFeatWords + kFeatDense) << 8;
+  return ((2 * word + (b >> 5)) << 8) | ((b & 31u) << 1) | 1u;
+}
+
+CG_HD float feature_from_record(const u32* rec, u32 src) {
+  const u32 v = rec[src >> 8];
+  const float as_bit = (float)((v >> ((src >> 1) & 31u)) & 1u);
+  return (src & 1u) ? as_bit : __builtin_bit_cast(float, v);
 }
 
 }  // namespace cugo_amd

@@ -89,85 +89,121 @@ __global__ __launch_bounds__(kTile) void create_kernel(const i64* seeds, const i
 }
 
 // ------------------------------------------------------------------ observe ----
-struct FeatTile {
-  u64 w[kTile][kFeatWords];
-  float d[kTile][kFeatDense];
-  u64 legal[kTile][3];
+// LDS of one observe tile: the staged rows are dead once every lane has unpacked its
+// row, so the per-row feature records and masks reuse the same bytes.
+struct ObserveTile {
+  union {
+    u64 rows[kTileWords];
+    struct {
+      u32 rec[kTile][kFeatRecordStride];
+      u64 legal[kTile][3];
+    } out;
+  };
 };
+
+// Four consecutive mask bits -> four bytes 0/1 (little-endian).
+__device__ inline u32 spread4(u32 x) {
+  return (x & 1u) | ((x & 2u) << 7) | ((x & 4u) << 14) | ((x & 8u) << 21);
+}
 
 template <bool kIndexed>
 __global__ __launch_bounds__(kTile) void observe_kernel(const u64* states, i64 env_count,
                                                         const i64* ids, i64 n, float* features,
                                                         u8* legal, u8* player, u8* done,
                                                         i16* status) {
-  __shared__ u64 rows[kTileWords];
+  __shared__ ObserveTile t;
   __shared__ i64 tile_ids[kTile];
-  __shared__ FeatTile ft;
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int lane = threadIdx.x;
   if (kIndexed && lane < count) tile_ids[lane] = ids[base + lane];
   __syncthreads();
-  stage_in(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
+  stage_in(t.rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
   __syncthreads();
-  if (lane < count) {
+  const bool active = lane < count;
+  const bool ok = active && (!kIndexed || valid_id(tile_ids[lane], env_count));
+  Env e;
+  if (ok) e = unpack_row(t.rows + lane * kRowWords);
+  __syncthreads();  // rows are dead from here on; their bytes become the records
+  if (active) {
     const i64 i = base + lane;
-    const bool ok = !kIndexed || valid_id(tile_ids[lane], env_count);
-    FeatRow fr;
+    u32* rec = t.out.rec[lane];
     if (ok) {
-      const Env e = unpack_row(rows + lane * kRowWords);
       const Packet pk = make_packet(e);
+      FeatRow fr;
       feature_row(pk, c_stop_bits, fr);
-      ft.legal[lane][0] = pk.head.legal.w0;
-      ft.legal[lane][1] = pk.head.legal.w1;
-      ft.legal[lane][2] = pk.head.legal.w2;
+      feature_record(fr, rec);
+      t.out.legal[lane][0] = pk.head.legal.w0;
+      t.out.legal[lane][1] = pk.head.legal.w1;
+      t.out.legal[lane][2] = pk.head.legal.w2;
       player[i] = pk.head.player;
       done[i] = e.done != 0;
       status[i] = (i16)pk.head.status;
-    } else {  // torch50_ext.cu:71-87
-      for (int k = 0; k < kFeatWords; ++k) fr.w[k] = 0;
-      for (int k = 0; k < kFeatDense; ++k) fr.d[k] = 0.0f;
-      ft.legal[lane][0] = ft.legal[lane][1] = ft.legal[lane][2] = 0;
+    } else {  // invalid id (torch50_ext.cu:71-87): an all-zero row
+      for (int k = 0; k < kFeatRecord; ++k) rec[k] = 0u;
+      t.out.legal[lane][0] = t.out.legal[lane][1] = t.out.legal[lane][2] = 0;
       player[i] = 0;
       done[i] = 1;
       status[i] = CUGO_INVALID_INDEX_STATUS;
     }
-    for (int k = 0; k < kFeatWords; ++k) ft.w[lane][k] = fr.w[k];
-    for (int k = 0; k < kFeatDense; ++k) ft.d[lane][k] = fr.d[k];
   }
   __syncthreads();
-  // Features: count rows x 180 float4, consecutive lanes -> consecutive float4.
+  // Features: lane owns float4 columns q = lane, lane + 64, lane + 128 (< 180) of every
+  // row, so a store instruction covers 1 KiB of one row and each lane resolves its
+  // twelve feature sources once.
+  constexpr int kQuads = kFeatureCount / 4;  // 180
+  u32 src[3][4];
+  for (int c = 0; c < 3; ++c)
+    for (int k = 0; k < 4; ++k) {
+      const u32 q = (u32)(lane + kTile * c);
+      src[c][k] = feature_source(q < (u32)kQuads ? q * 4u + (u32)k : 719u);
+    }
   float4* fout = reinterpret_cast<float4*>(features + base * kFeatureCount);
-  const int quads = count * (kFeatureCount / 4);
-  for (int q = lane; q < quads; q += kTile) {
-    const int r = q / (kFeatureCount / 4);
-    const u32 f = (u32)(q - r * (kFeatureCount / 4)) * 4u;
-    float4 v;
-    v.x = feature_at(ft.w[r], ft.d[r], f);
-    v.y = feature_at(ft.w[r], ft.d[r], f + 1);
-    v.z = feature_at(ft.w[r], ft.d[r], f + 2);
-    v.w = feature_at(ft.w[r], ft.d[r], f + 3);
-    fout[q] = v;
+  for (int r = 0; r < count; ++r) {
+    const u32* rec = t.out.rec[r];
+    for (int c = 0; c < 3; ++c) {
+      const int q = lane + kTile * c;
+      if (q < kQuads) {
+        float4 v;
+        v.x = feature_from_record(rec, src[c][0]);
+        v.y = feature_from_record(rec, src[c][1]);
+        v.z = feature_from_record(rec, src[c][2]);
+        v.w = feature_from_record(rec, src[c][3]);
+        fout[r * kQuads + q] = v;
+      }
+    }
   }
-  // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0).
+  // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0); word
+  // w holds tile bytes 4w..4w+3, i.e. actions a..a+3 of row r unless it straddles rows.
   u8* lout = legal + base * kActionCount;
   const int bytes = count * kActionCount;
   const int full = bytes / 4;
   for (int w = lane; w < full; w += kTile) {
-    u32 packed = 0;
-    for (int b = 0; b < 4; ++b) {
-      const int at = w * 4 + b;
-      const int r = at / kActionCount;
-      const int a = at - r * kActionCount;
-      const u64 word = ft.legal[r][a >> 6];
-      packed |= (u32)((word >> (a & 63)) & 1u) << (8 * b);
+    const int b0 = w * 4;
+    const int r = b0 / kActionCount;
+    const int a = b0 - r * kActionCount;
+    u32 packed;
+    if (a + 3 < kActionCount) {
+      const u64* m = t.out.legal[r];
+      const int lo = a >> 6, sh = a & 63;
+      u64 bits = m[lo] >> sh;
+      if (sh > 60) bits |= m[lo + 1] << (64 - sh);
+      packed = spread4((u32)(bits & 0xFu));
+    } else {
+      packed = 0;
+      for (int b = 0; b < 4; ++b) {
+        const int at = b0 + b;
+        const int rr = at / kActionCount;
+        const int aa = at - rr * kActionCount;
+        packed |= (u32)((t.out.legal[rr][aa >> 6] >> (aa & 63)) & 1u) << (8 * b);
+      }
     }
     reinterpret_cast<u32*>(lout)[w] = packed;
   }
   for (int at = full * 4 + lane; at < bytes; at += kTile) {
     const int r = at / kActionCount;
     const int a = at - r * kActionCount;
-    lout[at] = (u8)((ft.legal[r][a >> 6] >> (a & 63)) & 1u);
+    lout[at] = (u8)((t.out.legal[r][a >> 6] >> (a & 63)) & 1u);
   }
 }
 

@@ -165,10 +165,10 @@ class RefEngine:
 
     # -- whole random-policy games and branch work -----------------------------------
     def play_random(self, base_seed: int, n: int, threads: int = 1, record_games: int = 0,
-                    record_cap: int = 64):
-        digest = np.zeros(n, dtype=np.uint64)
-        steps = np.zeros(n, dtype=np.int32)
-        reward = np.zeros(n, dtype=np.int64)
+                    record_cap: int = 64, outputs: bool = True):
+        digest = np.zeros(n, dtype=np.uint64) if outputs else None
+        steps = np.zeros(n, dtype=np.int32) if outputs else None
+        reward = np.zeros(n, dtype=np.int64) if outputs else None
         records = None
         if record_games:
             records = np.zeros((record_games, record_cap, self.record_bytes), dtype=np.uint8)

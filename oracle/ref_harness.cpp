@@ -266,7 +266,9 @@ std::int64_t cugo_ref_reward0(const std::uint8_t* row) { return cg::torch_reward
 // If records != nullptr, the first `record_games` games also dump every step record:
 //   [features f32 x720][mask u8 x179][player u8][done u8][status i16][action i64]
 //   [reward f32][done u8][nagari u8][status i16][committed u8][events i64 x9]
-// with at most `record_cap` steps per game.  Returns the total number of decisions.
+// with at most `record_cap` steps per game.  Null output arrays are skipped (the
+// timed CPU baseline passes none, so it does only the engine work).  Returns the total
+// number of decisions.
 constexpr int kRecordBytes = kF * 4 + kA + 1 + 1 + 2 + 8 + 4 + 1 + 1 + 2 + 1 + kE * 8;
 
 int cugo_ref_record_bytes() { return kRecordBytes; }
@@ -312,15 +314,15 @@ std::int64_t cugo_ref_play_random(std::uint64_t base_seed, std::int64_t n, int t
       std::int64_t words[kE];
       cg::pack_torch_event50(ev, words);
       std::memcpy(q + 9, words, sizeof words);
-      h = fnv(h, rec, kRecordBytes);
+      if (digest != nullptr) h = fnv(h, rec, kRecordBytes);
       if (records != nullptr && i < record_games && count < record_cap)
         std::memcpy(records + (i * record_cap + count) * kRecordBytes, rec, kRecordBytes);
       ++count;
       if (m == 0) break;
     }
-    digest[i] = h;
-    steps[i] = count;
-    final_reward[i] = cg::torch_reward0_50(env);
+    if (digest != nullptr) digest[i] = h;
+    if (steps != nullptr) steps[i] = count;
+    if (final_reward != nullptr) final_reward[i] = cg::torch_reward0_50(env);
     total.fetch_add(count);
   });
   return total.load();
