@@ -13,6 +13,8 @@ Also reported (not timed into `value`):
                 timed with HIP events on the stream it runs on
   branch        4,096 roots (3-15 seeded random decisions deep) x 256 children:
                 branch_indexed (clone + step) and the observation of all children
+  decode        sequence-policy decode over a [4, 4,096, 8, 320, 32] bf16 KV cache:
+                tokens/s of the 4-layer step and the HIP decode kernel's HBM fraction
   cpu_baseline  the reference engine (oracle/_ref) on this host's cores, same protocol,
                 bounded sample
 """
@@ -45,6 +47,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--branch-iters", type=int, default=20)
     p.add_argument("--no-branch", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--decode-steps", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     return p.parse_args()
 
@@ -145,6 +149,109 @@ def branch_workload(ext, torch, iters: int) -> dict:
     }
 
 
+def event_lengths(ext, torch, games: int, base_seed: int) -> "torch.Tensor":
+    """Committed events per game of `games` seeded random-policy games (seed = base + j,
+    first = j & 1), played to the end on the GPU engine."""
+    dev = torch.device("cuda")
+    idx = torch.arange(games, dtype=torch.int64, device=dev)
+    states = ext.create(idx + base_seed, idx & 1)
+    gen = torch.zeros(games, dtype=torch.int32, device=dev)
+    sampler = ext.seed_samplers(games, base_seed, gen)
+    count = torch.zeros(games, dtype=torch.int64, device=dev)
+    for _ in range(128):
+        _, legal, _, done, _ = ext.observe(states)
+        if bool(done.all()):
+            break
+        actions = ext.sample_uniform(legal, sampler)
+        out = ext.step_events_indexed(states, idx, actions)
+        count += (out[4] & ~done).long()
+    return count
+
+
+def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) -> dict:
+    """Sequence-policy decode: a 4-layer causal transformer (d_model 256, 8 heads of 32,
+    GELU MLP 1024, pre-norm, bf16, N(0, 0.02) weights from seed 0) runs one query token
+    per cache row through `cached_step` (per layer: in-projection GEMM -> KV append fused
+    with the HIP decode attention -> out-projection and MLP GEMMs).  KV cache
+    [4, 4,096, 8, 320, 32] bf16.  Row lengths come from seeded random-policy games: row i
+    concatenates the event logs of games i, i + 4,096, i + 8,192, ... (one opening token
+    plus each game's events) while they fit below 320 slots ("stress", pos ~300), or holds
+    one game (the reference's 50-slot regime, "natural")."""
+    from torch import nn
+
+    from cugo_amd.seq_decode import KVCache, cached_step
+    from cugo_amd.cugo_seq_attention50 import decode_attention_append
+
+    dev = torch.device("cuda")
+    layers, d, heads = 4, 256, 8
+    dh = d // heads
+    torch.manual_seed(0)
+    layer = nn.TransformerEncoderLayer(d, heads, 4 * d, dropout=0.0, activation="gelu",
+                                       batch_first=True, norm_first=True)
+    model = nn.Module()
+    model.encoder = nn.TransformerEncoder(layer, layers, enable_nested_tensor=False)
+    with torch.no_grad():
+        for p in model.parameters():
+            p.normal_(0.0, 0.02)
+    model = model.to(dev).to(torch.bfloat16).eval()
+
+    per_row = 16
+    ev = event_lengths(ext, torch, rows * per_row, SEED_BASE + 0xDEC0DE).view(per_row, rows)
+    natural = (1 + ev[0]).clamp_max(slots - 1)
+    total = torch.cumsum(ev, 0) + 1  # opening token + events of the first k games
+    fits = total <= slots - 1
+    stress = torch.where(fits, total, torch.zeros_like(total)).max(0).values
+    stress = torch.where(stress == 0, natural, stress)
+
+    cache = KVCache(layers, rows, heads, d, slots, dev)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    for t in (cache.k, cache.v):
+        t.copy_((torch.randn(t.shape, generator=gen, device=dev) * 0.5).to(t.dtype))
+    x = (torch.randn(rows, d, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+    out = {}
+    stream = torch.cuda.current_stream()
+    with torch.no_grad():
+        for name, lengths in (("stress", stress), ("natural", natural)):
+            cache.length.copy_(lengths)
+            for _ in range(3):
+                cached_step(model, cache, x)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                cached_step(model, cache, x)
+            torch.cuda.synchronize()
+            step_s = (time.perf_counter() - t0) / steps
+            # The decode kernel alone, same call as inside the step (layer 0's cache).
+            q = (torch.randn(rows, heads, dh, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+            kn, vn = q.clone(), q.clone()
+            pos = lengths.clamp_max(slots - 1)
+            for _ in range(3):
+                decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos)
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 50
+            ev0.record(stream)
+            for _ in range(reps):
+                decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos)
+            ev1.record(stream)
+            torch.cuda.synchronize()
+            kernel_ms = ev0.elapsed_time(ev1) / reps
+            # cache reads (slots < pos; slot pos comes from registers) + q, k_new, v_new
+            # reads + k/v slot writes + out writes + pos
+            row_bytes = heads * dh * 2
+            nbytes = int(pos.sum()) * row_bytes * 2 + rows * row_bytes * 6 + rows * 8
+            gbs = nbytes / (kernel_ms * 1e-3) / 1e9
+            out[name] = {"tokens_per_s": round(rows / step_s, 1),
+                         "step_ms": round(step_s * 1e3, 4),
+                         "mean_pos": round(float(pos.float().mean()), 2),
+                         "max_pos": int(pos.max()),
+                         "decode_kernel_ms": round(kernel_ms, 4),
+                         "decode_bytes": nbytes,
+                         "decode_gbs": round(gbs, 1),
+                         "decode_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    out["cache"] = [layers, rows, heads, slots, dh]
+    return out
+
+
 def cpu_baseline(seconds: float) -> dict:
     """The reference engine (oracle/_ref) on the host cores, same random-policy protocol
     (observe + sample + step_events per decision), growing the sample to ~`seconds`."""
@@ -206,6 +313,8 @@ def main() -> None:
     }
     if not args.no_branch:
         result["branch"] = branch_workload(ext, torch, args.branch_iters)
+    if not args.no_decode:
+        result["decode"] = decode_workload(ext, torch, args.decode_steps)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

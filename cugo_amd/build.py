@@ -70,7 +70,8 @@ def generate_stop_bits(force: bool = True) -> Path:
 def build_library() -> Path:
     generate_stop_bits()
     out = PKG / "libcugo_hip.so"
-    _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "kernels.hip"), "-o", str(out)])
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "kernels.hip"), str(CSRC / "decode.hip"),
+          "-o", str(out)])
     return out
 
 

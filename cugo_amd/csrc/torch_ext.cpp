@@ -12,6 +12,7 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <cmath>
 #include <cstdint>
 #include <vector>
 
@@ -277,6 +278,91 @@ torch::Tensor seed_samplers(int64_t n, int64_t base_seed, torch::Tensor generati
   return sampler;
 }
 
+int dtype_code(at::ScalarType t) {
+  switch (t) {
+    case at::kFloat:
+      return CUGO_DTYPE_F32;
+    case at::kHalf:
+      return CUGO_DTYPE_F16;
+    case at::kBFloat16:
+      return CUGO_DTYPE_BF16;
+    default:
+      TORCH_CHECK(false, "decode_attention supports float32, float16 and bfloat16, got ", t);
+  }
+}
+
+// Checks shared by both decode entry points.
+void check_decode(const torch::Tensor& q, const torch::Tensor& keys, const torch::Tensor& values,
+                  const torch::Tensor& pos, const c10::optional<torch::Tensor>& rows) {
+  TORCH_CHECK(q.is_cuda(), "q must be a CUDA tensor");
+  TORCH_CHECK(q.dim() == 3, "q must have shape [n, heads, dh]");
+  TORCH_CHECK(keys.dim() == 4 && values.sizes() == keys.sizes(),
+              "keys and values must have the same shape [rows, heads, slots, dh]");
+  TORCH_CHECK(keys.is_contiguous() && values.is_contiguous(), "keys and values must be contiguous");
+  TORCH_CHECK(keys.scalar_type() == values.scalar_type(), "keys and values must have one dtype");
+  TORCH_CHECK(keys.size(1) == q.size(1) && keys.size(3) == q.size(2),
+              "q [n, heads, dh] does not match the cache's heads and dh");
+  check_same_device(q, keys, "q", "keys");
+  check_same_device(q, values, "q", "values");
+  check_1d(pos, at::kLong, "pos");
+  TORCH_CHECK(pos.numel() == q.size(0), "pos must have one entry per query");
+  check_same_device(q, pos, "q", "pos");
+  if (rows.has_value()) {
+    check_1d(*rows, at::kLong, "rows");
+    TORCH_CHECK(rows->numel() == q.size(0), "rows must have one entry per query");
+    check_same_device(q, *rows, "q", "rows");
+  }
+}
+
+// decode_attention(q, keys, values, pos, rows=None)
+// (python/cugo_seq_attention50.py:43-62): q [n, heads, dh]; keys/values
+// [rows, heads, slots, dh]; pos/rows int64 [n] -> [n, heads, dh] in q's dtype.
+torch::Tensor decode_attention(torch::Tensor q, torch::Tensor keys, torch::Tensor values,
+                               torch::Tensor pos, c10::optional<torch::Tensor> rows) {
+  check_decode(q, keys, values, pos, rows);
+  const DeviceGuard guard(q.device());
+  q = q.contiguous();
+  auto out = torch::empty_like(q);
+  const int64_t dh = q.size(2);
+  const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(dh)));
+  check_call(cugo_decode_attention(dtype_code(q.scalar_type()), dtype_code(keys.scalar_type()),
+                                   q.data_ptr(), keys.data_ptr(), values.data_ptr(),
+                                   pos.data_ptr<int64_t>(),
+                                   rows.has_value() ? rows->data_ptr<int64_t>() : nullptr,
+                                   q.size(0), q.size(1), dh, keys.size(2), keys.size(0), scale,
+                                   out.data_ptr(), stream()),
+             "decode_attention");
+  return out;
+}
+
+// decode_attention_append(q, k_new, v_new, keys, values, pos, rows=None): writes k_new and
+// v_new ([n, heads, dh], cast to the cache dtype) to slot pos of each query's row, in place,
+// then attends as decode_attention (python/cugo_seq50.py:313-320 in one launch).
+torch::Tensor decode_attention_append(torch::Tensor q, torch::Tensor k_new, torch::Tensor v_new,
+                                      torch::Tensor keys, torch::Tensor values, torch::Tensor pos,
+                                      c10::optional<torch::Tensor> rows) {
+  check_decode(q, keys, values, pos, rows);
+  TORCH_CHECK(k_new.sizes() == q.sizes() && v_new.sizes() == q.sizes(),
+              "k_new and v_new must have q's shape [n, heads, dh]");
+  check_same_device(q, k_new, "q", "k_new");
+  check_same_device(q, v_new, "q", "v_new");
+  const DeviceGuard guard(q.device());
+  q = q.contiguous();
+  k_new = k_new.to(keys.scalar_type()).contiguous();
+  v_new = v_new.to(keys.scalar_type()).contiguous();
+  auto out = torch::empty_like(q);
+  const int64_t dh = q.size(2);
+  const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(dh)));
+  check_call(cugo_decode_attention_append(
+                 dtype_code(q.scalar_type()), dtype_code(keys.scalar_type()), q.data_ptr(),
+                 k_new.data_ptr(), v_new.data_ptr(), keys.data_ptr(), values.data_ptr(),
+                 pos.data_ptr<int64_t>(), rows.has_value() ? rows->data_ptr<int64_t>() : nullptr,
+                 q.size(0), q.size(1), dh, keys.size(2), keys.size(0), scale, out.data_ptr(),
+                 stream()),
+             "decode_attention_append");
+  return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -296,6 +382,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("sample_uniform", &sample_uniform, "Uniform legal action per row (xorshift64)");
   m.def("reset_done", &reset_done, "Re-create finished rows with their next seed");
   m.def("seed_samplers", &seed_samplers, "Per-row sampler state from the row seeds");
+  m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
+        pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
+        pybind11::arg("rows") = pybind11::none());
+  m.def("decode_attention_append", &decode_attention_append,
+        "Write the new key/value at slot pos, then single-query attention",
+        pybind11::arg("q"), pybind11::arg("k_new"), pybind11::arg("v_new"),
+        pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
+        pybind11::arg("rows") = pybind11::none());
   m.attr("FEATURE_COUNT") = pybind11::int_(CUGO_FEATURE_COUNT);
   m.attr("ACTION_COUNT") = pybind11::int_(CUGO_ACTION_COUNT);
   m.attr("PRIMARY_ACTION_COUNT") = pybind11::int_(CUGO_PRIMARY_ACTION_COUNT);

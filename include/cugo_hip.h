@@ -114,6 +114,46 @@ int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t ba
 int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation,
                        uint64_t* sampler, hipStream_t stream);
 
+/*
+ * Single-query decode attention over a per-row KV cache
+ * (python/cugo_seq_attention50.py:43-62, the Triton `_decode_kernel` at :21-40 and its
+ * two-matmul fallback at :58-62):
+ *
+ *   out[i, h, :] = sum_t softmax_t(scale * q[i,h,:] . keys[r,h,t,:]) values[r,h,t,:]
+ *   with r = rows[i] (rows == NULL: r = i) and t = 0 .. min(pos[i], slots - 1).
+ *
+ *   q, out        [n, heads, dh] of q_dtype, contiguous
+ *   keys, values  [cache_rows, heads, slots, dh] of kv_dtype, contiguous, 16-byte aligned
+ *   pos, rows     int64 [n]
+ * Softmax and accumulation are fp32; out is rounded to q_dtype.  dh is 16, 32, 64 or 128
+ * (dh * element size >= 16 bytes).  A query whose pos is negative, or whose row is outside
+ * [0, cache_rows), gets a NaN output (the reference's softmax over no slot is NaN) and
+ * reads no cache memory.  Returns -1 for a bad count or null pointer, -2 for an
+ * unsupported dtype, -3 for an unsupported dh, -4 for a misaligned cache pointer.
+ */
+#define CUGO_DTYPE_F32 0
+#define CUGO_DTYPE_F16 1
+#define CUGO_DTYPE_BF16 2
+
+int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, const void* keys,
+                          const void* values, const int64_t* pos, const int64_t* rows,
+                          int64_t n, int64_t heads, int64_t dh, int64_t slots,
+                          int64_t cache_rows, float scale, void* out, hipStream_t stream);
+
+/*
+ * The reference caller's KV append fused with the decode (python/cugo_seq50.py:313-320:
+ * index_put_ of the new key/value at slot pos[i] of row rows[i], then decode_attention):
+ * k_new/v_new [n, heads, dh] of kv_dtype (16-byte aligned) are written to slot
+ * min(pos[i], slots - 1) of each query's row, and the query attends slots 0..pos as
+ * above, taking the new slot from registers.  Two queries naming the same row write the
+ * same slot (as index_put_ with repeated indices, the value that lands is either one).
+ */
+int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, const void* k_new,
+                                 const void* v_new, void* keys, void* values,
+                                 const int64_t* pos, const int64_t* rows, int64_t n,
+                                 int64_t heads, int64_t dh, int64_t slots, int64_t cache_rows,
+                                 float scale, void* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

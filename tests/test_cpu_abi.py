@@ -42,7 +42,7 @@ def test_extension_module_constants():
                 720, 179, 127, 127, 9, 8, 248, 0)
     for op in ("create", "observe", "observe_indexed", "step", "step_indexed", "clone_indexed",
                "branch_indexed", "hands_indexed", "stock_indexed", "step_events_indexed",
-               "start"):
+               "start", "decode_attention", "decode_attention_append"):
         assert callable(getattr(m, op))
 
 

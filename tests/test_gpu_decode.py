@@ -1,0 +1,221 @@
+"""GPU parity of the HIP decode attention (cugo_decode_attention / _append) against the
+reference's matmul formulation (python/cugo_seq_attention50.py:58-62, restated in
+oracle/decode_ref.py) and the float64 brute force.
+
+Tolerances: relative Frobenius error <= 1e-2 against the matmul path in bf16 (the
+north-star bar; the matmul path itself rounds scores and probabilities to bf16), and
+<= 4e-3 against the float64 definition (bf16 output rounding is 2^-9 relative).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from cugo_amd.cugo_seq_attention50 import decode_attention, decode_attention_append
+from oracle.decode_ref import brute_force, matmul_path
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def rel_err(got: torch.Tensor, want) -> float:
+    got = got.double().cpu()
+    want = torch.as_tensor(want).double().cpu()
+    return float(torch.linalg.vector_norm(got - want) / torch.linalg.vector_norm(want))
+
+
+def make_case(n, rows, heads, slots, dh, seed, qdt=torch.bfloat16, kvdt=torch.bfloat16,
+              qscale=0.5, kscale=0.5):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    q = (torch.randn(n, heads, dh, generator=g) * qscale).to(qdt).to(DEV)
+    k = (torch.randn(rows, heads, slots, dh, generator=g) * kscale).to(kvdt).to(DEV)
+    v = torch.randn(rows, heads, slots, dh, generator=g).to(kvdt).to(DEV)
+    return q, k, v
+
+
+def test_small_shapes_against_float64(ext):
+    announce("decode small shapes vs float64")
+    for dh, kvdt, qdt in ((32, torch.bfloat16, torch.bfloat16), (16, torch.bfloat16, torch.bfloat16),
+                          (64, torch.bfloat16, torch.bfloat16), (128, torch.bfloat16, torch.bfloat16),
+                          (32, torch.bfloat16, torch.float32), (32, torch.float16, torch.float16),
+                          (32, torch.float32, torch.float32), (64, torch.float32, torch.bfloat16)):
+        n, rows, heads, slots = 37, 23, 8, 77
+        q, k, v = make_case(n, rows, heads, slots, dh, seed=dh + 3 * n, qdt=qdt, kvdt=kvdt)
+        g = np.random.default_rng(dh)
+        row_ids = torch.from_numpy(g.integers(0, rows, n)).to(DEV)
+        pos = torch.from_numpy(g.integers(0, slots, n)).to(DEV)
+        pos[:4] = torch.tensor([0, slots - 1, slots + 5, 63], device=DEV)
+        out = decode_attention(q, k, v, pos, rows=row_ids)
+        assert out.dtype == q.dtype and out.shape == q.shape
+        want = brute_force(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                           v.float().cpu().numpy(), pos.cpu().numpy(), row_ids.cpu().numpy())
+        tol = 4e-3 if qdt == torch.bfloat16 else 1e-5 if qdt == torch.float32 else 1e-3
+        err = rel_err(out, want)
+        assert err <= tol, (dh, kvdt, qdt, err)
+
+
+def test_reference_shape_against_matmul_path(ext):
+    """The reference's cache: [2 x 4,096 rows, 8 heads, 50 slots, 32] bf16, 4,096 queries
+    on distinct random rows, ragged pos in [0, 49]."""
+    announce("decode reference shape vs matmul path")
+    q, k, v = make_case(4096, 8192, 8, 50, 32, seed=5)
+    g = np.random.default_rng(6)
+    rows = torch.from_numpy(g.permutation(8192)[:4096]).to(DEV)
+    pos = torch.from_numpy(g.integers(0, 50, 4096)).to(DEV)
+    out = decode_attention(q, k, v, pos, rows=rows)
+    want = matmul_path(q, k, v, pos, rows)
+    assert rel_err(out, want.float()) <= 1e-2
+    # no rows argument: row i
+    out0 = decode_attention(q, k[:4096].contiguous(), v[:4096].contiguous(), pos)
+    want0 = matmul_path(q, k[:4096], v[:4096], pos)
+    assert rel_err(out0, want0.float()) <= 1e-2
+
+
+def test_320_slot_cache_against_matmul_path(ext):
+    """One layer of the 320-slot cache [4,096, 8, 320, 32] bf16 with ragged pos up to 319."""
+    announce("decode 320-slot cache vs matmul path")
+    q, k, v = make_case(4096, 4096, 8, 320, 32, seed=7)
+    g = np.random.default_rng(8)
+    pos = torch.from_numpy(g.integers(0, 320, 4096)).to(DEV)
+    pos[:3] = torch.tensor([0, 319, 255], device=DEV)
+    out = decode_attention(q, k, v, pos)
+    want = matmul_path(q, k, v, pos)
+    assert rel_err(out, want.float()) <= 1e-2
+    # per-query check as well: no query may be far off even if the aggregate is close
+    per = ((out.float() - want.float()).norm(dim=(1, 2)) / want.float().norm(dim=(1, 2)))
+    assert float(per.max()) <= 2e-2
+
+
+def test_append_equals_index_put_then_decode(ext):
+    announce("decode append vs index_put_ + decode")
+    n, rows, heads, slots, dh = 1000, 2048, 8, 50, 32
+    q, k, v = make_case(n, rows, heads, slots, dh, seed=9)
+    g = torch.Generator(device="cpu").manual_seed(10)
+    k_new = torch.randn(n, heads, dh, generator=g).to(torch.bfloat16).to(DEV)
+    v_new = torch.randn(n, heads, dh, generator=g).to(torch.bfloat16).to(DEV)
+    row_ids = torch.from_numpy(np.random.default_rng(11).permutation(rows)[:n]).to(DEV)
+    pos = torch.from_numpy(np.random.default_rng(12).integers(0, slots, n)).to(DEV)
+    pos[:2] = torch.tensor([0, slots - 1], device=DEV)
+    k1, v1 = k.clone(), v.clone()
+    flat_rows = (row_ids.view(n, 1) * heads + torch.arange(heads, device=DEV).view(1, heads)).flatten()
+    flat_pos = pos.repeat_interleave(heads)
+    k1.view(-1, slots, dh).index_put_((flat_rows, flat_pos), k_new.reshape(n * heads, dh))
+    v1.view(-1, slots, dh).index_put_((flat_rows, flat_pos), v_new.reshape(n * heads, dh))
+    want = decode_attention(q, k1, v1, pos, rows=row_ids)
+    k2, v2 = k.clone(), v.clone()
+    got = decode_attention_append(q, k_new, v_new, k2, v2, pos, rows=row_ids)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert rel_err(got, want.float()) <= 2e-3
+    assert rel_err(got, matmul_path(q, k1, v1, pos, row_ids).float()) <= 1e-2
+
+
+def test_nan_and_clamp_semantics(ext):
+    announce("decode NaN / clamp semantics")
+    q, k, v = make_case(6, 4, 8, 10, 32, seed=13)
+    rows = torch.tensor([0, 1, 2, 3, 4, -1], device=DEV)
+    pos = torch.tensor([-1, 3, 9, 50, 2, 2], device=DEV)
+    out = decode_attention(q, k, v, pos, rows=rows).float()
+    assert torch.isnan(out[0]).all() and torch.isnan(out[4]).all() and torch.isnan(out[5]).all()
+    assert not torch.isnan(out[1:4]).any()
+    clamp = decode_attention(q[3:4], k, v, torch.tensor([9], device=DEV), rows=rows[3:4])
+    assert torch.equal(out[3].to(torch.bfloat16), clamp[0])
+    empty = decode_attention(q[:0], k, v, pos[:0], rows=rows[:0])
+    assert empty.shape == (0, 8, 32)
+
+
+def test_argument_errors(ext):
+    announce("decode argument errors")
+    q, k, v = make_case(4, 4, 8, 10, 32, seed=14)
+    pos = torch.zeros(4, dtype=torch.int64, device=DEV)
+    with pytest.raises(RuntimeError):
+        decode_attention(q, k[:, :4].contiguous(), v[:, :4].contiguous(), pos)  # heads mismatch
+    with pytest.raises(RuntimeError):
+        decode_attention(q, k.transpose(1, 2), v.transpose(1, 2), pos)  # not contiguous
+    with pytest.raises(RuntimeError):
+        decode_attention(q, k, v, pos.int())
+    with pytest.raises(RuntimeError):
+        decode_attention(q.cpu(), k, v, pos)
+    q48, k48, v48 = make_case(2, 2, 2, 4, 48, seed=15)
+    with pytest.raises(RuntimeError):
+        decode_attention(q48, k48, v48, pos[:2])  # dh = 48 is not supported
+
+
+def _layered_model(layers=4, d=256, heads=8, seed=0):
+    torch.manual_seed(seed)
+    layer = torch.nn.TransformerEncoderLayer(d, heads, 4 * d, dropout=0.0, activation="gelu",
+                                             batch_first=True, norm_first=True)
+    enc = torch.nn.TransformerEncoder(layer, layers, enable_nested_tensor=False)
+    model = torch.nn.Module()
+    model.encoder = enc
+    with torch.no_grad():
+        for p in model.parameters():
+            p.normal_(0.0, 0.02)
+    return model.to(DEV).to(torch.bfloat16).eval()
+
+
+def _reference_cached_step(model, cache, x, rows):
+    """python/cugo_seq50.py:291-322 restated with the matmul decode path."""
+    import torch.nn.functional as F
+
+    n, d = x.shape
+    heads, dh = cache.heads, d // cache.heads
+    pos = cache.length.index_select(0, rows).clamp_max(cache.slots - 1)
+    flat_rows = (rows.view(n, 1) * heads + torch.arange(heads, device=DEV).view(1, heads)).flatten()
+    flat_pos = pos.repeat_interleave(heads)
+    for i, layer in enumerate(model.encoder.layers):
+        attn = layer.self_attn
+        q, k, v = F.linear(layer.norm1(x), attn.in_proj_weight, attn.in_proj_bias).chunk(3, -1)
+        kc, vc = cache.k[i], cache.v[i]
+        kc.view(-1, cache.slots, dh).index_put_((flat_rows, flat_pos), k.reshape(n * heads, dh).to(kc.dtype))
+        vc.view(-1, cache.slots, dh).index_put_((flat_rows, flat_pos), v.reshape(n * heads, dh).to(vc.dtype))
+        a = matmul_path(q.reshape(n, heads, dh), kc, vc, pos, rows)
+        x = x + attn.out_proj(a.reshape(n, d))
+        x = x + layer.linear2(layer.activation(layer.linear1(layer.norm2(x))))
+    return x
+
+
+def test_cached_step_matches_reference_and_replays_in_a_graph(ext):
+    """Four steps of the 4-layer d256 policy decode through the fused HIP step and the
+    reference formulation; then the fused step captured in a HIP graph and replayed."""
+    announce("decode cached_step vs reference, graph replay")
+    from cugo_amd.seq_decode import KVCache, cached_step
+
+    model = _layered_model()
+    rows_n, n = 512, 256
+    ca = KVCache(4, rows_n, 8, 256, 50, torch.device(DEV))
+    cb = KVCache(4, rows_n, 8, 256, 50, torch.device(DEV))
+    g = torch.Generator(device="cpu").manual_seed(16)
+    with torch.no_grad():
+        for step in range(4):
+            rows = torch.randperm(rows_n, generator=g)[:n].to(DEV)
+            x = (torch.randn(n, 256, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+            ha = cached_step(model, ca, x, rows=rows)
+            hb = _reference_cached_step(model, cb, x, rows)
+            assert rel_err(ha, hb.float()) <= 1e-2, step
+            ca.length.index_add_(0, rows, torch.ones_like(rows))
+            cb.length.index_add_(0, rows, torch.ones_like(rows))
+        assert rel_err(ca.k.float(), cb.k.float()) <= 1e-2
+
+        rows = torch.randperm(rows_n, generator=g)[:n].to(DEV)
+        x = (torch.randn(n, 256, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+        k0, v0 = ca.k.clone(), ca.v.clone()
+        eager = cached_step(model, ca, x, rows=rows)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            cached_step(model, ca, x, rows=rows)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = cached_step(model, ca, x, rows=rows)
+        for _ in range(3):
+            ca.k.copy_(k0)
+            ca.v.copy_(v0)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert rel_err(out, eager.float()) <= 1e-3
