@@ -48,6 +48,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-branch", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
     p.add_argument("--decode-steps", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     return p.parse_args()
@@ -283,6 +285,13 @@ def main() -> None:
     from cugo_amd import load_extension
 
     ext = load_extension()
+    if args.copy_probe:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     rp = random_policy(ext, torch, args.batch, args.steps, args.warmup)
     games_per_s = rp["games"] / rp["seconds"]
     ms_per_step = 1000.0 * rp["seconds"] / args.steps

@@ -106,21 +106,41 @@ __device__ inline u32 spread4(u32 x) {
   return (x & 1u) | ((x & 2u) << 7) | ((x & 4u) << 14) | ((x & 8u) << 21);
 }
 
+// One tile of 64 games per 256-thread workgroup: wave 0 runs the 64 games (one per
+// lane) and writes their records; then all four waves share the 64 x 3,059 output
+// bytes, so a wave whose games took long to compute does not store its rows alone.
+constexpr int kObsThreads = 256;
+
 template <bool kIndexed>
-__global__ __launch_bounds__(kTile) void observe_kernel(const u64* states, i64 env_count,
-                                                        const i64* ids, i64 n, float* features,
-                                                        u8* legal, u8* player, u8* done,
-                                                        i16* status) {
+__global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states, i64 env_count,
+                                                              const i64* ids, i64 n,
+                                                              float* features, u8* legal,
+                                                              u8* player, u8* done,
+                                                              i16* status) {
   __shared__ ObserveTile t;
   __shared__ i64 tile_ids[kTile];
   const i64 base = tile_base();
   const int count = tile_count(base, n);
-  const int lane = threadIdx.x;
-  if (kIndexed && lane < count) tile_ids[lane] = ids[base + lane];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kTile - 1);
+  const int wave = tid / kTile;
+  if (kIndexed && tid < count) tile_ids[tid] = ids[base + tid];
   __syncthreads();
-  stage_in(t.rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
+  {  // stage the tile's rows, all threads
+    const int words = count * kRowWords;
+    if (!kIndexed) {
+      const u64* src = states + base * kRowWords;
+      for (int j = tid; j < words; j += kObsThreads) t.rows[j] = src[j];
+    } else {
+      for (int j = tid; j < words; j += kObsThreads) {
+        const int r = j / kRowWords;
+        const i64 id = tile_ids[r];
+        t.rows[j] = valid_id(id, env_count) ? states[id * kRowWords + (j - r * kRowWords)] : 0ull;
+      }
+    }
+  }
   __syncthreads();
-  const bool active = lane < count;
+  const bool active = wave == 0 && lane < count;
   const bool ok = active && (!kIndexed || valid_id(tile_ids[lane], env_count));
   Env e;
   if (ok) e = unpack_row(t.rows + lane * kRowWords);
@@ -148,10 +168,11 @@ __global__ __launch_bounds__(kTile) void observe_kernel(const u64* states, i64 e
     }
   }
   __syncthreads();
-  // Features: lane owns float4 columns q = lane, lane + 64, lane + 128 (< 180) of every
-  // row, so a store instruction covers 1 KiB of one row and each lane resolves its
-  // twelve feature sources once.
+  // Features: wave w stores rows w, w + 4, ...; lane owns float4 columns q = lane,
+  // lane + 64, lane + 128 (< 180) of each, so a store instruction covers 1 KiB of one
+  // row and each lane resolves its twelve feature sources once.
   constexpr int kQuads = kFeatureCount / 4;  // 180
+  constexpr int kWaves = kObsThreads / kTile;
   u32 src[3][4];
   for (int c = 0; c < 3; ++c)
     for (int k = 0; k < 4; ++k) {
@@ -159,7 +180,7 @@ __global__ __launch_bounds__(kTile) void observe_kernel(const u64* states, i64 e
       src[c][k] = feature_source(q < (u32)kQuads ? q * 4u + (u32)k : 719u);
     }
   float4* fout = reinterpret_cast<float4*>(features + base * kFeatureCount);
-  for (int r = 0; r < count; ++r) {
+  for (int r = wave; r < count; r += kWaves) {
     const u32* rec = t.out.rec[r];
     for (int c = 0; c < 3; ++c) {
       const int q = lane + kTile * c;
@@ -178,7 +199,7 @@ __global__ __launch_bounds__(kTile) void observe_kernel(const u64* states, i64 e
   u8* lout = legal + base * kActionCount;
   const int bytes = count * kActionCount;
   const int full = bytes / 4;
-  for (int w = lane; w < full; w += kTile) {
+  for (int w = tid; w < full; w += kObsThreads) {
     const int b0 = w * 4;
     const int r = b0 / kActionCount;
     const int a = b0 - r * kActionCount;
@@ -200,7 +221,7 @@ __global__ __launch_bounds__(kTile) void observe_kernel(const u64* states, i64 e
     }
     reinterpret_cast<u32*>(lout)[w] = packed;
   }
-  for (int at = full * 4 + lane; at < bytes; at += kTile) {
+  for (int at = full * 4 + tid; at < bytes; at += kObsThreads) {
     const int r = at / kActionCount;
     const int a = at - r * kActionCount;
     lout[at] = (u8)((t.out.legal[r][a >> 6] >> (a & 63)) & 1u);
@@ -339,10 +360,17 @@ __device__ inline u64 sampler_seed(u64 seed) {
   return v != 0 ? v : 1ull;
 }
 
-// Tile of 64 mask rows staged in LDS as bytes; lane r scans its row.
+// Tile of 64 mask rows staged in LDS (coalesced dwords); lane r turns its row's 179
+// bytes into three 64-bit words and picks the rank-th set bit.  A dword of four 0/1
+// bytes becomes a nibble with one multiply: d * 0x00204081 = d + d<<7 + d<<14 + d<<21
+// puts byte k's bit at position 21 + k with no other term landing in bits 21..24.
+constexpr int kMaskWords = kTile * kActionCount / 4;  // 2,864
+
+__device__ inline u32 nibble_of_bytes(u32 d) { return ((d * 0x00204081u) >> 21) & 0xFu; }
+
 __global__ __launch_bounds__(kTile) void sample_kernel(const u8* legal, i64 n, u64* sampler,
                                                        i64* actions) {
-  __shared__ u32 masks[kTile * kActionCount / 4];
+  __shared__ u32 masks[kMaskWords + 2];  // +2: a row's last dword read may pass the tile
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int lane = threadIdx.x;
@@ -350,25 +378,36 @@ __global__ __launch_bounds__(kTile) void sample_kernel(const u8* legal, i64 n, u
   const int bytes = count * kActionCount;
   const int full = bytes / 4;
   for (int w = lane; w < full; w += kTile) masks[w] = reinterpret_cast<const u32*>(src)[w];
-  u8* mb = reinterpret_cast<u8*>(masks);
-  for (int at = full * 4 + lane; at < bytes; at += kTile) mb[at] = src[at];
+  if (lane < 2) masks[kMaskWords + lane] = 0u;
+  if (full * 4 < bytes && lane == 0) {  // partial last dword (only in a partial tile)
+    u32 d = 0;
+    for (int at = full * 4; at < bytes; ++at) d |= (u32)src[at] << (8 * (at - full * 4));
+    masks[full] = d;
+  }
   __syncthreads();
   if (lane >= count) return;
-  const u8* row = mb + lane * kActionCount;
-  u32 total = 0;
-  for (int a = 0; a < kActionCount; ++a) total += row[a] != 0;
+  const int b0 = lane * kActionCount;
+  const int k0 = b0 >> 2;
+  const int off = b0 & 3;  // the row starts at byte `off` of dword k0
+  u64 w[3] = {0, 0, 0};    // bit 4j + i = byte i of dword k0 + j
+#pragma unroll
+  for (int j = 0; j < 46; ++j)
+    w[j >> 4] |= (u64)nibble_of_bytes(masks[k0 + j]) << ((j & 15) * 4);
+  // drop the `off` leading bits, keep 179
+  const u64 m0 = (w[0] >> off) | (off ? w[1] << (64 - off) : 0ull);
+  const u64 m1 = (w[1] >> off) | (off ? w[2] << (64 - off) : 0ull);
+  const u64 m2 = (w[2] >> off) & ((1ull << (kActionCount - 128)) - 1ull);
+  const u32 c0 = popc(m0), c1 = popc(m1);
+  const u32 total = c0 + c1 + popc(m2);
   const i64 i = base + lane;
   if (total == 0) { actions[i] = -1; return; }
   u64 x = sampler[i];
   u32 pick = (u32)(xorshift64(x) % total);
   sampler[i] = x;
-  int chosen = -1;
-  for (int a = 0; a < kActionCount; ++a) {
-    if (row[a] != 0) {
-      if (pick == 0) { chosen = a; break; }
-      --pick;
-    }
-  }
+  int chosen;
+  if (pick < c0) chosen = select_rank(m0, pick);
+  else if (pick < c0 + c1) chosen = 64 + select_rank(m1, pick - c0);
+  else chosen = 128 + select_rank(m2, pick - c0 - c1);
   actions[i] = chosen;
 }
 
@@ -438,7 +477,7 @@ int cugo_observe(const uint8_t* states, int64_t n, float* features, uint8_t* leg
   if (n < 0 || (n > 0 && (!states || !features || !legal || !player || !done || !status)))
     return kBadArgument;
   if (n == 0) return 0;
-  observe_kernel<false><<<tiles(n), kTile, 0, stream>>>(
+  observe_kernel<false><<<tiles(n), kObsThreads, 0, stream>>>(
       reinterpret_cast<const u64*>(states), n, nullptr, n, features, legal, player, done,
       status);
   return launched();
@@ -451,7 +490,7 @@ int cugo_observe_indexed(const uint8_t* states, int64_t env_count, const int64_t
       (n > 0 && (!ids || !features || !legal || !player || !done || !status)))
     return kBadArgument;
   if (n == 0) return 0;
-  observe_kernel<true><<<tiles(n), kTile, 0, stream>>>(
+  observe_kernel<true><<<tiles(n), kObsThreads, 0, stream>>>(
       reinterpret_cast<const u64*>(states), env_count, ids, n, features, legal, player, done,
       status);
   return launched();
