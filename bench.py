@@ -255,11 +255,13 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
 
 
 def cpu_baseline(seconds: float) -> dict:
-    """The reference engine (oracle/_ref) on the host cores, same random-policy protocol
-    (observe + sample + step_events per decision), growing the sample to ~`seconds`."""
-    from oracle.ref import SEED_BASE as base, RefEngine
+    """The reference engine's own build (oracle/_ref; the oracle's C restatement when that
+    is absent) on the host cores, same random-policy protocol (observe + sample +
+    step_events per decision), growing the sample to ~`seconds`."""
+    from oracle.ref import REF_LIB, SEED_BASE as base, RefEngine
 
-    ref = RefEngine()
+    reference = REF_LIB.exists()
+    ref = RefEngine(reference=reference)
     threads = min(os.cpu_count() or 1, 16)
     n = 4096
     while True:
@@ -269,7 +271,8 @@ def cpu_baseline(seconds: float) -> dict:
         if dt >= seconds or n >= 1 << 24:
             break
         n = int(n * min(8.0, max(1.5, seconds / max(dt, 1e-3))))
-    return {"value": n / dt, "unit": "games/s", "cores": threads, "kind": "reference",
+    return {"value": n / dt, "unit": "games/s", "cores": threads,
+            "kind": "reference" if reference else "port",
             "sample": f"{n} random-policy games ({decisions} decisions) in {dt:.1f} s",
             "steps_per_s": decisions / dt}
 

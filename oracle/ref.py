@@ -1,10 +1,14 @@
 """ctypes binding of the oracle libraries (TEST INFRASTRUCTURE ONLY).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
-module.  It binds oracle/_ref/libcugo_ref.so: this repository's harness
-(oracle/ref_harness.cpp) compiled against the reference's own header-only engine
-(include/cugo/game/torch50.h of the reference), exposing the reference extension's
-batch operations (python/csrc/torch50_ext.cu:53-363) as CPU loops over 248-byte rows.
+module.  It binds
+  oracle/libcugo_oracle.so  the oracle: this repository's plain-C restatement of the
+                            reference engine (oracle/matgo/), and
+  oracle/_ref/libcugo_ref.so  this repository's harness (oracle/ref_harness.cpp) compiled
+                            against the reference's own header-only engine, built only
+                            where the reference checkout is present; it pins the oracle.
+Both expose the reference extension's batch operations
+(python/csrc/torch50_ext.cu:53-363) as CPU loops over 248-byte rows.
 
 Arrays are numpy; rows are uint8 [n, 248].
 """
@@ -18,6 +22,7 @@ import numpy as np
 
 ORACLE_DIR = Path(__file__).resolve().parent
 REF_LIB = ORACLE_DIR / "_ref" / "libcugo_ref.so"
+ORACLE_LIB = ORACLE_DIR / "libcugo_oracle.so"
 
 STATE_BYTES = 248
 FEATURES = 720
@@ -34,47 +39,57 @@ def _ptr(a: np.ndarray | None) -> int | None:
     return None if a is None else a.ctypes.data
 
 
-class RefEngine:
-    """The reference engine on the CPU, batch API of the reference extension."""
+class _Lib:
+    """Binds one library's batch API (`<prefix>_create`, ...) under short names."""
 
-    def __init__(self, path: Path | str = REF_LIB) -> None:
-        path = Path(path)
-        if not path.exists():
-            raise FileNotFoundError(
-                f"{path} is missing: build it with `make -C oracle ref` where the reference "
-                "checkout is present")
-        lib = ctypes.CDLL(str(path))
-        sig = {
-            "cugo_ref_state_bytes": ([], ctypes.c_int),
-            "cugo_ref_create": ([_P, _P, _I64, _P], None),
-            "cugo_ref_observe_indexed": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P], None),
-            "cugo_ref_step_indexed": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P], None),
-            "cugo_ref_start": ([_P, _I64, _P], None),
-            "cugo_ref_clone_indexed": ([_P, _P, _I64, _I64, _P], None),
-            "cugo_ref_branch_indexed": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P], None),
-            "cugo_ref_hands_indexed": ([_P, _P, _I64, _I64, _P], None),
-            "cugo_ref_stock_indexed": ([_P, _P, _I64, _I64, _P], None),
-            "cugo_ref_reward0": ([_P], ctypes.c_int64),
-            "cugo_ref_record_bytes": ([], ctypes.c_int),
-            "cugo_ref_play_random": ([ctypes.c_uint64, _I64, ctypes.c_int, _P, _P, _P, _P, _I64,
-                                      ctypes.c_int32], ctypes.c_int64),
-            "cugo_ref_branch_work": ([_P, _P, _P, _I64, ctypes.c_int, ctypes.c_int],
-                                     ctypes.c_uint64),
-        }
-        for name, (args, res) in sig.items():
-            fn = getattr(lib, name)
+    SIG = {
+        "state_bytes": ([], ctypes.c_int),
+        "create": ([_P, _P, _I64, _P], None),
+        "observe_indexed": ([_P, _P, _I64, _I64, _P, _P, _P, _P, _P], None),
+        "step_indexed": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P], None),
+        "start": ([_P, _I64, _P], None),
+        "clone_indexed": ([_P, _P, _I64, _I64, _P], None),
+        "branch_indexed": ([_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P], None),
+        "hands_indexed": ([_P, _P, _I64, _I64, _P], None),
+        "stock_indexed": ([_P, _P, _I64, _I64, _P], None),
+        "reward0": ([_P], ctypes.c_int64),
+        "record_bytes": ([], ctypes.c_int),
+        "play_random": ([ctypes.c_uint64, _I64, ctypes.c_int, _P, _P, _P, _P, _I64,
+                         ctypes.c_int32], ctypes.c_int64),
+        "branch_work": ([_P, _P, _P, _I64, ctypes.c_int, ctypes.c_int], ctypes.c_uint64),
+    }
+
+    def __init__(self, lib: ctypes.CDLL, prefix: str) -> None:
+        for name, (args, res) in self.SIG.items():
+            fn = getattr(lib, f"{prefix}_{name}")
             fn.argtypes = args
             fn.restype = res
-        self.lib = lib
-        assert lib.cugo_ref_state_bytes() == STATE_BYTES
-        self.record_bytes = lib.cugo_ref_record_bytes()
+            setattr(self, name, fn)
+
+
+class RefEngine:
+    """A CPU engine with the batch API of the reference extension.  By default the
+    oracle (this repository's plain-C restatement, oracle/matgo/); `reference=True`
+    loads the reference's own build (oracle/_ref), which pins the restatement."""
+
+    def __init__(self, path: Path | str | None = None, reference: bool = False) -> None:
+        path = Path(path) if path is not None else (REF_LIB if reference else ORACLE_LIB)
+        if not path.exists():
+            hint = ("`make -C oracle ref` where the reference checkout is present" if reference
+                    else "`make -C oracle oracle`")
+            raise FileNotFoundError(f"{path} is missing: build it with {hint}")
+        self.path = path
+        self.kind = "reference" if reference else "oracle"
+        self.lib = _Lib(ctypes.CDLL(str(path)), "cugo_ref" if reference else "cugo_oracle")
+        assert self.lib.state_bytes() == STATE_BYTES
+        self.record_bytes = self.lib.record_bytes()
 
     # -- extension operations -------------------------------------------------------
     def create(self, seeds: np.ndarray, first: np.ndarray) -> np.ndarray:
         seeds = np.ascontiguousarray(seeds, dtype=np.int64)
         first = np.ascontiguousarray(first, dtype=np.int64)
         out = np.zeros((seeds.size, STATE_BYTES), dtype=np.uint8)
-        self.lib.cugo_ref_create(_ptr(seeds), _ptr(first), seeds.size, _ptr(out))
+        self.lib.create(_ptr(seeds), _ptr(first), seeds.size, _ptr(out))
         return out
 
     def observe(self, states: np.ndarray, ids: np.ndarray | None = None):
@@ -87,7 +102,7 @@ class RefEngine:
         player = np.zeros(n, dtype=np.uint8)
         done = np.zeros(n, dtype=np.uint8)
         status = np.zeros(n, dtype=np.int16)
-        self.lib.cugo_ref_observe_indexed(_ptr(states), _ptr(ids), n, states.shape[0], _ptr(f),
+        self.lib.observe_indexed(_ptr(states), _ptr(ids), n, states.shape[0], _ptr(f),
                                           _ptr(legal), _ptr(player), _ptr(done), _ptr(status))
         return f, legal.astype(bool), player, done.astype(bool), status
 
@@ -105,7 +120,7 @@ class RefEngine:
         status = np.zeros(n, dtype=np.int16)
         committed = np.zeros(n, dtype=np.uint8)
         ev = np.zeros((n, EVENT_WORDS), dtype=np.int64) if events else None
-        self.lib.cugo_ref_step_indexed(_ptr(states), _ptr(ids), _ptr(actions), n,
+        self.lib.step_indexed(_ptr(states), _ptr(ids), _ptr(actions), n,
                                        states.shape[0], _ptr(reward), _ptr(done), _ptr(nagari),
                                        _ptr(status), _ptr(committed), _ptr(ev))
         out = (reward, done.astype(bool), nagari.astype(bool), status, committed.astype(bool))
@@ -114,14 +129,14 @@ class RefEngine:
     def start(self, states: np.ndarray) -> np.ndarray:
         states = np.ascontiguousarray(states, dtype=np.uint8)
         out = np.zeros((states.shape[0], START_WORDS), dtype=np.int64)
-        self.lib.cugo_ref_start(_ptr(states), states.shape[0], _ptr(out))
+        self.lib.start(_ptr(states), states.shape[0], _ptr(out))
         return out
 
     def clone(self, states: np.ndarray, ids: np.ndarray) -> np.ndarray:
         states = np.ascontiguousarray(states, dtype=np.uint8)
         ids = np.ascontiguousarray(ids, dtype=np.int64)
         out = np.zeros((ids.size, STATE_BYTES), dtype=np.uint8)
-        self.lib.cugo_ref_clone_indexed(_ptr(states), _ptr(ids), ids.size, states.shape[0],
+        self.lib.clone_indexed(_ptr(states), _ptr(ids), ids.size, states.shape[0],
                                         _ptr(out))
         return out
 
@@ -136,7 +151,7 @@ class RefEngine:
         nagari = np.zeros(n, dtype=np.uint8)
         status = np.zeros(n, dtype=np.int16)
         committed = np.zeros(n, dtype=np.uint8)
-        self.lib.cugo_ref_branch_indexed(_ptr(states), _ptr(ids), _ptr(actions), n,
+        self.lib.branch_indexed(_ptr(states), _ptr(ids), _ptr(actions), n,
                                          states.shape[0], _ptr(children), _ptr(reward),
                                          _ptr(done), _ptr(nagari), _ptr(status),
                                          _ptr(committed))
@@ -147,7 +162,7 @@ class RefEngine:
         states = np.ascontiguousarray(states, dtype=np.uint8)
         ids = np.ascontiguousarray(ids, dtype=np.int64)
         out = np.zeros((ids.size, 2), dtype=np.int64)
-        self.lib.cugo_ref_hands_indexed(_ptr(states), _ptr(ids), ids.size, states.shape[0],
+        self.lib.hands_indexed(_ptr(states), _ptr(ids), ids.size, states.shape[0],
                                         _ptr(out))
         return out
 
@@ -155,13 +170,13 @@ class RefEngine:
         states = np.ascontiguousarray(states, dtype=np.uint8)
         ids = np.ascontiguousarray(ids, dtype=np.int64)
         out = np.zeros(ids.size, dtype=np.int64)
-        self.lib.cugo_ref_stock_indexed(_ptr(states), _ptr(ids), ids.size, states.shape[0],
+        self.lib.stock_indexed(_ptr(states), _ptr(ids), ids.size, states.shape[0],
                                         _ptr(out))
         return out
 
     def reward0(self, row: np.ndarray) -> int:
         row = np.ascontiguousarray(row, dtype=np.uint8)
-        return int(self.lib.cugo_ref_reward0(_ptr(row)))
+        return int(self.lib.reward0(_ptr(row)))
 
     # -- whole random-policy games and branch work -----------------------------------
     def play_random(self, base_seed: int, n: int, threads: int = 1, record_games: int = 0,
@@ -172,7 +187,7 @@ class RefEngine:
         records = None
         if record_games:
             records = np.zeros((record_games, record_cap, self.record_bytes), dtype=np.uint8)
-        total = self.lib.cugo_ref_play_random(ctypes.c_uint64(base_seed & (2**64 - 1)), n,
+        total = self.lib.play_random(ctypes.c_uint64(base_seed & (2**64 - 1)), n,
                                               threads, _ptr(digest), _ptr(steps), _ptr(reward),
                                               _ptr(records), record_games, record_cap)
         return digest, steps, reward, records, int(total)
@@ -182,7 +197,7 @@ class RefEngine:
         roots = np.ascontiguousarray(roots, dtype=np.uint8)
         ids = np.ascontiguousarray(ids, dtype=np.int64)
         actions = np.ascontiguousarray(actions, dtype=np.int64)
-        return int(self.lib.cugo_ref_branch_work(_ptr(roots), _ptr(ids), _ptr(actions), ids.size,
+        return int(self.lib.branch_work(_ptr(roots), _ptr(ids), _ptr(actions), ids.size,
                                                  threads, int(observe)))
 
 
@@ -261,3 +276,36 @@ def step_record(features, legal, player, done, status, actions, reward, sdone, n
 # Byte ranges of a row that hold no field (zero in every row the engines write).
 PADDING = ((78, 80), (90, 96), (103, 104), (116, 120), (125, 126), (130, 136), (153, 160),
            (197, 200), (220, 224), (241, 248))
+
+
+class OracleRules:
+    """Rule-level entry points of the oracle (oracle/matgo/matgo.c) for the reference's
+    known-answer tests: score_captured, go_adjusted_score50 and settle_terminal50."""
+
+    def __init__(self, path: Path | str = ORACLE_LIB) -> None:
+        lib = ctypes.CDLL(str(path))
+        lib.cugo_oracle_score.argtypes = [ctypes.c_uint64, ctypes.c_int, _P]
+        lib.cugo_oracle_score.restype = None
+        lib.cugo_oracle_go_points.argtypes = [ctypes.c_uint8, ctypes.c_uint8]
+        lib.cugo_oracle_go_points.restype = ctypes.c_uint64
+        lib.cugo_oracle_settle.argtypes = [_P, _P]
+        lib.cugo_oracle_settle.restype = None
+        self.lib = lib
+
+    FIELDS = ("bright_count", "animal_count", "ribbon_count", "pi_units", "bright_points",
+              "animal_points", "ribbon_points", "pi_points", "flags", "total_points")
+
+    def score(self, cards: int, gukjin_as_pi: bool = False) -> dict:
+        out = np.zeros(10, dtype=np.uint8)
+        self.lib.cugo_oracle_score(ctypes.c_uint64(cards), int(gukjin_as_pi), _ptr(out))
+        return dict(zip(self.FIELDS, (int(v) for v in out)))
+
+    def go_points(self, base: int, go_count: int) -> int:
+        return int(self.lib.cugo_oracle_go_points(base, go_count))
+
+    def settle(self, row: np.ndarray) -> dict:
+        row = np.ascontiguousarray(row, dtype=np.uint8)
+        out = np.zeros(4, dtype=np.int64)
+        self.lib.cugo_oracle_settle(_ptr(row), _ptr(out))
+        return {"status": int(out[0]), "winner": int(out[1]), "final_points": int(out[2]),
+                "side0": int(out[3])}

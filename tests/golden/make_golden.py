@@ -81,7 +81,7 @@ def rows(ref: RefEngine) -> None:
 
 
 def main() -> None:
-    ref = RefEngine()
+    ref = RefEngine(reference=True)
     c1(ref)
     rows(ref)
 

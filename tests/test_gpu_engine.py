@@ -1,8 +1,10 @@
-"""GPU parity: every operation of the HIP extension against the reference engine.
+"""GPU parity: every operation of the HIP extension against the oracle.
 
-The checker is the reference's own C++ engine (oracle/_ref, driven through
-oracle/ref.py) on the same inputs; integer, byte and mask outputs must be identical and
-float features/rewards bit-identical (compared as raw 32-bit patterns).
+The checker is the oracle (oracle/matgo/, the plain-C restatement of the reference
+engine, driven through oracle/ref.py) on the same inputs; the oracle itself is pinned by
+the golden fixtures and the reference's own build (tests/test_cpu_oracle*.py).  Integer,
+byte and mask outputs must be identical and float features/rewards bit-identical
+(compared as raw 32-bit patterns).
 """
 
 from __future__ import annotations
