@@ -1837,25 +1837,42 @@ struct Packet {
   u8 revealed;
 };
 
+// One probe and one pack_observation per lane: a pending row observes its staged
+// state, every other row the state itself.  The kernels inline everything, so a wave
+// with both kinds of rows would otherwise run the probe and the observation (with its
+// Go/Stop settlement) once per branch.
 CG_HD Packet make_packet(const Env& e) {
   Packet pk;
-  pk.head = packet_head(e);  // not reused below for the pending branch's staged state
-  if (e.pactive != 0) {
+  const bool pending = e.pactive != 0;
+  Env src = e;
+  Probe probe;
+  probe.status = kOk;
+  probe.decision = kDecNone;
+  probe.legal_cards = 0;
+  probe.revealed = kNoCard;
+  if (pending) {
     const Pending p = pending_of(e);
     Env staged;
-    const Probe probe = probe_postchance(e, p, staged);
-    pk.primary_action = p.prim;
+    probe = probe_postchance(e, p, staged);
+    if (probe.status == kOk) {  // pack_postchance_observation50 (postchance50.h:458-466)
+      src = staged;
+      src.actor = p.actor;
+      src.turn = e.turn;
+    }
+  }
+  Obs o = pack_observation(src);
+  if (pending) {
+    pk.primary_action = e.prim;
     pk.revealed = probe.revealed;
+    pk.head.player = e.pactor;
     if (probe.status != kOk) {
+      pk.head.status = probe.status;
+      pk.head.decision_kind = kDecNone;
+      pk.head.legal = Mask3{0, 0, 0};
       pk.obs = empty_obs();
       return pk;
     }
-    // pack_postchance_observation50 (postchance50.h:458-481)
-    Env view = staged;
-    view.actor = p.actor;
-    view.turn = e.turn;
-    Obs o = pack_observation(view);
-    o.decision_kind = probe.decision;
+    o.decision_kind = probe.decision;  // postchance50.h:467-480
     if (is_physical(probe.revealed)) {
       const u64 b = bit(probe.revealed);
       const u64 known = o.own_hand | o.floor | o.own_cap | o.opp_cap | o.pending_public;
@@ -1864,10 +1881,29 @@ CG_HD Packet make_packet(const Env& e) {
         o.unseen &= ~b;
       }
     }
+    pk.head.status = kOk;
+    pk.head.decision_kind = probe.decision;
+    pk.head.legal = choice_mask(probe.legal_cards);
     pk.obs = o;
     return pk;
   }
-  pk.obs = pack_observation(e);
+  // torch50.h:245-296, primary branch
+  u8 player = decision_player(e);
+  if (player > 1u) player = e.actor & 1u;
+  pk.head.player = player;
+  pk.head.status = kOk;
+  const u8 kind = decision_kind(e);
+  if (e.done != 0) {
+    pk.head.legal = Mask3{0, 0, 0};
+    pk.head.decision_kind = 0;
+  } else if (kind == kDecGukjin) {
+    pk.head.legal = Mask3{0, 0, (1ull << (kActGukjinPi - 128)) | (1ull << (kActGukjinAnimal - 128))};
+    pk.head.decision_kind = kind;
+  } else {
+    pk.head.legal = legal_primary(e);
+    pk.head.decision_kind = kind;
+  }
+  pk.obs = o;
   pk.primary_action = kInvalidAction16;
   pk.revealed = kNoCard;
   return pk;
