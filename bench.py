@@ -38,6 +38,17 @@ STEP_BYTES_PER_ROW = 248 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # 513
 BRANCH_BYTES_PER_CHILD = 8 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # parent reads hit L2: 273
 
 
+def measured_traffic(kernel: str, key: str) -> int | None:
+    """HBM bytes per launch of `kernel` for workload `key`, from the committed
+    rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by what the
+    counter reads for a plain copy of known size); None when not measured for this size."""
+    path = REPO / "profiles" / "pmc_traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get(kernel, {}).get(key)
+    return None if entry is None else int(entry["bytes"])
+
+
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -87,8 +98,19 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
     games = int(completed.item()) - start_games
-    observe_ms = sum(a.elapsed_time(b) for a, b in pairs) / steps
-    return {"seconds": seconds, "games": games, "observe_ms": observe_ms}
+    in_loop_ms = sum(a.elapsed_time(b) for a, b in pairs) / steps
+    # The observe kernel alone on the loop's live (mid-game) states: back-to-back launches
+    # between two events on its stream, so per-launch event overhead does not count.
+    reps = 50
+    burst = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    burst[0].record(stream)
+    for _ in range(reps):
+        ext.observe(states)
+    burst[1].record(stream)
+    torch.cuda.synchronize()
+    observe_ms = burst[0].elapsed_time(burst[1]) / reps
+    return {"seconds": seconds, "games": games, "observe_ms": observe_ms,
+            "observe_in_loop_ms": in_loop_ms}
 
 
 def branch_workload(ext, torch, iters: int) -> dict:
@@ -242,14 +264,18 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
             row_bytes = heads * dh * 2
             nbytes = int(pos.sum()) * row_bytes * 2 + rows * row_bytes * 6 + rows * 8
             gbs = nbytes / (kernel_ms * 1e-3) / 1e9
+            traffic = measured_traffic("decode_kernel", f"{rows} {name}")
             out[name] = {"tokens_per_s": round(rows / step_s, 1),
+                         "roofline": {"kernel": "decode_kernel", "bound": "hbm",
+                                      "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                                      "traffic": traffic},
                          "step_ms": round(step_s * 1e3, 4),
                          "mean_pos": round(float(pos.float().mean()), 2),
                          "max_pos": int(pos.max()),
                          "decode_kernel_ms": round(kernel_ms, 4),
                          "decode_bytes": nbytes,
-                         "decode_gbs": round(gbs, 1),
-                         "decode_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+                         }
     out["cache"] = [layers, rows, heads, slots, dh]
     return out
 
@@ -320,8 +346,10 @@ def main() -> None:
         "roofline": {"kernel": "observe_kernel", "bound": "hbm",
                      "achieved": round(observe_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(observe_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("observe_kernel", str(args.batch)),
                      "bytes_per_row": OBSERVE_BYTES_PER_ROW,
-                     "avg_launch_ms": round(rp["observe_ms"], 4), "traffic": None},
+                     "avg_launch_ms": round(rp["observe_ms"], 4),
+                     "in_loop_event_ms": round(rp["observe_in_loop_ms"], 4)},
     }
     if not args.no_branch:
         result["branch"] = branch_workload(ext, torch, args.branch_iters)
