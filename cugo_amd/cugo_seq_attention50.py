@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import torch
 
-from .cugo_torch50_ext import load_extension
+from cugo_amd.cugo_torch50_ext import load_extension
 
 _EXT = None
 

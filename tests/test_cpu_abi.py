@@ -35,6 +35,8 @@ def test_abi_rejects_bad_arguments_without_launching():
 
 
 def test_extension_module_constants():
+    import torch  # noqa: F401  (loads libc10 / libtorch, which the module links)
+
     from cugo_amd import _cugo_torch50_hip as m
 
     assert (m.FEATURE_COUNT, m.ACTION_COUNT, m.PRIMARY_ACTION_COUNT, m.CHOICE_ACTION_BEGIN,
@@ -74,3 +76,22 @@ def test_load_extension_fails_loudly_without_gpu(monkeypatch):
         assert "not available" in str(exc)
     else:
         raise AssertionError("load_extension must raise without a GPU")
+
+
+def test_drop_in_modules_import_under_reference_names():
+    """With cugo_amd/ first on sys.path, the reference's import lines resolve to this
+    package's modules (python/cugo_torch50_ext.py, python/cugo_seq_attention50.py)."""
+    import subprocess
+    import sys
+
+    code = ("import sys; sys.path[:0] = [sys.argv[1], sys.argv[2]];"
+            "from cugo_torch50_ext import load_extension;"
+            "from cugo_seq_attention50 import decode_attention;"
+            "import torch;"
+            "q = torch.zeros(1, 1, 32)\n"
+            "try:\n decode_attention(q, q.view(1, 1, 1, 32), q.view(1, 1, 1, 32), torch.zeros(1, dtype=torch.long))\n"
+            "except RuntimeError as e:\n print('raised', e)\n")
+    out = subprocess.run([sys.executable, "-c", code, str(REPO / "cugo_amd"), str(REPO)],
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert "raised" in out.stdout and "GPU" in out.stdout
