@@ -15,6 +15,8 @@ Also reported (not timed into `value`):
                 branch_indexed (clone + step) and the observation of all children
   decode        sequence-policy decode over a [4, 4,096, 8, 320, 32] bf16 KV cache:
                 tokens/s of the 4-layer step and the HIP decode kernel's HBM fraction
+  rollout       MLP PPO self-play rollout, B = 32,768 x 128 steps: env steps/s and the
+                engine's share of the wall time
   cpu_baseline  the reference engine (oracle/_ref) on this host's cores, same protocol,
                 bounded sample
 """
@@ -59,6 +61,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-branch", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--no-rollout", action="store_true")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
     p.add_argument("--decode-steps", type=int, default=20)
@@ -280,6 +283,115 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
     return out
 
 
+def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict:
+    """MLP PPO self-play rollout: B games, a residual MLP policy (720 features -> Linear 512
+    -> 3 blocks of h + Linear(ReLU(Linear(LayerNorm(h)))) -> 179 logits and a value head,
+    bf16, N(0, 0.02) weights from seed 0), legal-masked softmax sampling (Gumbel-max), and
+    a `horizon`-step rollout buffer (bf16 features, mask, action, log-prob, value, reward,
+    done), finished games re-dealt in place.  Reports env steps/s and the engine's share of
+    the wall time (observe + step + re-deal, HIP events on the stream)."""
+    from torch import nn
+
+    dev = torch.device("cuda")
+    torch.manual_seed(0)
+
+    class Block(nn.Module):
+        def __init__(self, d: int) -> None:
+            super().__init__()
+            self.norm = nn.LayerNorm(d)
+            self.fc1 = nn.Linear(d, d)
+            self.fc2 = nn.Linear(d, d)
+
+        def forward(self, h):
+            return h + self.fc2(torch.relu(self.fc1(self.norm(h))))
+
+    class Actor(nn.Module):
+        def __init__(self, d: int = 512) -> None:
+            super().__init__()
+            self.inp = nn.Linear(720, d)
+            self.blocks = nn.Sequential(Block(d), Block(d), Block(d))
+            self.norm = nn.LayerNorm(d)
+            self.logits = nn.Linear(d, 179)
+            self.value = nn.Linear(d, 1)
+
+        def forward(self, f):
+            h = self.norm(self.blocks(self.inp(f)))
+            return self.logits(h), self.value(h).squeeze(-1)
+
+    actor = Actor()
+    with torch.no_grad():
+        for prm in actor.parameters():
+            prm.normal_(0.0, 0.02)
+    actor = actor.to(dev).to(torch.bfloat16).eval()
+
+    idx = torch.arange(batch, dtype=torch.int64, device=dev)
+    base = SEED_BASE + 0xC4
+    states = ext.create(idx + base, idx & 1)
+    gen = torch.zeros(batch, dtype=torch.int32, device=dev)
+    sampler = ext.seed_samplers(batch, base, gen)
+    completed = torch.zeros(1, dtype=torch.int64, device=dev)
+    buf = {
+        "features": torch.empty(horizon, batch, 720, dtype=torch.bfloat16, device=dev),
+        "legal": torch.empty(horizon, batch, 179, dtype=torch.bool, device=dev),
+        "action": torch.empty(horizon, batch, dtype=torch.int64, device=dev),
+        "logp": torch.empty(horizon, batch, dtype=torch.float32, device=dev),
+        "value": torch.empty(horizon, batch, dtype=torch.float32, device=dev),
+        "reward": torch.empty(horizon, batch, dtype=torch.float32, device=dev),
+        "done": torch.empty(horizon, batch, dtype=torch.bool, device=dev),
+    }
+    gumbel_gen = torch.Generator(device=dev).manual_seed(1)
+    stream = torch.cuda.current_stream()
+
+    def one_step(t: int, ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        features, legal, _, _, _ = ext.observe(states)
+        if ev is not None:
+            ev[1].record(stream)
+        f16 = features.to(torch.bfloat16)
+        logits, value = actor(f16)
+        masked = logits.float().masked_fill(~legal, float("-inf"))
+        u = torch.rand(masked.shape, generator=gumbel_gen, device=dev).clamp_(1e-20, 1.0)
+        action = (masked - torch.log(-torch.log(u))).argmax(1)
+        logp = torch.log_softmax(masked, 1).gather(1, action.unsqueeze(1)).squeeze(1)
+        if ev is not None:
+            ev[2].record(stream)
+        reward, done, _, _, _ = ext.step(states, action)
+        ext.reset_done(states, done, base, gen, sampler, completed)
+        if ev is not None:
+            ev[3].record(stream)
+        buf["features"][t].copy_(f16)
+        buf["legal"][t].copy_(legal)
+        buf["action"][t].copy_(action)
+        buf["logp"][t].copy_(logp)
+        buf["value"][t].copy_(value.float())
+        buf["reward"][t].copy_(reward)
+        buf["done"][t].copy_(done)
+
+    with torch.no_grad():
+        for t in range(8):  # warm-up: GEMM handles, allocator
+            one_step(t)
+        torch.cuda.synchronize()
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(horizon)]
+        games0 = int(completed.item())
+        t0 = time.perf_counter()
+        for t in range(horizon):
+            one_step(t, events[t])
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    engine_ms = sum(e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[3]) for e in events)
+    policy_ms = sum(e[1].elapsed_time(e[2]) for e in events)
+    flops = 2 * (720 * 512 + 6 * 512 * 512 + 512 * 179 + 512) * batch * horizon
+    return {"env_steps_per_s": round(batch * horizon / wall, 1),
+            "wall_ms": round(wall * 1e3, 2),
+            "engine_share": round(engine_ms / (wall * 1e3), 4),
+            "policy_share": round(policy_ms / (wall * 1e3), 4),
+            "engine_ms": round(engine_ms, 2), "policy_ms": round(policy_ms, 2),
+            "policy_tflops": round(flops / (policy_ms * 1e-3) / 1e12, 1),
+            "games_completed": int(completed.item()) - games0,
+            "batch": batch, "horizon": horizon, "dtype": "bf16"}
+
+
 def cpu_baseline(seconds: float) -> dict:
     """The reference engine's own build (oracle/_ref; the oracle's C restatement when that
     is absent) on the host cores, same random-policy protocol (observe + sample +
@@ -355,6 +467,8 @@ def main() -> None:
         result["branch"] = branch_workload(ext, torch, args.branch_iters)
     if not args.no_decode:
         result["decode"] = decode_workload(ext, torch, args.decode_steps)
+    if not args.no_rollout:
+        result["rollout"] = rollout_workload(ext, torch)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)
