@@ -1844,37 +1844,38 @@ struct Packet {
 CG_HD Packet make_packet(const Env& e) {
   Packet pk;
   const bool pending = e.pactive != 0;
+  // The probe's fields as scalars, and the probe writes straight into the state that is
+  // observed: a conditionally assigned aggregate is not split into registers and would
+  // live in private memory.
+  u8 pr_status = kOk, pr_decision = kDecNone, pr_revealed = kNoCard;
+  u64 pr_legal = 0;
   Env src = e;
-  Probe probe;
-  probe.status = kOk;
-  probe.decision = kDecNone;
-  probe.legal_cards = 0;
-  probe.revealed = kNoCard;
   if (pending) {
-    const Pending p = pending_of(e);
-    Env staged;
-    probe = probe_postchance(e, p, staged);
-    if (probe.status == kOk) {  // pack_postchance_observation50 (postchance50.h:458-466)
-      src = staged;
-      src.actor = p.actor;
-      src.turn = e.turn;
-    }
+    const Probe probe = probe_postchance(e, pending_of(e), src);
+    pr_status = probe.status;
+    pr_decision = probe.decision;
+    pr_revealed = probe.revealed;
+    pr_legal = probe.legal_cards;
+    // pack_postchance_observation50 (postchance50.h:458-466); on a failed probe the
+    // observation is discarded below
+    src.actor = e.pactor;
+    src.turn = e.turn;
   }
   Obs o = pack_observation(src);
   if (pending) {
     pk.primary_action = e.prim;
-    pk.revealed = probe.revealed;
+    pk.revealed = pr_revealed;
     pk.head.player = e.pactor;
-    if (probe.status != kOk) {
-      pk.head.status = probe.status;
+    if (pr_status != kOk) {
+      pk.head.status = pr_status;
       pk.head.decision_kind = kDecNone;
       pk.head.legal = Mask3{0, 0, 0};
       pk.obs = empty_obs();
       return pk;
     }
-    o.decision_kind = probe.decision;  // postchance50.h:467-480
-    if (is_physical(probe.revealed)) {
-      const u64 b = bit(probe.revealed);
+    o.decision_kind = pr_decision;  // postchance50.h:467-480
+    if (is_physical(pr_revealed)) {
+      const u64 b = bit(pr_revealed);
       const u64 known = o.own_hand | o.floor | o.own_cap | o.opp_cap | o.pending_public;
       if ((known & b) == 0) {
         o.pending_public |= b;
@@ -1882,8 +1883,8 @@ CG_HD Packet make_packet(const Env& e) {
       }
     }
     pk.head.status = kOk;
-    pk.head.decision_kind = probe.decision;
-    pk.head.legal = choice_mask(probe.legal_cards);
+    pk.head.decision_kind = pr_decision;
+    pk.head.legal = choice_mask(pr_legal);
     pk.obs = o;
     return pk;
   }

@@ -106,10 +106,12 @@ __device__ inline u32 spread4(u32 x) {
   return (x & 1u) | ((x & 2u) << 7) | ((x & 4u) << 14) | ((x & 8u) << 21);
 }
 
-// One tile of 64 games per 256-thread workgroup: wave 0 runs the 64 games (one per
-// lane) and writes their records; then all four waves share the 64 x 3,059 output
+// One tile of 64 games per 192-thread workgroup: wave 0 runs the 64 games (one per
+// lane) and writes their records; then all three waves share the 64 x 3,059 output
 // bytes, so a wave whose games took long to compute does not store its rows alone.
-constexpr int kObsThreads = 256;
+// Three waves, because the kernel's ~160 VGPRs allow three waves per SIMD: four
+// workgroups per CU then hold all 1,024 tiles of a 65,536-row batch at once.
+constexpr int kObsThreads = 192;
 
 template <bool kIndexed>
 __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states, i64 env_count,
@@ -168,7 +170,7 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
     }
   }
   __syncthreads();
-  // Features: wave w stores rows w, w + 4, ...; lane owns float4 columns q = lane,
+  // Features: wave w stores rows w, w + 3, ...; lane owns float4 columns q = lane,
   // lane + 64, lane + 128 (< 180) of each, so a store instruction covers 1 KiB of one
   // row and each lane resolves its twelve feature sources once.
   constexpr int kQuads = kFeatureCount / 4;  // 180
