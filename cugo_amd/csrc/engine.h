@@ -1658,16 +1658,36 @@ CG_HD Probe probe_postchance(const Env& e, const Pending& p, Env& staged) {
 }
 
 // postchance50.h:509-539.  Returns the ActionStatus50; committed set on commit.
+// postchance50.h:509-539.  The reference probes the staged action and then applies it.
+// apply_action is transactional and fails wherever the probe would stop the action (a
+// floor choice still open, an empty stock, an invalid choice), so with no pi card
+// selected the action is applied first and the probe runs only when the apply fails;
+// a pi selection (which the probe checks more strictly than the transfer) keeps the
+// reference order.  Same status, same state, same commit in every case.
 CG_HD u8 continue_postchance(Env& e, bool& committed) {
   committed = false;
   Pending p = pending_of(e);
+  Action a = p.action;
+  if (p.sel_pi != 0) a.pisel = p.sel_pi;
+  u8 s = kOk;
+  if (p.sel_pi == 0) {
+    Env applied = e;
+    s = apply_action(applied, a);
+    if (s == kOk) {
+      e = applied;
+      p.action = a;
+      p.active = 0;
+      set_pending(e, p);
+      committed = true;
+      return kOk;
+    }
+  }
   Env staged;
   const Probe probe = probe_postchance(e, p, staged);
   if (probe.status != kOk) return probe.status;
   if (probe.decision != kDecNone) return kOk;
-  Action a = p.action;
-  if (p.sel_pi != 0) a.pisel = p.sel_pi;
-  const u8 s = apply_action(e, a);
+  if (p.sel_pi == 0) return s;  // the apply above failed with `s`
+  s = apply_action(e, a);
   if (s != kOk) return s;
   p.action = a;
   p.active = 0;

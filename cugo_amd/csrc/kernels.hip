@@ -33,16 +33,17 @@ __device__ inline int tile_count(i64 base, i64 n) {
 
 __device__ inline bool valid_id(i64 id, i64 env_count) { return id >= 0 && id < env_count; }
 
-// Loads the tile's rows into LDS; src row r is `ids[r]` (gathered, zero row when the id
-// is invalid) or base + r (contiguous) when ids_lds is null.
+// Loads the tile's rows into LDS with kThreads threads; src row r is `ids[r]` (gathered,
+// zero row when the id is invalid) or base + r (contiguous) when ids_lds is null.
+template <int kThreads = kTile>
 __device__ inline void stage_in(u64* lds, const u64* states, const i64* ids_lds, i64 base,
                                 int count, i64 env_count) {
   const int words = count * kRowWords;
   if (ids_lds == nullptr) {
     const u64* src = states + base * kRowWords;
-    for (int j = threadIdx.x; j < words; j += kTile) lds[j] = src[j];
+    for (int j = threadIdx.x; j < words; j += kThreads) lds[j] = src[j];
   } else {
-    for (int j = threadIdx.x; j < words; j += kTile) {
+    for (int j = threadIdx.x; j < words; j += kThreads) {
       const int r = j / kRowWords;
       const int k = j - r * kRowWords;
       const i64 id = ids_lds[r];
@@ -51,16 +52,18 @@ __device__ inline void stage_in(u64* lds, const u64* states, const i64* ids_lds,
   }
 }
 
-// Stores the tile's rows from LDS: to dst rows base + r (contiguous) or, when ids_lds
-// is given, to rows ids[r] with a valid id (scatter, in place).
+// Stores the tile's rows from LDS with kThreads threads: to dst rows base + r
+// (contiguous) or, when ids_lds is given, to rows ids[r] with a valid id (scatter, in
+// place).
+template <int kThreads = kTile>
 __device__ inline void stage_out(const u64* lds, u64* dst, const i64* ids_lds, i64 base,
                                  int count, i64 env_count) {
   const int words = count * kRowWords;
   if (ids_lds == nullptr) {
     u64* out = dst + base * kRowWords;
-    for (int j = threadIdx.x; j < words; j += kTile) out[j] = lds[j];
+    for (int j = threadIdx.x; j < words; j += kThreads) out[j] = lds[j];
   } else {
-    for (int j = threadIdx.x; j < words; j += kTile) {
+    for (int j = threadIdx.x; j < words; j += kThreads) {
       const int r = j / kRowWords;
       const int k = j - r * kRowWords;
       const i64 id = ids_lds[r];
@@ -233,8 +236,13 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
 // --------------------------------------------------------------------- step ----
 // kMode: 0 = step (contiguous, in place), 1 = step_indexed (gather/scatter in place),
 // 2 = branch_indexed (gather from parents, children written contiguously).
+// Two waves per tile of 64 games: both stage the rows in and out, wave 0 runs the games
+// (one per lane).  At ~190 VGPRs two waves fit per SIMD, so 1,024 tiles of 128 threads
+// are resident at once on 256 CUs.
+constexpr int kStepThreads = 128;
+
 template <int kMode, bool kEvents>
-__global__ __launch_bounds__(kTile) void step_kernel(u64* states, i64 env_count, const i64* ids,
+__global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env_count, const i64* ids,
                                                      const i64* actions, i64 n, u64* children,
                                                      float* reward, u8* done, u8* nagari,
                                                      i16* status, u8* committed, i64* events) {
@@ -247,7 +255,7 @@ __global__ __launch_bounds__(kTile) void step_kernel(u64* states, i64 env_count,
   constexpr bool kIndexed = kMode != 0;
   if (kIndexed && lane < count) tile_ids[lane] = ids[base + lane];
   __syncthreads();
-  stage_in(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
+  stage_in<kStepThreads>(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
   __syncthreads();
   if (lane < count) {
     const i64 i = base + lane;
@@ -286,12 +294,12 @@ __global__ __launch_bounds__(kTile) void step_kernel(u64* states, i64 env_count,
     }
   }
   __syncthreads();
-  if (kMode == 0) stage_out(rows, states, nullptr, base, count, env_count);
-  else if (kMode == 1) stage_out(rows, states, tile_ids, base, count, env_count);
-  else stage_out(rows, children, nullptr, base, count, env_count);
+  if (kMode == 0) stage_out<kStepThreads>(rows, states, nullptr, base, count, env_count);
+  else if (kMode == 1) stage_out<kStepThreads>(rows, states, tile_ids, base, count, env_count);
+  else stage_out<kStepThreads>(rows, children, nullptr, base, count, env_count);
   if (kEvents) {
     i64* eout = events + base * kEventWords;
-    for (int j = lane; j < count * kEventWords; j += kTile) eout[j] = ev[j];
+    for (int j = lane; j < count * kEventWords; j += kStepThreads) eout[j] = ev[j];
   }
 }
 
@@ -504,7 +512,7 @@ int cugo_step(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
                           !committed)))
     return kBadArgument;
   if (n == 0) return 0;
-  step_kernel<0, false><<<tiles(n), kTile, 0, stream>>>(
+  step_kernel<0, false><<<tiles(n), kStepThreads, 0, stream>>>(
       reinterpret_cast<u64*>(states), n, nullptr, actions, n, nullptr, reward, done, nagari,
       status, committed, nullptr);
   return launched();
@@ -518,7 +526,7 @@ int cugo_step_indexed(uint8_t* states, int64_t env_count, const int64_t* ids,
       (n > 0 && (!ids || !actions || !reward || !done || !nagari || !status || !committed)))
     return kBadArgument;
   if (n == 0) return 0;
-  step_kernel<1, false><<<tiles(n), kTile, 0, stream>>>(
+  step_kernel<1, false><<<tiles(n), kStepThreads, 0, stream>>>(
       reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
       nagari, status, committed, nullptr);
   return launched();
@@ -533,7 +541,7 @@ int cugo_step_events_indexed(uint8_t* states, int64_t env_count, const int64_t* 
                  !events)))
     return kBadArgument;
   if (n == 0) return 0;
-  step_kernel<1, true><<<tiles(n), kTile, 0, stream>>>(
+  step_kernel<1, true><<<tiles(n), kStepThreads, 0, stream>>>(
       reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
       nagari, status, committed, events);
   return launched();
@@ -568,7 +576,7 @@ int cugo_branch_indexed(const uint8_t* states, int64_t env_count, const int64_t*
                  !committed)))
     return kBadArgument;
   if (n == 0) return 0;
-  step_kernel<2, false><<<tiles(n), kTile, 0, stream>>>(
+  step_kernel<2, false><<<tiles(n), kStepThreads, 0, stream>>>(
       const_cast<u64*>(reinterpret_cast<const u64*>(states)), env_count, ids, actions, n,
       reinterpret_cast<u64*>(children), reward, done, nagari, status, committed, nullptr);
   return launched();
