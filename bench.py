@@ -5,7 +5,7 @@
 Workload (timed, one JSON line on stdout): random-policy self-play on B = 65,536
 GPU-resident games.  One step = observe (720 features + 179-way mask for every game)
 -> uniform legal sample (per-game xorshift64) -> step -> re-create finished games with
-their next seed.  `value` = complete games per second over K steps.  Games are dealt
+their next seed (pre-dealt in a full-width batch every 8 steps, included in the timing).  `value` = complete games per second over K steps.  Games are dealt
 from seed = 0x243F6A8885A308D3 + i (+ B per later game of row i), first = i & 1.
 
 Also reported (not timed into `value`):
@@ -35,6 +35,7 @@ sys.path.insert(0, str(REPO))
 
 SEED_BASE = 0x243F6A8885A308D3
 HBM_PEAK_GBS = 8000.0
+REFILL = 8  # steps between batched pre-deals of the next games
 OBSERVE_BYTES_PER_ROW = 248 + 720 * 4 + 179 + 1 + 1 + 2  # 3,311
 STEP_BYTES_PER_ROW = 248 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # 513
 BRANCH_BYTES_PER_CHILD = 8 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # parent reads hit L2: 273
@@ -76,9 +77,17 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int) -> dict:
     gen = torch.zeros(batch, dtype=torch.int32, device=dev)
     sampler = ext.seed_samplers(batch, SEED_BASE, gen)
     completed = torch.zeros(1, dtype=torch.int64, device=dev)
+    # Next games are pre-dealt in full-width batches every REFILL steps; a finished row
+    # copies its spare (dealt inline if stale), the same rows reset_done would deal.
+    spares = torch.empty((batch, 248), dtype=torch.uint8, device=dev)
+    spare_gen = torch.zeros(batch, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream()
+    counter = [0]
 
     def one_step(events=None):
+        if counter[0] % REFILL == 0:
+            ext.refill_spares(spares, spare_gen, gen, SEED_BASE)
+        counter[0] += 1
         if events is not None:
             events[0].record(stream)
         _, legal, _, _, _ = ext.observe(states)
@@ -86,7 +95,7 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int) -> dict:
             events[1].record(stream)
         actions = ext.sample_uniform(legal, sampler)
         _, done, _, _, _ = ext.step(states, actions)
-        ext.reset_done(states, done, SEED_BASE, gen, sampler, completed)
+        ext.reset_done_spares(states, done, SEED_BASE, gen, sampler, completed, spares, spare_gen)
 
     for _ in range(warmup):
         one_step()

@@ -236,12 +236,12 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
 // --------------------------------------------------------------------- step ----
 // kMode: 0 = step (contiguous, in place), 1 = step_indexed (gather/scatter in place),
 // 2 = branch_indexed (gather from parents, children written contiguously).
-// Two waves per tile of 64 games: both stage the rows in and out, wave 0 runs the games
-// (one per lane).  At ~190 VGPRs two waves fit per SIMD, so 1,024 tiles of 128 threads
-// are resident at once on 256 CUs.
-constexpr int kStepThreads = 128;
-
-template <int kMode, bool kEvents>
+// kThreads = 128: two waves per tile of 64 games, both stage the rows in and out and
+// wave 0 runs the games (one per lane).  At ~250 VGPRs two waves fit per SIMD, so this
+// is the shape while every tile of the grid is resident at once (up to four per CU);
+// a larger grid queues tiles, and then one wave per tile (kThreads = 64) keeps twice as
+// many games computing per CU.
+template <int kMode, bool kEvents, int kStepThreads>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env_count, const i64* ids,
                                                      const i64* actions, i64 n, u64* children,
                                                      float* reward, u8* done, u8* nagari,
@@ -449,6 +449,72 @@ __global__ __launch_bounds__(kTile) void reset_kernel(u64* states, const u8* don
     if (flags[j / kRowWords]) out[j] = rows[j];
 }
 
+// Pre-deals the next game of each row whose spare is stale: spare row i <- game
+// generation[i] + 1 of row i, spare_gen[i] = generation[i] + 1.
+__global__ __launch_bounds__(kTile) void refill_kernel(u64* spares, u32* spare_gen,
+                                                       const u32* generation, i64 n,
+                                                       u64 base_seed) {
+  __shared__ u64 rows[kTileWords];
+  __shared__ int flags[kTile];
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int lane = threadIdx.x;
+  const i64 i = base + lane;
+  const u32 next = lane < count ? generation[i] + 1u : 0u;
+  const bool stale = lane < count && spare_gen[i] != next;
+  flags[lane] = stale;
+  if (stale) {
+    const u64 seed = base_seed + (u64)i + (u64)n * next;
+    pack_row(create_env(seed, (u32)(i & 1)), rows + lane * kRowWords);
+    spare_gen[i] = next;
+  }
+  __syncthreads();
+  u64* out = spares + base * kRowWords;
+  for (int j = lane; j < count * kRowWords; j += kTile)
+    if (flags[j / kRowWords]) out[j] = rows[j];
+}
+
+// reset_kernel's result, taking a finished row's next game from its pre-dealt spare
+// (dealt inline only when the spare is stale).
+__global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u8* done, i64 n,
+                                                            u64 base_seed, u32* generation,
+                                                            u64* sampler,
+                                                            unsigned long long* completed,
+                                                            const u64* spares,
+                                                            const u32* spare_gen) {
+  __shared__ u64 rows[kTileWords];
+  __shared__ int flags[kTile];
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int lane = threadIdx.x;
+  const i64 i = base + lane;
+  const bool reset = lane < count && done[i] != 0;
+  u32 gen = 0;
+  bool from_spare = false;
+  if (reset) {
+    gen = generation[i] + 1u;
+    generation[i] = gen;
+    from_spare = spare_gen[i] == gen;
+    sampler[i] = sampler_seed(base_seed + (u64)i + (u64)n * gen);
+  }
+  flags[lane] = reset;
+  // spare rows of this tile: whole rows, 31 lanes per row
+  u64 copy = __ballot(from_spare);
+  while (copy != 0) {
+    const int r = __builtin_ctzll(copy);
+    copy &= copy - 1;
+    if (lane < kRowWords) rows[r * kRowWords + lane] = spares[(base + r) * kRowWords + lane];
+  }
+  if (reset && !from_spare)
+    pack_row(create_env(base_seed + (u64)i + (u64)n * gen, (u32)(i & 1)), rows + lane * kRowWords);
+  const u64 ballot = __ballot(reset);
+  if (lane == 0 && ballot != 0) atomicAdd(completed, (unsigned long long)__popcll(ballot));
+  __syncthreads();
+  u64* out = states + base * kRowWords;
+  for (int j = lane; j < count * kRowWords; j += kTile)
+    if (flags[j / kRowWords]) out[j] = rows[j];
+}
+
 __global__ __launch_bounds__(256) void seed_kernel(i64 n, u64 base_seed, const u32* generation,
                                                    u64* sampler) {
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
@@ -464,6 +530,30 @@ using namespace cugo_amd;
 
 namespace {
 inline unsigned tiles(int64_t n) { return (unsigned)((n + kTile - 1) / kTile); }
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// step_kernel launch: two waves per tile while all tiles fit at once (four per CU).
+template <int kMode, bool kEvents, class... Args>
+inline void launch_step(int64_t n, hipStream_t stream, Args... args) {
+  if ((int64_t)tiles(n) <= 4 * (int64_t)device_cus())
+    step_kernel<kMode, kEvents, 128><<<tiles(n), 128, 0, stream>>>(args...);
+  else
+    step_kernel<kMode, kEvents, 64><<<tiles(n), 64, 0, stream>>>(args...);
+}
 inline unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
 inline int launched() { return (int)hipGetLastError(); }
 constexpr int kBadArgument = -22;
@@ -512,7 +602,7 @@ int cugo_step(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
                           !committed)))
     return kBadArgument;
   if (n == 0) return 0;
-  step_kernel<0, false><<<tiles(n), kStepThreads, 0, stream>>>(
+  launch_step<0, false>(n, stream, 
       reinterpret_cast<u64*>(states), n, nullptr, actions, n, nullptr, reward, done, nagari,
       status, committed, nullptr);
   return launched();
@@ -526,7 +616,7 @@ int cugo_step_indexed(uint8_t* states, int64_t env_count, const int64_t* ids,
       (n > 0 && (!ids || !actions || !reward || !done || !nagari || !status || !committed)))
     return kBadArgument;
   if (n == 0) return 0;
-  step_kernel<1, false><<<tiles(n), kStepThreads, 0, stream>>>(
+  launch_step<1, false>(n, stream, 
       reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
       nagari, status, committed, nullptr);
   return launched();
@@ -541,7 +631,7 @@ int cugo_step_events_indexed(uint8_t* states, int64_t env_count, const int64_t* 
                  !events)))
     return kBadArgument;
   if (n == 0) return 0;
-  step_kernel<1, true><<<tiles(n), kStepThreads, 0, stream>>>(
+  launch_step<1, true>(n, stream, 
       reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
       nagari, status, committed, events);
   return launched();
@@ -576,7 +666,7 @@ int cugo_branch_indexed(const uint8_t* states, int64_t env_count, const int64_t*
                  !committed)))
     return kBadArgument;
   if (n == 0) return 0;
-  step_kernel<2, false><<<tiles(n), kStepThreads, 0, stream>>>(
+  launch_step<2, false>(n, stream, 
       const_cast<u64*>(reinterpret_cast<const u64*>(states)), env_count, ids, actions, n,
       reinterpret_cast<u64*>(children), reward, done, nagari, status, committed, nullptr);
   return launched();
@@ -616,6 +706,29 @@ int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t ba
   if (n == 0) return 0;
   reset_kernel<<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<u64*>(states), done, n,
                                                base_seed, generation, sampler, completed);
+  return launched();
+}
+
+int cugo_refill_spares(uint8_t* spares, uint32_t* spare_gen, const uint32_t* generation,
+                       int64_t n, uint64_t base_seed, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!spares || !spare_gen || !generation))) return kBadArgument;
+  if (n == 0) return 0;
+  refill_kernel<<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<u64*>(spares), spare_gen,
+                                                generation, n, base_seed);
+  return launched();
+}
+
+int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
+                           uint32_t* generation, uint64_t* sampler,
+                           unsigned long long* completed, const uint8_t* spares,
+                           const uint32_t* spare_gen, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!states || !done || !generation || !sampler || !completed || !spares ||
+                          !spare_gen)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  reset_spare_kernel<<<tiles(n), kTile, 0, stream>>>(
+      reinterpret_cast<u64*>(states), done, n, base_seed, generation, sampler, completed,
+      reinterpret_cast<const u64*>(spares), spare_gen);
   return launched();
 }
 

@@ -266,6 +266,46 @@ void reset_done(torch::Tensor states, torch::Tensor done, int64_t base_seed,
              "reset_done");
 }
 
+void refill_spares(torch::Tensor spares, torch::Tensor spare_gen, torch::Tensor generation,
+                   int64_t base_seed) {
+  check_states(spares);
+  const int64_t n = spares.size(0);
+  check_1d(spare_gen, at::kInt, "spare_gen");
+  check_1d(generation, at::kInt, "generation");
+  TORCH_CHECK(spare_gen.numel() == n && generation.numel() == n,
+              "spare_gen and generation must have one entry per spare row");
+  const DeviceGuard guard(spares.device());
+  check_call(cugo_refill_spares(u8p(spares), reinterpret_cast<uint32_t*>(spare_gen.data_ptr()),
+                                reinterpret_cast<const uint32_t*>(generation.data_ptr()), n,
+                                static_cast<uint64_t>(base_seed), stream()),
+             "refill_spares");
+}
+
+void reset_done_spares(torch::Tensor states, torch::Tensor done, int64_t base_seed,
+                       torch::Tensor generation, torch::Tensor sampler, torch::Tensor completed,
+                       torch::Tensor spares, torch::Tensor spare_gen) {
+  check_states(states);
+  check_states(spares);
+  const int64_t n = states.size(0);
+  check_1d(done, at::kBool, "done");
+  check_1d(generation, at::kInt, "generation");
+  check_1d(sampler, at::kLong, "sampler");
+  check_1d(completed, at::kLong, "completed");
+  check_1d(spare_gen, at::kInt, "spare_gen");
+  TORCH_CHECK(done.numel() == n && generation.numel() == n && sampler.numel() == n &&
+                  spares.size(0) == n && spare_gen.numel() == n,
+              "done, generation, sampler, spares and spare_gen must have one entry per row");
+  TORCH_CHECK(completed.numel() >= 1, "completed must hold one counter");
+  const DeviceGuard guard(states.device());
+  check_call(cugo_reset_done_spares(
+                 u8p(states), u8p(done), n, static_cast<uint64_t>(base_seed),
+                 reinterpret_cast<uint32_t*>(generation.data_ptr()),
+                 reinterpret_cast<uint64_t*>(sampler.data_ptr()),
+                 reinterpret_cast<unsigned long long*>(completed.data_ptr()), u8p(spares),
+                 reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), stream()),
+             "reset_done_spares");
+}
+
 torch::Tensor seed_samplers(int64_t n, int64_t base_seed, torch::Tensor generation) {
   check_1d(generation, at::kInt, "generation");
   TORCH_CHECK(generation.numel() == n, "generation must have n entries");
@@ -382,6 +422,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("sample_uniform", &sample_uniform, "Uniform legal action per row (xorshift64)");
   m.def("reset_done", &reset_done, "Re-create finished rows with their next seed");
   m.def("seed_samplers", &seed_samplers, "Per-row sampler state from the row seeds");
+  m.def("refill_spares", &refill_spares, "Pre-deal the next game of rows with a stale spare");
+  m.def("reset_done_spares", &reset_done_spares,
+        "reset_done, taking each finished row's next game from its pre-dealt spare");
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
         pybind11::arg("rows") = pybind11::none());

@@ -269,6 +269,40 @@ def test_driver_sample_and_reset(ext, ref):
     assert int(completed.item()) == int(to_np(gen).sum())
 
 
+def test_driver_spare_reset_matches_reset(ext):
+    """reset_done_spares (next games pre-dealt by refill_spares every few steps, dealt
+    inline when a spare is stale) leaves states, generations, samplers and the completed
+    count identical to reset_done."""
+    announce("driver_spare_reset")
+    n = 2500
+    base = 0x7654321
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    first = torch.from_numpy(np.arange(n) & 1).to(DEV)
+    a = ext.create(torch.from_numpy(seeds).to(DEV), first)
+    b = a.clone()
+    gen_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    gen_b = gen_a.clone()
+    smp_a = ext.seed_samplers(n, base, gen_a)
+    smp_b = smp_a.clone()
+    done_a = torch.zeros(1, dtype=torch.long, device=DEV)
+    done_b = done_a.clone()
+    spares = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
+    spare_gen = torch.zeros(n, dtype=torch.int32, device=DEV)
+    for step in range(60):
+        if step % 3 == 0:
+            ext.refill_spares(spares, spare_gen, gen_b, base)
+        _, legal, _, _, _ = ext.observe(a)
+        actions = ext.sample_uniform(legal, smp_a)
+        smp_b.copy_(smp_a)
+        _, sdone, _, _, _ = ext.step(a, actions)
+        ext.step(b, actions)
+        ext.reset_done(a, sdone, base, gen_a, smp_a, done_a)
+        ext.reset_done_spares(b, sdone, base, gen_b, smp_b, done_b, spares, spare_gen)
+        assert torch.equal(a, b), step
+        assert torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), step
+    assert int(done_a.item()) == int(done_b.item()) > n
+
+
 def test_repeatable(ext):
     announce("repeatable")
     golden = np.load(GOLDEN / "rows.npz")
