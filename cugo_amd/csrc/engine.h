@@ -134,6 +134,41 @@ CG_HD u8 select_rank(u64 mask, u32 rank) {
   return (u8)pos;
 }
 
+// ------------------------------------------------------------ month nibbles ----
+// A card mask holds month m in bits 4m..4m+3, so per-month questions are nibble-parallel
+// bit arithmetic instead of twelve-iteration loops.
+constexpr u64 kNibbleLow = 0x111111111111ull;  // bit 4m of each of the 12 months
+
+// bit 4m -> bit m for m < 12 (other bits must be clear)
+CG_HD u16 gather_months(u64 x) {
+  x = (x | (x >> 3)) & 0x0303030303030303ull;
+  x = (x | (x >> 6)) & 0x000F000F000F000Full;
+  x = (x | (x >> 12)) & 0x000000FF000000FFull;
+  x = (x | (x >> 24)) & 0xFFFFull;
+  return (u16)(x & 0x0FFFu);
+}
+// bit m -> nibble 0xF of month m: the cards of the given months
+CG_HD u64 month_cards_of(u16 months) {
+  u64 x = months & 0x0FFFu;
+  x = (x | (x << 24)) & 0x000000FF000000FFull;
+  x = (x | (x << 12)) & 0x000F000F000F000Full;
+  x = (x | (x << 6)) & 0x0303030303030303ull;
+  x = (x | (x << 3)) & kNibbleLow;
+  return x * 0xFull;
+}
+// each nibble := number of cards of that month (0..4)
+CG_HD u64 month_counts(u64 cards) {
+  cards &= kStdMask;
+  cards = cards - ((cards >> 1) & 0x5555555555555555ull);
+  return (cards & 0x3333333333333333ull) + ((cards >> 2) & 0x3333333333333333ull);
+}
+// months whose count nibble equals k (k <= 4; counts <= 4, so count ^ k fits 3 bits)
+CG_HD u16 months_with_count(u64 counts, u32 k) {
+  const u64 d = counts ^ (kNibbleLow * k);
+  const u64 nonzero = (d | (d >> 1) | (d >> 2)) & kNibbleLow;
+  return gather_months(~nonzero & kNibbleLow);
+}
+
 // --------------------------------------------------------------------- rng.h ----
 // SplitMix64 (rng.h:13-32): the state is advanced in place.
 CG_HD u64 sm_next(u64& s) {
@@ -144,19 +179,23 @@ CG_HD u64 sm_next(u64& s) {
   return z ^ (z >> 31);
 }
 
-// Lemire's bounded draw with rejection (rng.h:34-54).
+// Lemire's bounded draw with rejection (rng.h:34-54).  The rejection threshold
+// (2^32 - bound) % bound is below bound, so a first draw with low >= bound is accepted
+// without it; only the rare low < bound case computes the modulo (written this way the
+// integer division stays in that branch instead of running for every draw) and redraws
+// while low < threshold, exactly as the reference loop does.
 CG_HD u32 uniform_bounded(u64& s, u32 bound) {
   if (bound <= 1u) return 0u;
-  for (;;) {
-    const u32 x = (u32)(sm_next(s) >> 32);
-    const u64 product = (u64)x * bound;
-    const u32 low = (u32)product;
-    if (low < bound) {
-      const u32 threshold = (0u - bound) % bound;
-      if (low < threshold) continue;
+  u64 product = (u64)(u32)(sm_next(s) >> 32) * bound;
+  u32 low = (u32)product;
+  if (low < bound) {
+    const u32 threshold = (0u - bound) % bound;
+    while (low < threshold) {
+      product = (u64)(u32)(sm_next(s) >> 32) * bound;
+      low = (u32)product;
     }
-    return (u32)(product >> 32);
   }
+  return (u32)(product >> 32);
 }
 
 // deal.h:50-80: draw a uniform card from `remaining` with the stream `s`.
@@ -386,10 +425,7 @@ CG_HD bool auto_floor_choice(u64 matches) {  // turn50.h:200-202
   return popc(matches) == 2 && (matches & ~kPlainPi) == 0;
 }
 CG_HD u16 floor_triple_months(u64 floor) {  // turn50.h:139-146
-  u16 months = 0;
-  for (u32 m = 0; m < 12; ++m)
-    if (popc(floor & month_cards(m)) == 3) months |= (u16)(1u << m);
-  return months;
+  return months_with_count(month_counts(floor), 3);
 }
 
 struct Resolve {
@@ -789,14 +825,8 @@ CG_HD u16 legal_special_months(const Env& e, u32 hand_count, u32 floor_count, bo
   const u64 h = active_hand(e) & kStdMask;
   const u64 f = std_floor(e);
   const u16 old = !exclude ? 0 : hand_count == 4 ? sh4_of(e, e.actor) : shaken_of(e, e.actor);
-  u16 out = 0;
-  for (u32 m = 0; m < 12; ++m) {
-    const u16 mb = (u16)(1u << m);
-    if ((old & mb) == 0 && popc(h & month_cards(m)) == hand_count &&
-        popc(f & month_cards(m)) == floor_count)
-      out |= mb;
-  }
-  return out;
+  return (u16)(months_with_count(month_counts(h), hand_count) &
+               months_with_count(month_counts(f), floor_count) & ~old & 0x0FFFu);
 }
 CG_HD u16 legal_shake_months(const Env& e) {  // special50.h:92-95
   return (u16)(legal_special_months(e, 3, 0, true) | legal_special_months(e, 4, 0, true));
@@ -976,12 +1006,9 @@ CG_HD void update_missions(Env& e, u32 actor, u64 acquired) {
   if ((e.mission & ~mine) == 0) set_mm(e, actor, e.mmult);
 }
 
-CG_HD u16 chongtong_months(u64 cards) {  // terminal50.h:215-224
+CG_HD u16 chongtong_months(u64 cards) {  // terminal50.h:215-224: all four cards held
   cards &= kStdMask;
-  u16 r = 0;
-  for (u32 m = 0; m < 12; ++m)
-    if ((cards & month_cards(m)) == month_cards(m)) r |= (u16)(1u << m);
-  return r;
+  return gather_months(cards & (cards >> 1) & (cards >> 2) & (cards >> 3) & kNibbleLow);
 }
 
 CG_HD bool terminal_finished(const Env& e) { return e.treason != kReasonNone; }
@@ -1314,12 +1341,8 @@ CG_HD Mask3 legal_primary(const Env& e) {
   const u16 shakes = legal_shake_months(e);
   u64 standard = hand & kStdMask;
   // card plays 0..47 (one bit per card, minus forced months)
-  u64 plays = 0, shake_cards = 0;
-  for (u32 mth = 0; mth < 12; ++mth) {
-    const u64 mc = standard & month_cards(mth);
-    if (!((forced >> mth) & 1u)) plays |= mc;
-    if ((shakes >> mth) & 1u) shake_cards |= mc;
-  }
+  const u64 plays = standard & ~month_cards_of(forced);
+  const u64 shake_cards = standard & month_cards_of(shakes);
   m.w0 |= plays;                                    // actions 0..47
   if (hand & bit(kBonus2)) m.w0 |= 1ull << 48;      // action 48
   if (hand & bit(kBonus3)) m.w0 |= 1ull << 49;      // action 49

@@ -497,22 +497,22 @@ __global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u
     from_spare = spare_gen[i] == gen;
     sampler[i] = sampler_seed(base_seed + (u64)i + (u64)n * gen);
   }
-  flags[lane] = reset;
-  // spare rows of this tile: whole rows, 31 lanes per row
-  u64 copy = __ballot(from_spare);
-  while (copy != 0) {
-    const int r = __builtin_ctzll(copy);
-    copy &= copy - 1;
-    if (lane < kRowWords) rows[r * kRowWords + lane] = spares[(base + r) * kRowWords + lane];
-  }
+  // 1: copy the spare row, 2: the row dealt inline into LDS
+  flags[lane] = reset ? (from_spare ? 1 : 2) : 0;
   if (reset && !from_spare)
     pack_row(create_env(base_seed + (u64)i + (u64)n * gen, (u32)(i & 1)), rows + lane * kRowWords);
   const u64 ballot = __ballot(reset);
   if (lane == 0 && ballot != 0) atomicAdd(completed, (unsigned long long)__popcll(ballot));
   __syncthreads();
+  // Consecutive lanes move consecutive words of the tile's flagged rows: independent,
+  // coalesced loads, spare rows straight from HBM to HBM.
   u64* out = states + base * kRowWords;
-  for (int j = lane; j < count * kRowWords; j += kTile)
-    if (flags[j / kRowWords]) out[j] = rows[j];
+  const u64* spare = spares + base * kRowWords;
+  for (int j = lane; j < count * kRowWords; j += kTile) {
+    const int f = flags[j / kRowWords];
+    if (f == 1) out[j] = spare[j];
+    else if (f == 2) out[j] = rows[j];
+  }
 }
 
 __global__ __launch_bounds__(256) void seed_kernel(i64 n, u64 base_seed, const u32* generation,
