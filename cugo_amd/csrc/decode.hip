@@ -16,7 +16,7 @@
 //   * a slot row of dh elements is split into 16-byte parts; L = dh*elem/16 lanes hold
 //     one slot and the wavefront covers S = 64/L consecutive slots per load
 //     instruction, so each load instruction reads 1 KiB of contiguous cache;
-//   * U = 4 such loads of K and of V are issued before any math (8 KiB in flight per
+//   * U = 8 such loads of K and of V are issued before any math (16 KiB in flight per
 //     wave), then scores are reduced over the L lanes of a slot;
 //   * softmax is online (running max / sum per lane group, base-2 exponentials with
 //     log2(e) folded into the scale) and the S lane groups merge their partial
@@ -80,7 +80,7 @@ struct F32 {
 
 constexpr float kNegInf = -__builtin_inff();
 constexpr int kWaves = 4;   // (query, head) pairs per workgroup
-constexpr int kUnroll = 4;  // loads of K (and of V) in flight per lane
+constexpr int kUnroll = 8;  // loads of K (and of V) in flight per lane
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -94,7 +94,7 @@ __device__ inline float reduce_lanes(float s) {
   return s;
 }
 
-template <class QT, class KT, int DH, bool APPEND>
+template <class QT, class KT, int DH, bool APPEND, int U = kUnroll>
 __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     const typename QT::storage* __restrict__ q, typename KT::storage* __restrict__ keys,
     typename KT::storage* __restrict__ values, const typename KT::storage* __restrict__ k_new,
@@ -169,18 +169,18 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 
   int64_t c = 0;
   // Full chunks: U loads of S slots each, every slot valid.
-  for (; c + (int64_t)S * kUnroll <= limit; c += (int64_t)S * kUnroll) {
-    uint4 kr[kUnroll], vr[kUnroll];
+  for (; c + (int64_t)S * U <= limit; c += (int64_t)S * U) {
+    uint4 kr[U], vr[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const size_t off = (size_t)(c + u * S + srow) * DH;
       kr[u] = *reinterpret_cast<const uint4*>(kb + off);
       vr[u] = *reinterpret_cast<const uint4*>(vb + off);
     }
-    float s[kUnroll];
+    float s[U];
     float mx = kNegInf;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       float kf[E];
       KT::unpack(kr[u], kf);
       float d = 0.f;
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[e] *= alpha;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       const float p = exp2_fast(s[u] - mn);
       l += p;
       float vf[E];
