@@ -63,6 +63,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-rollout", action="store_true")
+    p.add_argument("--streams", type=int, default=4,
+                   help="slices of the batch stepped on their own streams")
+    p.add_argument("--no-graph", action="store_true", help="issue the loop eagerly")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
     p.add_argument("--decode-steps", type=int, default=20)
@@ -70,7 +73,13 @@ def parse() -> argparse.Namespace:
     return p.parse_args()
 
 
-def random_policy(ext, torch, batch: int, steps: int, warmup: int) -> dict:
+def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
+                  graph: bool) -> dict:
+    """The timed loop.  The batch is cut into `streams` contiguous slices (even length),
+    each stepped on its own default-priority stream; REFILL steps of every slice form one
+    block, captured once as a HIP graph and replayed (or issued eagerly with graph=False).
+    Every slice deals the same games the unsliced batch would: seed = base + global row +
+    batch * generation."""
     dev = torch.device("cuda")
     idx = torch.arange(batch, dtype=torch.int64, device=dev)
     states = ext.create(idx + SEED_BASE, idx & 1)
@@ -81,38 +90,58 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int) -> dict:
     # copies its spare (dealt inline if stale), the same rows reset_done would deal.
     spares = torch.empty((batch, 248), dtype=torch.uint8, device=dev)
     spare_gen = torch.zeros(batch, dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream()
-    counter = [0]
+    if batch % (2 * streams):
+        raise SystemExit("the batch must split into slices of even length")
+    width = batch // streams
+    side = [torch.cuda.Stream() for _ in range(streams)]
 
-    def one_step(events=None):
-        if counter[0] % REFILL == 0:
-            ext.refill_spares(spares, spare_gen, gen, SEED_BASE)
-        counter[0] += 1
-        if events is not None:
-            events[0].record(stream)
-        _, legal, _, _, _ = ext.observe(states)
-        if events is not None:
-            events[1].record(stream)
-        actions = ext.sample_uniform(legal, sampler)
-        _, done, _, _, _ = ext.step(states, actions)
-        ext.reset_done_spares(states, done, SEED_BASE, gen, sampler, completed, spares, spare_gen)
+    def block(nsteps: int) -> None:
+        """nsteps loop steps on every slice; the first one pre-deals the spares."""
+        cur = torch.cuda.current_stream()
+        for s in side:
+            s.wait_stream(cur)
+        for k, s in enumerate(side):
+            r = slice(k * width, (k + 1) * width)
+            st, g, sm, sp, sg = states[r], gen[r], sampler[r], spares[r], spare_gen[r]
+            base = SEED_BASE + k * width
+            with torch.cuda.stream(s):
+                for t in range(nsteps):
+                    if t == 0:
+                        ext.refill_spares(sp, sg, g, base, batch)
+                    _, legal, _, _, _ = ext.observe(st)
+                    actions = ext.sample_uniform(legal, sm)
+                    _, done, _, _, _ = ext.step(st, actions)
+                    ext.reset_done_spares(st, done, base, g, sm, completed, sp, sg, batch)
+        for s in side:
+            cur.wait_stream(s)
 
-    for _ in range(warmup):
-        one_step()
+    def runner(nsteps: int):
+        if not graph or nsteps == 0:
+            return lambda: block(nsteps)
+        block(nsteps)  # warm the allocator and handles outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            block(nsteps)
+        return g.replay
+
+    for _ in range(warmup // REFILL):
+        block(REFILL)
+    block(warmup % REFILL)
+    full, rest = runner(REFILL), runner(steps % REFILL)
     torch.cuda.synchronize()
     start_games = int(completed.item())
-    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for k in range(steps):
-        one_step(pairs[k])
+    for _ in range(steps // REFILL):
+        full()
+    rest()
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
     games = int(completed.item()) - start_games
-    in_loop_ms = sum(a.elapsed_time(b) for a, b in pairs) / steps
-    # The observe kernel alone on the loop's live (mid-game) states: back-to-back launches
-    # between two events on its stream, so per-launch event overhead does not count.
+    # The observe kernel alone on the loop's live (mid-game) states, whole batch: 50
+    # back-to-back launches between two events on the stream they run on.
+    stream = torch.cuda.current_stream()
     reps = 50
     burst = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
     burst[0].record(stream)
@@ -121,8 +150,7 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int) -> dict:
     burst[1].record(stream)
     torch.cuda.synchronize()
     observe_ms = burst[0].elapsed_time(burst[1]) / reps
-    return {"seconds": seconds, "games": games, "observe_ms": observe_ms,
-            "observe_in_loop_ms": in_loop_ms}
+    return {"seconds": seconds, "games": games, "observe_ms": observe_ms}
 
 
 def branch_workload(ext, torch, iters: int) -> dict:
@@ -442,7 +470,8 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    rp = random_policy(ext, torch, args.batch, args.steps, args.warmup)
+    rp = random_policy(ext, torch, args.batch, args.steps, args.warmup, args.streams,
+                       not args.no_graph)
     games_per_s = rp["games"] / rp["seconds"]
     ms_per_step = 1000.0 * rp["seconds"] / args.steps
     observe_gbs = args.batch * OBSERVE_BYTES_PER_ROW / (rp["observe_ms"] * 1e-3) / 1e9
@@ -461,7 +490,8 @@ def main() -> None:
         "data": "synthetic",
         "config": {"workload": "random-policy self-play: observe -> sample -> step -> reset",
                    "batch": args.batch, "seed_base": hex(SEED_BASE),
-                   "policy": "uniform legal action, per-game xorshift64"},
+                   "policy": "uniform legal action, per-game xorshift64",
+                   "streams": args.streams, "hip_graph": not args.no_graph},
         "steps_per_s": round(args.batch * args.steps / rp["seconds"], 1),
         "games_timed": rp["games"],
         "roofline": {"kernel": "observe_kernel", "bound": "hbm",
@@ -469,8 +499,7 @@ def main() -> None:
                      "frac": round(observe_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("observe_kernel", str(args.batch)),
                      "bytes_per_row": OBSERVE_BYTES_PER_ROW,
-                     "avg_launch_ms": round(rp["observe_ms"], 4),
-                     "in_loop_event_ms": round(rp["observe_in_loop_ms"], 4)},
+                     "avg_launch_ms": round(rp["observe_ms"], 4)},
     }
     if not args.no_branch:
         result["branch"] = branch_workload(ext, torch, args.branch_iters)

@@ -453,7 +453,7 @@ __global__ __launch_bounds__(kTile) void reset_kernel(u64* states, const u8* don
 // generation[i] + 1 of row i, spare_gen[i] = generation[i] + 1.
 __global__ __launch_bounds__(kTile) void refill_kernel(u64* spares, u32* spare_gen,
                                                        const u32* generation, i64 n,
-                                                       u64 base_seed) {
+                                                       u64 base_seed, u64 stride) {
   __shared__ u64 rows[kTileWords];
   __shared__ int flags[kTile];
   const i64 base = tile_base();
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(kTile) void refill_kernel(u64* spares, u32* spare_g
   const bool stale = lane < count && spare_gen[i] != next;
   flags[lane] = stale;
   if (stale) {
-    const u64 seed = base_seed + (u64)i + (u64)n * next;
+    const u64 seed = base_seed + (u64)i + stride * next;
     pack_row(create_env(seed, (u32)(i & 1)), rows + lane * kRowWords);
     spare_gen[i] = next;
   }
@@ -477,7 +477,8 @@ __global__ __launch_bounds__(kTile) void refill_kernel(u64* spares, u32* spare_g
 // reset_kernel's result, taking a finished row's next game from its pre-dealt spare
 // (dealt inline only when the spare is stale).
 __global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u8* done, i64 n,
-                                                            u64 base_seed, u32* generation,
+                                                            u64 base_seed, u64 stride,
+                                                            u32* generation,
                                                             u64* sampler,
                                                             unsigned long long* completed,
                                                             const u64* spares,
@@ -495,12 +496,12 @@ __global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u
     gen = generation[i] + 1u;
     generation[i] = gen;
     from_spare = spare_gen[i] == gen;
-    sampler[i] = sampler_seed(base_seed + (u64)i + (u64)n * gen);
+    sampler[i] = sampler_seed(base_seed + (u64)i + stride * gen);
   }
   // 1: copy the spare row, 2: the row dealt inline into LDS
   flags[lane] = reset ? (from_spare ? 1 : 2) : 0;
   if (reset && !from_spare)
-    pack_row(create_env(base_seed + (u64)i + (u64)n * gen, (u32)(i & 1)), rows + lane * kRowWords);
+    pack_row(create_env(base_seed + (u64)i + stride * gen, (u32)(i & 1)), rows + lane * kRowWords);
   const u64 ballot = __ballot(reset);
   if (lane == 0 && ballot != 0) atomicAdd(completed, (unsigned long long)__popcll(ballot));
   __syncthreads();
@@ -710,25 +711,27 @@ int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t ba
 }
 
 int cugo_refill_spares(uint8_t* spares, uint32_t* spare_gen, const uint32_t* generation,
-                       int64_t n, uint64_t base_seed, hipStream_t stream) {
-  if (n < 0 || (n > 0 && (!spares || !spare_gen || !generation))) return kBadArgument;
+                       int64_t n, uint64_t base_seed, int64_t seed_stride, hipStream_t stream) {
+  if (n < 0 || seed_stride < 0 || (n > 0 && (!spares || !spare_gen || !generation)))
+    return kBadArgument;
   if (n == 0) return 0;
   refill_kernel<<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<u64*>(spares), spare_gen,
-                                                generation, n, base_seed);
+                                                generation, n, base_seed, (u64)seed_stride);
   return launched();
 }
 
 int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
-                           uint32_t* generation, uint64_t* sampler,
+                           int64_t seed_stride, uint32_t* generation, uint64_t* sampler,
                            unsigned long long* completed, const uint8_t* spares,
                            const uint32_t* spare_gen, hipStream_t stream) {
-  if (n < 0 || (n > 0 && (!states || !done || !generation || !sampler || !completed || !spares ||
-                          !spare_gen)))
+  if (n < 0 || seed_stride < 0 ||
+      (n > 0 && (!states || !done || !generation || !sampler || !completed || !spares ||
+                 !spare_gen)))
     return kBadArgument;
   if (n == 0) return 0;
   reset_spare_kernel<<<tiles(n), kTile, 0, stream>>>(
-      reinterpret_cast<u64*>(states), done, n, base_seed, generation, sampler, completed,
-      reinterpret_cast<const u64*>(spares), spare_gen);
+      reinterpret_cast<u64*>(states), done, n, base_seed, (u64)seed_stride, generation, sampler,
+      completed, reinterpret_cast<const u64*>(spares), spare_gen);
   return launched();
 }
 

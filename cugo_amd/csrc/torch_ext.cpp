@@ -267,7 +267,7 @@ void reset_done(torch::Tensor states, torch::Tensor done, int64_t base_seed,
 }
 
 void refill_spares(torch::Tensor spares, torch::Tensor spare_gen, torch::Tensor generation,
-                   int64_t base_seed) {
+                   int64_t base_seed, int64_t seed_stride) {
   check_states(spares);
   const int64_t n = spares.size(0);
   check_1d(spare_gen, at::kInt, "spare_gen");
@@ -277,13 +277,14 @@ void refill_spares(torch::Tensor spares, torch::Tensor spare_gen, torch::Tensor 
   const DeviceGuard guard(spares.device());
   check_call(cugo_refill_spares(u8p(spares), reinterpret_cast<uint32_t*>(spare_gen.data_ptr()),
                                 reinterpret_cast<const uint32_t*>(generation.data_ptr()), n,
-                                static_cast<uint64_t>(base_seed), stream()),
+                                static_cast<uint64_t>(base_seed),
+                                seed_stride < 0 ? n : seed_stride, stream()),
              "refill_spares");
 }
 
 void reset_done_spares(torch::Tensor states, torch::Tensor done, int64_t base_seed,
                        torch::Tensor generation, torch::Tensor sampler, torch::Tensor completed,
-                       torch::Tensor spares, torch::Tensor spare_gen) {
+                       torch::Tensor spares, torch::Tensor spare_gen, int64_t seed_stride) {
   check_states(states);
   check_states(spares);
   const int64_t n = states.size(0);
@@ -299,6 +300,7 @@ void reset_done_spares(torch::Tensor states, torch::Tensor done, int64_t base_se
   const DeviceGuard guard(states.device());
   check_call(cugo_reset_done_spares(
                  u8p(states), u8p(done), n, static_cast<uint64_t>(base_seed),
+                 seed_stride < 0 ? n : seed_stride,
                  reinterpret_cast<uint32_t*>(generation.data_ptr()),
                  reinterpret_cast<uint64_t*>(sampler.data_ptr()),
                  reinterpret_cast<unsigned long long*>(completed.data_ptr()), u8p(spares),
@@ -422,9 +424,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("sample_uniform", &sample_uniform, "Uniform legal action per row (xorshift64)");
   m.def("reset_done", &reset_done, "Re-create finished rows with their next seed");
   m.def("seed_samplers", &seed_samplers, "Per-row sampler state from the row seeds");
-  m.def("refill_spares", &refill_spares, "Pre-deal the next game of rows with a stale spare");
+  m.def("refill_spares", &refill_spares, "Pre-deal the next game of rows with a stale spare",
+        pybind11::arg("spares"), pybind11::arg("spare_gen"), pybind11::arg("generation"),
+        pybind11::arg("base_seed"), pybind11::arg("seed_stride") = -1);
   m.def("reset_done_spares", &reset_done_spares,
-        "reset_done, taking each finished row's next game from its pre-dealt spare");
+        "reset_done, taking each finished row's next game from its pre-dealt spare",
+        pybind11::arg("states"), pybind11::arg("done"), pybind11::arg("base_seed"),
+        pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("completed"),
+        pybind11::arg("spares"), pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1);
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
         pybind11::arg("rows") = pybind11::none());

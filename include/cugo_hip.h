@@ -112,14 +112,17 @@ int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t ba
                     hipStream_t stream);
 /* Pre-dealt next games for cugo_reset_done_spares: every row i whose spare_gen[i] is not
  * generation[i] + 1 gets game generation[i] + 1 of row i dealt into spare row i
- * (seed = base_seed + i + n * (generation[i] + 1), first = i & 1) and spare_gen[i] set.
- * spares: uint8 [n, CUGO_STATE_BYTES]; spare_gen: uint32 [n], start it at 0. */
+ * (seed = base_seed + i + seed_stride * (generation[i] + 1), first = i & 1) and
+ * spare_gen[i] set.  spares: uint8 [n, CUGO_STATE_BYTES]; spare_gen: uint32 [n], start
+ * it at 0.  seed_stride = n gives cugo_reset_done's seeds; a slice of a larger batch
+ * starting at an even row r0 passes base_seed + r0 and the whole batch's size. */
 int cugo_refill_spares(uint8_t* spares, uint32_t* spare_gen, const uint32_t* generation,
-                       int64_t n, uint64_t base_seed, hipStream_t stream);
-/* Same effect as cugo_reset_done, except that a finished row copies its next game from
- * its spare row when spare_gen[i] names it (deals it inline otherwise). */
+                       int64_t n, uint64_t base_seed, int64_t seed_stride, hipStream_t stream);
+/* Same effect as cugo_reset_done with seed = base_seed + i + seed_stride * generation[i],
+ * except that a finished row copies its next game from its spare row when spare_gen[i]
+ * names it (deals it inline otherwise). */
 int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
-                           uint32_t* generation, uint64_t* sampler,
+                           int64_t seed_stride, uint32_t* generation, uint64_t* sampler,
                            unsigned long long* completed, const uint8_t* spares,
                            const uint32_t* spare_gen, hipStream_t stream);
 /* sampler[i] = SplitMix64(base_seed + i + batch * generation[i]).next(), never 0. */

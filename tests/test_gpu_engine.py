@@ -288,19 +288,40 @@ def test_driver_spare_reset_matches_reset(ext):
     done_b = done_a.clone()
     spares = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
     spare_gen = torch.zeros(n, dtype=torch.int32, device=DEV)
+    # c: the same batch as two slices on their own streams, seeds strided by the batch
+    c = a.clone()
+    gen_c, smp_c, done_c = gen_a.clone(), smp_a.clone(), done_a.clone()
+    spares_c = torch.zeros_like(spares)
+    spare_gen_c = torch.zeros_like(spare_gen)
+    half = n // 2  # even
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
     for step in range(60):
         if step % 3 == 0:
             ext.refill_spares(spares, spare_gen, gen_b, base)
         _, legal, _, _, _ = ext.observe(a)
         actions = ext.sample_uniform(legal, smp_a)
         smp_b.copy_(smp_a)
+        smp_c.copy_(smp_a)
         _, sdone, _, _, _ = ext.step(a, actions)
         ext.step(b, actions)
         ext.reset_done(a, sdone, base, gen_a, smp_a, done_a)
         ext.reset_done_spares(b, sdone, base, gen_b, smp_b, done_b, spares, spare_gen)
-        assert torch.equal(a, b), step
+        cur = torch.cuda.current_stream()
+        for k, st in enumerate(streams):
+            st.wait_stream(cur)
+            with torch.cuda.stream(st):
+                r = slice(k * half, (k + 1) * half)
+                if step % 5 == 0:
+                    ext.refill_spares(spares_c[r], spare_gen_c[r], gen_c[r], base + k * half, n)
+                _, cdone, _, _, _ = ext.step(c[r], actions[r])
+                ext.reset_done_spares(c[r], cdone, base + k * half, gen_c[r], smp_c[r], done_c,
+                                      spares_c[r], spare_gen_c[r], n)
+        for st in streams:
+            cur.wait_stream(st)
+        assert torch.equal(a, b) and torch.equal(a, c), step
         assert torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), step
-    assert int(done_a.item()) == int(done_b.item()) > n
+        assert torch.equal(gen_a, gen_c) and torch.equal(smp_a, smp_c), step
+    assert int(done_a.item()) == int(done_b.item()) == int(done_c.item()) > n
 
 
 def test_repeatable(ext):
