@@ -85,7 +85,6 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     states = ext.create(idx + SEED_BASE, idx & 1)
     gen = torch.zeros(batch, dtype=torch.int32, device=dev)
     sampler = ext.seed_samplers(batch, SEED_BASE, gen)
-    completed = torch.zeros(1, dtype=torch.int64, device=dev)
     # Next games are pre-dealt in full-width batches every REFILL steps; a finished row
     # copies its spare (dealt inline if stale), the same rows reset_done would deal.
     spares = torch.empty((batch, 248), dtype=torch.uint8, device=dev)
@@ -108,10 +107,10 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
                 for t in range(nsteps):
                     if t == 0:
                         ext.refill_spares(sp, sg, g, base, batch)
-                    _, legal, _, _, _ = ext.observe(st)
-                    actions = ext.sample_uniform(legal, sm)
-                    _, done, _, _, _ = ext.step(st, actions)
-                    ext.reset_done_spares(st, done, base, g, sm, completed, sp, sg, batch)
+                    # observe + the random policy's draw from the legal mask, one launch
+                    _, _, _, _, _, actions = ext.observe_sample(st, sm)
+                    # step + auto-reset of the finished rows from their spares, one launch
+                    ext.step_reset_spares(st, actions, base, g, sm, sp, sg, batch)
         for s in side:
             cur.wait_stream(s)
 
@@ -130,7 +129,8 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     block(warmup % REFILL)
     full, rest = runner(REFILL), runner(steps % REFILL)
     torch.cuda.synchronize()
-    start_games = int(completed.item())
+    # Every finished game bumps its row's generation once.
+    start_games = int(gen.sum(dtype=torch.int64).item())
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps // REFILL):
@@ -138,7 +138,7 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     rest()
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
-    games = int(completed.item()) - start_games
+    games = int(gen.sum(dtype=torch.int64).item()) - start_games
     # The observe kernel alone on the loop's live (mid-game) states, whole batch: 50
     # back-to-back launches between two events on the stream they run on.
     stream = torch.cuda.current_stream()
@@ -366,7 +366,6 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
     states = ext.create(idx + base, idx & 1)
     gen = torch.zeros(batch, dtype=torch.int32, device=dev)
     sampler = ext.seed_samplers(batch, base, gen)
-    completed = torch.zeros(1, dtype=torch.int64, device=dev)
     buf = {
         "features": torch.empty(horizon, batch, 720, dtype=torch.bfloat16, device=dev),
         "legal": torch.empty(horizon, batch, 179, dtype=torch.bool, device=dev),
@@ -394,7 +393,7 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         if ev is not None:
             ev[2].record(stream)
         reward, done, _, _, _ = ext.step(states, action)
-        ext.reset_done(states, done, base, gen, sampler, completed)
+        ext.reset_done(states, done, base, gen, sampler)
         if ev is not None:
             ev[3].record(stream)
         buf["features"][t].copy_(f16)
@@ -410,7 +409,7 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
             one_step(t)
         torch.cuda.synchronize()
         events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(horizon)]
-        games0 = int(completed.item())
+        games0 = int(gen.sum(dtype=torch.int64).item())
         t0 = time.perf_counter()
         for t in range(horizon):
             one_step(t, events[t])
@@ -425,7 +424,7 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
             "policy_share": round(policy_ms / (wall * 1e3), 4),
             "engine_ms": round(engine_ms, 2), "policy_ms": round(policy_ms, 2),
             "policy_tflops": round(flops / (policy_ms * 1e-3) / 1e12, 1),
-            "games_completed": int(completed.item()) - games0,
+            "games_completed": int(gen.sum(dtype=torch.int64).item()) - games0,
             "batch": batch, "horizon": horizon, "dtype": "bf16"}
 
 

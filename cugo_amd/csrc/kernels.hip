@@ -116,12 +116,43 @@ __device__ inline u32 spread4(u32 x) {
 // workgroups per CU then hold all 1,024 tiles of a 65,536-row batch at once.
 constexpr int kObsThreads = 192;
 
-template <bool kIndexed>
+// ------------------------------------------------------- random-policy draw ----
+__device__ inline u64 xorshift64(u64& x) {
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  return x;
+}
+
+__device__ inline u64 sampler_seed(u64 seed) {
+  u64 s = seed;
+  const u64 v = sm_next(s);
+  return v != 0 ? v : 1ull;
+}
+
+// Uniform draw over the set bits of a 179-bit action mask (actions 0..63 in m0, 64..127
+// in m1, 128..178 in m2): one xorshift64 step of the sampler word x, then the
+// (value % count)-th set bit.  -1, with x untouched, when no bit is set.
+__device__ inline i64 draw_legal(u64 m0, u64 m1, u64 m2, u64& x) {
+  const u32 c0 = popc(m0), c1 = popc(m1);
+  const u32 total = c0 + c1 + popc(m2);
+  if (total == 0) return -1;
+  const u32 pick = (u32)(xorshift64(x) % total);
+  if (pick < c0) return select_rank(m0, pick);
+  if (pick < c0 + c1) return 64 + select_rank(m1, pick - c0);
+  return 128 + select_rank(m2, pick - c0 - c1);
+}
+
+// kSample: also draw each row's random-policy action from its legal mask while the mask
+// is in registers (draw_legal with sampler[i], into actions[i]), as sample_kernel would
+// from the stored mask.
+template <bool kIndexed, bool kSample = false>
 __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states, i64 env_count,
                                                               const i64* ids, i64 n,
                                                               float* features, u8* legal,
                                                               u8* player, u8* done,
-                                                              i16* status) {
+                                                              i16* status, u64* sampler = nullptr,
+                                                              i64* actions = nullptr) {
   __shared__ ObserveTile t;
   __shared__ i64 tile_ids[kTile];
   const i64 base = tile_base();
@@ -164,12 +195,19 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
       player[i] = pk.head.player;
       done[i] = e.done != 0;
       status[i] = (i16)pk.head.status;
+      if (kSample) {
+        u64 x = sampler[i];
+        const i64 a = draw_legal(pk.head.legal.w0, pk.head.legal.w1, pk.head.legal.w2, x);
+        if (a >= 0) sampler[i] = x;
+        actions[i] = a;
+      }
     } else {  // invalid id (torch50_ext.cu:71-87): an all-zero row
       for (int k = 0; k < kFeatRecord; ++k) rec[k] = 0u;
       t.out.legal[lane][0] = t.out.legal[lane][1] = t.out.legal[lane][2] = 0;
       player[i] = 0;
       done[i] = 1;
       status[i] = CUGO_INVALID_INDEX_STATUS;
+      if (kSample) actions[i] = -1;
     }
   }
   __syncthreads();
@@ -234,8 +272,20 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
 }
 
 // --------------------------------------------------------------------- step ----
+// Auto-reset of finished rows inside the step (kMode 3): the next game of row i is
+// seed = base_seed + i + stride * (++generation[i]), copied from spare row i when
+// spare_gen[i] names it and dealt inline otherwise; sampler[i] is re-seeded from it.
+struct AutoReset {
+  u64 base_seed, stride;
+  u32* generation;
+  u64* sampler;
+  const u64* spares;
+  const u32* spare_gen;
+};
+
 // kMode: 0 = step (contiguous, in place), 1 = step_indexed (gather/scatter in place),
-// 2 = branch_indexed (gather from parents, children written contiguously).
+// 2 = branch_indexed (gather from parents, children written contiguously),
+// 3 = step with the auto-reset above (contiguous, in place).
 // kThreads = 128: two waves per tile of 64 games, both stage the rows in and out and
 // wave 0 runs the games (one per lane).  At ~250 VGPRs two waves fit per SIMD, so this
 // is the shape while every tile of the grid is resident at once (up to four per CU);
@@ -245,18 +295,22 @@ template <int kMode, bool kEvents, int kStepThreads>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env_count, const i64* ids,
                                                      const i64* actions, i64 n, u64* children,
                                                      float* reward, u8* done, u8* nagari,
-                                                     i16* status, u8* committed, i64* events) {
+                                                     i16* status, u8* committed, i64* events,
+                                                     AutoReset ar) {
   __shared__ u64 rows[kTileWords];
   __shared__ i64 tile_ids[kTile];
   __shared__ i64 ev[kTile * kEventWords];
+  __shared__ int spare_rows[kTile];  // kMode 3: tile rows whose next game is a spare
+  __shared__ int spare_count;
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int lane = threadIdx.x;
-  constexpr bool kIndexed = kMode != 0;
+  constexpr bool kIndexed = kMode == 1 || kMode == 2;
   if (kIndexed && lane < count) tile_ids[lane] = ids[base + lane];
   __syncthreads();
   stage_in<kStepThreads>(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
   __syncthreads();
+  bool take_spare = false;
   if (lane < count) {
     const i64 i = base + lane;
     const bool ok = !kIndexed || valid_id(tile_ids[lane], env_count);
@@ -283,6 +337,14 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
       nagari[i] = so.nagari;
       status[i] = (i16)so.status;
       committed[i] = so.committed;
+      if (kMode == 3 && so.done) {
+        const u32 gen = ar.generation[i] + 1u;
+        ar.generation[i] = gen;
+        const u64 seed = ar.base_seed + (u64)i + ar.stride * gen;
+        ar.sampler[i] = sampler_seed(seed);
+        take_spare = ar.spare_gen[i] == gen;
+        if (!take_spare) pack_row(create_env(seed, (u32)(i & 1)), row);
+      }
     } else {  // torch50_ext.cu:108-118
       if (kEvents) for (int k = 0; k < kEventWords; ++k) evr[k] = 0;
       if (kMode == 2) for (int k = 0; k < kRowWords; ++k) row[k] = 0;
@@ -293,8 +355,22 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
       committed[i] = 0;
     }
   }
+  if (kMode == 3) {
+    // Compact the spare-taking rows so that every lane's spare load is independent:
+    // a tile with f such rows moves 31 f words in ceil(31 f / threads) passes.
+    const u64 ballot = __ballot(take_spare);
+    if (take_spare) spare_rows[__popcll(ballot & ((1ull << lane) - 1ull))] = lane;
+    if (lane == 0) spare_count = (int)__popcll(ballot);
+    __syncthreads();
+    const int words = spare_count * kRowWords;
+    for (int j = lane; j < words; j += kStepThreads) {
+      const int r = spare_rows[j / kRowWords];
+      const int k = j - (j / kRowWords) * kRowWords;
+      rows[r * kRowWords + k] = ar.spares[(base + r) * kRowWords + k];
+    }
+  }
   __syncthreads();
-  if (kMode == 0) stage_out<kStepThreads>(rows, states, nullptr, base, count, env_count);
+  if (kMode == 0 || kMode == 3) stage_out<kStepThreads>(rows, states, nullptr, base, count, env_count);
   else if (kMode == 1) stage_out<kStepThreads>(rows, states, tile_ids, base, count, env_count);
   else stage_out<kStepThreads>(rows, children, nullptr, base, count, env_count);
   if (kEvents) {
@@ -357,19 +433,6 @@ __global__ __launch_bounds__(256) void stock_kernel(const u64* states, i64 env_c
 }
 
 // ------------------------------------------------------- random-policy driver ----
-__device__ inline u64 xorshift64(u64& x) {
-  x ^= x << 13;
-  x ^= x >> 7;
-  x ^= x << 17;
-  return x;
-}
-
-__device__ inline u64 sampler_seed(u64 seed) {
-  u64 s = seed;
-  const u64 v = sm_next(s);
-  return v != 0 ? v : 1ull;
-}
-
 // Tile of 64 mask rows staged in LDS (coalesced dwords); lane r turns its row's 179
 // bytes into three 64-bit words and picks the rank-th set bit.  A dword of four 0/1
 // bytes becomes a nibble with one multiply: d * 0x00204081 = d + d<<7 + d<<14 + d<<21
@@ -407,18 +470,11 @@ __global__ __launch_bounds__(kTile) void sample_kernel(const u8* legal, i64 n, u
   const u64 m0 = (w[0] >> off) | (off ? w[1] << (64 - off) : 0ull);
   const u64 m1 = (w[1] >> off) | (off ? w[2] << (64 - off) : 0ull);
   const u64 m2 = (w[2] >> off) & ((1ull << (kActionCount - 128)) - 1ull);
-  const u32 c0 = popc(m0), c1 = popc(m1);
-  const u32 total = c0 + c1 + popc(m2);
   const i64 i = base + lane;
-  if (total == 0) { actions[i] = -1; return; }
   u64 x = sampler[i];
-  u32 pick = (u32)(xorshift64(x) % total);
-  sampler[i] = x;
-  int chosen;
-  if (pick < c0) chosen = select_rank(m0, pick);
-  else if (pick < c0 + c1) chosen = 64 + select_rank(m1, pick - c0);
-  else chosen = 128 + select_rank(m2, pick - c0 - c1);
-  actions[i] = chosen;
+  const i64 a = draw_legal(m0, m1, m2, x);
+  if (a >= 0) sampler[i] = x;
+  actions[i] = a;
 }
 
 __global__ __launch_bounds__(kTile) void reset_kernel(u64* states, const u8* done, i64 n,
@@ -442,7 +498,8 @@ __global__ __launch_bounds__(kTile) void reset_kernel(u64* states, const u8* don
     sampler[i] = sampler_seed(seed);
   }
   const u64 ballot = __ballot(reset);
-  if (lane == 0 && ballot != 0) atomicAdd(completed, (unsigned long long)__popcll(ballot));
+  if (completed != nullptr && lane == 0 && ballot != 0)
+    atomicAdd(completed, (unsigned long long)__popcll(ballot));
   __syncthreads();
   u64* out = states + base * kRowWords;
   for (int j = lane; j < count * kRowWords; j += kTile)
@@ -503,7 +560,8 @@ __global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u
   if (reset && !from_spare)
     pack_row(create_env(base_seed + (u64)i + stride * gen, (u32)(i & 1)), rows + lane * kRowWords);
   const u64 ballot = __ballot(reset);
-  if (lane == 0 && ballot != 0) atomicAdd(completed, (unsigned long long)__popcll(ballot));
+  if (completed != nullptr && lane == 0 && ballot != 0)
+    atomicAdd(completed, (unsigned long long)__popcll(ballot));
   __syncthreads();
   // Consecutive lanes move consecutive words of the tile's flagged rows: independent,
   // coalesced loads, spare rows straight from HBM to HBM.
@@ -584,6 +642,19 @@ int cugo_observe(const uint8_t* states, int64_t n, float* features, uint8_t* leg
   return launched();
 }
 
+int cugo_observe_sample(const uint8_t* states, int64_t n, float* features, uint8_t* legal,
+                        uint8_t* player, uint8_t* done, int16_t* status, uint64_t* sampler,
+                        int64_t* actions, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!states || !features || !legal || !player || !done || !status ||
+                          !sampler || !actions)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  observe_kernel<false, true><<<tiles(n), kObsThreads, 0, stream>>>(
+      reinterpret_cast<const u64*>(states), n, nullptr, n, features, legal, player, done,
+      status, reinterpret_cast<u64*>(sampler), actions);
+  return launched();
+}
+
 int cugo_observe_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids,
                          int64_t n, float* features, uint8_t* legal, uint8_t* player,
                          uint8_t* done, int16_t* status, hipStream_t stream) {
@@ -605,7 +676,24 @@ int cugo_step(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
   if (n == 0) return 0;
   launch_step<0, false>(n, stream, 
       reinterpret_cast<u64*>(states), n, nullptr, actions, n, nullptr, reward, done, nagari,
-      status, committed, nullptr);
+      status, committed, nullptr, AutoReset{});
+  return launched();
+}
+
+int cugo_step_reset_spares(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
+                           uint8_t* done, uint8_t* nagari, int16_t* status, uint8_t* committed,
+                           uint64_t base_seed, int64_t seed_stride, uint32_t* generation,
+                           uint64_t* sampler, const uint8_t* spares, const uint32_t* spare_gen,
+                           hipStream_t stream) {
+  if (n < 0 || seed_stride < 0 ||
+      (n > 0 && (!states || !actions || !reward || !done || !nagari || !status || !committed ||
+                 !generation || !sampler || !spares || !spare_gen)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  const AutoReset ar{base_seed, (u64)seed_stride, generation, reinterpret_cast<u64*>(sampler),
+                     reinterpret_cast<const u64*>(spares), spare_gen};
+  launch_step<3, false>(n, stream, reinterpret_cast<u64*>(states), n, nullptr, actions, n,
+                        nullptr, reward, done, nagari, status, committed, nullptr, ar);
   return launched();
 }
 
@@ -619,7 +707,7 @@ int cugo_step_indexed(uint8_t* states, int64_t env_count, const int64_t* ids,
   if (n == 0) return 0;
   launch_step<1, false>(n, stream, 
       reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
-      nagari, status, committed, nullptr);
+      nagari, status, committed, nullptr, AutoReset{});
   return launched();
 }
 
@@ -634,7 +722,7 @@ int cugo_step_events_indexed(uint8_t* states, int64_t env_count, const int64_t* 
   if (n == 0) return 0;
   launch_step<1, true>(n, stream, 
       reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
-      nagari, status, committed, events);
+      nagari, status, committed, events, AutoReset{});
   return launched();
 }
 
@@ -669,7 +757,8 @@ int cugo_branch_indexed(const uint8_t* states, int64_t env_count, const int64_t*
   if (n == 0) return 0;
   launch_step<2, false>(n, stream, 
       const_cast<u64*>(reinterpret_cast<const u64*>(states)), env_count, ids, actions, n,
-      reinterpret_cast<u64*>(children), reward, done, nagari, status, committed, nullptr);
+      reinterpret_cast<u64*>(children), reward, done, nagari, status, committed, nullptr,
+      AutoReset{});
   return launched();
 }
 
@@ -702,8 +791,7 @@ int cugo_sample_uniform(const uint8_t* legal, int64_t n, uint64_t* sampler, int6
 int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
                     uint32_t* generation, uint64_t* sampler, unsigned long long* completed,
                     hipStream_t stream) {
-  if (n < 0 || (n > 0 && (!states || !done || !generation || !sampler || !completed)))
-    return kBadArgument;
+  if (n < 0 || (n > 0 && (!states || !done || !generation || !sampler))) return kBadArgument;
   if (n == 0) return 0;
   reset_kernel<<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<u64*>(states), done, n,
                                                base_seed, generation, sampler, completed);
@@ -725,8 +813,7 @@ int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint
                            unsigned long long* completed, const uint8_t* spares,
                            const uint32_t* spare_gen, hipStream_t stream) {
   if (n < 0 || seed_stride < 0 ||
-      (n > 0 && (!states || !done || !generation || !sampler || !completed || !spares ||
-                 !spare_gen)))
+      (n > 0 && (!states || !done || !generation || !sampler || !spares || !spare_gen)))
     return kBadArgument;
   if (n == 0) return 0;
   reset_spare_kernel<<<tiles(n), kTile, 0, stream>>>(

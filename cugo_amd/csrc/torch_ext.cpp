@@ -95,6 +95,25 @@ std::vector<torch::Tensor> observe(torch::Tensor states) {
   return o;
 }
 
+// observe plus sample_uniform's draw in one launch: (features, legal, player, done,
+// status, actions); sampler advances in place as sample_uniform advances it.
+std::vector<torch::Tensor> observe_sample(torch::Tensor states, torch::Tensor sampler) {
+  check_states(states);
+  const int64_t n = states.size(0);
+  check_1d(sampler, at::kLong, "sampler");
+  TORCH_CHECK(sampler.numel() == n, "sampler must have one entry per state row");
+  check_same_device(states, sampler, "states", "sampler");
+  const DeviceGuard guard(states.device());
+  auto o = observation_outputs(n, states);
+  o.push_back(torch::empty({n}, on(states, at::kLong)));
+  check_call(cugo_observe_sample(u8p(states), n, o[0].data_ptr<float>(), u8p(o[1]), u8p(o[2]),
+                                 u8p(o[3]), o[4].data_ptr<int16_t>(),
+                                 reinterpret_cast<uint64_t*>(sampler.data_ptr()),
+                                 o[5].data_ptr<int64_t>(), stream()),
+             "observe_sample");
+  return o;
+}
+
 std::vector<torch::Tensor> observe_indexed(torch::Tensor states, torch::Tensor ids) {
   check_states(states);
   check_1d(ids, at::kLong, "env_ids");
@@ -229,7 +248,16 @@ torch::Tensor stock_indexed(torch::Tensor states, torch::Tensor ids) {
 
 // Random-policy driver operations (not in the reference module; used by the
 // throughput harness).  sampler: uint64 [N] (int64 tensor), generation: int32 [N],
-// completed: int64 [1] counter.
+// completed: int64 [1] counter, or None (generation then counts finished games).
+unsigned long long* counter_ptr(const c10::optional<torch::Tensor>& completed,
+                                const torch::Tensor& states) {
+  if (!completed.has_value()) return nullptr;
+  check_1d(*completed, at::kLong, "completed");
+  TORCH_CHECK(completed->numel() >= 1, "completed must hold one counter");
+  check_same_device(states, *completed, "states", "completed");
+  return reinterpret_cast<unsigned long long*>(completed->data_ptr());
+}
+
 torch::Tensor sample_uniform(torch::Tensor legal, torch::Tensor sampler) {
   TORCH_CHECK(legal.is_cuda() && legal.is_contiguous() && legal.dim() == 2 &&
                   legal.size(1) == CUGO_ACTION_COUNT && legal.scalar_type() == at::kBool,
@@ -247,22 +275,20 @@ torch::Tensor sample_uniform(torch::Tensor legal, torch::Tensor sampler) {
 }
 
 void reset_done(torch::Tensor states, torch::Tensor done, int64_t base_seed,
-                torch::Tensor generation, torch::Tensor sampler, torch::Tensor completed) {
+                torch::Tensor generation, torch::Tensor sampler,
+                c10::optional<torch::Tensor> completed) {
   check_states(states);
   const int64_t n = states.size(0);
   check_1d(done, at::kBool, "done");
   check_1d(generation, at::kInt, "generation");
   check_1d(sampler, at::kLong, "sampler");
-  check_1d(completed, at::kLong, "completed");
   TORCH_CHECK(done.numel() == n && generation.numel() == n && sampler.numel() == n,
               "done, generation and sampler must have one entry per state row");
-  TORCH_CHECK(completed.numel() >= 1, "completed must hold one counter");
   const DeviceGuard guard(states.device());
   check_call(cugo_reset_done(u8p(states), u8p(done), n, static_cast<uint64_t>(base_seed),
                              reinterpret_cast<uint32_t*>(generation.data_ptr()),
                              reinterpret_cast<uint64_t*>(sampler.data_ptr()),
-                             reinterpret_cast<unsigned long long*>(completed.data_ptr()),
-                             stream()),
+                             counter_ptr(completed, states), stream()),
              "reset_done");
 }
 
@@ -283,29 +309,61 @@ void refill_spares(torch::Tensor spares, torch::Tensor spare_gen, torch::Tensor 
 }
 
 void reset_done_spares(torch::Tensor states, torch::Tensor done, int64_t base_seed,
-                       torch::Tensor generation, torch::Tensor sampler, torch::Tensor completed,
-                       torch::Tensor spares, torch::Tensor spare_gen, int64_t seed_stride) {
+                       torch::Tensor generation, torch::Tensor sampler,
+                       c10::optional<torch::Tensor> completed, torch::Tensor spares,
+                       torch::Tensor spare_gen, int64_t seed_stride) {
   check_states(states);
   check_states(spares);
   const int64_t n = states.size(0);
   check_1d(done, at::kBool, "done");
   check_1d(generation, at::kInt, "generation");
   check_1d(sampler, at::kLong, "sampler");
-  check_1d(completed, at::kLong, "completed");
   check_1d(spare_gen, at::kInt, "spare_gen");
   TORCH_CHECK(done.numel() == n && generation.numel() == n && sampler.numel() == n &&
                   spares.size(0) == n && spare_gen.numel() == n,
               "done, generation, sampler, spares and spare_gen must have one entry per row");
-  TORCH_CHECK(completed.numel() >= 1, "completed must hold one counter");
   const DeviceGuard guard(states.device());
   check_call(cugo_reset_done_spares(
                  u8p(states), u8p(done), n, static_cast<uint64_t>(base_seed),
                  seed_stride < 0 ? n : seed_stride,
                  reinterpret_cast<uint32_t*>(generation.data_ptr()),
                  reinterpret_cast<uint64_t*>(sampler.data_ptr()),
-                 reinterpret_cast<unsigned long long*>(completed.data_ptr()), u8p(spares),
+                 counter_ptr(completed, states), u8p(spares),
                  reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), stream()),
              "reset_done_spares");
+}
+
+// step then reset_done_spares (completed=None) in one launch; returns the step outputs.
+std::vector<torch::Tensor> step_reset_spares(torch::Tensor states, torch::Tensor actions,
+                                             int64_t base_seed, torch::Tensor generation,
+                                             torch::Tensor sampler, torch::Tensor spares,
+                                             torch::Tensor spare_gen, int64_t seed_stride) {
+  check_states(states);
+  check_states(spares);
+  const int64_t n = states.size(0);
+  check_1d(actions, at::kLong, "actions");
+  check_1d(generation, at::kInt, "generation");
+  check_1d(sampler, at::kLong, "sampler");
+  check_1d(spare_gen, at::kInt, "spare_gen");
+  TORCH_CHECK(actions.numel() == n && generation.numel() == n && sampler.numel() == n &&
+                  spares.size(0) == n && spare_gen.numel() == n,
+              "actions, generation, sampler, spares and spare_gen must have one entry per row");
+  check_same_device(states, actions, "states", "actions");
+  check_same_device(states, generation, "states", "generation");
+  check_same_device(states, sampler, "states", "sampler");
+  check_same_device(states, spares, "states", "spares");
+  check_same_device(states, spare_gen, "states", "spare_gen");
+  const DeviceGuard guard(states.device());
+  auto o = step_outputs(n, states);
+  check_call(cugo_step_reset_spares(
+                 u8p(states), actions.data_ptr<int64_t>(), n, o[0].data_ptr<float>(), u8p(o[1]),
+                 u8p(o[2]), o[3].data_ptr<int16_t>(), u8p(o[4]),
+                 static_cast<uint64_t>(base_seed), seed_stride < 0 ? n : seed_stride,
+                 reinterpret_cast<uint32_t*>(generation.data_ptr()),
+                 reinterpret_cast<uint64_t*>(sampler.data_ptr()), u8p(spares),
+                 reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), stream()),
+             "step_reset_spares");
+  return o;
 }
 
 torch::Tensor seed_samplers(int64_t n, int64_t base_seed, torch::Tensor generation) {
@@ -422,7 +480,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "step_indexed plus [N, EVENT_WORDS] int64 event records");
   m.def("start", &start, "[N, START_WORDS] int64 opening records");
   m.def("sample_uniform", &sample_uniform, "Uniform legal action per row (xorshift64)");
-  m.def("reset_done", &reset_done, "Re-create finished rows with their next seed");
+  m.def("observe_sample", &observe_sample,
+        "observe plus sample_uniform's draw: (features, legal, player, done, status, actions)");
+  m.def("reset_done", &reset_done, "Re-create finished rows with their next seed",
+        pybind11::arg("states"), pybind11::arg("done"), pybind11::arg("base_seed"),
+        pybind11::arg("generation"), pybind11::arg("sampler"),
+        pybind11::arg("completed") = pybind11::none());
   m.def("seed_samplers", &seed_samplers, "Per-row sampler state from the row seeds");
   m.def("refill_spares", &refill_spares, "Pre-deal the next game of rows with a stale spare",
         pybind11::arg("spares"), pybind11::arg("spare_gen"), pybind11::arg("generation"),
@@ -432,6 +495,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("states"), pybind11::arg("done"), pybind11::arg("base_seed"),
         pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("completed"),
         pybind11::arg("spares"), pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1);
+  m.def("step_reset_spares", &step_reset_spares,
+        "step, then reset_done_spares of the finished rows, in one launch",
+        pybind11::arg("states"), pybind11::arg("actions"), pybind11::arg("base_seed"),
+        pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("spares"),
+        pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1);
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
         pybind11::arg("rows") = pybind11::none());

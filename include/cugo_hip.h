@@ -103,10 +103,18 @@ int cugo_stock_indexed(const uint8_t* states, int64_t env_count, const int64_t* 
  *     -1 when the row has no legal action; sampler words advance in place.
  *   cugo_reset_done: every row with done[i] != 0 is re-created from
  *     seed = base_seed + i + batch * (++generation[i]) with first = i & 1, and its
- *     sampler re-seeded from the same seed; completed[0] += number of rows reset.
+ *     sampler re-seeded from the same seed; completed[0] += number of rows reset
+ *     (completed may be NULL: generation[] already counts each row's finished games,
+ *     and one same-address atomic per 64 rows costs more than the rest of the kernel).
+ *   cugo_observe_sample: cugo_observe plus cugo_sample_uniform's draw for every row,
+ *     taken from the legal mask while the kernel holds it (one launch, the mask is not
+ *     read back); outputs are those of the two calls.
  */
 int cugo_sample_uniform(const uint8_t* legal, int64_t n, uint64_t* sampler, int64_t* actions,
                         hipStream_t stream);
+int cugo_observe_sample(const uint8_t* states, int64_t n, float* features, uint8_t* legal,
+                        uint8_t* player, uint8_t* done, int16_t* status, uint64_t* sampler,
+                        int64_t* actions, hipStream_t stream);
 int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
                     uint32_t* generation, uint64_t* sampler, unsigned long long* completed,
                     hipStream_t stream);
@@ -125,6 +133,15 @@ int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint
                            int64_t seed_stride, uint32_t* generation, uint64_t* sampler,
                            unsigned long long* completed, const uint8_t* spares,
                            const uint32_t* spare_gen, hipStream_t stream);
+/* cugo_step followed by cugo_reset_done_spares(states, done, n, base_seed, seed_stride,
+ * generation, sampler, NULL, spares, spare_gen) in one launch: the outputs are the
+ * step's (done[i] = 1 for the game that just finished), and each finished row already
+ * holds its next game when the call returns. */
+int cugo_step_reset_spares(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
+                           uint8_t* done, uint8_t* nagari, int16_t* status, uint8_t* committed,
+                           uint64_t base_seed, int64_t seed_stride, uint32_t* generation,
+                           uint64_t* sampler, const uint8_t* spares, const uint32_t* spare_gen,
+                           hipStream_t stream);
 /* sampler[i] = SplitMix64(base_seed + i + batch * generation[i]).next(), never 0. */
 int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation,
                        uint64_t* sampler, hipStream_t stream);

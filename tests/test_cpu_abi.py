@@ -44,7 +44,9 @@ def test_extension_module_constants():
                 720, 179, 127, 127, 9, 8, 248, 0)
     for op in ("create", "observe", "observe_indexed", "step", "step_indexed", "clone_indexed",
                "branch_indexed", "hands_indexed", "stock_indexed", "step_events_indexed",
-               "start", "decode_attention", "decode_attention_append"):
+               "start", "decode_attention", "decode_attention_append", "sample_uniform",
+               "observe_sample", "reset_done", "reset_done_spares", "refill_spares",
+               "seed_samplers", "step_reset_spares"):
         assert callable(getattr(m, op))
 
 

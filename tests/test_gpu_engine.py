@@ -289,8 +289,9 @@ def test_driver_spare_reset_matches_reset(ext):
     spares = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
     spare_gen = torch.zeros(n, dtype=torch.int32, device=DEV)
     # c: the same batch as two slices on their own streams, seeds strided by the batch
+    # (no counter: completed=None; generation counts the finished games)
     c = a.clone()
-    gen_c, smp_c, done_c = gen_a.clone(), smp_a.clone(), done_a.clone()
+    gen_c, smp_c = gen_a.clone(), smp_a.clone()
     spares_c = torch.zeros_like(spares)
     spare_gen_c = torch.zeros_like(spare_gen)
     half = n // 2  # even
@@ -314,14 +315,86 @@ def test_driver_spare_reset_matches_reset(ext):
                 if step % 5 == 0:
                     ext.refill_spares(spares_c[r], spare_gen_c[r], gen_c[r], base + k * half, n)
                 _, cdone, _, _, _ = ext.step(c[r], actions[r])
-                ext.reset_done_spares(c[r], cdone, base + k * half, gen_c[r], smp_c[r], done_c,
+                ext.reset_done_spares(c[r], cdone, base + k * half, gen_c[r], smp_c[r], None,
                                       spares_c[r], spare_gen_c[r], n)
         for st in streams:
             cur.wait_stream(st)
         assert torch.equal(a, b) and torch.equal(a, c), step
         assert torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), step
         assert torch.equal(gen_a, gen_c) and torch.equal(smp_a, smp_c), step
-    assert int(done_a.item()) == int(done_b.item()) == int(done_c.item()) > n
+    assert int(done_a.item()) == int(done_b.item()) == int(gen_c.sum().item()) > n
+
+
+def test_step_reset_spares_matches_step_then_reset(ext):
+    """step_reset_spares == step followed by reset_done_spares (no counter): the same step
+    outputs, states, generations and samplers, with spares refilled every few steps so
+    that both the spare copy and the inline deal occur; also as two strided slices."""
+    announce("step_reset_spares")
+    n = 2500  # a partial last tile
+    base = 0x3141592
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    a = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(np.arange(n) & 1).to(DEV))
+    gen_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp_a = ext.seed_samplers(n, base, gen_a)
+    spares_a = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
+    sg_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    b, gen_b, smp_b, spares_b, sg_b = (t.clone() for t in (a, gen_a, smp_a, spares_a, sg_a))
+    c, gen_c, smp_c, spares_c, sg_c = (t.clone() for t in (a, gen_a, smp_a, spares_a, sg_a))
+    half = n // 2  # even
+    for step in range(60):
+        if step % 4 == 0:
+            ext.refill_spares(spares_a, sg_a, gen_a, base)
+            ext.refill_spares(spares_b, sg_b, gen_b, base)
+        if step % 6 == 0:  # slice 1 never gets spares: its rows are all dealt inline
+            ext.refill_spares(spares_c[:half], sg_c[:half], gen_c[:half], base, n)
+        _, _, _, _, _, actions = ext.observe_sample(a, smp_a)
+        smp_b.copy_(smp_a)
+        smp_c.copy_(smp_a)
+        out_a = ext.step(a, actions)
+        ext.reset_done_spares(a, out_a[1], base, gen_a, smp_a, None, spares_a, sg_a)
+        out_b = ext.step_reset_spares(b, actions, base, gen_b, smp_b, spares_b, sg_b)
+        parts = []
+        for k in range(2):
+            r = slice(k * half, (k + 1) * half)
+            parts.append(ext.step_reset_spares(c[r], actions[r], base + k * half, gen_c[r],
+                                               smp_c[r], spares_c[r], sg_c[r], n))
+        for j in range(5):
+            assert torch.equal(out_a[j], out_b[j]), (step, j)
+            assert torch.equal(out_a[j], torch.cat([parts[0][j], parts[1][j]])), (step, j)
+        assert torch.equal(a, b) and torch.equal(a, c), step
+        assert torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), step
+        assert torch.equal(gen_a, gen_c) and torch.equal(smp_a, smp_c), step
+    assert int(gen_a.sum().item()) > n
+
+
+def test_observe_sample_matches_observe_then_sample(ext):
+    """observe_sample == observe followed by sample_uniform: the same five observation
+    outputs, actions and sampler words, over a random-policy run with resets (so rows
+    at every stage of a game, finished rows with an empty mask included)."""
+    announce("observe_sample")
+    n = 4100  # a partial last tile
+    base = 0x5A5A5A5
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    states = ext.create(torch.from_numpy(seeds).to(DEV),
+                        torch.from_numpy(np.arange(n) & 1).to(DEV))
+    gen = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp_a = ext.seed_samplers(n, base, gen)
+    smp_b = smp_a.clone()
+    empty = 0
+    for step in range(40):
+        obs = ext.observe(states)
+        actions = ext.sample_uniform(obs[1], smp_a)
+        fused = ext.observe_sample(states, smp_b)
+        for k in range(5):
+            assert torch.equal(obs[k], fused[k]), (step, k)
+        assert torch.equal(actions, fused[5]) and torch.equal(smp_a, smp_b), step
+        empty += int((actions < 0).sum().item())
+        _, done, _, _, _ = ext.step(states, actions)
+        if step % 7 == 6:  # leave finished rows in place for a few steps first
+            ext.reset_done(states, done, base, gen, smp_a)
+            smp_b.copy_(smp_a)
+    assert empty > 0 and int(gen.sum().item()) > 0
+    assert ext.observe_sample(states[:0], smp_a[:0])[5].numel() == 0
 
 
 def test_repeatable(ext):
