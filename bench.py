@@ -63,7 +63,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-rollout", action="store_true")
-    p.add_argument("--streams", type=int, default=4,
+    p.add_argument("--streams", type=int, default=1,
                    help="slices of the batch stepped on their own streams")
     p.add_argument("--no-graph", action="store_true", help="issue the loop eagerly")
     p.add_argument("--copy-probe", action="store_true",

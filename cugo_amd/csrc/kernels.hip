@@ -311,6 +311,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
   stage_in<kStepThreads>(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
   __syncthreads();
   bool take_spare = false;
+  u32 gen0 = 0, spare0 = 0;  // kMode 3: issued before the step so their latency hides
+  if (kMode == 3 && lane < count) {
+    gen0 = ar.generation[base + lane];
+    spare0 = ar.spare_gen[base + lane];
+  }
   if (lane < count) {
     const i64 i = base + lane;
     const bool ok = !kIndexed || valid_id(tile_ids[lane], env_count);
@@ -338,11 +343,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
       status[i] = (i16)so.status;
       committed[i] = so.committed;
       if (kMode == 3 && so.done) {
-        const u32 gen = ar.generation[i] + 1u;
+        const u32 gen = gen0 + 1u;
         ar.generation[i] = gen;
         const u64 seed = ar.base_seed + (u64)i + ar.stride * gen;
         ar.sampler[i] = sampler_seed(seed);
-        take_spare = ar.spare_gen[i] == gen;
+        take_spare = spare0 == gen;
         if (!take_spare) pack_row(create_env(seed, (u32)(i & 1)), row);
       }
     } else {  // torch50_ext.cu:108-118
