@@ -1,0 +1,334 @@
+// Token embeddings and action sampling of the event-sequence policy's self-play step,
+// for gfx950.
+//
+// Reference: python/cugo_seq50.py (encode_events :91-110, encode_start :113-128,
+// SeqNet.start_token :271-274, SeqNet.event_token :276-282) and the sampling lines of
+// WaveCollector._step (python/cugo_seq_selfplay50.py:125-130).
+//
+// An event or opening token is a 0/1 vector (card planes, a one-hot kind or mission
+// type) plus a few small scalars, and the first thing the policy does with it is a
+// Linear layer.  Instead of materialising the [n, 414] or [n, 274] token and running a
+// GEMM, each row sums the weight columns of its set bits (weights stored transposed,
+// one contiguous d-element row per input feature, so a column read is coalesced), then
+// adds the bias, the position row and the token-type row with the same roundings as
+// the reference's bf16 ops:
+//   r1 = round(bias + sum_j token_j * W[:, j])      (nn.Linear, fp32 accumulation)
+//   r2 = round(r1 + position[p])                     (bf16 add)
+//   out = round(r2 + token_type[t])                  (bf16 add)
+// One 64-lane wavefront per row; the row's words are wave-uniform, so the walk over its
+// set bits is scalar and every lane owns columns lane, lane + 64, ... of the output.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "../../include/cugo_hip.h"
+
+namespace cugo_amd {
+namespace tokens {
+
+typedef int64_t i64;
+typedef uint64_t u64;
+
+constexpr u64 kCardMask = (1ull << 50) - 1ull;
+constexpr int kEventIn = 8 * 50 + 12 + 2;      // EVENT_IN, cugo_seq50.py:40
+constexpr int kStartIn = 5 * 50 + 12 + 8 + 4;  // START_IN, cugo_seq50.py:41
+constexpr int kKinds = 12;                     // KINDS, cugo_seq50.py:38
+constexpr int kMaxEvents = 48;                 // MAX_EVENTS, cugo_seq50.py:37
+constexpr int kRowsPerBlock = 4;
+
+struct BF16 {
+  using storage = uint16_t;
+  __device__ static float to_float(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+  // Round to nearest even; NaN stays a quiet NaN (the conversion torch uses).
+  __device__ static uint16_t from_float(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  }
+  __device__ static float round(float f) { return to_float(from_float(f)); }
+};
+
+struct F32 {
+  using storage = float;
+  __device__ static float to_float(float x) { return x; }
+  __device__ static float from_float(float f) { return f; }
+  __device__ static float round(float f) { return f; }
+};
+
+__device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// acc[k] += W[row j] at this lane's columns, for every set bit j of `bits` (offset `base`).
+template <class T, int K>
+__device__ inline void add_bits(float (&acc)[K], u64 bits, int base,
+                                const typename T::storage* wt, int d, int lane) {
+  while (bits != 0) {
+    const int j = base + __builtin_ctzll(bits);
+    bits &= bits - 1ull;
+    const typename T::storage* w = wt + (i64)j * d + lane;
+#pragma unroll
+    for (int k = 0; k < K; ++k) acc[k] += T::to_float(w[64 * k]);
+  }
+}
+
+template <class T, int K>
+__device__ inline void add_scaled(float (&acc)[K], float x, int j,
+                                  const typename T::storage* wt, int d, int lane) {
+  const typename T::storage* w = wt + (i64)j * d + lane;
+#pragma unroll
+  for (int k = 0; k < K; ++k) acc[k] += x * T::to_float(w[64 * k]);
+}
+
+template <class T, int K>
+__device__ inline void finish(float (&acc)[K], const typename T::storage* position,
+                              const typename T::storage* token_type,
+                              typename T::storage* out, int d, int lane) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = lane + 64 * k;
+    const float r1 = T::round(acc[k]);
+    const float r2 = T::round(r1 + T::to_float(position[c]));
+    out[c] = T::from_float(r2 + T::to_float(token_type[c]));
+  }
+}
+
+// SeqNet.event_token(words, seat, index) (cugo_seq50.py:276-282) with encode_events
+// (:91-110) on one event per row: slots played, own drawn (hidden unless the observer
+// is the actor), flipped, my/opponent gain, my/opponent loss (seat 0 reads players 0/1
+// as my/opponent, seat 1 the other way round), shown; then one-hot kind (clamped to 11),
+// the "me" bit and the opponent's hidden draw count; position row 1 + min(index, 47).
+template <class T, int K>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void event_tokens_kernel(
+    const i64* words, const i64* seat, const i64* index, i64 n,
+    const typename T::storage* wt, const typename T::storage* bias,
+    const typename T::storage* position, i64 position_rows,
+    const typename T::storage* token_type, int d, typename T::storage* out) {
+  const int lane = threadIdx.x & 63;
+  const i64 r = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
+  if (r >= n) return;
+  const i64* ev = words + r * 9;
+  const u64 header = (u64)ev[8];
+  const i64 s = seat[r];
+  const bool me = (i64)(header & 0xFFu) == s;
+  const bool first = s == 0;
+  const int kind = (int)((header >> 8) & 0xFFu);
+  float acc[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) acc[k] = T::to_float(bias[lane + 64 * k]);
+  const u64 w3 = (u64)ev[3], w4 = (u64)ev[4], w5 = (u64)ev[5], w6 = (u64)ev[6];
+  add_bits<T>(acc, (u64)ev[0] & kCardMask, 0, wt, d, lane);
+  if (me) add_bits<T>(acc, (u64)ev[1] & kCardMask, 50, wt, d, lane);
+  add_bits<T>(acc, (u64)ev[2] & kCardMask, 100, wt, d, lane);
+  add_bits<T>(acc, (first ? w3 : w4) & kCardMask, 150, wt, d, lane);
+  add_bits<T>(acc, (first ? w4 : w3) & kCardMask, 200, wt, d, lane);
+  add_bits<T>(acc, (first ? w5 : w6) & kCardMask, 250, wt, d, lane);
+  add_bits<T>(acc, (first ? w6 : w5) & kCardMask, 300, wt, d, lane);
+  add_bits<T>(acc, (u64)ev[7] & kCardMask, 350, wt, d, lane);
+  add_bits<T>(acc, 1ull, 400 + (kind < kKinds - 1 ? kind : kKinds - 1), wt, d, lane);
+  if (me) {
+    add_bits<T>(acc, 1ull, 412, wt, d, lane);
+  } else {
+    const int drawn = __builtin_popcountll((u64)ev[1] & kCardMask);
+    if (drawn != 0) add_scaled<T>(acc, (float)drawn, 413, wt, d, lane);
+  }
+  i64 p = index[r];
+  p = 1 + (p < kMaxEvents - 1 ? p : kMaxEvents - 1);
+  if (p < 0) p = 0;
+  if (p >= position_rows) p = position_rows - 1;
+  finish<T>(acc, position + p * d, token_type + d, out + r * d, d, lane);
+}
+
+// SeqNet.start_token(start, seat) (cugo_seq50.py:271-274) with encode_start (:113-128):
+// planes of the observer's hand, the floor, own and opponent captures and the mission
+// cards, the 12 neutral-month bits, one-hot mission type (clamped to 7), then four
+// scalars (multiplier / 4, observer moves first, own and opponent mission months / 8),
+// rounded to the token dtype as the reference's `.to(dtype)` does; position row 0.
+template <class T, int K>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void start_tokens_kernel(
+    const i64* start, const i64* seat, i64 n, const typename T::storage* wt,
+    const typename T::storage* bias, const typename T::storage* position,
+    const typename T::storage* token_type, int d, typename T::storage* out) {
+  const int lane = threadIdx.x & 63;
+  const i64 r = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
+  if (r >= n) return;
+  const i64* st = start + r * 8;
+  const i64 s = seat[r];
+  const bool first = s == 0;
+  const u64 header = (u64)st[7];
+  float acc[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) acc[k] = T::to_float(bias[lane + 64 * k]);
+  const u64 s0 = (u64)st[0], s1 = (u64)st[1], s3 = (u64)st[3], s4 = (u64)st[4];
+  add_bits<T>(acc, (first ? s0 : s1) & kCardMask, 0, wt, d, lane);
+  add_bits<T>(acc, (u64)st[2] & kCardMask, 50, wt, d, lane);
+  add_bits<T>(acc, (first ? s3 : s4) & kCardMask, 100, wt, d, lane);
+  add_bits<T>(acc, (first ? s4 : s3) & kCardMask, 150, wt, d, lane);
+  add_bits<T>(acc, (u64)st[5] & kCardMask, 200, wt, d, lane);
+  add_bits<T>(acc, (u64)st[6] & 0xFFFull, 250, wt, d, lane);
+  const int mtype = (int)(header & 0xFFu);
+  add_bits<T>(acc, 1ull, 262 + (mtype < 7 ? mtype : 7), wt, d, lane);
+  const float m0 = (float)((header >> 24) & 0xFFu) / 8.0f;
+  const float m1 = (float)((header >> 32) & 0xFFu) / 8.0f;
+  const float scalars[4] = {(float)((header >> 8) & 0xFFu) / 4.0f,
+                            (i64)((header >> 16) & 1u) == s ? 1.0f : 0.0f,
+                            first ? m0 : m1, first ? m1 : m0};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float x = T::round(scalars[q]);
+    if (x != 0.0f) add_scaled<T>(acc, x, 270 + q, wt, d, lane);
+  }
+  finish<T>(acc, position, token_type, out + r * d, d, lane);
+}
+
+// WaveCollector._step's sampling (cugo_seq_selfplay50.py:125-130) for one row per
+// wavefront: masked = legal ? logit : -1e30; action = argmax(masked - log(-log(clamp(u,
+// 1e-20, 1)))) with the first index on ties (torch.argmax); logp = log_softmax(masked)
+// at the action, computed as (masked[a] - max) - log(sum exp(masked - max)).
+__global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
+    const float* logits, const uint8_t* legal, const float* u, i64 n, int actions_count,
+    i64* actions, float* logp) {
+  const int lane = threadIdx.x & 63;
+  const i64 r = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
+  if (r >= n) return;
+  const float* lr = logits + r * actions_count;
+  const uint8_t* gr = legal + r * actions_count;
+  const float* ur = u + r * actions_count;
+  float best = -INFINITY, top = -INFINITY;
+  int best_a = actions_count;  // above every real index
+  for (int a = lane; a < actions_count; a += 64) {
+    const float m = gr[a] ? lr[a] : -1.0e30f;
+    const float uc = fminf(fmaxf(ur[a], 1.0e-20f), 1.0f);
+    const float v = m + -logf(-logf(uc));
+    if (v > best) { best = v; best_a = a; }
+    top = fmaxf(top, m);
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ob = __shfl_xor(best, off);
+    const int oa = __shfl_xor(best_a, off);
+    if (ob > best || (ob == best && oa < best_a)) { best = ob; best_a = oa; }
+    top = fmaxf(top, __shfl_xor(top, off));
+  }
+  float sum = 0.0f;
+  for (int a = lane; a < actions_count; a += 64) {
+    const float m = gr[a] ? lr[a] : -1.0e30f;
+    sum += expf(m - top);
+  }
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if (lane == 0) {
+    const int a = best_a < actions_count ? best_a : 0;
+    const float m = gr[a] ? lr[a] : -1.0e30f;
+    actions[r] = a;
+    logp[r] = (m - top) - logf(sum);
+  }
+}
+
+template <class T>
+int launch_event(const i64* words, const i64* seat, const i64* index, i64 n, const void* wt,
+                 const void* bias, const void* position, i64 position_rows,
+                 const void* token_type, int d, void* out, hipStream_t stream) {
+  using S = typename T::storage;
+  const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
+#define CUGO_EVENT_CASE(KK)                                                                 \
+  case KK:                                                                                  \
+    event_tokens_kernel<T, KK><<<grid, 64 * kRowsPerBlock, 0, stream>>>(                    \
+        words, seat, index, n, (const S*)wt, (const S*)bias, (const S*)position,            \
+        position_rows, (const S*)token_type, d, (S*)out);                                   \
+    break;
+  switch (d / 64) {
+    CUGO_EVENT_CASE(1)
+    CUGO_EVENT_CASE(2)
+    CUGO_EVENT_CASE(4)
+    CUGO_EVENT_CASE(8)
+    CUGO_EVENT_CASE(16)
+    default:
+      return -3;
+  }
+#undef CUGO_EVENT_CASE
+  return (int)hipGetLastError();
+}
+
+template <class T>
+int launch_start(const i64* start, const i64* seat, i64 n, const void* wt, const void* bias,
+                 const void* position, const void* token_type, int d, void* out,
+                 hipStream_t stream) {
+  using S = typename T::storage;
+  const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
+#define CUGO_START_CASE(KK)                                                                 \
+  case KK:                                                                                  \
+    start_tokens_kernel<T, KK><<<grid, 64 * kRowsPerBlock, 0, stream>>>(                    \
+        start, seat, n, (const S*)wt, (const S*)bias, (const S*)position,                   \
+        (const S*)token_type, d, (S*)out);                                                  \
+    break;
+  switch (d / 64) {
+    CUGO_START_CASE(1)
+    CUGO_START_CASE(2)
+    CUGO_START_CASE(4)
+    CUGO_START_CASE(8)
+    CUGO_START_CASE(16)
+    default:
+      return -3;
+  }
+#undef CUGO_START_CASE
+  return (int)hipGetLastError();
+}
+
+bool valid_width(int64_t d) {
+  return d == 64 || d == 128 || d == 256 || d == 512 || d == 1024;
+}
+
+}  // namespace tokens
+}  // namespace cugo_amd
+
+using namespace cugo_amd::tokens;
+
+extern "C" {
+
+int cugo_event_tokens(int dtype, const int64_t* words, const int64_t* seat,
+                      const int64_t* index, int64_t n, const void* weight_t, const void* bias,
+                      const void* position, int64_t position_rows, const void* token_type,
+                      int64_t d, void* out, hipStream_t stream) {
+  if (n < 0 || position_rows < 1 ||
+      (n > 0 && (!words || !seat || !index || !weight_t || !bias || !position ||
+                 !token_type || !out)))
+    return -1;
+  if (!valid_width(d)) return -3;
+  if (n == 0) return 0;
+  if (dtype == CUGO_DTYPE_BF16)
+    return launch_event<BF16>(words, seat, index, n, weight_t, bias, position, position_rows,
+                              token_type, (int)d, out, stream);
+  if (dtype == CUGO_DTYPE_F32)
+    return launch_event<F32>(words, seat, index, n, weight_t, bias, position, position_rows,
+                             token_type, (int)d, out, stream);
+  return -2;
+}
+
+int cugo_start_tokens(int dtype, const int64_t* start, const int64_t* seat, int64_t n,
+                      const void* weight_t, const void* bias, const void* position,
+                      const void* token_type, int64_t d, void* out, hipStream_t stream) {
+  if (n < 0 ||
+      (n > 0 && (!start || !seat || !weight_t || !bias || !position || !token_type || !out)))
+    return -1;
+  if (!valid_width(d)) return -3;
+  if (n == 0) return 0;
+  if (dtype == CUGO_DTYPE_BF16)
+    return launch_start<BF16>(start, seat, n, weight_t, bias, position, token_type, (int)d,
+                              out, stream);
+  if (dtype == CUGO_DTYPE_F32)
+    return launch_start<F32>(start, seat, n, weight_t, bias, position, token_type, (int)d,
+                             out, stream);
+  return -2;
+}
+
+int cugo_gumbel_sample(const float* logits, const uint8_t* legal, const float* uniforms,
+                       int64_t n, int64_t actions_count, int64_t* actions, float* logp,
+                       hipStream_t stream) {
+  if (n < 0 || actions_count < 1 || actions_count > (1 << 20) ||
+      (n > 0 && (!logits || !legal || !uniforms || !actions || !logp)))
+    return -1;
+  if (n == 0) return 0;
+  const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
+  gumbel_kernel<<<grid, 64 * kRowsPerBlock, 0, stream>>>(logits, legal, uniforms, n,
+                                                         (int)actions_count, actions, logp);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

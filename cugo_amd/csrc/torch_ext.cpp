@@ -465,6 +465,113 @@ torch::Tensor decode_attention_append(torch::Tensor q, torch::Tensor k_new, torc
 
 }  // namespace
 
+// ---------------------------------------------------------------- seq self-play ----
+void check_token_weights(const torch::Tensor& weight_t, const torch::Tensor& bias,
+                         const torch::Tensor& position, const torch::Tensor& token_type,
+                         int64_t in_features, const torch::Tensor& like) {
+  TORCH_CHECK(weight_t.is_cuda() && weight_t.is_contiguous() && weight_t.dim() == 2 &&
+                  weight_t.size(0) == in_features,
+              "weight_t must be a contiguous CUDA tensor [", in_features, ", d]");
+  const int64_t d = weight_t.size(1);
+  const auto t = weight_t.scalar_type();
+  TORCH_CHECK(t == at::kBFloat16 || t == at::kFloat, "token weights must be bfloat16 or float32");
+  TORCH_CHECK(bias.scalar_type() == t && position.scalar_type() == t &&
+                  token_type.scalar_type() == t,
+              "bias, position and token_type must have weight_t's dtype");
+  TORCH_CHECK(bias.is_contiguous() && bias.numel() == d, "bias must be contiguous [d]");
+  TORCH_CHECK(position.is_contiguous() && position.dim() == 2 && position.size(1) == d,
+              "position must be contiguous [rows, d]");
+  TORCH_CHECK(token_type.is_contiguous() && token_type.dim() == 2 && token_type.size(0) == 3 &&
+                  token_type.size(1) == d,
+              "token_type must be contiguous [3, d]");
+  TORCH_CHECK(d == 64 || d == 128 || d == 256 || d == 512 || d == 1024,
+              "d must be 64, 128, 256, 512 or 1024");
+  check_same_device(like, weight_t, "words", "weight_t");
+  check_same_device(like, bias, "words", "bias");
+  check_same_device(like, position, "words", "position");
+  check_same_device(like, token_type, "words", "token_type");
+}
+
+int token_dtype(const torch::Tensor& w) {
+  return w.scalar_type() == at::kBFloat16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32;
+}
+
+// event_tokens(words [n, 9], seat [n], index [n], weight_t [414, d], bias, position,
+// token_type) -> [n, d]: SeqNet.event_token (python/cugo_seq50.py:276-282).
+torch::Tensor event_tokens(torch::Tensor words, torch::Tensor seat, torch::Tensor index,
+                           torch::Tensor weight_t, torch::Tensor bias, torch::Tensor position,
+                           torch::Tensor token_type) {
+  TORCH_CHECK(words.is_cuda() && words.is_contiguous() && words.dim() == 2 &&
+                  words.size(1) == CUGO_EVENT_WORDS && words.scalar_type() == at::kLong,
+              "words must be a contiguous CUDA int64 [n, EVENT_WORDS] tensor");
+  const int64_t n = words.size(0);
+  check_1d(seat, at::kLong, "seat");
+  check_1d(index, at::kLong, "index");
+  TORCH_CHECK(seat.numel() == n && index.numel() == n, "seat and index must have n entries");
+  check_same_device(words, seat, "words", "seat");
+  check_same_device(words, index, "words", "index");
+  check_token_weights(weight_t, bias, position, token_type, 8 * 50 + 12 + 2, words);
+  const DeviceGuard guard(words.device());
+  auto out = torch::empty({n, weight_t.size(1)}, on(words, weight_t.scalar_type()));
+  check_call(cugo_event_tokens(token_dtype(weight_t), words.data_ptr<int64_t>(),
+                               seat.data_ptr<int64_t>(), index.data_ptr<int64_t>(), n,
+                               weight_t.data_ptr(), bias.data_ptr(), position.data_ptr(),
+                               position.size(0), token_type.data_ptr(), weight_t.size(1),
+                               out.data_ptr(), stream()),
+             "event_tokens");
+  return out;
+}
+
+// start_tokens(start [n, 8], seat [n], weight_t [274, d], bias, position, token_type)
+// -> [n, d]: SeqNet.start_token (python/cugo_seq50.py:271-274).
+torch::Tensor start_tokens(torch::Tensor start, torch::Tensor seat, torch::Tensor weight_t,
+                           torch::Tensor bias, torch::Tensor position,
+                           torch::Tensor token_type) {
+  TORCH_CHECK(start.is_cuda() && start.is_contiguous() && start.dim() == 2 &&
+                  start.size(1) == CUGO_START_WORDS && start.scalar_type() == at::kLong,
+              "start must be a contiguous CUDA int64 [n, START_WORDS] tensor");
+  const int64_t n = start.size(0);
+  check_1d(seat, at::kLong, "seat");
+  TORCH_CHECK(seat.numel() == n, "seat must have n entries");
+  check_same_device(start, seat, "start", "seat");
+  check_token_weights(weight_t, bias, position, token_type, 5 * 50 + 12 + 8 + 4, start);
+  const DeviceGuard guard(start.device());
+  auto out = torch::empty({n, weight_t.size(1)}, on(start, weight_t.scalar_type()));
+  check_call(cugo_start_tokens(token_dtype(weight_t), start.data_ptr<int64_t>(),
+                               seat.data_ptr<int64_t>(), n, weight_t.data_ptr(),
+                               bias.data_ptr(), position.data_ptr(), token_type.data_ptr(),
+                               weight_t.size(1), out.data_ptr(), stream()),
+             "start_tokens");
+  return out;
+}
+
+// gumbel_sample(logits f32 [n, A], legal bool [n, A], uniforms f32 [n, A]) -> (actions
+// int64 [n], logp f32 [n]): the sampling of WaveCollector._step
+// (python/cugo_seq_selfplay50.py:125-130) with the uniforms supplied.
+std::vector<torch::Tensor> gumbel_sample(torch::Tensor logits, torch::Tensor legal,
+                                         torch::Tensor uniforms) {
+  TORCH_CHECK(logits.is_cuda() && logits.is_contiguous() && logits.dim() == 2 &&
+                  logits.scalar_type() == at::kFloat,
+              "logits must be a contiguous CUDA float32 [n, A] tensor");
+  TORCH_CHECK(legal.is_contiguous() && legal.sizes() == logits.sizes() &&
+                  legal.scalar_type() == at::kBool,
+              "legal must be a contiguous bool tensor shaped like logits");
+  TORCH_CHECK(uniforms.is_contiguous() && uniforms.sizes() == logits.sizes() &&
+                  uniforms.scalar_type() == at::kFloat,
+              "uniforms must be a contiguous float32 tensor shaped like logits");
+  check_same_device(logits, legal, "logits", "legal");
+  check_same_device(logits, uniforms, "logits", "uniforms");
+  const DeviceGuard guard(logits.device());
+  const int64_t n = logits.size(0);
+  auto actions = torch::empty({n}, on(logits, at::kLong));
+  auto logp = torch::empty({n}, on(logits, at::kFloat));
+  check_call(cugo_gumbel_sample(logits.data_ptr<float>(), u8p(legal), uniforms.data_ptr<float>(),
+                                n, logits.size(1), actions.data_ptr<int64_t>(),
+                                logp.data_ptr<float>(), stream()),
+             "gumbel_sample");
+  return {actions, logp};
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Cugo Shin Matgo batch environment on gfx950 (HIP)";
   m.def("create", &create, "Create a GPU-resident batch of 248-byte game rows");
@@ -500,6 +607,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("states"), pybind11::arg("actions"), pybind11::arg("base_seed"),
         pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("spares"),
         pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1);
+  m.def("event_tokens", &event_tokens, "SeqNet.event_token: event_in(encode_events) + position + type");
+  m.def("start_tokens", &start_tokens, "SeqNet.start_token: start_in(encode_start) + position + type");
+  m.def("gumbel_sample", &gumbel_sample, "Masked Gumbel-max action and its log-softmax probability");
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
         pybind11::arg("rows") = pybind11::none());

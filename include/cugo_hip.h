@@ -186,6 +186,36 @@ int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, const
                                  int64_t heads, int64_t dh, int64_t slots, int64_t cache_rows,
                                  float scale, void* out, hipStream_t stream);
 
+/*
+ * Event-sequence policy self-play (python/cugo_seq50.py, python/cugo_seq_selfplay50.py).
+ * dtype: CUGO_DTYPE_BF16 or CUGO_DTYPE_F32 for every weight and the output; d in
+ * {64, 128, 256, 512, 1024}.  weight_t is the Linear weight transposed ([in, d],
+ * contiguous), bias [d], position [position_rows, d], token_type [3, d].
+ *
+ * cugo_event_tokens: out[i] = SeqNet.event_token(words[i], seat[i], index[i])
+ *   (cugo_seq50.py:276-282 with encode_events :91-110): event_in applied to the 414-wide
+ *   observer-relative token of the 9-word event, + position[1 + min(index, 47)] +
+ *   token_type[1], with the reference's bf16 roundings (after the Linear, after each add).
+ *   words int64 [n, 9], seat/index int64 [n], weight_t [414, d], out [n, d].
+ */
+int cugo_event_tokens(int dtype, const int64_t* words, const int64_t* seat,
+                      const int64_t* index, int64_t n, const void* weight_t, const void* bias,
+                      const void* position, int64_t position_rows, const void* token_type,
+                      int64_t d, void* out, hipStream_t stream);
+/* cugo_start_tokens: out[i] = SeqNet.start_token(start[i], seat[i]) (cugo_seq50.py:271-274
+ * with encode_start :113-128): start_in of the 274-wide opening token + position[0] +
+ * token_type[0].  start int64 [n, 8], seat int64 [n], weight_t [274, d], out [n, d]. */
+int cugo_start_tokens(int dtype, const int64_t* start, const int64_t* seat, int64_t n,
+                      const void* weight_t, const void* bias, const void* position,
+                      const void* token_type, int64_t d, void* out, hipStream_t stream);
+/* cugo_gumbel_sample: the sampling of WaveCollector._step (cugo_seq_selfplay50.py:125-130)
+ * given the uniforms torch.rand_like drew: masked = legal ? logits : -1e30;
+ * actions[i] = argmax_a(masked - log(-log(clamp(u, 1e-20, 1)))) (first index on ties);
+ * logp[i] = log_softmax(masked)[actions[i]].  logits/uniforms f32 [n, A], legal bool [n, A]. */
+int cugo_gumbel_sample(const float* logits, const uint8_t* legal, const float* uniforms,
+                       int64_t n, int64_t actions_count, int64_t* actions, float* logp,
+                       hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -97,3 +97,16 @@ def test_drop_in_modules_import_under_reference_names():
                          capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stderr
     assert "raised" in out.stdout and "GPU" in out.stdout
+
+
+def test_policy_state_dict_names():
+    """SeqPolicy carries the parameter names of a reference SeqNet(hybrid) checkpoint
+    (python/cugo_seq50.py:150-167)."""
+    from cugo_amd.seq_selfplay import SeqPolicy
+
+    names = set(SeqPolicy().state_dict())
+    for key in ("event_in.weight", "start_in.bias", "query_in.0.weight", "query_in.2.bias",
+                "position", "token_type", "encoder.layers.3.self_attn.in_proj_weight",
+                "encoder.layers.0.linear2.bias", "norm.weight", "head.2.weight"):
+        assert key in names, key
+    assert SeqPolicy().query_in[0].in_features == 720 + 179

@@ -1,0 +1,310 @@
+"""GPU parity of the sequence-policy self-play step.
+
+Event/opening token kernels against the oracle's token vectors (oracle/seq_ref.py,
+pinned in tests/test_cpu_seq_oracle.py) times the Linear in float64 with the reference's
+bf16 roundings; the Gumbel-max kernel against the reference's torch lines on the same
+uniforms; the HIP-graph self-play step against the reference formulation of the step
+(dense tokens, index_put_ + matmul attention), both driven with the same uniforms.
+Tolerances: bf16 outputs within 1e-2 relative (Frobenius) with at least 98 % of the
+elements bit-identical (a different fp32 summation order can move a bf16 rounding by one
+unit); fp32 token outputs within 1e-5 absolute; sampled actions identical.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.seq_ref import (encode_events_np, encode_start_np, gumbel_reference,
+                            reference_cached_step, token_reference)
+from tests.conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def rel_err(got: torch.Tensor, want: torch.Tensor) -> float:
+    got, want = got.double(), want.double()
+    return float((got - want).norm() / want.norm().clamp_min(1e-30))
+
+
+def random_events(ext, games: int, seed: int, steps: int = 40):
+    """Committed event words (and the counts before them) of seeded random-policy games."""
+    idx = torch.arange(games, dtype=torch.int64, device=DEV)
+    states = ext.create(idx * 7919 + seed, idx & 1)
+    gen = torch.zeros(games, dtype=torch.int32, device=DEV)
+    sampler = ext.seed_samplers(games, seed, gen)
+    words, counts = [], []
+    count = torch.zeros(games, dtype=torch.int64, device=DEV)
+    for _ in range(steps):
+        _, legal, _, done, _ = ext.observe(states)
+        actions = ext.sample_uniform(legal, sampler)
+        out = ext.step_events_indexed(states, idx, actions)
+        keep = out[4] & ~done
+        words.append(out[5][keep])
+        counts.append(count[keep])
+        count += keep.long()
+    return torch.cat(words), torch.cat(counts)
+
+
+def edge_events() -> torch.Tensor:
+    def m(*c):
+        return sum(1 << x for x in c)
+    rows = [
+        [m(49) | (1 << 50), m(0, 1), m(2), m(3), m(4), m(5), m(6), m(7), 0 | (200 << 8)],
+        [m(10), m(11, 12, 13), 0, 0, 0, 0, 0, 0, 1 | (3 << 8)],
+        [0, 0, 0, 0, 0, 0, 0, 0, 0],
+        [(1 << 64) - 1] * 8 + [1 | (11 << 8)],
+    ]
+    signed = [[w - (1 << 64) if w >= (1 << 63) else w for w in r] for r in rows]
+    return torch.tensor(signed, dtype=torch.int64, device=DEV)
+
+
+def make_weights(in_features: int, d: int, dtype, seed: int):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    w = (torch.randn(d, in_features, generator=g) * 0.05).to(dtype).to(DEV)
+    b = (torch.randn(d, generator=g) * 0.05).to(dtype).to(DEV)
+    pos = (torch.randn(49, d, generator=g) * 0.05).to(dtype).to(DEV)
+    tt = (torch.randn(3, d, generator=g) * 0.05).to(dtype).to(DEV)
+    return w, b, pos, tt
+
+
+def check_tokens(got: torch.Tensor, want: torch.Tensor, dtype) -> None:
+    if dtype == torch.float32:
+        assert float((got - want).abs().max()) <= 1e-5
+    else:
+        assert rel_err(got, want) <= 1e-2
+        same = float((got.view(torch.int16) == want.view(torch.int16)).float().mean())
+        assert same >= 0.98, same
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 64),
+                                     (torch.bfloat16, 1024)])
+def test_event_tokens_against_oracle(ext, dtype, d):
+    announce(f"event_tokens {dtype} d={d}")
+    words, counts = random_events(ext, 256, 0xE1)
+    words = torch.cat((words, edge_events()))
+    n = words.shape[0]
+    index = torch.cat((counts, torch.tensor([-1, 0, 47, 100], device=DEV)))
+    for seat_value in (0, 1):
+        seat = torch.full((n,), seat_value, dtype=torch.int64, device=DEV)
+        w, b, pos, tt = make_weights(414, d, dtype, seed=seat_value + d)
+        got = ext.event_tokens(words, seat, index, w.t().contiguous(), b, pos, tt)
+        tok = encode_events_np(words.cpu().numpy(), seat.cpu().numpy())
+        p = (1 + index.clamp(max=47)).clamp(min=0)
+        want = token_reference(tok, w, b, pos[p], tt[1].expand(n, d))
+        check_tokens(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 128)])
+def test_start_tokens_against_oracle(ext, dtype, d):
+    announce(f"start_tokens {dtype} d={d}")
+    n = 600
+    idx = torch.arange(n, dtype=torch.int64, device=DEV)
+    states = ext.create(idx * 104729 + 0x5EED, idx & 1)
+    start = ext.start(states)
+    w, b, pos, tt = make_weights(274, d, dtype, seed=7)
+    for seat_value in (0, 1):
+        seat = torch.full((n,), seat_value, dtype=torch.int64, device=DEV)
+        got = ext.start_tokens(start, seat, w.t().contiguous(), b, pos, tt)
+        tok = encode_start_np(start.cpu().numpy(), seat.cpu().numpy())
+        want = token_reference(tok, w, b, pos[0].expand(n, d), tt[0].expand(n, d))
+        check_tokens(got, want, dtype)
+
+
+def test_token_argument_errors(ext):
+    announce("token argument errors")
+    words = torch.zeros((4, 9), dtype=torch.int64, device=DEV)
+    seat = torch.zeros(4, dtype=torch.int64, device=DEV)
+    w, b, pos, tt = make_weights(414, 256, torch.bfloat16, 0)
+    with pytest.raises(RuntimeError):
+        ext.event_tokens(words, seat, seat, w, b, pos, tt)  # not transposed
+    with pytest.raises(RuntimeError):
+        ext.event_tokens(words, seat[:3], seat, w.t().contiguous(), b, pos, tt)
+    w2, b2, pos2, tt2 = make_weights(414, 96, torch.bfloat16, 0)
+    with pytest.raises(RuntimeError):
+        ext.event_tokens(words, seat, seat, w2.t().contiguous(), b2, pos2, tt2)  # d = 96
+    out = ext.event_tokens(words[:0], seat[:0], seat[:0], w.t().contiguous(), b, pos, tt)
+    assert out.shape == (0, 256)
+
+
+def test_gumbel_sample_matches_reference(ext):
+    announce("gumbel_sample")
+    g = torch.Generator(device=DEV).manual_seed(3)
+    n, a = 3000, 179
+    logits = torch.randn(n, a, generator=g, device=DEV) * 3.0
+    legal = torch.rand(n, a, generator=g, device=DEV) < 0.1
+    legal[:5] = False              # no legal action: every entry masked
+    legal[5:10] = True
+    u = torch.rand(n, a, generator=g, device=DEV)
+    u[10, :] = 0.0                 # clamps to 1e-20
+    u[11, 17] = 1.0                # -log(-log(1)) = +inf picks action 17
+    logits[12, :] = 0.5            # ties among equal scores pick the first index
+    u[12, :] = 0.5
+    actions, logp = ext.gumbel_sample(logits, legal, u)
+    want_a, want_lp = gumbel_reference(logits, legal, u)
+    assert torch.equal(actions, want_a)
+    assert int(actions[11]) == 17
+    assert float((logp - want_lp).abs().max()) <= 1e-5
+
+
+def _policy(d=256, layers=4, heads=8, seed=0):
+    from cugo_amd.seq_selfplay import SeqPolicy
+
+    torch.manual_seed(seed)
+    p = SeqPolicy(d_model=d, layers=layers, heads=heads)
+    with torch.no_grad():
+        for prm in p.parameters():
+            prm.normal_(0.0, 0.02)
+    return p.to(DEV).to(torch.bfloat16).eval()
+
+
+def _reference_step(policy, ref, actions_from=None):
+    """One WaveCollector step (cugo_seq_selfplay50.py:108-163, no pool) in the reference
+    formulation: dense tokens from the oracle, index_put_ + matmul attention, the torch
+    sampling lines.  `ref` holds the reference copy's tensors; with actions_from the
+    engine is stepped with those actions (teacher forcing) after sampling its own."""
+    ext, w, ids = ref["ext"], ref["w"], ref["ids"]
+    features, legal, players, done, status = ext.observe_indexed(ref["states"], ids)
+    active = ~done
+    player = players.long()
+    q = policy.query_token(features, legal)
+    hidden = reference_cached_step(policy, ref["cache"], q, (player & 1) * w + ids)
+    logits = policy.readout(hidden).float()
+    actions, logp = gumbel_reference(logits, legal, ref["noise"])
+    used = actions if actions_from is None else actions_from
+    _, new_done, _, _, committed, events = ext.step_events_indexed(ref["states"], ids, used)
+    commit = active & committed
+    seats2 = torch.cat((torch.zeros(w, dtype=torch.int64, device=DEV),
+                        torch.ones(w, dtype=torch.int64, device=DEV)))
+    ev2 = events.repeat(2, 1).cpu().numpy()
+    tok = encode_events_np(ev2, seats2.cpu().numpy())
+    index = ref["count"].repeat(2)
+    p = 1 + index.clamp(max=47)
+    x = token_reference(tok, policy.event_in.weight, policy.event_in.bias, policy.position[p],
+                        policy.token_type[1].expand(2 * w, -1))
+    reference_cached_step(policy, ref["cache"], x, torch.arange(2 * w, device=DEV))
+    ref["cache"].length += commit.repeat(2).long()
+    ref["count"] += commit.long()
+    return actions, logp, logits, features
+
+
+def test_selfplay_step_matches_reference_formulation(ext):
+    """The captured self-play step against the reference formulation for a wave of 256
+    games: identical engine trajectories (the reference copy replays the wave's actions),
+    logits within 1e-2 relative, the same sampled action for at least 99 % of the decisions,
+    the same engine states, counts and recorded features, and caches whose first layer
+    agrees within 1e-2 (deeper layers within 5e-2)."""
+    announce("selfplay step vs reference formulation")
+    from cugo_amd.seq_selfplay import SelfPlayWave, make_seeds, policy_cache
+
+    policy = _policy()
+    w = 256
+    wave = SelfPlayWave(ext, policy, w, max_steps=64)
+    wave.noise = torch.zeros((w, 179), device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    with torch.no_grad():
+        wave.capture()
+        seeds, first = make_seeds(w, 12345, DEV)
+        learner = torch.zeros(w, dtype=torch.int64, device=DEV)
+        wave.reset(seeds, first, learner)
+        ref = {"ext": ext, "w": w, "ids": torch.arange(w, device=DEV),
+               "states": ext.create(seeds, first), "cache": policy_cache(policy, 2 * w, DEV),
+               "count": torch.zeros(w, dtype=torch.int64, device=DEV), "noise": wave.noise}
+        start = ext.start(ref["states"])
+        seats2 = torch.cat((torch.zeros(w, dtype=torch.int64, device=DEV),
+                            torch.ones(w, dtype=torch.int64, device=DEV)))
+        tok = encode_start_np(start.repeat(2, 1).cpu().numpy(), seats2.cpu().numpy())
+        x0 = token_reference(tok, policy.start_in.weight, policy.start_in.bias,
+                             policy.position[0].expand(2 * w, -1),
+                             policy.token_type[0].expand(2 * w, -1))
+        reference_cached_step(policy, ref["cache"], x0, torch.arange(2 * w, device=DEV))
+        ref["cache"].length.fill_(1)
+        agree = total = 0
+        for step in range(30):
+            wave.noise.copy_(torch.rand((w, 179), generator=g, device=DEV))
+            wave.graph.replay()
+            actions = wave.rec_long["actions"][step]
+            a_ref, lp_ref, logits_ref, feats = _reference_step(policy, ref, actions_from=actions)
+            assert rel_err(wave.logits, logits_ref) <= 1e-2, step
+            same = actions == a_ref
+            agree += int(same.sum())
+            total += w
+            lp = wave.rec_logp[step]
+            assert float((lp - lp_ref)[same].abs().max()) <= 5e-2, step
+            assert torch.equal(wave.rec_features[step], feats.to(torch.bfloat16)), step
+            assert torch.equal(wave.states, ref["states"]), step
+            assert torch.equal(wave.count, ref["count"]), step
+            assert torch.equal(wave.cache.length, ref["cache"].length), step
+            if bool(wave.finished.all()):
+                break
+        assert agree >= 0.99 * total, (agree, total)
+        # Live slots only (below each row's length): slots past it still hold keys of
+        # the games played while capturing, which no query reads.  Layer 0's keys come
+        # from the tokens alone; deeper layers also carry the reference's bf16 rounding
+        # of attention scores and probabilities (the HIP decode keeps them in fp32).
+        live = (torch.arange(wave.cache.slots, device=DEV).view(1, -1)
+                < wave.cache.length.view(-1, 1)).view(1, -1, 1, wave.cache.slots, 1)
+        errs = [rel_err((wave.cache.k[i] * live[0]).float(), (ref["cache"].k[i] * live[0]).float())
+                for i in range(wave.cache.k.shape[0])]
+        assert errs[0] <= 1e-2, errs
+        assert max(errs) <= 2e-2, errs
+
+
+def test_selfplay_graph_replays_equal_eager_steps(ext):
+    """Replays of the captured step == eager step() calls from the same start (same
+    uniforms), repeated with eager work and synchronisations in between."""
+    announce("selfplay graph replay vs eager")
+    from cugo_amd.seq_selfplay import SelfPlayWave, make_seeds
+
+    policy = _policy(seed=1)
+    w = 128
+    wave = SelfPlayWave(ext, policy, w, max_steps=64)
+    wave.noise = torch.zeros((w, 179), device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    noises = [torch.rand((w, 179), generator=g, device=DEV) for _ in range(12)]
+    seeds, first = make_seeds(w, 777, DEV)
+    learner = torch.zeros(w, dtype=torch.int64, device=DEV)
+    runs = []
+    with torch.no_grad():
+        wave.capture()
+        for mode in ("eager", "graph", "graph"):
+            wave.reset(seeds, first, learner)
+            for k in range(12):
+                wave.noise.copy_(noises[k])
+                if mode == "eager":
+                    wave.step()
+                else:
+                    wave.graph.replay()
+                torch.cuda.synchronize()
+            runs.append([t.clone() for t in (wave.states, wave.events, wave.count,
+                                              wave.rec_long["actions"], wave.rec_logp,
+                                              wave.cache.length, wave.cache.k)])
+    for a, b in zip(runs[0], runs[1]):
+        assert torch.equal(a, b)
+    for a, b in zip(runs[1], runs[2]):
+        assert torch.equal(a, b)
+
+
+def test_selfplay_wave_plays_to_the_end(ext):
+    announce("selfplay wave to the end")
+    from cugo_amd.seq_selfplay import SelfPlayWave, make_seeds
+
+    policy = _policy(seed=2)
+    w = 512
+    wave = SelfPlayWave(ext, policy, w, max_steps=64)
+    seeds, first = make_seeds(w, 4242, DEV)
+    with torch.no_grad():
+        steps = wave.play(seeds, first, torch.zeros(w, dtype=torch.int64, device=DEV))
+    assert 16 <= steps <= 64
+    assert bool(wave.finished.all())
+    assert int(wave.bad) == 0
+    assert int(wave.count.max()) <= 48
+    # every recorded action was legal where the row was still playing
+    valid = wave.rec_valid[:steps]
+    acts = wave.rec_long["actions"][:steps]
+    legal = wave.rec_legal[:steps]
+    picked = legal.gather(2, acts.unsqueeze(2)).squeeze(2)
+    assert bool(picked[valid].all())
