@@ -63,6 +63,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-rollout", action="store_true")
+    p.add_argument("--no-selfplay", action="store_true")
     p.add_argument("--streams", type=int, default=1,
                    help="slices of the batch stepped on their own streams")
     p.add_argument("--no-graph", action="store_true", help="issue the loop eagerly")
@@ -320,6 +321,59 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
     return out
 
 
+def selfplay_workload(ext, torch, wave: int = 4096, waves: int = 3) -> dict:
+    """Event-sequence policy self-play (the reference's WaveCollector step): a 4-layer d256
+    SeqPolicy (8 heads of 32, bf16, N(0, 0.02) weights from seed 0) plays waves of `wave`
+    games to the end; each decision step (observe, query token, cached decode over the
+    [4, 2 * wave, 8, 50, 32] bf16 cache, readout, Gumbel-max, engine step with events, one
+    event token per seat appended) is one HIP-graph replay.  Reports complete games/s,
+    decision steps/s and tokens/s (three tokens per game per step: the query and two
+    event tokens), with the same step issued eagerly for comparison."""
+    from cugo_amd.seq_selfplay import SelfPlayWave, SeqPolicy, make_seeds
+
+    dev = torch.device("cuda")
+    torch.manual_seed(0)
+    policy = SeqPolicy(d_model=256, layers=4, heads=8)
+    with torch.no_grad():
+        for prm in policy.parameters():
+            prm.normal_(0.0, 0.02)
+    policy = policy.to(dev).to(torch.bfloat16).eval()
+    sp = SelfPlayWave(ext, policy, wave, max_steps=64)
+    learner = torch.zeros(wave, dtype=torch.int64, device=dev)
+    seeds, first = make_seeds(wave, 0, dev)
+    sp.play(seeds, first, learner)  # capture + one warm wave
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    steps = 0
+    for k in range(waves):
+        seeds, first = make_seeds(wave, (k + 1) * wave, dev)
+        steps += sp.play(seeds, first, learner)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # one step: graph replay vs eager, same state
+    reps = 16
+    sp.reset(seeds, first, learner)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(reps):
+        sp.graph.replay()
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t1) / reps * 1e3
+    sp.reset(seeds, first, learner)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(reps):
+        sp.step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t1) / reps * 1e3
+    return {"games_per_s": round(wave * waves / wall, 1),
+            "steps_per_wave": round(steps / waves, 2),
+            "decision_steps_per_s": round(wave * steps / wall, 1),
+            "tokens_per_s": round(3 * wave * steps / wall, 1),
+            "step_ms_graph": round(graph_ms, 4), "step_ms_eager": round(eager_ms, 4),
+            "wave": wave, "cache": [4, 2 * wave, 8, 50, 32], "dtype": "bf16"}
+
+
 def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict:
     """MLP PPO self-play rollout: B games, a residual MLP policy (720 features -> Linear 512
     -> 3 blocks of h + Linear(ReLU(Linear(LayerNorm(h)))) -> 179 logits and a value head,
@@ -504,6 +558,8 @@ def main() -> None:
         result["branch"] = branch_workload(ext, torch, args.branch_iters)
     if not args.no_decode:
         result["decode"] = decode_workload(ext, torch, args.decode_steps)
+    if not args.no_selfplay:
+        result["selfplay"] = selfplay_workload(ext, torch)
     if not args.no_rollout:
         result["rollout"] = rollout_workload(ext, torch)
     if not args.no_cpu:

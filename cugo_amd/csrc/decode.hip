@@ -10,17 +10,21 @@
 //
 // The work is a memory stream: every (query, head) reads (pos + 1) key and value rows
 // of dh elements once, and does ~2 flops per byte.  Layout of the work:
-//   * one 64-lane wavefront per (query, head); a 256-thread workgroup holds four
-//     consecutive (query, head) pairs, which for heads % 4 == 0 share the query and so
-//     the sequence length (no load imbalance inside a workgroup);
+//   * a 64-lane wavefront serves G consecutive heads of one query (64 / G lanes each);
+//     G = 1 for caches longer than one chunk of loads (below), otherwise the largest G
+//     whose chunk still covers the cache, so a short row costs one round trip and the
+//     wavefront count drops by G; a 256-thread workgroup holds four wavefronts, which
+//     for heads % (4 G) == 0 share the query and so the sequence length;
 //   * a slot row of dh elements is split into 16-byte parts; L = dh*elem/16 lanes hold
-//     one slot and the wavefront covers S = 64/L consecutive slots per load
-//     instruction, so each load instruction reads 1 KiB of contiguous cache;
+//     one slot and a head's lanes cover S = 64/(G L) consecutive slots per load
+//     instruction (1 KiB of contiguous cache per instruction at G = 1);
 //   * U = 8 such loads of K and of V are issued before any math (16 KiB in flight per
-//     wave), then scores are reduced over the L lanes of a slot;
+//     wave), the last partial chunk as one masked set of U loads; then scores are
+//     reduced over the L lanes of a slot;
 //   * softmax is online (running max / sum per lane group, base-2 exponentials with
 //     log2(e) folded into the scale) and the S lane groups merge their partial
 //     (max, sum, accumulator) triples with a log-sum-exp butterfly at the end.
+// CUGO_DECODE_FORCE_GROUP (a compile-time define) pins G for tuning builds.
 // Arithmetic is fp32 throughout, output rounded to the query's dtype (as the Triton
 // kernel does, cugo_seq_attention50.py:31-40).
 #include <hip/hip_runtime.h>
@@ -79,7 +83,7 @@ struct F32 {
 };
 
 constexpr float kNegInf = -__builtin_inff();
-constexpr int kWaves = 4;   // (query, head) pairs per workgroup
+constexpr int kWaves = 4;   // wavefronts per workgroup
 constexpr int kUnroll = 8;  // loads of K (and of V) in flight per lane
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -94,26 +98,34 @@ __device__ inline float reduce_lanes(float s) {
   return s;
 }
 
-template <class QT, class KT, int DH, bool APPEND, int U = kUnroll>
+// G (query, head) pairs per wavefront, consecutive heads of one query: W = 64 / G lanes
+// per head.  G = 1 streams long rows (16 slots of dh = 32 bf16 per load per head); a larger
+// G serves short rows (a 50-slot cache) with fewer wavefronts, each issuing the loads of
+// all its heads at once.
+template <class QT, class KT, int DH, bool APPEND, int G, int U = kUnroll>
 __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     const typename QT::storage* __restrict__ q, typename KT::storage* __restrict__ keys,
     typename KT::storage* __restrict__ values, const typename KT::storage* __restrict__ k_new,
     const typename KT::storage* __restrict__ v_new, const int64_t* __restrict__ pos_in,
-    const int64_t* __restrict__ rows, typename QT::storage* __restrict__ out, int64_t pairs,
+    const int64_t* __restrict__ rows, typename QT::storage* __restrict__ out, int64_t groups,
     int heads, int64_t slots, int64_t cache_rows, float scale_log2) {
   using KS = typename KT::storage;
   constexpr int E = 16 / (int)sizeof(KS);  // elements per 16-byte part
   constexpr int L = DH / E;                // lanes per slot
-  constexpr int S = 64 / L;                // slots per wavefront load
+  constexpr int W = 64 / G;                // lanes per head
+  constexpr int S = W / L;                 // slots per wavefront load, per head
   static_assert(DH % E == 0 && L >= 1 && L <= 64 && (L & (L - 1)) == 0, "unsupported dh");
+  static_assert(G >= 1 && (G & (G - 1)) == 0 && W % L == 0 && S >= 1, "unsupported grouping");
 
   const int lane = threadIdx.x & 63;
-  const int64_t pair = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (pair >= pairs) return;  // uniform over the wavefront
-  const int64_t query = pair / heads;
+  const int64_t group = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (group >= groups) return;  // uniform over the wavefront
+  const int64_t pair0 = group * G;
+  const int64_t query = pair0 / heads;
+  const int64_t pair = pair0 + lane / W;
   const int head = (int)(pair - query * heads);
-  const int sub = lane % L;   // which 16-byte part of a slot row
-  const int srow = lane / L;  // which slot of a load
+  const int sub = lane % L;         // which 16-byte part of a slot row
+  const int srow = (lane % W) / L;  // which slot of a load
   const int64_t row = rows ? rows[query] : query;
   int64_t pos = pos_in[query];
   typename QT::storage* o = out + pair * DH + sub * E;
@@ -205,37 +217,57 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     }
     m = mn;
   }
-  // Tail: one load of S slots at a time, slots >= limit masked.
-  for (; c < limit; c += S) {
-    const int64_t slot = c + srow;
-    const bool valid = slot < limit;
-    uint4 kr = make_uint4(0, 0, 0, 0), vr = make_uint4(0, 0, 0, 0);
-    if (valid) {
-      kr = *reinterpret_cast<const uint4*>(kb + (size_t)slot * DH);
-      vr = *reinterpret_cast<const uint4*>(vb + (size_t)slot * DH);
+  // Tail: one masked chunk of U loads (slots >= limit skipped), so a short row costs one
+  // round trip to memory rather than one per S slots.
+  if (c < limit) {
+    uint4 kr[U], vr[U];
+    bool valid[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t slot = c + u * S + srow;
+      valid[u] = slot < limit;  // uniform over a slot's L lanes
+      kr[u] = make_uint4(0, 0, 0, 0);
+      vr[u] = make_uint4(0, 0, 0, 0);
+      if (valid[u]) {
+        kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)slot * DH);
+        vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)slot * DH);
+      }
     }
-    float kf[E];
-    KT::unpack(kr, kf);
-    float d = 0.f;
+    float s[U];
+    float mx = kNegInf;
 #pragma unroll
-    for (int e = 0; e < E; ++e) d = __builtin_fmaf(qv[e], kf[e], d);
-    // Every lane takes part in the shuffles; `valid` is uniform over a slot's L lanes.
-    const float r = reduce_lanes<L>(d) * scale_log2;
-    const float s = valid ? r : kNegInf;
-    const float mn = fmaxf(m, s);
+    for (int u = 0; u < U; ++u) {
+      float kf[E];
+      KT::unpack(kr[u], kf);
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) d = __builtin_fmaf(qv[e], kf[e], d);
+      // every lane takes part in the shuffles, valid or not
+      const float r = reduce_lanes<L>(d) * scale_log2;
+      s[u] = valid[u] ? r : kNegInf;
+      mx = fmaxf(mx, s[u]);
+    }
+    const float mn = fmaxf(m, mx);
     const float alpha = rescale(m, mn);
-    const float p = valid ? exp2_fast(s - mn) : 0.f;
-    l = l * alpha + p;
-    float vf[E];
-    KT::unpack(vr, vf);
+    l *= alpha;
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e] * alpha);
+    for (int e = 0; e < E; ++e) acc[e] *= alpha;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float p = valid[u] ? exp2_fast(s[u] - mn) : 0.f;
+      l += p;
+      float vf[E];
+      KT::unpack(vr[u], vf);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e]);
+    }
     m = mn;
   }
 
-  // Merge the S slot groups (lanes with the same `sub`): log-sum-exp butterfly.
+  // Merge the S slot groups of each head (lanes with the same `sub`): log-sum-exp
+  // butterfly inside the head's W lanes.
 #pragma unroll
-  for (int off = L; off < 64; off <<= 1) {
+  for (int off = L; off < W; off <<= 1) {
     const float mo = __shfl_xor(m, off, 64);
     const float lo = __shfl_xor(l, off, 64);
     const float mn = fmaxf(m, mo);
@@ -256,21 +288,59 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
   }
 }
 
+template <class QT, class KT, int DH, bool APPEND, int G>
+int launch_group(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
+                 const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
+                 int64_t slots, int64_t cache_rows, float scale, hipStream_t stream) {
+  using QS = typename QT::storage;
+  using KS = typename KT::storage;
+  const int64_t groups = n * heads / G;
+  const int64_t blocks = (groups + kWaves - 1) / kWaves;
+  const float scale_log2 = scale * 1.4426950408889634f;  // softmax in base 2
+  hipLaunchKernelGGL((decode_kernel<QT, KT, DH, APPEND, G>), dim3((unsigned)blocks),
+                     dim3(64 * kWaves), 0, stream, static_cast<const QS*>(q),
+                     static_cast<KS*>(keys), static_cast<KS*>(values),
+                     static_cast<const KS*>(k_new), static_cast<const KS*>(v_new), pos, rows,
+                     static_cast<QS*>(out), groups, (int)heads, slots, cache_rows, scale_log2);
+  return (int)hipGetLastError();
+}
+
+// Heads per wavefront: the fewest wavefronts whose one chunk of U loads still covers every
+// slot of the cache (so a row is one round trip), among groupings that divide `heads`;
+// long caches (more slots than a chunk of G = 1 holds) use G = 1.
+template <int L>
+int pick_group(int64_t heads, int64_t slots) {
+#ifdef CUGO_DECODE_FORCE_GROUP
+  if (heads % CUGO_DECODE_FORCE_GROUP == 0 && CUGO_DECODE_FORCE_GROUP * L <= 64)
+    return CUGO_DECODE_FORCE_GROUP;
+#endif
+  int best = 1;
+  for (int g = 2; g <= 8; g <<= 1)
+    if (heads % g == 0 && g * L <= 64 && (int64_t)(64 / (g * L)) * kUnroll >= slots) best = g;
+  return best;
+}
+
 template <class QT, class KT, int DH, bool APPEND>
 int launch(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
            const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
            int64_t slots, int64_t cache_rows, float scale, hipStream_t stream) {
-  using QS = typename QT::storage;
-  using KS = typename KT::storage;
-  const int64_t pairs = n * heads;
-  const int64_t blocks = (pairs + kWaves - 1) / kWaves;
-  const float scale_log2 = scale * 1.4426950408889634f;  // softmax in base 2
-  hipLaunchKernelGGL((decode_kernel<QT, KT, DH, APPEND>), dim3((unsigned)blocks),
-                     dim3(64 * kWaves), 0, stream, static_cast<const QS*>(q),
-                     static_cast<KS*>(keys), static_cast<KS*>(values),
-                     static_cast<const KS*>(k_new), static_cast<const KS*>(v_new), pos, rows,
-                     static_cast<QS*>(out), pairs, (int)heads, slots, cache_rows, scale_log2);
-  return (int)hipGetLastError();
+  constexpr int L = DH / (16 / (int)sizeof(typename KT::storage));
+  switch (pick_group<L>(heads, slots)) {
+#define CUGO_GROUP(GG)                                                                        \
+  case GG:                                                                                    \
+    if constexpr (GG * L <= 64)                                                               \
+      return launch_group<QT, KT, DH, APPEND, GG>(q, keys, values, k_new, v_new, pos, rows,   \
+                                                  out, n, heads, slots, cache_rows, scale,    \
+                                                  stream);                                    \
+    return -3;
+    CUGO_GROUP(2)
+    CUGO_GROUP(4)
+    CUGO_GROUP(8)
+#undef CUGO_GROUP
+    default:
+      return launch_group<QT, KT, DH, APPEND, 1>(q, keys, values, k_new, v_new, pos, rows, out,
+                                                 n, heads, slots, cache_rows, scale, stream);
+  }
 }
 
 template <class QT, class KT, bool APPEND>

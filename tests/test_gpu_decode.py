@@ -58,6 +58,41 @@ def test_small_shapes_against_float64(ext):
         assert err <= tol, (dh, kvdt, qdt, err)
 
 
+def test_short_caches_every_head_grouping(ext):
+    """Short caches are served with several heads per wavefront (1, 2, 4 or 8, chosen from
+    the slot count and the heads): every grouping, plain and fused-append, against float64."""
+    announce("decode short caches, grouped heads")
+    for dh, kvdt, qdt in ((32, torch.bfloat16, torch.bfloat16), (64, torch.bfloat16, torch.bfloat16),
+                          (16, torch.bfloat16, torch.bfloat16), (32, torch.float32, torch.float32)):
+        for heads in (1, 2, 4, 8, 16):
+            for slots in (5, 16, 33, 50):
+                n, rows = 9, 11
+                seed = dh * 1000 + heads * 100 + slots
+                q, k, v = make_case(n, rows, heads, slots, dh, seed=seed, qdt=qdt, kvdt=kvdt)
+                g = np.random.default_rng(seed)
+                row_ids = torch.from_numpy(g.permutation(rows)[:n]).to(DEV)
+                pos = torch.from_numpy(g.integers(0, slots, n)).to(DEV)
+                pos[:2] = torch.tensor([0, slots - 1], device=DEV)
+                tol = 4e-3 if qdt == torch.bfloat16 else 1e-5
+                out = decode_attention(q, k, v, pos, rows=row_ids)
+                want = brute_force(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                   v.float().cpu().numpy(), pos.cpu().numpy(),
+                                   row_ids.cpu().numpy())
+                assert rel_err(out, want) <= tol, (dh, heads, slots)
+                kn = (q * 0.5).to(kvdt)
+                vn = (q * -0.25).to(kvdt)
+                k2, v2 = k.clone(), v.clone()
+                out2 = decode_attention_append(q, kn, vn, k2, v2, pos, rows=row_ids)
+                k3, v3 = k.clone(), v.clone()
+                k3[row_ids, :, pos] = kn
+                v3[row_ids, :, pos] = vn
+                assert torch.equal(k2, k3) and torch.equal(v2, v3), (dh, heads, slots)
+                want2 = brute_force(q.float().cpu().numpy(), k3.float().cpu().numpy(),
+                                    v3.float().cpu().numpy(), pos.cpu().numpy(),
+                                    row_ids.cpu().numpy())
+                assert rel_err(out2, want2) <= tol, (dh, heads, slots, "append")
+
+
 def test_reference_shape_against_matmul_path(ext):
     """The reference's cache: [2 x 4,096 rows, 8 heads, 50 slots, 32] bf16, 4,096 queries
     on distinct random rows, ragged pos in [0, 49]."""
