@@ -10,11 +10,11 @@
 //
 // The work is a memory stream: every (query, head) reads (pos + 1) key and value rows
 // of dh elements once, and does ~2 flops per byte.  Layout of the work:
-//   * a 64-lane wavefront serves G consecutive heads of one query (64 / G lanes each);
-//     G = 1 for caches longer than one chunk of loads (below), otherwise the largest G
-//     whose chunk still covers the cache, so a short row costs one round trip and the
-//     wavefront count drops by G; a 256-thread workgroup holds four wavefronts, which
-//     for heads % (4 G) == 0 share the query and so the sequence length;
+//   * a 64-lane wavefront serves G consecutive heads of one query (64 / G lanes each):
+//     up to 8 for short caches, so the wavefront count drops by G and each wavefront
+//     keeps its heads' loads in flight together, 2 for long ones (pick_group); a
+//     256-thread workgroup holds four wavefronts, which for heads % (4 G) == 0 share the
+//     query and so the sequence length;
 //   * a slot row of dh elements is split into 16-byte parts; L = dh*elem/16 lanes hold
 //     one slot and a head's lanes cover S = 64/(G L) consecutive slots per load
 //     instruction (1 KiB of contiguous cache per instruction at G = 1);
@@ -108,7 +108,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     typename KT::storage* __restrict__ values, const typename KT::storage* __restrict__ k_new,
     const typename KT::storage* __restrict__ v_new, const int64_t* __restrict__ pos_in,
     const int64_t* __restrict__ rows, typename QT::storage* __restrict__ out, int64_t groups,
-    int heads, int64_t slots, int64_t cache_rows, float scale_log2) {
+    int heads, int64_t slots, int64_t cache_rows, float scale_log2, int64_t q_stride,
+    int64_t new_stride) {
   using KS = typename KT::storage;
   constexpr int E = 16 / (int)sizeof(KS);  // elements per 16-byte part
   constexpr int L = DH / E;                // lanes per slot
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 
   float qv[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) qv[e] = QT::to_float(q[pair * DH + sub * E + e]);
+  for (int e = 0; e < E; ++e) qv[e] = QT::to_float(q[query * q_stride + head * DH + sub * E + e]);
 
   float m = kNegInf, l = 0.f, acc[E];
 #pragma unroll
@@ -158,8 +159,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     // The new key/value goes to slot `pos` (cugo_seq50.py:317-318) and is attended from
     // registers; the cache loop reads slots [0, pos).
     limit = pos;
-    const uint4 kn = *reinterpret_cast<const uint4*>(k_new + pair * DH + sub * E);
-    const uint4 vn = *reinterpret_cast<const uint4*>(v_new + pair * DH + sub * E);
+    const int64_t at = query * new_stride + head * DH + sub * E;
+    const uint4 kn = *reinterpret_cast<const uint4*>(k_new + at);
+    const uint4 vn = *reinterpret_cast<const uint4*>(v_new + at);
     if (srow == 0) {
       *reinterpret_cast<uint4*>(keys + base + (size_t)pos * DH) = kn;
       *reinterpret_cast<uint4*>(values + base + (size_t)pos * DH) = vn;
@@ -291,7 +293,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 template <class QT, class KT, int DH, bool APPEND, int G>
 int launch_group(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
                  const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
-                 int64_t slots, int64_t cache_rows, float scale, hipStream_t stream) {
+                 int64_t slots, int64_t cache_rows, float scale, int64_t q_stride,
+                 int64_t new_stride, hipStream_t stream) {
   using QS = typename QT::storage;
   using KS = typename KT::storage;
   const int64_t groups = n * heads / G;
@@ -301,29 +304,34 @@ int launch_group(const void* q, void* keys, void* values, const void* k_new, con
                      dim3(64 * kWaves), 0, stream, static_cast<const QS*>(q),
                      static_cast<KS*>(keys), static_cast<KS*>(values),
                      static_cast<const KS*>(k_new), static_cast<const KS*>(v_new), pos, rows,
-                     static_cast<QS*>(out), groups, (int)heads, slots, cache_rows, scale_log2);
+                     static_cast<QS*>(out), groups, (int)heads, slots, cache_rows, scale_log2,
+                     q_stride, new_stride);
   return (int)hipGetLastError();
 }
 
-// Heads per wavefront: the fewest wavefronts whose one chunk of U loads still covers every
-// slot of the cache (so a row is one round trip), among groupings that divide `heads`;
-// long caches (more slots than a chunk of G = 1 holds) use G = 1.
+// Heads per wavefront.  Measured on MI355X (4,096 queries x 8 heads, dh 32 bf16): rows of
+// up to ~50 slots run 2-2.5x faster with 8 heads per wavefront than with one (fewer
+// wavefronts, each with all its loads in flight); rows of up to 319 slots are within 5 %
+// for every grouping and fastest at 2.  So: up to 8 for caches of at most 64 slots, else 2
+// (a grouping must divide `heads` and fit G * L <= 64 lanes).
 template <int L>
 int pick_group(int64_t heads, int64_t slots) {
 #ifdef CUGO_DECODE_FORCE_GROUP
   if (heads % CUGO_DECODE_FORCE_GROUP == 0 && CUGO_DECODE_FORCE_GROUP * L <= 64)
     return CUGO_DECODE_FORCE_GROUP;
 #endif
+  const int want = slots <= 64 ? 8 : 2;
   int best = 1;
-  for (int g = 2; g <= 8; g <<= 1)
-    if (heads % g == 0 && g * L <= 64 && (int64_t)(64 / (g * L)) * kUnroll >= slots) best = g;
+  for (int g = 2; g <= want; g <<= 1)
+    if (heads % g == 0 && g * L <= 64) best = g;
   return best;
 }
 
 template <class QT, class KT, int DH, bool APPEND>
 int launch(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
            const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
-           int64_t slots, int64_t cache_rows, float scale, hipStream_t stream) {
+           int64_t slots, int64_t cache_rows, float scale, int64_t q_stride, int64_t new_stride,
+           hipStream_t stream) {
   constexpr int L = DH / (16 / (int)sizeof(typename KT::storage));
   switch (pick_group<L>(heads, slots)) {
 #define CUGO_GROUP(GG)                                                                        \
@@ -331,7 +339,7 @@ int launch(const void* q, void* keys, void* values, const void* k_new, const voi
     if constexpr (GG * L <= 64)                                                               \
       return launch_group<QT, KT, DH, APPEND, GG>(q, keys, values, k_new, v_new, pos, rows,   \
                                                   out, n, heads, slots, cache_rows, scale,    \
-                                                  stream);                                    \
+                                                  q_stride, new_stride, stream);              \
     return -3;
     CUGO_GROUP(2)
     CUGO_GROUP(4)
@@ -339,20 +347,23 @@ int launch(const void* q, void* keys, void* values, const void* k_new, const voi
 #undef CUGO_GROUP
     default:
       return launch_group<QT, KT, DH, APPEND, 1>(q, keys, values, k_new, v_new, pos, rows, out,
-                                                 n, heads, slots, cache_rows, scale, stream);
+                                                 n, heads, slots, cache_rows, scale, q_stride,
+                                                 new_stride, stream);
   }
 }
 
 template <class QT, class KT, bool APPEND>
 int by_dh(int64_t dh, const void* q, void* keys, void* values, const void* k_new,
           const void* v_new, const int64_t* pos, const int64_t* rows, void* out, int64_t n,
-          int64_t heads, int64_t slots, int64_t cache_rows, float scale, hipStream_t stream) {
+          int64_t heads, int64_t slots, int64_t cache_rows, float scale, int64_t q_stride,
+          int64_t new_stride, hipStream_t stream) {
   switch (dh) {
 #define CUGO_DH(D)                                                                       \
   case D:                                                                                \
     if constexpr (16 / sizeof(typename KT::storage) <= D)                                \
       return launch<QT, KT, D, APPEND>(q, keys, values, k_new, v_new, pos, rows, out, n, \
-                                       heads, slots, cache_rows, scale, stream);         \
+                                       heads, slots, cache_rows, scale, q_stride,        \
+                                       new_stride, stream);                              \
     return -3;
     CUGO_DH(16)
     CUGO_DH(32)
@@ -368,18 +379,21 @@ template <bool APPEND>
 int dispatch(int q_dtype, int kv_dtype, int64_t dh, const void* q, void* keys, void* values,
              const void* k_new, const void* v_new, const int64_t* pos, const int64_t* rows,
              void* out, int64_t n, int64_t heads, int64_t slots, int64_t cache_rows,
-             float scale, hipStream_t stream) {
+             float scale, int64_t q_stride, int64_t new_stride, hipStream_t stream) {
 #define CUGO_KV(QTYPE)                                                                      \
   switch (kv_dtype) {                                                                       \
     case CUGO_DTYPE_BF16:                                                                   \
       return by_dh<QTYPE, BF16, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, out, \
-                                        n, heads, slots, cache_rows, scale, stream);       \
+                                        n, heads, slots, cache_rows, scale, q_stride,      \
+                                        new_stride, stream);                               \
     case CUGO_DTYPE_F16:                                                                    \
       return by_dh<QTYPE, F16, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, out,  \
-                                       n, heads, slots, cache_rows, scale, stream);        \
+                                       n, heads, slots, cache_rows, scale, q_stride,       \
+                                       new_stride, stream);                                \
     case CUGO_DTYPE_F32:                                                                    \
       return by_dh<QTYPE, F32, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, out,  \
-                                       n, heads, slots, cache_rows, scale, stream);        \
+                                       n, heads, slots, cache_rows, scale, q_stride,       \
+                                       new_stride, stream);                                \
     default:                                                                                \
       return -2;                                                                            \
   }
@@ -412,32 +426,37 @@ int check_args(const void* q, const void* keys, const void* values, const int64_
 
 extern "C" {
 
-int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, const void* keys,
-                          const void* values, const int64_t* pos, const int64_t* rows,
-                          int64_t n, int64_t heads, int64_t dh, int64_t slots,
-                          int64_t cache_rows, float scale, void* out, hipStream_t stream) {
+int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, int64_t q_stride,
+                          const void* keys, const void* values, const int64_t* pos,
+                          const int64_t* rows, int64_t n, int64_t heads, int64_t dh,
+                          int64_t slots, int64_t cache_rows, float scale, void* out,
+                          hipStream_t stream) {
   using namespace cugo_amd::decode;
   const int bad = check_args(q, keys, values, pos, out, n, heads, dh, slots, cache_rows);
   if (bad) return bad;
+  if (q_stride < heads * dh) return -1;
   if (n == 0) return 0;
   return dispatch<false>(q_dtype, kv_dtype, dh, q, const_cast<void*>(keys),
                          const_cast<void*>(values), nullptr, nullptr, pos, rows, out, n, heads,
-                         slots, cache_rows, scale, stream);
+                         slots, cache_rows, scale, q_stride, 0, stream);
 }
 
-int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, const void* k_new,
-                                 const void* v_new, void* keys, void* values,
-                                 const int64_t* pos, const int64_t* rows, int64_t n,
-                                 int64_t heads, int64_t dh, int64_t slots, int64_t cache_rows,
-                                 float scale, void* out, hipStream_t stream) {
+int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, int64_t q_stride,
+                                 const void* k_new, const void* v_new, int64_t new_stride,
+                                 void* keys, void* values, const int64_t* pos,
+                                 const int64_t* rows, int64_t n, int64_t heads, int64_t dh,
+                                 int64_t slots, int64_t cache_rows, float scale, void* out,
+                                 hipStream_t stream) {
   using namespace cugo_amd::decode;
   const int bad = check_args(q, keys, values, pos, out, n, heads, dh, slots, cache_rows);
   if (bad) return bad;
   if (n > 0 && (!k_new || !v_new)) return -1;
-  if (!aligned16(k_new) || !aligned16(v_new)) return -4;
+  if (q_stride < heads * dh || new_stride < heads * dh) return -1;
+  const int64_t kv_size = kv_dtype == CUGO_DTYPE_F32 ? 4 : 2;
+  if (!aligned16(k_new) || !aligned16(v_new) || (new_stride * kv_size) % 16 != 0) return -4;
   if (n == 0) return 0;
   return dispatch<true>(q_dtype, kv_dtype, dh, q, keys, values, k_new, v_new, pos, rows, out,
-                        n, heads, slots, cache_rows, scale, stream);
+                        n, heads, slots, cache_rows, scale, q_stride, new_stride, stream);
 }
 
 }  // extern "C"

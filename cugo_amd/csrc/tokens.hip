@@ -1,5 +1,5 @@
-// Token embeddings and action sampling of the event-sequence policy's self-play step,
-// for gfx950.
+// Token embeddings, the residual add + LayerNorm of the decoder layers and action
+// sampling of the event-sequence policy's self-play step, for gfx950.
 //
 // Reference: python/cugo_seq50.py (encode_events :91-110, encode_start :113-128,
 // SeqNet.start_token :271-274, SeqNet.event_token :276-282) and the sampling lines of
@@ -221,6 +221,72 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
   }
 }
 
+// Pre-norm transformer residual step (nn.TransformerEncoderLayer with norm_first,
+// python/cugo_seq50.py:318-322): x_out = x + y rounded to the dtype (y == nullptr: x_out is
+// not written and x is normalised as is), then ln = LayerNorm(x_out) with fp32 mean and
+// variance over the row, rounded to the dtype.  One wavefront per row, K = d / 64 columns
+// per lane.
+template <class T, int K>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
+    const typename T::storage* x, const typename T::storage* y, const typename T::storage* w,
+    const typename T::storage* b, float eps, i64 n, int d, typename T::storage* x_out,
+    typename T::storage* ln) {
+  const int lane = threadIdx.x & 63;
+  const i64 r = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
+  if (r >= n) return;
+  float v[K];
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const i64 at = r * d + lane + 64 * k;
+    float t = T::to_float(x[at]);
+    if (y != nullptr) {
+      t = T::round(t + T::to_float(y[at]));
+      x_out[at] = T::from_float(t);
+    }
+    v[k] = t;
+    sum += t;
+  }
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const float mean = sum / (float)d;
+  float sq = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float c = v[k] - mean;
+    sq += c * c;
+  }
+  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+  const float rstd = 1.0f / sqrtf(sq / (float)d + eps);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int c = lane + 64 * k;
+    ln[r * d + c] = T::from_float((v[k] - mean) * rstd * T::to_float(w[c]) + T::to_float(b[c]));
+  }
+}
+
+template <class T>
+int launch_add_layernorm(const void* x, const void* y, const void* w, const void* b, float eps,
+                         i64 n, int d, void* x_out, void* ln, hipStream_t stream) {
+  using S = typename T::storage;
+  const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
+#define CUGO_LN_CASE(KK)                                                                    \
+  case KK:                                                                                  \
+    add_layernorm_kernel<T, KK><<<grid, 64 * kRowsPerBlock, 0, stream>>>(                   \
+        (const S*)x, (const S*)y, (const S*)w, (const S*)b, eps, n, d, (S*)x_out, (S*)ln);  \
+    break;
+  switch (d / 64) {
+    CUGO_LN_CASE(1)
+    CUGO_LN_CASE(2)
+    CUGO_LN_CASE(4)
+    CUGO_LN_CASE(8)
+    CUGO_LN_CASE(16)
+    default:
+      return -3;
+  }
+#undef CUGO_LN_CASE
+  return (int)hipGetLastError();
+}
+
 template <class T>
 int launch_event(const i64* words, const i64* seat, const i64* index, i64 n, const void* wt,
                  const void* bias, const void* position, i64 position_rows,
@@ -315,6 +381,19 @@ int cugo_start_tokens(int dtype, const int64_t* start, const int64_t* seat, int6
   if (dtype == CUGO_DTYPE_F32)
     return launch_start<F32>(start, seat, n, weight_t, bias, position, token_type, (int)d,
                              out, stream);
+  return -2;
+}
+
+int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weight,
+                       const void* bias, float eps, int64_t n, int64_t d, void* x_out, void* ln,
+                       hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!x || !weight || !bias || !ln || (y && !x_out)))) return -1;
+  if (!valid_width(d)) return -3;
+  if (n == 0) return 0;
+  if (dtype == CUGO_DTYPE_BF16)
+    return launch_add_layernorm<BF16>(x, y, weight, bias, eps, n, (int)d, x_out, ln, stream);
+  if (dtype == CUGO_DTYPE_F32)
+    return launch_add_layernorm<F32>(x, y, weight, bias, eps, n, (int)d, x_out, ln, stream);
   return -2;
 }
 

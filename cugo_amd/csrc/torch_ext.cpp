@@ -417,17 +417,29 @@ void check_decode(const torch::Tensor& q, const torch::Tensor& keys, const torch
 // decode_attention(q, keys, values, pos, rows=None)
 // (python/cugo_seq_attention50.py:43-62): q [n, heads, dh]; keys/values
 // [rows, heads, slots, dh]; pos/rows int64 [n] -> [n, heads, dh] in q's dtype.
+// [n, heads, dh] rows read in place when each row's [heads, dh] block is contiguous (a
+// column slice of a packed [n, 3 d] projection is); otherwise a contiguous copy.
+torch::Tensor row_blocks(const torch::Tensor& t) {
+  const bool in_place = t.stride(2) == 1 && t.stride(1) == t.size(2) &&
+                        (t.size(0) <= 1 || t.stride(0) >= t.size(1) * t.size(2));
+  return in_place ? t : t.contiguous();
+}
+
+int64_t block_stride(const torch::Tensor& t) {
+  return t.size(0) <= 1 ? t.size(1) * t.size(2) : t.stride(0);
+}
+
 torch::Tensor decode_attention(torch::Tensor q, torch::Tensor keys, torch::Tensor values,
                                torch::Tensor pos, c10::optional<torch::Tensor> rows) {
   check_decode(q, keys, values, pos, rows);
   const DeviceGuard guard(q.device());
-  q = q.contiguous();
-  auto out = torch::empty_like(q);
+  q = row_blocks(q);
+  auto out = torch::empty(q.sizes(), q.options());
   const int64_t dh = q.size(2);
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(dh)));
   check_call(cugo_decode_attention(dtype_code(q.scalar_type()), dtype_code(keys.scalar_type()),
-                                   q.data_ptr(), keys.data_ptr(), values.data_ptr(),
-                                   pos.data_ptr<int64_t>(),
+                                   q.data_ptr(), block_stride(q), keys.data_ptr(),
+                                   values.data_ptr(), pos.data_ptr<int64_t>(),
                                    rows.has_value() ? rows->data_ptr<int64_t>() : nullptr,
                                    q.size(0), q.size(1), dh, keys.size(2), keys.size(0), scale,
                                    out.data_ptr(), stream()),
@@ -447,15 +459,23 @@ torch::Tensor decode_attention_append(torch::Tensor q, torch::Tensor k_new, torc
   check_same_device(q, k_new, "q", "k_new");
   check_same_device(q, v_new, "q", "v_new");
   const DeviceGuard guard(q.device());
-  q = q.contiguous();
-  k_new = k_new.to(keys.scalar_type()).contiguous();
-  v_new = v_new.to(keys.scalar_type()).contiguous();
-  auto out = torch::empty_like(q);
+  q = row_blocks(q);
+  k_new = row_blocks(k_new.to(keys.scalar_type()));
+  v_new = row_blocks(v_new.to(keys.scalar_type()));
+  const int64_t elem = keys.element_size();
+  if (block_stride(k_new) != block_stride(v_new) || (block_stride(k_new) * elem) % 16 != 0 ||
+      (reinterpret_cast<uintptr_t>(k_new.data_ptr()) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(v_new.data_ptr()) & 15u) != 0) {
+    k_new = k_new.contiguous();
+    v_new = v_new.contiguous();
+  }
+  auto out = torch::empty(q.sizes(), q.options());
   const int64_t dh = q.size(2);
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(dh)));
   check_call(cugo_decode_attention_append(
                  dtype_code(q.scalar_type()), dtype_code(keys.scalar_type()), q.data_ptr(),
-                 k_new.data_ptr(), v_new.data_ptr(), keys.data_ptr(), values.data_ptr(),
+                 block_stride(q), k_new.data_ptr(), v_new.data_ptr(), block_stride(k_new),
+                 keys.data_ptr(), values.data_ptr(),
                  pos.data_ptr<int64_t>(), rows.has_value() ? rows->data_ptr<int64_t>() : nullptr,
                  q.size(0), q.size(1), dh, keys.size(2), keys.size(0), scale, out.data_ptr(),
                  stream()),
@@ -545,6 +565,40 @@ torch::Tensor start_tokens(torch::Tensor start, torch::Tensor seat, torch::Tenso
   return out;
 }
 
+// add_layernorm(x [n, d], y [n, d] or None, weight [d], bias [d], eps) -> (x + y, LN(x + y));
+// with y None: (x, LN(x)).  The residual add and the next pre-norm of a
+// TransformerEncoderLayer step (python/cugo_seq50.py:318-322) in one launch.
+std::vector<torch::Tensor> add_layernorm(torch::Tensor x, c10::optional<torch::Tensor> y,
+                                         torch::Tensor weight, torch::Tensor bias, double eps) {
+  TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.dim() == 2,
+              "x must be a contiguous CUDA [n, d] tensor");
+  const auto t = x.scalar_type();
+  TORCH_CHECK(t == at::kBFloat16 || t == at::kFloat, "add_layernorm supports bfloat16 and float32");
+  const int64_t n = x.size(0), d = x.size(1);
+  TORCH_CHECK(d == 64 || d == 128 || d == 256 || d == 512 || d == 1024,
+              "d must be 64, 128, 256, 512 or 1024");
+  TORCH_CHECK(weight.scalar_type() == t && bias.scalar_type() == t && weight.numel() == d &&
+                  bias.numel() == d && weight.is_contiguous() && bias.is_contiguous(),
+              "weight and bias must be contiguous [d] tensors of x's dtype");
+  check_same_device(x, weight, "x", "weight");
+  check_same_device(x, bias, "x", "bias");
+  torch::Tensor yc;
+  if (y.has_value()) {
+    yc = y->contiguous();
+    TORCH_CHECK(yc.sizes() == x.sizes() && yc.scalar_type() == t, "y must match x");
+    check_same_device(x, yc, "x", "y");
+  }
+  const DeviceGuard guard(x.device());
+  auto x_out = y.has_value() ? torch::empty_like(x) : x;
+  auto ln = torch::empty_like(x);
+  check_call(cugo_add_layernorm(t == at::kBFloat16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32,
+                                x.data_ptr(), y.has_value() ? yc.data_ptr() : nullptr,
+                                weight.data_ptr(), bias.data_ptr(), static_cast<float>(eps), n,
+                                d, x_out.data_ptr(), ln.data_ptr(), stream()),
+             "add_layernorm");
+  return {x_out, ln};
+}
+
 // gumbel_sample(logits f32 [n, A], legal bool [n, A], uniforms f32 [n, A]) -> (actions
 // int64 [n], logp f32 [n]): the sampling of WaveCollector._step
 // (python/cugo_seq_selfplay50.py:125-130) with the uniforms supplied.
@@ -609,6 +663,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1);
   m.def("event_tokens", &event_tokens, "SeqNet.event_token: event_in(encode_events) + position + type");
   m.def("start_tokens", &start_tokens, "SeqNet.start_token: start_in(encode_start) + position + type");
+  m.def("add_layernorm", &add_layernorm, "x + y and LayerNorm(x + y) in one launch",
+        pybind11::arg("x"), pybind11::arg("y"), pybind11::arg("weight"), pybind11::arg("bias"),
+        pybind11::arg("eps"));
   m.def("gumbel_sample", &gumbel_sample, "Masked Gumbel-max action and its log-softmax probability");
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),

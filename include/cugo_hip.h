@@ -154,7 +154,10 @@ int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation
  *   out[i, h, :] = sum_t softmax_t(scale * q[i,h,:] . keys[r,h,t,:]) values[r,h,t,:]
  *   with r = rows[i] (rows == NULL: r = i) and t = 0 .. min(pos[i], slots - 1).
  *
- *   q, out        [n, heads, dh] of q_dtype, contiguous
+ *   q             [n, heads, dh] of q_dtype: q[i, h, :] at q + i * q_stride + h * dh
+ *                 (q_stride >= heads * dh elements; a column slice of a packed
+ *                 in-projection output is read in place)
+ *   out           [n, heads, dh] of q_dtype, contiguous
  *   keys, values  [cache_rows, heads, slots, dh] of kv_dtype, contiguous, 16-byte aligned
  *   pos, rows     int64 [n]
  * Softmax and accumulation are fp32; out is rounded to q_dtype.  dh is 16, 32, 64 or 128
@@ -167,24 +170,27 @@ int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation
 #define CUGO_DTYPE_F16 1
 #define CUGO_DTYPE_BF16 2
 
-int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, const void* keys,
-                          const void* values, const int64_t* pos, const int64_t* rows,
-                          int64_t n, int64_t heads, int64_t dh, int64_t slots,
-                          int64_t cache_rows, float scale, void* out, hipStream_t stream);
+int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, int64_t q_stride,
+                          const void* keys, const void* values, const int64_t* pos,
+                          const int64_t* rows, int64_t n, int64_t heads, int64_t dh,
+                          int64_t slots, int64_t cache_rows, float scale, void* out,
+                          hipStream_t stream);
 
 /*
  * The reference caller's KV append fused with the decode (python/cugo_seq50.py:313-320:
  * index_put_ of the new key/value at slot pos[i] of row rows[i], then decode_attention):
- * k_new/v_new [n, heads, dh] of kv_dtype (16-byte aligned) are written to slot
+ * k_new/v_new [n, heads, dh] of kv_dtype (16-byte aligned; row i at i * new_stride
+ * elements, new_stride * element size a multiple of 16) are written to slot
  * min(pos[i], slots - 1) of each query's row, and the query attends slots 0..pos as
  * above, taking the new slot from registers.  Two queries naming the same row write the
  * same slot (as index_put_ with repeated indices, the value that lands is either one).
  */
-int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, const void* k_new,
-                                 const void* v_new, void* keys, void* values,
-                                 const int64_t* pos, const int64_t* rows, int64_t n,
-                                 int64_t heads, int64_t dh, int64_t slots, int64_t cache_rows,
-                                 float scale, void* out, hipStream_t stream);
+int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, int64_t q_stride,
+                                 const void* k_new, const void* v_new, int64_t new_stride,
+                                 void* keys, void* values, const int64_t* pos,
+                                 const int64_t* rows, int64_t n, int64_t heads, int64_t dh,
+                                 int64_t slots, int64_t cache_rows, float scale, void* out,
+                                 hipStream_t stream);
 
 /*
  * Event-sequence policy self-play (python/cugo_seq50.py, python/cugo_seq_selfplay50.py).
@@ -208,6 +214,14 @@ int cugo_event_tokens(int dtype, const int64_t* words, const int64_t* seat,
 int cugo_start_tokens(int dtype, const int64_t* start, const int64_t* seat, int64_t n,
                       const void* weight_t, const void* bias, const void* position,
                       const void* token_type, int64_t d, void* out, hipStream_t stream);
+/* cugo_add_layernorm: the residual step of a pre-norm transformer layer
+ * (nn.TransformerEncoderLayer, norm_first; python/cugo_seq50.py:318-322):
+ * x_out = x + y (rounded to dtype; y == NULL leaves x_out unwritten and normalises x),
+ * ln = LayerNorm(x_out) * weight + bias with fp32 row statistics, rounded to dtype.
+ * x, y, x_out, ln [n, d]; weight, bias [d]; x_out may alias x. */
+int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weight,
+                       const void* bias, float eps, int64_t n, int64_t d, void* x_out, void* ln,
+                       hipStream_t stream);
 /* cugo_gumbel_sample: the sampling of WaveCollector._step (cugo_seq_selfplay50.py:125-130)
  * given the uniforms torch.rand_like drew: masked = legal ? logits : -1e30;
  * actions[i] = argmax_a(masked - log(-log(clamp(u, 1e-20, 1)))) (first index on ties);

@@ -93,6 +93,27 @@ def test_short_caches_every_head_grouping(ext):
                 assert rel_err(out2, want2) <= tol, (dh, heads, slots, "append")
 
 
+def test_strided_rows_read_in_place(ext):
+    """q, k_new and v_new as column slices of one packed [n, 3 * heads * dh] projection
+    (what cached_step passes): results and cache writes identical to contiguous copies."""
+    announce("decode strided q / k_new / v_new")
+    n, rows, heads, slots, dh = 300, 512, 8, 50, 32
+    _, k, v = make_case(n, rows, heads, slots, dh, seed=21)
+    g = torch.Generator(device="cpu").manual_seed(22)
+    qkv = (torch.randn(n, 3 * heads * dh, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
+    q, kn, vn = (t.reshape(n, heads, dh) for t in qkv.chunk(3, -1))
+    assert not q.is_contiguous()
+    row_ids = torch.from_numpy(np.random.default_rng(23).permutation(rows)[:n]).to(DEV)
+    pos = torch.from_numpy(np.random.default_rng(24).integers(0, slots, n)).to(DEV)
+    k1, v1, k2, v2 = k.clone(), v.clone(), k.clone(), v.clone()
+    a = decode_attention_append(q, kn, vn, k1, v1, pos, rows=row_ids)
+    b = decode_attention_append(q.contiguous(), kn.contiguous(), vn.contiguous(), k2, v2, pos,
+                                rows=row_ids)
+    assert torch.equal(a, b) and torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert torch.equal(decode_attention(q, k1, v1, pos, rows=row_ids),
+                       decode_attention(q.contiguous(), k1, v1, pos, rows=row_ids))
+
+
 def test_reference_shape_against_matmul_path(ext):
     """The reference's cache: [2 x 4,096 rows, 8 heads, 50 slots, 32] bf16, 4,096 queries
     on distinct random rows, ragged pos in [0, 49]."""

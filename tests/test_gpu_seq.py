@@ -130,6 +130,34 @@ def test_token_argument_errors(ext):
     assert out.shape == (0, 256)
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 512),
+                                     (torch.bfloat16, 64)])
+def test_add_layernorm_matches_torch(ext, dtype, d):
+    """x + y rounded as torch's add, then nn.LayerNorm of it (and of x alone)."""
+    announce(f"add_layernorm {dtype} d={d}")
+    g = torch.Generator(device="cpu").manual_seed(d)
+    n = 3001
+    x = (torch.randn(n, d, generator=g) * 2.0 + 0.5).to(dtype).to(DEV)
+    y = torch.randn(n, d, generator=g).to(dtype).to(DEV)
+    norm = torch.nn.LayerNorm(d).to(DEV).to(dtype)
+    with torch.no_grad():
+        norm.weight.copy_((torch.randn(d, generator=g) * 0.3 + 1.0).to(dtype))
+        norm.bias.copy_((torch.randn(d, generator=g) * 0.1).to(dtype))
+        xs, ln = ext.add_layernorm(x, y, norm.weight, norm.bias, norm.eps)
+        assert torch.equal(xs, x + y)
+        want = norm(x + y)
+        x0, ln0 = ext.add_layernorm(x, None, norm.weight, norm.bias, norm.eps)
+        assert x0.data_ptr() == x.data_ptr()
+        want0 = norm(x)
+    for got, ref in ((ln, want), (ln0, want0)):
+        if dtype == torch.float32:
+            assert float((got - ref).abs().max()) <= 1e-4
+        else:
+            assert rel_err(got, ref) <= 1e-2
+            same = float((got.view(torch.int16) == ref.view(torch.int16)).float().mean())
+            assert same >= 0.98, same
+
+
 def test_gumbel_sample_matches_reference(ext):
     announce("gumbel_sample")
     g = torch.Generator(device=DEV).manual_seed(3)
