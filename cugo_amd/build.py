@@ -71,7 +71,7 @@ def build_library() -> Path:
     generate_stop_bits()
     out = PKG / "libcugo_hip.so"
     _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "kernels.hip"), str(CSRC / "decode.hip"),
-          str(CSRC / "tokens.hip"),
+          str(CSRC / "selfplay.hip"),
           "-o", str(out)])
     return out
 

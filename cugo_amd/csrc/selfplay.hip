@@ -16,10 +16,13 @@
 //   r2 = round(r1 + position[p])                     (bf16 add)
 //   out = round(r2 + token_type[t])                  (bf16 add)
 // One 64-lane wavefront per row; the row's words are wave-uniform, so the walk over its
-// set bits is scalar and every lane owns columns lane, lane + 64, ... of the output.
+// set bits is scalar, and lane l owns the d / 64 consecutive output columns from
+// l d / 64 (one wide load per weight row).
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
+
+#include <initializer_list>
 
 #include "../../include/cugo_hip.h"
 
@@ -57,6 +60,28 @@ struct F32 {
 
 __device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// K consecutive elements as one (K * element size)-byte access: every row of d = 64 K
+// elements starts 64 K-element aligned, and lane l owns columns l K .. l K + K - 1.
+template <class S, int K>
+struct alignas(sizeof(S) * K) Vec {
+  S v[K];
+};
+
+template <class T, int K>
+__device__ inline void load_row(const typename T::storage* p, float (&f)[K]) {
+  const auto vec = *reinterpret_cast<const Vec<typename T::storage, K>*>(p);
+#pragma unroll
+  for (int k = 0; k < K; ++k) f[k] = T::to_float(vec.v[k]);
+}
+
+template <class T, int K>
+__device__ inline void store_row(typename T::storage* p, const float (&f)[K]) {
+  Vec<typename T::storage, K> vec;
+#pragma unroll
+  for (int k = 0; k < K; ++k) vec.v[k] = T::from_float(f[k]);
+  *reinterpret_cast<Vec<typename T::storage, K>*>(p) = vec;
+}
+
 // acc[k] += W[row j] at this lane's columns, for every set bit j of `bits` (offset `base`).
 template <class T, int K>
 __device__ inline void add_bits(float (&acc)[K], u64 bits, int base,
@@ -64,31 +89,36 @@ __device__ inline void add_bits(float (&acc)[K], u64 bits, int base,
   while (bits != 0) {
     const int j = base + __builtin_ctzll(bits);
     bits &= bits - 1ull;
-    const typename T::storage* w = wt + (i64)j * d + lane;
+    float w[K];
+    load_row<T, K>(wt + (i64)j * d + lane * K, w);
 #pragma unroll
-    for (int k = 0; k < K; ++k) acc[k] += T::to_float(w[64 * k]);
+    for (int k = 0; k < K; ++k) acc[k] += w[k];
   }
 }
 
 template <class T, int K>
 __device__ inline void add_scaled(float (&acc)[K], float x, int j,
                                   const typename T::storage* wt, int d, int lane) {
-  const typename T::storage* w = wt + (i64)j * d + lane;
+  float w[K];
+  load_row<T, K>(wt + (i64)j * d + lane * K, w);
 #pragma unroll
-  for (int k = 0; k < K; ++k) acc[k] += x * T::to_float(w[64 * k]);
+  for (int k = 0; k < K; ++k) acc[k] += x * w[k];
 }
 
 template <class T, int K>
 __device__ inline void finish(float (&acc)[K], const typename T::storage* position,
                               const typename T::storage* token_type,
                               typename T::storage* out, int d, int lane) {
+  float p[K], t[K], o[K];
+  load_row<T, K>(position + lane * K, p);
+  load_row<T, K>(token_type + lane * K, t);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const int c = lane + 64 * k;
     const float r1 = T::round(acc[k]);
-    const float r2 = T::round(r1 + T::to_float(position[c]));
-    out[c] = T::from_float(r2 + T::to_float(token_type[c]));
+    const float r2 = T::round(r1 + p[k]);
+    o[k] = r2 + t[k];
   }
+  store_row<T, K>(out + lane * K, o);
 }
 
 // SeqNet.event_token(words, seat, index) (cugo_seq50.py:276-282) with encode_events
@@ -98,22 +128,22 @@ __device__ inline void finish(float (&acc)[K], const typename T::storage* positi
 // the "me" bit and the opponent's hidden draw count; position row 1 + min(index, 47).
 template <class T, int K>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void event_tokens_kernel(
-    const i64* words, const i64* seat, const i64* index, i64 n,
+    const i64* words, i64 word_rows, const i64* seat, const i64* index, i64 n,
     const typename T::storage* wt, const typename T::storage* bias,
     const typename T::storage* position, i64 position_rows,
     const typename T::storage* token_type, int d, typename T::storage* out) {
   const int lane = threadIdx.x & 63;
   const i64 r = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
   if (r >= n) return;
-  const i64* ev = words + r * 9;
+  const i64 wr = r % word_rows;  // one event read for every seat that observes it
+  const i64* ev = words + wr * 9;
   const u64 header = (u64)ev[8];
   const i64 s = seat[r];
   const bool me = (i64)(header & 0xFFu) == s;
   const bool first = s == 0;
   const int kind = (int)((header >> 8) & 0xFFu);
   float acc[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) acc[k] = T::to_float(bias[lane + 64 * k]);
+  load_row<T, K>(bias + lane * K, acc);
   const u64 w3 = (u64)ev[3], w4 = (u64)ev[4], w5 = (u64)ev[5], w6 = (u64)ev[6];
   add_bits<T>(acc, (u64)ev[0] & kCardMask, 0, wt, d, lane);
   if (me) add_bits<T>(acc, (u64)ev[1] & kCardMask, 50, wt, d, lane);
@@ -130,7 +160,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void event_tokens_kernel(
     const int drawn = __builtin_popcountll((u64)ev[1] & kCardMask);
     if (drawn != 0) add_scaled<T>(acc, (float)drawn, 413, wt, d, lane);
   }
-  i64 p = index[r];
+  i64 p = index[wr];
   p = 1 + (p < kMaxEvents - 1 ? p : kMaxEvents - 1);
   if (p < 0) p = 0;
   if (p >= position_rows) p = position_rows - 1;
@@ -155,8 +185,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void start_tokens_kernel(
   const bool first = s == 0;
   const u64 header = (u64)st[7];
   float acc[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) acc[k] = T::to_float(bias[lane + 64 * k]);
+  load_row<T, K>(bias + lane * K, acc);
   const u64 s0 = (u64)st[0], s1 = (u64)st[1], s3 = (u64)st[3], s4 = (u64)st[4];
   add_bits<T>(acc, (first ? s0 : s1) & kCardMask, 0, wt, d, lane);
   add_bits<T>(acc, (u64)st[2] & kCardMask, 50, wt, d, lane);
@@ -183,19 +212,21 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void start_tokens_kernel(
 // wavefront: masked = legal ? logit : -1e30; action = argmax(masked - log(-log(clamp(u,
 // 1e-20, 1)))) with the first index on ties (torch.argmax); logp = log_softmax(masked)
 // at the action, computed as (masked[a] - max) - log(sum exp(masked - max)).
+// Logits of type T (bf16 logits convert to fp32 exactly, as the reference's `.float()`).
+template <class T>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
-    const float* logits, const uint8_t* legal, const float* u, i64 n, int actions_count,
-    i64* actions, float* logp) {
+    const typename T::storage* logits, const uint8_t* legal, const float* u, i64 n,
+    int actions_count, i64* actions, float* logp) {
   const int lane = threadIdx.x & 63;
   const i64 r = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
   if (r >= n) return;
-  const float* lr = logits + r * actions_count;
+  const typename T::storage* lr = logits + r * actions_count;
   const uint8_t* gr = legal + r * actions_count;
   const float* ur = u + r * actions_count;
   float best = -INFINITY, top = -INFINITY;
   int best_a = actions_count;  // above every real index
   for (int a = lane; a < actions_count; a += 64) {
-    const float m = gr[a] ? lr[a] : -1.0e30f;
+    const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
     const float uc = fminf(fmaxf(ur[a], 1.0e-20f), 1.0f);
     const float v = m + -logf(-logf(uc));
     if (v > best) { best = v; best_a = a; }
@@ -209,23 +240,119 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
   }
   float sum = 0.0f;
   for (int a = lane; a < actions_count; a += 64) {
-    const float m = gr[a] ? lr[a] : -1.0e30f;
+    const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
     sum += expf(m - top);
   }
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   if (lane == 0) {
     const int a = best_a < actions_count ? best_a : 0;
-    const float m = gr[a] ? lr[a] : -1.0e30f;
+    const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
     actions[r] = a;
     logp[r] = (m - top) - logf(sum);
+  }
+}
+
+// ------------------------------------------------------------ step bookkeeping ----
+// WaveCollector._step (cugo_seq_selfplay50.py:108-163, no opponent pool) around the
+// policy: what it does with torch ops between observe and the query, and after the engine
+// step, as two kernels.
+
+constexpr int kFeatures = 720;
+constexpr int kActions = 179;
+constexpr int kStopPointsColumn = 471;  // cugo_contract50.py:31
+constexpr int kRowWords = 31;           // 248-byte state row
+
+// Before the policy (:110-140): bad += active & (status != OK | no legal action); the
+// query input row [bf16(features), legal as 0/1] of the policy dtype; the records of step
+// step_index (features as bf16, legal, opponent hand = hands word 1 - player of the row,
+// stock, stop points = round(exp2(12 f[471]) - 1) (cugo_contract50.py:40-42), seat,
+// count, valid = active); and the mover's cache row (player & 1) * w + game.
+// One wavefront per game.
+template <class T>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
+    CugoSelfPlayWave wave, const u64* states, const float* features, const uint8_t* legal,
+    const uint8_t* player, const uint8_t* done, const int16_t* status, const i64* stock,
+    typename T::storage* q_in, i64* query_rows) {
+  const int lane = threadIdx.x & 63;
+  const i64 i = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
+  const i64 w = wave.w;
+  if (i >= w) return;
+  const i64 step = wave.step_index[0];
+  const bool record = step >= 0 && step < wave.max_steps;
+  const i64 rec = step * w + i;
+  const float* f = features + i * kFeatures;
+  typename T::storage* q = q_in + i * (kFeatures + kActions);
+  for (int j = lane; j < kFeatures; j += 64) {
+    const float x = f[j];
+    q[j] = T::from_float(x);
+    if (record) wave.rec_features[rec * kFeatures + j] = BF16::from_float(x);
+  }
+  const uint8_t* g = legal + i * kActions;
+  bool any = false;
+  for (int j = lane; j < kActions; j += 64) {
+    const uint8_t b = g[j] != 0;
+    any |= b;
+    q[kFeatures + j] = T::from_float(b ? 1.0f : 0.0f);
+    if (record) wave.rec_legal[rec * kActions + j] = b;
+  }
+  any = __ballot(any) != 0;
+  if (lane != 0) return;
+  const bool active = done[i] == 0;
+  if (active && (status[i] != 0 || !any)) atomicAdd(wave.bad, 1ull);
+  const i64 p = (i64)player[i];
+  query_rows[i] = (p & 1) * w + i;
+  if (!record) return;
+  wave.rec_seat[rec] = p;
+  wave.rec_count[rec] = wave.count[i];
+  wave.rec_opp_hand[rec] = (i64)states[i * kRowWords + (1 - p)];
+  wave.rec_stock[rec] = stock[i];
+  wave.rec_stop_points[rec] = (i64)rintf(exp2f(12.0f * f[kStopPointsColumn]) - 1.0f);
+  wave.rec_valid[rec] = active;
+}
+
+// After the engine step (:146-163): bad += active & (step status != OK); a game that
+// finished now keeps its reward and nagari flag and is marked finished; a committed
+// action's event goes to slot min(count, 47) of the log, and both seats' cache lengths
+// and the count advance; the step's action and log-probability are recorded.  One thread
+// per game; call after the event tokens were appended (they use the old count).
+__global__ __launch_bounds__(256) void advance_kernel(
+    CugoSelfPlayWave wave, const uint8_t* done, const float* reward0, const uint8_t* new_done,
+    const uint8_t* nagari, const int16_t* step_status, const uint8_t* committed,
+    const i64* events, const i64* actions, const float* logp) {
+  const i64 w = wave.w;
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in = i < w;
+  const bool active = in && done[i] == 0;
+  const u64 bad = __ballot(active && step_status[i] != 0);
+  if ((threadIdx.x & 63) == 0 && bad != 0)
+    atomicAdd(wave.bad, (unsigned long long)__popcll(bad));
+  if (!in) return;
+  if (active && new_done[i]) {
+    wave.final_reward0[i] = reward0[i];
+    if (nagari[i]) wave.final_nagari[i] = 1;
+    wave.finished[i] = 1;
+  }
+  const i64 c = wave.count[i];
+  if (active && committed[i]) {
+    const i64 slot = c < kMaxEvents - 1 ? c : kMaxEvents - 1;
+    i64* log = wave.events + (i * kMaxEvents + slot) * 9;
+    for (int k = 0; k < 9; ++k) log[k] = events[i * 9 + k];
+    wave.cache_length[i] += 1;
+    wave.cache_length[w + i] += 1;
+    wave.count[i] = c + 1;
+  }
+  const i64 step = wave.step_index[0];
+  if (step >= 0 && step < wave.max_steps) {
+    wave.rec_actions[step * w + i] = actions[i];
+    wave.rec_logp[step * w + i] = logp[i];
   }
 }
 
 // Pre-norm transformer residual step (nn.TransformerEncoderLayer with norm_first,
 // python/cugo_seq50.py:318-322): x_out = x + y rounded to the dtype (y == nullptr: x_out is
 // not written and x is normalised as is), then ln = LayerNorm(x_out) with fp32 mean and
-// variance over the row, rounded to the dtype.  One wavefront per row, K = d / 64 columns
-// per lane.
+// variance over the row, rounded to the dtype.  One wavefront per row, K = d / 64
+// consecutive columns per lane.
 template <class T, int K>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
     const typename T::storage* x, const typename T::storage* y, const typename T::storage* w,
@@ -234,19 +361,19 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
   const int lane = threadIdx.x & 63;
   const i64 r = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
   if (r >= n) return;
+  const i64 at = r * d + lane * K;
   float v[K];
+  load_row<T, K>(x + at, v);
+  if (y != nullptr) {
+    float u[K];
+    load_row<T, K>(y + at, u);
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = T::round(v[k] + u[k]);
+    store_row<T, K>(x_out + at, v);
+  }
   float sum = 0.0f;
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const i64 at = r * d + lane + 64 * k;
-    float t = T::to_float(x[at]);
-    if (y != nullptr) {
-      t = T::round(t + T::to_float(y[at]));
-      x_out[at] = T::from_float(t);
-    }
-    v[k] = t;
-    sum += t;
-  }
+  for (int k = 0; k < K; ++k) sum += v[k];
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   const float mean = sum / (float)d;
   float sq = 0.0f;
@@ -257,11 +384,12 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
   }
   for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
   const float rstd = 1.0f / sqrtf(sq / (float)d + eps);
+  float wv[K], bv[K], o[K];
+  load_row<T, K>(w + lane * K, wv);
+  load_row<T, K>(b + lane * K, bv);
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int c = lane + 64 * k;
-    ln[r * d + c] = T::from_float((v[k] - mean) * rstd * T::to_float(w[c]) + T::to_float(b[c]));
-  }
+  for (int k = 0; k < K; ++k) o[k] = (v[k] - mean) * rstd * wv[k] + bv[k];
+  store_row<T, K>(ln + at, o);
 }
 
 template <class T>
@@ -288,7 +416,8 @@ int launch_add_layernorm(const void* x, const void* y, const void* w, const void
 }
 
 template <class T>
-int launch_event(const i64* words, const i64* seat, const i64* index, i64 n, const void* wt,
+int launch_event(const i64* words, i64 word_rows, const i64* seat, const i64* index, i64 n,
+                 const void* wt,
                  const void* bias, const void* position, i64 position_rows,
                  const void* token_type, int d, void* out, hipStream_t stream) {
   using S = typename T::storage;
@@ -296,7 +425,7 @@ int launch_event(const i64* words, const i64* seat, const i64* index, i64 n, con
 #define CUGO_EVENT_CASE(KK)                                                                 \
   case KK:                                                                                  \
     event_tokens_kernel<T, KK><<<grid, 64 * kRowsPerBlock, 0, stream>>>(                    \
-        words, seat, index, n, (const S*)wt, (const S*)bias, (const S*)position,            \
+        words, word_rows, seat, index, n, (const S*)wt, (const S*)bias, (const S*)position, \
         position_rows, (const S*)token_type, d, (S*)out);                                   \
     break;
   switch (d / 64) {
@@ -341,6 +470,14 @@ bool valid_width(int64_t d) {
   return d == 64 || d == 128 || d == 256 || d == 512 || d == 1024;
 }
 
+// Every row pointer must allow the (d / 64)-element accesses of load_row / store_row.
+bool aligned_rows(int dtype, int64_t d, std::initializer_list<const void*> ptrs) {
+  const uintptr_t bytes = (uintptr_t)(d / 64) * (dtype == CUGO_DTYPE_F32 ? 4u : 2u);
+  for (const void* p : ptrs)
+    if (p != nullptr && (reinterpret_cast<uintptr_t>(p) % bytes) != 0) return false;
+  return true;
+}
+
 }  // namespace tokens
 }  // namespace cugo_amd
 
@@ -348,22 +485,23 @@ using namespace cugo_amd::tokens;
 
 extern "C" {
 
-int cugo_event_tokens(int dtype, const int64_t* words, const int64_t* seat,
+int cugo_event_tokens(int dtype, const int64_t* words, int64_t word_rows, const int64_t* seat,
                       const int64_t* index, int64_t n, const void* weight_t, const void* bias,
                       const void* position, int64_t position_rows, const void* token_type,
                       int64_t d, void* out, hipStream_t stream) {
-  if (n < 0 || position_rows < 1 ||
+  if (n < 0 || position_rows < 1 || (n > 0 && (word_rows < 1 || n % word_rows != 0)) ||
       (n > 0 && (!words || !seat || !index || !weight_t || !bias || !position ||
                  !token_type || !out)))
     return -1;
   if (!valid_width(d)) return -3;
+  if (!aligned_rows(dtype, d, {weight_t, bias, position, token_type, out})) return -4;
   if (n == 0) return 0;
   if (dtype == CUGO_DTYPE_BF16)
-    return launch_event<BF16>(words, seat, index, n, weight_t, bias, position, position_rows,
-                              token_type, (int)d, out, stream);
+    return launch_event<BF16>(words, word_rows, seat, index, n, weight_t, bias, position,
+                              position_rows, token_type, (int)d, out, stream);
   if (dtype == CUGO_DTYPE_F32)
-    return launch_event<F32>(words, seat, index, n, weight_t, bias, position, position_rows,
-                             token_type, (int)d, out, stream);
+    return launch_event<F32>(words, word_rows, seat, index, n, weight_t, bias, position,
+                             position_rows, token_type, (int)d, out, stream);
   return -2;
 }
 
@@ -374,6 +512,7 @@ int cugo_start_tokens(int dtype, const int64_t* start, const int64_t* seat, int6
       (n > 0 && (!start || !seat || !weight_t || !bias || !position || !token_type || !out)))
     return -1;
   if (!valid_width(d)) return -3;
+  if (!aligned_rows(dtype, d, {weight_t, bias, position, token_type, out})) return -4;
   if (n == 0) return 0;
   if (dtype == CUGO_DTYPE_BF16)
     return launch_start<BF16>(start, seat, n, weight_t, bias, position, token_type, (int)d,
@@ -389,6 +528,7 @@ int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weig
                        hipStream_t stream) {
   if (n < 0 || (n > 0 && (!x || !weight || !bias || !ln || (y && !x_out)))) return -1;
   if (!valid_width(d)) return -3;
+  if (!aligned_rows(dtype, d, {x, y, weight, bias, x_out, ln})) return -4;
   if (n == 0) return 0;
   if (dtype == CUGO_DTYPE_BF16)
     return launch_add_layernorm<BF16>(x, y, weight, bias, eps, n, (int)d, x_out, ln, stream);
@@ -397,16 +537,68 @@ int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weig
   return -2;
 }
 
-int cugo_gumbel_sample(const float* logits, const uint8_t* legal, const float* uniforms,
-                       int64_t n, int64_t actions_count, int64_t* actions, float* logp,
-                       hipStream_t stream) {
+int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* legal,
+                       const float* uniforms, int64_t n, int64_t actions_count, int64_t* actions,
+                       float* logp, hipStream_t stream) {
   if (n < 0 || actions_count < 1 || actions_count > (1 << 20) ||
       (n > 0 && (!logits || !legal || !uniforms || !actions || !logp)))
     return -1;
   if (n == 0) return 0;
   const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
-  gumbel_kernel<<<grid, 64 * kRowsPerBlock, 0, stream>>>(logits, legal, uniforms, n,
-                                                         (int)actions_count, actions, logp);
+  if (logits_dtype == CUGO_DTYPE_F32)
+    gumbel_kernel<F32><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
+        (const float*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
+  else if (logits_dtype == CUGO_DTYPE_BF16)
+    gumbel_kernel<BF16><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
+        (const uint16_t*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
+  else
+    return -2;
+  return (int)hipGetLastError();
+}
+
+int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8_t* states,
+                          const float* features, const uint8_t* legal, const uint8_t* player,
+                          const uint8_t* done, const int16_t* status, const int64_t* stock,
+                          void* q_in, int64_t* query_rows, hipStream_t stream) {
+  if (!wave || wave->w < 0 || wave->max_steps < 0) return -1;
+  const int64_t w = wave->w;
+  if (w > 0 && (!states || !features || !legal || !player || !done || !status || !stock ||
+                !q_in || !query_rows || !wave->step_index || !wave->count || !wave->bad ||
+                !wave->rec_features || !wave->rec_legal || !wave->rec_opp_hand ||
+                !wave->rec_stock || !wave->rec_stop_points || !wave->rec_seat ||
+                !wave->rec_count || !wave->rec_valid))
+    return -1;
+  if (w == 0) return 0;
+  const unsigned grid = (unsigned)((w + kRowsPerBlock - 1) / kRowsPerBlock);
+  if (q_dtype == CUGO_DTYPE_BF16)
+    prepare_kernel<BF16><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
+        *wave, reinterpret_cast<const u64*>(states), features, legal, player, done, status,
+        stock, (uint16_t*)q_in, query_rows);
+  else if (q_dtype == CUGO_DTYPE_F32)
+    prepare_kernel<F32><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
+        *wave, reinterpret_cast<const u64*>(states), features, legal, player, done, status,
+        stock, (float*)q_in, query_rows);
+  else
+    return -2;
+  return (int)hipGetLastError();
+}
+
+int cugo_selfplay_advance(const CugoSelfPlayWave* wave, const uint8_t* done,
+                          const float* reward0, const uint8_t* new_done, const uint8_t* nagari,
+                          const int16_t* step_status, const uint8_t* committed,
+                          const int64_t* events, const int64_t* actions, const float* logp,
+                          hipStream_t stream) {
+  if (!wave || wave->w < 0 || wave->max_steps < 0) return -1;
+  const int64_t w = wave->w;
+  if (w > 0 && (!done || !reward0 || !new_done || !nagari || !step_status || !committed ||
+                !events || !actions || !logp || !wave->step_index || !wave->count ||
+                !wave->events || !wave->cache_length || !wave->final_reward0 ||
+                !wave->final_nagari || !wave->finished || !wave->bad || !wave->rec_actions ||
+                !wave->rec_logp))
+    return -1;
+  if (w == 0) return 0;
+  advance_kernel<<<(unsigned)((w + 255) / 256), 256, 0, stream>>>(
+      *wave, done, reward0, new_done, nagari, step_status, committed, events, actions, logp);
   return (int)hipGetLastError();
 }
 

@@ -524,16 +524,20 @@ torch::Tensor event_tokens(torch::Tensor words, torch::Tensor seat, torch::Tenso
   TORCH_CHECK(words.is_cuda() && words.is_contiguous() && words.dim() == 2 &&
                   words.size(1) == CUGO_EVENT_WORDS && words.scalar_type() == at::kLong,
               "words must be a contiguous CUDA int64 [n, EVENT_WORDS] tensor");
-  const int64_t n = words.size(0);
+  // seat names the rows; words and index may hold each event once for several seats
+  const int64_t word_rows = words.size(0);
   check_1d(seat, at::kLong, "seat");
   check_1d(index, at::kLong, "index");
-  TORCH_CHECK(seat.numel() == n && index.numel() == n, "seat and index must have n entries");
+  const int64_t n = seat.numel();
+  TORCH_CHECK(index.numel() == word_rows, "index must have one entry per event row");
+  TORCH_CHECK(n == 0 || (word_rows > 0 && n % word_rows == 0),
+              "the number of seats must be a multiple of the number of events");
   check_same_device(words, seat, "words", "seat");
   check_same_device(words, index, "words", "index");
   check_token_weights(weight_t, bias, position, token_type, 8 * 50 + 12 + 2, words);
   const DeviceGuard guard(words.device());
   auto out = torch::empty({n, weight_t.size(1)}, on(words, weight_t.scalar_type()));
-  check_call(cugo_event_tokens(token_dtype(weight_t), words.data_ptr<int64_t>(),
+  check_call(cugo_event_tokens(token_dtype(weight_t), words.data_ptr<int64_t>(), word_rows,
                                seat.data_ptr<int64_t>(), index.data_ptr<int64_t>(), n,
                                weight_t.data_ptr(), bias.data_ptr(), position.data_ptr(),
                                position.size(0), token_type.data_ptr(), weight_t.size(1),
@@ -605,8 +609,8 @@ std::vector<torch::Tensor> add_layernorm(torch::Tensor x, c10::optional<torch::T
 std::vector<torch::Tensor> gumbel_sample(torch::Tensor logits, torch::Tensor legal,
                                          torch::Tensor uniforms) {
   TORCH_CHECK(logits.is_cuda() && logits.is_contiguous() && logits.dim() == 2 &&
-                  logits.scalar_type() == at::kFloat,
-              "logits must be a contiguous CUDA float32 [n, A] tensor");
+                  (logits.scalar_type() == at::kFloat || logits.scalar_type() == at::kBFloat16),
+              "logits must be a contiguous CUDA float32 or bfloat16 [n, A] tensor");
   TORCH_CHECK(legal.is_contiguous() && legal.sizes() == logits.sizes() &&
                   legal.scalar_type() == at::kBool,
               "legal must be a contiguous bool tensor shaped like logits");
@@ -619,12 +623,146 @@ std::vector<torch::Tensor> gumbel_sample(torch::Tensor logits, torch::Tensor leg
   const int64_t n = logits.size(0);
   auto actions = torch::empty({n}, on(logits, at::kLong));
   auto logp = torch::empty({n}, on(logits, at::kFloat));
-  check_call(cugo_gumbel_sample(logits.data_ptr<float>(), u8p(legal), uniforms.data_ptr<float>(),
+  check_call(cugo_gumbel_sample(logits.scalar_type() == at::kFloat ? CUGO_DTYPE_F32 : CUGO_DTYPE_BF16,
+                                logits.data_ptr(), u8p(legal), uniforms.data_ptr<float>(),
                                 n, logits.size(1), actions.data_ptr<int64_t>(),
                                 logp.data_ptr<float>(), stream()),
              "gumbel_sample");
   return {actions, logp};
 }
+
+// The tensors of one self-play wave, held for the wave's life, and the step's two
+// bookkeeping launches (cugo_selfplay_prepare / _advance).
+class SelfPlayState {
+ public:
+  SelfPlayState(int64_t w, int64_t max_steps, torch::Tensor step_index, torch::Tensor count,
+                torch::Tensor events, torch::Tensor cache_length, torch::Tensor final_reward0,
+                torch::Tensor final_nagari, torch::Tensor finished, torch::Tensor bad,
+                torch::Tensor rec_features, torch::Tensor rec_legal, torch::Tensor rec_logp,
+                torch::Tensor rec_actions, torch::Tensor rec_opp_hand, torch::Tensor rec_stock,
+                torch::Tensor rec_stop_points, torch::Tensor rec_seat, torch::Tensor rec_count,
+                torch::Tensor rec_valid)
+      : keep_{step_index, count, events, cache_length, final_reward0, final_nagari, finished,
+              bad, rec_features, rec_legal, rec_logp, rec_actions, rec_opp_hand, rec_stock,
+              rec_stop_points, rec_seat, rec_count, rec_valid} {
+    TORCH_CHECK(w >= 0 && max_steps >= 0, "w and max_steps must be non-negative");
+    const auto dev = count.device();
+    for (const auto& t : keep_)
+      TORCH_CHECK(t.is_cuda() && t.device() == dev && t.is_contiguous(),
+                  "self-play tensors must be contiguous and on one CUDA device");
+    auto want = [](const torch::Tensor& t, at::ScalarType type, std::vector<int64_t> shape,
+                   const char* name) {
+      TORCH_CHECK(t.scalar_type() == type && t.sizes().vec() == shape, name,
+                  " has the wrong dtype or shape");
+    };
+    const int64_t s = max_steps;
+    want(step_index, at::kLong, {1}, "step_index");
+    want(count, at::kLong, {w}, "count");
+    want(events, at::kLong, {w, 48, CUGO_EVENT_WORDS}, "events");
+    want(cache_length, at::kLong, {2 * w}, "cache length");
+    want(final_reward0, at::kFloat, {w}, "final_reward0");
+    want(final_nagari, at::kBool, {w}, "final_nagari");
+    want(finished, at::kBool, {w}, "finished");
+    TORCH_CHECK(bad.scalar_type() == at::kLong && bad.numel() == 1, "bad must be one int64");
+    want(rec_features, at::kBFloat16, {s, w, CUGO_FEATURE_COUNT}, "rec_features");
+    want(rec_legal, at::kBool, {s, w, CUGO_ACTION_COUNT}, "rec_legal");
+    want(rec_logp, at::kFloat, {s, w}, "rec_logp");
+    want(rec_valid, at::kBool, {s, w}, "rec_valid");
+    for (const auto* t : {&rec_actions, &rec_opp_hand, &rec_stock, &rec_stop_points, &rec_seat,
+                          &rec_count})
+      want(*t, at::kLong, {s, w}, "a recorded int64 field");
+    auto l = [](const torch::Tensor& t) { return t.data_ptr<int64_t>(); };
+    c_ = CugoSelfPlayWave{w,
+                          max_steps,
+                          l(step_index),
+                          l(count),
+                          l(events),
+                          l(cache_length),
+                          final_reward0.data_ptr<float>(),
+                          u8p(final_nagari),
+                          u8p(finished),
+                          reinterpret_cast<unsigned long long*>(bad.data_ptr()),
+                          reinterpret_cast<uint16_t*>(rec_features.data_ptr()),
+                          u8p(rec_legal),
+                          rec_logp.data_ptr<float>(),
+                          l(rec_actions),
+                          l(rec_opp_hand),
+                          l(rec_stock),
+                          l(rec_stop_points),
+                          l(rec_seat),
+                          l(rec_count),
+                          u8p(rec_valid)};
+  }
+
+  // -> (q_in [w, 899] of q_dtype, query_rows int64 [w])
+  std::vector<torch::Tensor> prepare(torch::Tensor states, torch::Tensor features,
+                                     torch::Tensor legal, torch::Tensor player,
+                                     torch::Tensor done, torch::Tensor status,
+                                     torch::Tensor stock, at::ScalarType q_dtype) {
+    const int64_t w = c_.w;
+    check_states(states);
+    TORCH_CHECK(states.size(0) == w, "states must hold the wave's w rows");
+    TORCH_CHECK(features.is_contiguous() && features.scalar_type() == at::kFloat &&
+                    features.sizes() == torch::IntArrayRef({w, CUGO_FEATURE_COUNT}),
+                "features must be float32 [w, FEATURE_COUNT]");
+    TORCH_CHECK(legal.is_contiguous() && legal.scalar_type() == at::kBool &&
+                    legal.sizes() == torch::IntArrayRef({w, CUGO_ACTION_COUNT}),
+                "legal must be bool [w, ACTION_COUNT]");
+    TORCH_CHECK(player.numel() == w && done.numel() == w && status.numel() == w &&
+                    stock.numel() == w && player.scalar_type() == at::kByte &&
+                    done.scalar_type() == at::kBool && status.scalar_type() == at::kShort &&
+                    stock.scalar_type() == at::kLong,
+                "player/done/status/stock must be observe's and stock_indexed's [w] outputs");
+    TORCH_CHECK(q_dtype == at::kBFloat16 || q_dtype == at::kFloat,
+                "the query dtype must be bfloat16 or float32");
+    for (const auto* t : {&states, &features, &legal, &player, &done, &status, &stock})
+      TORCH_CHECK(t->device() == keep_[0].device(), "inputs must be on the wave's device");
+    const DeviceGuard guard(states.device());
+    auto q_in = torch::empty({w, CUGO_FEATURE_COUNT + CUGO_ACTION_COUNT}, on(states, q_dtype));
+    auto rows = torch::empty({w}, on(states, at::kLong));
+    check_call(cugo_selfplay_prepare(&c_, q_dtype == at::kBFloat16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32,
+                                     u8p(states), features.data_ptr<float>(), u8p(legal),
+                                     u8p(player), u8p(done), status.data_ptr<int16_t>(),
+                                     stock.data_ptr<int64_t>(), q_in.data_ptr(),
+                                     rows.data_ptr<int64_t>(), stream()),
+               "selfplay_prepare");
+    return {q_in, rows};
+  }
+
+  void advance(torch::Tensor done, torch::Tensor reward0, torch::Tensor new_done,
+               torch::Tensor nagari, torch::Tensor step_status, torch::Tensor committed,
+               torch::Tensor events, torch::Tensor actions, torch::Tensor logp) {
+    const int64_t w = c_.w;
+    TORCH_CHECK(done.numel() == w && reward0.numel() == w && new_done.numel() == w &&
+                    nagari.numel() == w && step_status.numel() == w && committed.numel() == w &&
+                    actions.numel() == w && logp.numel() == w,
+                "step outputs must have one entry per game");
+    TORCH_CHECK(done.scalar_type() == at::kBool && reward0.scalar_type() == at::kFloat &&
+                    new_done.scalar_type() == at::kBool && nagari.scalar_type() == at::kBool &&
+                    step_status.scalar_type() == at::kShort &&
+                    committed.scalar_type() == at::kBool && actions.scalar_type() == at::kLong &&
+                    logp.scalar_type() == at::kFloat,
+                "step outputs have the wrong dtypes");
+    TORCH_CHECK(events.is_contiguous() && events.scalar_type() == at::kLong &&
+                    events.sizes() == torch::IntArrayRef({w, CUGO_EVENT_WORDS}),
+                "events must be int64 [w, EVENT_WORDS]");
+    for (const auto* t : {&done, &reward0, &new_done, &nagari, &step_status, &committed,
+                          &actions, &logp})
+      TORCH_CHECK(t->is_contiguous() && t->device() == keep_[0].device(),
+                  "step outputs must be contiguous on the wave's device");
+    const DeviceGuard guard(done.device());
+    check_call(cugo_selfplay_advance(&c_, u8p(done), reward0.data_ptr<float>(), u8p(new_done),
+                                     u8p(nagari), step_status.data_ptr<int16_t>(),
+                                     u8p(committed), events.data_ptr<int64_t>(),
+                                     actions.data_ptr<int64_t>(), logp.data_ptr<float>(),
+                                     stream()),
+               "selfplay_advance");
+  }
+
+ private:
+  std::vector<torch::Tensor> keep_;
+  CugoSelfPlayWave c_{};
+};
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Cugo Shin Matgo batch environment on gfx950 (HIP)";
@@ -666,6 +804,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("add_layernorm", &add_layernorm, "x + y and LayerNorm(x + y) in one launch",
         pybind11::arg("x"), pybind11::arg("y"), pybind11::arg("weight"), pybind11::arg("bias"),
         pybind11::arg("eps"));
+  pybind11::class_<SelfPlayState>(m, "SelfPlayState",
+                                   "A self-play wave's tensors and its step bookkeeping")
+      .def(pybind11::init<int64_t, int64_t, torch::Tensor, torch::Tensor, torch::Tensor,
+                          torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor,
+                          torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor,
+                          torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor,
+                          torch::Tensor, torch::Tensor, torch::Tensor>())
+      .def("prepare", &SelfPlayState::prepare)
+      .def("advance", &SelfPlayState::advance);
   m.def("gumbel_sample", &gumbel_sample, "Masked Gumbel-max action and its log-softmax probability");
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),

@@ -106,7 +106,8 @@ class SeqPolicy(nn.Module):
     def event_token(self, words: torch.Tensor, seat: torch.Tensor,
                     index: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:276-282: event_in(encode_events) + position[1 + min(index, 47)]
-        + token_type[1]."""
+        + token_type[1].  Row r reads words[r % len(words)] and index[r % len(words)], so one
+        copy of the events serves every seat that observes them."""
         return self.ext().event_tokens(words.contiguous(), seat.contiguous(), index.contiguous(),
                                        self._weight_t("event_in"), self.event_in.bias.detach(),
                                        self.position.detach(), self.token_type.detach())
@@ -114,7 +115,11 @@ class SeqPolicy(nn.Module):
     def query_token(self, features: torch.Tensor, legal: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:166-180 (hybrid): query_in(features ++ legal) + token_type[2]."""
         dt = self.event_in.weight.dtype
-        return self.query_in(torch.cat((features.to(dt), legal.to(dt)), -1)) + self.token_type[2]
+        return self.query_from_input(torch.cat((features.to(dt), legal.to(dt)), -1))
+
+    def query_from_input(self, q_in: torch.Tensor) -> torch.Tensor:
+        """query_token on the already concatenated input [n, 720 + 179]."""
+        return self.query_in(q_in) + self.token_type[2]
 
     def readout(self, h: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:187-189 and :288-289."""
@@ -169,6 +174,12 @@ class SelfPlayWave:
         self.started = torch.zeros(w, dtype=torch.bool, device=device)
         self.bad = torch.zeros((), dtype=torch.int64, device=device)
         self.ok = int(ext.STATUS_OK)
+        self.native = ext.SelfPlayState(
+            w, s, self.step_index, self.count, self.events, self.cache.length,
+            self.final_reward0, self.final_nagari, self.finished, self.bad, self.rec_features,
+            self.rec_legal, self.rec_logp, self.rec_long["actions"], self.rec_long["opp_hand"],
+            self.rec_long["stock"], self.rec_long["stop_points"], self.rec_long["seat"],
+            self.rec_long["count"], self.rec_valid)
         # Sampling noise: None draws torch.rand_like inside the step (the reference's
         # choice); a tensor [wave, ACTIONS] is read instead (set by a caller that draws
         # its own uniforms before each step).
@@ -199,48 +210,25 @@ class SelfPlayWave:
 
     @torch.no_grad()
     def step(self) -> None:
-        """One decision of every game (cugo_seq_selfplay50.py:108-163, no pool)."""
-        w, ids, actor, ext = self.w, self.ids, self.actor, self.ext
+        """One decision of every game (cugo_seq_selfplay50.py:108-163, no pool).  The torch
+        bookkeeping around the policy runs as two kernels (`SelfPlayState.prepare` before
+        the query, `.advance` after the event tokens)."""
+        ids, actor, ext = self.ids, self.actor, self.ext
         features, legal, players, done, status = ext.observe_indexed(self.states, ids)
-        active = ~done
-        self.bad += (active & ((status != self.ok) | ~legal.any(1))).sum()
-        player = players.long()
-        hidden = actor.cached_step(self.cache, actor.query_token(features, legal),
-                                   rows=(player & 1) * w + ids)
-        logits = actor.readout(hidden).float()
-        self.logits = logits  # the last step's logits (kept for inspection)
-        uniforms = torch.rand_like(logits) if self.noise is None else self.noise
-        actions, logp = ext.gumbel_sample(logits, legal, uniforms)
-
-        hands = ext.hands_indexed(self.states, ids)
         stock = ext.stock_indexed(self.states, ids)
-        at = self.step_index
-        self.rec_features.index_copy_(0, at, features.to(torch.bfloat16).unsqueeze(0))
-        self.rec_legal.index_copy_(0, at, legal.unsqueeze(0))
-        self.rec_logp.index_copy_(0, at, logp.unsqueeze(0))
-        for name, value in (("actions", actions), ("seat", player), ("count", self.count),
-                            ("opp_hand", hands.gather(1, (1 - player).unsqueeze(1)).squeeze(1)),
-                            ("stock", stock), ("stop_points", stop_points(features))):
-            self.rec_long[name].index_copy_(0, at, value.unsqueeze(0))
-        # every move is the learner's here: no opponent pool
-        self.rec_valid.index_copy_(0, at, active.unsqueeze(0))
-
+        q_in, query_rows = self.native.prepare(self.states, features, legal, players, done,
+                                               status, stock, actor.event_in.weight.dtype)
+        hidden = actor.cached_step(self.cache, actor.query_from_input(q_in), rows=query_rows)
+        logits = actor.readout(hidden)  # the kernel reads bf16 logits as the fp32 .float()
+        self.logits = logits  # the last step's logits (kept for inspection)
+        uniforms = (torch.rand(logits.shape, dtype=torch.float32, device=logits.device)
+                    if self.noise is None else self.noise)
+        actions, logp = ext.gumbel_sample(logits.contiguous(), legal, uniforms)
         reward0, new_done, nagari, step_status, committed, events = ext.step_events_indexed(
             self.states, ids, actions)
-        self.bad += (active & (step_status != self.ok)).sum()
-        finished_now = active & new_done
-        self.final_reward0.copy_(torch.where(finished_now, reward0, self.final_reward0))
-        self.final_nagari |= finished_now & nagari
-        self.finished |= finished_now
-
-        commit = active & committed
-        slot = self.count.clamp_max(MAX_EVENTS - 1)
-        self.events.index_put_((ids, slot),
-                               torch.where(commit.unsqueeze(1), events, self.events[ids, slot]))
-        actor.cached_step(self.cache, actor.event_token(events.repeat(2, 1), self.seats2,
-                                                        self.count.repeat(2)))
-        self.cache.length += commit.repeat(2).long()
-        self.count += commit.long()
+        actor.cached_step(self.cache, actor.event_token(events, self.seats2, self.count))
+        self.native.advance(done, reward0, new_done, nagari, step_status, committed, events,
+                            actions, logp)
         self.step_index += 1
 
     @torch.no_grad()

@@ -198,13 +198,18 @@ int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, int64
  * {64, 128, 256, 512, 1024}.  weight_t is the Linear weight transposed ([in, d],
  * contiguous), bias [d], position [position_rows, d], token_type [3, d].
  *
- * cugo_event_tokens: out[i] = SeqNet.event_token(words[i], seat[i], index[i])
- *   (cugo_seq50.py:276-282 with encode_events :91-110): event_in applied to the 414-wide
- *   observer-relative token of the 9-word event, + position[1 + min(index, 47)] +
- *   token_type[1], with the reference's bf16 roundings (after the Linear, after each add).
- *   words int64 [n, 9], seat/index int64 [n], weight_t [414, d], out [n, d].
+ * Row pointers (weights, bias, position, token_type, x, y, outputs) must be aligned to
+ * (d / 64) elements (a torch allocation is); -4 otherwise.
+ *
+ * cugo_event_tokens: out[r] = SeqNet.event_token(words[j], seat[r], index[j]) with
+ *   j = r % word_rows (cugo_seq50.py:276-282 with encode_events :91-110): event_in applied
+ *   to the 414-wide observer-relative token of the 9-word event, + position[1 + min(index,
+ *   47)] + token_type[1], with the reference's bf16 roundings (after the Linear, after
+ *   each add).  words int64 [word_rows, 9] and index int64 [word_rows] (word_rows divides
+ *   n: the self-play step passes each event once for both seats), seat int64 [n],
+ *   weight_t [414, d], out [n, d].
  */
-int cugo_event_tokens(int dtype, const int64_t* words, const int64_t* seat,
+int cugo_event_tokens(int dtype, const int64_t* words, int64_t word_rows, const int64_t* seat,
                       const int64_t* index, int64_t n, const void* weight_t, const void* bias,
                       const void* position, int64_t position_rows, const void* token_type,
                       int64_t d, void* out, hipStream_t stream);
@@ -225,10 +230,60 @@ int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weig
 /* cugo_gumbel_sample: the sampling of WaveCollector._step (cugo_seq_selfplay50.py:125-130)
  * given the uniforms torch.rand_like drew: masked = legal ? logits : -1e30;
  * actions[i] = argmax_a(masked - log(-log(clamp(u, 1e-20, 1)))) (first index on ties);
- * logp[i] = log_softmax(masked)[actions[i]].  logits/uniforms f32 [n, A], legal bool [n, A]. */
-int cugo_gumbel_sample(const float* logits, const uint8_t* legal, const float* uniforms,
-                       int64_t n, int64_t actions_count, int64_t* actions, float* logp,
-                       hipStream_t stream);
+ * logp[i] = log_softmax(masked)[actions[i]].  logits [n, A] of logits_dtype (F32 or BF16,
+ * which converts exactly), uniforms f32 [n, A], legal bool [n, A]. */
+int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* legal,
+                       const float* uniforms, int64_t n, int64_t actions_count, int64_t* actions,
+                       float* logp, hipStream_t stream);
+
+/* The tensors of one self-play wave (WaveCollector, cugo_seq_selfplay50.py:45-76), w games,
+ * max_steps recorded steps; every pointer is device memory. */
+typedef struct CugoSelfPlayWave {
+  int64_t w, max_steps;
+  const int64_t* step_index;      /* [1]: the step being recorded */
+  int64_t* count;                 /* [w]: events committed so far */
+  int64_t* events;                /* [w, 48, 9]: event log */
+  int64_t* cache_length;          /* [2 w]: KV-cache lengths, row = seat * w + game */
+  float* final_reward0;           /* [w] */
+  uint8_t* final_nagari;          /* [w] bool */
+  uint8_t* finished;              /* [w] bool */
+  unsigned long long* bad;        /* [1] int64: bad observe/step results */
+  uint16_t* rec_features;         /* [max_steps, w, 720] bf16 */
+  uint8_t* rec_legal;             /* [max_steps, w, 179] bool */
+  float* rec_logp;                /* [max_steps, w] */
+  int64_t* rec_actions;           /* [max_steps, w], and likewise: */
+  int64_t* rec_opp_hand;
+  int64_t* rec_stock;
+  int64_t* rec_stop_points;
+  int64_t* rec_seat;
+  int64_t* rec_count;
+  uint8_t* rec_valid;             /* [max_steps, w] bool */
+} CugoSelfPlayWave;
+
+/* cugo_selfplay_prepare: the step's work between observe and the policy
+ * (cugo_seq_selfplay50.py:110-140, no pool): bad += active & (status != OK or no legal
+ * action); q_in [w, 899] of q_dtype = (features, legal as 0/1), the policy's query input;
+ * records of step step_index (skipped outside [0, max_steps)): features as bf16, legal,
+ * opponent hand (hands word 1 - player of the state row), stock, stop points
+ * (round(exp2(12 f[471]) - 1), cugo_contract50.py:40-42), seat, count, valid = active;
+ * query_rows [w] = (player & 1) * w + game.  states [w, 248] (row = game), features
+ * f32 [w, 720], legal bool [w, 179], player/done [w], status i16 [w] (observe outputs),
+ * stock int64 [w] (stock_indexed before the step). */
+int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8_t* states,
+                          const float* features, const uint8_t* legal, const uint8_t* player,
+                          const uint8_t* done, const int16_t* status, const int64_t* stock,
+                          void* q_in, int64_t* query_rows, hipStream_t stream);
+/* cugo_selfplay_advance: the step's work after the engine step (cugo_seq_selfplay50.py:
+ * 146-163): bad += active & (step status != OK); games that finished now keep reward0 and
+ * the nagari flag and are marked finished; a committed event goes to slot min(count, 47)
+ * of the log and advances both seats' cache lengths and the count; actions and logp are
+ * recorded at step step_index.  done = observe's done before the step; the others are
+ * step_events_indexed's outputs.  Call after the event tokens were appended. */
+int cugo_selfplay_advance(const CugoSelfPlayWave* wave, const uint8_t* done,
+                          const float* reward0, const uint8_t* new_done, const uint8_t* nagari,
+                          const int16_t* step_status, const uint8_t* committed,
+                          const int64_t* events, const int64_t* actions, const float* logp,
+                          hipStream_t stream);
 
 #ifdef __cplusplus
 }

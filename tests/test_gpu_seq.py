@@ -96,6 +96,13 @@ def test_event_tokens_against_oracle(ext, dtype, d):
         p = (1 + index.clamp(max=47)).clamp(min=0)
         want = token_reference(tok, w, b, pos[p], tt[1].expand(n, d))
         check_tokens(got, want, dtype)
+    # each event read once for both seats (rows r and r + n share event r)
+    seats2 = torch.cat((torch.zeros(n, dtype=torch.int64, device=DEV),
+                        torch.ones(n, dtype=torch.int64, device=DEV)))
+    wt = w.t().contiguous()
+    got2 = ext.event_tokens(words, seats2, index, wt, b, pos, tt)
+    want2 = ext.event_tokens(words.repeat(2, 1), seats2, index.repeat(2), wt, b, pos, tt)
+    assert torch.equal(got2, want2)
 
 
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 128)])
@@ -176,6 +183,12 @@ def test_gumbel_sample_matches_reference(ext):
     assert torch.equal(actions, want_a)
     assert int(actions[11]) == 17
     assert float((logp - want_lp).abs().max()) <= 1e-5
+    # bf16 logits read as the reference's .float()
+    lb = logits.to(torch.bfloat16)
+    actions, logp = ext.gumbel_sample(lb, legal, u)
+    want_a, want_lp = gumbel_reference(lb.float(), legal, u)
+    assert torch.equal(actions, want_a)
+    assert float((logp - want_lp).abs().max()) <= 1e-5
 
 
 def _policy(d=256, layers=4, heads=8, seed=0):
@@ -192,23 +205,45 @@ def _policy(d=256, layers=4, heads=8, seed=0):
 def _reference_step(policy, ref, actions_from=None):
     """One WaveCollector step (cugo_seq_selfplay50.py:108-163, no pool) in the reference
     formulation: dense tokens from the oracle, index_put_ + matmul attention, the torch
-    sampling lines.  `ref` holds the reference copy's tensors; with actions_from the
-    engine is stepped with those actions (teacher forcing) after sampling its own."""
+    sampling and bookkeeping lines.  `ref` holds the reference copy's tensors; with
+    actions_from the engine is stepped with those actions (teacher forcing) after
+    sampling its own.  Returns (sampled actions, their logp, logits)."""
     ext, w, ids = ref["ext"], ref["w"], ref["ids"]
     features, legal, players, done, status = ext.observe_indexed(ref["states"], ids)
     active = ~done
+    ref["bad"] += (active & ((status != 0) | ~legal.any(1))).sum()
     player = players.long()
     q = policy.query_token(features, legal)
     hidden = reference_cached_step(policy, ref["cache"], q, (player & 1) * w + ids)
     logits = policy.readout(hidden).float()
     actions, logp = gumbel_reference(logits, legal, ref["noise"])
     used = actions if actions_from is None else actions_from
-    _, new_done, _, _, committed, events = ext.step_events_indexed(ref["states"], ids, used)
+    hands = ext.hands_indexed(ref["states"], ids)
+    stock = ext.stock_indexed(ref["states"], ids)
+    stop = torch.round(torch.exp2(12.0 * features[:, 471].float()) - 1.0).long()
+    rec = ref["rec"]
+    rec["features"].append(features.to(torch.bfloat16))
+    rec["legal"].append(legal)
+    rec["seat"].append(player)
+    rec["count"].append(ref["count"].clone())
+    rec["opp_hand"].append(hands.gather(1, (1 - player).unsqueeze(1)).squeeze(1))
+    rec["stock"].append(stock)
+    rec["stop_points"].append(stop)
+    rec["valid"].append(active)
+    reward0, new_done, nagari, step_status, committed, events = ext.step_events_indexed(
+        ref["states"], ids, used)
+    ref["bad"] += (active & (step_status != 0)).sum()
+    finished_now = active & new_done
+    ref["final_reward0"].copy_(torch.where(finished_now, reward0, ref["final_reward0"]))
+    ref["final_nagari"] |= finished_now & nagari
+    ref["finished"] |= finished_now
     commit = active & committed
+    slot = ref["count"].clamp_max(47)
+    ref["events"].index_put_((ids, slot),
+                             torch.where(commit.unsqueeze(1), events, ref["events"][ids, slot]))
     seats2 = torch.cat((torch.zeros(w, dtype=torch.int64, device=DEV),
                         torch.ones(w, dtype=torch.int64, device=DEV)))
-    ev2 = events.repeat(2, 1).cpu().numpy()
-    tok = encode_events_np(ev2, seats2.cpu().numpy())
+    tok = encode_events_np(events.repeat(2, 1).cpu().numpy(), seats2.cpu().numpy())
     index = ref["count"].repeat(2)
     p = 1 + index.clamp(max=47)
     x = token_reference(tok, policy.event_in.weight, policy.event_in.bias, policy.position[p],
@@ -216,15 +251,16 @@ def _reference_step(policy, ref, actions_from=None):
     reference_cached_step(policy, ref["cache"], x, torch.arange(2 * w, device=DEV))
     ref["cache"].length += commit.repeat(2).long()
     ref["count"] += commit.long()
-    return actions, logp, logits, features
+    return actions, logp, logits
 
 
 def test_selfplay_step_matches_reference_formulation(ext):
     """The captured self-play step against the reference formulation for a wave of 256
     games: identical engine trajectories (the reference copy replays the wave's actions),
-    logits within 1e-2 relative, the same sampled action for at least 99 % of the decisions,
-    the same engine states, counts and recorded features, and caches whose first layer
-    agrees within 1e-2 (deeper layers within 5e-2)."""
+    logits within 1e-2 relative, the same sampled action for at least 99 % of the
+    decisions, identical records (features, mask, seat, count, opponent hand, stock, stop
+    points, valid), event logs, counts, cache lengths, finished flags, final rewards and
+    bad counts, and caches whose first layer agrees within 1e-2 (deeper layers 2e-2)."""
     announce("selfplay step vs reference formulation")
     from cugo_amd.seq_selfplay import SelfPlayWave, make_seeds, policy_cache
 
@@ -233,14 +269,22 @@ def test_selfplay_step_matches_reference_formulation(ext):
     wave = SelfPlayWave(ext, policy, w, max_steps=64)
     wave.noise = torch.zeros((w, 179), device=DEV)
     g = torch.Generator(device=DEV).manual_seed(11)
+    names = ("features", "legal", "seat", "count", "opp_hand", "stock", "stop_points", "valid")
     with torch.no_grad():
         wave.capture()
         seeds, first = make_seeds(w, 12345, DEV)
         learner = torch.zeros(w, dtype=torch.int64, device=DEV)
         wave.reset(seeds, first, learner)
-        ref = {"ext": ext, "w": w, "ids": torch.arange(w, device=DEV),
-               "states": ext.create(seeds, first), "cache": policy_cache(policy, 2 * w, DEV),
-               "count": torch.zeros(w, dtype=torch.int64, device=DEV), "noise": wave.noise}
+        states = ext.create(seeds, first)
+        ref = {"ext": ext, "w": w, "ids": torch.arange(w, device=DEV), "states": states,
+               "cache": policy_cache(policy, 2 * w, DEV),
+               "count": torch.zeros(w, dtype=torch.int64, device=DEV), "noise": wave.noise,
+               "bad": torch.zeros((), dtype=torch.int64, device=DEV),
+               "events": torch.zeros((w, 48, 9), dtype=torch.int64, device=DEV),
+               "final_reward0": torch.zeros(w, device=DEV),
+               "final_nagari": torch.zeros(w, dtype=torch.bool, device=DEV),
+               "finished": ext.observe_indexed(states, torch.arange(w, device=DEV))[3].clone(),
+               "rec": {k: [] for k in names}}
         start = ext.start(ref["states"])
         seats2 = torch.cat((torch.zeros(w, dtype=torch.int64, device=DEV),
                             torch.ones(w, dtype=torch.int64, device=DEV)))
@@ -251,24 +295,38 @@ def test_selfplay_step_matches_reference_formulation(ext):
         reference_cached_step(policy, ref["cache"], x0, torch.arange(2 * w, device=DEV))
         ref["cache"].length.fill_(1)
         agree = total = 0
-        for step in range(30):
+        steps = 0
+        for step in range(40):
             wave.noise.copy_(torch.rand((w, 179), generator=g, device=DEV))
             wave.graph.replay()
+            steps += 1
             actions = wave.rec_long["actions"][step]
-            a_ref, lp_ref, logits_ref, feats = _reference_step(policy, ref, actions_from=actions)
+            a_ref, lp_ref, logits_ref = _reference_step(policy, ref, actions_from=actions)
             assert rel_err(wave.logits, logits_ref) <= 1e-2, step
             same = actions == a_ref
             agree += int(same.sum())
             total += w
             lp = wave.rec_logp[step]
             assert float((lp - lp_ref)[same].abs().max()) <= 5e-2, step
-            assert torch.equal(wave.rec_features[step], feats.to(torch.bfloat16)), step
             assert torch.equal(wave.states, ref["states"]), step
             assert torch.equal(wave.count, ref["count"]), step
             assert torch.equal(wave.cache.length, ref["cache"].length), step
+            assert torch.equal(wave.events, ref["events"]), step
+            assert torch.equal(wave.finished, ref["finished"]), step
+            assert torch.equal(wave.final_nagari, ref["final_nagari"]), step
+            assert torch.equal(wave.final_reward0, ref["final_reward0"]), step
+            assert int(wave.bad) == int(ref["bad"]), step
+            assert int(wave.step_index) == steps
             if bool(wave.finished.all()):
                 break
         assert agree >= 0.99 * total, (agree, total)
+        recs = {"features": wave.rec_features, "legal": wave.rec_legal,
+                "seat": wave.rec_long["seat"], "count": wave.rec_long["count"],
+                "opp_hand": wave.rec_long["opp_hand"], "stock": wave.rec_long["stock"],
+                "stop_points": wave.rec_long["stop_points"], "valid": wave.rec_valid}
+        for name in names:
+            want = torch.stack(ref["rec"][name])
+            assert torch.equal(recs[name][:steps], want), name
         # Live slots only (below each row's length): slots past it still hold keys of
         # the games played while capturing, which no query reads.  Layer 0's keys come
         # from the tokens alone; deeper layers also carry the reference's bf16 rounding
