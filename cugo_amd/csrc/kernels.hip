@@ -579,6 +579,47 @@ __global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u
   }
 }
 
+// ---------------------------------------------------------------- redeal ----
+// _redeal (python/cugo_ppo50.py:122-148) on rows in place, given its random draws: the
+// observer's opponent gets a new unrevealed hand from the cards the observer cannot see
+// (the opponent's free cards and the stock), the rest becomes the stock, held follows the
+// new hand and the row's RNG word is replaced.  keys [n, 50] are the uniforms the
+// reference draws with torch.rand; the new free cards are the `count` unknown cards with
+// the smallest keys (ties to the lower card id: the reference's argsort leaves tie order
+// open).  One wavefront per row, lane j = card j.
+constexpr int kWordHand0 = 0, kWordHand1 = 1, kWordStock = 3, kWordRng = 6;
+constexpr int kWordHeld0 = 20, kWordHeld1 = 21, kWordRev0 = 22, kWordRev1 = 23;
+
+__global__ __launch_bounds__(256) void redeal_kernel(u64* states, const i64* seat,
+                                                     const float* keys, const i64* rng, i64 n) {
+  const int lane = threadIdx.x & 63;
+  const i64 r = (i64)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (r >= n) return;
+  u64* w = states + r * kRowWords;
+  const bool s0 = seat[r] == 0;
+  const u64 hand = s0 ? w[kWordHand1] : w[kWordHand0];
+  const u64 fixed = hand & (s0 ? w[kWordRev1] : w[kWordRev0]);  // shown by a shake
+  const u64 held = s0 ? w[kWordHeld1] : w[kWordHeld0];
+  const u64 free_cards = hand & ~fixed;
+  const u64 unknown = free_cards | w[kWordStock];
+  const u32 count = popc(free_cards);
+  const bool mine = lane < 50 && ((unknown >> lane) & 1ull);
+  const float key = mine ? keys[r * 50 + lane] : 2.0f;
+  u32 rank = 0;
+  for (int k = 0; k < 50; ++k) {
+    const float other = __shfl(key, k);
+    rank += (other < key || (other == key && k < lane)) ? 1u : 0u;
+  }
+  const u64 new_free = __ballot(mine && rank < count);
+  if (lane != 0) return;
+  const u64 new_hand = fixed | new_free;
+  const u64 new_held = (held & ~hand) | new_hand;
+  w[kWordStock] = unknown & ~new_free;
+  w[s0 ? kWordHand1 : kWordHand0] = new_hand;
+  w[s0 ? kWordHeld1 : kWordHeld0] = new_held;
+  w[kWordRng] = (u64)rng[r];
+}
+
 __global__ __launch_bounds__(256) void seed_kernel(i64 n, u64 base_seed, const u32* generation,
                                                    u64* sampler) {
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
@@ -824,6 +865,15 @@ int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint
   reset_spare_kernel<<<tiles(n), kTile, 0, stream>>>(
       reinterpret_cast<u64*>(states), done, n, base_seed, (u64)seed_stride, generation, sampler,
       completed, reinterpret_cast<const u64*>(spares), spare_gen);
+  return launched();
+}
+
+int cugo_redeal(uint8_t* states, const int64_t* seat, const float* keys, const int64_t* rng,
+                int64_t n, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!states || !seat || !keys || !rng))) return kBadArgument;
+  if (n == 0) return 0;
+  redeal_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(reinterpret_cast<u64*>(states), seat,
+                                                            keys, rng, n);
   return launched();
 }
 

@@ -213,6 +213,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void start_tokens_kernel(
 // 1e-20, 1)))) with the first index on ties (torch.argmax); logp = log_softmax(masked)
 // at the action, computed as (masked[a] - max) - log(sum exp(masked - max)).
 // Logits of type T (bf16 logits convert to fp32 exactly, as the reference's `.float()`).
+// u == nullptr: no noise, the greedy masked argmax (cugo_eval50.py:125-127).
 template <class T>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
     const typename T::storage* logits, const uint8_t* legal, const float* u, i64 n,
@@ -222,13 +223,16 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
   if (r >= n) return;
   const typename T::storage* lr = logits + r * actions_count;
   const uint8_t* gr = legal + r * actions_count;
-  const float* ur = u + r * actions_count;
+  const float* ur = u != nullptr ? u + r * actions_count : nullptr;
   float best = -INFINITY, top = -INFINITY;
   int best_a = actions_count;  // above every real index
   for (int a = lane; a < actions_count; a += 64) {
     const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
-    const float uc = fminf(fmaxf(ur[a], 1.0e-20f), 1.0f);
-    const float v = m + -logf(-logf(uc));
+    float v = m;
+    if (ur != nullptr) {
+      const float uc = fminf(fmaxf(ur[a], 1.0e-20f), 1.0f);
+      v = m + -logf(-logf(uc));
+    }
     if (v > best) { best = v; best_a = a; }
     top = fmaxf(top, m);
   }
@@ -239,16 +243,18 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
     top = fmaxf(top, __shfl_xor(top, off));
   }
   float sum = 0.0f;
-  for (int a = lane; a < actions_count; a += 64) {
-    const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
-    sum += expf(m - top);
+  if (logp != nullptr) {
+    for (int a = lane; a < actions_count; a += 64) {
+      const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
+      sum += expf(m - top);
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   }
-  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   if (lane == 0) {
     const int a = best_a < actions_count ? best_a : 0;
     const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
     actions[r] = a;
-    logp[r] = (m - top) - logf(sum);
+    if (logp != nullptr) logp[r] = (m - top) - logf(sum);
   }
 }
 
@@ -541,7 +547,7 @@ int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* lega
                        const float* uniforms, int64_t n, int64_t actions_count, int64_t* actions,
                        float* logp, hipStream_t stream) {
   if (n < 0 || actions_count < 1 || actions_count > (1 << 20) ||
-      (n > 0 && (!logits || !legal || !uniforms || !actions || !logp)))
+      (n > 0 && (!logits || !legal || !actions)))
     return -1;
   if (n == 0) return 0;
   const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);

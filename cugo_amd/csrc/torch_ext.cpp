@@ -366,6 +366,25 @@ std::vector<torch::Tensor> step_reset_spares(torch::Tensor states, torch::Tensor
   return o;
 }
 
+// redeal(states, seat, keys, rng): in place (python/cugo_ppo50.py:122-148 given its draws).
+void redeal(torch::Tensor states, torch::Tensor seat, torch::Tensor keys, torch::Tensor rng) {
+  check_states(states);
+  const int64_t n = states.size(0);
+  check_1d(seat, at::kLong, "seat");
+  check_1d(rng, at::kLong, "rng");
+  TORCH_CHECK(keys.is_cuda() && keys.is_contiguous() && keys.scalar_type() == at::kFloat &&
+                  keys.dim() == 2 && keys.size(0) == n && keys.size(1) == 50,
+              "keys must be a contiguous CUDA float32 [n, 50] tensor");
+  TORCH_CHECK(seat.numel() == n && rng.numel() == n, "seat and rng must have one entry per row");
+  check_same_device(states, seat, "states", "seat");
+  check_same_device(states, keys, "states", "keys");
+  check_same_device(states, rng, "states", "rng");
+  const DeviceGuard guard(states.device());
+  check_call(cugo_redeal(u8p(states), seat.data_ptr<int64_t>(), keys.data_ptr<float>(),
+                         rng.data_ptr<int64_t>(), n, stream()),
+             "redeal");
+}
+
 torch::Tensor seed_samplers(int64_t n, int64_t base_seed, torch::Tensor generation) {
   check_1d(generation, at::kInt, "generation");
   TORCH_CHECK(generation.numel() == n, "generation must have n entries");
@@ -603,6 +622,25 @@ std::vector<torch::Tensor> add_layernorm(torch::Tensor x, c10::optional<torch::T
   return {x_out, ln};
 }
 
+// masked_argmax(logits [n, A] f32/bf16, legal bool [n, A]) -> int64 [n]: the greedy
+// action of python/cugo_eval50.py:125-127 (argmax of logits.float() masked with -1e30).
+torch::Tensor masked_argmax(torch::Tensor logits, torch::Tensor legal) {
+  TORCH_CHECK(logits.is_cuda() && logits.is_contiguous() && logits.dim() == 2 &&
+                  (logits.scalar_type() == at::kFloat || logits.scalar_type() == at::kBFloat16),
+              "logits must be a contiguous CUDA float32 or bfloat16 [n, A] tensor");
+  TORCH_CHECK(legal.is_contiguous() && legal.sizes() == logits.sizes() &&
+                  legal.scalar_type() == at::kBool,
+              "legal must be a contiguous bool tensor shaped like logits");
+  check_same_device(logits, legal, "logits", "legal");
+  const DeviceGuard guard(logits.device());
+  auto actions = torch::empty({logits.size(0)}, on(logits, at::kLong));
+  check_call(cugo_gumbel_sample(logits.scalar_type() == at::kFloat ? CUGO_DTYPE_F32 : CUGO_DTYPE_BF16,
+                                logits.data_ptr(), u8p(legal), nullptr, logits.size(0),
+                                logits.size(1), actions.data_ptr<int64_t>(), nullptr, stream()),
+             "masked_argmax");
+  return actions;
+}
+
 // gumbel_sample(logits f32 [n, A], legal bool [n, A], uniforms f32 [n, A]) -> (actions
 // int64 [n], logp f32 [n]): the sampling of WaveCollector._step
 // (python/cugo_seq_selfplay50.py:125-130) with the uniforms supplied.
@@ -786,6 +824,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("generation"), pybind11::arg("sampler"),
         pybind11::arg("completed") = pybind11::none());
   m.def("seed_samplers", &seed_samplers, "Per-row sampler state from the row seeds");
+  m.def("redeal", &redeal, "Redeal the observer's opponent hand and the stock, in place");
   m.def("refill_spares", &refill_spares, "Pre-deal the next game of rows with a stale spare",
         pybind11::arg("spares"), pybind11::arg("spare_gen"), pybind11::arg("generation"),
         pybind11::arg("base_seed"), pybind11::arg("seed_stride") = -1);
@@ -813,6 +852,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                           torch::Tensor, torch::Tensor, torch::Tensor>())
       .def("prepare", &SelfPlayState::prepare)
       .def("advance", &SelfPlayState::advance);
+  m.def("masked_argmax", &masked_argmax, "Greedy action: argmax of the legal logits");
   m.def("gumbel_sample", &gumbel_sample, "Masked Gumbel-max action and its log-softmax probability");
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),

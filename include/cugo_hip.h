@@ -142,6 +142,14 @@ int cugo_step_reset_spares(uint8_t* states, const int64_t* actions, int64_t n, f
                            uint64_t base_seed, int64_t seed_stride, uint32_t* generation,
                            uint64_t* sampler, const uint8_t* spares, const uint32_t* spare_gen,
                            hipStream_t stream);
+/* redeal (python/cugo_ppo50.py:122-148, `_redeal`) in place on rows [n, CUGO_STATE_BYTES]
+ * for observer seat[i], given the reference's random draws: keys f32 [n, 50]
+ * (torch.rand(n, 50)) rank the unknown cards (the opponent's cards not shown by a shake,
+ * and the stock); the opponent's new free cards are the `count` unknown cards with the
+ * smallest keys, ties to the lower card id; the rest is the stock; held follows the new
+ * hand; the RNG word becomes rng[i] (torch.randint(-2**62, 2**62, (n,))). */
+int cugo_redeal(uint8_t* states, const int64_t* seat, const float* keys, const int64_t* rng,
+                int64_t n, hipStream_t stream);
 /* sampler[i] = SplitMix64(base_seed + i + batch * generation[i]).next(), never 0. */
 int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation,
                        uint64_t* sampler, hipStream_t stream);
@@ -231,7 +239,9 @@ int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weig
  * given the uniforms torch.rand_like drew: masked = legal ? logits : -1e30;
  * actions[i] = argmax_a(masked - log(-log(clamp(u, 1e-20, 1)))) (first index on ties);
  * logp[i] = log_softmax(masked)[actions[i]].  logits [n, A] of logits_dtype (F32 or BF16,
- * which converts exactly), uniforms f32 [n, A], legal bool [n, A]. */
+ * which converts exactly), uniforms f32 [n, A], legal bool [n, A].  uniforms == NULL
+ * gives the greedy masked argmax of cugo_eval50.py:125-127 (no noise); logp == NULL skips
+ * the log-probability. */
 int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* legal,
                        const float* uniforms, int64_t n, int64_t actions_count, int64_t* actions,
                        float* logp, hipStream_t stream);
