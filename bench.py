@@ -64,6 +64,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-rollout", action="store_true")
     p.add_argument("--no-selfplay", action="store_true")
+    p.add_argument("--no-redeal", action="store_true")
+    p.add_argument("--no-paired", action="store_true")
     p.add_argument("--streams", type=int, default=1,
                    help="slices of the batch stepped on their own streams")
     p.add_argument("--no-graph", action="store_true", help="issue the loop eagerly")
@@ -154,30 +156,36 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     return {"seconds": seconds, "games": games, "observe_ms": observe_ms}
 
 
-def branch_workload(ext, torch, iters: int) -> dict:
-    """4,096 roots from seeded random play of 3-15 decisions; child k of a root takes
-    legal[k] while k < count, then legal[xorshift % count]."""
+def mid_game_roots(ext, torch, n: int, base: int):
+    """n games dealt from seed base + i, each played 3-15 seeded random decisions deep (the
+    depth drawn from the game's own sampler); returns the rows still running and their
+    movers."""
     import numpy as np
 
     dev = torch.device("cuda")
-    roots_n, fan = 4096, 256
-    idx = torch.arange(roots_n, dtype=torch.int64, device=dev)
-    base = SEED_BASE + 0x5EED
+    idx = torch.arange(n, dtype=torch.int64, device=dev)
     roots = ext.create(idx + base, idx & 1)
-    gen = torch.zeros(roots_n, dtype=torch.int32, device=dev)
-    sampler = ext.seed_samplers(roots_n, base, gen)
+    gen = torch.zeros(n, dtype=torch.int32, device=dev)
+    sampler = ext.seed_samplers(n, base, gen)
     depth = 3 + (sampler.cpu().numpy().view(np.uint64) % np.uint64(13)).astype(np.int64)
     depth_t = torch.from_numpy(depth).to(dev)
     for d in range(15):
         _, legal, _, done, _ = ext.observe(roots)
         actions = ext.sample_uniform(legal, sampler)
-        actions = torch.where(depth_t > d, actions, torch.full_like(actions, -1))
         ext.step_indexed(roots, idx[depth_t > d], actions[depth_t > d])
-    # keep live roots (a root may have finished early); refill from live ones
-    _, legal, _, done, status = ext.observe(roots)
+    _, _, player, done, status = ext.observe(roots)
     live = torch.nonzero(~done & (status == 0)).flatten()
-    roots = roots.index_select(0, live).contiguous()
-    legal = legal.index_select(0, live)
+    return roots.index_select(0, live).contiguous(), player.long().index_select(0, live)
+
+
+def branch_workload(ext, torch, iters: int) -> dict:
+    """4,096 roots from seeded random play of 3-15 decisions; child k of a root takes
+    legal[k] while k < count, then legal[xorshift % count]."""
+    dev = torch.device("cuda")
+    roots_n, fan = 4096, 256
+    # live roots only (a root may have finished early); children cycle over them
+    roots, _ = mid_game_roots(ext, torch, roots_n, SEED_BASE + 0x5EED)
+    _, legal, _, _, _ = ext.observe(roots)
     n_live = roots.shape[0]
     parent = (torch.arange(roots_n * fan, device=dev) // fan) % n_live
     k = torch.arange(roots_n * fan, device=dev) % fan
@@ -374,6 +382,83 @@ def selfplay_workload(ext, torch, wave: int = 4096, waves: int = 3) -> dict:
             "wave": wave, "cache": [4, 2 * wave, 8, 50, 32], "dtype": "bf16"}
 
 
+def redeal_workload(ext, torch, rows: int = 4096, worlds: int = 8) -> dict:
+    """Redealt worlds (the reference's redeal_worlds): 4,096 mid-game rows from seeded
+    random play (3-15 decisions deep), 8 worlds each, every world redealt until the
+    observer's features and mask match (8 tries); plus the redeal kernel alone on all
+    32,768 copies."""
+    from cugo_amd.redeal import redeal, redeal_worlds
+
+    dev = torch.device("cuda")
+    roots, players = mid_game_roots(ext, torch, rows, SEED_BASE + 0x5EA1)
+    env_rows = torch.arange(roots.shape[0], device=dev)
+    torch.manual_seed(0)
+    redeal_worlds(ext, roots, env_rows, players, worlds)
+    torch.cuda.synchronize()
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        out = redeal_worlds(ext, roots, env_rows, players, worlds)
+    torch.cuda.synchronize()
+    worlds_s = (time.perf_counter() - t0) / reps
+    copies = roots.repeat(worlds, 1)
+    seats = players.repeat(worlds)
+    keys = torch.rand(copies.shape[0], 50, device=dev)
+    rng = torch.randint(-2**62, 2**62, (copies.shape[0],), device=dev)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ext.redeal(copies, seats, keys, rng)
+    e0.record(stream)
+    for _ in range(20):
+        ext.redeal(copies, seats, keys, rng)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    kernel_ms = e0.elapsed_time(e1) / 20
+    changed = float((out.view(torch.int64)[:, 3] != roots.repeat(worlds, 1).view(torch.int64)[:, 3])
+                    .float().mean())
+    return {"worlds_per_s": round(out.shape[0] / worlds_s, 1),
+            "redeal_worlds_ms": round(worlds_s * 1e3, 3),
+            "redeal_kernel_ms": round(kernel_ms, 4),
+            "redealt_fraction": round(changed, 4), "rows": int(roots.shape[0]), "worlds": worlds}
+
+
+def paired_workload(ext, torch, pairs: int = 4096) -> dict:
+    """Paired evaluation (the reference's evaluate_paired): 4,096 deals played twice with
+    the seats swapped, two 3x512 residual MLP policies (fp32 weights, fp16 autocast, random
+    N(0, 0.02) init), greedy actions; complete games/s."""
+    from torch import nn
+
+    from cugo_amd.paired_eval import evaluate_paired
+
+    dev = torch.device("cuda")
+
+    class Block(nn.Module):
+        def __init__(self, d: int) -> None:
+            super().__init__()
+            self.norm = nn.LayerNorm(d)
+            self.fc1 = nn.Linear(d, d)
+            self.fc2 = nn.Linear(d, d)
+
+        def forward(self, h):
+            return h + self.fc2(torch.relu(self.fc1(self.norm(h))))
+
+    def actor(seed: int) -> nn.Module:
+        torch.manual_seed(seed)
+        m = nn.Sequential(nn.Linear(720, 512), Block(512), Block(512), Block(512),
+                          nn.LayerNorm(512), nn.Linear(512, 179))
+        with torch.no_grad():
+            for prm in m.parameters():
+                prm.normal_(0.0, 0.02)
+        return m.to(dev)
+
+    a, b = actor(1), actor(2)
+    evaluate_paired(ext, a, b, 256, seed_offset=0, max_steps=128, use_amp=True)  # warm
+    s = evaluate_paired(ext, a, b, pairs, seed_offset=1 << 20, max_steps=128, use_amp=True)
+    return {"games_per_s": round(s.games / s.seconds, 1), "seconds": round(s.seconds, 4),
+            "decision_steps": s.decision_steps, "pairs": pairs,
+            "mean_pair_score_a": round(s.mean_pair_score_a, 4)}
+
+
 def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict:
     """MLP PPO self-play rollout: B games, a residual MLP policy (720 features -> Linear 512
     -> 3 blocks of h + Linear(ReLU(Linear(LayerNorm(h)))) -> 179 logits and a value head,
@@ -560,6 +645,10 @@ def main() -> None:
         result["decode"] = decode_workload(ext, torch, args.decode_steps)
     if not args.no_selfplay:
         result["selfplay"] = selfplay_workload(ext, torch)
+    if not args.no_redeal:
+        result["redeal"] = redeal_workload(ext, torch)
+    if not args.no_paired:
+        result["paired"] = paired_workload(ext, torch)
     if not args.no_rollout:
         result["rollout"] = rollout_workload(ext, torch)
     if not args.no_cpu:
