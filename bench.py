@@ -69,6 +69,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--streams", type=int, default=1,
                    help="slices of the batch stepped on their own streams")
     p.add_argument("--no-graph", action="store_true", help="issue the loop eagerly")
+    p.add_argument("--two-launch", action="store_true",
+                   help="observe_sample and step_reset_spares as two launches per step")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
     p.add_argument("--decode-steps", type=int, default=20)
@@ -77,7 +79,7 @@ def parse() -> argparse.Namespace:
 
 
 def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
-                  graph: bool) -> dict:
+                  graph: bool, fused: bool = True) -> dict:
     """The timed loop.  The batch is cut into `streams` contiguous slices (even length),
     each stepped on its own default-priority stream; REFILL steps of every slice form one
     block, captured once as a HIP graph and replayed (or issued eagerly with graph=False).
@@ -110,10 +112,14 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
                 for t in range(nsteps):
                     if t == 0:
                         ext.refill_spares(sp, sg, g, base, batch)
-                    # observe + the random policy's draw from the legal mask, one launch
-                    _, _, _, _, _, actions = ext.observe_sample(st, sm)
-                    # step + auto-reset of the finished rows from their spares, one launch
-                    ext.step_reset_spares(st, actions, base, g, sm, sp, sg, batch)
+                    if fused:
+                        # observe + draw + step + auto-reset in one launch
+                        ext.play_random(st, sm, base, g, sp, sg, batch)
+                    else:
+                        # observe + the random policy's draw from the legal mask, one launch
+                        _, _, _, _, _, actions = ext.observe_sample(st, sm)
+                        # step + auto-reset of the finished rows from their spares
+                        ext.step_reset_spares(st, actions, base, g, sm, sp, sg, batch)
         for s in side:
             cur.wait_stream(s)
 
@@ -609,7 +615,7 @@ def main() -> None:
         torch.cuda.synchronize()
         del src, dst
     rp = random_policy(ext, torch, args.batch, args.steps, args.warmup, args.streams,
-                       not args.no_graph)
+                       not args.no_graph, not args.two_launch)
     games_per_s = rp["games"] / rp["seconds"]
     ms_per_step = 1000.0 * rp["seconds"] / args.steps
     observe_gbs = args.batch * OBSERVE_BYTES_PER_ROW / (rp["observe_ms"] * 1e-3) / 1e9

@@ -109,6 +109,72 @@ __device__ inline u32 spread4(u32 x) {
   return (x & 1u) | ((x & 2u) << 7) | ((x & 4u) << 14) | ((x & 8u) << 21);
 }
 
+// The tile's observation from its LDS records: features (wave w of `waves` storing waves
+// stores rows w, w + waves, ...; lane owns float4 columns q = lane, lane + 64, lane + 128
+// (< 180) of each, so a store instruction covers 1 KiB of one row and each lane resolves
+// its twelve feature sources once) and the legal mask rows as 32-bit words.  Called by
+// the storing waves only (wave in [0, waves)).
+__device__ inline void store_observation(const ObserveTile& t, i64 base, int count,
+                                         float* features, u8* legal, int wave, int waves) {
+  const int lane = threadIdx.x & (kTile - 1);
+  constexpr int kQuads = kFeatureCount / 4;  // 180
+  u32 src[3][4];
+  for (int c = 0; c < 3; ++c)
+    for (int k = 0; k < 4; ++k) {
+      const u32 q = (u32)(lane + kTile * c);
+      src[c][k] = feature_source(q < (u32)kQuads ? q * 4u + (u32)k : 719u);
+    }
+  float4* fout = reinterpret_cast<float4*>(features + base * kFeatureCount);
+  for (int r = wave; r < count; r += waves) {
+    const u32* rec = t.out.rec[r];
+    for (int c = 0; c < 3; ++c) {
+      const int q = lane + kTile * c;
+      if (q < kQuads) {
+        float4 v;
+        v.x = feature_from_record(rec, src[c][0]);
+        v.y = feature_from_record(rec, src[c][1]);
+        v.z = feature_from_record(rec, src[c][2]);
+        v.w = feature_from_record(rec, src[c][3]);
+        fout[r * kQuads + q] = v;
+      }
+    }
+  }
+  // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0); word
+  // w holds tile bytes 4w..4w+3, i.e. actions a..a+3 of row r unless it straddles rows.
+  const int tid = wave * kTile + lane;
+  const int threads = waves * kTile;
+  u8* lout = legal + base * kActionCount;
+  const int bytes = count * kActionCount;
+  const int full = bytes / 4;
+  for (int w = tid; w < full; w += threads) {
+    const int b0 = w * 4;
+    const int r = b0 / kActionCount;
+    const int a = b0 - r * kActionCount;
+    u32 packed;
+    if (a + 3 < kActionCount) {
+      const u64* m = t.out.legal[r];
+      const int lo = a >> 6, sh = a & 63;
+      u64 bits = m[lo] >> sh;
+      if (sh > 60) bits |= m[lo + 1] << (64 - sh);
+      packed = spread4((u32)(bits & 0xFu));
+    } else {
+      packed = 0;
+      for (int b = 0; b < 4; ++b) {
+        const int at = b0 + b;
+        const int rr = at / kActionCount;
+        const int aa = at - rr * kActionCount;
+        packed |= (u32)((t.out.legal[rr][aa >> 6] >> (aa & 63)) & 1u) << (8 * b);
+      }
+    }
+    reinterpret_cast<u32*>(lout)[w] = packed;
+  }
+  for (int at = full * 4 + tid; at < bytes; at += threads) {
+    const int r = at / kActionCount;
+    const int a = at - r * kActionCount;
+    lout[at] = (u8)((t.out.legal[r][a >> 6] >> (a & 63)) & 1u);
+  }
+}
+
 // One tile of 64 games per 192-thread workgroup: wave 0 runs the 64 games (one per
 // lane) and writes their records; then all three waves share the 64 x 3,059 output
 // bytes, so a wave whose games took long to compute does not store its rows alone.
@@ -211,64 +277,7 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
     }
   }
   __syncthreads();
-  // Features: wave w stores rows w, w + 3, ...; lane owns float4 columns q = lane,
-  // lane + 64, lane + 128 (< 180) of each, so a store instruction covers 1 KiB of one
-  // row and each lane resolves its twelve feature sources once.
-  constexpr int kQuads = kFeatureCount / 4;  // 180
-  constexpr int kWaves = kObsThreads / kTile;
-  u32 src[3][4];
-  for (int c = 0; c < 3; ++c)
-    for (int k = 0; k < 4; ++k) {
-      const u32 q = (u32)(lane + kTile * c);
-      src[c][k] = feature_source(q < (u32)kQuads ? q * 4u + (u32)k : 719u);
-    }
-  float4* fout = reinterpret_cast<float4*>(features + base * kFeatureCount);
-  for (int r = wave; r < count; r += kWaves) {
-    const u32* rec = t.out.rec[r];
-    for (int c = 0; c < 3; ++c) {
-      const int q = lane + kTile * c;
-      if (q < kQuads) {
-        float4 v;
-        v.x = feature_from_record(rec, src[c][0]);
-        v.y = feature_from_record(rec, src[c][1]);
-        v.z = feature_from_record(rec, src[c][2]);
-        v.w = feature_from_record(rec, src[c][3]);
-        fout[r * kQuads + q] = v;
-      }
-    }
-  }
-  // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0); word
-  // w holds tile bytes 4w..4w+3, i.e. actions a..a+3 of row r unless it straddles rows.
-  u8* lout = legal + base * kActionCount;
-  const int bytes = count * kActionCount;
-  const int full = bytes / 4;
-  for (int w = tid; w < full; w += kObsThreads) {
-    const int b0 = w * 4;
-    const int r = b0 / kActionCount;
-    const int a = b0 - r * kActionCount;
-    u32 packed;
-    if (a + 3 < kActionCount) {
-      const u64* m = t.out.legal[r];
-      const int lo = a >> 6, sh = a & 63;
-      u64 bits = m[lo] >> sh;
-      if (sh > 60) bits |= m[lo + 1] << (64 - sh);
-      packed = spread4((u32)(bits & 0xFu));
-    } else {
-      packed = 0;
-      for (int b = 0; b < 4; ++b) {
-        const int at = b0 + b;
-        const int rr = at / kActionCount;
-        const int aa = at - rr * kActionCount;
-        packed |= (u32)((t.out.legal[rr][aa >> 6] >> (aa & 63)) & 1u) << (8 * b);
-      }
-    }
-    reinterpret_cast<u32*>(lout)[w] = packed;
-  }
-  for (int at = full * 4 + tid; at < bytes; at += kObsThreads) {
-    const int r = at / kActionCount;
-    const int a = at - r * kActionCount;
-    lout[at] = (u8)((t.out.legal[r][a >> 6] >> (a & 63)) & 1u);
-  }
+  store_observation(t, base, count, features, legal, wave, kObsThreads / kTile);
 }
 
 // --------------------------------------------------------------------- step ----
@@ -382,6 +391,110 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
     i64* eout = events + base * kEventWords;
     for (int j = lane; j < count * kEventWords; j += kStepThreads) eout[j] = ev[j];
   }
+}
+
+// ------------------------------------------------------------ random play ----
+// One random-policy self-play step in one launch: observe_kernel<false, true> (the
+// observation and the uniform legal draw) followed by step_kernel<3> (the step and the
+// auto-reset of finished rows), with the same outputs.  Two waves per tile of 64 games:
+// wave 0 computes the observation records and the actions, then runs the 64 games' steps
+// while wave 1 stores the observation from LDS, so the step's integer work overlaps the
+// HBM-bound feature stores instead of following them.  At ~250 VGPRs two waves fit per
+// SIMD: four tiles per CU, every tile of a 65,536-row batch resident at once.
+constexpr int kPlayThreads = 128;
+
+__global__ __launch_bounds__(kPlayThreads) void play_kernel(
+    u64* states, i64 n, u64* sampler, float* features, u8* legal, u8* player, u8* obs_done,
+    i16* obs_status, i64* actions, float* reward, u8* done, u8* nagari, i16* status,
+    u8* committed, AutoReset ar) {
+  __shared__ ObserveTile t;  // the rows, then the records and masks, then the new rows
+  __shared__ int spare_rows[kTile];
+  __shared__ int spare_count;
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int tid = threadIdx.x;
+  const int lane = tid & (kTile - 1);
+  const int wave = tid / kTile;
+  {
+    const u64* src = states + base * kRowWords;
+    for (int j = tid; j < count * kRowWords; j += kPlayThreads) t.rows[j] = src[j];
+  }
+  const bool active = wave == 0 && lane < count;
+  u32 gen0 = 0, spare0 = 0;
+  if (active) {  // issued early so their latency hides
+    gen0 = ar.generation[base + lane];
+    spare0 = ar.spare_gen[base + lane];
+  }
+  __syncthreads();
+  Env e;
+  if (active) e = unpack_row(t.rows + lane * kRowWords);
+  __syncthreads();  // rows are dead from here on; their bytes become the records
+  const i64 i = base + lane;
+  i64 a = -1;
+  u64 x = 0;
+  if (active) {
+    const Packet pk = make_packet(e);
+    FeatRow fr;
+    feature_row(pk, c_stop_bits, fr);
+    feature_record(fr, t.out.rec[lane]);
+    t.out.legal[lane][0] = pk.head.legal.w0;
+    t.out.legal[lane][1] = pk.head.legal.w1;
+    t.out.legal[lane][2] = pk.head.legal.w2;
+    player[i] = pk.head.player;
+    obs_done[i] = e.done != 0;
+    obs_status[i] = (i16)pk.head.status;
+    x = sampler[i];
+    a = draw_legal(pk.head.legal.w0, pk.head.legal.w1, pk.head.legal.w2, x);
+    actions[i] = a;
+  }
+  __syncthreads();
+  bool take_spare = false;
+  Env g;  // the game stepped; read again from its row (unchanged in HBM, in L2)
+  bool fresh = false;  // finished, next game dealt here (its spare is stale)
+  u64 next_seed = 0;
+  if (wave == 0) {
+    if (lane < count) {
+      // A fresh copy rather than the observed `e`: stepping `e`, which make_packet has
+      // read, leaves an engine temporary in private memory (96 B per lane).
+      g = unpack_row(states + i * kRowWords);
+      const StepOut so = torch_step(g, clamp_action(a));
+      reward[i] = (float)so.reward0;
+      done[i] = so.done;
+      nagari[i] = so.nagari;
+      status[i] = (i16)so.status;
+      committed[i] = so.committed;
+      if (so.done) {
+        const u32 gen = gen0 + 1u;
+        ar.generation[i] = gen;
+        const u64 seed = ar.base_seed + (u64)i + ar.stride * gen;
+        sampler[i] = sampler_seed(seed);
+        take_spare = spare0 == gen;
+        fresh = !take_spare;
+        next_seed = seed;
+      } else if (a >= 0) {
+        sampler[i] = x;
+      }
+    }
+  } else {
+    store_observation(t, base, count, features, legal, wave - 1, kPlayThreads / kTile - 1);
+  }
+  __syncthreads();  // records are dead: the region takes the new rows
+  if (wave == 0) {
+    // a finished game's row takes its next game: the spare (copied below) or a deal here
+    if (lane < count && !take_spare && !fresh) pack_row(g, t.rows + lane * kRowWords);
+    if (fresh) pack_row(create_env(next_seed, (u32)(i & 1)), t.rows + lane * kRowWords);
+    const u64 ballot = __ballot(take_spare);
+    if (take_spare) spare_rows[__popcll(ballot & ((1ull << lane) - 1ull))] = lane;
+    if (lane == 0) spare_count = (int)__popcll(ballot);
+  }
+  __syncthreads();
+  for (int j = tid; j < spare_count * kRowWords; j += kPlayThreads) {
+    const int r = spare_rows[j / kRowWords];
+    const int k = j - (j / kRowWords) * kRowWords;
+    t.rows[r * kRowWords + k] = ar.spares[(base + r) * kRowWords + k];
+  }
+  __syncthreads();
+  stage_out<kPlayThreads>(t.rows, states, nullptr, base, count, 0);
 }
 
 // -------------------------------------------------------------------- small ----
@@ -723,6 +836,26 @@ int cugo_step(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
   launch_step<0, false>(n, stream, 
       reinterpret_cast<u64*>(states), n, nullptr, actions, n, nullptr, reward, done, nagari,
       status, committed, nullptr, AutoReset{});
+  return launched();
+}
+
+int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
+                     uint8_t* legal, uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
+                     int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
+                     int16_t* status, uint8_t* committed, uint64_t base_seed,
+                     int64_t seed_stride, uint32_t* generation, const uint8_t* spares,
+                     const uint32_t* spare_gen, hipStream_t stream) {
+  if (n < 0 || seed_stride < 0 ||
+      (n > 0 && (!states || !sampler || !features || !legal || !player || !obs_done ||
+                 !obs_status || !actions || !reward || !done || !nagari || !status ||
+                 !committed || !generation || !spares || !spare_gen)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  const AutoReset ar{base_seed, (u64)seed_stride, generation, reinterpret_cast<u64*>(sampler),
+                     reinterpret_cast<const u64*>(spares), spare_gen};
+  play_kernel<<<tiles(n), kPlayThreads, 0, stream>>>(
+      reinterpret_cast<u64*>(states), n, reinterpret_cast<u64*>(sampler), features, legal,
+      player, obs_done, obs_status, actions, reward, done, nagari, status, committed, ar);
   return launched();
 }
 

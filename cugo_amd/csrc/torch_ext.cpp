@@ -333,6 +333,42 @@ void reset_done_spares(torch::Tensor states, torch::Tensor done, int64_t base_se
              "reset_done_spares");
 }
 
+// observe_sample then step_reset_spares in one launch: (features, legal, player, done,
+// status, actions, reward, step done, nagari, step status, committed).
+std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampler,
+                                       int64_t base_seed, torch::Tensor generation,
+                                       torch::Tensor spares, torch::Tensor spare_gen,
+                                       int64_t seed_stride) {
+  check_states(states);
+  check_states(spares);
+  const int64_t n = states.size(0);
+  check_1d(sampler, at::kLong, "sampler");
+  check_1d(generation, at::kInt, "generation");
+  check_1d(spare_gen, at::kInt, "spare_gen");
+  TORCH_CHECK(sampler.numel() == n && generation.numel() == n && spares.size(0) == n &&
+                  spare_gen.numel() == n,
+              "sampler, generation, spares and spare_gen must have one entry per row");
+  check_same_device(states, sampler, "states", "sampler");
+  check_same_device(states, generation, "states", "generation");
+  check_same_device(states, spares, "states", "spares");
+  check_same_device(states, spare_gen, "states", "spare_gen");
+  const DeviceGuard guard(states.device());
+  auto o = observation_outputs(n, states);
+  o.push_back(torch::empty({n}, on(states, at::kLong)));
+  auto st = step_outputs(n, states);
+  o.insert(o.end(), st.begin(), st.end());
+  check_call(cugo_play_random(u8p(states), n, reinterpret_cast<uint64_t*>(sampler.data_ptr()),
+                              o[0].data_ptr<float>(), u8p(o[1]), u8p(o[2]), u8p(o[3]),
+                              o[4].data_ptr<int16_t>(), o[5].data_ptr<int64_t>(),
+                              o[6].data_ptr<float>(), u8p(o[7]), u8p(o[8]),
+                              o[9].data_ptr<int16_t>(), u8p(o[10]),
+                              static_cast<uint64_t>(base_seed), seed_stride < 0 ? n : seed_stride,
+                              reinterpret_cast<uint32_t*>(generation.data_ptr()), u8p(spares),
+                              reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), stream()),
+             "play_random");
+  return o;
+}
+
 // step then reset_done_spares (completed=None) in one launch; returns the step outputs.
 std::vector<torch::Tensor> step_reset_spares(torch::Tensor states, torch::Tensor actions,
                                              int64_t base_seed, torch::Tensor generation,
@@ -833,6 +869,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("states"), pybind11::arg("done"), pybind11::arg("base_seed"),
         pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("completed"),
         pybind11::arg("spares"), pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1);
+  m.def("play_random", &play_random,
+        "observe_sample then step_reset_spares in one launch",
+        pybind11::arg("states"), pybind11::arg("sampler"), pybind11::arg("base_seed"),
+        pybind11::arg("generation"), pybind11::arg("spares"), pybind11::arg("spare_gen"),
+        pybind11::arg("seed_stride") = -1);
   m.def("step_reset_spares", &step_reset_spares,
         "step, then reset_done_spares of the finished rows, in one launch",
         pybind11::arg("states"), pybind11::arg("actions"), pybind11::arg("base_seed"),

@@ -133,6 +133,15 @@ int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint
                            int64_t seed_stride, uint32_t* generation, uint64_t* sampler,
                            unsigned long long* completed, const uint8_t* spares,
                            const uint32_t* spare_gen, hipStream_t stream);
+/* cugo_observe_sample followed by cugo_step_reset_spares on its actions, in one launch
+ * (one random-policy self-play step): the observation outputs, the actions, then the
+ * step's outputs; the step of a tile's games overlaps the stores of its observation. */
+int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
+                     uint8_t* legal, uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
+                     int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
+                     int16_t* status, uint8_t* committed, uint64_t base_seed,
+                     int64_t seed_stride, uint32_t* generation, const uint8_t* spares,
+                     const uint32_t* spare_gen, hipStream_t stream);
 /* cugo_step followed by cugo_reset_done_spares(states, done, n, base_seed, seed_stride,
  * generation, sampler, NULL, spares, spare_gen) in one launch: the outputs are the
  * step's (done[i] = 1 for the game that just finished), and each finished row already

@@ -367,6 +367,33 @@ def test_step_reset_spares_matches_step_then_reset(ext):
     assert int(gen_a.sum().item()) > n
 
 
+def test_play_random_matches_observe_sample_then_step(ext):
+    """play_random == observe_sample followed by step_reset_spares: all eleven outputs,
+    the rows, generations and samplers, over 60 steps with spares refilled every few
+    steps (spare and inline re-deals both occur), at a partial last tile."""
+    announce("play_random")
+    n = 3001 * 2  # a partial last tile, even
+    base = 0x2718281
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    a = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(np.arange(n) & 1).to(DEV))
+    gen_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp_a = ext.seed_samplers(n, base, gen_a)
+    sp_a = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
+    sg_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    b, gen_b, smp_b, sp_b, sg_b = (t.clone() for t in (a, gen_a, smp_a, sp_a, sg_a))
+    for step in range(60):
+        if step % 5 == 0:
+            ext.refill_spares(sp_a, sg_a, gen_a, base)
+            ext.refill_spares(sp_b, sg_b, gen_b, base)
+        obs = ext.observe_sample(a, smp_a)
+        st = ext.step_reset_spares(a, obs[5], base, gen_a, smp_a, sp_a, sg_a)
+        fused = ext.play_random(b, smp_b, base, gen_b, sp_b, sg_b)
+        for k, want in enumerate(list(obs) + list(st)):
+            assert torch.equal(fused[k], want), (step, k)
+        assert torch.equal(a, b) and torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), step
+    assert int(gen_a.sum().item()) > n
+
+
 def test_observe_sample_matches_observe_then_sample(ext):
     """observe_sample == observe followed by sample_uniform: the same five observation
     outputs, actions and sampler words, over a random-policy run with resets (so rows
