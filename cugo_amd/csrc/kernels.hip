@@ -433,7 +433,11 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
   i64 a = -1;
   u64 x = 0;
   if (active) {
-    const Packet pk = make_packet(e);
+    // The observation reads one copy of the game and the step another: building the
+    // packet from the very Env that is then stepped leaves an engine temporary in private
+    // memory (72-96 B per lane).
+    const Env seen = e;
+    const Packet pk = make_packet(seen);
     FeatRow fr;
     feature_row(pk, c_stop_bits, fr);
     feature_record(fr, t.out.rec[lane]);
@@ -441,7 +445,7 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
     t.out.legal[lane][1] = pk.head.legal.w1;
     t.out.legal[lane][2] = pk.head.legal.w2;
     player[i] = pk.head.player;
-    obs_done[i] = e.done != 0;
+    obs_done[i] = seen.done != 0;
     obs_status[i] = (i16)pk.head.status;
     x = sampler[i];
     a = draw_legal(pk.head.legal.w0, pk.head.legal.w1, pk.head.legal.w2, x);
@@ -449,14 +453,12 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
   }
   __syncthreads();
   bool take_spare = false;
-  Env g;  // the game stepped; read again from its row (unchanged in HBM, in L2)
+  Env g;  // the game stepped (a copy of `e`)
   bool fresh = false;  // finished, next game dealt here (its spare is stale)
   u64 next_seed = 0;
   if (wave == 0) {
     if (lane < count) {
-      // A fresh copy rather than the observed `e`: stepping `e`, which make_packet has
-      // read, leaves an engine temporary in private memory (96 B per lane).
-      g = unpack_row(states + i * kRowWords);
+      g = e;
       const StepOut so = torch_step(g, clamp_action(a));
       reward[i] = (float)so.reward0;
       done[i] = so.done;
