@@ -37,6 +37,11 @@ SEED_BASE = 0x243F6A8885A308D3
 HBM_PEAK_GBS = 8000.0
 REFILL = 8  # steps between batched pre-deals of the next games
 OBSERVE_BYTES_PER_ROW = 248 + 720 * 4 + 179 + 1 + 1 + 2  # 3,311
+# play_random per row: state read and written (2 x 248), the observation (2,880 + 179 + 4),
+# the sampler word read and written (16), the action (8), the step outputs (9), the
+# generation and spare generation read (8); a finished row's spare (248 B for ~5 % of rows
+# a step) is left out.
+PLAY_BYTES_PER_ROW = 2 * 248 + 720 * 4 + 179 + 4 + 16 + 8 + 9 + 8  # 3,600
 STEP_BYTES_PER_ROW = 248 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # 513
 BRANCH_BYTES_PER_CHILD = 8 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # parent reads hit L2: 273
 
@@ -159,7 +164,22 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     burst[1].record(stream)
     torch.cuda.synchronize()
     observe_ms = burst[0].elapsed_time(burst[1]) / reps
-    return {"seconds": seconds, "games": games, "observe_ms": observe_ms}
+    # play_random alone (one launch per step on the whole batch), continuing the games:
+    # 6 blocks of 8 back-to-back launches, spares refilled between blocks, outside the events.
+    play_ms = None
+    if fused:
+        total = 0.0
+        for _ in range(6):
+            ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch)
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record(stream)
+            for _ in range(REFILL):
+                ext.play_random(states, sampler, SEED_BASE, gen, spares, spare_gen, batch)
+            ev[1].record(stream)
+            torch.cuda.synchronize()
+            total += ev[0].elapsed_time(ev[1])
+        play_ms = total / (6 * REFILL)
+    return {"seconds": seconds, "games": games, "observe_ms": observe_ms, "play_ms": play_ms}
 
 
 def mid_game_roots(ext, torch, n: int, base: int):
@@ -619,6 +639,22 @@ def main() -> None:
     games_per_s = rp["games"] / rp["seconds"]
     ms_per_step = 1000.0 * rp["seconds"] / args.steps
     observe_gbs = args.batch * OBSERVE_BYTES_PER_ROW / (rp["observe_ms"] * 1e-3) / 1e9
+    observe_roofline = {"kernel": "observe_kernel", "bound": "hbm",
+                        "achieved": round(observe_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(observe_gbs / HBM_PEAK_GBS, 4),
+                        "traffic": measured_traffic("observe_kernel", str(args.batch)),
+                        "bytes_per_row": OBSERVE_BYTES_PER_ROW,
+                        "avg_launch_ms": round(rp["observe_ms"], 4)}
+    if rp["play_ms"] is not None:
+        play_gbs = args.batch * PLAY_BYTES_PER_ROW / (rp["play_ms"] * 1e-3) / 1e9
+        roofline = {"kernel": "play_kernel", "bound": "hbm",
+                    "achieved": round(play_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(play_gbs / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic("play_kernel", str(args.batch)),
+                    "bytes_per_row": PLAY_BYTES_PER_ROW,
+                    "avg_launch_ms": round(rp["play_ms"], 4)}
+    else:
+        roofline = observe_roofline
     result = {
         "metric": "complete games/sec (random-policy self-play, B=65536 resident games)",
         "value": round(games_per_s, 1),
@@ -632,18 +668,17 @@ def main() -> None:
         "vs_baseline": None,
         "dtype": "u64",
         "data": "synthetic",
-        "config": {"workload": "random-policy self-play: observe -> sample -> step -> reset",
+        "config": {"workload": "random-policy self-play: observe -> sample -> step -> "
+                               "auto-reset, "
+                               + ("one play_random launch per step" if not args.two_launch
+                                  else "observe_sample + step_reset_spares per step"),
                    "batch": args.batch, "seed_base": hex(SEED_BASE),
                    "policy": "uniform legal action, per-game xorshift64",
                    "streams": args.streams, "hip_graph": not args.no_graph},
         "steps_per_s": round(args.batch * args.steps / rp["seconds"], 1),
         "games_timed": rp["games"],
-        "roofline": {"kernel": "observe_kernel", "bound": "hbm",
-                     "achieved": round(observe_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(observe_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("observe_kernel", str(args.batch)),
-                     "bytes_per_row": OBSERVE_BYTES_PER_ROW,
-                     "avg_launch_ms": round(rp["observe_ms"], 4)},
+        "roofline": roofline,
+        "observe_roofline": observe_roofline,
     }
     if not args.no_branch:
         result["branch"] = branch_workload(ext, torch, args.branch_iters)
