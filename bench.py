@@ -236,7 +236,20 @@ def branch_workload(ext, torch, iters: int) -> dict:
     torch.cuda.synchronize()
     branch_ms = ev[0].elapsed_time(ev[1]) / iters
     observe_ms = ev[1].elapsed_time(ev[2]) / iters
+    # the same children branched and observed by one launch (branch_observe_indexed)
+    del children
+    out = ext.branch_observe_indexed(roots, parent, actions)
+    del out
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    for _ in range(iters):
+        out = ext.branch_observe_indexed(roots, parent, actions)
+        del out
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    fused_ms = ev[0].elapsed_time(ev[1]) / iters
     n = roots_n * fan
+    fused_bytes = n * (BRANCH_BYTES_PER_CHILD + OBSERVE_BYTES_PER_ROW - 248)
     return {
         "children": n,
         "live_roots": int(n_live),
@@ -245,6 +258,9 @@ def branch_workload(ext, torch, iters: int) -> dict:
         "branch_gbs": n * BRANCH_BYTES_PER_CHILD / (branch_ms * 1e-3) / 1e9,
         "observe_children_ms": round(observe_ms, 4),
         "branch_observe_per_s": n / ((branch_ms + observe_ms) * 1e-3),
+        "branch_observe_fused_ms": round(fused_ms, 4),
+        "branch_observe_fused_per_s": n / (fused_ms * 1e-3),
+        "branch_observe_fused_gbs": fused_bytes / (fused_ms * 1e-3) / 1e9,
     }
 
 

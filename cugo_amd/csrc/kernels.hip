@@ -499,6 +499,79 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
   stage_out<kPlayThreads>(t.rows, states, nullptr, base, count, 0);
 }
 
+// ---------------------------------------------------------- branch + observe ----
+// branch_indexed then observe_indexed of the children (the reference's callers do exactly
+// this, python/cugo_ppo50.py:96-98), in one launch with the same outputs.  Two waves per
+// tile of 64 children: wave 0 gathers the parents, steps the clones and builds the
+// children's observation records in LDS; then wave 1 stores the observations while wave 0
+// writes the child rows from registers (each lane its own row), so the children are never
+// read back.
+__global__ __launch_bounds__(kPlayThreads) void branch_observe_kernel(
+    const u64* parents, i64 env_count, const i64* ids, const i64* actions, i64 n,
+    u64* children, float* reward, u8* done, u8* nagari, i16* status, u8* committed,
+    float* features, u8* legal, u8* player, u8* obs_done, i16* obs_status) {
+  __shared__ ObserveTile t;
+  __shared__ i64 tile_ids[kTile];
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int tid = threadIdx.x;
+  const int lane = tid & (kTile - 1);
+  const int wave = tid / kTile;
+  if (tid < count) tile_ids[tid] = ids[base + tid];
+  __syncthreads();
+  stage_in<kPlayThreads>(t.rows, parents, tile_ids, base, count, env_count);
+  __syncthreads();
+  const bool active = wave == 0 && lane < count;
+  // The clone is unpacked and stepped in one block before the rows are overwritten: an
+  // Env unpacked before a barrier and stepped after it leaves an engine temporary in
+  // private memory.
+  Env e;  // the parent (a zero row for an invalid id), then the child
+  const i64 i = base + lane;
+  if (active) {
+    e = unpack_row(t.rows + lane * kRowWords);
+    if (valid_id(tile_ids[lane], env_count)) {
+      const StepOut so = torch_step(e, clamp_action(actions[i]));
+      reward[i] = (float)so.reward0;
+      done[i] = so.done;
+      nagari[i] = so.nagari;
+      status[i] = (i16)so.status;
+      committed[i] = so.committed;
+    } else {  // torch50_ext.cu:108-118: a zero child, whose observation follows
+      reward[i] = 0.0f;
+      done[i] = 1;
+      nagari[i] = 0;
+      status[i] = CUGO_INVALID_INDEX_STATUS;
+      committed[i] = 0;
+    }
+  }
+  __syncthreads();  // rows are dead from here on; their bytes become the records
+  if (active) {
+    const Env seen = e;  // observed from a copy (see play_kernel)
+    const Packet pk = make_packet(seen);
+    FeatRow fr;
+    feature_row(pk, c_stop_bits, fr);
+    feature_record(fr, t.out.rec[lane]);
+    t.out.legal[lane][0] = pk.head.legal.w0;
+    t.out.legal[lane][1] = pk.head.legal.w1;
+    t.out.legal[lane][2] = pk.head.legal.w2;
+    player[i] = pk.head.player;
+    obs_done[i] = seen.done != 0;
+    obs_status[i] = (i16)pk.head.status;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    if (lane < count) {
+      u64 row[kRowWords];
+      pack_row(e, row);
+      u64* out = children + i * kRowWords;
+#pragma unroll
+      for (int k = 0; k < kRowWords; ++k) out[k] = row[k];
+    }
+  } else {
+    store_observation(t, base, count, features, legal, wave - 1, kPlayThreads / kTile - 1);
+  }
+}
+
 // -------------------------------------------------------------------- small ----
 __global__ __launch_bounds__(256) void start_kernel(const u64* states, i64 n, i64* out) {
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
@@ -858,6 +931,24 @@ int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* featu
   play_kernel<<<tiles(n), kPlayThreads, 0, stream>>>(
       reinterpret_cast<u64*>(states), n, reinterpret_cast<u64*>(sampler), features, legal,
       player, obs_done, obs_status, actions, reward, done, nagari, status, committed, ar);
+  return launched();
+}
+
+int cugo_branch_observe_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids,
+                                const int64_t* actions, int64_t n, uint8_t* children,
+                                float* reward, uint8_t* done, uint8_t* nagari, int16_t* status,
+                                uint8_t* committed, float* features, uint8_t* legal,
+                                uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
+                                hipStream_t stream) {
+  if (n < 0 || env_count < 0 ||
+      (n > 0 && (!ids || !actions || !children || !reward || !done || !nagari || !status ||
+                 !committed || !features || !legal || !player || !obs_done || !obs_status)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  branch_observe_kernel<<<tiles(n), kPlayThreads, 0, stream>>>(
+      reinterpret_cast<const u64*>(states), env_count, ids, actions, n,
+      reinterpret_cast<u64*>(children), reward, done, nagari, status, committed, features,
+      legal, player, obs_done, obs_status);
   return launched();
 }
 

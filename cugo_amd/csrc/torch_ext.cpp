@@ -333,6 +333,29 @@ void reset_done_spares(torch::Tensor states, torch::Tensor done, int64_t base_se
              "reset_done_spares");
 }
 
+// branch_indexed then observe_indexed of the children in one launch: (children, reward,
+// done, nagari, status, committed, features, legal, player, obs_done, obs_status).
+std::vector<torch::Tensor> branch_observe_indexed(torch::Tensor states, torch::Tensor ids,
+                                                  torch::Tensor actions) {
+  check_indexed_actions(states, ids, actions);
+  const DeviceGuard guard(states.device());
+  const int64_t n = ids.numel();
+  auto children = torch::empty({n, CUGO_STATE_BYTES}, on(states, at::kByte));
+  auto st = step_outputs(n, states);
+  auto ob = observation_outputs(n, states);
+  check_call(cugo_branch_observe_indexed(
+                 u8p(states), states.size(0), ids.data_ptr<int64_t>(),
+                 actions.data_ptr<int64_t>(), n, u8p(children), st[0].data_ptr<float>(),
+                 u8p(st[1]), u8p(st[2]), st[3].data_ptr<int16_t>(), u8p(st[4]),
+                 ob[0].data_ptr<float>(), u8p(ob[1]), u8p(ob[2]), u8p(ob[3]),
+                 ob[4].data_ptr<int16_t>(), stream()),
+             "branch_observe_indexed");
+  std::vector<torch::Tensor> out{children};
+  out.insert(out.end(), st.begin(), st.end());
+  out.insert(out.end(), ob.begin(), ob.end());
+  return out;
+}
+
 // observe_sample then step_reset_spares in one launch: (features, legal, player, done,
 // status, actions, reward, step done, nagari, step status, committed).
 std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampler,
@@ -869,6 +892,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("states"), pybind11::arg("done"), pybind11::arg("base_seed"),
         pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("completed"),
         pybind11::arg("spares"), pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1);
+  m.def("branch_observe_indexed", &branch_observe_indexed,
+        "branch_indexed then observe_indexed of the children, in one launch");
   m.def("play_random", &play_random,
         "observe_sample then step_reset_spares in one launch",
         pybind11::arg("states"), pybind11::arg("sampler"), pybind11::arg("base_seed"),

@@ -133,6 +133,17 @@ int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint
                            int64_t seed_stride, uint32_t* generation, uint64_t* sampler,
                            unsigned long long* completed, const uint8_t* spares,
                            const uint32_t* spare_gen, hipStream_t stream);
+/* cugo_branch_indexed followed by cugo_observe_indexed of the children (ids 0..n-1), in
+ * one launch (the reference's callers do both, python/cugo_ppo50.py:96-98): children and
+ * the step outputs as cugo_branch_indexed, then the children's observation as
+ * cugo_observe (features/legal/player/obs_done/obs_status); the children are not read
+ * back. */
+int cugo_branch_observe_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids,
+                                const int64_t* actions, int64_t n, uint8_t* children,
+                                float* reward, uint8_t* done, uint8_t* nagari, int16_t* status,
+                                uint8_t* committed, float* features, uint8_t* legal,
+                                uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
+                                hipStream_t stream);
 /* cugo_observe_sample followed by cugo_step_reset_spares on its actions, in one launch
  * (one random-policy self-play step): the observation outputs, the actions, then the
  * step's outputs; the step of a tile's games overlaps the stores of its observation. */

@@ -46,7 +46,8 @@ def test_extension_module_constants():
                "branch_indexed", "hands_indexed", "stock_indexed", "step_events_indexed",
                "start", "decode_attention", "decode_attention_append", "sample_uniform",
                "observe_sample", "reset_done", "reset_done_spares", "refill_spares",
-               "seed_samplers", "step_reset_spares", "play_random"):
+               "seed_samplers", "step_reset_spares", "play_random",
+               "branch_observe_indexed"):
         assert callable(getattr(m, op))
 
 

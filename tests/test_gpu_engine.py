@@ -367,6 +367,30 @@ def test_step_reset_spares_matches_step_then_reset(ext):
     assert int(gen_a.sum().item()) > n
 
 
+def test_branch_observe_matches_branch_then_observe(ext):
+    """branch_observe_indexed == branch_indexed followed by observe_indexed of the children:
+    every output bit-identical, with invalid and duplicate parent ids, wild actions and a
+    partial last tile; the parents are not modified."""
+    announce("branch_observe_indexed")
+    rows = torch.from_numpy(np.load(GOLDEN / "rows.npz")["mid"]).to(DEV)
+    m = rows.shape[0]
+    g = np.random.default_rng(41)
+    n = 5000
+    ids = g.integers(0, m, n)
+    ids[:7] = [-1, m, m + 100, 0, 0, 5, -7]
+    actions = g.integers(-3, 185, n)
+    ids_t = torch.from_numpy(ids).to(DEV)
+    act_t = torch.from_numpy(actions).to(DEV)
+    before = rows.clone()
+    fused = ext.branch_observe_indexed(rows, ids_t, act_t)
+    assert torch.equal(rows, before)
+    br = ext.branch_indexed(rows, ids_t, act_t)
+    ob = ext.observe_indexed(br[0], torch.arange(n, device=DEV))
+    for k, want in enumerate(list(br) + list(ob)):
+        assert torch.equal(fused[k], want), k
+    assert ext.branch_observe_indexed(rows, ids_t[:0], act_t[:0])[0].shape == (0, 248)
+
+
 def test_play_random_matches_observe_sample_then_step(ext):
     """play_random == observe_sample followed by step_reset_spares: all eleven outputs,
     the rows, generations and samplers, over 60 steps with spares refilled every few
