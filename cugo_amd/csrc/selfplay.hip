@@ -287,18 +287,19 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   const bool record = step >= 0 && step < wave.max_steps;
   const i64 rec = step * w + i;
   const float* f = features + i * kFeatures;
-  typename T::storage* q = q_in + i * (kFeatures + kActions);
-  for (int j = lane; j < kFeatures; j += 64) {
-    const float x = f[j];
+  const int width = (int)wave.width;
+  typename T::storage* q = q_in + i * (width + kActions);
+  for (int j = lane; j < width; j += 64) {
+    const float x = f[wave.columns != nullptr ? wave.columns[j] : j];
     q[j] = T::from_float(x);
-    if (record) wave.rec_features[rec * kFeatures + j] = BF16::from_float(x);
+    if (record) wave.rec_features[rec * width + j] = BF16::from_float(x);
   }
   const uint8_t* g = legal + i * kActions;
   bool any = false;
   for (int j = lane; j < kActions; j += 64) {
     const uint8_t b = g[j] != 0;
     any |= b;
-    q[kFeatures + j] = T::from_float(b ? 1.0f : 0.0f);
+    q[width + j] = T::from_float(b ? 1.0f : 0.0f);
     if (record) wave.rec_legal[rec * kActions + j] = b;
   }
   any = __ballot(any) != 0;
@@ -313,7 +314,8 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   wave.rec_opp_hand[rec] = (i64)states[i * kRowWords + (1 - p)];
   wave.rec_stock[rec] = stock[i];
   wave.rec_stop_points[rec] = (i64)rintf(exp2f(12.0f * f[kStopPointsColumn]) - 1.0f);
-  wave.rec_valid[rec] = active;
+  // a pool game's decision belongs to the learner only when the learner's seat moves
+  wave.rec_valid[rec] = active && (i >= wave.pool_games || p == wave.learner_seat[i]);
 }
 
 // After the engine step (:146-163): bad += active & (step status != OK); a game that
@@ -345,6 +347,7 @@ __global__ __launch_bounds__(256) void advance_kernel(
     for (int k = 0; k < 9; ++k) log[k] = events[i * 9 + k];
     wave.cache_length[i] += 1;
     wave.cache_length[w + i] += 1;
+    if (i < wave.pool_games) wave.opp_cache_length[i] += 1;
     wave.count[i] = c + 1;
   }
   const i64 step = wave.step_index[0];
@@ -566,7 +569,11 @@ int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8
                           const float* features, const uint8_t* legal, const uint8_t* player,
                           const uint8_t* done, const int16_t* status, const int64_t* stock,
                           void* q_in, int64_t* query_rows, hipStream_t stream) {
-  if (!wave || wave->w < 0 || wave->max_steps < 0) return -1;
+  if (!wave || wave->w < 0 || wave->max_steps < 0 || wave->width < 1 ||
+      wave->width > kFeatures || (wave->columns == nullptr && wave->width != kFeatures) ||
+      wave->pool_games < 0 || wave->pool_games > wave->w ||
+      (wave->pool_games > 0 && !wave->learner_seat))
+    return -1;
   const int64_t w = wave->w;
   if (w > 0 && (!states || !features || !legal || !player || !done || !status || !stock ||
                 !q_in || !query_rows || !wave->step_index || !wave->count || !wave->bad ||
@@ -594,7 +601,9 @@ int cugo_selfplay_advance(const CugoSelfPlayWave* wave, const uint8_t* done,
                           const int16_t* step_status, const uint8_t* committed,
                           const int64_t* events, const int64_t* actions, const float* logp,
                           hipStream_t stream) {
-  if (!wave || wave->w < 0 || wave->max_steps < 0) return -1;
+  if (!wave || wave->w < 0 || wave->max_steps < 0 || wave->pool_games < 0 ||
+      wave->pool_games > wave->w || (wave->pool_games > 0 && !wave->opp_cache_length))
+    return -1;
   const int64_t w = wave->w;
   if (w > 0 && (!done || !reward0 || !new_done || !nagari || !step_status || !committed ||
                 !events || !actions || !logp || !wave->step_index || !wave->count ||

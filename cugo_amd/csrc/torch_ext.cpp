@@ -738,11 +738,39 @@ class SelfPlayState {
                 torch::Tensor rec_features, torch::Tensor rec_legal, torch::Tensor rec_logp,
                 torch::Tensor rec_actions, torch::Tensor rec_opp_hand, torch::Tensor rec_stock,
                 torch::Tensor rec_stop_points, torch::Tensor rec_seat, torch::Tensor rec_count,
-                torch::Tensor rec_valid)
+                torch::Tensor rec_valid, c10::optional<torch::Tensor> columns,
+                int64_t pool_games, torch::Tensor learner_seat,
+                c10::optional<torch::Tensor> opp_cache_length)
       : keep_{step_index, count, events, cache_length, final_reward0, final_nagari, finished,
               bad, rec_features, rec_legal, rec_logp, rec_actions, rec_opp_hand, rec_stock,
-              rec_stop_points, rec_seat, rec_count, rec_valid} {
+              rec_stop_points, rec_seat, rec_count, rec_valid, learner_seat} {
     TORCH_CHECK(w >= 0 && max_steps >= 0, "w and max_steps must be non-negative");
+    TORCH_CHECK(pool_games >= 0 && pool_games <= w, "pool_games must be in [0, w]");
+    int64_t width = CUGO_FEATURE_COUNT;
+    const int32_t* cols = nullptr;
+    if (columns.has_value()) {
+      const auto c = *columns;
+      TORCH_CHECK(c.is_cuda() && c.is_contiguous() && c.scalar_type() == at::kInt &&
+                      c.dim() == 1 && c.numel() >= 1 && c.numel() <= CUGO_FEATURE_COUNT,
+                  "columns must be a contiguous CUDA int32 [width] tensor");
+      const auto host = c.cpu();
+      const int32_t* v = host.data_ptr<int32_t>();
+      for (int64_t j = 0; j < host.numel(); ++j)
+        TORCH_CHECK(v[j] >= 0 && v[j] < CUGO_FEATURE_COUNT, "a feature column is out of range");
+      width = c.numel();
+      cols = c.data_ptr<int32_t>();
+      keep_.push_back(c);
+    }
+    int64_t* opp_len = nullptr;
+    if (pool_games > 0) {
+      TORCH_CHECK(opp_cache_length.has_value(), "a pool needs the opponent's cache lengths");
+      const auto o = *opp_cache_length;
+      TORCH_CHECK(o.is_cuda() && o.is_contiguous() && o.scalar_type() == at::kLong &&
+                      o.numel() >= pool_games,
+                  "the opponent's cache lengths must be int64 with one entry per pool game");
+      opp_len = o.data_ptr<int64_t>();
+      keep_.push_back(o);
+    }
     const auto dev = count.device();
     for (const auto& t : keep_)
       TORCH_CHECK(t.is_cuda() && t.device() == dev && t.is_contiguous(),
@@ -761,7 +789,8 @@ class SelfPlayState {
     want(final_nagari, at::kBool, {w}, "final_nagari");
     want(finished, at::kBool, {w}, "finished");
     TORCH_CHECK(bad.scalar_type() == at::kLong && bad.numel() == 1, "bad must be one int64");
-    want(rec_features, at::kBFloat16, {s, w, CUGO_FEATURE_COUNT}, "rec_features");
+    want(rec_features, at::kBFloat16, {s, w, width}, "rec_features");
+    want(learner_seat, at::kLong, {w}, "learner_seat");
     want(rec_legal, at::kBool, {s, w, CUGO_ACTION_COUNT}, "rec_legal");
     want(rec_logp, at::kFloat, {s, w}, "rec_logp");
     want(rec_valid, at::kBool, {s, w}, "rec_valid");
@@ -771,6 +800,11 @@ class SelfPlayState {
     auto l = [](const torch::Tensor& t) { return t.data_ptr<int64_t>(); };
     c_ = CugoSelfPlayWave{w,
                           max_steps,
+                          width,
+                          cols,
+                          pool_games,
+                          learner_seat.data_ptr<int64_t>(),
+                          opp_len,
                           l(step_index),
                           l(count),
                           l(events),
@@ -791,7 +825,7 @@ class SelfPlayState {
                           u8p(rec_valid)};
   }
 
-  // -> (q_in [w, 899] of q_dtype, query_rows int64 [w])
+  // -> (q_in [w, width + 179] of q_dtype, query_rows int64 [w])
   std::vector<torch::Tensor> prepare(torch::Tensor states, torch::Tensor features,
                                      torch::Tensor legal, torch::Tensor player,
                                      torch::Tensor done, torch::Tensor status,
@@ -815,7 +849,7 @@ class SelfPlayState {
     for (const auto* t : {&states, &features, &legal, &player, &done, &status, &stock})
       TORCH_CHECK(t->device() == keep_[0].device(), "inputs must be on the wave's device");
     const DeviceGuard guard(states.device());
-    auto q_in = torch::empty({w, CUGO_FEATURE_COUNT + CUGO_ACTION_COUNT}, on(states, q_dtype));
+    auto q_in = torch::empty({w, c_.width + CUGO_ACTION_COUNT}, on(states, q_dtype));
     auto rows = torch::empty({w}, on(states, at::kLong));
     check_call(cugo_selfplay_prepare(&c_, q_dtype == at::kBFloat16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32,
                                      u8p(states), features.data_ptr<float>(), u8p(legal),
@@ -915,7 +949,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                           torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor,
                           torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor,
                           torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor,
-                          torch::Tensor, torch::Tensor, torch::Tensor>())
+                          torch::Tensor, torch::Tensor, torch::Tensor,
+                          c10::optional<torch::Tensor>, int64_t, torch::Tensor,
+                          c10::optional<torch::Tensor>>())
       .def("prepare", &SelfPlayState::prepare)
       .def("advance", &SelfPlayState::advance);
   m.def("masked_argmax", &masked_argmax, "Greedy action: argmax of the legal logits");

@@ -270,6 +270,13 @@ int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* lega
  * max_steps recorded steps; every pointer is device memory. */
 typedef struct CugoSelfPlayWave {
   int64_t w, max_steps;
+  int64_t width;                  /* recorded / query feature columns: 720, or the
+                                     events-mode context columns */
+  const int32_t* columns;         /* [width] feature columns kept, NULL = all 720 */
+  int64_t pool_games;             /* games 0 .. pool_games-1 face the frozen opponent */
+  const int64_t* learner_seat;    /* [w]: the learner's seat (read for pool games) */
+  int64_t* opp_cache_length;      /* [max(1, pool_games)]: the opponent's cache lengths
+                                     (NULL without a pool) */
   const int64_t* step_index;      /* [1]: the step being recorded */
   int64_t* count;                 /* [w]: events committed so far */
   int64_t* events;                /* [w, 48, 9]: event log */
@@ -278,7 +285,7 @@ typedef struct CugoSelfPlayWave {
   uint8_t* final_nagari;          /* [w] bool */
   uint8_t* finished;              /* [w] bool */
   unsigned long long* bad;        /* [1] int64: bad observe/step results */
-  uint16_t* rec_features;         /* [max_steps, w, 720] bf16 */
+  uint16_t* rec_features;         /* [max_steps, w, width] bf16 */
   uint8_t* rec_legal;             /* [max_steps, w, 179] bool */
   float* rec_logp;                /* [max_steps, w] */
   int64_t* rec_actions;           /* [max_steps, w], and likewise: */
@@ -291,11 +298,12 @@ typedef struct CugoSelfPlayWave {
 } CugoSelfPlayWave;
 
 /* cugo_selfplay_prepare: the step's work between observe and the policy
- * (cugo_seq_selfplay50.py:110-140, no pool): bad += active & (status != OK or no legal
- * action); q_in [w, 899] of q_dtype = (features, legal as 0/1), the policy's query input;
- * records of step step_index (skipped outside [0, max_steps)): features as bf16, legal,
- * opponent hand (hands word 1 - player of the state row), stock, stop points
- * (round(exp2(12 f[471]) - 1), cugo_contract50.py:40-42), seat, count, valid = active;
+ * (cugo_seq_selfplay50.py:110-140): bad += active & (status != OK or no legal action);
+ * q_in [w, width + 179] of q_dtype = (the kept feature columns, legal as 0/1), the
+ * policy's query input; records of step step_index (skipped outside [0, max_steps)): the
+ * kept features as bf16, legal, opponent hand (hands word 1 - player of the state row),
+ * stock, stop points (round(exp2(12 f[471]) - 1), cugo_contract50.py:40-42), seat, count,
+ * valid = active and the learner moves (a pool game's mover may be the opponent);
  * query_rows [w] = (player & 1) * w + game.  states [w, 248] (row = game), features
  * f32 [w, 720], legal bool [w, 179], player/done [w], status i16 [w] (observe outputs),
  * stock int64 [w] (stock_indexed before the step). */
@@ -307,7 +315,8 @@ int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8
  * 146-163): bad += active & (step status != OK); games that finished now keep reward0 and
  * the nagari flag and are marked finished; a committed event goes to slot min(count, 47)
  * of the log and advances both seats' cache lengths and the count; actions and logp are
- * recorded at step step_index.  done = observe's done before the step; the others are
+ * recorded at step step_index; a pool game's committed event also advances the opponent's
+ * cache length.  done = observe's done before the step; the others are
  * step_events_indexed's outputs.  Call after the event tokens were appended. */
 int cugo_selfplay_advance(const CugoSelfPlayWave* wave, const uint8_t* done,
                           const float* reward0, const uint8_t* new_done, const uint8_t* nagari,

@@ -191,11 +191,11 @@ def test_gumbel_sample_matches_reference(ext):
     assert float((logp - want_lp).abs().max()) <= 1e-5
 
 
-def _policy(d=256, layers=4, heads=8, seed=0):
+def _policy(d=256, layers=4, heads=8, seed=0, mode="hybrid"):
     from cugo_amd.seq_selfplay import SeqPolicy
 
     torch.manual_seed(seed)
-    p = SeqPolicy(d_model=d, layers=layers, heads=heads)
+    p = SeqPolicy(mode=mode, d_model=d, layers=layers, heads=heads)
     with torch.no_grad():
         for prm in p.parameters():
             prm.normal_(0.0, 0.02)
@@ -209,6 +209,7 @@ def _reference_step(policy, ref, actions_from=None):
     actions_from the engine is stepped with those actions (teacher forcing) after
     sampling its own.  Returns (sampled actions, their logp, logits)."""
     ext, w, ids = ref["ext"], ref["w"], ref["ids"]
+    p, opp = ref["p"], ref["opp"]
     features, legal, players, done, status = ext.observe_indexed(ref["states"], ids)
     active = ~done
     ref["bad"] += (active & ((status != 0) | ~legal.any(1))).sum()
@@ -216,20 +217,29 @@ def _reference_step(policy, ref, actions_from=None):
     q = policy.query_token(features, legal)
     hidden = reference_cached_step(policy, ref["cache"], q, (player & 1) * w + ids)
     logits = policy.readout(hidden).float()
+    learner_move = torch.ones_like(active)
+    if p:
+        pids = torch.arange(p, device=DEV)
+        opp_q = opp.query_token(features[:p], legal[:p])
+        opp_logits = opp.readout(reference_cached_step(opp, ref["opp_cache"], opp_q, pids)).float()
+        opp_move = player[:p] != ref["learner_seat"][:p]
+        logits = torch.cat((torch.where(opp_move.unsqueeze(1), opp_logits, logits[:p]), logits[p:]))
+        learner_move = torch.cat((~opp_move, learner_move[p:]))
     actions, logp = gumbel_reference(logits, legal, ref["noise"])
     used = actions if actions_from is None else actions_from
     hands = ext.hands_indexed(ref["states"], ids)
     stock = ext.stock_indexed(ref["states"], ids)
     stop = torch.round(torch.exp2(12.0 * features[:, 471].float()) - 1.0).long()
     rec = ref["rec"]
-    rec["features"].append(features.to(torch.bfloat16))
+    kept = features if policy.mode == "hybrid" else features.index_select(1, policy.context_index)
+    rec["features"].append(kept.to(torch.bfloat16))
     rec["legal"].append(legal)
     rec["seat"].append(player)
     rec["count"].append(ref["count"].clone())
     rec["opp_hand"].append(hands.gather(1, (1 - player).unsqueeze(1)).squeeze(1))
     rec["stock"].append(stock)
     rec["stop_points"].append(stop)
-    rec["valid"].append(active)
+    rec["valid"].append(active & learner_move)
     reward0, new_done, nagari, step_status, committed, events = ext.step_events_indexed(
         ref["states"], ids, used)
     ref["bad"] += (active & (step_status != 0)).sum()
@@ -245,38 +255,52 @@ def _reference_step(policy, ref, actions_from=None):
                         torch.ones(w, dtype=torch.int64, device=DEV)))
     tok = encode_events_np(events.repeat(2, 1).cpu().numpy(), seats2.cpu().numpy())
     index = ref["count"].repeat(2)
-    p = 1 + index.clamp(max=47)
-    x = token_reference(tok, policy.event_in.weight, policy.event_in.bias, policy.position[p],
+    pos_idx = 1 + index.clamp(max=47)
+    x = token_reference(tok, policy.event_in.weight, policy.event_in.bias, policy.position[pos_idx],
                         policy.token_type[1].expand(2 * w, -1))
     reference_cached_step(policy, ref["cache"], x, torch.arange(2 * w, device=DEV))
+    if p:
+        opp_seat = 1 - ref["learner_seat"][:p]
+        tok = encode_events_np(events[:p].cpu().numpy(), opp_seat.cpu().numpy())
+        pp = 1 + ref["count"][:p].clamp(max=47)
+        xo = token_reference(tok, opp.event_in.weight, opp.event_in.bias, opp.position[pp],
+                             opp.token_type[1].expand(p, -1))
+        reference_cached_step(opp, ref["opp_cache"], xo, torch.arange(p, device=DEV))
+        ref["opp_cache"].length += commit[:p].long()
     ref["cache"].length += commit.repeat(2).long()
     ref["count"] += commit.long()
     return actions, logp, logits
 
 
-def test_selfplay_step_matches_reference_formulation(ext):
+@pytest.mark.parametrize("mode,pool", [("hybrid", False), ("events", True)])
+def test_selfplay_step_matches_reference_formulation(ext, mode, pool):
     """The captured self-play step against the reference formulation for a wave of 256
     games: identical engine trajectories (the reference copy replays the wave's actions),
     logits within 1e-2 relative, the same sampled action for at least 99 % of the
     decisions, identical records (features, mask, seat, count, opponent hand, stock, stop
     points, valid), event logs, counts, cache lengths, finished flags, final rewards and
     bad counts, and caches whose first layer agrees within 1e-2 (deeper layers 2e-2)."""
-    announce("selfplay step vs reference formulation")
+    announce(f"selfplay step vs reference formulation ({mode}, pool={pool})")
     from cugo_amd.seq_selfplay import SelfPlayWave, make_seeds, policy_cache
 
-    policy = _policy()
+    policy = _policy(mode=mode)
     w = 256
-    wave = SelfPlayWave(ext, policy, w, max_steps=64)
+    p = 96 if pool else 0
+    opp = _policy(seed=7, mode=mode) if pool else None
+    wave = SelfPlayWave(ext, policy, w, max_steps=64, opponent=opp, pool_games=p)
     wave.noise = torch.zeros((w, 179), device=DEV)
     g = torch.Generator(device=DEV).manual_seed(11)
     names = ("features", "legal", "seat", "count", "opp_hand", "stock", "stop_points", "valid")
     with torch.no_grad():
-        wave.capture()
+        wave.capture(pool)
         seeds, first = make_seeds(w, 12345, DEV)
-        learner = torch.zeros(w, dtype=torch.int64, device=DEV)
-        wave.reset(seeds, first, learner)
+        learner = torch.randint(2, (w,), generator=torch.Generator(device=DEV).manual_seed(3),
+                                device=DEV)
+        wave.reset(seeds, first, learner, pool)
         states = ext.create(seeds, first)
         ref = {"ext": ext, "w": w, "ids": torch.arange(w, device=DEV), "states": states,
+               "p": p, "opp": opp, "learner_seat": learner,
+               "opp_cache": policy_cache(opp, max(1, p), DEV) if pool else None,
                "cache": policy_cache(policy, 2 * w, DEV),
                "count": torch.zeros(w, dtype=torch.int64, device=DEV), "noise": wave.noise,
                "bad": torch.zeros((), dtype=torch.int64, device=DEV),
@@ -294,6 +318,12 @@ def test_selfplay_step_matches_reference_formulation(ext):
                              policy.token_type[0].expand(2 * w, -1))
         reference_cached_step(policy, ref["cache"], x0, torch.arange(2 * w, device=DEV))
         ref["cache"].length.fill_(1)
+        if pool:
+            tok = encode_start_np(start[:p].cpu().numpy(), (1 - learner[:p]).cpu().numpy())
+            xo = token_reference(tok, opp.start_in.weight, opp.start_in.bias,
+                                 opp.position[0].expand(p, -1), opp.token_type[0].expand(p, -1))
+            reference_cached_step(opp, ref["opp_cache"], xo, torch.arange(p, device=DEV))
+            ref["opp_cache"].length.fill_(1)
         agree = total = 0
         steps = 0
         for step in range(40):
@@ -311,6 +341,8 @@ def test_selfplay_step_matches_reference_formulation(ext):
             assert torch.equal(wave.states, ref["states"]), step
             assert torch.equal(wave.count, ref["count"]), step
             assert torch.equal(wave.cache.length, ref["cache"].length), step
+            if pool:
+                assert torch.equal(wave.opp_cache.length, ref["opp_cache"].length), step
             assert torch.equal(wave.events, ref["events"]), step
             assert torch.equal(wave.finished, ref["finished"]), step
             assert torch.equal(wave.final_nagari, ref["final_nagari"]), step
@@ -339,35 +371,39 @@ def test_selfplay_step_matches_reference_formulation(ext):
         assert max(errs) <= 2e-2, errs
 
 
-def test_selfplay_graph_replays_equal_eager_steps(ext):
+@pytest.mark.parametrize("pool", [False, True])
+def test_selfplay_graph_replays_equal_eager_steps(ext, pool):
     """Replays of the captured step == eager step() calls from the same start (same
     uniforms), repeated with eager work and synchronisations in between."""
-    announce("selfplay graph replay vs eager")
+    announce(f"selfplay graph replay vs eager (pool={pool})")
     from cugo_amd.seq_selfplay import SelfPlayWave, make_seeds
 
     policy = _policy(seed=1)
     w = 128
-    wave = SelfPlayWave(ext, policy, w, max_steps=64)
+    opp = _policy(seed=9) if pool else None
+    wave = SelfPlayWave(ext, policy, w, max_steps=64, opponent=opp, pool_games=40 if pool else 0)
     wave.noise = torch.zeros((w, 179), device=DEV)
     g = torch.Generator(device=DEV).manual_seed(5)
     noises = [torch.rand((w, 179), generator=g, device=DEV) for _ in range(12)]
     seeds, first = make_seeds(w, 777, DEV)
-    learner = torch.zeros(w, dtype=torch.int64, device=DEV)
+    learner = (torch.arange(w, device=DEV) % 3 == 0).long()
     runs = []
     with torch.no_grad():
-        wave.capture()
+        wave.capture(pool)
         for mode in ("eager", "graph", "graph"):
-            wave.reset(seeds, first, learner)
+            wave.reset(seeds, first, learner, pool)
             for k in range(12):
                 wave.noise.copy_(noises[k])
                 if mode == "eager":
-                    wave.step()
+                    wave.step(pool)
                 else:
                     wave.graph.replay()
                 torch.cuda.synchronize()
             runs.append([t.clone() for t in (wave.states, wave.events, wave.count,
                                               wave.rec_long["actions"], wave.rec_logp,
-                                              wave.cache.length, wave.cache.k)])
+                                              wave.cache.length, wave.cache.k, wave.rec_valid)]
+                        + ([wave.opp_cache.k.clone(), wave.opp_cache.length.clone()] if pool
+                           else []))
     for a, b in zip(runs[0], runs[1]):
         assert torch.equal(a, b)
     for a, b in zip(runs[1], runs[2]):
@@ -394,3 +430,32 @@ def test_selfplay_wave_plays_to_the_end(ext):
     legal = wave.rec_legal[:steps]
     picked = legal.gather(2, acts.unsqueeze(2)).squeeze(2)
     assert bool(picked[valid].all())
+
+
+def test_selfplay_collect_with_pool(ext):
+    """collect() over two waves with a frozen opponent loaded in place: outcomes for every
+    game, the learner's decisions only (none on the opponent's moves in pool games), the
+    event logs, and the opponent's new weights reach the captured step."""
+    announce("selfplay collect")
+    from cugo_amd.seq_selfplay import SelfPlayWave
+
+    policy = _policy(seed=3)
+    opp = _policy(seed=4)
+    w, p = 256, 64
+    wave = SelfPlayWave(ext, policy, w, max_steps=64, opponent=opp, pool_games=p)
+    other = _policy(seed=5).state_dict()
+    torch.manual_seed(0)
+    out = wave.collect(2 * w, seed_offset=1000, opponent_state=other)
+    assert out["vs_pool"].sum().item() == 2 * p
+    assert out["final_reward0"].shape == (2 * w,) and out["steps"] >= 16
+    dec = out["decisions"]
+    n = dec["actions"].numel()
+    assert all(v.shape[0] == n for v in dec.values())
+    assert dec["features"].shape[1] == 720
+    # no recorded decision of a pool game is the opponent's
+    pool_rows = dec["env_ids"] % w < p
+    seat_of = out["learner_seat"][dec["env_ids"]]
+    assert bool((dec["seat"][pool_rows] == seat_of[pool_rows]).all())
+    assert int(out["log"]["count"].max()) <= 48
+    w_t = wave.opponent._weight_t("event_in")
+    assert torch.equal(w_t, other["event_in.weight"].t().to(w_t.dtype))
