@@ -1719,9 +1719,9 @@ CG_HD u8 continue_postchance(Env& e, bool& committed) {
   return kOk;
 }
 
-// postchance50.h:541-556
-CG_HD u8 start_postchance(Env& e, u16 primary, const Mask3& legal, bool& committed) {
-  committed = false;
+// postchance50.h:541-556 up to its continue_postchance50 call: stages the decoded
+// primary action as the pending action.  The caller continues on kOk.
+CG_HD u8 stage_postchance(Env& e, u16 primary, const Mask3& legal) {
   Action a;
   const u8 status = decode_primary_raw(e, primary, legal, a);
   u8 actor = decision_player(e);
@@ -1730,15 +1730,15 @@ CG_HD u8 start_postchance(Env& e, u16 primary, const Mask3& legal, bool& committ
   set_pending(e, p);
   if (status != kOk) return status;
   e.pactive = 1;
-  return continue_postchance(e, committed);
+  return kOk;
 }
 
-// postchance50.h:558-587 (the card is already checked against the probe's legal set).
-CG_HD u8 choose_postchance(Env& e, u8 decision, u8 card, bool& committed) {
+// postchance50.h:558-587 up to its continue_postchance50 call (the card is already
+// checked against the probe's legal set): records the choice in the pending action.
+CG_HD void record_postchance_choice(Env& e, u8 decision, u8 card) {
   if (decision == kDecResolvePlayed) e.a_pmatch = card;
   else if (decision == kDecResolveDrawn) e.a_dmatch = card;
   else if (decision == kDecPiCard) e.sel_pi |= bit(card);
-  return continue_postchance(e, committed);
 }
 
 // ------------------------------------------------------------------ torch50.h ----
@@ -1956,13 +1956,13 @@ CG_HD Packet make_packet(const Env& e) {
 // Step result (TorchStepResult50, torch50.h:123-129).
 struct StepOut { u8 status; i64 reward0; u8 done, nagari, committed; };
 
-// torch50.h:491-540
-CG_HD StepOut torch_step(Env& e, u16 action) {
+// torch50.h:491-540 given `head` = packet_head(e) of this very state (the caller has it
+// from the observation it just built: make_packet(e).head is the same head).
+CG_HD StepOut torch_step_head(Env& e, u16 action, const PacketHead& head) {
   if (e.done != 0) {
     e.status = kGameFinished;
     return StepOut{e.status, reward0(e), e.done, e.nagari, 0};
   }
-  const PacketHead head = packet_head(e);
   if (head.status != kOk) {
     e.status = head.status;
     return StepOut{e.status, 0, e.done, e.nagari, 0};
@@ -1971,15 +1971,19 @@ CG_HD StepOut torch_step(Env& e, u16 action) {
     e.status = kNotLegal;
     return StepOut{e.status, 0, e.done, e.nagari, 0};
   }
-  bool committed;
-  u8 s;
+  // A pending row records its choice, any other row stages its primary action; both
+  // then continue the pending action (one call site, so a wave whose games take both
+  // branches runs the apply once).
+  bool committed = false;
+  u8 s = kOk;
   if (e.pactive != 0) {
     if (head.decision_kind == kDecPiCard) ++e.n_pi; else ++e.n_resolve;
     ++e.n_choice;
-    s = choose_postchance(e, head.decision_kind, (u8)(action - kActChoice), committed);
+    record_postchance_choice(e, head.decision_kind, (u8)(action - kActChoice));
   } else {
-    s = start_postchance(e, action, head.legal, committed);
+    s = stage_postchance(e, action, head.legal);
   }
+  if (s == kOk) s = continue_postchance(e, committed);
   if (s != kOk) {
     e.status = s;
     return StepOut{e.status, 0, e.done, e.nagari, 0};
@@ -1994,6 +1998,15 @@ CG_HD StepOut torch_step(Env& e, u16 action) {
   e.status = kOk;
   refresh_done(e);
   return StepOut{kOk, reward0(e), e.done, e.nagari, (u8)committed};
+}
+
+// torch50.h:491-540
+CG_HD StepOut torch_step(Env& e, u16 action) {
+  if (e.done != 0) {
+    e.status = kGameFinished;
+    return StepOut{e.status, reward0(e), e.done, e.nagari, 0};
+  }
+  return torch_step_head(e, action, packet_head(e));
 }
 
 // torch50.h:644-678: event words of a committed action (before/after diff).
@@ -2156,42 +2169,67 @@ CG_HD float feature_at(const u64* w, const float* d, u32 f) {
 }
 
 
-// Per-row dword record read by the GPU feature writer: the 20 bit-plane words as 40
-// dwords (low half first), the 56 dense floats, then one float 0.0 for the padding
-// features.  feature_source(f) names feature f's dword in that record and, for a bit
-// feature, the bit: (dword << 8) | (bit << 1) | 1; a float feature is (dword << 8).
-constexpr int kFeatRecord = 2 * kFeatWords + kFeatDense + 1;  // 97 used dwords
-constexpr int kFeatRecordStride = 98;                          // keeps u64 words aligned
+// Per-row dword record read by the GPU feature writer, laid out so that a lane turns
+// one record read into four consecutive features.  Feature quad q (features 4q..4q+3,
+// 180 quads) is one nibble of a 720-bit array in feature order - bit f is feature f for
+// a 0/1 feature, 0 for a dense one - at dword q / 8, bits 4 (q % 8) .. 4 (q % 8) + 3.  The
+// 16 quads that hold dense features also own four dwords of a dense section: the float
+// bits of each dense feature, 0 for the 0/1 features beside it.  A quad's floats are the
+// nibble's 0 / 1.0f bit patterns ORed with its dense dwords, which is exact for every
+// value (signed zeros included).
+constexpr int kRecBits = 24;        // 23 dwords of the 720-bit array, one pad
+constexpr int kRecDenseQuads = 16;
+constexpr int kFeatRecord = kRecBits + 4 * kRecDenseQuads;  // 88 dwords
+constexpr u32 kFeatQuads = 180;
 
+// Slot of quad q in the dense section, or -1: quads 111-119 (features 444-479),
+// 122-123 (488-495), 136-139 (544-559) and 177 (708-711).
+CG_HD int dense_slot(u32 q) {
+  if (q >= 111 && q <= 119) return (int)(q - 111);
+  if (q == 122 || q == 123) return (int)(q - 122 + 9);
+  if (q >= 136 && q <= 139) return (int)(q - 136 + 11);
+  if (q == 177) return 15;
+  return -1;
+}
+
+// ORs the low n bits of v into the bit array at bit `pos`.
+CG_HD void put_bits(u64* acc, u32 pos, u64 v, u32 n) {
+  v &= (1ull << n) - 1ull;  // n < 64
+  const u32 k = pos >> 6, s = pos & 63u;
+  acc[k] |= v << s;
+  if (s != 0 && s + n > 64u) acc[k + 1] |= v >> (64u - s);
+}
+
+// Every index below is a constant, so the row stays in registers.
 CG_HD void feature_record(const FeatRow& r, u32* rec) {
-  for (int k = 0; k < kFeatWords; ++k) {
-    rec[2 * k] = (u32)r.w[k];
-    rec[2 * k + 1] = (u32)(r.w[k] >> 32);
-  }
-  for (int k = 0; k < kFeatDense; ++k) rec[2 * kFeatWords + k] = __builtin_bit_cast(u32, r.d[k]);
-  rec[2 * kFeatWords + kFeatDense] = 0u;
-}
-
-CG_HD u32 feature_source(u32 f) {
-  u32 word, b;
-  if (f < 300) { word = f / 50; b = f % 50; }
-  else if (f < 396) { const u32 g = f - 300; word = 6 + g / 12; b = g % 12; }
-  else if (f < 446) { word = 14; b = f - 396; }
-  else if (f < 479) return (u32)(2 * kFeatWords + (f - 446)) << 8;
-  else if (f < 491) { word = 15; b = f - 479; }
-  else if (f < 496) return (u32)(2 * kFeatWords + 33 + (f - 491)) << 8;
-  else if (f < 544) { word = 16; b = f - 496; }
-  else if (f < 560) return (u32)(2 * kFeatWords + 38 + (f - 544)) << 8;
-  else if (f < 710) { const u32 g = f - 560; word = 17 + g / 50; b = g % 50; }
-  else if (f < 712) return (u32)(2 * kFeatWords + 54 + (f - 710)) << 8;
-  else return (u32)(2 * kFeatWords + kFeatDense) << 8;
-  return ((2 * word + (b >> 5)) << 8) | ((b & 31u) << 1) | 1u;
-}
-
-CG_HD float feature_from_record(const u32* rec, u32 src) {
-  const u32 v = rec[src >> 8];
-  const float as_bit = (float)((v >> ((src >> 1) & 31u)) & 1u);
-  return (src & 1u) ? as_bit : __builtin_bit_cast(float, v);
+  u64 acc[12];
+#pragma unroll
+  for (int k = 0; k < 12; ++k) acc[k] = 0;
+#pragma unroll
+  for (int p = 0; p < 6; ++p) put_bits(acc, 50u * p, r.w[p], 50);            // 0-299
+#pragma unroll
+  for (int m = 0; m < 8; ++m) put_bits(acc, 300u + 12u * m, r.w[6 + m], 12);  // 300-395
+  put_bits(acc, 396, r.w[14], 50);                                           // 396-445
+  put_bits(acc, 479, r.w[15], 12);                                           // 479-490
+  put_bits(acc, 496, r.w[16], 48);                                           // 496-543
+#pragma unroll
+  for (int p = 0; p < 3; ++p) put_bits(acc, 560u + 50u * p, r.w[17 + p], 50);  // 560-709
+#pragma unroll
+  for (int k = 0; k < kRecBits; ++k) rec[k] = (u32)(acc[k >> 1] >> (32 * (k & 1)));
+  // dense section, slot by slot: features 444-479 (dense 446-478 = d[0..32]),
+  // 488-495 (491-495 = d[33..37]), 544-559 (d[38..53]), 708-711 (710-711 = d[54..55])
+  u32* dn = rec + kRecBits;
+  dn[0] = dn[1] = dn[35] = 0u;
+#pragma unroll
+  for (int k = 0; k < 33; ++k) dn[2 + k] = __builtin_bit_cast(u32, r.d[k]);
+  dn[36] = dn[37] = dn[38] = 0u;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) dn[39 + k] = __builtin_bit_cast(u32, r.d[33 + k]);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) dn[44 + k] = __builtin_bit_cast(u32, r.d[38 + k]);
+  dn[60] = dn[61] = 0u;
+  dn[62] = __builtin_bit_cast(u32, r.d[54]);
+  dn[63] = __builtin_bit_cast(u32, r.d[55]);
 }
 
 }  // namespace cugo_amd

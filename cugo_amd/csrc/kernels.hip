@@ -94,11 +94,11 @@ __global__ __launch_bounds__(kTile) void create_kernel(const i64* seeds, const i
 // ------------------------------------------------------------------ observe ----
 // LDS of one observe tile: the staged rows are dead once every lane has unpacked its
 // row, so the per-row feature records and masks reuse the same bytes.
-struct ObserveTile {
+struct alignas(16) ObserveTile {
   union {
     u64 rows[kTileWords];
     struct {
-      u32 rec[kTile][kFeatRecordStride];
+      u32 rec[kTile][kFeatRecord];  // 16-byte aligned rows: dense quads load as one uint4
       u64 legal[kTile][3];
     } out;
   };
@@ -109,69 +109,93 @@ __device__ inline u32 spread4(u32 x) {
   return (x & 1u) | ((x & 2u) << 7) | ((x & 4u) << 14) | ((x & 8u) << 21);
 }
 
-// The tile's observation from its LDS records: features (wave w of `waves` storing waves
-// stores rows w, w + waves, ...; lane owns float4 columns q = lane, lane + 64, lane + 128
-// (< 180) of each, so a store instruction covers 1 KiB of one row and each lane resolves
-// its twelve feature sources once) and the legal mask rows as 32-bit words.  Called by
-// the storing waves only (wave in [0, waves)).
+// The tile's observation from its LDS records, stored by every wave that calls this.  A
+// wave claims work items from the tile's LDS counter `next` (zeroed before the records
+// were written) until none is left: items 0 .. count - 1 are feature rows (lane owns the
+// float4 columns q = lane, lane + 64, lane + 128 < 180 of the row, so a store instruction
+// covers 1 KiB; a column is one nibble of the record's bit array, ORed with the record's
+// dense dwords for the 16 columns that hold dense features), then 64-dword chunks of the
+// legal mask bytes, then their unaligned tail.  A wave that arrives late (one that also
+// stepped the games) takes what is left, so no wave idles while another stores alone.
+// The claiming lane is the wave's first active lane, and every pass raises the counter,
+// so every wave leaves the loop.
 __device__ inline void store_observation(const ObserveTile& t, i64 base, int count,
-                                         float* features, u8* legal, int wave, int waves) {
+                                         float* features, u8* legal, int* next) {
   const int lane = threadIdx.x & (kTile - 1);
   constexpr int kQuads = kFeatureCount / 4;  // 180
-  u32 src[3][4];
-  for (int c = 0; c < 3; ++c)
-    for (int k = 0; k < 4; ++k) {
-      const u32 q = (u32)(lane + kTile * c);
-      src[c][k] = feature_source(q < (u32)kQuads ? q * 4u + (u32)k : 719u);
-    }
-  float4* fout = reinterpret_cast<float4*>(features + base * kFeatureCount);
-  for (int r = wave; r < count; r += waves) {
-    const u32* rec = t.out.rec[r];
-    for (int c = 0; c < 3; ++c) {
-      const int q = lane + kTile * c;
-      if (q < kQuads) {
-        float4 v;
-        v.x = feature_from_record(rec, src[c][0]);
-        v.y = feature_from_record(rec, src[c][1]);
-        v.z = feature_from_record(rec, src[c][2]);
-        v.w = feature_from_record(rec, src[c][3]);
-        fout[r * kQuads + q] = v;
-      }
-    }
+  int slot[3];
+  for (int c = 0; c < 3; ++c) {
+    const int q = lane + kTile * c;
+    slot[c] = q < kQuads ? dense_slot((u32)q) : -1;
   }
+  uint4* fout = reinterpret_cast<uint4*>(features + base * kFeatureCount);
   // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0); word
   // w holds tile bytes 4w..4w+3, i.e. actions a..a+3 of row r unless it straddles rows.
-  const int tid = wave * kTile + lane;
-  const int threads = waves * kTile;
   u8* lout = legal + base * kActionCount;
   const int bytes = count * kActionCount;
   const int full = bytes / 4;
-  for (int w = tid; w < full; w += threads) {
-    const int b0 = w * 4;
-    const int r = b0 / kActionCount;
-    const int a = b0 - r * kActionCount;
-    u32 packed;
-    if (a + 3 < kActionCount) {
-      const u64* m = t.out.legal[r];
-      const int lo = a >> 6, sh = a & 63;
-      u64 bits = m[lo] >> sh;
-      if (sh > 60) bits |= m[lo + 1] << (64 - sh);
-      packed = spread4((u32)(bits & 0xFu));
+  const int chunks = (full + kTile - 1) / kTile;
+  const int items = count + chunks + (bytes > 4 * full ? 1 : 0);
+  const int leader = __ffsll((long long)__ballot(1)) - 1;
+  for (;;) {
+    int item = 0;
+    if (lane == leader) item = atomicAdd(next, 1);
+    item = __builtin_amdgcn_readfirstlane(item);
+    if (item >= items) break;
+    if (item < count) {
+      const int r = item;
+      const u32* rec = t.out.rec[r];
+      for (int c = 0; c < 3; ++c) {
+        const int q = lane + kTile * c;
+        if (q < kQuads) {
+          const u32 nib = rec[q >> 3] >> (4 * (q & 7));
+          uint4 v;  // 0 or 1.0f per bit
+          v.x = (0u - (nib & 1u)) & 0x3f800000u;
+          v.y = (0u - ((nib >> 1) & 1u)) & 0x3f800000u;
+          v.z = (0u - ((nib >> 2) & 1u)) & 0x3f800000u;
+          v.w = (0u - ((nib >> 3) & 1u)) & 0x3f800000u;
+          if (slot[c] >= 0) {
+            const uint4 d = *reinterpret_cast<const uint4*>(rec + kRecBits + 4 * slot[c]);
+            v.x |= d.x;
+            v.y |= d.y;
+            v.z |= d.z;
+            v.w |= d.w;
+          }
+          fout[r * kQuads + q] = v;
+        }
+      }
+    } else if (item < count + chunks) {
+      const int w = (item - count) * kTile + lane;
+      if (w < full) {
+        const int b0 = w * 4;
+        const int r = b0 / kActionCount;
+        const int a = b0 - r * kActionCount;
+        u32 packed;
+        if (a + 3 < kActionCount) {
+          const u64* m = t.out.legal[r];
+          const int lo = a >> 6, sh = a & 63;
+          u64 bits = m[lo] >> sh;
+          if (sh > 60) bits |= m[lo + 1] << (64 - sh);
+          packed = spread4((u32)(bits & 0xFu));
+        } else {
+          packed = 0;
+          for (int b = 0; b < 4; ++b) {
+            const int at = b0 + b;
+            const int rr = at / kActionCount;
+            const int aa = at - rr * kActionCount;
+            packed |= (u32)((t.out.legal[rr][aa >> 6] >> (aa & 63)) & 1u) << (8 * b);
+          }
+        }
+        reinterpret_cast<u32*>(lout)[w] = packed;
+      }
     } else {
-      packed = 0;
-      for (int b = 0; b < 4; ++b) {
-        const int at = b0 + b;
-        const int rr = at / kActionCount;
-        const int aa = at - rr * kActionCount;
-        packed |= (u32)((t.out.legal[rr][aa >> 6] >> (aa & 63)) & 1u) << (8 * b);
+      const int at = 4 * full + lane;
+      if (at < bytes) {
+        const int r = at / kActionCount;
+        const int a = at - r * kActionCount;
+        lout[at] = (u8)((t.out.legal[r][a >> 6] >> (a & 63)) & 1u);
       }
     }
-    reinterpret_cast<u32*>(lout)[w] = packed;
-  }
-  for (int at = full * 4 + tid; at < bytes; at += threads) {
-    const int r = at / kActionCount;
-    const int a = at - r * kActionCount;
-    lout[at] = (u8)((t.out.legal[r][a >> 6] >> (a & 63)) & 1u);
   }
 }
 
@@ -221,12 +245,14 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
                                                               i64* actions = nullptr) {
   __shared__ ObserveTile t;
   __shared__ i64 tile_ids[kTile];
+  __shared__ int next_item;  // store_observation's work counter
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int tid = threadIdx.x;
   const int lane = tid & (kTile - 1);
   const int wave = tid / kTile;
   if (kIndexed && tid < count) tile_ids[tid] = ids[base + tid];
+  if (tid == 0) next_item = 0;
   __syncthreads();
   {  // stage the tile's rows, all threads
     const int words = count * kRowWords;
@@ -277,7 +303,7 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
     }
   }
   __syncthreads();
-  store_observation(t, base, count, features, legal, wave, kObsThreads / kTile);
+  store_observation(t, base, count, features, legal, &next_item);
 }
 
 // --------------------------------------------------------------------- step ----
@@ -399,8 +425,9 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
 // auto-reset of finished rows), with the same outputs.  Two waves per tile of 64 games:
 // wave 0 computes the observation records and the actions, then runs the 64 games' steps
 // while wave 1 stores the observation from LDS, so the step's integer work overlaps the
-// HBM-bound feature stores instead of following them.  At ~250 VGPRs two waves fit per
-// SIMD: four tiles per CU, every tile of a 65,536-row batch resident at once.
+// HBM-bound feature stores instead of following them; wave 0 then takes over the stores
+// that are left.  At ~250 VGPRs two waves fit per SIMD: four tiles per CU, every tile of
+// a 65,536-row batch resident at once.
 constexpr int kPlayThreads = 128;
 
 __global__ __launch_bounds__(kPlayThreads) void play_kernel(
@@ -410,11 +437,13 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
   __shared__ ObserveTile t;  // the rows, then the records and masks, then the new rows
   __shared__ int spare_rows[kTile];
   __shared__ int spare_count;
+  __shared__ int next_item;  // store_observation's work counter
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int tid = threadIdx.x;
   const int lane = tid & (kTile - 1);
   const int wave = tid / kTile;
+  if (tid == 0) next_item = 0;
   {
     const u64* src = states + base * kRowWords;
     for (int j = tid; j < count * kRowWords; j += kPlayThreads) t.rows[j] = src[j];
@@ -432,6 +461,7 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
   const i64 i = base + lane;
   i64 a = -1;
   u64 x = 0;
+  PacketHead head{};
   if (active) {
     // The observation reads one copy of the game and the step another: building the
     // packet from the very Env that is then stepped leaves an engine temporary in private
@@ -450,6 +480,7 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
     x = sampler[i];
     a = draw_legal(pk.head.legal.w0, pk.head.legal.w1, pk.head.legal.w2, x);
     actions[i] = a;
+    head = pk.head;
   }
   __syncthreads();
   bool take_spare = false;
@@ -459,7 +490,7 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
   if (wave == 0) {
     if (lane < count) {
       g = e;
-      const StepOut so = torch_step(g, clamp_action(a));
+      const StepOut so = torch_step_head(g, clamp_action(a), head);
       reward[i] = (float)so.reward0;
       done[i] = so.done;
       nagari[i] = so.nagari;
@@ -477,9 +508,8 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
         sampler[i] = x;
       }
     }
-  } else {
-    store_observation(t, base, count, features, legal, wave - 1, kPlayThreads / kTile - 1);
   }
+  store_observation(t, base, count, features, legal, &next_item);  // wave 0 after its step
   __syncthreads();  // records are dead: the region takes the new rows
   if (wave == 0) {
     // a finished game's row takes its next game: the spare (copied below) or a deal here
@@ -505,19 +535,21 @@ __global__ __launch_bounds__(kPlayThreads) void play_kernel(
 // tile of 64 children: wave 0 gathers the parents, steps the clones and builds the
 // children's observation records in LDS; then wave 1 stores the observations while wave 0
 // writes the child rows from registers (each lane its own row), so the children are never
-// read back.
+// read back, and joins the stores after.
 __global__ __launch_bounds__(kPlayThreads) void branch_observe_kernel(
     const u64* parents, i64 env_count, const i64* ids, const i64* actions, i64 n,
     u64* children, float* reward, u8* done, u8* nagari, i16* status, u8* committed,
     float* features, u8* legal, u8* player, u8* obs_done, i16* obs_status) {
   __shared__ ObserveTile t;
   __shared__ i64 tile_ids[kTile];
+  __shared__ int next_item;  // store_observation's work counter
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int tid = threadIdx.x;
   const int lane = tid & (kTile - 1);
   const int wave = tid / kTile;
   if (tid < count) tile_ids[tid] = ids[base + tid];
+  if (tid == 0) next_item = 0;
   __syncthreads();
   stage_in<kPlayThreads>(t.rows, parents, tile_ids, base, count, env_count);
   __syncthreads();
@@ -567,9 +599,8 @@ __global__ __launch_bounds__(kPlayThreads) void branch_observe_kernel(
 #pragma unroll
       for (int k = 0; k < kRowWords; ++k) out[k] = row[k];
     }
-  } else {
-    store_observation(t, base, count, features, legal, wave - 1, kPlayThreads / kTile - 1);
   }
+  store_observation(t, base, count, features, legal, &next_item);  // wave 0 after its rows
 }
 
 // -------------------------------------------------------------------- small ----
