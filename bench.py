@@ -153,32 +153,49 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
     games = int(gen.sum(dtype=torch.int64).item()) - start_games
-    # The observe kernel alone on the loop's live (mid-game) states, whole batch: 50
-    # back-to-back launches between two events on the stream they run on.
+    # Per-kernel durations: launches captured in a HIP graph and replayed between two
+    # events on the stream the replay runs on, so the kernels run back to back (issued
+    # eagerly, a launch of the 43 us observe kernel waits on the host's allocation and
+    # launch instead).
     stream = torch.cuda.current_stream()
-    reps = 50
-    burst = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-    burst[0].record(stream)
-    for _ in range(reps):
-        ext.observe(states)
-    burst[1].record(stream)
-    torch.cuda.synchronize()
-    observe_ms = burst[0].elapsed_time(burst[1]) / reps
-    # play_random alone (one launch per step on the whole batch), continuing the games:
-    # 6 blocks of 8 back-to-back launches, spares refilled between blocks, outside the events.
-    play_ms = None
-    if fused:
+
+    def graph_of(fn, reps: int):
+        fn()  # warm the allocator outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        return g
+
+    def replay_ms(g, before=None, times: int = 1) -> float:
         total = 0.0
-        for _ in range(6):
-            ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch)
+        for _ in range(times):
+            if before is not None:
+                before()
             ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             ev[0].record(stream)
-            for _ in range(REFILL):
-                ext.play_random(states, sampler, SEED_BASE, gen, spares, spare_gen, batch)
+            g.replay()
             ev[1].record(stream)
             torch.cuda.synchronize()
             total += ev[0].elapsed_time(ev[1])
-        play_ms = total / (6 * REFILL)
+        return total
+
+    # The observe kernel alone on the loop's live (mid-game) states, whole batch:
+    # 5 replays of 10 launches.
+    obs = graph_of(lambda: ext.observe(states), 10)
+    observe_ms = replay_ms(obs, times=5) / 50
+    del obs
+    # play_random alone (one launch per step on the whole batch), continuing the games:
+    # 6 replays of 8 launches, spares refilled before each, outside the events.
+    play_ms = None
+    if fused:
+        ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch)
+        play = graph_of(lambda: ext.play_random(states, sampler, SEED_BASE, gen, spares,
+                                                spare_gen, batch), REFILL)
+        refill = lambda: ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch)  # noqa: E731
+        play_ms = replay_ms(play, before=refill, times=6) / (6 * REFILL)
+        del play
     return {"seconds": seconds, "games": games, "observe_ms": observe_ms, "play_ms": play_ms}
 
 

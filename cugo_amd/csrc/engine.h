@@ -638,20 +638,29 @@ CG_HD u8 pi_card_value(u32 card) {  // pi_transfer.h:79-84
   return 1;
 }
 
-// pi_transfer.h:90-110
+// The n lowest set bits of pool.
+CG_HD u64 lowest_bits(u64 pool, u32 n) {
+  if (popc(pool) <= n) return pool;
+  return pool & (bit(select_rank(pool, n)) - 1ull);
+}
+
+// pi_transfer.h:90-110.  Each of the six keys walks the candidates of one pi value,
+// inside or outside the mission cards, in card order and takes them while the count
+// lasts.  A card's pi value is fixed by its id (pi_card_value), so a key's pass is the
+// lowest `count` bits of one mask: six branch-free passes instead of a loop over cards.
 CG_HD u64 hangame_steal_selection(u64 candidates, u64 mission, bool owns_mission, u32 count) {
+  const u64 k3 = bit(kBonus3);
+  const u64 k2 = (bit(kBonus2) | bit(kGukjin) | kDoublePi) & ~k3;
+  const u64 v3 = candidates & k3, v2 = candidates & k2, v1 = candidates & ~(k2 | k3);
   u64 chosen = 0;
-  for (u32 key = 0; key < 6 && count != 0; ++key) {
+#pragma unroll
+  for (u32 key = 0; key < 6; ++key) {
     const bool use_mission = owns_mission ? key >= 3 : (key & 1u) != 0;
     const u32 value = owns_mission ? 1 + key % 3 : 1 + key / 2;
-    u64 pool = candidates & (use_mission ? mission : ~mission);
-    while (pool != 0 && count != 0) {
-      const u32 card = (u32)__builtin_ctzll(pool);
-      pool &= pool - 1;
-      if (pi_card_value(card) != value) continue;
-      chosen |= bit(card);
-      --count;
-    }
+    const u64 vm = value == 1 ? v1 : value == 2 ? v2 : v3;
+    const u64 take = lowest_bits(vm & (use_mission ? mission : ~mission), count);
+    chosen |= take;
+    count -= popc(take);
   }
   return chosen;
 }
