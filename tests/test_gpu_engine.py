@@ -470,3 +470,94 @@ def test_padding_bytes_zero(ext):
     rows = to_np(states)
     for lo, hi in PADDING:
         assert not rows[:, lo:hi].any()
+
+
+def test_play_random_full_batch_matches_oracle(ext, ref):
+    """The random-policy loop at its full size: 65,536 resident games, 24 play_random
+    launches with the spares refilled every 8 (the loop the throughput figure times).
+    Each step's observation, actions and step outputs, and the rows after it, against the
+    oracle playing the same protocol: observe, the uniform legal draw, step, and a
+    finished game's row re-dealt from seed base + i + 65,536 * generation with a fresh
+    sampler.  Most games finish within 24 steps, so spare and inline re-deals both run."""
+    announce("play_random full batch vs oracle")
+    n = 65536
+    seeds, first = c1_seeds(n)
+    states = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(first).to(DEV))
+    host = ref.create(seeds, first)
+    gen = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp = ext.seed_samplers(n, SEED_BASE, gen)
+    sampler = np.array([splitmix_first(int(s) & (2**64 - 1)) for s in seeds], dtype=np.uint64)
+    assert np.array_equal(to_np(smp).view(np.uint64), sampler)
+    spares = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
+    spare_gen = torch.zeros(n, dtype=torch.int32, device=DEV)
+    hgen = np.zeros(n, dtype=np.int64)
+    for step in range(24):
+        if step % 8 == 0:
+            ext.refill_spares(spares, spare_gen, gen, SEED_BASE, n)
+        out = ext.play_random(states, smp, SEED_BASE, gen, spares, spare_gen, n)
+        robs = ref.observe(host)
+        assert_observe_equal(out[:5], robs, f"observation, step {step}")
+        actions = sample_actions(robs[1], sampler, ~robs[3])
+        assert np.array_equal(to_np(out[5]), actions), f"actions, step {step}"
+        rout = ref.step(host, actions)
+        assert_step_equal(out[6:], rout, f"step {step}")
+        ended = np.nonzero(rout[1])[0]
+        hgen[ended] += 1
+        new_seeds = ((np.uint64(SEED_BASE) + ended.astype(np.uint64)
+                      + np.uint64(n) * hgen[ended].astype(np.uint64))).view(np.int64)
+        host[ended] = ref.create(new_seeds, ended & 1)
+        sampler[ended] = [splitmix_first(int(s) & (2**64 - 1)) for s in new_seeds]
+        assert np.array_equal(to_np(states), host), f"rows, step {step}"
+    assert np.array_equal(to_np(gen), hgen)
+    assert np.array_equal(to_np(smp).view(np.uint64), sampler)
+    assert hgen.sum() > n // 2
+
+
+def test_branch_observe_full_batch(ext, ref):
+    """The branch stress at its full size: 4,096 mid-game roots x 256 children (child k of
+    a root takes legal[k] while k < count, else legal[xorshift % count]) through
+    branch_observe_indexed.  32,768 sampled children against the oracle (branch, then
+    observe of the child), and the whole batch equal to branch_indexed followed by
+    observe_indexed; the roots are not modified."""
+    announce("branch_observe full batch")
+    roots_n, per = 4096, 256
+    idx = torch.arange(roots_n, dtype=torch.int64, device=DEV)
+    roots = ext.create(idx * 7919 + SEED_BASE, idx & 1)
+    gen = torch.zeros(roots_n, dtype=torch.int32, device=DEV)
+    smp = ext.seed_samplers(roots_n, SEED_BASE, gen)
+    depth = torch.from_numpy(np.random.default_rng(17).integers(3, 16, roots_n)).to(DEV)
+    for t in range(15):
+        _, legal, _, _, _ = ext.observe(roots)
+        acts = ext.sample_uniform(legal, smp)
+        acts = torch.where(depth > t, acts, torch.full_like(acts, -1))
+        keep = roots.clone()
+        ext.step(roots, acts)
+        roots = torch.where((depth > t).unsqueeze(1), roots, keep)
+    roots_np = to_np(roots)
+    _, legal, _, _, _ = ref.observe(roots_np)
+    g = np.random.default_rng(23)
+    ids = np.repeat(np.arange(roots_n, dtype=np.int64), per)
+    k = np.tile(np.arange(per, dtype=np.int64), roots_n)
+    counts = legal.sum(axis=1)[ids]
+    draw = g.integers(0, 2**62, ids.size)
+    pick = np.where(k < counts, k, draw % np.maximum(counts, 1))
+    order = np.argsort(~legal, axis=1, kind="stable")  # legal actions first, ascending
+    actions = np.where(counts > 0, order[ids, pick], -1).astype(np.int64)
+    ids_t, act_t = torch.from_numpy(ids).to(DEV), torch.from_numpy(actions).to(DEV)
+    before = roots.clone()
+    fused = ext.branch_observe_indexed(roots, ids_t, act_t)
+    assert torch.equal(roots, before)
+    sample = np.sort(g.choice(ids.size, 32768, replace=False))
+    rch = ref.branch(roots_np, ids[sample], actions[sample])
+    assert np.array_equal(to_np(fused[0][torch.from_numpy(sample).to(DEV)]), rch[0])
+    sel = torch.from_numpy(sample).to(DEV)
+    assert_step_equal([t[sel] for t in fused[1:6]], rch[1:], "sampled children")
+    robs = ref.observe(rch[0])
+    assert_observe_equal([t[sel] for t in fused[6:11]], robs, "sampled children's observation")
+    br = ext.branch_indexed(roots, ids_t, act_t)
+    for j, want in enumerate(br):
+        assert torch.equal(fused[j], want), j
+    del br
+    ob = ext.observe_indexed(fused[0], torch.arange(ids.size, device=DEV))
+    for j, want in enumerate(ob):
+        assert torch.equal(fused[6 + j], want), j
