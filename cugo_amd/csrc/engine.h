@@ -837,13 +837,35 @@ CG_HD u16 legal_special_months(const Env& e, u32 hand_count, u32 floor_count, bo
   return (u16)(months_with_count(month_counts(h), hand_count) &
                months_with_count(month_counts(f), floor_count) & ~old & 0x0FFFu);
 }
-CG_HD u16 legal_shake_months(const Env& e) {  // special50.h:92-95
-  return (u16)(legal_special_months(e, 3, 0, true) | legal_special_months(e, 4, 0, true));
+// months whose count nibble equals k, as the low bit of each month nibble
+CG_HD u64 count_is(u64 counts, u32 k) {
+  const u64 d = counts ^ (kNibbleLow * k);
+  return ~(d | (d >> 1) | (d >> 2)) & kNibbleLow;
 }
-CG_HD u16 legal_bomb_months(const Env& e) { return legal_special_months(e, 3, 1, false); }
-CG_HD u16 legal_grenade_months(const Env& e) { return legal_special_months(e, 2, 2, false); }
+
+// The three special-play month sets of special50.h:71-95 from one count of the hand and
+// the floor: bombs (3 in hand, 1 on the floor), grenades (2 and 2) and shakes (3 or 4 in
+// hand, none on the floor, not shaken before with that count), each
+// legal_special_months(e, ...) of the matching arguments.
+struct SpecialMonths { u16 bombs, grenades, shakes; };
+CG_HD SpecialMonths special_months(const Env& e) {
+  if (!special_ready(e)) return SpecialMonths{0, 0, 0};
+  const u64 hc = month_counts(active_hand(e));
+  const u64 fc = month_counts(std_floor(e));
+  const u64 h3 = count_is(hc, 3), f0 = count_is(fc, 0);
+  SpecialMonths s;
+  s.bombs = (u16)(gather_months(h3 & count_is(fc, 1)) & 0x0FFFu);
+  s.grenades = (u16)(gather_months(count_is(hc, 2) & count_is(fc, 2)) & 0x0FFFu);
+  s.shakes = (u16)(((gather_months(h3 & f0) & ~shaken_of(e, e.actor)) |
+                    (gather_months(count_is(hc, 4) & f0) & ~sh4_of(e, e.actor))) & 0x0FFFu);
+  return s;
+}
+CG_HD u16 legal_shake_months(const Env& e) { return special_months(e).shakes; }  // 92-95
+CG_HD u16 legal_bomb_months(const Env& e) { return special_months(e).bombs; }
+CG_HD u16 legal_grenade_months(const Env& e) { return special_months(e).grenades; }
 CG_HD u16 forced_special_months(const Env& e) {
-  return (u16)(legal_bomb_months(e) | legal_grenade_months(e));
+  const SpecialMonths s = special_months(e);
+  return (u16)(s.bombs | s.grenades);
 }
 CG_HD u8 shake_count(const Env& e, u32 p) {  // special50.h:107-110
   return (u8)(popc(shaken_of(e, p)) + popc(sh4_of(e, p)));
@@ -1344,10 +1366,9 @@ CG_HD Mask3 legal_primary(const Env& e) {
   if (d != kDecPrimary) return m;
   const u64 hand = active_hand(e);
   if (e.stock == 0) return m;
-  const u16 bombs = legal_bomb_months(e);
-  const u16 grenades = legal_grenade_months(e);
+  const SpecialMonths sp = special_months(e);
+  const u16 bombs = sp.bombs, grenades = sp.grenades, shakes = sp.shakes;
   const u16 forced = (u16)(bombs | grenades);
-  const u16 shakes = legal_shake_months(e);
   u64 standard = hand & kStdMask;
   // card plays 0..47 (one bit per card, minus forced months)
   const u64 plays = standard & ~month_cards_of(forced);
