@@ -486,11 +486,11 @@ CG_HD void finish_resolved_turn(Env& e) {  // turn50.h:409-416
   ++e.turn;
 }
 
-// turn50.h:418-508 (transactional: `e` changes only on success).
+// turn50.h:418-508.  On failure `e` may be partly changed: callers discard it.
 CG_HD Resolve resolve_turn(Env& e, u8 played_choice, u8 drawn_choice) {
   Resolve r{kResWrongPhase, 0, 0, 0, 0, 0};
   if (e.phase != kPhaseResolve) return r;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 played = n.pplayed, drawn = n.pdrawn;
   const u64 pm = floor_matches(n, played);
   const u32 pmc = popc(pm);
@@ -529,7 +529,6 @@ CG_HD Resolve resolve_turn(Env& e, u8 played_choice, u8 drawn_choice) {
   }
   if (n.floor == 0 && r.captured != 0) r.events |= kEvSweep;  // turn50.h:499-502
   finish_resolved_turn(n);
-  e = n;
   r.status = kResOk;
   return r;
 }
@@ -704,22 +703,21 @@ CG_HD PiResult apply_pi_steal(Env& e, u32 thief, u8 requested, u64 selection) {
   return PiResult{kPiOk, requested, available, transfer};
 }
 
-// pi_transfer.h:234-255: resolve, then steal; all or nothing.
+// pi_transfer.h:234-255: resolve, then steal (on failure the caller discards `e`).
 CG_HD Resolve resolve_turn_with_pi(Env& e, u8 pchoice, u8 dchoice, u64 sel, PiResult& pt) {
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 thief = e.actor;
   const Resolve r = resolve_turn(n, pchoice, dchoice);
   pt = PiResult{kPiOk, 0, 0, 0};
   if (r.status != kResOk) return r;
   pt = apply_pi_steal(n, thief, steal_count(r), sel);
   if (pt.status != kPiOk) return r;
-  e = n;
   return r;
 }
 
 // pi_transfer.h:274-294
 CG_HD u8 play_bonus_with_pi(Env& e, u8 bonus, u64 sel, PiResult& pt, u8& replacement) {
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 thief = e.actor;
   u8 steal;
   const u8 s = play_bonus_for_turn(n, bonus, steal, replacement);
@@ -727,7 +725,6 @@ CG_HD u8 play_bonus_with_pi(Env& e, u8 bonus, u64 sel, PiResult& pt, u8& replace
   if (s != kTurnOk) return s;
   pt = apply_pi_steal(n, thief, steal, sel);
   if (pt.status != kPiOk) return s;
-  e = n;
   return s;
 }
 
@@ -815,11 +812,10 @@ CG_HD Resolve resolve_game_turn(Env& e, u8 pchoice, u8 dchoice, u64 sel, PiResul
   pt = PiResult{kPiOk, 0, 0, 0};
   if (game_finished(e) || has_pending_choice(e)) return resolve_error(kResWrongPhase);
   const u8 completed = e.actor;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const Resolve r = resolve_turn_with_pi(n, pchoice, dchoice, sel, pt);
   if (r.status != kResOk || pt.status != kPiOk) return r;
   finish_turn_game(n, completed);
-  e = n;
   return r;
 }
 
@@ -913,12 +909,11 @@ CG_HD u8 begin_shake(Env& e, u8 card) {
   const u16 mb = month_bit(card);
   const u64 hand = active_hand(e);
   if ((legal_shake_months(e) & mb) == 0 || (hand & bit(card)) == 0) return kSpNotLegal;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const bool four = popc(hand & month_cards(card >> 2)) == 4;
   if (four) { if (n.actor == 0) n.sh4_0 |= mb; else n.sh4_1 |= mb; }
   else { if (n.actor == 0) n.shaken0 |= mb; else n.shaken1 |= mb; }
   if (begin_regular_play_game(n, card) != kTurnOk) return kSpNotLegal;
-  e = n;
   return kSpOk;
 }
 
@@ -935,7 +930,7 @@ CG_HD u8 capture_special(Env& e, u8 month, bool grenade, u8 choice, u64 sel, PiR
   const u16 mb = (u16)(1u << month);
   const u16 legal = grenade ? legal_grenade_months(e) : legal_bomb_months(e);
   if ((legal & mb) == 0) return kSpNotLegal;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 actor = n.actor;
   const u64 hand = hand_of(n, actor);
   const u64 hc = hand & month_cards(month);
@@ -952,7 +947,6 @@ CG_HD u8 capture_special(Env& e, u8 month, bool grenade, u8 choice, u64 sel, PiR
   pt = apply_pi_steal(n, actor, steal, sel);
   if (pt.status != kPiOk) return pi_to_special(pt.status);
   finish_turn_game(n, actor);
-  e = n;
   return kSpOk;
 }
 
@@ -962,7 +956,7 @@ CG_HD u8 play_bomb_credit(Env& e, u8 choice, u64 sel, PiResult& pt) {
   if (!special_ready(e)) return kSpWrongPhase;
   const u8 actor = e.actor;
   if (!cred_of(e, actor)) return kSpNotLegal;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   set_cred(n, actor, (u8)(cred_of(n, actor) - 1u));
   const DrawOnly d = draw_only_special(n, choice);
   if (d.status != kSpOk) return d.status;
@@ -971,7 +965,6 @@ CG_HD u8 play_bomb_credit(Env& e, u8 choice, u64 sel, PiResult& pt) {
   pt = apply_pi_steal(n, actor, steal, sel);
   if (pt.status != kPiOk) return pi_to_special(pt.status);
   finish_turn_game(n, actor);
-  e = n;
   return kSpOk;
 }
 
@@ -1131,7 +1124,7 @@ CG_HD u8 play_bonus_terminal(Env& e, u8 bonus, u64 sel, PiResult& pt) {
   pt = PiResult{kPiOk, 0, 0, 0};
   if (terminal_finished(e) || has_ct_choice(e)) return kTurnWrongPhase;
   if (game_finished(e) || has_pending_choice(e)) return kTurnWrongPhase;  // game50.h:263-267
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 actor = n.actor;
   const u16 before = chongtong_months(active_hand(n));
   u8 replacement;
@@ -1140,7 +1133,6 @@ CG_HD u8 play_bonus_terminal(Env& e, u8 bonus, u64 sel, PiResult& pt) {
   if (pt.transfer != 0) update_missions(n, actor, pt.transfer);
   const u16 after = chongtong_months(active_hand(n));
   open_bonus_chongtong_choice(n, actor, (u16)(after & ~before));
-  e = n;
   return s;
 }
 
@@ -1148,7 +1140,7 @@ CG_HD u8 play_bonus_terminal(Env& e, u8 bonus, u64 sel, PiResult& pt) {
 CG_HD Resolve resolve_terminal_turn(Env& e, u8 pchoice, u8 dchoice, u64 sel, PiResult& pt) {
   pt = PiResult{kPiOk, 0, 0, 0};
   if (terminal_finished(e) || has_ct_choice(e)) return resolve_error(kResWrongPhase);
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 actor = n.actor;
   const u64 before = cap_of(n, actor);
   const Resolve r = resolve_game_turn(n, pchoice, dchoice, sel, pt);
@@ -1157,14 +1149,13 @@ CG_HD Resolve resolve_terminal_turn(Env& e, u8 pchoice, u8 dchoice, u64 sel, PiR
   update_missions(n, actor, cap_of(n, actor) & ~before);
   record_completed_turn_ppuk(n, actor, (r.events & kEvPpuk) != 0);
   sync_game_stop(n);
-  e = n;
   return r;
 }
 
 // terminal50.h:505-530 for bomb/grenade/bomb-credit (shake handled by its caller).
 CG_HD u8 apply_terminal_special(Env& e, u8 kind, u8 month, u8 choice, u64 sel) {
   if (terminal_finished(e) || has_ct_choice(e)) return kSpWrongPhase;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 actor = n.actor;
   const u64 before = cap_of(n, actor);
   PiResult pt;
@@ -1174,7 +1165,6 @@ CG_HD u8 apply_terminal_special(Env& e, u8 kind, u8 month, u8 choice, u64 sel) {
   if (s != kSpOk) return s;
   update_missions(n, actor, cap_of(n, actor) & ~before);
   sync_game_stop(n);
-  e = n;
   return kSpOk;
 }
 
@@ -1185,21 +1175,19 @@ CG_HD u8 apply_terminal_shake(Env& e, u8 card) {  // terminal50.h:505-530, kShak
 
 CG_HD u8 apply_terminal_gukjin(Env& e, bool as_pi) {  // terminal50.h:532-544
   if (terminal_finished(e) || has_ct_choice(e)) return 2;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 s = apply_gukjin_decision(n, as_pi);
   if (s != 0) return s;
   sync_game_stop(n);
-  e = n;
   return 0;
 }
 
 CG_HD u8 apply_terminal_go_stop(Env& e, bool stop) {  // terminal50.h:546-559
   if (terminal_finished(e) || has_ct_choice(e)) return 2;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   const u8 s = apply_go_stop(n, stop);
   if (s != 0) return s;
   sync_game_stop(n);
-  e = n;
   return 0;
 }
 
@@ -1278,7 +1266,7 @@ CG_HD u8 map_special(u8 s) {  // rollout50.h:207-223
 CG_HD u8 apply_action(Env& e, const Action& a) {
   const u8 actor = e.actor;
   if (terminal_finished(e)) return kGameFinished;
-  Env n = e;
+  Env& n = e;  // in place: the caller's copy is the transaction
   n.held0 |= n.hand0;
   n.held1 |= n.hand1;
   u8 status = kOk;
@@ -1322,7 +1310,6 @@ CG_HD u8 apply_action(Env& e, const Action& a) {
   }
   n.held0 |= n.hand0;  // apply_action50 (rollout50.h:391-399)
   n.held1 |= n.hand1;
-  e = n;
   return kOk;
 }
 
@@ -1710,13 +1697,16 @@ CG_HD Probe probe_postchance(const Env& e, const Pending& p, Env& staged) {
   }
 }
 
-// postchance50.h:509-539.  Returns the ActionStatus50; committed set on commit.
-// postchance50.h:509-539.  The reference probes the staged action and then applies it.
-// apply_action is transactional and fails wherever the probe would stop the action (a
-// floor choice still open, an empty stock, an invalid choice), so with no pi card
-// selected the action is applied first and the probe runs only when the apply fails;
-// a pi selection (which the probe checks more strictly than the transfer) keeps the
-// reference order.  Same status, same state, same commit in every case.
+// postchance50.h:509-539.  Returns the ActionStatus50; committed set on commit.  The
+// reference probes the staged action and then applies it.  apply_action fails wherever
+// the probe would stop the action (a floor choice still open, an empty stock, an invalid
+// choice), so with no pi card selected the action is applied first and the probe runs
+// only when the apply fails; a pi selection (which the probe checks more strictly than
+// the transfer) keeps the reference order.  Same status, same state, same commit in
+// every case.  Both applies run on a copy that is kept only on success: apply_action and
+// every transition under it work in place and return a failure status as soon as one
+// step fails, so this copy is the whole action's transaction (apply_action50 copies the
+// state once, rollout50.h:238).
 CG_HD u8 continue_postchance(Env& e, bool& committed) {
   committed = false;
   Pending p = pending_of(e);
@@ -1740,8 +1730,10 @@ CG_HD u8 continue_postchance(Env& e, bool& committed) {
   if (probe.status != kOk) return probe.status;
   if (probe.decision != kDecNone) return kOk;
   if (p.sel_pi == 0) return s;  // the apply above failed with `s`
-  s = apply_action(e, a);
+  Env applied = e;
+  s = apply_action(applied, a);
   if (s != kOk) return s;
+  e = applied;
   p.action = a;
   p.active = 0;
   set_pending(e, p);
@@ -2199,26 +2191,29 @@ CG_HD float feature_at(const u64* w, const float* d, u32 f) {
 }
 
 
-// Per-row dword record read by the GPU feature writer, laid out so that a lane turns
-// one record read into four consecutive features.  Feature quad q (features 4q..4q+3,
-// 180 quads) is one nibble of a 720-bit array in feature order - bit f is feature f for
-// a 0/1 feature, 0 for a dense one - at dword q / 8, bits 4 (q % 8) .. 4 (q % 8) + 3.  The
-// 16 quads that hold dense features also own four dwords of a dense section: the float
-// bits of each dense feature, 0 for the 0/1 features beside it.  A quad's floats are the
-// nibble's 0 / 1.0f bit patterns ORed with its dense dwords, which is exact for every
-// value (signed zeros included).
-constexpr int kRecBits = 24;        // 23 dwords of the 720-bit array, one pad
-constexpr int kRecDenseQuads = 16;
-constexpr int kFeatRecord = kRecBits + 4 * kRecDenseQuads;  // 88 dwords
+// Per-row dword record read by the GPU feature writer, laid out so that a lane turns a
+// few record reads into four consecutive features.  The 720 features in feature order as
+// a bit array: bit f is feature f for every feature that is 0 or 1 (the planes and the
+// 0/1 flags and one-hots among the scalars), 0 for the others; feature quad q (features
+// 4q..4q+3) is one nibble, at dword q / 8, bits 4 (q % 8) .. 4 (q % 8) + 3.  Then the float
+// bits of the 37 other scalars, in feature order (dense_pos).  A feature is its bit's
+// 0 / 1.0f pattern ORed with its dense dword (0 where it has none), which is exact for
+// every value, signed zeros included.
+constexpr int kRecBits = 23;   // 720 bits
+constexpr int kRecDense = 37;
+constexpr int kFeatRecord = kRecBits + kRecDense;  // 60 dwords
 constexpr u32 kFeatQuads = 180;
 
-// Slot of quad q in the dense section, or -1: quads 111-119 (features 444-479),
-// 122-123 (488-495), 136-139 (544-559) and 177 (708-711).
-CG_HD int dense_slot(u32 q) {
-  if (q >= 111 && q <= 119) return (int)(q - 111);
-  if (q == 122 || q == 123) return (int)(q - 122 + 9);
-  if (q >= 136 && q <= 139) return (int)(q - 136 + 11);
-  if (q == 177) return 15;
+// Position of feature f among the dense dwords, or -1 for a 0/1 feature or the padding:
+// 452-468, 471-478 (scalars), 491-495 (counts), 549-551 and 556-557 (extension scalars),
+// 710-711 (ribbons).
+CG_HD int dense_pos(u32 f) {
+  if (f >= 452 && f <= 468) return (int)(f - 452);
+  if (f >= 471 && f <= 478) return (int)(17 + (f - 471));
+  if (f >= 491 && f <= 495) return (int)(25 + (f - 491));
+  if (f >= 549 && f <= 551) return (int)(30 + (f - 549));
+  if (f == 556 || f == 557) return (int)(33 + (f - 556));
+  if (f == 710 || f == 711) return (int)(35 + (f - 710));
   return -1;
 }
 
@@ -2229,6 +2224,9 @@ CG_HD void put_bits(u64* acc, u32 pos, u64 v, u32 n) {
   acc[k] |= v << s;
   if (s != 0 && s + n > 64u) acc[k + 1] |= v >> (64u - s);
 }
+
+// 1 when a 0/1 scalar is 1.0f.
+CG_HD u64 flag_bit(float v) { return v != 0.0f ? 1ull : 0ull; }
 
 // Every index below is a constant, so the row stays in registers.
 CG_HD void feature_record(const FeatRow& r, u32* rec) {
@@ -2244,22 +2242,34 @@ CG_HD void feature_record(const FeatRow& r, u32* rec) {
   put_bits(acc, 496, r.w[16], 48);                                           // 496-543
 #pragma unroll
   for (int p = 0; p < 3; ++p) put_bits(acc, 560u + 50u * p, r.w[17 + p], 50);  // 560-709
+  // the 0/1 scalars (feature f = dense index + 446, 491 or 544 - 38 as in feature_at)
+  const float* d = r.d;
+#pragma unroll
+  for (int k = 0; k <= 5; ++k) put_bits(acc, 446u + k, flag_bit(d[k]), 1);  // 446-451
+  put_bits(acc, 469, flag_bit(d[23]), 1);
+  put_bits(acc, 470, flag_bit(d[24]), 1);
+#pragma unroll
+  for (int k = 0; k < 5; ++k) put_bits(acc, 544u + k, flag_bit(d[38 + k]), 1);  // 544-548
+#pragma unroll
+  for (int k = 0; k < 4; ++k) put_bits(acc, 552u + k, flag_bit(d[46 + k]), 1);  // 552-555
+  put_bits(acc, 558, flag_bit(d[52]), 1);
+  put_bits(acc, 559, flag_bit(d[53]), 1);
 #pragma unroll
   for (int k = 0; k < kRecBits; ++k) rec[k] = (u32)(acc[k >> 1] >> (32 * (k & 1)));
-  // dense section, slot by slot: features 444-479 (dense 446-478 = d[0..32]),
-  // 488-495 (491-495 = d[33..37]), 544-559 (d[38..53]), 708-711 (710-711 = d[54..55])
+  // the other scalars, in feature order
   u32* dn = rec + kRecBits;
-  dn[0] = dn[1] = dn[35] = 0u;
 #pragma unroll
-  for (int k = 0; k < 33; ++k) dn[2 + k] = __builtin_bit_cast(u32, r.d[k]);
-  dn[36] = dn[37] = dn[38] = 0u;
+  for (int k = 0; k < 17; ++k) dn[k] = __builtin_bit_cast(u32, d[6 + k]);        // 452-468
 #pragma unroll
-  for (int k = 0; k < 5; ++k) dn[39 + k] = __builtin_bit_cast(u32, r.d[33 + k]);
+  for (int k = 0; k < 8; ++k) dn[17 + k] = __builtin_bit_cast(u32, d[25 + k]);   // 471-478
 #pragma unroll
-  for (int k = 0; k < 16; ++k) dn[44 + k] = __builtin_bit_cast(u32, r.d[38 + k]);
-  dn[60] = dn[61] = 0u;
-  dn[62] = __builtin_bit_cast(u32, r.d[54]);
-  dn[63] = __builtin_bit_cast(u32, r.d[55]);
+  for (int k = 0; k < 5; ++k) dn[25 + k] = __builtin_bit_cast(u32, d[33 + k]);   // 491-495
+#pragma unroll
+  for (int k = 0; k < 3; ++k) dn[30 + k] = __builtin_bit_cast(u32, d[43 + k]);   // 549-551
+  dn[33] = __builtin_bit_cast(u32, d[50]);                                       // 556
+  dn[34] = __builtin_bit_cast(u32, d[51]);                                       // 557
+  dn[35] = __builtin_bit_cast(u32, d[54]);                                       // 710
+  dn[36] = __builtin_bit_cast(u32, d[55]);                                       // 711
 }
 
 }  // namespace cugo_amd

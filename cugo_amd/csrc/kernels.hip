@@ -94,11 +94,12 @@ __global__ __launch_bounds__(kTile) void create_kernel(const i64* seeds, const i
 // ------------------------------------------------------------------ observe ----
 // LDS of one observe tile: the staged rows are dead once every lane has unpacked its
 // row, so the per-row feature records and masks reuse the same bytes.
-struct alignas(16) ObserveTile {
+constexpr int kRecStride = kFeatRecord + 1;  // odd: a lane's own row, no bank conflicts
+struct ObserveTile {
   union {
     u64 rows[kTileWords];
     struct {
-      u32 rec[kTile][kFeatRecord];  // 16-byte aligned rows: dense quads load as one uint4
+      u32 rec[kTile][kRecStride];
       u64 legal[kTile][3];
     } out;
   };
@@ -114,7 +115,7 @@ __device__ inline u32 spread4(u32 x) {
 // were written) until none is left: items 0 .. count - 1 are feature rows (lane owns the
 // float4 columns q = lane, lane + 64, lane + 128 < 180 of the row, so a store instruction
 // covers 1 KiB; a column is one nibble of the record's bit array, ORed with the record's
-// dense dwords for the 16 columns that hold dense features), then 64-dword chunks of the
+// dense dwords for the 12 columns that hold other scalars), then 64-dword chunks of the
 // legal mask bytes, then their unaligned tail.  A wave that arrives late (one that also
 // stepped the games) takes what is left, so no wave idles while another stores alone.
 // The claiming lane is the wave's first active lane, and every pass raises the counter,
@@ -123,11 +124,12 @@ __device__ inline void store_observation(const ObserveTile& t, i64 base, int cou
                                          float* features, u8* legal, int* next) {
   const int lane = threadIdx.x & (kTile - 1);
   constexpr int kQuads = kFeatureCount / 4;  // 180
-  int slot[3];
-  for (int c = 0; c < 3; ++c) {
-    const int q = lane + kTile * c;
-    slot[c] = q < kQuads ? dense_slot((u32)q) : -1;
-  }
+  int dpos[3][4];  // each of the lane's columns: its features' dense dwords (or -1)
+  for (int c = 0; c < 3; ++c)
+    for (int k = 0; k < 4; ++k) {
+      const int q = lane + kTile * c;
+      dpos[c][k] = q < kQuads ? dense_pos((u32)(4 * q + k)) : -1;
+    }
   uint4* fout = reinterpret_cast<uint4*>(features + base * kFeatureCount);
   // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0); word
   // w holds tile bytes 4w..4w+3, i.e. actions a..a+3 of row r unless it straddles rows.
@@ -154,13 +156,10 @@ __device__ inline void store_observation(const ObserveTile& t, i64 base, int cou
           v.y = (0u - ((nib >> 1) & 1u)) & 0x3f800000u;
           v.z = (0u - ((nib >> 2) & 1u)) & 0x3f800000u;
           v.w = (0u - ((nib >> 3) & 1u)) & 0x3f800000u;
-          if (slot[c] >= 0) {
-            const uint4 d = *reinterpret_cast<const uint4*>(rec + kRecBits + 4 * slot[c]);
-            v.x |= d.x;
-            v.y |= d.y;
-            v.z |= d.z;
-            v.w |= d.w;
-          }
+          if (dpos[c][0] >= 0) v.x |= rec[kRecBits + dpos[c][0]];
+          if (dpos[c][1] >= 0) v.y |= rec[kRecBits + dpos[c][1]];
+          if (dpos[c][2] >= 0) v.z |= rec[kRecBits + dpos[c][2]];
+          if (dpos[c][3] >= 0) v.w |= rec[kRecBits + dpos[c][3]];
           fout[r * kQuads + q] = v;
         }
       }
