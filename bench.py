@@ -37,11 +37,17 @@ SEED_BASE = 0x243F6A8885A308D3
 HBM_PEAK_GBS = 8000.0
 REFILL = 8  # steps between batched pre-deals of the next games
 OBSERVE_BYTES_PER_ROW = 248 + 720 * 4 + 179 + 1 + 1 + 2  # 3,311
-# play_random per row: state read and written (2 x 248), the observation (2,880 + 179 + 4),
-# the sampler word read and written (16), the action (8), the step outputs (9), the
-# generation and spare generation read (8); a finished row's spare (248 B for ~5 % of rows
-# a step) is left out.
-PLAY_BYTES_PER_ROW = 2 * 248 + 720 * 4 + 179 + 4 + 16 + 8 + 9 + 8  # 3,600
+# play_random per row: every step writes the observation (2,880 + 179 + 4), the action (8)
+# and the step outputs (9); once per launch the state is read and written (2 x 248), the
+# sampler word read and written (16) and the generation read and written (8).  A finished
+# row's spare (248 B for ~5 % of rows a step) is left out.
+PLAY_STEP_BYTES_PER_ROW = 720 * 4 + 179 + 4 + 8 + 9  # 3,080
+PLAY_LAUNCH_BYTES_PER_ROW = 2 * 248 + 16 + 8  # 520
+
+
+def play_bytes_per_row(steps: int) -> int:
+    """Algorithmic bytes per row of one play_random launch of `steps` steps."""
+    return steps * PLAY_STEP_BYTES_PER_ROW + PLAY_LAUNCH_BYTES_PER_ROW
 STEP_BYTES_PER_ROW = 248 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # 513
 BRANCH_BYTES_PER_CHILD = 8 + 8 + 248 + 4 + 1 + 1 + 2 + 1  # parent reads hit L2: 273
 
@@ -87,7 +93,8 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
                   graph: bool, fused: bool = True) -> dict:
     """The timed loop.  The batch is cut into `streams` contiguous slices (even length),
     each stepped on its own default-priority stream; REFILL steps of every slice form one
-    block, captured once as a HIP graph and replayed (or issued eagerly with graph=False).
+    block (the spares refill, then one play_random launch of REFILL steps), captured once
+    as a HIP graph and replayed (or issued eagerly with graph=False).
     Every slice deals the same games the unsliced batch would: seed = base + global row +
     batch * generation."""
     dev = torch.device("cuda")
@@ -114,17 +121,17 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
             st, g, sm, sp, sg = states[r], gen[r], sampler[r], spares[r], spare_gen[r]
             base = SEED_BASE + k * width
             with torch.cuda.stream(s):
-                for t in range(nsteps):
+                if fused and nsteps:
+                    # nsteps x (observe + draw + step + auto-reset) in one launch
+                    ext.refill_spares(sp, sg, g, base, batch)
+                    ext.play_random(st, sm, base, g, sp, sg, batch, nsteps)
+                for t in range(0 if fused else nsteps):
                     if t == 0:
                         ext.refill_spares(sp, sg, g, base, batch)
-                    if fused:
-                        # observe + draw + step + auto-reset in one launch
-                        ext.play_random(st, sm, base, g, sp, sg, batch)
-                    else:
-                        # observe + the random policy's draw from the legal mask, one launch
-                        _, _, _, _, _, actions = ext.observe_sample(st, sm)
-                        # step + auto-reset of the finished rows from their spares
-                        ext.step_reset_spares(st, actions, base, g, sm, sp, sg, batch)
+                    # observe + the random policy's draw from the legal mask, one launch
+                    _, _, _, _, _, actions = ext.observe_sample(st, sm)
+                    # step + auto-reset of the finished rows from their spares
+                    ext.step_reset_spares(st, actions, base, g, sm, sp, sg, batch)
         for s in side:
             cur.wait_stream(s)
 
@@ -186,16 +193,29 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     obs = graph_of(lambda: ext.observe(states), 10)
     observe_ms = replay_ms(obs, times=5) / 50
     del obs
-    # play_random alone (one launch per step on the whole batch), continuing the games:
-    # 6 replays of 8 launches, spares refilled before each, outside the events.
+    # play_random alone (one launch of REFILL steps on the whole batch, as in the loop),
+    # continuing the games: 6 back-to-back replays of the loop's block (refill_spares, then
+    # the launch) less 6 of refill_spares alone, so that only the first replay's submission
+    # falls between the events.
     play_ms = None
     if fused:
-        ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch)
-        play = graph_of(lambda: ext.play_random(states, sampler, SEED_BASE, gen, spares,
-                                                spare_gen, batch), REFILL)
-        refill = lambda: ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch)  # noqa: E731
-        play_ms = replay_ms(play, before=refill, times=6) / (6 * REFILL)
-        del play
+        def block_once():
+            ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch)
+            ext.play_random(states, sampler, SEED_BASE, gen, spares, spare_gen, batch, REFILL)
+
+        def six(g) -> float:
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record(stream)
+            for _ in range(6):
+                g.replay()
+            ev[1].record(stream)
+            torch.cuda.synchronize()
+            return ev[0].elapsed_time(ev[1])
+
+        blocks = graph_of(block_once, 1)
+        refills = graph_of(lambda: ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch), 1)
+        play_ms = (six(blocks) - six(refills)) / 6
+        del blocks, refills
     return {"seconds": seconds, "games": games, "observe_ms": observe_ms, "play_ms": play_ms}
 
 
@@ -679,13 +699,15 @@ def main() -> None:
                         "bytes_per_row": OBSERVE_BYTES_PER_ROW,
                         "avg_launch_ms": round(rp["observe_ms"], 4)}
     if rp["play_ms"] is not None:
-        play_gbs = args.batch * PLAY_BYTES_PER_ROW / (rp["play_ms"] * 1e-3) / 1e9
+        play_bytes = play_bytes_per_row(REFILL)
+        play_gbs = args.batch * play_bytes / (rp["play_ms"] * 1e-3) / 1e9
         roofline = {"kernel": "play_kernel", "bound": "hbm",
                     "achieved": round(play_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(play_gbs / HBM_PEAK_GBS, 4),
-                    "traffic": measured_traffic("play_kernel", str(args.batch)),
-                    "bytes_per_row": PLAY_BYTES_PER_ROW,
-                    "avg_launch_ms": round(rp["play_ms"], 4)}
+                    "traffic": measured_traffic("play_kernel", f"{args.batch} x {REFILL}"),
+                    "bytes_per_row": play_bytes, "steps_per_launch": REFILL,
+                    "avg_launch_ms": round(rp["play_ms"], 4),
+                    "ms_per_step": round(rp["play_ms"] / REFILL, 4)}
     else:
         roofline = observe_roofline
     result = {
@@ -703,7 +725,8 @@ def main() -> None:
         "data": "synthetic",
         "config": {"workload": "random-policy self-play: observe -> sample -> step -> "
                                "auto-reset, "
-                               + ("one play_random launch per step" if not args.two_launch
+                               + (f"one play_random launch per {REFILL} steps (every step's "
+                                  "observation written)" if not args.two_launch
                                   else "observe_sample + step_reset_spares per step"),
                    "batch": args.batch, "seed_base": hex(SEED_BASE),
                    "policy": "uniform legal action, per-game xorshift64",

@@ -95,13 +95,14 @@ __global__ __launch_bounds__(kTile) void create_kernel(const i64* seeds, const i
 // LDS of one observe tile: the staged rows are dead once every lane has unpacked its
 // row, so the per-row feature records and masks reuse the same bytes.
 constexpr int kRecStride = kFeatRecord + 1;  // odd: a lane's own row, no bank conflicts
+struct RecordBuffer {  // one step's observation of a tile, before it is stored
+  u32 rec[kTile][kRecStride];
+  u64 legal[kTile][3];
+};
 struct ObserveTile {
   union {
     u64 rows[kTileWords];
-    struct {
-      u32 rec[kTile][kRecStride];
-      u64 legal[kTile][3];
-    } out;
+    RecordBuffer out;
   };
 };
 
@@ -120,7 +121,7 @@ __device__ inline u32 spread4(u32 x) {
 // stepped the games) takes what is left, so no wave idles while another stores alone.
 // The claiming lane is the wave's first active lane, and every pass raises the counter,
 // so every wave leaves the loop.
-__device__ inline void store_observation(const ObserveTile& t, i64 base, int count,
+__device__ inline void store_observation(const RecordBuffer& t, i64 base, int count,
                                          float* features, u8* legal, int* next) {
   const int lane = threadIdx.x & (kTile - 1);
   constexpr int kQuads = kFeatureCount / 4;  // 180
@@ -146,7 +147,7 @@ __device__ inline void store_observation(const ObserveTile& t, i64 base, int cou
     if (item >= items) break;
     if (item < count) {
       const int r = item;
-      const u32* rec = t.out.rec[r];
+      const u32* rec = t.rec[r];
       for (int c = 0; c < 3; ++c) {
         const int q = lane + kTile * c;
         if (q < kQuads) {
@@ -171,7 +172,7 @@ __device__ inline void store_observation(const ObserveTile& t, i64 base, int cou
         const int a = b0 - r * kActionCount;
         u32 packed;
         if (a + 3 < kActionCount) {
-          const u64* m = t.out.legal[r];
+          const u64* m = t.legal[r];
           const int lo = a >> 6, sh = a & 63;
           u64 bits = m[lo] >> sh;
           if (sh > 60) bits |= m[lo + 1] << (64 - sh);
@@ -182,7 +183,7 @@ __device__ inline void store_observation(const ObserveTile& t, i64 base, int cou
             const int at = b0 + b;
             const int rr = at / kActionCount;
             const int aa = at - rr * kActionCount;
-            packed |= (u32)((t.out.legal[rr][aa >> 6] >> (aa & 63)) & 1u) << (8 * b);
+            packed |= (u32)((t.legal[rr][aa >> 6] >> (aa & 63)) & 1u) << (8 * b);
           }
         }
         reinterpret_cast<u32*>(lout)[w] = packed;
@@ -192,7 +193,7 @@ __device__ inline void store_observation(const ObserveTile& t, i64 base, int cou
       if (at < bytes) {
         const int r = at / kActionCount;
         const int a = at - r * kActionCount;
-        lout[at] = (u8)((t.out.legal[r][a >> 6] >> (a & 63)) & 1u);
+        lout[at] = (u8)((t.legal[r][a >> 6] >> (a & 63)) & 1u);
       }
     }
   }
@@ -302,7 +303,7 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
     }
   }
   __syncthreads();
-  store_observation(t, base, count, features, legal, &next_item);
+  store_observation(t.out, base, count, features, legal, &next_item);
 }
 
 // --------------------------------------------------------------------- step ----
@@ -419,110 +420,110 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
 }
 
 // ------------------------------------------------------------ random play ----
-// One random-policy self-play step in one launch: observe_kernel<false, true> (the
-// observation and the uniform legal draw) followed by step_kernel<3> (the step and the
-// auto-reset of finished rows), with the same outputs.  Two waves per tile of 64 games:
-// wave 0 computes the observation records and the actions, then runs the 64 games' steps
-// while wave 1 stores the observation from LDS, so the step's integer work overlaps the
-// HBM-bound feature stores instead of following them; wave 0 then takes over the stores
-// that are left.  At ~250 VGPRs two waves fit per SIMD: four tiles per CU, every tile of
-// a 65,536-row batch resident at once.
+// `steps` random-policy self-play steps in one launch, each the work of
+// observe_kernel<false, true> (the observation and the uniform legal draw) followed by
+// step_kernel<3> (the step and the auto-reset of finished rows), with the last step's
+// outputs.  Two waves per tile of 64 games; wave 0 keeps the games in registers for the
+// whole launch.  Step s's observation records go to LDS buffer s % 2: while wave 1 stores
+// step s - 1's observation from the other buffer, wave 0 steps the games, deals the
+// finished ones their next game, builds step s's records and draws its actions, then
+// takes over the stores that are left.  So the HBM-bound stores run beside the integer
+// work of both the step and the next observation, and the rows are read and written
+// once per launch.  Two waves per SIMD (the register budget is pinned to 256 VGPRs; the
+// loop keeps a few dwords in scratch): four tiles per CU (34 KiB of LDS each), every tile
+// of a 65,536-row batch resident at once.
 constexpr int kPlayThreads = 128;
+constexpr int64_t kMaxPlaySteps = 1 << 20;
 
-__global__ __launch_bounds__(kPlayThreads) void play_kernel(
+__global__ __launch_bounds__(kPlayThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void play_kernel(
     u64* states, i64 n, u64* sampler, float* features, u8* legal, u8* player, u8* obs_done,
     i16* obs_status, i64* actions, float* reward, u8* done, u8* nagari, i16* status,
-    u8* committed, AutoReset ar) {
-  __shared__ ObserveTile t;  // the rows, then the records and masks, then the new rows
-  __shared__ int spare_rows[kTile];
-  __shared__ int spare_count;
-  __shared__ int next_item;  // store_observation's work counter
+    u8* committed, AutoReset ar, int steps) {
+  __shared__ ObserveTile t;    // the rows, then the records of even steps, then the rows
+  __shared__ RecordBuffer t1;  // the records of odd steps
+  __shared__ int next_item[2];  // store_observation's work counters, by step parity
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int tid = threadIdx.x;
   const int lane = tid & (kTile - 1);
   const int wave = tid / kTile;
-  if (tid == 0) next_item = 0;
+  const i64 i = base + lane;
+  if (tid < 2) next_item[tid] = 0;
   {
     const u64* src = states + base * kRowWords;
     for (int j = tid; j < count * kRowWords; j += kPlayThreads) t.rows[j] = src[j];
   }
   const bool active = wave == 0 && lane < count;
-  u32 gen0 = 0, spare0 = 0;
+  u32 gen = 0, spare0 = 0;
+  u64 xc = 0;  // the committed sampler state
   if (active) {  // issued early so their latency hides
-    gen0 = ar.generation[base + lane];
-    spare0 = ar.spare_gen[base + lane];
+    gen = ar.generation[i];
+    spare0 = ar.spare_gen[i];
+    xc = sampler[i];
   }
   __syncthreads();
-  Env e;
+  Env e;  // the game this lane plays (its next game once it finishes)
   if (active) e = unpack_row(t.rows + lane * kRowWords);
-  __syncthreads();  // rows are dead from here on; their bytes become the records
-  const i64 i = base + lane;
+  __syncthreads();  // rows are dead from here on; their bytes become even steps' records
   i64 a = -1;
-  u64 x = 0;
+  u64 xt = 0;  // the sampler state after the draw (committed with the step)
   PacketHead head{};
-  if (active) {
-    // The observation reads one copy of the game and the step another: building the
-    // packet from the very Env that is then stepped leaves an engine temporary in private
-    // memory (72-96 B per lane).
-    const Env seen = e;
-    const Packet pk = make_packet(seen);
-    FeatRow fr;
-    feature_row(pk, c_stop_bits, fr);
-    feature_record(fr, t.out.rec[lane]);
-    t.out.legal[lane][0] = pk.head.legal.w0;
-    t.out.legal[lane][1] = pk.head.legal.w1;
-    t.out.legal[lane][2] = pk.head.legal.w2;
-    player[i] = pk.head.player;
-    obs_done[i] = seen.done != 0;
-    obs_status[i] = (i16)pk.head.status;
-    x = sampler[i];
-    a = draw_legal(pk.head.legal.w0, pk.head.legal.w1, pk.head.legal.w2, x);
-    actions[i] = a;
-    head = pk.head;
-  }
-  __syncthreads();
-  bool take_spare = false;
-  Env g;  // the game stepped (a copy of `e`)
-  bool fresh = false;  // finished, next game dealt here (its spare is stale)
-  u64 next_seed = 0;
-  if (wave == 0) {
-    if (lane < count) {
-      g = e;
-      const StepOut so = torch_step_head(g, clamp_action(a), head);
-      reward[i] = (float)so.reward0;
-      done[i] = so.done;
-      nagari[i] = so.nagari;
-      status[i] = (i16)so.status;
-      committed[i] = so.committed;
-      if (so.done) {
-        const u32 gen = gen0 + 1u;
-        ar.generation[i] = gen;
-        const u64 seed = ar.base_seed + (u64)i + ar.stride * gen;
-        sampler[i] = sampler_seed(seed);
-        take_spare = spare0 == gen;
-        fresh = !take_spare;
-        next_seed = seed;
-      } else if (a >= 0) {
-        sampler[i] = x;
+  // Iteration s steps the games for step s - 1 (s > 0), observes step s into buffer s % 2
+  // (s < steps) and stores step s - 1's observation (s > 0).
+  for (int s = 0; s <= steps; ++s) {
+    RecordBuffer& cur = (s & 1) ? t1 : t.out;
+    if (active) {
+      if (s > 0) {
+        // The observation reads one copy of the game and the step another: building the
+        // packet from the very Env that is then stepped leaves an engine temporary in
+        // private memory.
+        Env g = e;
+        const StepOut so = torch_step_head(g, clamp_action(a), head);
+        reward[i] = (float)so.reward0;
+        done[i] = so.done;
+        nagari[i] = so.nagari;
+        status[i] = (i16)so.status;
+        committed[i] = so.committed;
+        if (so.done) {  // the next game: this generation's spare, or dealt here if stale
+          ++gen;
+          const u64 seed = ar.base_seed + (u64)i + ar.stride * gen;
+          xc = sampler_seed(seed);
+          if (spare0 == gen) g = unpack_row(ar.spares + i * kRowWords);
+          else g = create_env(seed, (u32)(i & 1));
+        } else if (a >= 0) {
+          xc = xt;
+        }
+        e = g;
+      }
+      if (s < steps) {
+        const Env seen = e;
+        const Packet pk = make_packet(seen);
+        FeatRow fr;
+        feature_row(pk, c_stop_bits, fr);
+        feature_record(fr, cur.rec[lane]);
+        cur.legal[lane][0] = pk.head.legal.w0;
+        cur.legal[lane][1] = pk.head.legal.w1;
+        cur.legal[lane][2] = pk.head.legal.w2;
+        player[i] = pk.head.player;
+        obs_done[i] = seen.done != 0;
+        obs_status[i] = (i16)pk.head.status;
+        xt = xc;
+        a = draw_legal(pk.head.legal.w0, pk.head.legal.w1, pk.head.legal.w2, xt);
+        actions[i] = a;
+        head = pk.head;
       }
     }
+    if (s > 0)  // step s - 1's observation, from the other buffer
+      store_observation((s & 1) ? t.out : t1, base, count, features, legal,
+                        &next_item[(s - 1) & 1]);
+    if (tid == 0) next_item[s & 1] = 0;  // for iteration s + 1 (its last use has ended)
+    __syncthreads();
   }
-  store_observation(t, base, count, features, legal, &next_item);  // wave 0 after its step
-  __syncthreads();  // records are dead: the region takes the new rows
-  if (wave == 0) {
-    // a finished game's row takes its next game: the spare (copied below) or a deal here
-    if (lane < count && !take_spare && !fresh) pack_row(g, t.rows + lane * kRowWords);
-    if (fresh) pack_row(create_env(next_seed, (u32)(i & 1)), t.rows + lane * kRowWords);
-    const u64 ballot = __ballot(take_spare);
-    if (take_spare) spare_rows[__popcll(ballot & ((1ull << lane) - 1ull))] = lane;
-    if (lane == 0) spare_count = (int)__popcll(ballot);
-  }
-  __syncthreads();
-  for (int j = tid; j < spare_count * kRowWords; j += kPlayThreads) {
-    const int r = spare_rows[j / kRowWords];
-    const int k = j - (j / kRowWords) * kRowWords;
-    t.rows[r * kRowWords + k] = ar.spares[(base + r) * kRowWords + k];
+  if (active) {
+    pack_row(e, t.rows + lane * kRowWords);
+    ar.generation[i] = gen;
+    sampler[i] = xc;
   }
   __syncthreads();
   stage_out<kPlayThreads>(t.rows, states, nullptr, base, count, 0);
@@ -599,7 +600,7 @@ __global__ __launch_bounds__(kPlayThreads) void branch_observe_kernel(
       for (int k = 0; k < kRowWords; ++k) out[k] = row[k];
     }
   }
-  store_observation(t, base, count, features, legal, &next_item);  // wave 0 after its rows
+  store_observation(t.out, base, count, features, legal, &next_item);  // wave 0 after its rows
 }
 
 // -------------------------------------------------------------------- small ----
@@ -949,8 +950,8 @@ int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* featu
                      int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
                      int16_t* status, uint8_t* committed, uint64_t base_seed,
                      int64_t seed_stride, uint32_t* generation, const uint8_t* spares,
-                     const uint32_t* spare_gen, hipStream_t stream) {
-  if (n < 0 || seed_stride < 0 ||
+                     const uint32_t* spare_gen, int64_t steps, hipStream_t stream) {
+  if (n < 0 || seed_stride < 0 || steps < 1 || steps > kMaxPlaySteps ||
       (n > 0 && (!states || !sampler || !features || !legal || !player || !obs_done ||
                  !obs_status || !actions || !reward || !done || !nagari || !status ||
                  !committed || !generation || !spares || !spare_gen)))
@@ -960,7 +961,8 @@ int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* featu
                      reinterpret_cast<const u64*>(spares), spare_gen};
   play_kernel<<<tiles(n), kPlayThreads, 0, stream>>>(
       reinterpret_cast<u64*>(states), n, reinterpret_cast<u64*>(sampler), features, legal,
-      player, obs_done, obs_status, actions, reward, done, nagari, status, committed, ar);
+      player, obs_done, obs_status, actions, reward, done, nagari, status, committed, ar,
+      (int)steps);
   return launched();
 }
 

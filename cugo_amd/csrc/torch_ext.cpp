@@ -356,14 +356,16 @@ std::vector<torch::Tensor> branch_observe_indexed(torch::Tensor states, torch::T
   return out;
 }
 
-// observe_sample then step_reset_spares in one launch: (features, legal, player, done,
-// status, actions, reward, step done, nagari, step status, committed).
+// `steps` x (observe_sample then step_reset_spares) in one launch, the last step's
+// (features, legal, player, done, status, actions, reward, step done, nagari, step status,
+// committed).
 std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampler,
                                        int64_t base_seed, torch::Tensor generation,
                                        torch::Tensor spares, torch::Tensor spare_gen,
-                                       int64_t seed_stride) {
+                                       int64_t seed_stride, int64_t steps) {
   check_states(states);
   check_states(spares);
+  TORCH_CHECK(steps >= 1 && steps <= (1 << 20), "steps must lie in [1, 2^20]");
   const int64_t n = states.size(0);
   check_1d(sampler, at::kLong, "sampler");
   check_1d(generation, at::kInt, "generation");
@@ -387,7 +389,8 @@ std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampl
                               o[9].data_ptr<int16_t>(), u8p(o[10]),
                               static_cast<uint64_t>(base_seed), seed_stride < 0 ? n : seed_stride,
                               reinterpret_cast<uint32_t*>(generation.data_ptr()), u8p(spares),
-                              reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), stream()),
+                              reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), steps,
+                              stream()),
              "play_random");
   return o;
 }
@@ -929,10 +932,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("branch_observe_indexed", &branch_observe_indexed,
         "branch_indexed then observe_indexed of the children, in one launch");
   m.def("play_random", &play_random,
-        "observe_sample then step_reset_spares in one launch",
+        "steps x (observe_sample then step_reset_spares) in one launch; last step's outputs",
         pybind11::arg("states"), pybind11::arg("sampler"), pybind11::arg("base_seed"),
         pybind11::arg("generation"), pybind11::arg("spares"), pybind11::arg("spare_gen"),
-        pybind11::arg("seed_stride") = -1);
+        pybind11::arg("seed_stride") = -1, pybind11::arg("steps") = 1);
   m.def("step_reset_spares", &step_reset_spares,
         "step, then reset_done_spares of the finished rows, in one launch",
         pybind11::arg("states"), pybind11::arg("actions"), pybind11::arg("base_seed"),

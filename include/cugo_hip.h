@@ -144,15 +144,19 @@ int cugo_branch_observe_indexed(const uint8_t* states, int64_t env_count, const 
                                 uint8_t* committed, float* features, uint8_t* legal,
                                 uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
                                 hipStream_t stream);
-/* cugo_observe_sample followed by cugo_step_reset_spares on its actions, in one launch
- * (one random-policy self-play step): the observation outputs, the actions, then the
- * step's outputs; the step of a tile's games overlaps the stores of its observation. */
+/* `steps` (1 .. 2^20) random-policy self-play steps in one launch, each
+ * cugo_observe_sample followed by cugo_step_reset_spares on its actions, with the effect
+ * of `steps` calls of one step each: the outputs (observation, actions, then the step's
+ * outputs) are the last step's, and every step's observation is written.  The games stay
+ * on chip between steps, and one step's observation stores overlap the step and the next
+ * observation.  The reference's loop calls observe, samples and steps once per step
+ * (python/torch50_smoke.py); steps = 1 is that loop's step in one launch. */
 int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
                      uint8_t* legal, uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
                      int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
                      int16_t* status, uint8_t* committed, uint64_t base_seed,
                      int64_t seed_stride, uint32_t* generation, const uint8_t* spares,
-                     const uint32_t* spare_gen, hipStream_t stream);
+                     const uint32_t* spare_gen, int64_t steps, hipStream_t stream);
 /* cugo_step followed by cugo_reset_done_spares(states, done, n, base_seed, seed_stride,
  * generation, sampler, NULL, spares, spare_gen) in one launch: the outputs are the
  * step's (done[i] = 1 for the game that just finished), and each finished row already

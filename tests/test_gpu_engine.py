@@ -561,3 +561,33 @@ def test_branch_observe_full_batch(ext, ref):
     ob = ext.observe_indexed(fused[0], torch.arange(ids.size, device=DEV))
     for j, want in enumerate(ob):
         assert torch.equal(fused[6 + j], want), j
+
+
+@pytest.mark.parametrize("n", [3001 * 2, 65536])
+def test_play_random_steps_match_single_steps(ext, n):
+    """play_random(steps=K) == K calls of one step: rows, generations, samplers and the
+    eleven outputs of the last step, for K = 1, 3 and 8 over several blocks, with the spares
+    refilled only every other block (so spare and inline re-deals both occur), at a
+    partial last tile and at the full batch."""
+    announce(f"play_random steps (n={n})")
+    base = 0x31415926
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    a = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(np.arange(n) & 1).to(DEV))
+    gen_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp_a = ext.seed_samplers(n, base, gen_a)
+    sp_a = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
+    sg_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    b, gen_b, smp_b, sp_b, sg_b = (t.clone() for t in (a, gen_a, smp_a, sp_a, sg_a))
+    for block, k in enumerate([8, 3, 8, 1, 8, 8]):
+        if block % 2 == 0:
+            ext.refill_spares(sp_a, sg_a, gen_a, base)
+            ext.refill_spares(sp_b, sg_b, gen_b, base)
+        for _ in range(k):
+            single = ext.play_random(a, smp_a, base, gen_a, sp_a, sg_a)
+        multi = ext.play_random(b, smp_b, base, gen_b, sp_b, sg_b, steps=k)
+        for j, (x, y) in enumerate(zip(single, multi)):
+            assert torch.equal(x, y), (block, k, j)
+        assert torch.equal(a, b) and torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), block
+    assert int(gen_a.sum().item()) > n // 2
+    with pytest.raises(RuntimeError):
+        ext.play_random(b, smp_b, base, gen_b, sp_b, sg_b, steps=0)
