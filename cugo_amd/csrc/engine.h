@@ -2198,7 +2198,8 @@ CG_HD float feature_at(const u64* w, const float* d, u32 f) {
 // 4q..4q+3) is one nibble, at dword q / 8, bits 4 (q % 8) .. 4 (q % 8) + 3.  Then the float
 // bits of the 37 other scalars, in feature order (dense_pos).  A feature is its bit's
 // 0 / 1.0f pattern ORed with its dense dword (0 where it has none), which is exact for
-// every value, signed zeros included.
+// every value, signed zeros included.  A record takes kFeatRecord + 1 dwords: the last is
+// a zero pad that a reader may OR into any feature.
 constexpr int kRecBits = 23;   // 720 bits
 constexpr int kRecDense = 37;
 constexpr int kFeatRecord = kRecBits + kRecDense;  // 60 dwords
@@ -2270,6 +2271,7 @@ CG_HD void feature_record(const FeatRow& r, u32* rec) {
   dn[34] = __builtin_bit_cast(u32, d[51]);                                       // 557
   dn[35] = __builtin_bit_cast(u32, d[54]);                                       // 710
   dn[36] = __builtin_bit_cast(u32, d[55]);                                       // 711
+  rec[kFeatRecord] = 0u;  // the pad that features without a dense dword read
 }
 
 }  // namespace cugo_amd

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kTile) void create_kernel(const i64* seeds, const i
 // ------------------------------------------------------------------ observe ----
 // LDS of one observe tile: the staged rows are dead once every lane has unpacked its
 // row, so the per-row feature records and masks reuse the same bytes.
-constexpr int kRecStride = kFeatRecord + 1;  // odd: a lane's own row, no bank conflicts
+constexpr int kRecStride = kFeatRecord + 1;  // + the zero pad; odd: no bank conflicts
 struct RecordBuffer {  // one step's observation of a tile, before it is stored
   u32 rec[kTile][kRecStride];
   u64 legal[kTile][3];
@@ -125,11 +125,14 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
                                          float* features, u8* legal, int* next) {
   const int lane = threadIdx.x & (kTile - 1);
   constexpr int kQuads = kFeatureCount / 4;  // 180
-  int dpos[3][4];  // each of the lane's columns: its features' dense dwords (or -1)
-  for (int c = 0; c < 3; ++c)
+  // Each of the lane's columns 1 and 2: its features' dense dwords, or the record's zero
+  // pad dword (column 0, quads 0..63, holds no dense feature).
+  int dpos[3][4];
+  for (int c = 1; c < 3; ++c)
     for (int k = 0; k < 4; ++k) {
       const int q = lane + kTile * c;
-      dpos[c][k] = q < kQuads ? dense_pos((u32)(4 * q + k)) : -1;
+      const int pos = q < kQuads ? dense_pos((u32)(4 * q + k)) : -1;
+      dpos[c][k] = kRecBits + (pos >= 0 ? pos : kRecDense);
     }
   uint4* fout = reinterpret_cast<uint4*>(features + base * kFeatureCount);
   // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0); word
@@ -157,10 +160,12 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
           v.y = (0u - ((nib >> 1) & 1u)) & 0x3f800000u;
           v.z = (0u - ((nib >> 2) & 1u)) & 0x3f800000u;
           v.w = (0u - ((nib >> 3) & 1u)) & 0x3f800000u;
-          if (dpos[c][0] >= 0) v.x |= rec[kRecBits + dpos[c][0]];
-          if (dpos[c][1] >= 0) v.y |= rec[kRecBits + dpos[c][1]];
-          if (dpos[c][2] >= 0) v.z |= rec[kRecBits + dpos[c][2]];
-          if (dpos[c][3] >= 0) v.w |= rec[kRecBits + dpos[c][3]];
+          if (c > 0) {  // unconditional reads: lanes without a dense feature read the pad
+            v.x |= rec[dpos[c][0]];
+            v.y |= rec[dpos[c][1]];
+            v.z |= rec[dpos[c][2]];
+            v.w |= rec[dpos[c][3]];
+          }
           fout[r * kQuads + q] = v;
         }
       }
@@ -294,7 +299,7 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
         actions[i] = a;
       }
     } else {  // invalid id (torch50_ext.cu:71-87): an all-zero row
-      for (int k = 0; k < kFeatRecord; ++k) rec[k] = 0u;
+      for (int k = 0; k <= kFeatRecord; ++k) rec[k] = 0u;
       t.out.legal[lane][0] = t.out.legal[lane][1] = t.out.legal[lane][2] = 0;
       player[i] = 0;
       done[i] = 1;
