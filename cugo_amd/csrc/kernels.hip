@@ -126,7 +126,8 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
   const int lane = threadIdx.x & (kTile - 1);
   constexpr int kQuads = kFeatureCount / 4;  // 180
   // Each of the lane's columns 1 and 2: its features' dense dwords, or the record's zero
-  // pad dword (column 0, quads 0..63, holds no dense feature).
+  // pad dword (column 0, quads 0..63, holds no dense feature; lanes past quad 179 read the
+  // pad too).
   int dpos[3][4];
   for (int c = 1; c < 3; ++c)
     for (int k = 0; k < 4; ++k) {
@@ -144,10 +145,49 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
   const int items = count + chunks + (bytes > 4 * full ? 1 : 0);
   const int leader = __ffsll((long long)__ballot(1)) - 1;
   for (;;) {
-    int item = 0;
-    if (lane == leader) item = atomicAdd(next, 1);
-    item = __builtin_amdgcn_readfirstlane(item);
-    if (item >= items) break;
+    int claim = 0;
+    if (lane == leader) claim = atomicAdd(next, 2);  // two items a claim
+    const int item0 = __builtin_amdgcn_readfirstlane(claim);
+    if (item0 >= items) break;
+    if (item0 + 1 < count) {
+      // Two feature rows: every LDS read of both rows first (column 2's lanes past quad
+      // 179 read in-range dwords and store nothing), then the six float4 stores.
+      u32 nib[2][3], dv[2][3][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const u32* rec = t.rec[item0 + j];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+          const int q = lane + kTile * c;
+          nib[j][c] = rec[q >> 3] >> (4 * (q & 7));
+          if (c > 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dv[j][c][k] = rec[dpos[c][k]];
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+          const int q = lane + kTile * c;
+          uint4 v;  // 0 or 1.0f per bit
+          v.x = (0u - (nib[j][c] & 1u)) & 0x3f800000u;
+          v.y = (0u - ((nib[j][c] >> 1) & 1u)) & 0x3f800000u;
+          v.z = (0u - ((nib[j][c] >> 2) & 1u)) & 0x3f800000u;
+          v.w = (0u - ((nib[j][c] >> 3) & 1u)) & 0x3f800000u;
+          if (c > 0) {
+            v.x |= dv[j][c][0];
+            v.y |= dv[j][c][1];
+            v.z |= dv[j][c][2];
+            v.w |= dv[j][c][3];
+          }
+          if (q < kQuads) fout[(item0 + j) * kQuads + q] = v;
+        }
+      }
+      continue;
+    }
+    for (int item = item0; item < item0 + 2 && item < items; ++item) {
     if (item < count) {
       const int r = item;
       const u32* rec = t.rec[r];
@@ -200,6 +240,7 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
         const int a = at - r * kActionCount;
         lout[at] = (u8)((t.legal[r][a >> 6] >> (a & 63)) & 1u);
       }
+    }
     }
   }
 }
