@@ -1,0 +1,122 @@
+// Host checks of engine helpers that replace a plainer formulation with bit arithmetic.
+// Built and run by tests/test_cpu_engine_host.py (host code only; no GPU):
+//  1. feature_record + the GPU writer's decode (nibble -> 0/1.0f patterns, OR the dense
+//     dword or the zero pad) == feature_at for every one of the 720 features;
+//  2. hangame_steal_selection (six mask passes) == the card-by-card loop of
+//     pi_transfer.h:90-110;
+//  3. special_months == legal_special_months (special50.h:71-95) for bombs, grenades and
+//     shakes.
+// Prints one line per check and exits non-zero on the first mismatch.
+#include "engine.h"
+
+#include <cstdio>
+#include <cstring>
+#include <random>
+
+using namespace cugo_amd;
+
+static u32 bits_of(float f) { u32 b; std::memcpy(&b, &f, 4); return b; }
+
+static int check_records(std::mt19937_64& g) {
+  const int binary[] = {0, 1, 2, 3, 4, 5, 23, 24, 38, 39, 40, 41, 42, 46, 47, 48, 49, 52, 53};
+  for (int it = 0; it < 20000; ++it) {
+    FeatRow r;
+    for (int k = 0; k < kFeatWords; ++k) r.w[k] = g() & (it % 3 ? ~0ull : g());
+    for (int k = 0; k < kFeatDense; ++k) {
+      u32 b = (u32)g();
+      if (it % 5 == 0) b = 0x80000000u;  // -0.0
+      if (it % 7 == 0) b = 0x7fc00001u;  // a NaN payload
+      std::memcpy(&r.d[k], &b, 4);
+    }
+    for (int k : binary) r.d[k] = (g() & 1) ? 1.0f : 0.0f;
+    u32 rec[kFeatRecord + 1];
+    std::memset(rec, 0xAB, sizeof rec);
+    feature_record(r, rec);
+    for (u32 q = 0; q < kFeatQuads; ++q) {
+      const u32 nib = rec[q >> 3] >> (4 * (q & 7));
+      for (u32 k = 0; k < 4; ++k) {
+        const int pos = dense_pos(4 * q + k);
+        const u32 got = ((0u - ((nib >> k) & 1u)) & 0x3f800000u) |
+                        rec[kRecBits + (pos >= 0 ? pos : kRecDense)];
+        const u32 want = bits_of(feature_at(r.w, r.d, 4 * q + k));
+        if (got != want) {
+          std::printf("record: feature %u got %08x want %08x\n", 4 * q + k, got, want);
+          return 1;
+        }
+      }
+    }
+  }
+  std::printf("records: 20000 rows, 720 features each, equal\n");
+  return 0;
+}
+
+// pi_transfer.h:90-110 as written there: keys in order, cards in ascending order.
+static u64 steal_loop(u64 candidates, u64 mission, bool owns_mission, u32 count) {
+  u64 chosen = 0;
+  for (u32 key = 0; key < 6 && count != 0; ++key) {
+    const bool use_mission = owns_mission ? key >= 3 : (key & 1u) != 0;
+    const u32 value = owns_mission ? 1 + key % 3 : 1 + key / 2;
+    u64 pool = candidates & (use_mission ? mission : ~mission);
+    while (pool != 0 && count != 0) {
+      const u32 card = (u32)__builtin_ctzll(pool);
+      pool &= pool - 1;
+      if (pi_card_value(card) != value) continue;
+      chosen |= bit(card);
+      --count;
+    }
+  }
+  return chosen;
+}
+
+static int check_steal(std::mt19937_64& g) {
+  const u64 pis = kPlainPi | kDoublePi | kBonusMask | bit(kGukjin);
+  for (int it = 0; it < 500000; ++it) {
+    const u64 cand = (g() & g() & pis) | (it % 4 == 0 ? pis & g() : 0);
+    const u64 mission = g() & g() & kDeckMask;
+    const bool owns = g() & 1;
+    const u32 count = (u32)(g() % 8);
+    if (hangame_steal_selection(cand, mission, owns, count) != steal_loop(cand, mission, owns, count)) {
+      std::printf("steal: candidates %llx mission %llx owns %d count %u\n",
+                  (unsigned long long)cand, (unsigned long long)mission, owns, count);
+      return 1;
+    }
+  }
+  std::printf("steal selection: 500000 cases equal\n");
+  return 0;
+}
+
+static int check_special_months(std::mt19937_64& g) {
+  for (int it = 0; it < 500000; ++it) {
+    Env e{};
+    e.hand0 = g() & g() & kDeckMask;
+    e.hand1 = g() & g() & kDeckMask;
+    if (it % 3 == 0) e.hand0 |= g() & kDeckMask;
+    e.floor = g() & g() & (it % 2 ? g() : ~0ull) & kDeckMask;
+    e.actor = (u8)(g() & 1);
+    e.shaken0 = (u16)g(); e.shaken1 = (u16)g(); e.sh4_0 = (u16)g(); e.sh4_1 = (u16)g();
+    e.phase = it % 17 == 0 ? kPhaseResolve : kPhasePlay;
+    e.winner = it % 19 == 0 ? 0 : kNoPlayer;
+    e.dact = kNoPlayer;
+    e.gdec = it % 23 == 0 ? 1 : 0;
+    const SpecialMonths s = special_months(e);
+    const u16 bombs = legal_special_months(e, 3, 1, false);
+    const u16 grenades = legal_special_months(e, 2, 2, false);
+    const u16 shakes =
+        (u16)(legal_special_months(e, 3, 0, true) | legal_special_months(e, 4, 0, true));
+    if (s.bombs != bombs || s.grenades != grenades || s.shakes != shakes) {
+      std::printf("special months: %x/%x %x/%x %x/%x\n", s.bombs, bombs, s.grenades, grenades,
+                  s.shakes, shakes);
+      return 1;
+    }
+  }
+  std::printf("special months: 500000 states equal\n");
+  return 0;
+}
+
+int main() {
+  std::mt19937_64 g(20261201);
+  if (check_records(g)) return 1;
+  if (check_steal(g)) return 1;
+  if (check_special_months(g)) return 1;
+  return 0;
+}
