@@ -11,8 +11,8 @@
 // The work is a memory stream: every (query, head) reads (pos + 1) key and value rows
 // of dh elements once, and does ~2 flops per byte.  Layout of the work:
 //   * a 64-lane wavefront serves G consecutive heads of one query (64 / G lanes each):
-//     up to 8 for short caches, so the wavefront count drops by G and each wavefront
-//     keeps its heads' loads in flight together, 2 for long ones (pick_group); a
+//     up to 8, so the wavefront count drops by G and each wavefront keeps its heads'
+//     loads in flight together (pick_group); a
 //     256-thread workgroup holds four wavefronts, which for heads % (4 G) == 0 share the
 //     query and so the sequence length;
 //   * a slot row of dh elements is split into 16-byte parts; L = dh*elem/16 lanes hold
@@ -311,16 +311,18 @@ int launch_group(const void* q, void* keys, void* values, const void* k_new, con
 
 // Heads per wavefront.  Measured on MI355X (4,096 queries x 8 heads, dh 32 bf16): rows of
 // up to ~50 slots run 2-2.5x faster with 8 heads per wavefront than with one (fewer
-// wavefronts, each with all its loads in flight); rows of up to 319 slots are within 5 %
-// for every grouping and fastest at 2.  So: up to 8 for caches of at most 64 slots, else 2
-// (a grouping must divide `heads` and fit G * L <= 64 lanes).
+// wavefronts, each with all its loads in flight), and on a 320-slot cache 8 beats 2 both
+// for one game's rows (mean 20 slots: 18.5 against 23.5 us) and for full rows (mean 297:
+// 219 against 223 us).  So: up to 8, whatever the capacity (a grouping must divide
+// `heads` and fit G * L <= 64 lanes).
 template <int L>
 int pick_group(int64_t heads, int64_t slots) {
 #ifdef CUGO_DECODE_FORCE_GROUP
   if (heads % CUGO_DECODE_FORCE_GROUP == 0 && CUGO_DECODE_FORCE_GROUP * L <= 64)
     return CUGO_DECODE_FORCE_GROUP;
 #endif
-  const int want = slots <= 64 ? 8 : 2;
+  (void)slots;  // the row lengths, not the capacity, decide, and they are not known here
+  const int want = 8;
   int best = 1;
   for (int g = 2; g <= want; g <<= 1)
     if (heads % g == 0 && g * L <= 64) best = g;
