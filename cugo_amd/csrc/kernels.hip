@@ -120,7 +120,10 @@ __device__ inline u32 spread4(u32 x) {
 // legal mask bytes, then their unaligned tail.  A wave that arrives late (one that also
 // stepped the games) takes what is left, so no wave idles while another stores alone.
 // The claiming lane is the wave's first active lane, and every pass raises the counter,
-// so every wave leaves the loop.
+// so every wave leaves the loop.  A claim is kClaim items: a claim of kClaim feature rows
+// issues all its LDS reads before its 3 x kClaim stores, so more rows a claim keep more
+// stores in flight per wave, at the cost of 20 VGPRs a row.
+template <int kClaim>
 __device__ inline void store_observation(const RecordBuffer& t, i64 base, int count,
                                          float* features, u8* legal, int* next) {
   const int lane = threadIdx.x & (kTile - 1);
@@ -146,15 +149,15 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
   const int leader = __ffsll((long long)__ballot(1)) - 1;
   for (;;) {
     int claim = 0;
-    if (lane == leader) claim = atomicAdd(next, 2);  // two items a claim
+    if (lane == leader) claim = atomicAdd(next, kClaim);
     const int item0 = __builtin_amdgcn_readfirstlane(claim);
     if (item0 >= items) break;
-    if (item0 + 1 < count) {
-      // Two feature rows: every LDS read of both rows first (column 2's lanes past quad
-      // 179 read in-range dwords and store nothing), then the six float4 stores.
-      u32 nib[2][3], dv[2][3][4];
+    if (item0 + kClaim - 1 < count) {
+      // kClaim feature rows: every LDS read of the rows first (column 2's lanes past quad
+      // 179 read in-range dwords and store nothing), then the 3 x kClaim float4 stores.
+      u32 nib[kClaim][3], dv[kClaim][3][4];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < kClaim; ++j) {
         const u32* rec = t.rec[item0 + j];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
@@ -167,7 +170,7 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
         }
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < kClaim; ++j) {
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
           const int q = lane + kTile * c;
@@ -187,7 +190,7 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
       }
       continue;
     }
-    for (int item = item0; item < item0 + 2 && item < items; ++item) {
+    for (int item = item0; item < item0 + kClaim && item < items; ++item) {
     if (item < count) {
       const int r = item;
       const u32* rec = t.rec[r];
@@ -349,7 +352,7 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
     }
   }
   __syncthreads();
-  store_observation(t.out, base, count, features, legal, &next_item);
+  store_observation<2>(t.out, base, count, features, legal, &next_item);
 }
 
 // --------------------------------------------------------------------- step ----
@@ -480,6 +483,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
 // of a 65,536-row batch resident at once.
 constexpr int kPlayThreads = 128;
 constexpr int64_t kMaxPlaySteps = 1 << 20;
+constexpr int kPlayClaim = 4;  // rows a store claim (the observe kernels' third wave needs 2)
 
 __global__ __launch_bounds__(kPlayThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void play_kernel(
@@ -561,7 +565,7 @@ void play_kernel(
       }
     }
     if (s > 0)  // step s - 1's observation, from the other buffer
-      store_observation((s & 1) ? t.out : t1, base, count, features, legal,
+      store_observation<kPlayClaim>((s & 1) ? t.out : t1, base, count, features, legal,
                         &next_item[(s - 1) & 1]);
     if (tid == 0) next_item[s & 1] = 0;  // for iteration s + 1 (its last use has ended)
     __syncthreads();
@@ -646,7 +650,7 @@ __global__ __launch_bounds__(kPlayThreads) void branch_observe_kernel(
       for (int k = 0; k < kRowWords; ++k) out[k] = row[k];
     }
   }
-  store_observation(t.out, base, count, features, legal, &next_item);  // wave 0 after its rows
+  store_observation<2>(t.out, base, count, features, legal, &next_item);  // wave 0 after its rows
 }
 
 // -------------------------------------------------------------------- small ----
