@@ -669,6 +669,30 @@ def cpu_baseline(seconds: float) -> dict:
             "steps_per_s": decisions / dt}
 
 
+def store_ceiling(torch) -> dict:
+    """What plain stores reach on this GPU: torch's fill_ of a 192 MiB float32 tensor (about
+    the bytes of one observation step at B = 65,536), 20 launches timed with events.  The
+    observation kernels are store-bound, so this is their practical ceiling below the
+    published 8 TB/s."""
+    buf = torch.empty(48 << 20, dtype=torch.float32, device="cuda")
+    for _ in range(3):
+        buf.fill_(1.0)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 20
+    e0.record(stream)
+    for _ in range(reps):
+        buf.fill_(1.0)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    gbs = buf.numel() * 4 / (ms * 1e-3) / 1e9
+    del buf
+    return {"kernel": "torch fill_, 192 MiB float32", "gbs": round(gbs, 1),
+            "avg_launch_ms": round(ms, 4)}
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -687,6 +711,7 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    ceiling = store_ceiling(torch)
     rp = random_policy(ext, torch, args.batch, args.steps, args.warmup, args.streams,
                        not args.no_graph, not args.two_launch)
     games_per_s = rp["games"] / rp["seconds"]
@@ -697,7 +722,8 @@ def main() -> None:
                         "frac": round(observe_gbs / HBM_PEAK_GBS, 4),
                         "traffic": measured_traffic("observe_kernel", str(args.batch)),
                         "bytes_per_row": OBSERVE_BYTES_PER_ROW,
-                        "avg_launch_ms": round(rp["observe_ms"], 4)}
+                        "avg_launch_ms": round(rp["observe_ms"], 4),
+                        "frac_of_store_ceiling": round(observe_gbs / ceiling["gbs"], 4)}
     if rp["play_ms"] is not None:
         play_bytes = play_bytes_per_row(REFILL)
         play_gbs = args.batch * play_bytes / (rp["play_ms"] * 1e-3) / 1e9
@@ -707,7 +733,8 @@ def main() -> None:
                     "traffic": measured_traffic("play_kernel", f"{args.batch} x {REFILL}"),
                     "bytes_per_row": play_bytes, "steps_per_launch": REFILL,
                     "avg_launch_ms": round(rp["play_ms"], 4),
-                    "ms_per_step": round(rp["play_ms"] / REFILL, 4)}
+                    "ms_per_step": round(rp["play_ms"] / REFILL, 4),
+                    "frac_of_store_ceiling": round(play_gbs / ceiling["gbs"], 4)}
     else:
         roofline = observe_roofline
     result = {
@@ -735,6 +762,7 @@ def main() -> None:
         "games_timed": rp["games"],
         "roofline": roofline,
         "observe_roofline": observe_roofline,
+        "store_ceiling": ceiling,
     }
     if not args.no_branch:
         result["branch"] = branch_workload(ext, torch, args.branch_iters)

@@ -1262,14 +1262,207 @@ CG_HD u8 map_special(u8 s) {  // rollout50.h:207-223
   }
 }
 
+// rollout50.h:268-376: the six turn-taking kinds (play card, shake, bonus, bomb, grenade,
+// bomb credit) composed from the per-kind transitions, as the reference composes them.
+// The product runs apply_turn_action (same statuses, same state); this composition is its
+// plain restatement, kept for the host check of the two.
+CG_HD u8 apply_turn_action_per_kind(Env& n, const Action& a) {
+  const u8 actor = n.actor;
+  u8 status = kOk;
+  if (a.kind == kPlayBonus) {
+    PiResult pt;
+    status = map_turn(play_bonus_terminal(n, a.card, a.pisel, pt));
+    if (status == kOk) status = map_pi(pt.status);
+  } else if (a.kind == kBomb || a.kind == kGrenade || a.kind == kBombCredit) {
+    status = map_special(apply_terminal_special(n, a.kind, a.month, a.dmatch, a.pisel));
+  } else if (a.kind == kShake || a.kind == kPlayCard) {
+    if (a.kind == kShake) {
+      if (is_std(a.card)) {  // a shake shows the month's cards in hand
+        const u64 shown = active_hand(n) & month_cards(a.card >> 2);
+        if (actor == 0) n.rev0 |= shown; else n.rev1 |= shown;
+      }
+      status = map_special(apply_terminal_shake(n, a.card));
+    } else {
+      if (is_std(a.card) && (forced_special_months(n) & month_bit(a.card)) != 0)
+        return kNotLegal;
+      status = map_turn(begin_regular_play_terminal(n, a.card));
+    }
+    if (status != kOk) return status;
+    status = map_turn(draw_for_terminal(n));
+    if (status != kOk) return status;
+    PiResult pt;
+    const Resolve r = resolve_terminal_turn(n, a.pmatch, a.dmatch, a.pisel, pt);
+    status = map_resolve(r.status);
+    if (status == kOk) status = map_pi(pt.status);
+  } else {
+    return kInvalidAction;
+  }
+  return status;
+}
+
+CG_HD bool is_turn_kind(u8 k) {
+  return k == kPlayBonus || k == kBomb || k == kGrenade || k == kBombCredit || k == kShake ||
+         k == kPlayCard;
+}
+
+// The same six kinds as one transition.  In the composition above every kind's body
+// carries its own stock draw, floor resolution, pi steal and mission/stop bookkeeping, and
+// a wave whose games take different kinds runs each body in turn.  Here each kind runs
+// only its prologue (its checks and the cards it moves before the draw); the draw, the
+// floor resolution, the steal and the bookkeeping then run once for every kind:
+//   * the draw: a bonus play takes one card, any card (bonus.h:37-66); the others flip
+//     until a standard card, collecting the bonus cards met (bonus.h:68-81);
+//   * the resolution: a played card's turn resolves as resolve_turn (turn50.h:418-508);
+//     a bomb, grenade or bomb credit resolves the drawn card alone, as resolve_turn's
+//     last two steps do (special50.h:131-163);
+//   * the steal: the turn's pi count (pi_transfer.h:51-62), plus one for a bomb or
+//     grenade before the last turn (special50.h:207), or one for a bonus play;
+//   * the bookkeeping: terminal50.h:456-503 for a played card, 505-530 for a special,
+//     415-454 for a bonus play.
+// The checks run in the composition's order and return its statuses; the state updates
+// are the composition's, in its order.  `n` is the caller's transaction copy: a failure
+// may leave it partly changed.
+CG_HD u8 apply_turn_action(Env& n, const Action& a) {
+  const u8 actor = n.actor;
+  const bool bonus = a.kind == kPlayBonus;
+  const bool special = a.kind == kBomb || a.kind == kGrenade || a.kind == kBombCredit;
+  const bool play = !bonus && !special;  // kShake or kPlayCard
+  if (!is_turn_kind(a.kind)) return kInvalidAction;
+  const u64 cap_before = cap_of(n, actor);
+  u16 ct_before = 0;
+  u8 base_steal = 0;
+  if (bonus) {  // play_bonus_terminal and play_bonus_for_turn up to the draw
+    if (terminal_finished(n) || has_ct_choice(n)) return kWrongPhase;
+    if (game_finished(n) || has_pending_choice(n)) return kWrongPhase;
+    ct_before = chongtong_months(active_hand(n));
+    if (n.phase != kPhasePlay) return kWrongPhase;
+    if (!is_bonus_card(a.card)) return kNotLegal;
+    if ((active_hand(n) & bit(a.card)) == 0) return kNotLegal;
+    if (n.stock == 0) return kStockEmpty;
+  } else if (special) {  // apply_terminal_special, capture_special / play_bomb_credit
+    if (terminal_finished(n) || has_ct_choice(n)) return kWrongPhase;
+    if (!special_ready(n)) return kWrongPhase;
+    if (a.kind == kBombCredit) {
+      if (!cred_of(n, actor)) return kNotLegal;
+      set_cred(n, actor, (u8)(cred_of(n, actor) - 1u));
+    } else {
+      const bool grenade = a.kind == kGrenade;
+      const u8 month = a.month;
+      if (month >= 12) return kNotLegal;
+      const u16 mb = (u16)(1u << month);
+      const u16 legal = grenade ? legal_grenade_months(n) : legal_bomb_months(n);
+      if ((legal & mb) == 0) return kNotLegal;
+      const u64 hand = hand_of(n, actor);
+      const u64 hc = hand & month_cards(month);
+      const u64 fc = std_floor(n) & month_cards(month);
+      set_hand(n, actor, hand & ~hc);
+      n.floor &= ~fc;
+      set_cap(n, actor, cap_of(n, actor) | hc | fc);
+      set_cred(n, actor, (u8)(cred_of(n, actor) + (grenade ? 1u : 2u)));
+      if (!grenade) { if (actor == 0) ++n.bombs0; else ++n.bombs1; }
+      base_steal = is_last_turn(n) ? 0 : 1;
+    }
+  } else {
+    if (a.kind == kShake) {
+      if (is_std(a.card)) {  // a shake shows the month's cards in hand
+        const u64 shown = active_hand(n) & month_cards(a.card >> 2);
+        if (actor == 0) n.rev0 |= shown; else n.rev1 |= shown;
+      }
+      if (terminal_finished(n) || has_ct_choice(n)) return kWrongPhase;
+      const u8 s = map_special(begin_shake(n, a.card));
+      if (s != kOk) return s;
+    } else {
+      if (is_std(a.card) && (forced_special_months(n) & month_bit(a.card)) != 0)
+        return kNotLegal;
+      const u8 s = map_turn(begin_regular_play_terminal(n, a.card));
+      if (s != kOk) return s;
+    }
+    // draw_for_terminal -> draw_for_game -> draw_for_turn, up to the draw
+    if (terminal_finished(n) || has_ct_choice(n)) return kWrongPhase;
+    if (game_finished(n) || has_pending_choice(n)) return kWrongPhase;
+    if (n.phase != kPhaseDraw) return kWrongPhase;
+  }
+  // The draw.
+  u64 stock = n.stock, rng = n.rng, flipped = 0;
+  u8 card = kNoCard;
+  while (stock != 0) {
+    card = draw_uniform(stock, rng);
+    if (bonus || !is_bonus_card(card)) break;
+    flipped |= bit(card);
+    card = kNoCard;
+  }
+  if (bonus ? !is_physical(card) : !is_std(card)) return kStockEmpty;
+  n.stock = stock;
+  n.rng = rng;
+  u8 steal;
+  Resolve r{kResOk, 0, 0, 0, 0, (u8)is_last_turn(n)};
+  if (bonus) {
+    set_hand(n, actor, (active_hand(n) & ~bit(a.card)) | bit(card));
+    set_cap(n, actor, cap_of(n, actor) | bit(a.card));
+    steal = r.last_turn ? 0 : 1;
+  } else {
+    u8 played = kNoCard;
+    if (play) {
+      n.pdrawn = card;
+      n.pend_bonus = flipped;
+      n.phase = kPhaseResolve;
+      // resolve_terminal_turn, resolve_game_turn and resolve_turn, up to the resolution
+      if (terminal_finished(n) || has_ct_choice(n)) return kWrongPhase;
+      if (game_finished(n) || has_pending_choice(n)) return kWrongPhase;
+      played = n.pplayed;
+    }
+    const u64 pm = play ? floor_matches(n, played) : 0;
+    const u32 pmc = popc(pm);
+    const bool same = play && (played >> 2) == (card >> 2);
+    if (same && pmc == 1 && !r.last_turn) {  // ppuk: the three cards stay on the floor
+      n.floor |= bit(played) | bit(card) | flipped;
+      const u16 mb = month_bit(played);
+      n.ppuk |= mb;
+      if (n.actor == 0) n.owner1 &= (u16)~mb; else n.owner1 |= mb;
+      if (flipped & bit(kBonus2)) n.b2ppuk |= mb;  // turn50.h:241-250
+      if (flipped & bit(kBonus3)) n.b3ppuk |= mb;
+      r.events |= kEvPpuk;
+    } else if (same && pmc == 2) {
+      n.floor &= ~pm;
+      capture_cards(n, pm | bit(played) | bit(card) | flipped, r);
+      r.events |= kEvTtadak;
+    } else if (same && pmc == 0) {
+      capture_cards(n, bit(played) | bit(card) | flipped, r);
+      if (!r.last_turn) r.events |= kEvJjok;
+    } else {
+      if (play) {
+        const u8 rs = resolve_card_against_floor(n, played, a.pmatch, r);
+        if (rs != kResOk) return map_resolve(rs);
+      }
+      const u8 rs = resolve_card_against_floor(n, card, a.dmatch, r);
+      if (rs != kResOk) return map_resolve(rs);
+      if (flipped) capture_cards(n, flipped, r);
+    }
+    if (n.floor == 0 && r.captured != 0) r.events |= kEvSweep;  // turn50.h:499-502
+    finish_resolved_turn(n);
+    steal = (u8)(base_steal + steal_count(r));
+  }
+  const PiResult pt = apply_pi_steal(n, actor, steal, a.pisel);
+  if (pt.status != kPiOk) return map_pi(pt.status);
+  if (!bonus) finish_turn_game(n, actor);
+  if (play && (r.events & kEvTtadak) && n.turn == 1u) add_side_payment(n, actor, 7);
+  if (!bonus || pt.transfer != 0)
+    update_missions(n, actor, bonus ? pt.transfer : cap_of(n, actor) & ~cap_before);
+  if (bonus) {
+    open_bonus_chongtong_choice(n, actor, (u16)(chongtong_months(active_hand(n)) & ~ct_before));
+    return kOk;
+  }
+  if (play) record_completed_turn_ppuk(n, actor, (r.events & kEvPpuk) != 0);
+  sync_game_stop(n);
+  return kOk;
+}
+
 // rollout50.h:231-385; the held-card bookkeeping of apply_action50 (391-399) included.
 CG_HD u8 apply_action(Env& e, const Action& a) {
-  const u8 actor = e.actor;
   if (terminal_finished(e)) return kGameFinished;
   Env& n = e;  // in place: the caller's copy is the transaction
   n.held0 |= n.hand0;
   n.held1 |= n.hand1;
-  u8 status = kOk;
   if (a.kind == kChongtongWin || a.kind == kChongtongContinue) {
     if (apply_chongtong_action(n, a.kind == kChongtongWin) != 0) return kNotLegal;
   } else if (a.kind == kGo || a.kind == kStop) {
@@ -1278,34 +1471,7 @@ CG_HD u8 apply_action(Env& e, const Action& a) {
     if (apply_terminal_gukjin(n, a.kind == kGukjinPi) != 0) return kNotLegal;
   } else {
     if (has_ct_choice(n) || has_pending_choice(n)) return kWrongPhase;
-    if (a.kind == kPlayBonus) {
-      PiResult pt;
-      status = map_turn(play_bonus_terminal(n, a.card, a.pisel, pt));
-      if (status == kOk) status = map_pi(pt.status);
-    } else if (a.kind == kBomb || a.kind == kGrenade || a.kind == kBombCredit) {
-      status = map_special(apply_terminal_special(n, a.kind, a.month, a.dmatch, a.pisel));
-    } else if (a.kind == kShake || a.kind == kPlayCard) {
-      if (a.kind == kShake) {
-        if (is_std(a.card)) {  // a shake shows the month's cards in hand
-          const u64 shown = active_hand(n) & month_cards(a.card >> 2);
-          if (actor == 0) n.rev0 |= shown; else n.rev1 |= shown;
-        }
-        status = map_special(apply_terminal_shake(n, a.card));
-      } else {
-        if (is_std(a.card) && (forced_special_months(n) & month_bit(a.card)) != 0)
-          return kNotLegal;
-        status = map_turn(begin_regular_play_terminal(n, a.card));
-      }
-      if (status != kOk) return status;
-      status = map_turn(draw_for_terminal(n));
-      if (status != kOk) return status;
-      PiResult pt;
-      const Resolve r = resolve_terminal_turn(n, a.pmatch, a.dmatch, a.pisel, pt);
-      status = map_resolve(r.status);
-      if (status == kOk) status = map_pi(pt.status);
-    } else {
-      return kInvalidAction;
-    }
+    const u8 status = apply_turn_action(n, a);
     if (status != kOk) return status;
   }
   n.held0 |= n.hand0;  // apply_action50 (rollout50.h:391-399)

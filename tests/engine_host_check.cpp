@@ -5,7 +5,10 @@
 //  2. hangame_steal_selection (six mask passes) == the card-by-card loop of
 //     pi_transfer.h:90-110;
 //  3. special_months == legal_special_months (special50.h:71-95) for bombs, grenades and
-//     shakes.
+//     shakes;
+//  4. apply_turn_action (the six turn-taking kinds as one transition) == the per-kind
+//     composition (rollout50.h:268-376) on states of random games: same status, and on
+//     success the same row.
 // Prints one line per check and exits non-zero on the first mismatch.
 #include "engine.h"
 
@@ -113,10 +116,74 @@ static int check_special_months(std::mt19937_64& g) {
   return 0;
 }
 
+// Any set bit of m, or kNoCard.
+static u8 any_bit(u64 m, std::mt19937_64& g) {
+  const u32 c = (u32)__builtin_popcountll(m);
+  return c == 0 ? kNoCard : select_rank(m, (u32)(g() % c));
+}
+
+static int check_turn_actions(std::mt19937_64& g) {
+  static const u8 kinds[] = {kPlayCard, kPlayCard, kPlayCard, kShake, kPlayBonus,
+                             kBomb, kGrenade, kBombCredit};
+  long cases = 0, ok = 0;
+  for (int game = 0; game < 3000; ++game) {
+    Env e = create_env(g(), (u32)(g() & 1));
+    for (int t = 0; t < 60 && !e.done; ++t) {
+      // The two transitions on actions built from this state: mostly cards from the
+      // actor's hand, months of its legal specials and floor cards of the card's month,
+      // sometimes anything.
+      for (int k = 0; k < 24; ++k) {
+        Action a = make_action(kinds[g() % 8]);
+        const u64 hand = active_hand(e);
+        const bool wild = g() % 5 == 0;
+        a.card = wild ? (u8)(g() % 52) : any_bit(hand, g);
+        const SpecialMonths sm = special_months(e);
+        const u16 months = a.kind == kBomb ? sm.bombs : a.kind == kGrenade ? sm.grenades
+                                                                            : sm.shakes;
+        a.month = wild || months == 0 ? (u8)(g() % 13) : (u8)__builtin_ctz(months);
+        a.pmatch = g() % 3 ? kNoCard : any_bit(std_floor(e), g);
+        a.dmatch = g() % 3 ? kNoCard : any_bit(std_floor(e), g);
+        const u64 opp = pi_card_mask(cap_of(e, e.actor ^ 1u), false);
+        a.pisel = g() % 4 ? 0 : opp & g();
+        Env x = e, y = e;
+        const u8 sx = apply_turn_action(x, a);
+        const u8 sy = apply_turn_action_per_kind(y, a);
+        u64 rx[kRowWords], ry[kRowWords];
+        pack_row(x, rx);
+        pack_row(y, ry);
+        ++cases;
+        if (sx != sy || (sx == kOk && std::memcmp(rx, ry, sizeof rx) != 0)) {
+          std::printf("turn action: game %d turn %d kind %u card %u month %u: status %u vs %u\n",
+                      game, t, a.kind, a.card, a.month, sx, sy);
+          return 1;
+        }
+        ok += sx == kOk;
+      }
+      // Advance the game with a uniform legal action.
+      const PacketHead h = packet_head(e);
+      const u64 w[3] = {h.legal.w0, h.legal.w1, h.legal.w2};
+      const u32 c = (u32)(__builtin_popcountll(w[0]) + __builtin_popcountll(w[1]) +
+                          __builtin_popcountll(w[2]));
+      if (c == 0) break;
+      u32 r = (u32)(g() % c);
+      u16 act = 0;
+      for (u32 i = 0; i < 3; ++i) {
+        const u32 ci = (u32)__builtin_popcountll(w[i]);
+        if (r < ci) { act = (u16)(64 * i + select_rank(w[i], r)); break; }
+        r -= ci;
+      }
+      torch_step(e, act);
+    }
+  }
+  std::printf("turn actions: %ld cases (%ld applied) equal\n", cases, ok);
+  return 0;
+}
+
 int main() {
   std::mt19937_64 g(20261201);
   if (check_records(g)) return 1;
   if (check_steal(g)) return 1;
   if (check_special_months(g)) return 1;
+  if (check_turn_actions(g)) return 1;
   return 0;
 }
