@@ -1843,8 +1843,135 @@ CG_HD Probe probe_special(const Env& e, const Pending& p, Env& staged) {
   return probe_pi_choice(staged, p, d.drawn, requested);
 }
 
-// postchance50.h:418-456
-CG_HD Probe probe_postchance(const Env& e, const Pending& p, Env& staged) {
+// The probe of the six turn-taking kinds as one transition, as apply_turn_action is to
+// apply_turn_action_per_kind: each kind runs its own prologue (probe_regular's begin and
+// draw checks, probe_bonus's play_bonus_for_turn checks, probe_special's card moves), then
+// one draw, one resolution and one pi-choice probe serve every kind.  The resolution of a
+// played card runs once and stops at the first floor choice, where probe_regular resolves
+// on a copy to find the choice (probe_resolve_choices) and, when none is open, resolves
+// again with resolve_turn: the same captures in the same order, so the same state.  Same
+// Probe fields and, where the probe succeeds, the same staged state as the per-kind probes
+// (the caller observes it).
+CG_HD Probe probe_turn_action(const Env& e, const Pending& p, Env& staged) {
+  const Action& a = p.action;
+  const bool bonus = a.kind == kPlayBonus;
+  const bool special = a.kind == kBomb || a.kind == kGrenade || a.kind == kBombCredit;
+  const bool play = !bonus && !special;  // kShake or kPlayCard
+  staged = e;
+  u8 base_steal = 0;
+  if (bonus) {  // play_bonus_for_turn up to the draw
+    if (staged.phase != kPhasePlay) return Probe{kWrongPhase, kDecNone, 0, kNoCard, 0};
+    if (!is_bonus_card(a.card) || (active_hand(staged) & bit(a.card)) == 0)
+      return Probe{kNotLegal, kDecNone, 0, kNoCard, 0};
+    if (staged.stock == 0) return Probe{kStockEmpty, kDecNone, 0, kNoCard, 0};
+  } else if (special) {  // probe_special's moves
+    const u8 actor = p.actor;
+    if (a.kind == kBombCredit) {
+      if (!special_ready(staged) || cred_of(staged, actor) == 0)
+        return Probe{kNotLegal, kDecNone, 0, kNoCard, 0};
+      set_cred(staged, actor, (u8)(cred_of(staged, actor) - 1u));
+    } else {
+      const bool grenade = a.kind == kGrenade;
+      const u8 month = a.month;
+      if (!special_ready(staged) || month >= 12) return Probe{kNotLegal, kDecNone, 0, kNoCard, 0};
+      const u16 mb = (u16)(1u << month);
+      const u16 legal = grenade ? legal_grenade_months(staged) : legal_bomb_months(staged);
+      if ((legal & mb) == 0) return Probe{kNotLegal, kDecNone, 0, kNoCard, 0};
+      const u64 hand = hand_of(staged, actor);
+      const u64 hc = hand & month_cards(month);
+      const u64 fc = std_floor(staged) & month_cards(month);
+      set_hand(staged, actor, hand & ~hc);
+      staged.floor &= ~fc;
+      set_cap(staged, actor, cap_of(staged, actor) | hc | fc);
+      set_cred(staged, actor, (u8)(cred_of(staged, actor) + (grenade ? 1u : 2u)));
+      if (!grenade) { if (actor == 0) ++staged.bombs0; else ++staged.bombs1; }
+      base_steal = is_last_turn(staged) ? 0 : 1;
+    }
+  } else {  // probe_regular: begin, then draw_for_terminal up to the draw
+    const u8 status = a.kind == kShake ? map_special(begin_shake(staged, a.card))
+                                       : map_turn(begin_regular_play_terminal(staged, a.card));
+    if (status != kOk) return Probe{status, kDecNone, 0, kNoCard, 0};
+    if (terminal_finished(staged) || has_ct_choice(staged) || game_finished(staged) ||
+        has_pending_choice(staged) || staged.phase != kPhaseDraw)
+      return Probe{kWrongPhase, kDecNone, 0, kNoCard, 0};
+  }
+  // The draw (as in apply_turn_action).
+  u64 stock = staged.stock, rng = staged.rng, flipped = 0;
+  u8 card = kNoCard;
+  while (stock != 0) {
+    card = draw_uniform(stock, rng);
+    if (bonus || !is_bonus_card(card)) break;
+    flipped |= bit(card);
+    card = kNoCard;
+  }
+  if (bonus ? !is_physical(card) : !is_std(card))
+    return Probe{kStockEmpty, kDecNone, 0, kNoCard, 0};
+  staged.stock = stock;
+  staged.rng = rng;
+  u8 steal;
+  if (bonus) {
+    const u64 hand = active_hand(staged);
+    set_hand(staged, staged.actor, (hand & ~bit(a.card)) | bit(card));
+    set_cap(staged, staged.actor, cap_of(staged, staged.actor) | bit(a.card));
+    steal = is_last_turn(staged) ? 0 : 1;
+  } else {
+    if (play) {
+      staged.pdrawn = card;
+      staged.pend_bonus = flipped;
+      staged.phase = kPhaseResolve;
+    }
+    Env n = staged;
+    Resolve r{kResOk, 0, 0, 0, 0, (u8)is_last_turn(n)};
+    const u8 played = play ? n.pplayed : kNoCard;
+    const u64 pm = play ? floor_matches(n, played) : 0;
+    const u32 pmc = popc(pm);
+    const bool same = play && (played >> 2) == (card >> 2);
+    if (same && pmc == 1 && !r.last_turn) {  // resolve_turn's same-month cases: no choice
+      n.floor |= bit(played) | bit(card) | flipped;
+      const u16 mb = month_bit(played);
+      n.ppuk |= mb;
+      if (n.actor == 0) n.owner1 &= (u16)~mb; else n.owner1 |= mb;
+      if (flipped & bit(kBonus2)) n.b2ppuk |= mb;
+      if (flipped & bit(kBonus3)) n.b3ppuk |= mb;
+      r.events |= kEvPpuk;
+    } else if (same && pmc == 2) {
+      n.floor &= ~pm;
+      capture_cards(n, pm | bit(played) | bit(card) | flipped, r);
+      r.events |= kEvTtadak;
+    } else if (same && pmc == 0) {
+      capture_cards(n, bit(played) | bit(card) | flipped, r);
+      if (!r.last_turn) r.events |= kEvJjok;
+    } else {
+      if (play) {
+        const u8 rs = resolve_card_against_floor(n, played, a.pmatch, r);
+        if (rs == kResChoiceRequired) return Probe{kOk, kDecResolvePlayed, pm, card, 0};
+        if (rs != kResOk) return Probe{kInvalidResolveChoice, kDecNone, 0, card, 0};
+        n.pplayed = kNoCard;  // ResolveChoiceProbe50::table (postchance50.h:150-204)
+      }
+      const u64 candidates = floor_matches(n, card);
+      const u8 rs = resolve_card_against_floor(n, card, a.dmatch, r);
+      if (rs == kResChoiceRequired) {
+        if (special) {
+          n.pdrawn = card;
+          n.pend_bonus = flipped;
+        }
+        staged = n;
+        return Probe{kOk, kDecResolveDrawn, candidates, card, 0};
+      }
+      if (rs != kResOk) return Probe{kInvalidResolveChoice, kDecNone, 0, card, 0};
+      if (flipped) capture_cards(n, flipped, r);
+    }
+    if (n.floor == 0 && r.captured != 0) r.events |= kEvSweep;
+    finish_resolved_turn(n);
+    staged = n;
+    steal = (u8)(base_steal + steal_count(r));
+  }
+  return probe_pi_choice(staged, p, card, steal);
+}
+
+// postchance50.h:418-456, the turn-taking kinds per kind (the plain restatement of
+// probe_postchance, kept for the host check of the two).
+CG_HD Probe probe_postchance_per_kind(const Env& e, const Pending& p, Env& staged) {
   if (!p.active) { staged = e; return Probe{kWrongPhase, kDecNone, 0, kNoCard, 0}; }
   switch (p.action.kind) {
     case kPlayCard: return probe_regular(e, p, staged, false);
@@ -1860,6 +1987,22 @@ CG_HD Probe probe_postchance(const Env& e, const Pending& p, Env& staged) {
     case kGukjinPi:
     case kGukjinAnimal: staged = e; return Probe{kOk, kDecNone, 0, kNoCard, 0};
     default: staged = e; return Probe{kInvalidAction, kDecNone, 0, kNoCard, 0};
+  }
+}
+
+// postchance50.h:418-456
+CG_HD Probe probe_postchance(const Env& e, const Pending& p, Env& staged) {
+  if (!p.active) { staged = e; return Probe{kWrongPhase, kDecNone, 0, kNoCard, 0}; }
+  if (is_turn_kind(p.action.kind)) return probe_turn_action(e, p, staged);
+  staged = e;
+  switch (p.action.kind) {
+    case kGo:
+    case kStop:
+    case kChongtongWin:
+    case kChongtongContinue:
+    case kGukjinPi:
+    case kGukjinAnimal: return Probe{kOk, kDecNone, 0, kNoCard, 0};
+    default: return Probe{kInvalidAction, kDecNone, 0, kNoCard, 0};
   }
 }
 

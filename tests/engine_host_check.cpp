@@ -8,7 +8,10 @@
 //     shakes;
 //  4. apply_turn_action (the six turn-taking kinds as one transition) == the per-kind
 //     composition (rollout50.h:268-376) on states of random games: same status, and on
-//     success the same row.
+//     success the same row;
+//  5. probe_postchance (the same kinds' post-chance probe as one transition) ==
+//     probe_postchance_per_kind (postchance50.h:418-456) on the same states: same Probe
+//     fields, and where the probe succeeds the same staged row.
 // Prints one line per check and exits non-zero on the first mismatch.
 #include "engine.h"
 
@@ -125,7 +128,7 @@ static u8 any_bit(u64 m, std::mt19937_64& g) {
 static int check_turn_actions(std::mt19937_64& g) {
   static const u8 kinds[] = {kPlayCard, kPlayCard, kPlayCard, kShake, kPlayBonus,
                              kBomb, kGrenade, kBombCredit};
-  long cases = 0, ok = 0;
+  long cases = 0, ok = 0, probes = 0, probes_ok = 0, choices = 0;
   for (int game = 0; game < 3000; ++game) {
     Env e = create_env(g(), (u32)(g() & 1));
     for (int t = 0; t < 60 && !e.done; ++t) {
@@ -158,6 +161,28 @@ static int check_turn_actions(std::mt19937_64& g) {
           return 1;
         }
         ok += sx == kOk;
+        // The post-chance probe of the same action staged as the pending one.
+        Pending pd{a, 0, 0, (u8)(g() % 8 ? e.actor : g() & 1), 1};
+        if (g() % 4 == 0) pd.sel_pi = opp & g();
+        Env sa, sb;
+        const Probe pa = probe_postchance(e, pd, sa);
+        const Probe pb = probe_postchance_per_kind(e, pd, sb);
+        u64 qa[kRowWords], qb[kRowWords];
+        pack_row(sa, qa);
+        pack_row(sb, qb);
+        ++probes;
+        if (pa.status != pb.status || pa.decision != pb.decision ||
+            pa.legal_cards != pb.legal_cards || pa.revealed != pb.revealed ||
+            pa.requested != pb.requested ||
+            (pa.status == kOk && std::memcmp(qa, qb, sizeof qa) != 0)) {
+          std::printf("probe: game %d turn %d kind %u card %u month %u: status %u/%u "
+                      "decision %u/%u revealed %u/%u requested %u/%u\n", game, t, a.kind,
+                      a.card, a.month, pa.status, pb.status, pa.decision, pb.decision,
+                      pa.revealed, pb.revealed, pa.requested, pb.requested);
+          return 1;
+        }
+        probes_ok += pa.status == kOk;
+        choices += pa.decision != kDecNone;
       }
       // Advance the game with a uniform legal action.
       const PacketHead h = packet_head(e);
@@ -176,6 +201,8 @@ static int check_turn_actions(std::mt19937_64& g) {
     }
   }
   std::printf("turn actions: %ld cases (%ld applied) equal\n", cases, ok);
+  std::printf("post-chance probes: %ld cases (%ld ok, %ld open a choice) equal\n", probes,
+              probes_ok, choices);
   return 0;
 }
 
