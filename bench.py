@@ -5,12 +5,15 @@
 Workload (timed, one JSON line on stdout): random-policy self-play on B = 65,536
 GPU-resident games.  One step = observe (720 features + 179-way mask for every game)
 -> uniform legal sample (per-game xorshift64) -> step -> re-create finished games with
-their next seed (pre-dealt in a full-width batch every 8 steps, included in the timing).  `value` = complete games per second over K steps.  Games are dealt
-from seed = 0x243F6A8885A308D3 + i (+ B per later game of row i), first = i & 1.
+their next seed (pre-dealt in a full-width batch every 16 steps, included in the timing).
+`value` = complete games per second over K steps.  Games are dealt from
+seed = 0x243F6A8885A308D3 + i (+ B per later game of row i), first = i & 1.
 
 Also reported (not timed into `value`):
-  roofline      the observe kernel (the widest), bytes per row = 248 read + 3,063 written,
-                timed with HIP events on the stream it runs on
+  roofline      play_kernel (16 steps a launch, the loop's dominant kernel): algorithmic
+                bytes per launch over its duration, HIP events on its stream;
+                observe_roofline the same for the observe kernel (248 read + 3,063
+                written a row); store_ceiling what a plain fill reaches
   branch        4,096 roots (3-15 seeded random decisions deep) x 256 children:
                 branch_indexed (clone + step) and the observation of all children
   decode        sequence-policy decode over a [4, 4,096, 8, 320, 32] bf16 KV cache:
@@ -35,7 +38,11 @@ sys.path.insert(0, str(REPO))
 
 SEED_BASE = 0x243F6A8885A308D3
 HBM_PEAK_GBS = 8000.0
-REFILL = 8  # steps between batched pre-deals of the next games
+# Steps between batched pre-deals of the next games, and steps per play_random launch:
+# 16 measured best (8: 86M games/s, 16: 94M, 24: 94M, 32: 93M); a launch's first and last
+# steps run without the overlap of stores and stepping, and the refill is one launch of
+# create_env's latency whatever the number of stale rows.
+REFILL = 16
 OBSERVE_BYTES_PER_ROW = 248 + 720 * 4 + 179 + 1 + 1 + 2  # 3,311
 # play_random per row: every step writes the observation (2,880 + 179 + 4), the action (8)
 # and the step outputs (9); once per launch the state is read and written (2 x 248), the
