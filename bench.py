@@ -43,6 +43,10 @@ HBM_PEAK_GBS = 8000.0
 # steps run without the overlap of stores and stepping, and the refill is one launch of
 # create_env's latency whatever the number of stale rows.
 REFILL = 16
+# Pre-dealt next games per row: with games of about 20 steps, a row often finishes twice in
+# a block of 16, and a second finish with one spare slot deals its game inline (the whole
+# wavefront waits on create_env); two slots hold the next two games.
+SPARE_SLOTS = 2
 OBSERVE_BYTES_PER_ROW = 248 + 720 * 4 + 179 + 1 + 1 + 2  # 3,311
 # play_random per row: every step writes the observation (2,880 + 179 + 4), the action (8)
 # and the step outputs (9); once per launch the state is read and written (2 x 248), the
@@ -111,11 +115,13 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     sampler = ext.seed_samplers(batch, SEED_BASE, gen)
     # Next games are pre-dealt in full-width batches every REFILL steps; a finished row
     # copies its spare (dealt inline if stale), the same rows reset_done would deal.
-    spares = torch.empty((batch, 248), dtype=torch.uint8, device=dev)
-    spare_gen = torch.zeros(batch, dtype=torch.int32, device=dev)
     if batch % (2 * streams):
         raise SystemExit("the batch must split into slices of even length")
     width = batch // streams
+    spares = [torch.empty((SPARE_SLOTS * width, 248), dtype=torch.uint8, device=dev)
+              for _ in range(streams)]
+    spare_gen = [torch.zeros(SPARE_SLOTS * width, dtype=torch.int32, device=dev)
+                 for _ in range(streams)]
     side = [torch.cuda.Stream() for _ in range(streams)]
 
     def block(nsteps: int) -> None:
@@ -125,7 +131,7 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
             s.wait_stream(cur)
         for k, s in enumerate(side):
             r = slice(k * width, (k + 1) * width)
-            st, g, sm, sp, sg = states[r], gen[r], sampler[r], spares[r], spare_gen[r]
+            st, g, sm, sp, sg = states[r], gen[r], sampler[r], spares[k], spare_gen[k]
             base = SEED_BASE + k * width
             with torch.cuda.stream(s):
                 if fused and nsteps:
@@ -205,10 +211,11 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     # the launch) less 6 of refill_spares alone, so that only the first replay's submission
     # falls between the events.
     play_ms = None
-    if fused:
+    if fused and streams == 1:
         def block_once():
-            ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch)
-            ext.play_random(states, sampler, SEED_BASE, gen, spares, spare_gen, batch, REFILL)
+            ext.refill_spares(spares[0], spare_gen[0], gen, SEED_BASE, batch)
+            ext.play_random(states, sampler, SEED_BASE, gen, spares[0], spare_gen[0], batch,
+                            REFILL)
 
         def six(g) -> float:
             ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -220,7 +227,8 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
             return ev[0].elapsed_time(ev[1])
 
         blocks = graph_of(block_once, 1)
-        refills = graph_of(lambda: ext.refill_spares(spares, spare_gen, gen, SEED_BASE, batch), 1)
+        refills = graph_of(lambda: ext.refill_spares(spares[0], spare_gen[0], gen, SEED_BASE,
+                                                     batch), 1)
         play_ms = (six(blocks) - six(refills)) / 6
         del blocks, refills
     return {"seconds": seconds, "games": games, "observe_ms": observe_ms, "play_ms": play_ms}
@@ -764,7 +772,8 @@ def main() -> None:
                                   else "observe_sample + step_reset_spares per step"),
                    "batch": args.batch, "seed_base": hex(SEED_BASE),
                    "policy": "uniform legal action, per-game xorshift64",
-                   "streams": args.streams, "hip_graph": not args.no_graph},
+                   "streams": args.streams, "hip_graph": not args.no_graph,
+                   "spare_slots": SPARE_SLOTS},
         "steps_per_s": round(args.batch * args.steps / rp["seconds"], 1),
         "games_timed": rp["games"],
         "roofline": roofline,

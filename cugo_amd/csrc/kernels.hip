@@ -357,15 +357,24 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
 
 // --------------------------------------------------------------------- step ----
 // Auto-reset of finished rows inside the step (kMode 3): the next game of row i is
-// seed = base_seed + i + stride * (++generation[i]), copied from spare row i when
-// spare_gen[i] names it and dealt inline otherwise; sampler[i] is re-seeded from it.
+// seed = base_seed + i + stride * (++generation[i]), copied from its pre-dealt spare when
+// one is there and dealt inline otherwise; sampler[i] is re-seeded from it.  Spares come in
+// S = slot_mask + 1 slots of `rows` rows (S = 1, 2 or 4): generation g of row i is pre-dealt
+// in spare row (g & slot_mask) * rows + i, valid when spare_gen of that row equals g.
+// play_kernel deals a stale spare's game into its slot before taking it; the step
+// kernels only read the spares.
 struct AutoReset {
   u64 base_seed, stride;
   u32* generation;
   u64* sampler;
-  const u64* spares;
+  u64* spares;
   const u32* spare_gen;
+  i64 rows;
+  u32 slot_mask;
 };
+__device__ inline i64 spare_row(const AutoReset& ar, i64 i, u32 gen) {
+  return (i64)(gen & ar.slot_mask) * ar.rows + i;
+}
 
 // kMode: 0 = step (contiguous, in place), 1 = step_indexed (gather/scatter in place),
 // 2 = branch_indexed (gather from parents, children written contiguously),
@@ -385,6 +394,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
   __shared__ i64 tile_ids[kTile];
   __shared__ i64 ev[kTile * kEventWords];
   __shared__ int spare_rows[kTile];  // kMode 3: tile rows whose next game is a spare
+  __shared__ i64 spare_src[kTile];   // kMode 3: their spare rows
   __shared__ int spare_count;
   const i64 base = tile_base();
   const int count = tile_count(base, n);
@@ -396,9 +406,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
   __syncthreads();
   bool take_spare = false;
   u32 gen0 = 0, spare0 = 0;  // kMode 3: issued before the step so their latency hides
+  i64 src = 0;                // kMode 3: the spare row of generation gen0 + 1
   if (kMode == 3 && lane < count) {
     gen0 = ar.generation[base + lane];
-    spare0 = ar.spare_gen[base + lane];
+    src = spare_row(ar, base + lane, gen0 + 1u);
+    spare0 = ar.spare_gen[src];
   }
   if (lane < count) {
     const i64 i = base + lane;
@@ -448,14 +460,18 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
     // Compact the spare-taking rows so that every lane's spare load is independent:
     // a tile with f such rows moves 31 f words in ceil(31 f / threads) passes.
     const u64 ballot = __ballot(take_spare);
-    if (take_spare) spare_rows[__popcll(ballot & ((1ull << lane) - 1ull))] = lane;
+    if (take_spare) {
+      const int at = (int)__popcll(ballot & ((1ull << lane) - 1ull));
+      spare_rows[at] = lane;
+      spare_src[at] = src;
+    }
     if (lane == 0) spare_count = (int)__popcll(ballot);
     __syncthreads();
     const int words = spare_count * kRowWords;
     for (int j = lane; j < words; j += kStepThreads) {
-      const int r = spare_rows[j / kRowWords];
-      const int k = j - (j / kRowWords) * kRowWords;
-      rows[r * kRowWords + k] = ar.spares[(base + r) * kRowWords + k];
+      const int c = j / kRowWords;
+      const int k = j - c * kRowWords;
+      rows[spare_rows[c] * kRowWords + k] = ar.spares[spare_src[c] * kRowWords + k];
     }
   }
   __syncthreads();
@@ -483,6 +499,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
 // of a 65,536-row batch resident at once.
 constexpr int kPlayThreads = 128;
 constexpr int64_t kMaxPlaySteps = 1 << 20;
+
+// The game of `seed` dealt into the 31-word row `dst`.
+__device__ __attribute__((noinline)) void deal_into(u64 seed, u32 first, u64* dst) {
+  pack_row(create_env(seed, first), dst);
+}
 constexpr int kPlayClaim = 4;  // rows a store claim (the observe kernels' third wave needs 2)
 
 __global__ __launch_bounds__(kPlayThreads) __attribute__((amdgpu_waves_per_eu(2)))
@@ -505,11 +526,13 @@ void play_kernel(
     for (int j = tid; j < count * kRowWords; j += kPlayThreads) t.rows[j] = src[j];
   }
   const bool active = wave == 0 && lane < count;
-  u32 gen = 0, spare0 = 0;
-  u64 xc = 0;  // the committed sampler state
+  u32 gen = 0;
+  u32 have = 0;  // bit k: the spare of generation gen + 1 + k is pre-dealt
+  u64 xc = 0;    // the committed sampler state
   if (active) {  // issued early so their latency hides
     gen = ar.generation[i];
-    spare0 = ar.spare_gen[i];
+    for (u32 k = 0; k <= ar.slot_mask; ++k)
+      if (ar.spare_gen[spare_row(ar, i, gen + 1u + k)] == gen + 1u + k) have |= 1u << k;
     xc = sampler[i];
   }
   __syncthreads();
@@ -539,8 +562,12 @@ void play_kernel(
           ++gen;
           const u64 seed = ar.base_seed + (u64)i + ar.stride * gen;
           xc = sampler_seed(seed);
-          if (spare0 == gen) g = unpack_row(ar.spares + i * kRowWords);
-          else g = create_env(seed, (u32)(i & 1));
+          // A stale spare gets its game dealt into its own slot first (out of line: the
+          // deal inlined here doubles the loop's register pressure for a rare path).
+          const i64 row = spare_row(ar, i, gen);
+          if ((have & 1u) == 0) deal_into(seed, (u32)(i & 1), ar.spares + row * kRowWords);
+          g = unpack_row(ar.spares + row * kRowWords);
+          have >>= 1;
         } else if (a >= 0) {
           xc = xt;
         }
@@ -780,29 +807,37 @@ __global__ __launch_bounds__(kTile) void reset_kernel(u64* states, const u8* don
     if (flags[j / kRowWords]) out[j] = rows[j];
 }
 
-// Pre-deals the next game of each row whose spare is stale: spare row i <- game
-// generation[i] + 1 of row i, spare_gen[i] = generation[i] + 1.
+// Pre-deals the next S games of each row where their spares are stale: generation
+// g = generation[i] + k (k = 1 .. S) of row i goes to spare row (g & (S - 1)) * n + i, with
+// spare_gen of that row = g.  Block b serves k = 1 + b / tiles, so the S deals of a row run
+// side by side rather than one after another.
 __global__ __launch_bounds__(kTile) void refill_kernel(u64* spares, u32* spare_gen,
                                                        const u32* generation, i64 n,
-                                                       u64 base_seed, u64 stride) {
+                                                       u64 base_seed, u64 stride,
+                                                       u32 slot_mask, i64 tiles_per_slot) {
   __shared__ u64 rows[kTileWords];
   __shared__ int flags[kTile];
-  const i64 base = tile_base();
+  __shared__ i64 dst_row[kTile];
+  const u32 k = 1u + (u32)(blockIdx.x / tiles_per_slot);
+  const i64 base = (i64)(blockIdx.x % tiles_per_slot) * kTile;
   const int count = tile_count(base, n);
   const int lane = threadIdx.x;
   const i64 i = base + lane;
-  const u32 next = lane < count ? generation[i] + 1u : 0u;
-  const bool stale = lane < count && spare_gen[i] != next;
+  const u32 g = lane < count ? generation[i] + k : 0u;
+  const i64 dst = (i64)(g & slot_mask) * n + i;
+  const bool stale = lane < count && spare_gen[dst] != g;
   flags[lane] = stale;
+  dst_row[lane] = dst;
   if (stale) {
-    const u64 seed = base_seed + (u64)i + stride * next;
+    const u64 seed = base_seed + (u64)i + stride * g;
     pack_row(create_env(seed, (u32)(i & 1)), rows + lane * kRowWords);
-    spare_gen[i] = next;
+    spare_gen[dst] = g;
   }
   __syncthreads();
-  u64* out = spares + base * kRowWords;
-  for (int j = lane; j < count * kRowWords; j += kTile)
-    if (flags[j / kRowWords]) out[j] = rows[j];
+  for (int j = lane; j < count * kRowWords; j += kTile) {
+    const int r = j / kRowWords;
+    if (flags[r]) spares[dst_row[r] * kRowWords + (j - r * kRowWords)] = rows[j];
+  }
 }
 
 // reset_kernel's result, taking a finished row's next game from its pre-dealt spare
@@ -813,9 +848,11 @@ __global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u
                                                             u64* sampler,
                                                             unsigned long long* completed,
                                                             const u64* spares,
-                                                            const u32* spare_gen) {
+                                                            const u32* spare_gen,
+                                                            u32 slot_mask) {
   __shared__ u64 rows[kTileWords];
   __shared__ int flags[kTile];
+  __shared__ i64 src_row[kTile];
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int lane = threadIdx.x;
@@ -826,7 +863,9 @@ __global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u
   if (reset) {
     gen = generation[i] + 1u;
     generation[i] = gen;
-    from_spare = spare_gen[i] == gen;
+    const i64 src = (i64)(gen & slot_mask) * n + i;
+    src_row[lane] = src;
+    from_spare = spare_gen[src] == gen;
     sampler[i] = sampler_seed(base_seed + (u64)i + stride * gen);
   }
   // 1: copy the spare row, 2: the row dealt inline into LDS
@@ -840,10 +879,10 @@ __global__ __launch_bounds__(kTile) void reset_spare_kernel(u64* states, const u
   // Consecutive lanes move consecutive words of the tile's flagged rows: independent,
   // coalesced loads, spare rows straight from HBM to HBM.
   u64* out = states + base * kRowWords;
-  const u64* spare = spares + base * kRowWords;
   for (int j = lane; j < count * kRowWords; j += kTile) {
-    const int f = flags[j / kRowWords];
-    if (f == 1) out[j] = spare[j];
+    const int r = j / kRowWords;
+    const int f = flags[r];
+    if (f == 1) out[j] = spares[src_row[r] * kRowWords + (j - r * kRowWords)];
     else if (f == 2) out[j] = rows[j];
   }
 }
@@ -904,6 +943,8 @@ using namespace cugo_amd;
 
 namespace {
 inline unsigned tiles(int64_t n) { return (unsigned)((n + kTile - 1) / kTile); }
+// Spare slots per row: 1, 2 or 4 (a power of two: a generation's slot is a mask of it).
+inline bool valid_slots(int64_t s) { return s == 1 || s == 2 || s == 4; }
 
 // Compute units of the current device (cached per device).
 inline int device_cus() {
@@ -999,16 +1040,18 @@ int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* featu
                      uint8_t* legal, uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
                      int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
                      int16_t* status, uint8_t* committed, uint64_t base_seed,
-                     int64_t seed_stride, uint32_t* generation, const uint8_t* spares,
-                     const uint32_t* spare_gen, int64_t steps, hipStream_t stream) {
+                     int64_t seed_stride, uint32_t* generation, uint8_t* spares,
+                     const uint32_t* spare_gen, int64_t spare_slots, int64_t steps,
+                     hipStream_t stream) {
   if (n < 0 || seed_stride < 0 || steps < 1 || steps > kMaxPlaySteps ||
+      !valid_slots(spare_slots) ||
       (n > 0 && (!states || !sampler || !features || !legal || !player || !obs_done ||
                  !obs_status || !actions || !reward || !done || !nagari || !status ||
                  !committed || !generation || !spares || !spare_gen)))
     return kBadArgument;
   if (n == 0) return 0;
   const AutoReset ar{base_seed, (u64)seed_stride, generation, reinterpret_cast<u64*>(sampler),
-                     reinterpret_cast<const u64*>(spares), spare_gen};
+                     reinterpret_cast<u64*>(spares), spare_gen, n, (u32)(spare_slots - 1)};
   play_kernel<<<tiles(n), kPlayThreads, 0, stream>>>(
       reinterpret_cast<u64*>(states), n, reinterpret_cast<u64*>(sampler), features, legal,
       player, obs_done, obs_status, actions, reward, done, nagari, status, committed, ar,
@@ -1038,14 +1081,16 @@ int cugo_step_reset_spares(uint8_t* states, const int64_t* actions, int64_t n, f
                            uint8_t* done, uint8_t* nagari, int16_t* status, uint8_t* committed,
                            uint64_t base_seed, int64_t seed_stride, uint32_t* generation,
                            uint64_t* sampler, const uint8_t* spares, const uint32_t* spare_gen,
-                           hipStream_t stream) {
-  if (n < 0 || seed_stride < 0 ||
+                           int64_t spare_slots, hipStream_t stream) {
+  if (n < 0 || seed_stride < 0 || !valid_slots(spare_slots) ||
       (n > 0 && (!states || !actions || !reward || !done || !nagari || !status || !committed ||
                  !generation || !sampler || !spares || !spare_gen)))
     return kBadArgument;
   if (n == 0) return 0;
+  // step_kernel<3> only reads the spares
   const AutoReset ar{base_seed, (u64)seed_stride, generation, reinterpret_cast<u64*>(sampler),
-                     reinterpret_cast<const u64*>(spares), spare_gen};
+                     const_cast<u64*>(reinterpret_cast<const u64*>(spares)), spare_gen, n,
+                     (u32)(spare_slots - 1)};
   launch_step<3, false>(n, stream, reinterpret_cast<u64*>(states), n, nullptr, actions, n,
                         nullptr, reward, done, nagari, status, committed, nullptr, ar);
   return launched();
@@ -1153,26 +1198,30 @@ int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t ba
 }
 
 int cugo_refill_spares(uint8_t* spares, uint32_t* spare_gen, const uint32_t* generation,
-                       int64_t n, uint64_t base_seed, int64_t seed_stride, hipStream_t stream) {
-  if (n < 0 || seed_stride < 0 || (n > 0 && (!spares || !spare_gen || !generation)))
+                       int64_t n, uint64_t base_seed, int64_t seed_stride, int64_t spare_slots,
+                       hipStream_t stream) {
+  if (n < 0 || seed_stride < 0 || !valid_slots(spare_slots) ||
+      (n > 0 && (!spares || !spare_gen || !generation)))
     return kBadArgument;
   if (n == 0) return 0;
-  refill_kernel<<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<u64*>(spares), spare_gen,
-                                                generation, n, base_seed, (u64)seed_stride);
+  const i64 per_slot = tiles(n);
+  refill_kernel<<<(unsigned)(per_slot * spare_slots), kTile, 0, stream>>>(
+      reinterpret_cast<u64*>(spares), spare_gen, generation, n, base_seed, (u64)seed_stride,
+      (u32)(spare_slots - 1), per_slot);
   return launched();
 }
 
 int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
                            int64_t seed_stride, uint32_t* generation, uint64_t* sampler,
                            unsigned long long* completed, const uint8_t* spares,
-                           const uint32_t* spare_gen, hipStream_t stream) {
-  if (n < 0 || seed_stride < 0 ||
+                           const uint32_t* spare_gen, int64_t spare_slots, hipStream_t stream) {
+  if (n < 0 || seed_stride < 0 || !valid_slots(spare_slots) ||
       (n > 0 && (!states || !done || !generation || !sampler || !spares || !spare_gen)))
     return kBadArgument;
   if (n == 0) return 0;
   reset_spare_kernel<<<tiles(n), kTile, 0, stream>>>(
       reinterpret_cast<u64*>(states), done, n, base_seed, (u64)seed_stride, generation, sampler,
-      completed, reinterpret_cast<const u64*>(spares), spare_gen);
+      completed, reinterpret_cast<const u64*>(spares), spare_gen, (u32)(spare_slots - 1));
   return launched();
 }
 

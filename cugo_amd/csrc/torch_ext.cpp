@@ -292,19 +292,29 @@ void reset_done(torch::Tensor states, torch::Tensor done, int64_t base_seed,
              "reset_done");
 }
 
+// Spare slots per row: spares holds S * n rows (S = 1, 2 or 4) and spare_gen S * n entries,
+// slot-major (the C ABI's cugo_refill_spares layout).
+int64_t spare_slots(const torch::Tensor& spares, const torch::Tensor& spare_gen, int64_t n) {
+  const int64_t rows = spares.size(0);
+  const int64_t s = n > 0 ? rows / n : 1;
+  TORCH_CHECK(n > 0 ? rows == s * n && (s == 1 || s == 2 || s == 4) : rows == 0,
+              "spares must hold 1, 2 or 4 rows per game row");
+  TORCH_CHECK(spare_gen.numel() == rows, "spare_gen must have one entry per spare row");
+  return s;
+}
+
 void refill_spares(torch::Tensor spares, torch::Tensor spare_gen, torch::Tensor generation,
                    int64_t base_seed, int64_t seed_stride) {
   check_states(spares);
-  const int64_t n = spares.size(0);
   check_1d(spare_gen, at::kInt, "spare_gen");
   check_1d(generation, at::kInt, "generation");
-  TORCH_CHECK(spare_gen.numel() == n && generation.numel() == n,
-              "spare_gen and generation must have one entry per spare row");
+  const int64_t n = generation.numel();
+  const int64_t slots = spare_slots(spares, spare_gen, n);
   const DeviceGuard guard(spares.device());
   check_call(cugo_refill_spares(u8p(spares), reinterpret_cast<uint32_t*>(spare_gen.data_ptr()),
                                 reinterpret_cast<const uint32_t*>(generation.data_ptr()), n,
                                 static_cast<uint64_t>(base_seed),
-                                seed_stride < 0 ? n : seed_stride, stream()),
+                                seed_stride < 0 ? n : seed_stride, slots, stream()),
              "refill_spares");
 }
 
@@ -319,9 +329,9 @@ void reset_done_spares(torch::Tensor states, torch::Tensor done, int64_t base_se
   check_1d(generation, at::kInt, "generation");
   check_1d(sampler, at::kLong, "sampler");
   check_1d(spare_gen, at::kInt, "spare_gen");
-  TORCH_CHECK(done.numel() == n && generation.numel() == n && sampler.numel() == n &&
-                  spares.size(0) == n && spare_gen.numel() == n,
-              "done, generation, sampler, spares and spare_gen must have one entry per row");
+  TORCH_CHECK(done.numel() == n && generation.numel() == n && sampler.numel() == n,
+              "done, generation and sampler must have one entry per row");
+  const int64_t slots = spare_slots(spares, spare_gen, n);
   const DeviceGuard guard(states.device());
   check_call(cugo_reset_done_spares(
                  u8p(states), u8p(done), n, static_cast<uint64_t>(base_seed),
@@ -329,7 +339,7 @@ void reset_done_spares(torch::Tensor states, torch::Tensor done, int64_t base_se
                  reinterpret_cast<uint32_t*>(generation.data_ptr()),
                  reinterpret_cast<uint64_t*>(sampler.data_ptr()),
                  counter_ptr(completed, states), u8p(spares),
-                 reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), stream()),
+                 reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), slots, stream()),
              "reset_done_spares");
 }
 
@@ -370,9 +380,9 @@ std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampl
   check_1d(sampler, at::kLong, "sampler");
   check_1d(generation, at::kInt, "generation");
   check_1d(spare_gen, at::kInt, "spare_gen");
-  TORCH_CHECK(sampler.numel() == n && generation.numel() == n && spares.size(0) == n &&
-                  spare_gen.numel() == n,
-              "sampler, generation, spares and spare_gen must have one entry per row");
+  TORCH_CHECK(sampler.numel() == n && generation.numel() == n,
+              "sampler and generation must have one entry per row");
+  const int64_t slots = spare_slots(spares, spare_gen, n);
   check_same_device(states, sampler, "states", "sampler");
   check_same_device(states, generation, "states", "generation");
   check_same_device(states, spares, "states", "spares");
@@ -389,8 +399,8 @@ std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampl
                               o[9].data_ptr<int16_t>(), u8p(o[10]),
                               static_cast<uint64_t>(base_seed), seed_stride < 0 ? n : seed_stride,
                               reinterpret_cast<uint32_t*>(generation.data_ptr()), u8p(spares),
-                              reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), steps,
-                              stream()),
+                              reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), slots,
+                              steps, stream()),
              "play_random");
   return o;
 }
@@ -407,9 +417,9 @@ std::vector<torch::Tensor> step_reset_spares(torch::Tensor states, torch::Tensor
   check_1d(generation, at::kInt, "generation");
   check_1d(sampler, at::kLong, "sampler");
   check_1d(spare_gen, at::kInt, "spare_gen");
-  TORCH_CHECK(actions.numel() == n && generation.numel() == n && sampler.numel() == n &&
-                  spares.size(0) == n && spare_gen.numel() == n,
-              "actions, generation, sampler, spares and spare_gen must have one entry per row");
+  TORCH_CHECK(actions.numel() == n && generation.numel() == n && sampler.numel() == n,
+              "actions, generation and sampler must have one entry per row");
+  const int64_t slots = spare_slots(spares, spare_gen, n);
   check_same_device(states, actions, "states", "actions");
   check_same_device(states, generation, "states", "generation");
   check_same_device(states, sampler, "states", "sampler");
@@ -423,7 +433,7 @@ std::vector<torch::Tensor> step_reset_spares(torch::Tensor states, torch::Tensor
                  static_cast<uint64_t>(base_seed), seed_stride < 0 ? n : seed_stride,
                  reinterpret_cast<uint32_t*>(generation.data_ptr()),
                  reinterpret_cast<uint64_t*>(sampler.data_ptr()), u8p(spares),
-                 reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), stream()),
+                 reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), slots, stream()),
              "step_reset_spares");
   return o;
 }

@@ -118,21 +118,26 @@ int cugo_observe_sample(const uint8_t* states, int64_t n, float* features, uint8
 int cugo_reset_done(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
                     uint32_t* generation, uint64_t* sampler, unsigned long long* completed,
                     hipStream_t stream);
-/* Pre-dealt next games for cugo_reset_done_spares: every row i whose spare_gen[i] is not
- * generation[i] + 1 gets game generation[i] + 1 of row i dealt into spare row i
- * (seed = base_seed + i + seed_stride * (generation[i] + 1), first = i & 1) and
- * spare_gen[i] set.  spares: uint8 [n, CUGO_STATE_BYTES]; spare_gen: uint32 [n], start
- * it at 0.  seed_stride = n gives cugo_reset_done's seeds; a slice of a larger batch
- * starting at an even row r0 passes base_seed + r0 and the whole batch's size. */
+/* Pre-dealt next games for cugo_reset_done_spares: each row i holds spares for its next
+ * S = spare_slots games (1, 2 or 4).  Game g of row i (seed = base_seed + i +
+ * seed_stride * g, first = i & 1) is pre-dealt in spare row (g & (S - 1)) * n + i, valid
+ * when spare_gen of that row equals g.  For g = generation[i] + 1 .. generation[i] + S,
+ * every stale one is dealt and its spare_gen set.  spares: uint8 [S * n,
+ * CUGO_STATE_BYTES]; spare_gen: uint32 [S * n], start it at 0.  seed_stride = n gives
+ * cugo_reset_done's seeds; a slice of a larger batch starting at an even row r0 passes
+ * base_seed + r0 and the whole batch's size.  More slots serve rows that finish several
+ * games between refills without dealing inline. */
 int cugo_refill_spares(uint8_t* spares, uint32_t* spare_gen, const uint32_t* generation,
-                       int64_t n, uint64_t base_seed, int64_t seed_stride, hipStream_t stream);
+                       int64_t n, uint64_t base_seed, int64_t seed_stride, int64_t spare_slots,
+                       hipStream_t stream);
 /* Same effect as cugo_reset_done with seed = base_seed + i + seed_stride * generation[i],
- * except that a finished row copies its next game from its spare row when spare_gen[i]
- * names it (deals it inline otherwise). */
+ * except that a finished row copies its next game from its pre-dealt spare (the
+ * cugo_refill_spares layout with the same spare_slots) when one is there, and deals it
+ * inline otherwise. */
 int cugo_reset_done_spares(uint8_t* states, const uint8_t* done, int64_t n, uint64_t base_seed,
                            int64_t seed_stride, uint32_t* generation, uint64_t* sampler,
                            unsigned long long* completed, const uint8_t* spares,
-                           const uint32_t* spare_gen, hipStream_t stream);
+                           const uint32_t* spare_gen, int64_t spare_slots, hipStream_t stream);
 /* cugo_branch_indexed followed by cugo_observe_indexed of the children (ids 0..n-1), in
  * one launch (the reference's callers do both, python/cugo_ppo50.py:96-98): children and
  * the step outputs as cugo_branch_indexed, then the children's observation as
@@ -150,22 +155,25 @@ int cugo_branch_observe_indexed(const uint8_t* states, int64_t env_count, const 
  * outputs) are the last step's, and every step's observation is written.  The games stay
  * on chip between steps, and one step's observation stores overlap the step and the next
  * observation.  The reference's loop calls observe, samples and steps once per step
- * (python/torch50_smoke.py); steps = 1 is that loop's step in one launch. */
+ * (python/torch50_smoke.py); steps = 1 is that loop's step in one launch.  A finished row
+ * whose next game's spare is stale gets that game dealt into the spare's slot (spare_gen is
+ * left as it was) and takes it from there. */
 int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
                      uint8_t* legal, uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
                      int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
                      int16_t* status, uint8_t* committed, uint64_t base_seed,
-                     int64_t seed_stride, uint32_t* generation, const uint8_t* spares,
-                     const uint32_t* spare_gen, int64_t steps, hipStream_t stream);
+                     int64_t seed_stride, uint32_t* generation, uint8_t* spares,
+                     const uint32_t* spare_gen, int64_t spare_slots, int64_t steps,
+                     hipStream_t stream);
 /* cugo_step followed by cugo_reset_done_spares(states, done, n, base_seed, seed_stride,
- * generation, sampler, NULL, spares, spare_gen) in one launch: the outputs are the
+ * generation, sampler, NULL, spares, spare_gen, spare_slots) in one launch: the outputs are the
  * step's (done[i] = 1 for the game that just finished), and each finished row already
  * holds its next game when the call returns. */
 int cugo_step_reset_spares(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
                            uint8_t* done, uint8_t* nagari, int16_t* status, uint8_t* committed,
                            uint64_t base_seed, int64_t seed_stride, uint32_t* generation,
                            uint64_t* sampler, const uint8_t* spares, const uint32_t* spare_gen,
-                           hipStream_t stream);
+                           int64_t spare_slots, hipStream_t stream);
 /* redeal (python/cugo_ppo50.py:122-148, `_redeal`) in place on rows [n, CUGO_STATE_BYTES]
  * for observer seat[i], given the reference's random draws: keys f32 [n, 50]
  * (torch.rand(n, 50)) rank the unknown cards (the opponent's cards not shown by a shake,

@@ -591,3 +591,52 @@ def test_play_random_steps_match_single_steps(ext, n):
     assert int(gen_a.sum().item()) > n // 2
     with pytest.raises(RuntimeError):
         ext.play_random(b, smp_b, base, gen_b, sp_b, sg_b, steps=0)
+
+
+@pytest.mark.parametrize("slots", [2, 4])
+def test_spare_slots_do_not_change_results(ext, slots):
+    """Several pre-dealt games per row (spares [slots * n, 248], slot-major) change where
+    a finished row's next game comes from, never which game it is: play_random blocks of
+    16 steps, and step_reset_spares / reset_done_spares step by step, give the same rows,
+    generations, samplers and outputs as one slot, at a partial last tile."""
+    announce(f"spare slots ({slots})")
+    n, base = 3001 * 2, 0x27182818
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    a = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(np.arange(n) & 1).to(DEV))
+    gen_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp_a = ext.seed_samplers(n, base, gen_a)
+    b, gen_b, smp_b = a.clone(), gen_a.clone(), smp_a.clone()
+    sp_a = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
+    sg_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    sp_b = torch.zeros((slots * n, 248), dtype=torch.uint8, device=DEV)
+    sg_b = torch.zeros(slots * n, dtype=torch.int32, device=DEV)
+    for block in range(4):
+        ext.refill_spares(sp_a, sg_a, gen_a, base)
+        ext.refill_spares(sp_b, sg_b, gen_b, base)
+        x = ext.play_random(a, smp_a, base, gen_a, sp_a, sg_a, steps=16)
+        y = ext.play_random(b, smp_b, base, gen_b, sp_b, sg_b, steps=16)
+        for j, (u, v) in enumerate(zip(x, y)):
+            assert torch.equal(u, v), (block, j)
+        assert torch.equal(a, b) and torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), block
+    # the two-launch path: every slot's refill, then single steps with auto-reset
+    ext.refill_spares(sp_a, sg_a, gen_a, base)
+    ext.refill_spares(sp_b, sg_b, gen_b, base)
+    for t in range(12):
+        _, _, _, _, _, act = ext.observe_sample(a, smp_a)
+        _, _, _, _, _, act_b = ext.observe_sample(b, smp_b)
+        assert torch.equal(act, act_b), t
+        if t % 2:
+            x = ext.step_reset_spares(a, act, base, gen_a, smp_a, sp_a, sg_a)
+            y = ext.step_reset_spares(b, act, base, gen_b, smp_b, sp_b, sg_b)
+        else:
+            x = ext.step(a, act)
+            y = ext.step(b, act)
+            ext.reset_done_spares(a, x[1].bool(), base, gen_a, smp_a, None, sp_a, sg_a)
+            ext.reset_done_spares(b, y[1].bool(), base, gen_b, smp_b, None, sp_b, sg_b)
+        for j, (u, v) in enumerate(zip(x, y)):
+            assert torch.equal(u, v), (t, j)
+        assert torch.equal(a, b) and torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), t
+    assert int(gen_a.sum().item()) > n
+    with pytest.raises(RuntimeError):
+        ext.refill_spares(torch.zeros((3 * n, 248), dtype=torch.uint8, device=DEV),
+                          torch.zeros(3 * n, dtype=torch.int32, device=DEV), gen_b, base)
