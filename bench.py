@@ -5,12 +5,12 @@
 Workload (timed, one JSON line on stdout): random-policy self-play on B = 65,536
 GPU-resident games.  One step = observe (720 features + 179-way mask for every game)
 -> uniform legal sample (per-game xorshift64) -> step -> re-create finished games with
-their next seed (pre-dealt in a full-width batch every 16 steps, included in the timing).
+their next seed (pre-dealt in a full-width batch every 32 steps, included in the timing).
 `value` = complete games per second over K steps.  Games are dealt from
 seed = 0x243F6A8885A308D3 + i (+ B per later game of row i), first = i & 1.
 
 Also reported (not timed into `value`):
-  roofline      play_kernel (16 steps a launch, the loop's dominant kernel): algorithmic
+  roofline      play_kernel (32 steps a launch, the loop's dominant kernel): algorithmic
                 bytes per launch over its duration, HIP events on its stream;
                 observe_roofline the same for the observe kernel (248 read + 3,063
                 written a row); store_ceiling what a plain fill reaches
@@ -38,14 +38,15 @@ sys.path.insert(0, str(REPO))
 
 SEED_BASE = 0x243F6A8885A308D3
 HBM_PEAK_GBS = 8000.0
-# Steps between batched pre-deals of the next games, and steps per play_random launch:
-# 16 measured best (8: 86M games/s, 16: 94M, 24: 94M, 32: 93M); a launch's first and last
-# steps run without the overlap of stores and stepping, and the refill is one launch of
-# create_env's latency whatever the number of stale rows.
-REFILL = 16
-# Pre-dealt next games per row: with games of about 20 steps, a row often finishes twice in
-# a block of 16, and a second finish with one spare slot deals its game inline (the whole
-# wavefront waits on create_env); two slots hold the next two games.
+# Steps between batched pre-deals of the next games, and steps per play_random launch.  A
+# launch's first and last steps run without the overlap of stores and stepping and the
+# refill is one launch of create_env's latency, so longer blocks amortise both, while rows
+# that finish more often than there are spare slots deal inline.  With two slots: 16 steps
+# 97M games/s, 24: 100M, 32: 101M, 48: 99M (one slot: 8: 86M, 16: 95M, 32: 93M).
+REFILL = 32
+# Pre-dealt next games per row: games last about 20 steps, so a row finishes about 1.6
+# times in a block of 32, and a finish with no spare left deals its game inline (the whole
+# wavefront waits on create_env); two slots hold the next two games (four: 99M games/s).
 SPARE_SLOTS = 2
 OBSERVE_BYTES_PER_ROW = 248 + 720 * 4 + 179 + 1 + 1 + 2  # 3,311
 # play_random per row: every step writes the observation (2,880 + 179 + 4), the action (8)
@@ -77,8 +78,8 @@ def measured_traffic(kernel: str, key: str) -> int | None:
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=1000)
-    p.add_argument("--warmup", type=int, default=100)
+    p.add_argument("--steps", type=int, default=1024)
+    p.add_argument("--warmup", type=int, default=128)
     p.add_argument("--batch", type=int, default=65536)
     p.add_argument("--branch-iters", type=int, default=20)
     p.add_argument("--no-branch", action="store_true")

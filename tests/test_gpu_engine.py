@@ -566,7 +566,7 @@ def test_branch_observe_full_batch(ext, ref):
 @pytest.mark.parametrize("n", [3001 * 2, 65536])
 def test_play_random_steps_match_single_steps(ext, n):
     """play_random(steps=K) == K calls of one step: rows, generations, samplers and the
-    eleven outputs of the last step, for K = 1, 3, 8 and 16 (the bench's block) over several
+    eleven outputs of the last step, for K = 1, 3, 8, 16 and 32 (the bench's block) over several
     blocks, with the spares refilled only every other block (so spare and inline re-deals
     both occur), at a partial last tile and at the full batch."""
     announce(f"play_random steps (n={n})")
@@ -578,7 +578,7 @@ def test_play_random_steps_match_single_steps(ext, n):
     sp_a = torch.zeros((n, 248), dtype=torch.uint8, device=DEV)
     sg_a = torch.zeros(n, dtype=torch.int32, device=DEV)
     b, gen_b, smp_b, sp_b, sg_b = (t.clone() for t in (a, gen_a, smp_a, sp_a, sg_a))
-    for block, k in enumerate([8, 3, 16, 1, 8, 16]):
+    for block, k in enumerate([8, 3, 16, 1, 32, 16]):
         if block % 2 == 0:
             ext.refill_spares(sp_a, sg_a, gen_a, base)
             ext.refill_spares(sp_b, sg_b, gen_b, base)
