@@ -32,6 +32,13 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert lib.cugo_create(None, None, -1, None, None) < 0
     assert lib.cugo_create(None, None, 5, None, None) < 0
     assert lib.cugo_create(None, None, 0, None, None) == 0
+    # spare slots: 1, 2 or 4 pre-dealt games per row; any other count is refused
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.cugo_refill_spares.argtypes = [P, P, P, I, ctypes.c_uint64, I, I, P]
+    buf = ctypes.create_string_buffer(64)
+    for slots, want_ok in ((1, True), (2, True), (4, True), (0, False), (3, False), (8, False)):
+        rc = lib.cugo_refill_spares(buf, buf, buf, 0, 0, 0, slots, None)
+        assert (rc == 0) == want_ok, (slots, rc)
 
 
 def test_extension_module_constants():
