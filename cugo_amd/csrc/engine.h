@@ -2100,9 +2100,38 @@ CG_HD Env create_env(u64 seed, u32 first) {
   u64 s = seed;
   u64 remaining = kDeckMask;
   u64 hand0 = 0, hand1 = 0, floor = 0;
-  for (int i = 0; i < 10; ++i) hand0 |= bit(draw_uniform(remaining, s));
-  for (int i = 0; i < 10; ++i) hand1 |= bit(draw_uniform(remaining, s));
-  for (int i = 0; i < 8; ++i) floor |= bit(draw_uniform(remaining, s));
+  // Draw k (k = 0 .. 27) picks among 50 - k cards with the (k + 1)-th SplitMix64 word of
+  // the seed, unless Lemire's product falls below the bound (then uniform_bounded may
+  // redraw).  The words do not depend on the cards, so they are computed up front, side by
+  // side, and only the picks run in sequence; a deal with any product below its bound
+  // (about 28 x 50 / 2^32 of deals) takes the draw-by-draw path instead.
+  u32 rank[28];
+  bool direct = true;
+#pragma unroll
+  for (int k = 0; k < 28; ++k) {
+    u64 w = seed + (u64)(k + 1) * 0x9e3779b97f4a7c15ull;
+    w = (w ^ (w >> 30)) * 0xbf58476d1ce4e5b9ull;
+    w = (w ^ (w >> 27)) * 0x94d049bb133111ebull;
+    w ^= w >> 31;
+    const u64 product = (u64)(u32)(w >> 32) * (u64)(50 - k);
+    direct = direct && (u32)product >= (u32)(50 - k);
+    rank[k] = (u32)(product >> 32);
+  }
+  if (direct) {
+#pragma unroll
+    for (int k = 0; k < 28; ++k) {
+      const u8 card = select_rank(remaining, rank[k]);
+      remaining &= ~bit(card);
+      if (k < 10) hand0 |= bit(card);
+      else if (k < 20) hand1 |= bit(card);
+      else floor |= bit(card);
+    }
+    s = seed + 28ull * 0x9e3779b97f4a7c15ull;
+  } else {
+    for (int i = 0; i < 10; ++i) hand0 |= bit(draw_uniform(remaining, s));
+    for (int i = 0; i < 10; ++i) hand1 |= bit(draw_uniform(remaining, s));
+    for (int i = 0; i < 8; ++i) floor |= bit(draw_uniform(remaining, s));
+  }
   const u64 deal_rng = s;
   Env e;
   e.hand0 = hand0; e.hand1 = hand1; e.cap0 = 0; e.cap1 = 0;

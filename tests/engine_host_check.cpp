@@ -11,13 +11,17 @@
 //     success the same row;
 //  5. probe_postchance (the same kinds' post-chance probe as one transition) ==
 //     probe_postchance_per_kind (postchance50.h:418-456) on the same states: same Probe
-//     fields, and where the probe succeeds the same staged row.
+//     fields, and where the probe succeeds the same staged row;
+//  6. create_env's deal (the draws' SplitMix64 words computed up front) == the draw-by-draw
+//     deal (deal.h:82-92 with draw_uniform) on random seeds and on seeds where a draw's
+//     Lemire product falls below its bound (found by search, so the fallback runs).
 // Prints one line per check and exits non-zero on the first mismatch.
 #include "engine.h"
 
 #include <cstdio>
 #include <cstring>
 #include <random>
+#include <vector>
 
 using namespace cugo_amd;
 
@@ -206,11 +210,59 @@ static int check_turn_actions(std::mt19937_64& g) {
   return 0;
 }
 
+// deal.h:82-92 draw by draw: hands of 10, floor of 8, the stream left after them.
+static void deal_by_draws(u64 seed, u64& h0, u64& h1, u64& fl, u64& rest, u64& rng) {
+  u64 s = seed, remaining = kDeckMask;
+  h0 = h1 = fl = 0;
+  for (int i = 0; i < 10; ++i) h0 |= bit(draw_uniform(remaining, s));
+  for (int i = 0; i < 10; ++i) h1 |= bit(draw_uniform(remaining, s));
+  for (int i = 0; i < 8; ++i) fl |= bit(draw_uniform(remaining, s));
+  rest = remaining;
+  rng = s;
+}
+
+// Some draw of the deal of `seed` has Lemire's low word below its bound.
+static bool low_draw(u64 seed) {
+  u64 s = seed;
+  for (u32 k = 0; k < 28; ++k) {
+    const u64 product = (u64)(u32)(sm_next(s) >> 32) * (50u - k);
+    if ((u32)product < 50u - k) return true;
+  }
+  return false;
+}
+
+static int check_deal(std::mt19937_64& g) {
+  std::vector<u64> seeds;
+  for (int i = 0; i < 200000; ++i) seeds.push_back(g());
+  int found = 0;
+  for (u64 seed = 0x9E3779B97F4A7C15ull; found < 4; seed += 0x2545F4914F6CDD1Dull)
+    if (low_draw(seed)) { seeds.push_back(seed); ++found; }
+  for (const u64 seed : seeds) {
+    const Env e = create_env(seed, (u32)(seed & 1));
+    u64 h0, h1, fl, rest, rng;
+    deal_by_draws(seed, h0, h1, fl, rest, rng);
+    // create_env moves floor bonus cards to the first player and refills the floor from
+    // the stock: compare before that, through the cards and the stream it left.
+    const u64 bonus = fl & kBonusMask;
+    const u64 caps = e.cap0 | e.cap1;
+    if (e.hand0 != h0 || e.hand1 != h1 || (bonus != 0 ? (caps & bonus) != bonus
+                                                      : (e.floor != fl || e.stock != rest ||
+                                                         e.rng != rng))) {
+      std::printf("deal: seed %llx differs\n", (unsigned long long)seed);
+      return 1;
+    }
+  }
+  std::printf("deal: %zu seeds (%d with a draw in the rejection zone) equal\n", seeds.size(),
+              found);
+  return 0;
+}
+
 int main() {
   std::mt19937_64 g(20261201);
   if (check_records(g)) return 1;
   if (check_steal(g)) return 1;
   if (check_special_months(g)) return 1;
   if (check_turn_actions(g)) return 1;
+  if (check_deal(g)) return 1;
   return 0;
 }

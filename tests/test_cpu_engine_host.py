@@ -4,8 +4,9 @@ tests/engine_host_check.cpp includes cugo_amd/csrc/engine.h in host code and che
 feature record decode against feature_at, the steal selection against the reference's
 card-by-card loop, the special-play months against legal_special_months, and the six
 turn-taking kinds as one transition (apply_turn_action) and their post-chance probe
-(probe_postchance) against the per-kind compositions (the GPU parity tests check the same
-functions end to end against the oracle).
+(probe_postchance) against the per-kind compositions, and create_env's deal against the
+draw-by-draw deal (the GPU parity tests check the same functions end to end against the
+oracle).
 """
 
 from __future__ import annotations
@@ -30,4 +31,4 @@ def test_engine_helpers_match_plain_formulations(tmp_path):
                     "-o", str(exe)], check=True, capture_output=True, timeout=300)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stdout + out.stderr
-    assert out.stdout.count("equal") == 5, out.stdout
+    assert out.stdout.count("equal") == 6, out.stdout
