@@ -11,9 +11,11 @@ and the generated csrc/stop_bits.inc table (the host C library's log2f, see belo
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 import sysconfig
+import tempfile
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -22,7 +24,10 @@ CSRC = PKG / "csrc"
 ARCH = os.environ.get("CUGO_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-# Shared by every HIP compile: IEEE fp32 division, no contraction, no packed fp32.
+# Shared by every HIP compile: IEEE fp32 division, no contraction, no packed fp32.  The
+# packed-fp32 feature switch applies to the device pass (a float2 multiply-add probe
+# compiles to one packed FMA without it and to two scalar ones with it); hipcc's host pass
+# warns that it does not know the feature.  check_no_packed_fp32() verifies the result.
 HIP_FLAGS = [
     "-O3",
     "-std=c++17",
@@ -67,12 +72,52 @@ def generate_stop_bits(force: bool = True) -> Path:
     return out
 
 
+LLVM_BIN = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "llvm" / "bin"
+PACKED_FP32 = re.compile(r"\bv_pk_(add|mul|fma)_f32\b")
+BUNDLE_MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
+
+
+def device_disassembly(lib: Path) -> str:
+    """The gfx950 disassembly of every code object in `lib`'s .hip_fatbin section (one
+    offload bundle per source file, concatenated)."""
+    with tempfile.TemporaryDirectory() as tmp:
+        fatbin = Path(tmp) / "fatbin"
+        _run(["objcopy", "--dump-section", f".hip_fatbin={fatbin}", str(lib)])
+        data = fatbin.read_bytes()
+        starts = [m.start() for m in re.finditer(re.escape(BUNDLE_MAGIC), data)]
+        text = []
+        for k, begin in enumerate(starts):
+            end = starts[k + 1] if k + 1 < len(starts) else len(data)
+            part, obj = Path(tmp) / f"b{k}", Path(tmp) / f"b{k}.co"
+            part.write_bytes(data[begin:end])
+            _run([str(LLVM_BIN / "clang-offload-bundler"), "--type=o",
+                  f"--targets=hipv4-amdgcn-amd-amdhsa--{ARCH}", f"--input={part}",
+                  f"--output={obj}", "--unbundle"])
+            text.append(subprocess.run([str(LLVM_BIN / "llvm-objdump"), "-d", str(obj)],
+                                       check=True, capture_output=True, text=True).stdout)
+        return "\n".join(text)
+
+
+def check_no_packed_fp32(lib: Path) -> None:
+    """Fails the build when the device code holds a packed fp32 add, multiply or FMA (some
+    of their forms have given wrong results on this hardware without an error)."""
+    asm = device_disassembly(lib)
+    if not asm.strip():
+        raise RuntimeError(f"{lib}: no device code found to check")
+    hits = sorted({m.group(0) for m in PACKED_FP32.finditer(asm)})
+    if hits:
+        raise RuntimeError(f"{lib}: packed fp32 instructions in device code: {hits}")
+    print(f"  {lib.name}: no packed fp32 instructions in {asm.count(chr(10))} lines of "
+          "device code", flush=True)
+
+
 def build_library() -> Path:
     generate_stop_bits()
     out = PKG / "libcugo_hip.so"
     _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "kernels.hip"), str(CSRC / "decode.hip"),
           str(CSRC / "selfplay.hip"),
           "-o", str(out)])
+    check_no_packed_fp32(out)
     return out
 
 

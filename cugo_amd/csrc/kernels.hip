@@ -506,11 +506,14 @@ __device__ __attribute__((noinline)) void deal_into(u64 seed, u32 first, u64* ds
 }
 constexpr int kPlayClaim = 4;  // rows a store claim (the observe kernels' third wave needs 2)
 
+// step_rows = 0: every step's outputs overwrite the same n rows (the loop keeps only the
+// last step's); step_rows >= n, a multiple of 4: step s writes rows s * step_rows + i of
+// outputs with `steps` blocks of step_rows rows, so every step's observation is kept.
 __global__ __launch_bounds__(kPlayThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void play_kernel(
     u64* states, i64 n, u64* sampler, float* features, u8* legal, u8* player, u8* obs_done,
     i16* obs_status, i64* actions, float* reward, u8* done, u8* nagari, i16* status,
-    u8* committed, AutoReset ar, int steps) {
+    u8* committed, AutoReset ar, int steps, i64 step_rows) {
   __shared__ ObserveTile t;    // the rows, then the records of even steps, then the rows
   __shared__ RecordBuffer t1;  // the records of odd steps
   __shared__ int next_item[2];  // store_observation's work counters, by step parity
@@ -553,11 +556,12 @@ void play_kernel(
         // private memory.
         Env g = e;
         const StepOut so = torch_step_head(g, clamp_action(a), head);
-        reward[i] = (float)so.reward0;
-        done[i] = so.done;
-        nagari[i] = so.nagari;
-        status[i] = (i16)so.status;
-        committed[i] = so.committed;
+        const i64 at = i + (i64)(s - 1) * step_rows;  // step s - 1's output row
+        reward[at] = (float)so.reward0;
+        done[at] = so.done;
+        nagari[at] = so.nagari;
+        status[at] = (i16)so.status;
+        committed[at] = so.committed;
         if (so.done) {  // the next game: this generation's spare, or dealt here if stale
           ++gen;
           const u64 seed = ar.base_seed + (u64)i + ar.stride * gen;
@@ -582,18 +586,23 @@ void play_kernel(
         cur.legal[lane][0] = pk.head.legal.w0;
         cur.legal[lane][1] = pk.head.legal.w1;
         cur.legal[lane][2] = pk.head.legal.w2;
-        player[i] = pk.head.player;
-        obs_done[i] = seen.done != 0;
-        obs_status[i] = (i16)pk.head.status;
+        const i64 at = i + (i64)s * step_rows;  // step s's output row
+        player[at] = pk.head.player;
+        obs_done[at] = seen.done != 0;
+        obs_status[at] = (i16)pk.head.status;
         xt = xc;
         a = draw_legal(pk.head.legal.w0, pk.head.legal.w1, pk.head.legal.w2, xt);
-        actions[i] = a;
+        actions[at] = a;
         head = pk.head;
       }
     }
-    if (s > 0)  // step s - 1's observation, from the other buffer
-      store_observation<kPlayClaim>((s & 1) ? t.out : t1, base, count, features, legal,
-                        &next_item[(s - 1) & 1]);
+    if (s > 0) {  // step s - 1's observation, from the other buffer
+      const i64 rows_before = (i64)(s - 1) * step_rows;
+      store_observation<kPlayClaim>((s & 1) ? t.out : t1, base, count,
+                                    features + rows_before * kFeatureCount,
+                                    legal + rows_before * kActionCount,
+                                    &next_item[(s - 1) & 1]);
+    }
     if (tid == 0) next_item[s & 1] = 0;  // for iteration s + 1 (its last use has ended)
     __syncthreads();
   }
@@ -1036,13 +1045,16 @@ int cugo_step(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
   return launched();
 }
 
-int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
-                     uint8_t* legal, uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
-                     int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
-                     int16_t* status, uint8_t* committed, uint64_t base_seed,
-                     int64_t seed_stride, uint32_t* generation, uint8_t* spares,
-                     const uint32_t* spare_gen, int64_t spare_slots, int64_t steps,
-                     hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+// play_random and its recording form: step_rows = 0 keeps only the last step's outputs.
+int play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
+                uint8_t* legal, uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
+                int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
+                int16_t* status, uint8_t* committed, uint64_t base_seed, int64_t seed_stride,
+                uint32_t* generation, uint8_t* spares, const uint32_t* spare_gen,
+                int64_t spare_slots, int64_t steps, int64_t step_rows, hipStream_t stream) {
   if (n < 0 || seed_stride < 0 || steps < 1 || steps > kMaxPlaySteps ||
       !valid_slots(spare_slots) ||
       (n > 0 && (!states || !sampler || !features || !legal || !player || !obs_done ||
@@ -1055,8 +1067,39 @@ int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* featu
   play_kernel<<<tiles(n), kPlayThreads, 0, stream>>>(
       reinterpret_cast<u64*>(states), n, reinterpret_cast<u64*>(sampler), features, legal,
       player, obs_done, obs_status, actions, reward, done, nagari, status, committed, ar,
-      (int)steps);
+      (int)steps, step_rows);
   return launched();
+}
+}  // namespace
+
+extern "C" {
+
+int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
+                     uint8_t* legal, uint8_t* player, uint8_t* obs_done, int16_t* obs_status,
+                     int64_t* actions, float* reward, uint8_t* done, uint8_t* nagari,
+                     int16_t* status, uint8_t* committed, uint64_t base_seed,
+                     int64_t seed_stride, uint32_t* generation, uint8_t* spares,
+                     const uint32_t* spare_gen, int64_t spare_slots, int64_t steps,
+                     hipStream_t stream) {
+  return play_random(states, n, sampler, features, legal, player, obs_done, obs_status,
+                     actions, reward, done, nagari, status, committed, base_seed, seed_stride,
+                     generation, spares, spare_gen, spare_slots, steps, 0, stream);
+}
+
+int cugo_play_random_record(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
+                            uint8_t* legal, uint8_t* player, uint8_t* obs_done,
+                            int16_t* obs_status, int64_t* actions, float* reward,
+                            uint8_t* done, uint8_t* nagari, int16_t* status,
+                            uint8_t* committed, uint64_t base_seed, int64_t seed_stride,
+                            uint32_t* generation, uint8_t* spares, const uint32_t* spare_gen,
+                            int64_t spare_slots, int64_t steps, int64_t step_rows,
+                            hipStream_t stream) {
+  // Step s's legal-mask block starts at byte s * step_rows * 179, which the kernel's
+  // 32-bit mask stores need 4-byte aligned.
+  if (step_rows < n || step_rows % 4 != 0) return kBadArgument;
+  return play_random(states, n, sampler, features, legal, player, obs_done, obs_status,
+                     actions, reward, done, nagari, status, committed, base_seed, seed_stride,
+                     generation, spares, spare_gen, spare_slots, steps, step_rows, stream);
 }
 
 int cugo_branch_observe_indexed(const uint8_t* states, int64_t env_count, const int64_t* ids,

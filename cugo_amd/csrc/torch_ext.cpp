@@ -368,11 +368,11 @@ std::vector<torch::Tensor> branch_observe_indexed(torch::Tensor states, torch::T
 
 // `steps` x (observe_sample then step_reset_spares) in one launch, the last step's
 // (features, legal, player, done, status, actions, reward, step done, nagari, step status,
-// committed).
+// committed); with record=True every step's, each output [steps, n, ...].
 std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampler,
                                        int64_t base_seed, torch::Tensor generation,
                                        torch::Tensor spares, torch::Tensor spare_gen,
-                                       int64_t seed_stride, int64_t steps) {
+                                       int64_t seed_stride, int64_t steps, bool record) {
   check_states(states);
   check_states(spares);
   TORCH_CHECK(steps >= 1 && steps <= (1 << 20), "steps must lie in [1, 2^20]");
@@ -388,19 +388,39 @@ std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampl
   check_same_device(states, spares, "states", "spares");
   check_same_device(states, spare_gen, "states", "spare_gen");
   const DeviceGuard guard(states.device());
-  auto o = observation_outputs(n, states);
-  o.push_back(torch::empty({n}, on(states, at::kLong)));
-  auto st = step_outputs(n, states);
+  // Recorded: `steps` blocks of step_rows rows (n rounded up to 4: a block's mask bytes
+  // start 4-byte aligned), returned as [steps, n, ...] views.
+  const int64_t step_rows = record ? (n + 3) / 4 * 4 : 0;
+  const int64_t rows = record ? steps * step_rows : n;
+  auto o = observation_outputs(rows, states);
+  o.push_back(torch::empty({rows}, on(states, at::kLong)));
+  auto st = step_outputs(rows, states);
   o.insert(o.end(), st.begin(), st.end());
-  check_call(cugo_play_random(u8p(states), n, reinterpret_cast<uint64_t*>(sampler.data_ptr()),
-                              o[0].data_ptr<float>(), u8p(o[1]), u8p(o[2]), u8p(o[3]),
-                              o[4].data_ptr<int16_t>(), o[5].data_ptr<int64_t>(),
-                              o[6].data_ptr<float>(), u8p(o[7]), u8p(o[8]),
-                              o[9].data_ptr<int16_t>(), u8p(o[10]),
-                              static_cast<uint64_t>(base_seed), seed_stride < 0 ? n : seed_stride,
-                              reinterpret_cast<uint32_t*>(generation.data_ptr()), u8p(spares),
-                              reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), slots,
-                              steps, stream()),
+  uint64_t* smp = reinterpret_cast<uint64_t*>(sampler.data_ptr());
+  uint32_t* gen = reinterpret_cast<uint32_t*>(generation.data_ptr());
+  const uint32_t* sg = reinterpret_cast<const uint32_t*>(spare_gen.data_ptr());
+  const int64_t stride = seed_stride < 0 ? n : seed_stride;
+  if (record) {
+    check_call(cugo_play_random_record(
+                   u8p(states), n, smp, o[0].data_ptr<float>(), u8p(o[1]), u8p(o[2]),
+                   u8p(o[3]), o[4].data_ptr<int16_t>(), o[5].data_ptr<int64_t>(),
+                   o[6].data_ptr<float>(), u8p(o[7]), u8p(o[8]), o[9].data_ptr<int16_t>(),
+                   u8p(o[10]), static_cast<uint64_t>(base_seed), stride, gen, u8p(spares), sg,
+                   slots, steps, step_rows, stream()),
+               "play_random");
+    for (auto& t : o) {
+      std::vector<int64_t> shape{steps, step_rows};
+      for (int64_t d = 1; d < t.dim(); ++d) shape.push_back(t.size(d));
+      t = t.view(shape).narrow(1, 0, n);
+    }
+    return o;
+  }
+  check_call(cugo_play_random(u8p(states), n, smp, o[0].data_ptr<float>(), u8p(o[1]),
+                              u8p(o[2]), u8p(o[3]), o[4].data_ptr<int16_t>(),
+                              o[5].data_ptr<int64_t>(), o[6].data_ptr<float>(), u8p(o[7]),
+                              u8p(o[8]), o[9].data_ptr<int16_t>(), u8p(o[10]),
+                              static_cast<uint64_t>(base_seed), stride, gen, u8p(spares), sg,
+                              slots, steps, stream()),
              "play_random");
   return o;
 }
@@ -945,7 +965,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "steps x (observe_sample then step_reset_spares) in one launch; last step's outputs",
         pybind11::arg("states"), pybind11::arg("sampler"), pybind11::arg("base_seed"),
         pybind11::arg("generation"), pybind11::arg("spares"), pybind11::arg("spare_gen"),
-        pybind11::arg("seed_stride") = -1, pybind11::arg("steps") = 1);
+        pybind11::arg("seed_stride") = -1, pybind11::arg("steps") = 1,
+        pybind11::arg("record") = false);
   m.def("step_reset_spares", &step_reset_spares,
         "step, then reset_done_spares of the finished rows, in one launch",
         pybind11::arg("states"), pybind11::arg("actions"), pybind11::arg("base_seed"),

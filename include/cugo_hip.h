@@ -165,6 +165,22 @@ int cugo_play_random(uint8_t* states, int64_t n, uint64_t* sampler, float* featu
                      int64_t seed_stride, uint32_t* generation, uint8_t* spares,
                      const uint32_t* spare_gen, int64_t spare_slots, int64_t steps,
                      hipStream_t stream);
+/* cugo_play_random (the same kernel) keeping every step's outputs: step s (0 .. steps - 1)
+ * writes rows s * step_rows .. s * step_rows + n - 1 of each output, so the outputs hold
+ * `steps` blocks of step_rows rows (features [steps * step_rows, 720], and so on), and
+ * the states, generation and sampler end as cugo_play_random leaves them.  step_rows must
+ * be at least n and a multiple of 4; rows n .. step_rows - 1 of a block are not written.
+ * A test and diagnostics form of the random-policy loop (no counterpart in the reference,
+ * whose loop keeps each step's outputs by calling observe and step once per step,
+ * python/torch50_smoke.py:22-50). */
+int cugo_play_random_record(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
+                            uint8_t* legal, uint8_t* player, uint8_t* obs_done,
+                            int16_t* obs_status, int64_t* actions, float* reward,
+                            uint8_t* done, uint8_t* nagari, int16_t* status,
+                            uint8_t* committed, uint64_t base_seed, int64_t seed_stride,
+                            uint32_t* generation, uint8_t* spares, const uint32_t* spare_gen,
+                            int64_t spare_slots, int64_t steps, int64_t step_rows,
+                            hipStream_t stream);
 /* cugo_step followed by cugo_reset_done_spares(states, done, n, base_seed, seed_stride,
  * generation, sampler, NULL, spares, spare_gen, spare_slots) in one launch: the outputs are the
  * step's (done[i] = 1 for the game that just finished), and each finished row already

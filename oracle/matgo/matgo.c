@@ -137,44 +137,77 @@ static uint64_t xorshift_next(uint64_t* x) {
 
 int cugo_oracle_state_bytes(void) { return (int)sizeof(Env); }
 
+/* Threads of the batch loops below (1 by default).  Rows are independent, so a threaded
+ * loop gives the sequential loop's outputs; step_indexed with ids stays sequential, since
+ * duplicate ids step the same row in order. */
+static int g_threads = 1;
+
+void cugo_oracle_set_threads(int threads) { g_threads = threads < 1 ? 1 : threads; }
+
+typedef struct { const int64_t* seeds; const int64_t* first; uint8_t* states; } CreateCtx;
+
+static void create_one(void* ctx, int64_t i) {
+  const CreateCtx* c = (const CreateCtx*)ctx;
+  const Env e = make_env((uint64_t)c->seeds[i], (unsigned)(c->first[i] & 1));
+  store_row(&e, c->states + i * ROW);
+}
+
 void cugo_oracle_create(const int64_t* seeds, const int64_t* first, int64_t n, uint8_t* states) {
-  for (int64_t i = 0; i < n; ++i) {
-    const Env e = make_env((uint64_t)seeds[i], (unsigned)(first[i] & 1));
-    store_row(&e, states + i * ROW);
+  CreateCtx c = {seeds, first, states};
+  parallel_for(n, g_threads, create_one, &c);
+}
+
+typedef struct {
+  const uint8_t* states; const int64_t* ids; int64_t env_count;
+  float* features; uint8_t* legal; uint8_t* player; uint8_t* done; int16_t* status;
+} ObserveCtx;
+
+static void observe_one(void* ctx, int64_t i) {
+  const ObserveCtx* c = (const ObserveCtx*)ctx;
+  const int64_t id = c->ids ? c->ids[i] : i;
+  if (!valid_id(id, c->env_count)) {
+    write_invalid_observation(c->features + i * FEATURES, c->legal + i * ACTIONS, c->player + i,
+                              c->done + i, c->status + i);
+    return;
   }
+  const Env e = load_row(c->states + id * ROW);
+  write_observation(&e, c->features + i * FEATURES, c->legal + i * ACTIONS, c->player + i,
+                    c->done + i, c->status + i);
 }
 
 void cugo_oracle_observe_indexed(const uint8_t* states, const int64_t* ids, int64_t n, int64_t env_count,
                                  float* features, uint8_t* legal, uint8_t* player, uint8_t* done,
                                  int16_t* status) {
-  for (int64_t i = 0; i < n; ++i) {
-    const int64_t id = ids ? ids[i] : i;
-    if (!valid_id(id, env_count)) {
-      write_invalid_observation(features + i * FEATURES, legal + i * ACTIONS, player + i, done + i,
-                                status + i);
-      continue;
-    }
-    const Env e = load_row(states + id * ROW);
-    write_observation(&e, features + i * FEATURES, legal + i * ACTIONS, player + i, done + i, status + i);
+  ObserveCtx c = {states, ids, env_count, features, legal, player, done, status};
+  parallel_for(n, g_threads, observe_one, &c);
+}
+
+typedef struct {
+  uint8_t* states; const int64_t* ids; const int64_t* actions; int64_t env_count;
+  float* reward; uint8_t* done; uint8_t* nagari; int16_t* status; uint8_t* committed;
+  int64_t* events;
+} StepCtx;
+
+static void step_one(void* ctx, int64_t i) {
+  const StepCtx* c = (const StepCtx*)ctx;
+  const int64_t id = c->ids ? c->ids[i] : i;
+  int64_t ev[EVENT_WORDS] = {0};
+  if (!valid_id(id, c->env_count)) {
+    write_invalid_step(c->reward + i, c->done + i, c->nagari + i, c->status + i, c->committed + i);
+  } else {
+    Env e = load_row(c->states + id * ROW);
+    const StepResult r = torch_step_event(&e, clamp_action(c->actions[i]), ev);
+    store_row(&e, c->states + id * ROW);
+    write_step(&r, c->reward + i, c->done + i, c->nagari + i, c->status + i, c->committed + i);
   }
+  if (c->events) memcpy(c->events + i * EVENT_WORDS, ev, sizeof ev);
 }
 
 void cugo_oracle_step_indexed(uint8_t* states, const int64_t* ids, const int64_t* actions, int64_t n,
                               int64_t env_count, float* reward, uint8_t* done, uint8_t* nagari,
                               int16_t* status, uint8_t* committed, int64_t* events) {
-  for (int64_t i = 0; i < n; ++i) {
-    const int64_t id = ids ? ids[i] : i;
-    int64_t ev[EVENT_WORDS] = {0};
-    if (!valid_id(id, env_count)) {
-      write_invalid_step(reward + i, done + i, nagari + i, status + i, committed + i);
-    } else {
-      Env e = load_row(states + id * ROW);
-      const StepResult r = torch_step_event(&e, clamp_action(actions[i]), ev);
-      store_row(&e, states + id * ROW);
-      write_step(&r, reward + i, done + i, nagari + i, status + i, committed + i);
-    }
-    if (events) memcpy(events + i * EVENT_WORDS, ev, sizeof ev);
-  }
+  StepCtx c = {states, ids, actions, env_count, reward, done, nagari, status, committed, events};
+  parallel_for(n, ids ? 1 : g_threads, step_one, &c);
 }
 
 void cugo_oracle_start(const uint8_t* states, int64_t n, int64_t* out) {

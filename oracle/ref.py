@@ -16,6 +16,7 @@ Arrays are numpy; rows are uint8 [n, 248].
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
@@ -72,7 +73,8 @@ class RefEngine:
     oracle (this repository's plain-C restatement, oracle/matgo/); `reference=True`
     loads the reference's own build (oracle/_ref), which pins the restatement."""
 
-    def __init__(self, path: Path | str | None = None, reference: bool = False) -> None:
+    def __init__(self, path: Path | str | None = None, reference: bool = False,
+                 threads: int | None = None) -> None:
         path = Path(path) if path is not None else (REF_LIB if reference else ORACLE_LIB)
         if not path.exists():
             hint = ("`make -C oracle ref` where the reference checkout is present" if reference
@@ -80,9 +82,17 @@ class RefEngine:
             raise FileNotFoundError(f"{path} is missing: build it with {hint}")
         self.path = path
         self.kind = "reference" if reference else "oracle"
-        self.lib = _Lib(ctypes.CDLL(str(path)), "cugo_ref" if reference else "cugo_oracle")
+        cdll = ctypes.CDLL(str(path))
+        self.lib = _Lib(cdll, "cugo_ref" if reference else "cugo_oracle")
         assert self.lib.state_bytes() == STATE_BYTES
         self.record_bytes = self.lib.record_bytes()
+        # The oracle's contiguous batch loops (create, observe, step without ids) run on a
+        # thread pool; rows are independent, so the outputs are the sequential loop's.
+        setter = getattr(cdll, "cugo_oracle_set_threads", None)
+        if setter is not None:
+            setter.argtypes = [ctypes.c_int]
+            setter.restype = None
+            setter(threads if threads is not None else min(os.cpu_count() or 1, 16))
 
     # -- extension operations -------------------------------------------------------
     def create(self, seeds: np.ndarray, first: np.ndarray) -> np.ndarray:

@@ -513,6 +513,80 @@ def test_play_random_full_batch_matches_oracle(ext, ref):
     assert hgen.sum() > n // 2
 
 
+def test_play_random_bench_block_every_step_matches_oracle(ext, ref):
+    """The throughput loop exactly as bench.py runs it: 65,536 resident games, two spare
+    slots (spares [2 x 65,536, 248]), blocks of refill_spares then one play_random launch
+    of 32 steps, three blocks.  The launch keeps every step's outputs (record=True: the
+    same kernel, writing step s to its own block of rows), and each of the 96 steps'
+    observation (features as bit patterns, mask, player, done, status), action and step
+    outputs is compared with the oracle playing the same protocol, then the rows,
+    generations and samplers after each block."""
+    announce("play_random bench block (65,536 x 32 steps x 3, 2 slots) vs oracle")
+    n, k, slots = 65536, 32, 2
+    seeds, first = c1_seeds(n)
+    states = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(first).to(DEV))
+    host = ref.create(seeds, first)
+    gen = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp = ext.seed_samplers(n, SEED_BASE, gen)
+    sampler = np.array([splitmix_first(int(s) & (2**64 - 1)) for s in seeds], dtype=np.uint64)
+    spares = torch.zeros((slots * n, 248), dtype=torch.uint8, device=DEV)
+    spare_gen = torch.zeros(slots * n, dtype=torch.int32, device=DEV)
+    hgen = np.zeros(n, dtype=np.int64)
+    for block in range(3):
+        ext.refill_spares(spares, spare_gen, gen, SEED_BASE, n)
+        out = ext.play_random(states, smp, SEED_BASE, gen, spares, spare_gen, n, k, record=True)
+        assert tuple(out[0].shape) == (k, n, 720) and tuple(out[10].shape) == (k, n)
+        for step in range(k):
+            label = f"block {block}, step {step}"
+            robs = ref.observe(host)
+            assert_observe_equal([t[step] for t in out[:5]], robs, f"observation, {label}")
+            actions = sample_actions(robs[1], sampler, ~robs[3])
+            assert np.array_equal(to_np(out[5][step]), actions), f"actions, {label}"
+            rout = ref.step(host, actions)
+            assert_step_equal([t[step] for t in out[6:]], rout, label)
+            ended = np.nonzero(rout[1])[0]
+            hgen[ended] += 1
+            new_seeds = ((np.uint64(SEED_BASE) + ended.astype(np.uint64)
+                          + np.uint64(n) * hgen[ended].astype(np.uint64))).view(np.int64)
+            host[ended] = ref.create(new_seeds, ended & 1)
+            sampler[ended] = [splitmix_first(int(s) & (2**64 - 1)) for s in new_seeds]
+        del out
+        assert np.array_equal(to_np(states), host), f"rows after block {block}"
+        assert np.array_equal(to_np(gen), hgen), f"generations after block {block}"
+        assert np.array_equal(to_np(smp).view(np.uint64), sampler), f"samplers, block {block}"
+    # most rows finished at least twice, so both slots' spares and inline deals ran
+    assert (hgen >= 2).mean() > 0.5, np.bincount(hgen)
+
+
+@pytest.mark.parametrize("n", [3001 * 2 + 2, 65536])
+def test_play_random_record_matches_single_steps(ext, n):
+    """record=True changes where the outputs go, never what they are: a recorded launch
+    of K steps gives, in block s, the outputs of the s-th of K one-step launches, and the
+    same rows, generations and samplers, at a partial last tile (n not a multiple of 4
+    or 64: the blocks are padded to a multiple of 4 rows) and at the full batch."""
+    announce(f"play_random record (n={n})")
+    base = 0x5A5A5A5A
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    a = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(np.arange(n) & 1).to(DEV))
+    gen_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp_a = ext.seed_samplers(n, base, gen_a)
+    sp_a = torch.zeros((2 * n, 248), dtype=torch.uint8, device=DEV)
+    sg_a = torch.zeros(2 * n, dtype=torch.int32, device=DEV)
+    b, gen_b, smp_b, sp_b, sg_b = (t.clone() for t in (a, gen_a, smp_a, sp_a, sg_a))
+    for block, k in enumerate([5, 32, 1]):
+        ext.refill_spares(sp_a, sg_a, gen_a, base)
+        ext.refill_spares(sp_b, sg_b, gen_b, base)
+        rec = ext.play_random(b, smp_b, base, gen_b, sp_b, sg_b, steps=k, record=True)
+        for step in range(k):
+            single = ext.play_random(a, smp_a, base, gen_a, sp_a, sg_a)
+            for j, (x, y) in enumerate(zip(single, rec)):
+                assert torch.equal(x, y[step]), (block, step, j)
+        assert torch.equal(a, b) and torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), block
+    empty = ext.play_random(b[:0], smp_b[:0], base, gen_b[:0], sp_b[:0], sg_b[:0], steps=3,
+                            record=True)
+    assert tuple(empty[0].shape) == (3, 0, 720)
+
+
 def test_branch_observe_full_batch(ext, ref):
     """The branch stress at its full size: 4,096 mid-game roots x 256 children (child k of
     a root takes legal[k] while k < count, else legal[xorshift % count]) through
