@@ -10,6 +10,8 @@
 // every output byte is written once, in order.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "engine.h"
 #include "../../include/cugo_hip.h"
 
@@ -945,6 +947,22 @@ __global__ __launch_bounds__(256) void seed_kernel(i64 n, u64 base_seed, const u
   sampler[i] = sampler_seed(base_seed + (u64)i + (u64)n * gen);
 }
 
+// ------------------------------------------------------ allocation-free play ----
+// The spares of cugo_play_random_noalloc: kNoAllocSlots pre-dealt games for each of up to
+// CUGO_NOALLOC_MAX_ROWS rows (slot-major, 31 words a row), then their spare_gen words
+// (uint32, two a word).  Allocated with the code object on each device the library runs
+// on and held until the process ends (31.5 MiB).  Host code never passes `scratch` itself
+// to a kernel: it passes the device address that hipGetSymbolAddress returns for it.
+constexpr int kNoAllocSlots = 2;
+constexpr i64 kNoAllocSpareWords = (i64)kNoAllocSlots * CUGO_NOALLOC_MAX_ROWS * kRowWords;
+constexpr i64 kNoAllocGenWords = (i64)kNoAllocSlots * CUGO_NOALLOC_MAX_ROWS / 2;
+static __device__ __align__(256) u64 scratch[kNoAllocSpareWords + kNoAllocGenWords];
+
+__global__ __launch_bounds__(256) void clear_u32_kernel(u32* words, i64 n) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) words[i] = 0u;
+}
+
 }  // namespace cugo_amd
 
 // ===================================================================== C ABI ====
@@ -1283,6 +1301,69 @@ int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation
   if (n == 0) return 0;
   seed_kernel<<<blocks256(n), 256, 0, stream>>>(n, base_seed, generation, sampler);
   return launched();
+}
+
+// ---------------------------------------------------- allocation-free play ----
+}  // extern "C"
+
+namespace {
+// The device address of `scratch` on each device, looked up on the first
+// cugo_play_random_noalloc call with that device current.
+std::mutex g_scratch_lock;
+u64* g_scratch[64] = {};
+
+int scratch_on_current_device(u64** out) {
+  int dev = 0;
+  const hipError_t got = hipGetDevice(&dev);
+  if (got != hipSuccess) return (int)got;
+  if (dev < 0 || dev >= 64) return kBadArgument;
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (g_scratch[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(cugo_amd::scratch));
+    if (rc != hipSuccess) return (int)rc;
+    if (ptr == nullptr) return (int)hipErrorInvalidSymbol;
+    g_scratch[dev] = static_cast<u64*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" {
+
+int cugo_play_random_noalloc(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
+                             uint8_t* legal, uint8_t* player, uint8_t* obs_done,
+                             int16_t* obs_status, int64_t* actions, float* reward,
+                             uint8_t* done, uint8_t* nagari, int16_t* status,
+                             uint8_t* committed, uint64_t base_seed, int64_t seed_stride,
+                             uint32_t* generation, int64_t steps, hipStream_t stream) {
+  if (n > CUGO_NOALLOC_MAX_ROWS) return CUGO_ERROR_SCRATCH_LIMIT;
+  if (n < 0 || seed_stride < 0 || steps < 1 || steps > kMaxPlaySteps ||
+      (n > 0 && (!states || !sampler || !features || !legal || !player || !obs_done ||
+                 !obs_status || !actions || !reward || !done || !nagari || !status ||
+                 !committed || !generation)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  u64* base = nullptr;
+  const int rc = scratch_on_current_device(&base);
+  if (rc != 0) return rc;
+  u64* spares = base;
+  u32* spare_gen = reinterpret_cast<u32*>(base + kNoAllocSpareWords);
+  // The previous call's spares belong to other games: mark every slot stale (a fill
+  // kernel, so the sequence can be captured into a graph), then deal them all.
+  const i64 slot_rows = (i64)kNoAllocSlots * n;
+  clear_u32_kernel<<<blocks256(slot_rows), 256, 0, stream>>>(spare_gen, slot_rows);
+  const i64 per_slot = tiles(n);
+  refill_kernel<<<(unsigned)(per_slot * kNoAllocSlots), kTile, 0, stream>>>(
+      spares, spare_gen, generation, n, base_seed, (u64)seed_stride,
+      (u32)(kNoAllocSlots - 1), per_slot);
+  const int queued = launched();
+  if (queued != 0) return queued;
+  return play_random(states, n, sampler, features, legal, player, obs_done, obs_status,
+                     actions, reward, done, nagari, status, committed, base_seed, seed_stride,
+                     generation, reinterpret_cast<uint8_t*>(spares), spare_gen, kNoAllocSlots,
+                     steps, 0, stream);
 }
 
 }  // extern "C"

@@ -202,6 +202,26 @@ int cugo_redeal(uint8_t* states, const int64_t* seat, const float* keys, const i
 int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation,
                        uint64_t* sampler, hipStream_t stream);
 
+/* Allocation-free random-policy play.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It computes exactly what cugo_refill_spares (2 slots,
+ * on fresh spares) followed by cugo_play_random(..., steps) computes on the same states,
+ * sampler and generation, with the spares taken from a static device array the library
+ * holds on each device (31.5 MiB, allocated with the code object) instead of a caller's
+ * workspace.  It calls no allocator.  n may be at most CUGO_NOALLOC_MAX_ROWS; a larger n
+ * returns CUGO_ERROR_SCRATCH_LIMIT and launches nothing.  `stream` must belong to the
+ * current device.  Every call on one device shares that array (each call first marks
+ * all its spares stale, so earlier calls do not change the results): calls that overlap
+ * on one device, on different streams or from different threads, race. */
+#define CUGO_NOALLOC_MAX_ROWS 65536
+#define CUGO_ERROR_SCRATCH_LIMIT (-27)
+int cugo_play_random_noalloc(uint8_t* states, int64_t n, uint64_t* sampler, float* features,
+                             uint8_t* legal, uint8_t* player, uint8_t* obs_done,
+                             int16_t* obs_status, int64_t* actions, float* reward,
+                             uint8_t* done, uint8_t* nagari, int16_t* status,
+                             uint8_t* committed, uint64_t base_seed, int64_t seed_stride,
+                             uint32_t* generation, int64_t steps, hipStream_t stream);
+
 /*
  * Single-query decode attention over a per-row KV cache
  * (python/cugo_seq_attention50.py:43-62, the Triton `_decode_kernel` at :21-40 and its
