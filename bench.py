@@ -15,7 +15,8 @@ Also reported (not timed into `value`):
                 observe_roofline the same for the observe kernel (248 read + 3,063
                 written a row); store_ceiling what a plain fill reaches
   branch        4,096 roots (3-15 seeded random decisions deep) x 256 children:
-                branch_indexed (clone + step) and the observation of all children
+                branch_indexed (clone + step) and the observation of all children, their
+                rooflines, and the same children on the host's cores (reference build)
   decode        sequence-policy decode over a [4, 4,096, 8, 320, 32] bf16 KV cache:
                 tokens/s of the 4-layer step and the HIP decode kernel's HBM fraction
   rollout       MLP PPO self-play rollout, B = 32,768 x 128 steps: env steps/s and the
@@ -98,6 +99,8 @@ def parse() -> argparse.Namespace:
                    help="also run a plain 1 GiB device copy (calibrates HBM byte counters)")
     p.add_argument("--decode-steps", type=int, default=20)
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--branch-cpu-seconds", type=float, default=3.0,
+                   help="per branch CPU baseline (clone + step, and with observe)")
     return p.parse_args()
 
 
@@ -263,7 +266,33 @@ def mid_game_roots(ext, torch, n: int, base: int):
     return roots.index_select(0, live).contiguous(), player.long().index_select(0, live)
 
 
-def branch_workload(ext, torch, iters: int) -> dict:
+def branch_cpu_baseline(roots, parent, actions, seconds: float) -> dict:
+    """The same children on the host's cores: the reference engine's own build
+    (oracle/_ref; the oracle's C restatement where it is absent) clones each child's root
+    and steps it (branch_indexed), then also observes the child (branch + observe), one
+    child per task on a thread pool, repeated over the whole 1,048,576-child batch until
+    `seconds` have passed.  The CPU writes no child rows or observations to memory, so it
+    does less memory work per child than the GPU."""
+    from oracle.ref import REF_LIB, RefEngine
+
+    reference = REF_LIB.exists()
+    ref = RefEngine(reference=reference)
+    threads = min(os.cpu_count() or 1, 16)
+    r, ids, acts = (t.cpu().numpy() for t in (roots, parent, actions))
+    out = {"cores": threads, "kind": "reference" if reference else "port"}
+    for name, observe in (("branch", False), ("branch_observe", True)):
+        reps, dt = 0, 0.0
+        t0 = time.perf_counter()
+        while dt < seconds:
+            ref.branch_work(r, ids, acts, threads, observe)
+            reps += 1
+            dt = time.perf_counter() - t0
+        out[name] = {"value": round(reps * ids.size / dt, 1), "unit": "children/s",
+                     "sample": f"{reps} x {ids.size} children in {dt:.1f} s"}
+    return out
+
+
+def branch_workload(ext, torch, iters: int, cpu_seconds: float | None) -> dict:
     """4,096 roots from seeded random play of 3-15 decisions; child k of a root takes
     legal[k] while k < count, then legal[xorshift % count]."""
     dev = torch.device("cuda")
@@ -308,19 +337,40 @@ def branch_workload(ext, torch, iters: int) -> dict:
     torch.cuda.synchronize()
     fused_ms = ev[0].elapsed_time(ev[1]) / iters
     n = roots_n * fan
-    fused_bytes = n * (BRANCH_BYTES_PER_CHILD + OBSERVE_BYTES_PER_ROW - 248)
-    return {
+    branch_gbs = n * BRANCH_BYTES_PER_CHILD / (branch_ms * 1e-3) / 1e9
+    fused_per_child = BRANCH_BYTES_PER_CHILD + OBSERVE_BYTES_PER_ROW - 248
+    fused_gbs = n * fused_per_child / (fused_ms * 1e-3) / 1e9
+    out = {
         "children": n,
         "live_roots": int(n_live),
         "branch_ms": round(branch_ms, 4),
         "branches_per_s": n / (branch_ms * 1e-3),
-        "branch_gbs": n * BRANCH_BYTES_PER_CHILD / (branch_ms * 1e-3) / 1e9,
+        "branch_gbs": branch_gbs,
         "observe_children_ms": round(observe_ms, 4),
         "branch_observe_per_s": n / ((branch_ms + observe_ms) * 1e-3),
         "branch_observe_fused_ms": round(fused_ms, 4),
         "branch_observe_fused_per_s": n / (fused_ms * 1e-3),
-        "branch_observe_fused_gbs": fused_bytes / (fused_ms * 1e-3) / 1e9,
+        "branch_observe_fused_gbs": fused_gbs,
+        # branch_indexed: 8 (id) + 8 (action) + 248 (child) + 9 (step outputs) B a child,
+        # the parents read from L2.  branch_observe_indexed: that plus the child's
+        # observation (2,880 + 179 + 1 + 1 + 2 B) and no child read-back.
+        "roofline": {"kernel": "step_kernel<2> (branch_indexed)", "bound": "hbm",
+                     "achieved": round(branch_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(branch_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("branch_step_kernel", str(n)),
+                     "bytes_per_child": BRANCH_BYTES_PER_CHILD,
+                     "avg_launch_ms": round(branch_ms, 4)},
+        "observe_roofline": {"kernel": "branch_observe_kernel (branch_observe_indexed)",
+                             "bound": "hbm", "achieved": round(fused_gbs, 2),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(fused_gbs / HBM_PEAK_GBS, 4),
+                             "traffic": measured_traffic("branch_observe_kernel", str(n)),
+                             "bytes_per_child": fused_per_child,
+                             "avg_launch_ms": round(fused_ms, 4)},
     }
+    if cpu_seconds:
+        out["cpu_baseline"] = branch_cpu_baseline(roots, parent, actions, cpu_seconds)
+    return out
 
 
 def event_lengths(ext, torch, games: int, base_seed: int) -> "torch.Tensor":
@@ -561,110 +611,83 @@ def paired_workload(ext, torch, pairs: int = 4096) -> dict:
 
 
 def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict:
-    """MLP PPO self-play rollout: B games, a residual MLP policy (720 features -> Linear 512
-    -> 3 blocks of h + Linear(ReLU(Linear(LayerNorm(h)))) -> 179 logits and a value head,
-    bf16, N(0, 0.02) weights from seed 0), legal-masked softmax sampling (Gumbel-max), and
-    a `horizon`-step rollout buffer (bf16 features, mask, action, log-prob, value, reward,
-    done), finished games re-dealt in place.  Reports env steps/s and the engine's share of
-    the wall time (observe + step + re-deal, HIP events on the stream)."""
-    from torch import nn
+    """MLP PPO self-play rollout (cugo_amd/rollout.py): B games, a residual MLP actor
+    (720 features -> Linear 512 -> 3 blocks of h + Linear(ReLU(Linear(LayerNorm(h)))) ->
+    LayerNorm -> 179 logits and a value head; bf16, N(0, 0.02) weights from seed 0),
+    Gumbel-max sampling over the legal actions, a `horizon`-step buffer (bf16 features,
+    mask, action, log-prob, value, reward, done), finished games re-dealt from pre-dealt
+    spares inside the step.  Reports env steps/s, the engine's and the actor's shares of
+    the wall time (HIP events on the stream) and a roofline for each: the actor's
+    FLOPs over its forward time against the bf16 MFMA peak, the engine's bytes (observe
+    3,311 B a row, step with auto-reset 513 B a row) over its time against HBM."""
+    from cugo_amd.rollout import MlpRollout, ResidualMlpActor, fused_forward
 
     dev = torch.device("cuda")
     torch.manual_seed(0)
-
-    class Block(nn.Module):
-        def __init__(self, d: int) -> None:
-            super().__init__()
-            self.norm = nn.LayerNorm(d)
-            self.fc1 = nn.Linear(d, d)
-            self.fc2 = nn.Linear(d, d)
-
-        def forward(self, h):
-            return h + self.fc2(torch.relu(self.fc1(self.norm(h))))
-
-    class Actor(nn.Module):
-        def __init__(self, d: int = 512) -> None:
-            super().__init__()
-            self.inp = nn.Linear(720, d)
-            self.blocks = nn.Sequential(Block(d), Block(d), Block(d))
-            self.norm = nn.LayerNorm(d)
-            self.logits = nn.Linear(d, 179)
-            self.value = nn.Linear(d, 1)
-
-        def forward(self, f):
-            h = self.norm(self.blocks(self.inp(f)))
-            return self.logits(h), self.value(h).squeeze(-1)
-
-    actor = Actor()
+    actor = ResidualMlpActor()
     with torch.no_grad():
         for prm in actor.parameters():
             prm.normal_(0.0, 0.02)
     actor = actor.to(dev).to(torch.bfloat16).eval()
-
-    idx = torch.arange(batch, dtype=torch.int64, device=dev)
-    base = SEED_BASE + 0xC4
-    states = ext.create(idx + base, idx & 1)
-    gen = torch.zeros(batch, dtype=torch.int32, device=dev)
-    sampler = ext.seed_samplers(batch, base, gen)
-    buf = {
-        "features": torch.empty(horizon, batch, 720, dtype=torch.bfloat16, device=dev),
-        "legal": torch.empty(horizon, batch, 179, dtype=torch.bool, device=dev),
-        "action": torch.empty(horizon, batch, dtype=torch.int64, device=dev),
-        "logp": torch.empty(horizon, batch, dtype=torch.float32, device=dev),
-        "value": torch.empty(horizon, batch, dtype=torch.float32, device=dev),
-        "reward": torch.empty(horizon, batch, dtype=torch.float32, device=dev),
-        "done": torch.empty(horizon, batch, dtype=torch.bool, device=dev),
-    }
-    gumbel_gen = torch.Generator(device=dev).manual_seed(1)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    ro = MlpRollout(ext, actor, batch, horizon, SEED_BASE + 0xC4, generator=gen)
     stream = torch.cuda.current_stream()
-
-    def one_step(t: int, ev=None):
-        if ev is not None:
-            ev[0].record(stream)
-        features, legal, _, _, _ = ext.observe(states)
-        if ev is not None:
-            ev[1].record(stream)
-        f16 = features.to(torch.bfloat16)
-        logits, value = actor(f16)
-        masked = logits.float().masked_fill(~legal, float("-inf"))
-        u = torch.rand(masked.shape, generator=gumbel_gen, device=dev).clamp_(1e-20, 1.0)
-        action = (masked - torch.log(-torch.log(u))).argmax(1)
-        logp = torch.log_softmax(masked, 1).gather(1, action.unsqueeze(1)).squeeze(1)
-        if ev is not None:
-            ev[2].record(stream)
-        reward, done, _, _, _ = ext.step(states, action)
-        ext.reset_done(states, done, base, gen, sampler)
-        if ev is not None:
-            ev[3].record(stream)
-        buf["features"][t].copy_(f16)
-        buf["legal"][t].copy_(legal)
-        buf["action"][t].copy_(action)
-        buf["logp"][t].copy_(logp)
-        buf["value"][t].copy_(value.float())
-        buf["reward"][t].copy_(reward)
-        buf["done"][t].copy_(done)
-
     with torch.no_grad():
         for t in range(8):  # warm-up: GEMM handles, allocator
-            one_step(t)
+            ro.observe()
+            ro.step(t, ro.act(t))
         torch.cuda.synchronize()
-        events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(horizon)]
-        games0 = int(gen.sum(dtype=torch.int64).item())
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]
+                  for _ in range(horizon)]
+        games0 = ro.games_completed()
+        ro.steps = 0
         t0 = time.perf_counter()
         for t in range(horizon):
-            one_step(t, events[t])
+            ev = events[t]
+            ev[0].record(stream)
+            ro.observe()
+            ev[1].record(stream)
+            action = ro.act(t)
+            ev[2].record(stream)
+            ro.step(t, action)
+            ev[3].record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        games = ro.games_completed() - games0
+        # the actor's forward alone, on the last step's input: 20 back-to-back passes
+        x = ro.buffer.features[horizon - 1]
+        fused_forward(ext, actor, x)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(20):
+            fused_forward(ext, actor, x)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        forward_ms = e0.elapsed_time(e1) / 20
     engine_ms = sum(e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[3]) for e in events)
-    policy_ms = sum(e[1].elapsed_time(e[2]) for e in events)
-    flops = 2 * (720 * 512 + 6 * 512 * 512 + 512 * 179 + 512) * batch * horizon
+    actor_ms = sum(e[1].elapsed_time(e[2]) for e in events)
+    flops_row = actor.flops_per_row()
+    tflops = flops_row * batch / (forward_ms * 1e-3) / 1e12
+    engine_bytes = batch * (OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW) * horizon
+    engine_gbs = engine_bytes / (engine_ms * 1e-3) / 1e9
     return {"env_steps_per_s": round(batch * horizon / wall, 1),
+            "games_per_s": round(games / wall, 1),
             "wall_ms": round(wall * 1e3, 2),
             "engine_share": round(engine_ms / (wall * 1e3), 4),
-            "policy_share": round(policy_ms / (wall * 1e3), 4),
-            "engine_ms": round(engine_ms, 2), "policy_ms": round(policy_ms, 2),
-            "policy_tflops": round(flops / (policy_ms * 1e-3) / 1e12, 1),
-            "games_completed": int(gen.sum(dtype=torch.int64).item()) - games0,
+            "actor_share": round(actor_ms / (wall * 1e3), 4),
+            "engine_ms": round(engine_ms, 2), "actor_ms": round(actor_ms, 2),
+            "roofline": {"kernel": "actor forward (hipBLASLt GEMMs + HIP add_layernorm)",
+                         "bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
+                         "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
+                         "traffic": None, "flops_per_row": flops_row,
+                         "avg_forward_ms": round(forward_ms, 4)},
+            "engine_roofline": {"kernel": "observe + step_reset_spares (+ refill_spares)",
+                                "bound": "hbm", "achieved": round(engine_gbs, 2),
+                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(engine_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                                "bytes_per_row_step": OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW,
+                                "ms_per_step": round(engine_ms / horizon, 4)},
+            "games_completed": games,
             "batch": batch, "horizon": horizon, "dtype": "bf16"}
 
 
@@ -790,7 +813,8 @@ def main() -> None:
         "store_ceiling": ceiling,
     }
     if not args.no_branch:
-        result["branch"] = branch_workload(ext, torch, args.branch_iters)
+        result["branch"] = branch_workload(ext, torch, args.branch_iters,
+                                           None if args.no_cpu else args.branch_cpu_seconds)
     if not args.no_decode:
         result["decode"] = decode_workload(ext, torch, args.decode_steps)
     if not args.no_selfplay:

@@ -1,0 +1,178 @@
+"""MLP PPO self-play rollouts on the HIP engine.
+
+The reference's collector (python/cugo_ppo50.py:321-450, `collect`) plays each step as
+observe -> actor forward -> masked sampling -> step, records (features, legal, action,
+logp) per decision and the settled reward at the end.  This module plays the same loop
+over a resident batch of games with auto-reset, for a residual MLP actor:
+
+  * engine: `observe` (720 features + 179-way mask), then `step_reset_spares`, which steps
+    every game and gives each finished row its next game (seed base + i + B * generation,
+    first player i & 1) from a pre-dealt spare (`refill_spares` every REFILL steps; a
+    stale spare is dealt inline), so a finished game costs no separate reset launch;
+  * actor: bf16 GEMMs through PyTorch-ROCm (hipBLASLt), the bias and ReLU of each block's
+    first Linear fused into its GEMM (`torch._addmm_activation`), each residual add fused
+    with the next LayerNorm (`add_layernorm`, one HIP launch);
+  * sampling: the Gumbel-max draw over the legal actions and its log-probability in one
+    HIP launch (`gumbel_sample`), on uniforms from torch's generator (the reference draws
+    with torch as well, cugo_seq_selfplay50.py:125-130).
+
+The observation's cast to bf16 is written straight into the rollout buffer, and the actor
+reads its input from there.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+REFILL = 32  # steps between pre-deals of the next games
+SPARE_SLOTS = 2  # pre-dealt games per row
+
+
+class ResidualBlock(nn.Module):
+    """h + fc2(relu(fc1(norm(h))))."""
+
+    def __init__(self, d: int) -> None:
+        super().__init__()
+        self.norm = nn.LayerNorm(d)
+        self.fc1 = nn.Linear(d, d)
+        self.fc2 = nn.Linear(d, d)
+
+    def forward(self, h: torch.Tensor) -> torch.Tensor:
+        return h + self.fc2(torch.relu(self.fc1(self.norm(h))))
+
+
+class ResidualMlpActor(nn.Module):
+    """720 features -> Linear(720, d) -> `blocks` residual blocks -> LayerNorm -> 179
+    logits and a scalar value.  `forward` is the plain PyTorch form; `fused_forward` the
+    rollout's."""
+
+    def __init__(self, d: int = 512, blocks: int = 3, features: int = 720,
+                 actions: int = 179) -> None:
+        super().__init__()
+        self.inp = nn.Linear(features, d)
+        self.blocks = nn.ModuleList(ResidualBlock(d) for _ in range(blocks))
+        self.norm = nn.LayerNorm(d)
+        self.logits = nn.Linear(d, actions)
+        self.value = nn.Linear(d, 1)
+
+    def forward(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        h = self.inp(x)
+        for block in self.blocks:
+            h = block(h)
+        h = self.norm(h)
+        return self.logits(h), self.value(h).squeeze(-1)
+
+    def flops_per_row(self) -> int:
+        """Multiply-adds x 2 of one forward pass (the Linear layers)."""
+        return 2 * sum(m.in_features * m.out_features for m in self.modules()
+                       if isinstance(m, nn.Linear))
+
+
+def fused_forward(ext, actor: ResidualMlpActor, x: torch.Tensor):
+    """actor(x) for a bf16 actor on a contiguous bf16 [n, 720] input: the same layers,
+    with fc1's bias and ReLU in its GEMM's epilogue and every residual add fused with the
+    LayerNorm that follows it.  Returns (logits [n, 179], value [n]) in bf16."""
+    h = F.linear(x, actor.inp.weight, actor.inp.bias)
+    norms = [b.norm for b in actor.blocks] + [actor.norm]
+    _, z = ext.add_layernorm(h, None, norms[0].weight, norms[0].bias, norms[0].eps)
+    for k, block in enumerate(actor.blocks):
+        u = torch._addmm_activation(block.fc1.bias, z, block.fc1.weight.t())
+        y = torch.addmm(block.fc2.bias, u, block.fc2.weight.t())
+        nxt = norms[k + 1]
+        h, z = ext.add_layernorm(h, y, nxt.weight, nxt.bias, nxt.eps)
+    logits = F.linear(z, actor.logits.weight, actor.logits.bias)
+    value = F.linear(z, actor.value.weight, actor.value.bias).squeeze(-1)
+    return logits, value
+
+
+@dataclass
+class RolloutBuffer:
+    """`horizon` steps of B games: the actor's bf16 input, the legal mask, the sampled
+    action and its log-probability, the value estimate, and the step's reward for seat 0
+    (non-zero only when the game settles) and done flag."""
+
+    features: torch.Tensor  # bf16 [H, B, 720]
+    legal: torch.Tensor     # bool [H, B, 179]
+    action: torch.Tensor    # int64 [H, B]
+    logp: torch.Tensor      # f32 [H, B]
+    value: torch.Tensor     # f32 [H, B]
+    reward: torch.Tensor    # f32 [H, B]
+    done: torch.Tensor      # bool [H, B]
+
+    @classmethod
+    def empty(cls, horizon: int, batch: int, device) -> "RolloutBuffer":
+        def e(*shape, dtype):
+            return torch.empty((horizon, batch, *shape), dtype=dtype, device=device)
+        return cls(e(720, dtype=torch.bfloat16), e(179, dtype=torch.bool), e(dtype=torch.int64),
+                   e(dtype=torch.float32), e(dtype=torch.float32), e(dtype=torch.float32),
+                   e(dtype=torch.bool))
+
+
+class MlpRollout:
+    """B resident games played by `actor` with auto-reset.  Game j of row i is dealt
+    from seed base_seed + i + B * j with first player i & 1 (j = generation[i])."""
+
+    def __init__(self, ext, actor: ResidualMlpActor, batch: int, horizon: int,
+                 base_seed: int, generator: torch.Generator | None = None) -> None:
+        self.ext, self.actor = ext, actor
+        self.batch, self.horizon, self.base = batch, horizon, base_seed
+        dev = next(actor.parameters()).device
+        idx = torch.arange(batch, dtype=torch.int64, device=dev)
+        self.states = ext.create(idx + base_seed, idx & 1)
+        self.generation = torch.zeros(batch, dtype=torch.int32, device=dev)
+        # step_reset_spares re-seeds a finished row's sampler word; the actor does not
+        # use it.
+        self.sampler = ext.seed_samplers(batch, base_seed, self.generation)
+        self.spares = torch.empty((SPARE_SLOTS * batch, 248), dtype=torch.uint8, device=dev)
+        self.spare_gen = torch.zeros(SPARE_SLOTS * batch, dtype=torch.int32, device=dev)
+        self.buffer = RolloutBuffer.empty(horizon, batch, dev)
+        self.generator = generator
+        self.steps = 0
+        self.observation = None  # the last step's observe outputs
+        self.step_out = None     # the last step's step outputs
+
+    def observe(self):
+        if self.steps % REFILL == 0:
+            self.ext.refill_spares(self.spares, self.spare_gen, self.generation, self.base)
+        self.observation = self.ext.observe(self.states)
+        return self.observation
+
+    def act(self, t: int):
+        """The actor's action for every game of the last observation, recorded in row t
+        of the buffer."""
+        features, legal = self.observation[0], self.observation[1]
+        buf = self.buffer
+        x = buf.features[t]
+        x.copy_(features)
+        logits, value = fused_forward(self.ext, self.actor, x)
+        u = torch.rand(logits.shape, generator=self.generator, device=logits.device)
+        action, logp = self.ext.gumbel_sample(logits, legal, u)
+        buf.legal[t].copy_(legal)
+        buf.action[t].copy_(action)
+        buf.logp[t].copy_(logp)
+        buf.value[t].copy_(value)
+        return action
+
+    def step(self, t: int, action: torch.Tensor):
+        self.step_out = self.ext.step_reset_spares(
+            self.states, action, self.base, self.generation, self.sampler, self.spares,
+            self.spare_gen)
+        self.buffer.reward[t].copy_(self.step_out[0])
+        self.buffer.done[t].copy_(self.step_out[1])
+        self.steps += 1
+        return self.step_out
+
+    def collect(self) -> RolloutBuffer:
+        """`horizon` steps into the buffer (the games carry on across calls)."""
+        with torch.no_grad():
+            for t in range(self.horizon):
+                self.observe()
+                self.step(t, self.act(t))
+        return self.buffer
+
+    def games_completed(self) -> int:
+        return int(self.generation.sum(dtype=torch.int64).item())
