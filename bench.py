@@ -17,6 +17,8 @@ Also reported (not timed into `value`):
   branch        4,096 roots (3-15 seeded random decisions deep) x 256 children:
                 branch_indexed (clone + step) and the observation of all children, their
                 rooflines, and the same children on the host's cores (reference build)
+  canonical     the reference's canonical whole-game driver, 131,072 games a launch:
+                complete games/s
   decode        sequence-policy decode over a [4, 4,096, 8, 320, 32] bf16 KV cache:
                 tokens/s of the 4-layer step and the HIP decode kernel's HBM fraction
   rollout       MLP PPO self-play rollout, B = 32,768 x 128 steps: env steps/s and the
@@ -86,6 +88,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-branch", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
+    p.add_argument("--no-canonical", action="store_true")
     p.add_argument("--no-rollout", action="store_true")
     p.add_argument("--no-selfplay", action="store_true")
     p.add_argument("--no-redeal", action="store_true")
@@ -390,6 +393,36 @@ def event_lengths(ext, torch, games: int, base_seed: int) -> "torch.Tensor":
         out = ext.step_events_indexed(states, idx, actions)
         count += (out[4] & ~done).long()
     return count
+
+
+def canonical_workload(ext, torch, games: int = 131072, iters: int = 8) -> dict:
+    """The reference's canonical whole-game driver (rollout_canonical_torch50; its GPU
+    bench times 131,072 games a launch, tests/cuda_rollout50_bench.cu:22-33, 111):
+    seeds 0xBB67AE8584CAA73B + i * 0x9E3779B97F4A7C15, first = i & 1, one game per lane
+    played to the end in registers.  Complete games/s over `iters` launches (HIP events),
+    and the HBM roofline of its 56 bytes a game (seed, first, five digest words)."""
+    dev = torch.device("cuda")
+    i = torch.arange(games, dtype=torch.int64, device=dev)
+    seeds = i * -7046029254386353131 + (0xBB67AE8584CAA73B - (1 << 64))
+    first = i & 1
+    ext.rollout_canonical(seeds, first)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        digest = ext.rollout_canonical(seeds, first)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    actions = ((digest[:, 2] & 0xFFFF).sum()).item()
+    gbs = games * 56 / (ms * 1e-3) / 1e9
+    return {"games_per_s": round(games / (ms * 1e-3), 1), "launch_ms": round(ms, 4),
+            "games": games, "primary_actions_per_game": round(actions / games, 2),
+            "roofline": {"kernel": "canonical_kernel", "bound": "hbm", "achieved": round(gbs, 2),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
+                         "bytes_per_game": 56, "avg_launch_ms": round(ms, 4)}}
 
 
 def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) -> dict:
@@ -815,6 +848,8 @@ def main() -> None:
     if not args.no_branch:
         result["branch"] = branch_workload(ext, torch, args.branch_iters,
                                            None if args.no_cpu else args.branch_cpu_seconds)
+    if not args.no_canonical:
+        result["canonical"] = canonical_workload(ext, torch)
     if not args.no_decode:
         result["decode"] = decode_workload(ext, torch, args.decode_steps)
     if not args.no_selfplay:

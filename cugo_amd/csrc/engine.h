@@ -109,6 +109,7 @@ CG_HD u64 bit(u32 c) { return 1ull << (c & 63u); }
 CG_HD u64 month_cards(u32 m) { return 0xFull << ((4u * m) & 63u); }
 CG_HD u32 popc(u64 x) { return (u32)__builtin_popcountll(x); }
 CG_HD u8 first_card(u64 m) { return m ? (u8)__builtin_ctzll(m) : kNoCard; }
+CG_HD u32 ctz64(u64 x) { return (u32)__builtin_ctzll(x); }  // x != 0
 CG_HD bool is_std(u8 c) { return c < 48; }
 CG_HD bool is_bonus_card(u8 c) { return c == kBonus2 || c == kBonus3; }
 CG_HD bool is_physical(u8 c) { return c < 50; }
@@ -2396,6 +2397,112 @@ CG_HD void pack_start(const Env& e, i64* out) {
   out[6] = (i64)e.neutral;
   out[7] = (i64)e.mtype | ((i64)e.mmult << 8) | ((i64)(e.actor & 1u) << 16) |
            ((i64)e.mm0 << 24) | ((i64)e.mm1 << 32);
+}
+
+// ------------------------------------------------------- canonical driver ----
+// canonical_torch_action50 (torch50.h:542-558): the deterministic action of the
+// reference's canonical rollout, as a unified action index (kInvalidAction16 when there
+// is none).  A pending row takes its lowest legal choice card.  Otherwise the kinds are
+// taken in canonical_action50's order (rollout50.h:496-574): Chongtong win, Gukjin as
+// double pi, Go on the first decision and Stop after, then in the play phase a bomb
+// credit, the lower bonus card, the first bomb month, the first grenade month, the first
+// shake month (its lowest card in hand), the lowest standard card; primary_action_index50
+// (policy50.h:238-271) maps each to its index.  The reference also probes each play kind
+// on a copy (canonicalize_*, rollout50.h:400-489) and gives no action when a probe fails;
+// only the probe's status reaches the torch form, and in reachable states it is kOk (the
+// oracle's restatement keeps the probes and is checked against the reference build).
+CG_HD u16 canonical_action(const Env& e) {
+  if (e.done != 0) return kInvalidAction16;
+  if (e.pactive != 0) {
+    const PacketHead h = packet_head(e);
+    if (h.status != kOk) return kInvalidAction16;
+    // choice_mask: action 127 + card in bits 63 of w1 and 0..48 of w2
+    if ((h.legal.w1 >> 63) != 0) return kActChoice;
+    if (h.legal.w2 != 0) return (u16)(kActChoice + 1 + ctz64(h.legal.w2));
+    return kInvalidAction16;
+  }
+  if (terminal_finished(e)) return kInvalidAction16;
+  if (has_ct_choice(e)) return kActCtWin;
+  if (has_gukjin_decision(e)) return kActGukjinPi;
+  if (has_decision(e)) return go_of(e, e.dact) == 0 ? kActGo : kActStop;
+  if (e.phase != kPhasePlay) return kInvalidAction16;
+  if (cred_of(e, e.actor) != 0) return kActBombCredit;
+  const u64 hand = active_hand(e);
+  const u64 bonuses = hand & kBonusMask;
+  if (bonuses != 0) return (bonuses & bit(kBonus2)) != 0 ? kActBonus : (u16)(kActBonus + 1);
+  const SpecialMonths sm = special_months(e);
+  if (sm.bombs != 0) return (u16)(kActBomb + ctz64(sm.bombs));
+  if (sm.grenades != 0) return (u16)(kActGrenade + ctz64(sm.grenades));
+  if (sm.shakes != 0) {
+    const u32 month = ctz64(sm.shakes);
+    const u64 cards = hand & kStdMask & (0xFull << (4 * month));
+    return cards != 0 ? (u16)(kActShake + ctz64(cards)) : kInvalidAction16;
+  }
+  const u64 standard = hand & kStdMask;
+  if (standard != 0) return (u16)ctz64(standard);
+  return kInvalidAction16;
+}
+
+// RolloutEnd50 (rollout50.h:70-76)
+enum : u8 { kEndTerminal = 0, kEndNagari = 1, kEndStalled = 2, kEndActionError = 3,
+            kEndMaxActions = 4 };
+
+// finish_torch_rollout50 (torch50.h:560-596) with finish_terminal_rollout50
+// (rollout50.h:584-614), packed into five words:
+//   0 final_points   1 reward0
+//   2 actions | turns << 16 | bonus_actions << 32 | special_actions << 48
+//   3 go_actions | end << 16 | action_status << 24 | terminal_reason << 32 | winner << 40
+//     | next_round_multiplier << 48
+//   4 choice_actions | resolve_choices << 16 | pi_choices << 32
+CG_HD void canonical_digest(const Env& e, u8 fallback_end, i64* out) {
+  u64 points = 0;
+  i64 reward = 0;
+  u8 end = fallback_end, status = e.status, reason = kReasonNone, winner = kNoPlayer, mult = 1;
+  if (terminal_finished(e)) {
+    const Settlement st = settle(e);
+    reason = e.treason;
+    if (!st.ok) {
+      end = kEndActionError;
+      status = kInvalidAction;
+      winner = e.twinner;
+    } else {
+      end = kEndTerminal;
+      status = kOk;
+      winner = st.winner;
+      points = st.final_points;
+      reward = settlement_reward0(st);
+    }
+  } else if (e.nagari != 0) {
+    end = kEndNagari;
+    status = kOk;
+    mult = 2;
+    reward = e.side0;  // nagari_reward50 (settlement50.h:220-225)
+  }
+  out[0] = (i64)points;
+  out[1] = reward;
+  out[2] = (i64)((u64)e.n_primary | (u64)e.turn << 16 | (u64)e.n_bonus << 32 |
+                 (u64)e.n_special << 48);
+  out[3] = (i64)((u64)e.n_go | (u64)end << 16 | (u64)status << 24 | (u64)reason << 32 |
+                 (u64)winner << 40 | (u64)mult << 48);
+  out[4] = (i64)((u64)e.n_choice | (u64)e.n_resolve << 16 | (u64)e.n_pi << 32);
+}
+
+// rollout_canonical_torch50 (torch50.h:598-619) on a dealt game, in place.
+CG_HD void rollout_canonical(Env& e, u32 max_actions, i64* out) {
+  while (e.done == 0 && e.n_primary < max_actions) {
+    const u16 action = canonical_action(e);
+    if (action == kInvalidAction16) {
+      e.status = kInvalidAction;
+      canonical_digest(e, kEndStalled, out);
+      return;
+    }
+    const StepOut so = torch_step(e, action);
+    if (so.status != kOk) {
+      canonical_digest(e, kEndActionError, out);
+      return;
+    }
+  }
+  canonical_digest(e, e.done != 0 ? kEndTerminal : kEndMaxActions, out);
 }
 
 // stock_indexed (torch50_ext.cu:336-363): next 8 draws, stopping at the first

@@ -939,6 +939,29 @@ __global__ __launch_bounds__(256) void redeal_kernel(u64* states, const i64* sea
   w[kWordRng] = (u64)rng[r];
 }
 
+// ------------------------------------------------------- canonical rollout ----
+// rollout_canonical_torch50 (torch50.h:598-619): each lane deals game i from seeds[i] /
+// first[i] and plays it to the end with the canonical action in registers, then writes
+// its five digest words; a tile's 64 x 5 words leave through LDS as one contiguous block.
+// The whole game is integer work with 56 bytes of HBM traffic, so the kernel is bound by
+// instruction issue; one wave per workgroup lets a wave whose games end early retire.
+constexpr int kCanonicalWords = 5;
+
+__global__ __launch_bounds__(kTile) void canonical_kernel(const i64* seeds, const i64* first,
+                                                          i64 n, u32 max_actions, i64* out) {
+  __shared__ i64 digest[kTile * kCanonicalWords];
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int lane = threadIdx.x;
+  if (lane < count) {
+    Env e = create_env((u64)seeds[base + lane], (u32)(first[base + lane] & 1));
+    rollout_canonical(e, max_actions, digest + lane * kCanonicalWords);
+  }
+  __syncthreads();
+  i64* dst = out + base * kCanonicalWords;
+  for (int j = lane; j < count * kCanonicalWords; j += kTile) dst[j] = digest[j];
+}
+
 __global__ __launch_bounds__(256) void seed_kernel(i64 n, u64 base_seed, const u32* generation,
                                                    u64* sampler) {
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1364,6 +1387,17 @@ int cugo_play_random_noalloc(uint8_t* states, int64_t n, uint64_t* sampler, floa
                      actions, reward, done, nagari, status, committed, base_seed, seed_stride,
                      generation, reinterpret_cast<uint8_t*>(spares), spare_gen, kNoAllocSlots,
                      steps, 0, stream);
+}
+
+int cugo_rollout_canonical(const int64_t* seeds, const int64_t* first_players, int64_t n,
+                           int64_t max_actions, int64_t* digest, hipStream_t stream) {
+  if (n < 0 || max_actions < 0 || max_actions > 0xFFFF ||
+      (n > 0 && (!seeds || !first_players || !digest)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  canonical_kernel<<<tiles(n), kTile, 0, stream>>>(seeds, first_players, n, (u32)max_actions,
+                                                   digest);
+  return launched();
 }
 
 }  // extern "C"

@@ -366,6 +366,23 @@ std::vector<torch::Tensor> branch_observe_indexed(torch::Tensor states, torch::T
   return out;
 }
 
+// rollout_canonical(seeds, first_players, max_actions=128) -> int64 [N, 5] digest words of
+// the canonical whole-game driver (torch50.h:598-619).
+torch::Tensor rollout_canonical(torch::Tensor seeds, torch::Tensor first, int64_t max_actions) {
+  check_1d(seeds, at::kLong, "seeds");
+  check_1d(first, at::kLong, "first_players");
+  TORCH_CHECK(seeds.numel() == first.numel(), "seeds and first_players must have the same length");
+  check_same_device(seeds, first, "seeds", "first_players");
+  TORCH_CHECK(max_actions >= 0 && max_actions <= 0xFFFF, "max_actions must lie in [0, 65535]");
+  const DeviceGuard guard(seeds.device());
+  const int64_t n = seeds.numel();
+  auto out = torch::empty({n, 5}, on(seeds, at::kLong));
+  check_call(cugo_rollout_canonical(seeds.data_ptr<int64_t>(), first.data_ptr<int64_t>(), n,
+                                    max_actions, out.data_ptr<int64_t>(), stream()),
+             "rollout_canonical");
+  return out;
+}
+
 // `steps` x (observe_sample then step_reset_spares) in one launch, the last step's
 // (features, legal, player, done, status, actions, reward, step done, nagari, step status,
 // committed); with record=True every step's, each output [steps, n, ...].
@@ -967,6 +984,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("generation"), pybind11::arg("spares"), pybind11::arg("spare_gen"),
         pybind11::arg("seed_stride") = -1, pybind11::arg("steps") = 1,
         pybind11::arg("record") = false);
+  m.def("rollout_canonical", &rollout_canonical,
+        "Canonical whole-game rollouts (rollout_canonical_torch50): [N, 5] digest words",
+        pybind11::arg("seeds"), pybind11::arg("first_players"),
+        pybind11::arg("max_actions") = 128);
   m.def("step_reset_spares", &step_reset_spares,
         "step, then reset_done_spares of the finished rows, in one launch",
         pybind11::arg("states"), pybind11::arg("actions"), pybind11::arg("base_seed"),

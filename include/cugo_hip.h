@@ -202,6 +202,23 @@ int cugo_redeal(uint8_t* states, const int64_t* seat, const float* keys, const i
 int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation,
                        uint64_t* sampler, hipStream_t stream);
 
+/* The reference's canonical rollout driver (rollout_canonical_torch50, torch50.h:598-619,
+ * over canonical_torch_action50, torch50.h:542-558, and canonical_action50,
+ * rollout50.h:496-574; the digest of rollout_digest50, rollout50.h:706-719, plus
+ * TorchRollout50's choice counters): game i is dealt from seeds[i] / first_players[i]
+ * and played with the deterministic canonical action until it ends or has taken
+ * max_actions (0 .. 65535) primary actions.  digest int64 [n, 5]:
+ *   0 final_points   1 reward0 (seat 0)
+ *   2 actions | turns << 16 | bonus_actions << 32 | special_actions << 48
+ *   3 go_actions | end << 16 | action_status << 24 | terminal_reason << 32 | winner << 40
+ *     | next_round_multiplier << 48    (end: RolloutEnd50, rollout50.h:70-76)
+ *   4 choice_actions | resolve_choices << 16 | pi_choices << 32
+ * The reference runs it on the CPU (torch50_test.cpp:160-191) and times its explicit
+ * form on the GPU (tests/cuda_rollout50_bench.cu:22-33), whose digest words 0-3 equal
+ * these. */
+int cugo_rollout_canonical(const int64_t* seeds, const int64_t* first_players, int64_t n,
+                           int64_t max_actions, int64_t* digest, hipStream_t stream);
+
 /* Allocation-free random-policy play.  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It computes exactly what cugo_refill_spares (2 slots,

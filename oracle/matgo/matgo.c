@@ -20,7 +20,7 @@
 #include <stdint.h>
 #include <string.h>
 
-#include "torch.h"
+#include "canonical.h"
 
 #define ROW 248
 
@@ -419,4 +419,71 @@ void cugo_oracle_settle(const uint8_t* row, int64_t* out) {
   out[1] = st.winner;
   out[2] = (int64_t)st.final_points;
   out[3] = st.side0;
+}
+
+/* rollout_canonical_torch50 (torch50.h:598-619) from seeds[i] / first[i] with at most
+ * max_actions primary actions: five digest words a game (pack_canonical). */
+typedef struct { const int64_t* seeds; const int64_t* first; int max_actions; int64_t* out; } CanonCtx;
+
+static void canonical_one(void* arg, int64_t i) {
+  const CanonCtx* c = (const CanonCtx*)arg;
+  const CanonicalResult r = rollout_canonical_torch((uint64_t)c->seeds[i], (unsigned)(c->first[i] & 1),
+                                                    (uint16_t)c->max_actions);
+  pack_canonical(&r, c->out + 5 * i);
+}
+
+void cugo_oracle_rollout_canonical(const int64_t* seeds, const int64_t* first, int64_t n, int max_actions,
+                                   int threads, int explicit_form, int64_t* out) {
+  (void)explicit_form; /* the oracle restates the torch form only */
+  CanonCtx c = {seeds, first, max_actions, out};
+  parallel_for(n, threads, canonical_one, &c);
+}
+
+/* For the canonical driver's probes: over n games from seed base + i * 0x9E3779B97F4A7C15
+ * (first = i & 1) played with the canonical action (random_policy = 0) or a uniform
+ * random legal action (xorshift64 from SplitMix64(i), random_policy = 1), counts the
+ * decision states outside a pending choice (out[0]) and those where canonical_action50's
+ * probe status is not kOk (out[1]).  random_policy = 2 plays the canonical action but
+ * probes a copy of each state whose stock is emptied (a planted failure for the tests). */
+typedef struct { uint64_t base; int random_policy; _Atomic int64_t states, failures; } ProbeCtx;
+
+static void probe_one(void* arg, int64_t i) {
+  ProbeCtx* c = (ProbeCtx*)arg;
+  Env e = make_env(c->base + (uint64_t)i * 0x9E3779B97F4A7C15ull, (unsigned)(i & 1));
+  uint64_t x = splitmix_first((uint64_t)i);
+  int64_t states = 0, failures = 0;
+  while (!e.done && e.n_primary < 128) {
+    if (!e.pending.active) {
+      ++states;
+      Terminal probed = e.g;
+      if (c->random_policy == 2) probed.sp.game.turn.stock = 0; /* planted: nothing to draw */
+      if (canonical_action(&probed).status != AS_OK) ++failures;
+    }
+    uint16_t a = INVALID_TORCH_ACTION;
+    if (c->random_policy != 1) {
+      a = canonical_torch_action(&e);
+    } else {
+      const Packet p = make_packet(&e);
+      uint16_t list[ACTIONS];
+      int count = 0;
+      for (unsigned k = 0; k < ACTIONS; ++k)
+        if (tm_has(p.legal, k)) list[count++] = (uint16_t)k;
+      if (count) a = list[xorshift_next(&x) % (uint64_t)count];
+    }
+    if (a == INVALID_TORCH_ACTION || torch_step(&e, a).status != AS_OK) break;
+  }
+  atomic_fetch_add(&c->states, states);
+  atomic_fetch_add(&c->failures, failures);
+}
+
+void cugo_oracle_canonical_probe_failures(uint64_t base, int64_t n, int random_policy, int threads,
+                                          int64_t* out) {
+  ProbeCtx c;
+  c.base = base;
+  c.random_policy = random_policy;
+  atomic_init(&c.states, 0);
+  atomic_init(&c.failures, 0);
+  parallel_for(n, threads, probe_one, &c);
+  out[0] = atomic_load(&c.states);
+  out[1] = atomic_load(&c.failures);
 }

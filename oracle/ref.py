@@ -58,6 +58,8 @@ class _Lib:
         "play_random": ([ctypes.c_uint64, _I64, ctypes.c_int, _P, _P, _P, _P, _I64,
                          ctypes.c_int32], ctypes.c_int64),
         "branch_work": ([_P, _P, _P, _I64, ctypes.c_int, ctypes.c_int], ctypes.c_uint64),
+        "rollout_canonical": ([_P, _P, _I64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P],
+                              None),
     }
 
     def __init__(self, lib: ctypes.CDLL, prefix: str) -> None:
@@ -209,6 +211,40 @@ class RefEngine:
         actions = np.ascontiguousarray(actions, dtype=np.int64)
         return int(self.lib.branch_work(_ptr(roots), _ptr(ids), _ptr(actions), ids.size,
                                                  threads, int(observe)))
+
+
+    def rollout_canonical(self, seeds: np.ndarray, first: np.ndarray, max_actions: int = 128,
+                          threads: int | None = None, explicit: bool = False) -> np.ndarray:
+        """The canonical whole-game driver (rollout_canonical_torch50, torch50.h:598-619;
+        explicit=True on the reference build: rollout_canonical50, rollout50.h:616-703)
+        from seeds[i] / first[i]: int64 [n, 5] digest words (CANONICAL_FIELDS)."""
+        seeds = np.ascontiguousarray(seeds, dtype=np.int64)
+        first = np.ascontiguousarray(first, dtype=np.int64)
+        out = np.zeros((seeds.size, 5), dtype=np.int64)
+        threads = threads if threads is not None else min(os.cpu_count() or 1, 16)
+        self.lib.rollout_canonical(_ptr(seeds), _ptr(first), seeds.size, max_actions, threads,
+                                   int(explicit), _ptr(out))
+        return out
+
+
+# Digest words of a canonical rollout: (word, shift, bits) of each field.
+CANONICAL_FIELDS = {
+    "final_points": (0, 0, 64), "reward0": (1, 0, 64),
+    "actions": (2, 0, 16), "turns": (2, 16, 16), "bonus_actions": (2, 32, 16),
+    "special_actions": (2, 48, 16), "go_actions": (3, 0, 16), "end": (3, 16, 8),
+    "action_status": (3, 24, 8), "terminal_reason": (3, 32, 8), "winner": (3, 40, 8),
+    "next_round_multiplier": (3, 48, 8), "choice_actions": (4, 0, 16),
+    "resolve_choices": (4, 16, 16), "pi_choices": (4, 32, 16),
+}
+
+
+def canonical_field(words: np.ndarray, name: str) -> np.ndarray:
+    """One field of int64 [n, 5] canonical digest words."""
+    w, shift, bits = CANONICAL_FIELDS[name]
+    col = words[:, w]
+    if bits == 64:
+        return col
+    return ((col.view(np.uint64) >> np.uint64(shift)) & np.uint64((1 << bits) - 1)).astype(np.int64)
 
 
 # -- the C1 random-policy protocol, in numpy (shared by tests and the bench) ----------

@@ -355,4 +355,41 @@ std::uint64_t cugo_ref_branch_work(const std::uint8_t* roots, const std::int64_t
   return sum.load();
 }
 
+// The reference's canonical rollouts (include/cugo/game/torch50.h:598-619, the torch
+// form, and rollout50.h:616-703, the explicit form its GPU bench times) from
+// seed[i] / first[i] with at most max_actions primary actions; five digest words a game
+// (packing in oracle/matgo/canonical.h).  The explicit form has no choice counters: its
+// word 4 is zero.
+void pack_rollout(const cg::RolloutResult50& r, std::uint16_t choice, std::uint16_t resolve,
+                  std::uint16_t pi, std::int64_t* out) {
+  out[0] = static_cast<std::int64_t>(r.final_points);
+  out[1] = r.reward0;
+  out[2] = static_cast<std::int64_t>(
+      std::uint64_t{r.actions} | std::uint64_t{r.turns} << 16 |
+      std::uint64_t{r.bonus_actions} << 32 | std::uint64_t{r.special_actions} << 48);
+  out[3] = static_cast<std::int64_t>(
+      std::uint64_t{r.go_actions} | std::uint64_t{static_cast<std::uint8_t>(r.end)} << 16 |
+      std::uint64_t{static_cast<std::uint8_t>(r.action_status)} << 24 |
+      std::uint64_t{static_cast<std::uint8_t>(r.terminal_reason)} << 32 |
+      std::uint64_t{r.winner} << 40 | std::uint64_t{r.next_round_multiplier} << 48);
+  out[4] = static_cast<std::int64_t>(std::uint64_t{choice} | std::uint64_t{resolve} << 16 |
+                                     std::uint64_t{pi} << 32);
+}
+
+void cugo_ref_rollout_canonical(const std::int64_t* seeds, const std::int64_t* first,
+                                std::int64_t n, int max_actions, int threads, int explicit_form,
+                                std::int64_t* out) {
+  parallel_for(n, threads, [&](std::int64_t i) {
+    const auto seed = static_cast<std::uint64_t>(seeds[i]);
+    const auto f = static_cast<std::uint8_t>(first[i] & 1);
+    const auto cap = static_cast<std::uint16_t>(max_actions);
+    if (explicit_form) {
+      pack_rollout(cg::rollout_canonical50(seed, f, cap), 0, 0, 0, out + 5 * i);
+    } else {
+      const cg::TorchRollout50 r = cg::rollout_canonical_torch50(seed, f, cap);
+      pack_rollout(r.result, r.choice_actions, r.resolve_choices, r.pi_choices, out + 5 * i);
+    }
+  });
+}
+
 }  // extern "C"

@@ -14,6 +14,9 @@ outputs as .npz data:
   rows.npz              created rows and start records of games 0..255; mid-game rows
                         (incl. pending floor choices) with their observations, hands,
                         stock peeks and the step results of a fixed action list.
+  canonical.npz         digests of the canonical whole-game driver (see canonical()).
+
+    python tests/golden/make_golden.py canonical     (one fixture only)
 """
 
 from __future__ import annotations
@@ -80,10 +83,37 @@ def rows(ref: RefEngine) -> None:
     print(f"rows: created={n} mid={mid.shape[0]} pending={pending} done={int(obs[3].sum())}")
 
 
+GOLDEN_GAMMA = 0x9E3779B97F4A7C15
+
+
+def canonical(ref: RefEngine) -> None:
+    """Canonical-driver digests (rollout_canonical_torch50, five words a game): the
+    8,192 seeds of the reference's rollout-equivalence test (torch50_test.cpp:160-191),
+    4,096 seeds of its GPU bench (cuda_rollout50_bench.cu:22-33, warm-up base), and 512
+    of those games cut at 5 primary actions (the max-actions ending)."""
+    def seeds_of(base: int, n: int) -> np.ndarray:
+        i = np.arange(n, dtype=np.uint64)
+        return (np.uint64(base) + i * np.uint64(GOLDEN_GAMMA)).view(np.int64)
+
+    test_seeds = seeds_of(0x1F83D9ABFB41BD6B, 8192)
+    bench_seeds = seeds_of(0x6A09E667F3BCC909, 4096)
+    test_first = np.arange(8192, dtype=np.int64) & 1
+    bench_first = np.arange(4096, dtype=np.int64) & 1
+    np.savez_compressed(
+        HERE / "canonical.npz", test_seeds=test_seeds, test_first=test_first,
+        test_digest=ref.rollout_canonical(test_seeds, test_first),
+        bench_seeds=bench_seeds, bench_first=bench_first,
+        bench_digest=ref.rollout_canonical(bench_seeds, bench_first),
+        bench_explicit=ref.rollout_canonical(bench_seeds, bench_first, explicit=True),
+        cut_digest=ref.rollout_canonical(bench_seeds[:512], bench_first[:512], max_actions=5))
+    print("canonical: 8,192 + 4,096 + 512 digests")
+
+
 def main() -> None:
     ref = RefEngine(reference=True)
-    c1(ref)
-    rows(ref)
+    what = sys.argv[1:] or ["c1", "rows", "canonical"]
+    for name in what:
+        {"c1": c1, "rows": rows, "canonical": canonical}[name](ref)
 
 
 if __name__ == "__main__":
