@@ -164,232 +164,260 @@ def policy_cache(policy: SeqPolicy, rows: int, device, slots: int = MAX_EVENTS +
     return KVCache(layers, rows, heads, d, slots, torch.device(device))
 
 
+DONE_BYTE = 239  # TorchEnv50::done (torch50.h:108-121)
+RECORD_LONG = ("actions", "opp_hand", "stock", "stop_points", "seat", "count")
+
+
+class _WaveTensors:
+    """Every device tensor of one wave of `w` games, made from one table of names, shapes
+    and dtypes; `per_wave` lists those a new wave starts from zero."""
+
+    def __init__(self, w: int, steps: int, width: int, device) -> None:
+        i64, b, f32 = torch.int64, torch.bool, torch.float32
+        table = {
+            "events": ((w, MAX_EVENTS, EVENT_WORDS), i64), "count": ((w,), i64),
+            "start": ((w, START_WORDS), i64), "learner_seat": ((w,), i64),
+            "rec_features": ((steps, w, width), torch.bfloat16),
+            "rec_legal": ((steps, w, ACTIONS), b), "rec_logp": ((steps, w), f32),
+            "rec_valid": ((steps, w), b), "step_index": ((1,), i64),
+            "final_reward0": ((w,), f32), "final_nagari": ((w,), b), "finished": ((w,), b),
+            "started": ((w,), b), "bad": ((), i64),
+        }
+        for name, (shape, dtype) in table.items():
+            setattr(self, name, torch.zeros(shape, dtype=dtype, device=device))
+        self.rec_long = {k: torch.zeros((steps, w), dtype=i64, device=device) for k in RECORD_LONG}
+        self.per_wave = [self.events, self.count, self.rec_valid, self.step_index,
+                         self.final_reward0, self.final_nagari, self.bad]
+
+
 class SelfPlayWave:
-    """Self-play of `wave` games at a time, one HIP graph per decision step
-    (WaveCollector, cugo_seq_selfplay50.py:36-238).  With an opponent and pool_games > 0,
-    games 0 .. pool_games - 1 of a wave played with `pool=True` put the frozen opponent on
-    the seat the learner does not hold."""
+    """Self-play of `wave` games at a time on the HIP engine, one HIP graph replay per
+    decision step.  Plays what the reference's WaveCollector plays
+    (cugo_seq_selfplay50.py:36-238) and leaves the same tensors behind (events, count,
+    start, rec_*, final_reward0, final_nagari, finished, started, bad).  With an opponent
+    and pool_games > 0, a wave started with pool=True seats the frozen opponent opposite
+    the learner in its first pool_games games.
+
+    KV cache rows: the learner's policy keeps one row per seat and game, row
+    seat * wave + game (the query goes to the mover's row, event tokens to both); the
+    opponent keeps one row per pool game, for its own seat."""
 
     def __init__(self, ext, actor: SeqPolicy, wave: int, max_steps: int = 64,
                  opponent: SeqPolicy | None = None, pool_games: int = 0) -> None:
-        device = next(actor.parameters()).device
         if not 0 <= pool_games <= wave:
-            raise ValueError(f"pool_games ({pool_games}) must lie in [0, {wave}]")
+            raise ValueError(f"pool_games must be between 0 and the wave size {wave}, "
+                             f"got {pool_games}")
         if opponent is not None and opponent.kept_columns() != actor.kept_columns():
-            # both read the one query input the step builds from the kept columns
-            raise ValueError("the opponent's query mode must be the actor's")
-        self.ext, self.actor, self.w, self.max_steps = ext, actor, wave, max_steps
-        self.opponent, self.p = opponent, (pool_games if opponent is not None else 0)
-        w = wave
-        self.ids = torch.arange(w, device=device)
-        self.seats2 = torch.cat((torch.zeros(w, dtype=torch.int64, device=device),
-                                 torch.ones(w, dtype=torch.int64, device=device)))
-        seeds, first = make_seeds(w, 0, device)
-        self.states = ext.create(seeds, first)
-        self.events = torch.zeros((w, MAX_EVENTS, EVENT_WORDS), dtype=torch.int64, device=device)
-        self.count = torch.zeros(w, dtype=torch.int64, device=device)
-        self.start = torch.zeros((w, START_WORDS), dtype=torch.int64, device=device)
-        self.learner_seat = torch.zeros(w, dtype=torch.int64, device=device)
-        self.cache = policy_cache(actor, 2 * w, device)  # row = seat * w + game
-        # row = pool game (the opponent's seat)
-        self.opp_cache = (policy_cache(opponent, max(1, self.p), device)
-                          if opponent is not None else None)
+            raise ValueError("actor and opponent read different query columns")
+        dev = next(actor.parameters()).device
         cols = actor.kept_columns()
-        self.columns = (None if cols is None
-                        else torch.tensor(cols, dtype=torch.int32, device=device))
-        width = FEATURES if cols is None else len(cols)
-        s = max_steps
-        self.rec_features = torch.zeros((s, w, width), dtype=torch.bfloat16, device=device)
-        self.rec_legal = torch.zeros((s, w, ACTIONS), dtype=torch.bool, device=device)
-        self.rec_logp = torch.zeros((s, w), dtype=torch.float32, device=device)
-        self.rec_long = {name: torch.zeros((s, w), dtype=torch.int64, device=device)
-                         for name in ("actions", "opp_hand", "stock", "stop_points", "seat",
-                                      "count")}
-        self.rec_valid = torch.zeros((s, w), dtype=torch.bool, device=device)
-        self.step_index = torch.zeros(1, dtype=torch.int64, device=device)
-        self.final_reward0 = torch.zeros(w, device=device)
-        self.final_nagari = torch.zeros(w, dtype=torch.bool, device=device)
-        self.finished = torch.zeros(w, dtype=torch.bool, device=device)
-        self.started = torch.zeros(w, dtype=torch.bool, device=device)
-        self.bad = torch.zeros((), dtype=torch.int64, device=device)
-        self.ok = int(ext.STATUS_OK)
-        def native(pool_games: int):
-            return ext.SelfPlayState(
-                w, s, self.step_index, self.count, self.events, self.cache.length,
-                self.final_reward0, self.final_nagari, self.finished, self.bad,
-                self.rec_features, self.rec_legal, self.rec_logp, self.rec_long["actions"],
-                self.rec_long["opp_hand"], self.rec_long["stock"], self.rec_long["stop_points"],
-                self.rec_long["seat"], self.rec_long["count"], self.rec_valid, self.columns,
-                pool_games, self.learner_seat,
-                None if self.opp_cache is None else self.opp_cache.length)
-        self.native = {False: native(0)}
-        if self.p > 0:
-            self.native[True] = native(self.p)
-        # Sampling noise: None draws torch.rand_like inside the step (the reference's
-        # choice); a tensor [wave, ACTIONS] is read instead (set by a caller that draws
-        # its own uniforms before each step).
+        self.ext, self.actor, self.opponent = ext, actor, opponent
+        self.w, self.max_steps = wave, max_steps
+        self.p = pool_games if opponent is not None else 0
+        self.t = _WaveTensors(wave, max_steps, FEATURES if cols is None else len(cols), dev)
+        self.ids = torch.arange(wave, device=dev)
+        self.seats2 = torch.arange(2 * wave, device=dev) // wave  # seat of each cache row
+        self.states = ext.create(*make_seeds(wave, 0, dev))
+        self.cache = policy_cache(actor, 2 * wave, dev)
+        self.opp_cache = None if opponent is None else policy_cache(opponent, max(1, self.p), dev)
+        self.columns = None if cols is None else torch.tensor(cols, dtype=torch.int32, device=dev)
+        self.native = {pool: self._native(pool) for pool in ((False, True) if self.p else (False,))}
+        # Gumbel noise: None draws torch.rand inside each step; a [wave, 179] float32
+        # tensor is read instead (its caller refills it between replays).
         self.noise: torch.Tensor | None = None
-        self.graph: torch.cuda.CUDAGraph | None = None
+        self.logits: torch.Tensor | None = None  # the last step's logits
+        self.graph: torch.cuda.CUDAGraph | None = None  # one step, for `pool` below
         self.graph_pool: bool | None = None
-        self.logits: torch.Tensor | None = None
+        self._done_flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
+
+    # the reference's tensor names, for callers of the wave's outcome
+    def __getattr__(self, name: str):
+        t = self.__dict__.get("t")
+        if t is not None and hasattr(t, name):
+            return getattr(t, name)
+        raise AttributeError(name)
+
+    def _native(self, pool: bool):
+        """The prepare/advance kernels' view of this wave's tensors."""
+        t, rl = self.t, self.t.rec_long
+        return self.ext.SelfPlayState(
+            self.w, self.max_steps, t.step_index, t.count, t.events, self.cache.length,
+            t.final_reward0, t.final_nagari, t.finished, t.bad, t.rec_features, t.rec_legal,
+            t.rec_logp, rl["actions"], rl["opp_hand"], rl["stock"], rl["stop_points"],
+            rl["seat"], rl["count"], t.rec_valid, self.columns, self.p if pool else 0,
+            t.learner_seat, None if self.opp_cache is None else self.opp_cache.length)
+
+    @staticmethod
+    def _open(policy: SeqPolicy, cache: KVCache, start: torch.Tensor, seat: torch.Tensor) -> None:
+        """Every row's opening token into slot 0 of `cache`."""
+        cache.length.zero_()
+        policy.cached_step(cache, policy.start_token(start, seat), 1)
+        cache.length.fill_(1)
 
     @torch.no_grad()
     def reset(self, seeds: torch.Tensor, first: torch.Tensor, learner_seat: torch.Tensor,
               pool: bool = False) -> None:
-        """cugo_seq_selfplay50.py:78-106."""
+        """Deals a new wave (the reference's _reset, cugo_seq_selfplay50.py:78-106)."""
+        t = self.t
         self.states.copy_(self.ext.create(seeds, first))
-        self.start.copy_(self.ext.start(self.states))
-        self.events.zero_()
-        self.count.zero_()
-        self.learner_seat.copy_(learner_seat)
-        done = self.ext.observe_indexed(self.states, self.ids)[3]
-        self.started.copy_(~done)
-        self.finished.copy_(done)
-        self.final_reward0.zero_()
-        self.final_nagari.zero_()
-        self.bad.zero_()
-        self.step_index.zero_()
-        self.rec_valid.zero_()
-        self.cache.length.zero_()
-        actor = self.actor
-        actor.cached_step(self.cache, actor.start_token(self.start.repeat(2, 1), self.seats2), 1)
-        self.cache.length.fill_(1)
-        if pool and self.p > 0:
-            p, opp = self.p, self.opponent
-            self.opp_cache.length.zero_()
-            opp.cached_step(self.opp_cache, opp.start_token(self.start[:p], 1 - self.learner_seat[:p]), 1)
-            self.opp_cache.length.fill_(1)
+        t.start.copy_(self.ext.start(self.states))
+        t.learner_seat.copy_(learner_seat)
+        for x in t.per_wave:
+            x.zero_()
+        over = self.states[:, DONE_BYTE] != 0  # a game dealt finished (initial Chongtong)
+        t.finished.copy_(over)
+        t.started.copy_(~over)
+        self._open(self.actor, self.cache, t.start.repeat(2, 1), self.seats2)
+        if pool and self.p:
+            self._open(self.opponent, self.opp_cache, t.start[:self.p],
+                       1 - t.learner_seat[:self.p])
 
     @torch.no_grad()
     def step(self, pool: bool = False) -> None:
-        """One decision of every game (cugo_seq_selfplay50.py:108-163).  The torch
-        bookkeeping around the policy runs as two kernels (`SelfPlayState.prepare` before
-        the query, `.advance` after the event tokens)."""
-        ids, actor, ext = self.ids, self.actor, self.ext
+        """One decision of every game (the reference's _step,
+        cugo_seq_selfplay50.py:108-163); the bookkeeping around the policy is two HIP
+        launches (SelfPlayState.prepare before the query, .advance after the event
+        tokens)."""
+        ext, actor, t = self.ext, self.actor, self.t
         pool = pool and self.p > 0
         native = self.native[pool]
-        features, legal, players, done, status = ext.observe_indexed(self.states, ids)
-        stock = ext.stock_indexed(self.states, ids)
+        features, legal, players, done, status = ext.observe_indexed(self.states, self.ids)
+        stock = ext.stock_indexed(self.states, self.ids)
         q_in, query_rows = native.prepare(self.states, features, legal, players, done, status,
                                           stock, actor.event_in.weight.dtype)
-        hidden = actor.cached_step(self.cache, actor.query_from_input(q_in), rows=query_rows)
-        logits = actor.readout(hidden)  # the kernel reads bf16 logits as the fp32 .float()
+        logits = actor.readout(actor.cached_step(self.cache, actor.query_from_input(q_in),
+                                                 rows=query_rows))
         if pool:
-            # the opponent answers every pool game; its logits count where it moves
             p, opp = self.p, self.opponent
-            opp_logits = opp.readout(opp.cached_step(self.opp_cache, opp.query_from_input(q_in[:p])))
-            opp_move = players[:p].long() != self.learner_seat[:p]
-            logits = torch.cat((torch.where(opp_move.unsqueeze(1), opp_logits.to(logits.dtype),
-                                            logits[:p]), logits[p:]))
-        self.logits = logits  # the last step's logits (kept for inspection)
-        uniforms = (torch.rand(logits.shape, dtype=torch.float32, device=logits.device)
-                    if self.noise is None else self.noise)
-        actions, logp = ext.gumbel_sample(logits.contiguous(), legal, uniforms)
+            theirs = opp.readout(opp.cached_step(self.opp_cache, opp.query_from_input(q_in[:p])))
+            their_turn = (players[:p].long() != t.learner_seat[:p]).unsqueeze(1)
+            logits = torch.cat((torch.where(their_turn, theirs.to(logits.dtype), logits[:p]),
+                                logits[p:]))
+        self.logits = logits
+        noise = self.noise if self.noise is not None else torch.rand(
+            logits.shape, dtype=torch.float32, device=logits.device)
+        actions, logp = ext.gumbel_sample(logits.contiguous(), legal, noise)
         reward0, new_done, nagari, step_status, committed, events = ext.step_events_indexed(
-            self.states, ids, actions)
-        actor.cached_step(self.cache, actor.event_token(events, self.seats2, self.count))
+            self.states, self.ids, actions)
+        actor.cached_step(self.cache, actor.event_token(events, self.seats2, t.count))
         if pool:
-            opp = self.opponent
-            opp.cached_step(self.opp_cache, opp.event_token(events[:p], 1 - self.learner_seat[:p],
-                                                            self.count[:p]))
+            opp.cached_step(self.opp_cache,
+                            opp.event_token(events[:p], 1 - t.learner_seat[:p], t.count[:p]))
         native.advance(done, reward0, new_done, nagari, step_status, committed, events, actions,
                        logp)
-        self.step_index += 1
+        t.step_index += 1
 
-    @torch.no_grad()
-    def capture(self, pool: bool = False) -> None:
-        """Record step(pool) once as a HIP graph (cugo_seq_selfplay50.py:165-180)."""
-        pool = pool and self.p > 0
-        if self.graph is not None and self.graph_pool == pool:
-            return
-        self.graph = None
+    def _capture_step(self, pool: bool) -> torch.cuda.CUDAGraph:
+        """step(pool) as a HIP graph.  Library handles, the caching allocator's blocks and
+        the token weights are set up by two eager steps on a side stream first, so the
+        capture records kernel launches only."""
         self.actor.prepare()
         if self.opponent is not None:
             self.opponent.prepare()
-        seeds, first = make_seeds(self.w, 0, self.states.device)
-        self.reset(seeds, first, torch.zeros_like(self.learner_seat), pool)
+        self.reset(*make_seeds(self.w, 0, self.states.device),
+                   torch.zeros_like(self.t.learner_seat), pool)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            for _ in range(2):  # warm-up (GEMM handles, allocator) outside the capture
-                self.step(pool)
+            self.step(pool)
+            self.step(pool)
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             self.step(pool)
-        self.graph, self.graph_pool = graph, pool
+        return graph
+
+    @torch.no_grad()
+    def capture(self, pool: bool = False) -> None:
+        """Captures one step (for `pool`) into self.graph unless it already holds it."""
+        pool = pool and self.p > 0
+        if self.graph is None or self.graph_pool != pool:
+            self.graph, self.graph_pool = None, None
+            self.graph, self.graph_pool = self._capture_step(pool), pool
 
     @torch.no_grad()
     def play(self, seeds: torch.Tensor, first: torch.Tensor, learner_seat: torch.Tensor,
              pool: bool = False) -> int:
-        """Plays one wave to the end by replaying the captured step; returns the number of
-        steps replayed (cugo_seq_selfplay50.py:203-219)."""
+        """Deals a wave and replays the step until every game has finished; returns the
+        number of steps run.  After each replay the finished flag is copied to pinned
+        host memory behind it, and the host reads the flag of the replay before the one
+        it has just queued, so the GPU never waits for the host: the wave runs at most
+        one step past its end."""
         self.capture(pool)
         self.reset(seeds, first, learner_seat, pool)
-        for k in range(self.max_steps):
-            self.graph.replay()
-            if (k + 1) % 4 == 0 and k + 1 >= 16 and bool(self.finished.all()):
-                steps = k + 1
-                break
-        else:
-            if not bool(self.finished.all()):
-                raise RuntimeError(f"games did not finish within {self.max_steps} steps")
-            steps = self.max_steps
-        if int(self.bad):
-            raise RuntimeError(f"{int(self.bad)} bad observe/step results in a wave")
-        if int(self.count.max()) > MAX_EVENTS:
-            raise RuntimeError("event log overflow")
+        flags, t = self._done_flags, self.t
+        stream = torch.cuda.current_stream()
+        queued = None  # (event, steps, flag slot) of the latest replay
+        steps = 0
+        while True:
+            behind = queued
+            if steps < self.max_steps:
+                self.graph.replay()
+                steps += 1
+                flags[steps & 1].copy_(t.finished.all(), non_blocking=True)
+                queued = (torch.cuda.Event(), steps, steps & 1)
+                queued[0].record(stream)
+            if behind is not None:
+                behind[0].synchronize()
+                if bool(flags[behind[2]]):
+                    break
+                if behind[1] == self.max_steps:
+                    raise RuntimeError(f"a wave ran {self.max_steps} steps with games left")
+        problems = int(t.bad)
+        if problems:
+            raise RuntimeError(f"{problems} observe or step results of active games were "
+                               "not ok in this wave")
+        if int(t.count.max()) > MAX_EVENTS:
+            raise RuntimeError(f"a game committed more than {MAX_EVENTS} events")
         return steps
+
+    def _decisions(self, offset: int) -> dict[str, torch.Tensor]:
+        """The learner's recorded decisions of the last wave in step-major order (each
+        step's games in order), as the reference appends them to its storage."""
+        t = self.t
+        flat = torch.nonzero(t.rec_valid.flatten()).squeeze(1)
+        step_of, game_of = flat // self.w, flat % self.w
+        out = {"features": t.rec_features[step_of, game_of],
+               "legal": t.rec_legal[step_of, game_of], "logp": t.rec_logp[step_of, game_of],
+               "env_ids": offset + game_of}
+        out.update({k: v.flatten()[flat] for k, v in t.rec_long.items()})
+        return out
 
     @torch.no_grad()
     def collect(self, games: int, seed_offset: int, opponent_state: dict | None = None) -> dict:
-        """Plays `games` games, a multiple of the wave (cugo_seq_selfplay50.py:182-238).
-        With opponent_state (loaded into the opponent in place, so the captured step keeps
-        its pointers) the first pool_games of every wave face it.  Returns the outcomes
-        the reference returns, plus what it hands its rollout storage and event log: the
-        learner's decisions step-major within each wave (`decisions`) and every game's
-        event log, count and opening (`log`)."""
+        """Plays games seed_offset .. seed_offset + games - 1, wave by wave (the
+        reference's collect, cugo_seq_selfplay50.py:182-238; games must be a multiple of
+        the wave).  opponent_state, loaded into the opponent in place so the captured
+        graph keeps reading the same weights, puts it in the first pool_games of every
+        wave.  Returns the reference's outcome tensors, the learner's decisions
+        ("decisions", what the reference hands its rollout storage) and every game's
+        event log, count and opening ("log")."""
         if games % self.w:
-            raise ValueError(f"games ({games}) must be a multiple of the wave size ({self.w})")
-        device = self.states.device
+            raise ValueError(f"{games} games do not split into waves of {self.w}")
+        dev = self.states.device
         pool = opponent_state is not None and self.p > 0
         if pool:
             self.opponent.load_state_dict(opponent_state)
             self.opponent.prepare()
-        seeds, first = make_seeds(games, seed_offset, device)
-        learner_seat = torch.randint(2, (games,), device=device)
-        vs_pool = torch.zeros(games, dtype=torch.bool, device=device)
-        final_reward0 = torch.zeros(games, device=device)
-        final_nagari = torch.zeros(games, dtype=torch.bool, device=device)
-        started = torch.zeros(games, dtype=torch.bool, device=device)
-        log = {"events": torch.zeros((games, MAX_EVENTS, EVENT_WORDS), dtype=torch.int64,
-                                     device=device),
-               "count": torch.zeros(games, dtype=torch.int64, device=device),
-               "start": torch.zeros((games, START_WORDS), dtype=torch.int64, device=device)}
-        parts: dict[str, list[torch.Tensor]] = {k: [] for k in (
-            "features", "legal", "actions", "logp", "opp_hand", "stock", "stop_points",
-            "env_ids", "seat", "count")}
+        seeds, first = make_seeds(games, seed_offset, dev)
+        learner_seat = torch.randint(2, (games,), device=dev)
+        waves: list[dict[str, torch.Tensor]] = []
+        decisions: list[dict[str, torch.Tensor]] = []
         steps = 0
+        t = self.t
         for offset in range(0, games, self.w):
             part = slice(offset, offset + self.w)
             steps = max(steps, self.play(seeds[part], first[part], learner_seat[part], pool))
-            at = torch.nonzero(self.rec_valid)  # step-major: decisions stay in game order
-            s_idx, g_idx = at[:, 0], at[:, 1]
-            parts["features"].append(self.rec_features[s_idx, g_idx])
-            parts["legal"].append(self.rec_legal[s_idx, g_idx])
-            parts["logp"].append(self.rec_logp[s_idx, g_idx])
-            parts["env_ids"].append(offset + g_idx)
-            for name in ("actions", "opp_hand", "stock", "stop_points", "seat", "count"):
-                parts[name].append(self.rec_long[name][s_idx, g_idx])
-            log["events"][part] = self.events
-            log["count"][part] = self.count
-            log["start"][part] = self.start
-            final_reward0[part] = self.final_reward0
-            final_nagari[part] = self.final_nagari
-            started[part] = self.started
-            if pool:
-                vs_pool[offset:offset + self.p] = True
-        return {"final_reward0": final_reward0, "final_nagari": final_nagari,
-                "started": started, "learner_seat": learner_seat, "vs_pool": vs_pool,
-                "steps": steps, "decisions": {k: torch.cat(v) for k, v in parts.items()},
-                "log": log}
+            decisions.append(self._decisions(offset))
+            vs_pool = torch.zeros(self.w, dtype=torch.bool, device=dev)
+            vs_pool[:self.p if pool else 0] = True
+            waves.append({"final_reward0": t.final_reward0.clone(),
+                          "final_nagari": t.final_nagari.clone(), "started": t.started.clone(),
+                          "vs_pool": vs_pool, "events": t.events.clone(),
+                          "count": t.count.clone(), "start": t.start.clone()})
+        joined = {k: torch.cat([wv[k] for wv in waves]) for k in waves[0]}
+        return {"final_reward0": joined["final_reward0"], "final_nagari": joined["final_nagari"],
+                "started": joined["started"], "learner_seat": learner_seat,
+                "vs_pool": joined["vs_pool"], "steps": steps,
+                "decisions": {k: torch.cat([d[k] for d in decisions]) for k in decisions[0]},
+                "log": {k: joined[k] for k in ("events", "count", "start")}}
