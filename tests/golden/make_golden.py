@@ -15,6 +15,8 @@ outputs as .npz data:
                         (incl. pending floor choices) with their observations, hands,
                         stock peeks and the step results of a fixed action list.
   canonical.npz         digests of the canonical whole-game driver (see canonical()).
+  scenarios.npz         the hand-built rule scenarios of scenarios.py, played (see
+                        scenario_fixture()).
 
     python tests/golden/make_golden.py canonical     (one fixture only)
 """
@@ -109,11 +111,59 @@ def canonical(ref: RefEngine) -> None:
     print("canonical: 8,192 + 4,096 + 512 digests")
 
 
+def scenario_fixture(ref: RefEngine) -> None:
+    """The hand-built rule scenarios of tests/golden/scenarios.py played on the reference
+    build: for each step of each scenario the row before it, its observation, the action,
+    the step outputs with the event record, and the row after; for each scenario's first
+    row its start words, hands and stock peek, and one child for every legal action plus
+    an illegal and an out-of-range one (branch_indexed)."""
+    from tests.golden.scenarios import scenarios
+
+    rec = {k: [] for k in ("step_scenario", "step_row", "step_action", "features", "legal",
+                           "player", "done", "status", "reward", "step_done", "nagari",
+                           "step_status", "committed", "events", "after")}
+    br = {k: [] for k in ("branch_scenario", "branch_action", "children", "b_reward", "b_done",
+                          "b_nagari", "b_status", "b_committed")}
+    names, firsts = [], []
+    for k, (name, first, actions, _) in enumerate(scenarios()):
+        names.append(name)
+        firsts.append(first)
+        rows = first[None].copy()
+        for a in actions:
+            f, legal, player, done, status = ref.observe(rows)
+            before = rows.copy()
+            out = ref.step(rows, np.array([a], dtype=np.int64), events=True)
+            for key, v in zip(("step_scenario", "step_row", "step_action", "features", "legal",
+                               "player", "done", "status", "reward", "step_done", "nagari",
+                               "step_status", "committed", "events", "after"),
+                              (np.array([k]), before, np.array([a], dtype=np.int64), f, legal,
+                               player, done, status, *out, rows.copy())):
+                rec[key].append(v)
+            print(f"  {name:26s} action {a:3d} -> status {int(out[3][0])} done {int(out[1][0])} "
+                  f"reward {float(out[0][0]):g}")
+        _, legal, _, _, _ = ref.observe(first[None])
+        acts = np.concatenate([np.nonzero(legal[0])[0], [0 if not legal[0, 0] else 1, 400]])
+        acts = np.unique(acts).astype(np.int64)
+        out = ref.branch(first[None], np.zeros(acts.size, dtype=np.int64), acts)
+        for key, v in zip(br, (np.full(acts.size, k), acts, *out)):
+            br[key].append(v)
+    firsts = np.stack(firsts)
+    ids = np.arange(len(firsts), dtype=np.int64)
+    np.savez_compressed(
+        HERE / "scenarios.npz", names=np.array(names), first=firsts, start=ref.start(firsts),
+        hands=ref.hands(firsts, ids), stock=ref.stock(firsts, ids),
+        **{k: np.concatenate(v) for k, v in rec.items()},
+        **{k: np.concatenate(v) for k, v in br.items()})
+    print(f"scenarios: {len(names)} scenarios, {sum(map(len, rec['step_action']))} steps, "
+          f"{sum(map(len, br['branch_action']))} children")
+
+
 def main() -> None:
     ref = RefEngine(reference=True)
-    what = sys.argv[1:] or ["c1", "rows", "canonical"]
+    what = sys.argv[1:] or ["c1", "rows", "canonical", "scenarios"]
     for name in what:
-        {"c1": c1, "rows": rows, "canonical": canonical}[name](ref)
+        {"c1": c1, "rows": rows, "canonical": canonical,
+         "scenarios": scenario_fixture}[name](ref)
 
 
 if __name__ == "__main__":

@@ -275,3 +275,70 @@ def test_cached_step_matches_reference_and_replays_in_a_graph(ext):
             graph.replay()
             torch.cuda.synchronize()
             assert rel_err(out, eager.float()) <= 1e-3
+
+
+def _event_counts(ext, games: int, base: int) -> torch.Tensor:
+    """Committed events of each of `games` seeded random-policy games (seed base + j,
+    first j & 1), played to the end on the HIP engine."""
+    idx = torch.arange(games, dtype=torch.int64, device=DEV)
+    states = ext.create(idx + base, idx & 1)
+    sampler = ext.seed_samplers(games, base, torch.zeros(games, dtype=torch.int32, device=DEV))
+    count = torch.zeros(games, dtype=torch.int64, device=DEV)
+    for _ in range(128):
+        _, legal, _, done, _ = ext.observe(states)
+        if bool(done.all()):
+            return count
+        out = ext.step_events_indexed(states, idx, ext.sample_uniform(legal, sampler))
+        count += (out[4] & ~done).long()
+    raise AssertionError("random-policy games did not finish")
+
+
+@pytest.mark.parametrize("lengths", ["stress", "natural"])
+def test_cached_step_full_cache_with_game_lengths(ext, lengths):
+    """The sequence policy's step at its full cache shape: 4 layers, d 256, 8 heads of 32,
+    cache [4, 4,096, 8, 320, 32] bf16.  Row lengths come from seeded random-policy games:
+    "stress" concatenates consecutive games' event logs (one opening token plus each
+    game's events) while they fit below 320 slots, "natural" holds one game.  Two steps
+    of the fused HIP step against the reference formulation (index_put_ + the matmul
+    decode path, oracle/seq_ref.py) on identical caches: hidden states within 1e-2
+    relative, and the appended key/value slots within 1e-2."""
+    from cugo_amd.seq_decode import KVCache, cached_step
+    from oracle.seq_ref import reference_cached_step
+
+    announce(f"cached_step full cache [4, 4096, 8, 320, 32], {lengths} lengths")
+    rows, slots, per_row = 4096, 320, 16
+    ev = _event_counts(ext, rows * per_row, 0x243F6A8885A308D3 + 0xDEC0DE).view(per_row, rows)
+    if lengths == "natural":
+        length = (1 + ev[0]).clamp_max(slots - 1)
+    else:
+        total = torch.cumsum(ev, 0) + 1
+        length = torch.where(total <= slots - 2, total, torch.zeros_like(total)).max(0).values
+        length = torch.where(length == 0, (1 + ev[0]).clamp_max(slots - 2), length)
+    assert int(length.max()) <= slots - 2 and int(length.min()) >= 1
+    mean = float(length.float().mean())
+    assert (mean > 250) if lengths == "stress" else (10 < mean < 40), mean
+    model = _layered_model()
+    ca = KVCache(4, rows, 8, 256, slots, torch.device(DEV))
+    cb = KVCache(4, rows, 8, 256, slots, torch.device(DEV))
+    g = torch.Generator(device=DEV).manual_seed(21)
+    for t in (ca.k, ca.v):
+        t.copy_((torch.randn(t.shape, generator=g, device=DEV) * 0.5).to(t.dtype))
+    cb.k.copy_(ca.k)
+    cb.v.copy_(ca.v)
+    ca.length.copy_(length)
+    cb.length.copy_(length)
+    ids = torch.arange(rows, device=DEV)
+    with torch.no_grad():
+        for step in range(2):
+            x = (torch.randn(rows, 256, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+            ha = cached_step(model, ca, x)
+            hb = reference_cached_step(model, cb, x, ids)
+            assert rel_err(ha, hb.float()) <= 1e-2, step
+            at = ca.length.clamp_max(slots - 1)
+            for layer in range(4):
+                for a, b in ((ca.k, cb.k), (ca.v, cb.v)):
+                    new_a = a[layer, ids, :, at]
+                    new_b = b[layer, ids, :, at]
+                    assert rel_err(new_a, new_b.float()) <= 1e-2, (step, layer)
+            ca.length += 1
+            cb.length += 1
