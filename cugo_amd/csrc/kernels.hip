@@ -379,8 +379,8 @@ __device__ inline i64 spare_row(const AutoReset& ar, i64 i, u32 gen) {
 }
 
 // kMode: 0 = step (contiguous, in place), 1 = step_indexed (gather/scatter in place),
-// 2 = branch_indexed (gather from parents, children written contiguously),
-// 3 = step with the auto-reset above (contiguous, in place).
+// 3 = step with the auto-reset above (contiguous, in place); branch_indexed has its own
+// kernel below.
 // kThreads = 128: two waves per tile of 64 games, both stage the rows in and out and
 // wave 0 runs the games (one per lane).  At ~250 VGPRs two waves fit per SIMD, so this
 // is the shape while every tile of the grid is resident at once (up to four per CU);
@@ -388,7 +388,7 @@ __device__ inline i64 spare_row(const AutoReset& ar, i64 i, u32 gen) {
 // many games computing per CU.
 template <int kMode, bool kEvents, int kStepThreads>
 __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env_count, const i64* ids,
-                                                     const i64* actions, i64 n, u64* children,
+                                                     const i64* actions, i64 n,
                                                      float* reward, u8* done, u8* nagari,
                                                      i16* status, u8* committed, i64* events,
                                                      AutoReset ar) {
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
   const i64 base = tile_base();
   const int count = tile_count(base, n);
   const int lane = threadIdx.x;
-  constexpr bool kIndexed = kMode == 1 || kMode == 2;
+  constexpr bool kIndexed = kMode == 1;
   if (kIndexed && lane < count) tile_ids[lane] = ids[base + lane];
   __syncthreads();
   stage_in<kStepThreads>(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
@@ -450,7 +450,6 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
       }
     } else {  // torch50_ext.cu:108-118
       if (kEvents) for (int k = 0; k < kEventWords; ++k) evr[k] = 0;
-      if (kMode == 2) for (int k = 0; k < kRowWords; ++k) row[k] = 0;
       reward[i] = 0.0f;
       done[i] = 1;
       nagari[i] = 0;
@@ -477,13 +476,54 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
     }
   }
   __syncthreads();
-  if (kMode == 0 || kMode == 3) stage_out<kStepThreads>(rows, states, nullptr, base, count, env_count);
-  else if (kMode == 1) stage_out<kStepThreads>(rows, states, tile_ids, base, count, env_count);
-  else stage_out<kStepThreads>(rows, children, nullptr, base, count, env_count);
+  stage_out<kStepThreads>(rows, states, kIndexed ? tile_ids : nullptr, base, count, env_count);
   if (kEvents) {
     i64* eout = events + base * kEventWords;
     for (int j = lane; j < count * kEventWords; j += kStepThreads) eout[j] = ev[j];
   }
+}
+
+// ------------------------------------------------------------------ branch ----
+// branch_indexed (torch50_ext.cu:288-314) without LDS: each lane reads its parent row
+// straight from global memory (branching children of one root read the same row, so a
+// wave's loads are broadcasts from L2), steps it in registers and writes its child row
+// from registers.  The transition holds ~200 VGPRs, which allows two waves per SIMD;
+// capping registers for three or four waves spills 144 / 356 bytes a lane and measured
+// 1.35x / 2.7x slower on 1,048,576 children, and staging the rows through LDS as the other
+// step kernels do measured 1.13x slower.
+__global__ __launch_bounds__(kTile) void branch_kernel(const u64* parents, i64 env_count,
+                                                       const i64* ids, const i64* actions,
+                                                       i64 n, u64* children, float* reward,
+                                                       u8* done, u8* nagari, i16* status,
+                                                       u8* committed) {
+  const i64 i = (i64)blockIdx.x * kTile + threadIdx.x;
+  if (i >= n) return;
+  const i64 id = ids[i];
+  u64 row[kRowWords];
+  if (valid_id(id, env_count)) {
+    const u64* src = parents + id * kRowWords;
+#pragma unroll
+    for (int k = 0; k < kRowWords; ++k) row[k] = src[k];
+    Env e = unpack_row(row);
+    const StepOut so = torch_step(e, clamp_action(actions[i]));
+    pack_row(e, row);
+    reward[i] = (float)so.reward0;
+    done[i] = so.done;
+    nagari[i] = so.nagari;
+    status[i] = (i16)so.status;
+    committed[i] = so.committed;
+  } else {  // torch50_ext.cu:108-118: a zero child
+#pragma unroll
+    for (int k = 0; k < kRowWords; ++k) row[k] = 0;
+    reward[i] = 0.0f;
+    done[i] = 1;
+    nagari[i] = 0;
+    status[i] = CUGO_INVALID_INDEX_STATUS;
+    committed[i] = 0;
+  }
+  u64* out = children + i * kRowWords;
+#pragma unroll
+  for (int k = 0; k < kRowWords; ++k) out[k] = row[k];
 }
 
 // ------------------------------------------------------------ random play ----
@@ -1081,7 +1121,7 @@ int cugo_step(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
     return kBadArgument;
   if (n == 0) return 0;
   launch_step<0, false>(n, stream, 
-      reinterpret_cast<u64*>(states), n, nullptr, actions, n, nullptr, reward, done, nagari,
+      reinterpret_cast<u64*>(states), n, nullptr, actions, n, reward, done, nagari,
       status, committed, nullptr, AutoReset{});
   return launched();
 }
@@ -1176,7 +1216,7 @@ int cugo_step_reset_spares(uint8_t* states, const int64_t* actions, int64_t n, f
                      const_cast<u64*>(reinterpret_cast<const u64*>(spares)), spare_gen, n,
                      (u32)(spare_slots - 1)};
   launch_step<3, false>(n, stream, reinterpret_cast<u64*>(states), n, nullptr, actions, n,
-                        nullptr, reward, done, nagari, status, committed, nullptr, ar);
+                        reward, done, nagari, status, committed, nullptr, ar);
   return launched();
 }
 
@@ -1189,7 +1229,7 @@ int cugo_step_indexed(uint8_t* states, int64_t env_count, const int64_t* ids,
     return kBadArgument;
   if (n == 0) return 0;
   launch_step<1, false>(n, stream, 
-      reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
+      reinterpret_cast<u64*>(states), env_count, ids, actions, n, reward, done,
       nagari, status, committed, nullptr, AutoReset{});
   return launched();
 }
@@ -1204,7 +1244,7 @@ int cugo_step_events_indexed(uint8_t* states, int64_t env_count, const int64_t* 
     return kBadArgument;
   if (n == 0) return 0;
   launch_step<1, true>(n, stream, 
-      reinterpret_cast<u64*>(states), env_count, ids, actions, n, nullptr, reward, done,
+      reinterpret_cast<u64*>(states), env_count, ids, actions, n, reward, done,
       nagari, status, committed, events, AutoReset{});
   return launched();
 }
@@ -1238,10 +1278,10 @@ int cugo_branch_indexed(const uint8_t* states, int64_t env_count, const int64_t*
                  !committed)))
     return kBadArgument;
   if (n == 0) return 0;
-  launch_step<2, false>(n, stream, 
-      const_cast<u64*>(reinterpret_cast<const u64*>(states)), env_count, ids, actions, n,
-      reinterpret_cast<u64*>(children), reward, done, nagari, status, committed, nullptr,
-      AutoReset{});
+  branch_kernel<<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<const u64*>(states),
+                                                env_count, ids, actions, n,
+                                                reinterpret_cast<u64*>(children), reward,
+                                                done, nagari, status, committed);
   return launched();
 }
 

@@ -214,6 +214,11 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void start_tokens_kernel(
 // at the action, computed as (masked[a] - max) - log(sum exp(masked - max)).
 // Logits of type T (bf16 logits convert to fp32 exactly, as the reference's `.float()`).
 // u == nullptr: no noise, the greedy masked argmax (cugo_eval50.py:125-127).
+// Only legal actions need the two logarithms and the exponential: for u < 1 the noise
+// lies in [-3.9, 16.7], and -1e30 plus it rounds to -1e30 in fp32 (the spacing there is
+// 2^76), so an illegal action's noisy value is -1e30 (+inf when u = 1, where
+// -log(-log(1)) = +inf); and its exp(-1e30 - max) is 0 whenever some action is legal.
+// A row with no legal action sums exp(0) over every action, as the reference does.
 template <class T>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
     const typename T::storage* logits, const uint8_t* legal, const float* u, i64 n,
@@ -226,12 +231,16 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
   const float* ur = u != nullptr ? u + r * actions_count : nullptr;
   float best = -INFINITY, top = -INFINITY;
   int best_a = actions_count;  // above every real index
+  bool any = false;
   for (int a = lane; a < actions_count; a += 64) {
-    const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
+    const bool ok = gr[a] != 0;
+    any |= ok;
+    const float m = ok ? T::to_float(lr[a]) : -1.0e30f;
     float v = m;
     if (ur != nullptr) {
       const float uc = fminf(fmaxf(ur[a], 1.0e-20f), 1.0f);
-      v = m + -logf(-logf(uc));
+      if (ok) v = m + -logf(-logf(uc));
+      else if (uc >= 1.0f) v = INFINITY;
     }
     if (v > best) { best = v; best_a = a; }
     top = fmaxf(top, m);
@@ -242,11 +251,13 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
     if (ob > best || (ob == best && oa < best_a)) { best = ob; best_a = oa; }
     top = fmaxf(top, __shfl_xor(top, off));
   }
+  any = __ballot(any) != 0;
   float sum = 0.0f;
   if (logp != nullptr) {
     for (int a = lane; a < actions_count; a += 64) {
-      const float m = gr[a] ? T::to_float(lr[a]) : -1.0e30f;
-      sum += expf(m - top);
+      const bool ok = gr[a] != 0;
+      if (ok) sum += expf(T::to_float(lr[a]) - top);
+      else if (!any) sum += 1.0f;  // exp(-1e30 - (-1e30))
     }
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
   }

@@ -176,12 +176,13 @@ def test_gumbel_sample_matches_reference(ext):
     u = torch.rand(n, a, generator=g, device=DEV)
     u[10, :] = 0.0                 # clamps to 1e-20
     u[11, 17] = 1.0                # -log(-log(1)) = +inf picks action 17
+    u[2, 30] = 1.0                 # also where no action is legal: -1e30 + inf = inf
     logits[12, :] = 0.5            # ties among equal scores pick the first index
     u[12, :] = 0.5
     actions, logp = ext.gumbel_sample(logits, legal, u)
     want_a, want_lp = gumbel_reference(logits, legal, u)
     assert torch.equal(actions, want_a)
-    assert int(actions[11]) == 17
+    assert int(actions[11]) == 17 and int(actions[2]) == 30 and int(actions[3]) == 0
     assert float((logp - want_lp).abs().max()) <= 1e-5
     # bf16 logits read as the reference's .float()
     lb = logits.to(torch.bfloat16)
