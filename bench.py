@@ -399,26 +399,34 @@ def canonical_workload(ext, torch, games: int = 131072, iters: int = 8) -> dict:
     """The reference's canonical whole-game driver (rollout_canonical_torch50; its GPU
     bench times 131,072 games a launch, tests/cuda_rollout50_bench.cu:22-33, 111):
     seeds 0xBB67AE8584CAA73B + i * 0x9E3779B97F4A7C15, first = i & 1, one game per lane
-    played to the end in registers.  Complete games/s over `iters` launches (HIP events),
-    and the HBM roofline of its 56 bytes a game (seed, first, five digest words)."""
+    played to the end in registers.  Complete games/s over `iters` launches (HIP events)
+    at that size and at 8x it, and the HBM roofline of its 56 bytes a game (seed, first,
+    five digest words) at the reference's size."""
     dev = torch.device("cuda")
-    i = torch.arange(games, dtype=torch.int64, device=dev)
-    seeds = i * -7046029254386353131 + (0xBB67AE8584CAA73B - (1 << 64))
-    first = i & 1
-    ext.rollout_canonical(seeds, first)
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(iters):
-        digest = ext.rollout_canonical(seeds, first)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / iters
+
+    def timed(n: int):
+        i = torch.arange(n, dtype=torch.int64, device=dev)
+        seeds = i * -7046029254386353131 + (0xBB67AE8584CAA73B - (1 << 64))
+        first = i & 1
+        ext.rollout_canonical(seeds, first)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(iters):
+            digest = ext.rollout_canonical(seeds, first)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters, digest
+
+    ms, digest = timed(games)
+    big_ms, _ = timed(8 * games)
     actions = ((digest[:, 2] & 0xFFFF).sum()).item()
     gbs = games * 56 / (ms * 1e-3) / 1e9
     return {"games_per_s": round(games / (ms * 1e-3), 1), "launch_ms": round(ms, 4),
             "games": games, "primary_actions_per_game": round(actions / games, 2),
+            "games_per_s_8x": round(8 * games / (big_ms * 1e-3), 1),
+            "launch_ms_8x": round(big_ms, 4),
             "roofline": {"kernel": "canonical_kernel", "bound": "hbm", "achieved": round(gbs, 2),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
@@ -650,9 +658,11 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
     Gumbel-max sampling over the legal actions, a `horizon`-step buffer (bf16 features,
     mask, action, log-prob, value, reward, done), finished games re-dealt from pre-dealt
     spares inside the step.  Reports env steps/s, the engine's and the actor's shares of
-    the wall time (HIP events on the stream) and a roofline for each: the actor's
-    FLOPs over its forward time against the bf16 MFMA peak, the engine's bytes (observe
-    3,311 B a row, step with auto-reset 513 B a row) over its time against HBM."""
+    the step time and a roofline for each: the actor's FLOPs over its forward time
+    against the bf16 MFMA peak, the engine's bytes (observe 3,311 B a row, step with
+    auto-reset 513 B a row) over its time against HBM.  The rollout runs as one HIP graph
+    per horizon; the shares come from graphs of the engine's and the actor's launches
+    alone."""
     from cugo_amd.rollout import MlpRollout, ResidualMlpActor, fused_forward
 
     dev = torch.device("cuda")
@@ -665,29 +675,67 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
     gen = torch.Generator(device=dev).manual_seed(1)
     ro = MlpRollout(ext, actor, batch, horizon, SEED_BASE + 0xC4, generator=gen)
     stream = torch.cuda.current_stream()
-    with torch.no_grad():
-        for t in range(8):  # warm-up: GEMM handles, allocator
-            ro.observe()
-            ro.step(t, ro.act(t))
+
+    def graph_ms(g, reps: int) -> float:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
         torch.cuda.synchronize()
-        events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]
-                  for _ in range(horizon)]
+        return e0.elapsed_time(e1) / reps
+
+    # PyTorch-ROCm's TunableOp times the library's GEMM solutions for each shape on its
+    # first call (the eager warm-up steps of capture(), about 2 s) and keeps the fastest
+    # for the captured graph; its results file goes to the temporary directory.
+    tunable = torch.cuda.tunable
+    tunable.set_filename(os.path.join(os.environ.get("TMPDIR", "/tmp"),
+                                      "cugo_tunableop_results.csv"))
+    tunable.enable(True)
+    tunable.tuning_enable(True)
+    with torch.no_grad():
+        ro.capture()  # the whole horizon as one HIP graph
+        ro.replay()   # first replay outside the timed region
+        torch.cuda.synchronize()
         games0 = ro.games_completed()
-        ro.steps = 0
+        reps = 2
         t0 = time.perf_counter()
-        for t in range(horizon):
-            ev = events[t]
-            ev[0].record(stream)
-            ro.observe()
-            ev[1].record(stream)
-            action = ro.act(t)
-            ev[2].record(stream)
-            ro.step(t, action)
-            ev[3].record(stream)
+        for _ in range(reps):
+            ro.replay()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         games = ro.games_completed() - games0
-        # the actor's forward alone, on the last step's input: 20 back-to-back passes
+        step_ms = wall * 1e3 / (reps * horizon)
+        # The engine's share: its launches alone (observe with the random policy's draw,
+        # then step_reset_spares, the spares refilled every 32 steps) on a copy of the
+        # games, 32 steps in one graph; the actor's: its forward pass, the uniforms, the
+        # Gumbel-max draw and the buffer writes of one step, one graph.
+        st, g2, smp = ro.states.clone(), ro.generation.clone(), ro.sampler.clone()
+        sp, sg = ro.spares.clone(), ro.spare_gen.clone()
+
+        def engine_block():
+            ext.refill_spares(sp, sg, g2, SEED_BASE + 0xC4)
+            for _ in range(32):
+                _, _, _, _, _, acts = ext.observe_sample(st, smp)
+                ext.step_reset_spares(st, acts, SEED_BASE + 0xC4, g2, smp, sp, sg)
+
+        engine_block()
+        torch.cuda.synchronize()
+        eg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(eg):
+            engine_block()
+        engine_step_ms = graph_ms(eg, 3) / 32
+        del eg
+        ro.observe(0)
+        ro.act(0)
+        torch.cuda.synchronize()
+        ag = torch.cuda.CUDAGraph()
+        ag.register_generator_state(gen)
+        with torch.cuda.graph(ag):
+            ro.act(0)
+        actor_step_ms = graph_ms(ag, 10)
+        del ag
+        # the forward pass alone, 20 back-to-back passes on the last step's input
         x = ro.buffer.features[horizon - 1]
         fused_forward(ext, actor, x)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -697,18 +745,20 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         e1.record(stream)
         torch.cuda.synchronize()
         forward_ms = e0.elapsed_time(e1) / 20
-    engine_ms = sum(e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[3]) for e in events)
-    actor_ms = sum(e[1].elapsed_time(e[2]) for e in events)
+    tunable.tuning_enable(False)
+    tunable.enable(False)
     flops_row = actor.flops_per_row()
     tflops = flops_row * batch / (forward_ms * 1e-3) / 1e12
-    engine_bytes = batch * (OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW) * horizon
-    engine_gbs = engine_bytes / (engine_ms * 1e-3) / 1e9
-    return {"env_steps_per_s": round(batch * horizon / wall, 1),
+    engine_bytes = batch * (OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW)
+    engine_gbs = engine_bytes / (engine_step_ms * 1e-3) / 1e9
+    return {"env_steps_per_s": round(batch * reps * horizon / wall, 1),
             "games_per_s": round(games / wall, 1),
-            "wall_ms": round(wall * 1e3, 2),
-            "engine_share": round(engine_ms / (wall * 1e3), 4),
-            "actor_share": round(actor_ms / (wall * 1e3), 4),
-            "engine_ms": round(engine_ms, 2), "actor_ms": round(actor_ms, 2),
+            "step_ms": round(step_ms, 4),
+            "engine_share": round(engine_step_ms / step_ms, 4),
+            "actor_share": round(actor_step_ms / step_ms, 4),
+            "engine_step_ms": round(engine_step_ms, 4), "actor_step_ms": round(actor_step_ms, 4),
+            "hip_graph": "one graph per rollout of horizon steps",
+            "gemm_selection": "PyTorch-ROCm TunableOp",
             "roofline": {"kernel": "actor forward (hipBLASLt GEMMs + HIP add_layernorm)",
                          "bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
                          "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
@@ -719,7 +769,7 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(engine_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                                 "bytes_per_row_step": OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW,
-                                "ms_per_step": round(engine_ms / horizon, 4)},
+                                "ms_per_step": round(engine_step_ms, 4)},
             "games_completed": games,
             "batch": batch, "horizon": horizon, "dtype": "bf16"}
 

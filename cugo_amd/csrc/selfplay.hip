@@ -269,6 +269,79 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
   }
 }
 
+// The same sampling with 16 lanes per row and four rows per wavefront, for rows of at
+// most kGumbelLanes * kGumbelPer actions: lane j of a row takes actions j, j + 16, ...,
+// issues all of its loads before any arithmetic, and keeps its masked logits in
+// registers for the softmax sum, so a row costs one round of memory latency.  Ties and
+// the reductions follow gumbel_kernel (the largest value, the first index among equal
+// ones); only the order of the fp32 softmax sum differs.
+constexpr int kGumbelLanes = 16;
+constexpr int kGumbelPer = 12;  // up to 192 actions
+
+template <class T>
+__global__ __launch_bounds__(256) void gumbel_rows_kernel(
+    const typename T::storage* logits, const uint8_t* legal, const float* u, i64 n,
+    int actions_count, i64* actions, float* logp) {
+  const int j = threadIdx.x & (kGumbelLanes - 1);
+  const i64 r = (i64)blockIdx.x * (256 / kGumbelLanes) + (threadIdx.x / kGumbelLanes);
+  const bool row_ok = r < n;
+  const typename T::storage* lr = logits + r * actions_count;
+  const uint8_t* gr = legal + r * actions_count;
+  const float* ur = u != nullptr ? u + r * actions_count : nullptr;
+  bool ok[kGumbelPer];
+  float m[kGumbelPer], uc[kGumbelPer];
+#pragma unroll
+  for (int k = 0; k < kGumbelPer; ++k) {
+    const int a = j + kGumbelLanes * k;
+    const bool in = row_ok && a < actions_count;
+    ok[k] = in && gr[a] != 0;
+    m[k] = ok[k] ? T::to_float(lr[a]) : -1.0e30f;
+    uc[k] = (in && ur != nullptr) ? fminf(fmaxf(ur[a], 1.0e-20f), 1.0f) : 0.0f;
+  }
+  float best = -INFINITY, best_m = -1.0e30f, top = -INFINITY;
+  int best_a = 1 << 30;  // above every real index
+  bool any = false;
+#pragma unroll
+  for (int k = 0; k < kGumbelPer; ++k) {
+    const int a = j + kGumbelLanes * k;
+    if (!row_ok || a >= actions_count) continue;
+    any |= ok[k];
+    float v = m[k];
+    if (ur != nullptr) {
+      if (ok[k]) v = m[k] + -logf(-logf(uc[k]));
+      else if (uc[k] >= 1.0f) v = INFINITY;
+    }
+    if (v > best) { best = v; best_a = a; best_m = m[k]; }
+    top = fmaxf(top, m[k]);
+  }
+  for (int off = kGumbelLanes / 2; off > 0; off >>= 1) {
+    const float ob = __shfl_xor(best, off);
+    const int oa = __shfl_xor(best_a, off);
+    const float om = __shfl_xor(best_m, off);
+    if (ob > best || (ob == best && oa < best_a)) { best = ob; best_a = oa; best_m = om; }
+    top = fmaxf(top, __shfl_xor(top, off));
+    const int other = __shfl_xor((int)any, off);  // every lane takes part in the shuffle
+    any = any || other != 0;
+  }
+  float sum = 0.0f;
+  if (logp != nullptr) {
+#pragma unroll
+    for (int k = 0; k < kGumbelPer; ++k) {
+      const int a = j + kGumbelLanes * k;
+      if (!row_ok || a >= actions_count) continue;
+      if (ok[k]) sum += expf(m[k] - top);
+      else if (!any) sum += 1.0f;  // exp(-1e30 - (-1e30))
+    }
+    for (int off = kGumbelLanes / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  }
+  if (j == 0 && row_ok) {
+    const bool found = best_a < actions_count;
+    actions[r] = found ? best_a : 0;
+    const float mv = found ? best_m : (gr[0] ? T::to_float(lr[0]) : -1.0e30f);
+    if (logp != nullptr) logp[r] = (mv - top) - logf(sum);
+  }
+}
+
 // ------------------------------------------------------------ step bookkeeping ----
 // WaveCollector._step (cugo_seq_selfplay50.py:108-163, no opponent pool) around the
 // policy: what it does with torch ops between observe and the query, and after the engine
@@ -564,15 +637,25 @@ int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* lega
       (n > 0 && (!logits || !legal || !actions)))
     return -1;
   if (n == 0) return 0;
+  if (logits_dtype != CUGO_DTYPE_F32 && logits_dtype != CUGO_DTYPE_BF16) return -2;
+  const bool f32 = logits_dtype == CUGO_DTYPE_F32;
+  if (actions_count <= kGumbelLanes * kGumbelPer) {
+    const unsigned grid = (unsigned)((n + 256 / kGumbelLanes - 1) / (256 / kGumbelLanes));
+    if (f32)
+      gumbel_rows_kernel<F32><<<grid, 256, 0, stream>>>(
+          (const float*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
+    else
+      gumbel_rows_kernel<BF16><<<grid, 256, 0, stream>>>(
+          (const uint16_t*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
+    return (int)hipGetLastError();
+  }
   const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
-  if (logits_dtype == CUGO_DTYPE_F32)
+  if (f32)
     gumbel_kernel<F32><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
         (const float*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
-  else if (logits_dtype == CUGO_DTYPE_BF16)
+  else
     gumbel_kernel<BF16><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
         (const uint16_t*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
-  else
-    return -2;
   return (int)hipGetLastError();
 }
 

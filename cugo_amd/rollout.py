@@ -114,7 +114,12 @@ class RolloutBuffer:
 
 class MlpRollout:
     """B resident games played by `actor` with auto-reset.  Game j of row i is dealt
-    from seed base_seed + i + B * j with first player i & 1 (j = generation[i])."""
+    from seed base_seed + i + B * j with first player i & 1 (j = generation[i]).
+
+    `collect()` plays `horizon` steps eagerly; `capture()` records those steps once as a
+    HIP graph and `replay()` plays the next `horizon` steps from it (no per-op launch cost
+    on the host).  Uniforms come from `generator` (registered with the graph), or from
+    `noise` [B, 179] when set, which every step then reads."""
 
     def __init__(self, ext, actor: ResidualMlpActor, batch: int, horizon: int,
                  base_seed: int, generator: torch.Generator | None = None) -> None:
@@ -131,12 +136,14 @@ class MlpRollout:
         self.spare_gen = torch.zeros(SPARE_SLOTS * batch, dtype=torch.int32, device=dev)
         self.buffer = RolloutBuffer.empty(horizon, batch, dev)
         self.generator = generator
-        self.steps = 0
+        self.noise: torch.Tensor | None = None
+        self.graph: torch.cuda.CUDAGraph | None = None
         self.observation = None  # the last step's observe outputs
         self.step_out = None     # the last step's step outputs
 
-    def observe(self):
-        if self.steps % REFILL == 0:
+    def observe(self, t: int):
+        """Step t's observation (the next games are pre-dealt every REFILL steps)."""
+        if t % REFILL == 0:
             self.ext.refill_spares(self.spares, self.spare_gen, self.generation, self.base)
         self.observation = self.ext.observe(self.states)
         return self.observation
@@ -149,7 +156,8 @@ class MlpRollout:
         x = buf.features[t]
         x.copy_(features)
         logits, value = fused_forward(self.ext, self.actor, x)
-        u = torch.rand(logits.shape, generator=self.generator, device=logits.device)
+        u = self.noise if self.noise is not None else torch.rand(
+            logits.shape, generator=self.generator, device=logits.device)
         action, logp = self.ext.gumbel_sample(logits, legal, u)
         buf.legal[t].copy_(legal)
         buf.action[t].copy_(action)
@@ -163,15 +171,43 @@ class MlpRollout:
             self.spare_gen)
         self.buffer.reward[t].copy_(self.step_out[0])
         self.buffer.done[t].copy_(self.step_out[1])
-        self.steps += 1
         return self.step_out
 
+    def _steps(self) -> None:
+        for t in range(self.horizon):
+            self.observe(t)
+            self.step(t, self.act(t))
+
+    @torch.no_grad()
     def collect(self) -> RolloutBuffer:
-        """`horizon` steps into the buffer (the games carry on across calls)."""
-        with torch.no_grad():
-            for t in range(self.horizon):
-                self.observe()
+        """`horizon` steps into the buffer, issued eagerly (the games carry on across
+        calls)."""
+        self._steps()
+        return self.buffer
+
+    @torch.no_grad()
+    def capture(self) -> None:
+        """Records `horizon` steps as one HIP graph.  Two eager steps on a side stream set
+        up the GEMM handles and the allocator's blocks first; they advance the games."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for t in range(2):
+                self.observe(t)
                 self.step(t, self.act(t))
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        if self.generator is not None and self.noise is None:
+            graph.register_generator_state(self.generator)
+        with torch.cuda.graph(graph):
+            self._steps()
+        self.graph = graph
+
+    def replay(self) -> RolloutBuffer:
+        """The next `horizon` steps from the captured graph."""
+        if self.graph is None:
+            raise RuntimeError("capture() the rollout before replaying it")
+        self.graph.replay()
         return self.buffer
 
     def games_completed(self) -> int:

@@ -50,7 +50,7 @@ def test_rollout_engine_matches_oracle(ext, ref):
     hgen = np.zeros(n, dtype=np.int64)
     with torch.no_grad():
         for t in range(steps):
-            obs = ro.observe()
+            obs = ro.observe(t)
             robs = ref.observe(host)
             assert_observe_equal(obs, robs, f"observation, step {t}")
             action = ro.act(t)
@@ -108,3 +108,35 @@ def test_fused_forward_matches_float32(ext):
     assert float((got_l.float() - plain_l.float()).norm() / plain_l.float().norm()) <= 2e-2
     agree = float((got_l.float().argmax(1) == want_l.argmax(1)).float().mean())
     assert agree >= 0.97, agree
+
+
+def test_rollout_graph_replay_equals_eager(ext):
+    """capture() + replay() plays what collect() plays: two rollouts from the same deals
+    with the same fixed noise, one eager and one from the captured graph, for two horizons
+    of 40 steps (refills at steps 0 and 32 of each): identical rows, generations, samplers
+    and buffers after each horizon."""
+    from cugo_amd.rollout import MlpRollout
+
+    announce("MLP rollout graph replay vs eager")
+    n, horizon, base = 8192, 40, 0x1234567
+    actor = _actor(1, 0.05).to(torch.bfloat16).eval()
+    a = MlpRollout(ext, actor, n, horizon, base)
+    b = MlpRollout(ext, actor, n, horizon, base)
+    noise = torch.rand((n, 179), generator=torch.Generator(device=DEV).manual_seed(9),
+                       device=DEV)
+    a.noise, b.noise = noise, noise
+    with torch.no_grad():
+        b.capture()  # runs two eager warm-up steps (t = 0, 1) before recording
+        for t in range(2):
+            a.observe(t)
+            a.step(t, a.act(t))
+        for _ in range(2):
+            a.collect()
+            b.replay()
+            torch.cuda.synchronize()
+            for x, y in ((a.states, b.states), (a.generation, b.generation),
+                         (a.sampler, b.sampler)):
+                assert torch.equal(x, y)
+            for name in ("features", "legal", "action", "logp", "value", "reward", "done"):
+                assert torch.equal(getattr(a.buffer, name), getattr(b.buffer, name)), name
+    assert a.games_completed() > n

@@ -190,6 +190,21 @@ def test_gumbel_sample_matches_reference(ext):
     want_a, want_lp = gumbel_reference(lb.float(), legal, u)
     assert torch.equal(actions, want_a)
     assert float((logp - want_lp).abs().max()) <= 1e-5
+    # other action counts: one lane group short of full (33), the 16-lane form's limit
+    # (192) and beyond it (250, one row per wavefront), at a partial last block
+    for width in (33, 192, 250):
+        lg = torch.randn(1001, width, generator=g, device=DEV)
+        ok = torch.rand(1001, width, generator=g, device=DEV) < 0.2
+        ok[:3] = False
+        un = torch.rand(1001, width, generator=g, device=DEV)
+        un[1, width - 1] = 1.0
+        got_a, got_lp = ext.gumbel_sample(lg, ok, un)
+        want_a, want_lp = gumbel_reference(lg, ok, un)
+        assert torch.equal(got_a, want_a), width
+        assert float((got_lp - want_lp).abs().max()) <= 1e-5, width
+        assert int(got_a[1]) == width - 1
+        greedy = ext.masked_argmax(lg, ok)
+        assert torch.equal(greedy, lg.masked_fill(~ok, -1.0e30).argmax(1)), width
 
 
 def _policy(d=256, layers=4, heads=8, seed=0, mode="hybrid"):
