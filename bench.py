@@ -30,6 +30,7 @@ Also reported (not timed into `value`):
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import os
 import sys
@@ -89,6 +90,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-decode", action="store_true")
     p.add_argument("--no-canonical", action="store_true")
+    p.add_argument("--no-tunable", action="store_true",
+                   help="keep hipBLASLt's own GEMM choice (no TunableOp timing)")
     p.add_argument("--no-rollout", action="store_true")
     p.add_argument("--no-selfplay", action="store_true")
     p.add_argument("--no-redeal", action="store_true")
@@ -685,14 +688,6 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps
 
-    # PyTorch-ROCm's TunableOp times the library's GEMM solutions for each shape on its
-    # first call (the eager warm-up steps of capture(), about 2 s) and keeps the fastest
-    # for the captured graph; its results file goes to the temporary directory.
-    tunable = torch.cuda.tunable
-    tunable.set_filename(os.path.join(os.environ.get("TMPDIR", "/tmp"),
-                                      "cugo_tunableop_results.csv"))
-    tunable.enable(True)
-    tunable.tuning_enable(True)
     with torch.no_grad():
         ro.capture()  # the whole horizon as one HIP graph
         ro.replay()   # first replay outside the timed region
@@ -745,8 +740,6 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         e1.record(stream)
         torch.cuda.synchronize()
         forward_ms = e0.elapsed_time(e1) / 20
-    tunable.tuning_enable(False)
-    tunable.enable(False)
     flops_row = actor.flops_per_row()
     tflops = flops_row * batch / (forward_ms * 1e-3) / 1e12
     engine_bytes = batch * (OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW)
@@ -758,7 +751,6 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
             "actor_share": round(actor_step_ms / step_ms, 4),
             "engine_step_ms": round(engine_step_ms, 4), "actor_step_ms": round(actor_step_ms, 4),
             "hip_graph": "one graph per rollout of horizon steps",
-            "gemm_selection": "PyTorch-ROCm TunableOp",
             "roofline": {"kernel": "actor forward (hipBLASLt GEMMs + HIP add_layernorm)",
                          "bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
                          "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
@@ -819,6 +811,26 @@ def store_ceiling(torch) -> dict:
     del buf
     return {"kernel": "torch fill_, 192 MiB float32", "gbs": round(gbs, 1),
             "avg_launch_ms": round(ms, 4)}
+
+
+@contextlib.contextmanager
+def tuned_gemms(torch, enabled: bool):
+    """PyTorch-ROCm TunableOp for the legs whose eager warm-up runs every GEMM shape they
+    then capture into a HIP graph (self-play, rollout): each shape's first call times the
+    library's solutions (about 2 s in all) and the graph keeps the fastest.  Its results
+    file goes to the temporary directory."""
+    tunable = torch.cuda.tunable
+    if enabled:
+        tunable.set_filename(os.path.join(os.environ.get("TMPDIR", "/tmp"),
+                                          "cugo_tunableop_results.csv"))
+        tunable.enable(True)
+        tunable.tuning_enable(True)
+    try:
+        yield
+    finally:
+        if enabled:
+            tunable.tuning_enable(False)
+            tunable.enable(False)
 
 
 def main() -> None:
@@ -886,7 +898,10 @@ def main() -> None:
                    "batch": args.batch, "seed_base": hex(SEED_BASE),
                    "policy": "uniform legal action, per-game xorshift64",
                    "streams": args.streams, "hip_graph": not args.no_graph,
-                   "spare_slots": SPARE_SLOTS},
+                   "spare_slots": SPARE_SLOTS,
+                   "gemm_selection": ("hipBLASLt heuristics" if args.no_tunable else
+                                      "PyTorch-ROCm TunableOp for the self-play and "
+                                      "rollout legs")},
         "kernel_ms_per_step": (round(rp["play_ms"] / REFILL, 4)
                                if rp["play_ms"] is not None else None),
         "steps_per_s": round(args.batch * args.steps / rp["seconds"], 1),
@@ -903,13 +918,15 @@ def main() -> None:
     if not args.no_decode:
         result["decode"] = decode_workload(ext, torch, args.decode_steps)
     if not args.no_selfplay:
-        result["selfplay"] = selfplay_workload(ext, torch)
+        with tuned_gemms(torch, not args.no_tunable):
+            result["selfplay"] = selfplay_workload(ext, torch)
     if not args.no_redeal:
         result["redeal"] = redeal_workload(ext, torch)
     if not args.no_paired:
         result["paired"] = paired_workload(ext, torch)
     if not args.no_rollout:
-        result["rollout"] = rollout_workload(ext, torch)
+        with tuned_gemms(torch, not args.no_tunable):
+            result["rollout"] = rollout_workload(ext, torch)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)
