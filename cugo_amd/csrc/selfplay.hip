@@ -278,25 +278,40 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
 constexpr int kGumbelLanes = 16;
 constexpr int kGumbelPer = 12;  // up to 192 actions
 
-template <class T>
+template <class T, bool kNoise>
 __global__ __launch_bounds__(256) void gumbel_rows_kernel(
     const typename T::storage* logits, const uint8_t* legal, const float* u, i64 n,
     int actions_count, i64* actions, float* logp) {
   const int j = threadIdx.x & (kGumbelLanes - 1);
   const i64 r = (i64)blockIdx.x * (256 / kGumbelLanes) + (threadIdx.x / kGumbelLanes);
   const bool row_ok = r < n;
-  const typename T::storage* lr = logits + r * actions_count;
-  const uint8_t* gr = legal + r * actions_count;
-  const float* ur = u != nullptr ? u + r * actions_count : nullptr;
+  // Every load is unconditional, at an index clamped into the arrays (a lane past the
+  // last row or action reads an element that exists and ignores it), so all of a lane's
+  // loads are in flight together instead of each waiting on the legal byte before it.
+  const i64 rr = row_ok ? r : n - 1;
+  const typename T::storage* lr = logits + rr * actions_count;
+  const uint8_t* gr = legal + rr * actions_count;
+  const float* ur = kNoise ? u + rr * actions_count : nullptr;
+  uint8_t gb[kGumbelPer];
+  typename T::storage lv[kGumbelPer];
+  float uv[kGumbelPer];
+#pragma unroll
+  for (int k = 0; k < kGumbelPer; ++k) {
+    const int a = j + kGumbelLanes * k;
+    const int ac = a < actions_count ? a : actions_count - 1;
+    gb[k] = gr[ac];
+    lv[k] = lr[ac];
+    uv[k] = kNoise ? ur[ac] : 0.0f;
+  }
   bool ok[kGumbelPer];
   float m[kGumbelPer], uc[kGumbelPer];
 #pragma unroll
   for (int k = 0; k < kGumbelPer; ++k) {
     const int a = j + kGumbelLanes * k;
     const bool in = row_ok && a < actions_count;
-    ok[k] = in && gr[a] != 0;
-    m[k] = ok[k] ? T::to_float(lr[a]) : -1.0e30f;
-    uc[k] = (in && ur != nullptr) ? fminf(fmaxf(ur[a], 1.0e-20f), 1.0f) : 0.0f;
+    ok[k] = in && gb[k] != 0;
+    m[k] = ok[k] ? T::to_float(lv[k]) : -1.0e30f;
+    uc[k] = fminf(fmaxf(uv[k], 1.0e-20f), 1.0f);
   }
   float best = -INFINITY, best_m = -1.0e30f, top = -INFINITY;
   int best_a = 1 << 30;  // above every real index
@@ -307,7 +322,7 @@ __global__ __launch_bounds__(256) void gumbel_rows_kernel(
     if (!row_ok || a >= actions_count) continue;
     any |= ok[k];
     float v = m[k];
-    if (ur != nullptr) {
+    if (kNoise) {
       if (ok[k]) v = m[k] + -logf(-logf(uc[k]));
       else if (uc[k] >= 1.0f) v = INFINITY;
     }
@@ -337,7 +352,7 @@ __global__ __launch_bounds__(256) void gumbel_rows_kernel(
   if (j == 0 && row_ok) {
     const bool found = best_a < actions_count;
     actions[r] = found ? best_a : 0;
-    const float mv = found ? best_m : (gr[0] ? T::to_float(lr[0]) : -1.0e30f);
+    const float mv = found ? best_m : m[0];  // lane 0 holds action 0
     if (logp != nullptr) logp[r] = (mv - top) - logf(sum);
   }
 }
@@ -641,12 +656,14 @@ int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* lega
   const bool f32 = logits_dtype == CUGO_DTYPE_F32;
   if (actions_count <= kGumbelLanes * kGumbelPer) {
     const unsigned grid = (unsigned)((n + 256 / kGumbelLanes - 1) / (256 / kGumbelLanes));
-    if (f32)
-      gumbel_rows_kernel<F32><<<grid, 256, 0, stream>>>(
-          (const float*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
-    else
-      gumbel_rows_kernel<BF16><<<grid, 256, 0, stream>>>(
-          (const uint16_t*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
+#define CUGO_GUMBEL_ROWS(TT, NOISE, PTR)                                                   \
+  gumbel_rows_kernel<TT, NOISE><<<grid, 256, 0, stream>>>(                                  \
+      (PTR)logits, legal, uniforms, n, (int)actions_count, actions, logp)
+    if (f32 && uniforms) CUGO_GUMBEL_ROWS(F32, true, const float*);
+    else if (f32) CUGO_GUMBEL_ROWS(F32, false, const float*);
+    else if (uniforms) CUGO_GUMBEL_ROWS(BF16, true, const uint16_t*);
+    else CUGO_GUMBEL_ROWS(BF16, false, const uint16_t*);
+#undef CUGO_GUMBEL_ROWS
     return (int)hipGetLastError();
   }
   const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
