@@ -36,40 +36,79 @@ __device__ inline int tile_count(i64 base, i64 n) {
 __device__ inline bool valid_id(i64 id, i64 env_count) { return id >= 0 && id < env_count; }
 
 // Loads the tile's rows into LDS with kThreads threads; src row r is `ids[r]` (gathered,
-// zero row when the id is invalid) or base + r (contiguous) when ids_lds is null.
+// zero row when the id is invalid) or base + r (contiguous) when ids_lds is null.  Each
+// thread first loads all of its words into registers, at indices clamped into the rows
+// that exist, and only then writes LDS: loads guarded by a branch, or a store of each
+// load before the next, would each wait out a full memory round trip.
 template <int kThreads = kTile>
 __device__ inline void stage_in(u64* lds, const u64* states, const i64* ids_lds, i64 base,
                                 int count, i64 env_count) {
-  const int words = count * kRowWords;
-  if (ids_lds == nullptr) {
-    const u64* src = states + base * kRowWords;
-    for (int j = threadIdx.x; j < words; j += kThreads) lds[j] = src[j];
-  } else {
-    for (int j = threadIdx.x; j < words; j += kThreads) {
-      const int r = j / kRowWords;
-      const int k = j - r * kRowWords;
-      const i64 id = ids_lds[r];
-      lds[j] = valid_id(id, env_count) ? states[id * kRowWords + k] : 0ull;
+  constexpr int kPer = (kTileWords + kThreads - 1) / kThreads;
+  constexpr int kBatch = kPer < 16 ? kPer : 16;  // words in flight per thread
+  const int words = count * kRowWords;  // count >= 1 in every launched tile
+  const bool gather = ids_lds != nullptr;
+  if (gather && env_count <= 0) {  // no row to read: every id is invalid
+    for (int j = threadIdx.x; j < words; j += kThreads) lds[j] = 0ull;
+    return;
+  }
+  const u64* src = states + base * kRowWords;
+#pragma unroll
+  for (int p0 = 0; p0 < kPer; p0 += kBatch) {
+    u64 v[kBatch];
+    bool ok[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int j0 = threadIdx.x + (p0 + q) * kThreads;
+      const int j = j0 < words ? j0 : words - 1;
+      if (!gather) {
+        ok[q] = true;
+        v[q] = src[j];
+      } else {
+        const int r = j / kRowWords;
+        const int k = j - r * kRowWords;
+        const i64 id = ids_lds[r];
+        ok[q] = valid_id(id, env_count);
+        v[q] = states[(ok[q] ? id : 0) * kRowWords + k];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int j = threadIdx.x + (p0 + q) * kThreads;
+      if (p0 + q < kPer && j < words) lds[j] = ok[q] ? v[q] : 0ull;
     }
   }
 }
 
 // Stores the tile's rows from LDS with kThreads threads: to dst rows base + r
 // (contiguous) or, when ids_lds is given, to rows ids[r] with a valid id (scatter, in
-// place).
+// place).  All of a thread's LDS reads come before its stores.
 template <int kThreads = kTile>
 __device__ inline void stage_out(const u64* lds, u64* dst, const i64* ids_lds, i64 base,
                                  int count, i64 env_count) {
+  constexpr int kPer = (kTileWords + kThreads - 1) / kThreads;
   const int words = count * kRowWords;
+  u64 v[kPer];
+#pragma unroll
+  for (int p = 0; p < kPer; ++p) {
+    const int j = threadIdx.x + p * kThreads;
+    v[p] = lds[j < words ? j : words - 1];
+  }
   if (ids_lds == nullptr) {
     u64* out = dst + base * kRowWords;
-    for (int j = threadIdx.x; j < words; j += kThreads) out[j] = lds[j];
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int j = threadIdx.x + p * kThreads;
+      if (j < words) out[j] = v[p];
+    }
   } else {
-    for (int j = threadIdx.x; j < words; j += kThreads) {
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int j = threadIdx.x + p * kThreads;
+      if (j >= words) continue;
       const int r = j / kRowWords;
       const int k = j - r * kRowWords;
       const i64 id = ids_lds[r];
-      if (valid_id(id, env_count)) dst[id * kRowWords + k] = lds[j];
+      if (valid_id(id, env_count)) dst[id * kRowWords + k] = v[p];
     }
   }
 }
@@ -305,19 +344,8 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
   if (kIndexed && tid < count) tile_ids[tid] = ids[base + tid];
   if (tid == 0) next_item = 0;
   __syncthreads();
-  {  // stage the tile's rows, all threads
-    const int words = count * kRowWords;
-    if (!kIndexed) {
-      const u64* src = states + base * kRowWords;
-      for (int j = tid; j < words; j += kObsThreads) t.rows[j] = src[j];
-    } else {
-      for (int j = tid; j < words; j += kObsThreads) {
-        const int r = j / kRowWords;
-        const i64 id = tile_ids[r];
-        t.rows[j] = valid_id(id, env_count) ? states[id * kRowWords + (j - r * kRowWords)] : 0ull;
-      }
-    }
-  }
+  stage_in<kObsThreads>(t.rows, states, kIndexed ? tile_ids : nullptr, base, count,
+                        env_count);  // all threads
   __syncthreads();
   const bool active = wave == 0 && lane < count;
   const bool ok = active && (!kIndexed || valid_id(tile_ids[lane], env_count));
@@ -566,6 +594,8 @@ void play_kernel(
   const int wave = tid / kTile;
   const i64 i = base + lane;
   if (tid < 2) next_item[tid] = 0;
+  // A plain loop: the rows are read once per launch, and the batched form of stage_in
+  // measured 3-4 % slower here (this kernel's loop runs at its full register budget).
   {
     const u64* src = states + base * kRowWords;
     for (int j = tid; j < count * kRowWords; j += kPlayThreads) t.rows[j] = src[j];
@@ -654,7 +684,10 @@ void play_kernel(
     sampler[i] = xc;
   }
   __syncthreads();
-  stage_out<kPlayThreads>(t.rows, states, nullptr, base, count, 0);
+  {
+    u64* out = states + base * kRowWords;
+    for (int j = tid; j < count * kRowWords; j += kPlayThreads) out[j] = t.rows[j];
+  }
 }
 
 // ---------------------------------------------------------- branch + observe ----
@@ -679,7 +712,12 @@ __global__ __launch_bounds__(kPlayThreads) void branch_observe_kernel(
   if (tid < count) tile_ids[tid] = ids[base + tid];
   if (tid == 0) next_item = 0;
   __syncthreads();
-  stage_in<kPlayThreads>(t.rows, parents, tile_ids, base, count, env_count);
+  // A plain gather loop: the batched form of stage_in measured 3.5 % slower here.
+  for (int j = tid; j < count * kRowWords; j += kPlayThreads) {
+    const int r = j / kRowWords;
+    const i64 id = tile_ids[r];
+    t.rows[j] = valid_id(id, env_count) ? parents[id * kRowWords + (j - r * kRowWords)] : 0ull;
+  }
   __syncthreads();
   const bool active = wave == 0 && lane < count;
   // The clone is unpacked and stepped in one block before the rows are overwritten: an
