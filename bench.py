@@ -79,6 +79,20 @@ def measured_traffic(kernel: str, key: str) -> int | None:
     return None if entry is None else int(entry["bytes"])
 
 
+@contextlib.contextmanager
+def region(name: str):
+    """A ROCTx range named `name` around a timed region (torch.cuda.nvtx is ROCTx on
+    ROCm), so that a `rocprofv3 --marker-trace --kernel-trace` run can attribute the
+    kernels that ran inside it."""
+    import torch
+
+    torch.cuda.nvtx.range_push(name)
+    try:
+        yield
+    finally:
+        torch.cuda.nvtx.range_pop()
+
+
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -182,12 +196,13 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
     # Every finished game bumps its row's generation once.
     start_games = int(gen.sum(dtype=torch.int64).item())
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps // REFILL):
-        full()
-    rest()
-    torch.cuda.synchronize()
-    seconds = time.perf_counter() - t0
+    with region("c2.loop"):
+        t0 = time.perf_counter()
+        for _ in range(steps // REFILL):
+            full()
+        rest()
+        torch.cuda.synchronize()
+        seconds = time.perf_counter() - t0
     games = int(gen.sum(dtype=torch.int64).item()) - start_games
     # Per-kernel durations: launches captured in a HIP graph and replayed between two
     # events on the stream the replay runs on, so the kernels run back to back (issued
@@ -204,50 +219,63 @@ def random_policy(ext, torch, batch: int, steps: int, warmup: int, streams: int,
                 fn()
         return g
 
-    def replay_ms(g, before=None, times: int = 1) -> float:
+    def replay_ms(g, name: str, times: int = 1) -> float:
         total = 0.0
-        for _ in range(times):
-            if before is not None:
-                before()
-            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            ev[0].record(stream)
-            g.replay()
-            ev[1].record(stream)
-            torch.cuda.synchronize()
-            total += ev[0].elapsed_time(ev[1])
+        with region(name):
+            for _ in range(times):
+                ev = (torch.cuda.Event(enable_timing=True),
+                      torch.cuda.Event(enable_timing=True))
+                ev[0].record(stream)
+                g.replay()
+                ev[1].record(stream)
+                torch.cuda.synchronize()
+                total += ev[0].elapsed_time(ev[1])
         return total
 
     # The observe kernel alone on the loop's live (mid-game) states, whole batch:
     # 5 replays of 10 launches.
     obs = graph_of(lambda: ext.observe(states), 10)
-    observe_ms = replay_ms(obs, times=5) / 50
+    observe_ms = replay_ms(obs, "c2.observe", times=5) / 50
     del obs
     # play_random alone (one launch of REFILL steps on the whole batch, as in the loop),
     # continuing the games: 6 back-to-back replays of the loop's block (refill_spares, then
     # the launch) less 6 of refill_spares alone, so that only the first replay's submission
     # falls between the events.
-    play_ms = None
+    play_ms = record_ms = None
     if fused and streams == 1:
         def block_once():
             ext.refill_spares(spares[0], spare_gen[0], gen, SEED_BASE, batch)
             ext.play_random(states, sampler, SEED_BASE, gen, spares[0], spare_gen[0], batch,
                             REFILL)
 
-        def six(g) -> float:
+        def six(g, name: str) -> float:
             ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            ev[0].record(stream)
-            for _ in range(6):
-                g.replay()
-            ev[1].record(stream)
-            torch.cuda.synchronize()
+            with region(name):
+                ev[0].record(stream)
+                for _ in range(6):
+                    g.replay()
+                ev[1].record(stream)
+                torch.cuda.synchronize()
             return ev[0].elapsed_time(ev[1])
+
+        def block_record():
+            ext.refill_spares(spares[0], spare_gen[0], gen, SEED_BASE, batch)
+            ext.play_random(states, sampler, SEED_BASE, gen, spares[0], spare_gen[0], batch,
+                            REFILL, record=True)
 
         blocks = graph_of(block_once, 1)
         refills = graph_of(lambda: ext.refill_spares(spares[0], spare_gen[0], gen, SEED_BASE,
                                                      batch), 1)
-        play_ms = (six(blocks) - six(refills)) / 6
-        del blocks, refills
-    return {"seconds": seconds, "games": games, "observe_ms": observe_ms, "play_ms": play_ms}
+        play_ms = (six(blocks, "c2.play") - six(refills, "c2.refill")) / 6
+        del blocks
+        # The same launch with every step's outputs at their own addresses (record mode:
+        # 6.4 GB of observations a launch, 25x the GPU's 256 MB last-level cache), so no
+        # step's stores can be absorbed by a cache line that the next step overwrites.
+        records = graph_of(block_record, 1)
+        record_ms = (six(records, "c2.play_record") - six(refills, "c2.refill")) / 6
+        del records, refills
+    return {"seconds": seconds, "games": games, "observe_ms": observe_ms, "play_ms": play_ms,
+            "record_ms": record_ms}
 
 
 def mid_game_roots(ext, torch, n: int, base: int):
@@ -320,27 +348,33 @@ def branch_workload(ext, torch, iters: int, cpu_seconds: float | None) -> dict:
     torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     stream = torch.cuda.current_stream()
-    ev[0].record(stream)
-    for _ in range(iters):
-        children = ext.branch_indexed(roots, parent, actions)[0]
-    ev[1].record(stream)
-    for _ in range(iters):
-        ext.observe(children)
-    ev[2].record(stream)
-    torch.cuda.synchronize()
+    with region("c3.branch"):
+        ev[0].record(stream)
+        for _ in range(iters):
+            children = ext.branch_indexed(roots, parent, actions)[0]
+        ev[1].record(stream)
+        torch.cuda.synchronize()
+    ev.append(torch.cuda.Event(enable_timing=True))
+    with region("c3.observe"):
+        ev[3].record(stream)
+        for _ in range(iters):
+            ext.observe(children)
+        ev[2].record(stream)
+        torch.cuda.synchronize()
     branch_ms = ev[0].elapsed_time(ev[1]) / iters
-    observe_ms = ev[1].elapsed_time(ev[2]) / iters
+    observe_ms = ev[3].elapsed_time(ev[2]) / iters
     # the same children branched and observed by one launch (branch_observe_indexed)
     del children
     out = ext.branch_observe_indexed(roots, parent, actions)
     del out
     torch.cuda.synchronize()
-    ev[0].record(stream)
-    for _ in range(iters):
-        out = ext.branch_observe_indexed(roots, parent, actions)
-        del out
-    ev[1].record(stream)
-    torch.cuda.synchronize()
+    with region("c3.branch_observe"):
+        ev[0].record(stream)
+        for _ in range(iters):
+            out = ext.branch_observe_indexed(roots, parent, actions)
+            del out
+        ev[1].record(stream)
+        torch.cuda.synchronize()
     fused_ms = ev[0].elapsed_time(ev[1]) / iters
     n = roots_n * fan
     branch_gbs = n * BRANCH_BYTES_PER_CHILD / (branch_ms * 1e-3) / 1e9
@@ -415,11 +449,12 @@ def canonical_workload(ext, torch, games: int = 131072, iters: int = 8) -> dict:
         ext.rollout_canonical(seeds, first)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(iters):
-            digest = ext.rollout_canonical(seeds, first)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        with region(f"a16.canonical_{n}"):
+            e0.record(stream)
+            for _ in range(iters):
+                digest = ext.rollout_canonical(seeds, first)
+            e1.record(stream)
+            torch.cuda.synchronize()
         return e0.elapsed_time(e1) / iters, digest
 
     ms, digest = timed(games)
@@ -436,6 +471,28 @@ def canonical_workload(ext, torch, games: int = 131072, iters: int = 8) -> dict:
                          "bytes_per_game": 56, "avg_launch_ms": round(ms, 4)}}
 
 
+def decode_lengths(torch, events: "torch.Tensor", slots: int, seed: int) -> dict:
+    """Cache row lengths from per-game event counts `events` [games per row, rows] (game k
+    of row i is seeded game i + rows * k): each game adds its opening token and its events.
+    "stress": games are concatenated until a per-row target drawn uniformly from
+    [1, slots] (torch generator seeded with `seed`) is reached; "full": as many games as
+    fit below `slots` - 1; "natural": one game.  Every length is clamped to `slots` - 2, so
+    that a row can take two more tokens."""
+    total = torch.cumsum(events + 1, 0)
+    cap = slots - 2
+    natural = total[0].clamp_max(cap)
+    gen = torch.Generator(device=events.device).manual_seed(seed)
+    target = torch.randint(1, slots + 1, (events.shape[1],), generator=gen,
+                           device=events.device)
+    reached = total >= target
+    first = torch.where(reached.any(0), reached.int().argmax(0),
+                        torch.full_like(target, events.shape[0] - 1))
+    stress = total.gather(0, first[None]).squeeze(0).clamp_max(cap)
+    full = torch.where(total <= cap, total, torch.zeros_like(total)).max(0).values
+    full = torch.where(full == 0, natural, full)
+    return {"stress": stress, "full": full, "natural": natural}
+
+
 def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) -> dict:
     """Sequence-policy decode: a 4-layer causal transformer (d_model 256, 8 heads of 32,
     GELU MLP 1024, pre-norm, bf16, N(0, 0.02) weights from seed 0) runs one query token
@@ -443,8 +500,9 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
     with the HIP decode attention -> out-projection and MLP GEMMs).  KV cache
     [4, 4,096, 8, 320, 32] bf16.  Row lengths come from seeded random-policy games: row i
     concatenates the event logs of games i, i + 4,096, i + 8,192, ... (one opening token
-    plus each game's events) while they fit below 320 slots ("stress", pos ~300), or holds
-    one game (the reference's 50-slot regime, "natural")."""
+    plus each game's events) until a per-row target drawn uniformly from [1, 320] is
+    reached ("stress", mean pos ~170), or while they fit below 320 slots ("full", pos
+    ~300), or holds one game (the reference's 50-slot regime, "natural")."""
     from torch import nn
 
     from cugo_amd.seq_decode import KVCache, cached_step
@@ -463,13 +521,9 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
             p.normal_(0.0, 0.02)
     model = model.to(dev).to(torch.bfloat16).eval()
 
-    per_row = 16
+    per_row = 24
     ev = event_lengths(ext, torch, rows * per_row, SEED_BASE + 0xDEC0DE).view(per_row, rows)
-    natural = (1 + ev[0]).clamp_max(slots - 1)
-    total = torch.cumsum(ev, 0) + 1  # opening token + events of the first k games
-    fits = total <= slots - 1
-    stress = torch.where(fits, total, torch.zeros_like(total)).max(0).values
-    stress = torch.where(stress == 0, natural, stress)
+    lengths = decode_lengths(torch, ev, slots, seed=0xC5)
 
     cache = KVCache(layers, rows, heads, d, slots, dev)
     gen = torch.Generator(device=dev).manual_seed(1)
@@ -479,29 +533,31 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
     out = {}
     stream = torch.cuda.current_stream()
     with torch.no_grad():
-        for name, lengths in (("stress", stress), ("natural", natural)):
-            cache.length.copy_(lengths)
+        for name in ("stress", "full", "natural"):
+            cache.length.copy_(lengths[name])
             for _ in range(3):
                 cached_step(model, cache, x)
             torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(steps):
-                cached_step(model, cache, x)
-            torch.cuda.synchronize()
-            step_s = (time.perf_counter() - t0) / steps
+            with region(f"c5.step_{name}"):
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    cached_step(model, cache, x)
+                torch.cuda.synchronize()
+                step_s = (time.perf_counter() - t0) / steps
             # The decode kernel alone, same call as inside the step (layer 0's cache).
             q = (torch.randn(rows, heads, dh, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
             kn, vn = q.clone(), q.clone()
-            pos = lengths.clamp_max(slots - 1)
+            pos = lengths[name].clamp_max(slots - 1)
             for _ in range(3):
                 decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos)
             ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             reps = 50
-            ev0.record(stream)
-            for _ in range(reps):
-                decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos)
-            ev1.record(stream)
-            torch.cuda.synchronize()
+            with region(f"c5.decode_{name}"):
+                ev0.record(stream)
+                for _ in range(reps):
+                    decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos)
+                ev1.record(stream)
+                torch.cuda.synchronize()
             kernel_ms = ev0.elapsed_time(ev1) / reps
             # cache reads (slots < pos; slot pos comes from registers) + q, k_new, v_new
             # reads + k/v slot writes + out writes + pos
@@ -546,13 +602,14 @@ def selfplay_workload(ext, torch, wave: int = 4096, waves: int = 3) -> dict:
     seeds, first = make_seeds(wave, 0, dev)
     sp.play(seeds, first, learner)  # capture + one warm wave
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    steps = 0
-    for k in range(waves):
-        seeds, first = make_seeds(wave, (k + 1) * wave, dev)
-        steps += sp.play(seeds, first, learner)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with region("f1.selfplay"):
+        t0 = time.perf_counter()
+        steps = 0
+        for k in range(waves):
+            seeds, first = make_seeds(wave, (k + 1) * wave, dev)
+            steps += sp.play(seeds, first, learner)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     # one step: graph replay vs eager, same state
     reps = 16
     sp.reset(seeds, first, learner)
@@ -591,11 +648,12 @@ def redeal_workload(ext, torch, rows: int = 4096, worlds: int = 8) -> dict:
     redeal_worlds(ext, roots, env_rows, players, worlds)
     torch.cuda.synchronize()
     reps = 5
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        out = redeal_worlds(ext, roots, env_rows, players, worlds)
-    torch.cuda.synchronize()
-    worlds_s = (time.perf_counter() - t0) / reps
+    with region("f3.redeal_worlds"):
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            out = redeal_worlds(ext, roots, env_rows, players, worlds)
+        torch.cuda.synchronize()
+        worlds_s = (time.perf_counter() - t0) / reps
     copies = roots.repeat(worlds, 1)
     seats = players.repeat(worlds)
     keys = torch.rand(copies.shape[0], 50, device=dev)
@@ -603,11 +661,12 @@ def redeal_workload(ext, torch, rows: int = 4096, worlds: int = 8) -> dict:
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ext.redeal(copies, seats, keys, rng)
-    e0.record(stream)
-    for _ in range(20):
-        ext.redeal(copies, seats, keys, rng)
-    e1.record(stream)
-    torch.cuda.synchronize()
+    with region("f3.redeal_kernel"):
+        e0.record(stream)
+        for _ in range(20):
+            ext.redeal(copies, seats, keys, rng)
+        e1.record(stream)
+        torch.cuda.synchronize()
     kernel_ms = e0.elapsed_time(e1) / 20
     changed = float((out.view(torch.int64)[:, 3] != roots.repeat(worlds, 1).view(torch.int64)[:, 3])
                     .float().mean())
@@ -648,7 +707,9 @@ def paired_workload(ext, torch, pairs: int = 4096) -> dict:
 
     a, b = actor(1), actor(2)
     evaluate_paired(ext, a, b, 256, seed_offset=0, max_steps=128, use_amp=True)  # warm
-    s = evaluate_paired(ext, a, b, pairs, seed_offset=1 << 20, max_steps=128, use_amp=True)
+    with region("f4.paired"):
+        s = evaluate_paired(ext, a, b, pairs, seed_offset=1 << 20, max_steps=128,
+                            use_amp=True)
     return {"games_per_s": round(s.games / s.seconds, 1), "seconds": round(s.seconds, 4),
             "decision_steps": s.decision_steps, "pairs": pairs,
             "mean_pair_score_a": round(s.mean_pair_score_a, 4)}
@@ -679,13 +740,14 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
     ro = MlpRollout(ext, actor, batch, horizon, SEED_BASE + 0xC4, generator=gen)
     stream = torch.cuda.current_stream()
 
-    def graph_ms(g, reps: int) -> float:
+    def graph_ms(g, reps: int, name: str) -> float:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            g.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
+        with region(name):
+            e0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps
 
     with torch.no_grad():
@@ -694,11 +756,12 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         torch.cuda.synchronize()
         games0 = ro.games_completed()
         reps = 2
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            ro.replay()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
+        with region("c4.rollout"):
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                ro.replay()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
         games = ro.games_completed() - games0
         step_ms = wall * 1e3 / (reps * horizon)
         # The engine's share: its launches alone (observe with the random policy's draw,
@@ -719,7 +782,7 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         eg = torch.cuda.CUDAGraph()
         with torch.cuda.graph(eg):
             engine_block()
-        engine_step_ms = graph_ms(eg, 3) / 32
+        engine_step_ms = graph_ms(eg, 3, "c4.engine") / 32
         del eg
         ro.observe(0)
         ro.act(0)
@@ -728,17 +791,18 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         ag.register_generator_state(gen)
         with torch.cuda.graph(ag):
             ro.act(0)
-        actor_step_ms = graph_ms(ag, 10)
+        actor_step_ms = graph_ms(ag, 10, "c4.actor")
         del ag
         # the forward pass alone, 20 back-to-back passes on the last step's input
         x = ro.buffer.features[horizon - 1]
         fused_forward(ext, actor, x)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(20):
-            fused_forward(ext, actor, x)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        with region("c4.forward"):
+            e0.record(stream)
+            for _ in range(20):
+                fused_forward(ext, actor, x)
+            e1.record(stream)
+            torch.cuda.synchronize()
         forward_ms = e0.elapsed_time(e1) / 20
     flops_row = actor.flops_per_row()
     tflops = flops_row * batch / (forward_ms * 1e-3) / 1e12
@@ -874,7 +938,11 @@ def main() -> None:
                     "bytes_per_row": play_bytes, "steps_per_launch": REFILL,
                     "avg_launch_ms": round(rp["play_ms"], 4),
                     "ms_per_step": round(rp["play_ms"] / REFILL, 4),
-                    "frac_of_store_ceiling": round(play_gbs / ceiling["gbs"], 4)}
+                    "frac_of_store_ceiling": round(play_gbs / ceiling["gbs"], 4),
+                    # the same launch writing each step's outputs to distinct addresses
+                    "record_avg_launch_ms": round(rp["record_ms"], 4),
+                    "record_achieved": round(args.batch * play_bytes
+                                             / (rp["record_ms"] * 1e-3) / 1e9, 2)}
     else:
         roofline = observe_roofline
     result = {

@@ -293,30 +293,28 @@ def _event_counts(ext, games: int, base: int) -> torch.Tensor:
     raise AssertionError("random-policy games did not finish")
 
 
-@pytest.mark.parametrize("lengths", ["stress", "natural"])
+@pytest.mark.parametrize("lengths", ["stress", "full", "natural"])
 def test_cached_step_full_cache_with_game_lengths(ext, lengths):
     """The sequence policy's step at its full cache shape: 4 layers, d 256, 8 heads of 32,
-    cache [4, 4,096, 8, 320, 32] bf16.  Row lengths come from seeded random-policy games:
-    "stress" concatenates consecutive games' event logs (one opening token plus each
-    game's events) while they fit below 320 slots, "natural" holds one game.  Two steps
-    of the fused HIP step against the reference formulation (index_put_ + the matmul
-    decode path, oracle/seq_ref.py) on identical caches: hidden states within 1e-2
-    relative, and the appended key/value slots within 1e-2."""
+    cache [4, 4,096, 8, 320, 32] bf16.  Row lengths come from seeded random-policy games,
+    as the bench draws them (bench.decode_lengths): "stress" concatenates consecutive
+    games' token logs (each game's opening token and events) until a per-row target
+    uniform in [1, 320] is reached, "full" while they fit below 320 slots, "natural"
+    holds one game.  Two steps of the fused HIP step against the reference formulation
+    (index_put_ + the matmul decode path, oracle/seq_ref.py) on identical caches: hidden
+    states within 1e-2 relative, and the appended key/value slots within 1e-2."""
+    from bench import decode_lengths
     from cugo_amd.seq_decode import KVCache, cached_step
     from oracle.seq_ref import reference_cached_step
 
     announce(f"cached_step full cache [4, 4096, 8, 320, 32], {lengths} lengths")
-    rows, slots, per_row = 4096, 320, 16
+    rows, slots, per_row = 4096, 320, 24
     ev = _event_counts(ext, rows * per_row, 0x243F6A8885A308D3 + 0xDEC0DE).view(per_row, rows)
-    if lengths == "natural":
-        length = (1 + ev[0]).clamp_max(slots - 1)
-    else:
-        total = torch.cumsum(ev, 0) + 1
-        length = torch.where(total <= slots - 2, total, torch.zeros_like(total)).max(0).values
-        length = torch.where(length == 0, (1 + ev[0]).clamp_max(slots - 2), length)
+    length = decode_lengths(torch, ev, slots, seed=0xC5)[lengths]
     assert int(length.max()) <= slots - 2 and int(length.min()) >= 1
     mean = float(length.float().mean())
-    assert (mean > 250) if lengths == "stress" else (10 < mean < 40), mean
+    expect = {"stress": (140, 200), "full": (250, 318), "natural": (10, 40)}[lengths]
+    assert expect[0] < mean < expect[1], mean
     model = _layered_model()
     ca = KVCache(4, rows, 8, 256, slots, torch.device(DEV))
     cb = KVCache(4, rows, 8, 256, slots, torch.device(DEV))
