@@ -394,10 +394,10 @@ def branch_workload(ext, torch, iters: int, cpu_seconds: float | None) -> dict:
         # branch_indexed: 8 (id) + 8 (action) + 248 (child) + 9 (step outputs) B a child,
         # the parents read from L2.  branch_observe_indexed: that plus the child's
         # observation (2,880 + 179 + 1 + 1 + 2 B) and no child read-back.
-        "roofline": {"kernel": "step_kernel<2> (branch_indexed)", "bound": "hbm",
+        "roofline": {"kernel": "branch_kernel (branch_indexed)", "bound": "hbm",
                      "achieved": round(branch_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(branch_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("branch_step_kernel", str(n)),
+                     "traffic": measured_traffic("branch_kernel", str(n)),
                      "bytes_per_child": BRANCH_BYTES_PER_CHILD,
                      "avg_launch_ms": round(branch_ms, 4)},
         "observe_roofline": {"kernel": "branch_observe_kernel (branch_observe_indexed)",
@@ -467,7 +467,8 @@ def canonical_workload(ext, torch, games: int = 131072, iters: int = 8) -> dict:
             "launch_ms_8x": round(big_ms, 4),
             "roofline": {"kernel": "canonical_kernel", "bound": "hbm", "achieved": round(gbs, 2),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None,
+                         "frac": round(gbs / HBM_PEAK_GBS, 6),
+                         "traffic": measured_traffic("canonical_kernel", str(games)),
                          "bytes_per_game": 56, "avg_launch_ms": round(ms, 4)}}
 
 
@@ -715,6 +716,17 @@ def paired_workload(ext, torch, pairs: int = 4096) -> dict:
             "mean_pair_score_a": round(s.mean_pair_score_a, 4)}
 
 
+def engine_traffic(batch: int) -> int | None:
+    """HBM bytes of one engine step of the rollout (observe with the draw, step with
+    auto-reset, and a 32nd of the spares' refill) from the committed counter summary."""
+    parts = [measured_traffic("observe_sample_kernel", str(batch)),
+             measured_traffic("step_reset_spares_kernel", str(batch)),
+             measured_traffic("refill_kernel", str(batch))]
+    if None in parts:
+        return None
+    return parts[0] + parts[1] + parts[2] // 32
+
+
 def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict:
     """MLP PPO self-play rollout (cugo_amd/rollout.py): B games, a residual MLP actor
     (720 features -> Linear 512 -> 3 blocks of h + Linear(ReLU(Linear(LayerNorm(h)))) ->
@@ -823,7 +835,8 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
             "engine_roofline": {"kernel": "observe + step_reset_spares (+ refill_spares)",
                                 "bound": "hbm", "achieved": round(engine_gbs, 2),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                "frac": round(engine_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                                "frac": round(engine_gbs / HBM_PEAK_GBS, 4),
+                                "traffic": engine_traffic(batch),
                                 "bytes_per_row_step": OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW,
                                 "ms_per_step": round(engine_step_ms, 4)},
             "games_completed": games,
@@ -855,26 +868,34 @@ def cpu_baseline(seconds: float) -> dict:
 
 def store_ceiling(torch) -> dict:
     """What plain stores reach on this GPU: torch's fill_ of a 192 MiB float32 tensor (about
-    the bytes of one observation step at B = 65,536), 20 launches timed with events.  The
-    observation kernels are store-bound, so this is their practical ceiling below the
-    published 8 TB/s."""
-    buf = torch.empty(48 << 20, dtype=torch.float32, device="cuda")
-    for _ in range(3):
-        buf.fill_(1.0)
-    torch.cuda.synchronize()
+    the bytes of one observation step at B = 65,536; it fits in the GPU's 256 MB last-level
+    cache, as the loop's output buffers do) and of a 4 GiB one (every byte has to reach
+    DRAM), 20 launches each timed with events.  The observation kernels are store-bound, so
+    these are their practical ceilings below the published 8 TB/s."""
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 20
-    e0.record(stream)
-    for _ in range(reps):
-        buf.fill_(1.0)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    gbs = buf.numel() * 4 / (ms * 1e-3) / 1e9
-    del buf
+
+    def fill_gbs(numel: int) -> tuple[float, float]:
+        buf = torch.empty(numel, dtype=torch.float32, device="cuda")
+        for _ in range(3):
+            buf.fill_(1.0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        with region("ceiling.fill"):
+            e0.record(stream)
+            for _ in range(reps):
+                buf.fill_(1.0)
+            e1.record(stream)
+            torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        del buf
+        return numel * 4 / (ms * 1e-3) / 1e9, ms
+
+    gbs, ms = fill_gbs(48 << 20)
+    large_gbs, large_ms = fill_gbs(1 << 30)
     return {"kernel": "torch fill_, 192 MiB float32", "gbs": round(gbs, 1),
-            "avg_launch_ms": round(ms, 4)}
+            "avg_launch_ms": round(ms, 4), "large_fill_gbs": round(large_gbs, 1),
+            "large_fill": "torch fill_, 4 GiB float32", "large_fill_ms": round(large_ms, 4)}
 
 
 @contextlib.contextmanager
@@ -942,7 +963,10 @@ def main() -> None:
                     # the same launch writing each step's outputs to distinct addresses
                     "record_avg_launch_ms": round(rp["record_ms"], 4),
                     "record_achieved": round(args.batch * play_bytes
-                                             / (rp["record_ms"] * 1e-3) / 1e9, 2)}
+                                             / (rp["record_ms"] * 1e-3) / 1e9, 2),
+                    "record_frac_of_large_fill": round(
+                        args.batch * play_bytes / (rp["record_ms"] * 1e-3) / 1e9
+                        / ceiling["large_fill_gbs"], 4)}
     else:
         roofline = observe_roofline
     result = {
