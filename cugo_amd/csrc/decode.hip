@@ -12,9 +12,11 @@
 // of dh elements once, and does ~2 flops per byte.  Layout of the work:
 //   * a 64-lane wavefront serves G consecutive heads of one query (64 / G lanes each):
 //     up to 8, so the wavefront count drops by G and each wavefront keeps its heads'
-//     loads in flight together (pick_group); a
-//     256-thread workgroup holds four wavefronts, which for heads % (4 G) == 0 share the
-//     query and so the sequence length;
+//     loads in flight together (pick_group);
+//   * P wavefronts serve one such group, each taking every P-th chunk of the row's slots,
+//     and merge their partial softmaxes through LDS (pick: split_rows): P = 1 on short
+//     caches, 2 on long ones, so that long ragged rows do not end a launch alone;
+//     a 256-thread workgroup holds four wavefronts (4 / P groups);
 //   * a slot row of dh elements is split into 16-byte parts; L = dh*elem/16 lanes hold
 //     one slot and a head's lanes cover S = 64/(G L) consecutive slots per load
 //     instruction (1 KiB of contiguous cache per instruction at G = 1);
@@ -23,7 +25,8 @@
 //     reduced over the L lanes of a slot;
 //   * softmax is online (running max / sum per lane group, base-2 exponentials with
 //     log2(e) folded into the scale) and the S lane groups merge their partial
-//     (max, sum, accumulator) triples with a log-sum-exp butterfly at the end.
+//     (max, sum, accumulator) triples with a log-sum-exp butterfly at the end; then
+//     the P parts' triples merge the same way.
 // CUGO_DECODE_FORCE_GROUP (a compile-time define) pins G for tuning builds.
 // Arithmetic is fp32 throughout, output rounded to the query's dtype (as the Triton
 // kernel does, cugo_seq_attention50.py:31-40).
@@ -98,11 +101,69 @@ __device__ inline float reduce_lanes(float s) {
   return s;
 }
 
-// G (query, head) pairs per wavefront, consecutive heads of one query: W = 64 / G lanes
-// per head.  G = 1 streams long rows (16 slots of dh = 32 bf16 per load per head); a larger
-// G serves short rows (a 50-slot cache) with fewer wavefronts, each issuing the loads of
-// all its heads at once.
-template <class QT, class KT, int DH, bool APPEND, int G, int U = kUnroll>
+// Online softmax state of one lane: running maximum (base 2), sum and accumulator.
+template <int E>
+struct Partial {
+  float m, l, acc[E];
+};
+
+// Folds `U` loaded key/value rows (scores already scaled, -inf where masked) into `st`.
+template <class KT, int E, int L, int U>
+__device__ inline void fold_chunk(Partial<E>& st, const float (&qv)[E], const uint4 (&kr)[U],
+                                  const uint4 (&vr)[U], const bool (&valid)[U],
+                                  float scale_log2) {
+  float s[U];
+  float mx = kNegInf;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float kf[E];
+    KT::unpack(kr[u], kf);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) d = __builtin_fmaf(qv[e], kf[e], d);
+    // every lane takes part in the shuffles, valid or not
+    const float r = reduce_lanes<L>(d) * scale_log2;
+    s[u] = valid[u] ? r : kNegInf;
+    mx = fmaxf(mx, s[u]);
+  }
+  const float mn = fmaxf(st.m, mx);
+  const float alpha = rescale(st.m, mn);
+  st.l *= alpha;
+#pragma unroll
+  for (int e = 0; e < E; ++e) st.acc[e] *= alpha;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const float p = valid[u] ? exp2_fast(s[u] - mn) : 0.f;
+    st.l += p;
+    float vf[E];
+    KT::unpack(vr[u], vf);
+#pragma unroll
+    for (int e = 0; e < E; ++e) st.acc[e] = __builtin_fmaf(p, vf[e], st.acc[e]);
+  }
+  st.m = mn;
+}
+
+// a <- a merged with (mo, lo, ao): the log-sum-exp combination of two partial softmaxes.
+template <int E>
+__device__ inline void merge(Partial<E>& a, float mo, float lo, const float (&ao)[E]) {
+  const float mn = fmaxf(a.m, mo);
+  const float x = rescale(a.m, mn);
+  const float y = rescale(mo, mn);
+  a.l = a.l * x + lo * y;
+#pragma unroll
+  for (int e = 0; e < E; ++e) a.acc[e] = a.acc[e] * x + ao[e] * y;
+  a.m = mn;
+}
+
+// G (query, head) pairs per group, consecutive heads of one query: W = 64 / G lanes per
+// head.  G = 1 streams long rows (16 slots of dh = 32 bf16 per load per head); a larger G
+// serves short rows with fewer wavefronts, each issuing the loads of all its heads at once.
+// P wavefronts of a workgroup serve one group: wavefront p takes the slot chunks p, p + P,
+// p + 2P, ... of the group's row, and the P partial softmaxes merge through LDS.  With P = 1
+// a wavefront's work is its row's length, so on ragged rows the longest rows end the launch
+// with few loads in flight; with P > 1 a row's chunks spread over P wavefronts and a launch
+// holds P times as many, which the dispatcher starts as others finish.
+template <class QT, class KT, int DH, bool APPEND, int G, int P, int U = kUnroll>
 __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     const typename QT::storage* __restrict__ q, typename KT::storage* __restrict__ keys,
     typename KT::storage* __restrict__ values, const typename KT::storage* __restrict__ k_new,
@@ -115,182 +176,166 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
   constexpr int L = DH / E;                // lanes per slot
   constexpr int W = 64 / G;                // lanes per head
   constexpr int S = W / L;                 // slots per wavefront load, per head
+  constexpr int CH = S * U;                // slots per chunk (U loads)
   static_assert(DH % E == 0 && L >= 1 && L <= 64 && (L & (L - 1)) == 0, "unsupported dh");
   static_assert(G >= 1 && (G & (G - 1)) == 0 && W % L == 0 && S >= 1, "unsupported grouping");
+  static_assert(P >= 1 && kWaves % P == 0, "parts must divide the workgroup's wavefronts");
 
   const int lane = threadIdx.x & 63;
-  const int64_t group = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (group >= groups) return;  // uniform over the wavefront
-  const int64_t pair0 = group * G;
-  const int64_t query = pair0 / heads;
-  const int64_t pair = pair0 + lane / W;
-  const int head = (int)(pair - query * heads);
+  const int wave = threadIdx.x >> 6;
+  const int part = wave % P;
+  const int64_t group = (int64_t)blockIdx.x * (kWaves / P) + wave / P;
   const int sub = lane % L;         // which 16-byte part of a slot row
   const int srow = (lane % W) / L;  // which slot of a load
-  const int64_t row = rows ? rows[query] : query;
-  int64_t pos = pos_in[query];
-  typename QT::storage* o = out + pair * DH + sub * E;
-
-  if (row < 0 || row >= cache_rows || pos < 0) {
-    // No slot to attend (the reference's softmax over an all -inf row is NaN) or a row
-    // outside the cache: the output is NaN and nothing is read or written.
-    if (srow == 0) {
+  // Every wavefront runs to the end of the kernel (P > 1 merges after a barrier); `live`
+  // says whether this group attends, `nan_out` whether it writes NaN instead.
+  bool live = false, nan_out = false;
+  Partial<E> st;
+  st.m = kNegInf;
+  st.l = 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) o[e] = QT::from_float(__builtin_nanf(""));
+  for (int e = 0; e < E; ++e) st.acc[e] = 0.f;
+  int64_t pair = 0;
+  if (group < groups) {  // uniform over the wavefront (and over the group's P wavefronts)
+    const int64_t pair0 = group * G;
+    const int64_t query = pair0 / heads;
+    pair = pair0 + lane / W;
+    const int head = (int)(pair - query * heads);
+    const int64_t row = rows ? rows[query] : query;
+    int64_t pos = pos_in[query];
+    if (row < 0 || row >= cache_rows || pos < 0) {
+      // No slot to attend (the reference's softmax over an all -inf row is NaN) or a row
+      // outside the cache: the output is NaN and nothing is read or written.
+      nan_out = true;
+    } else {
+      live = true;
+      if (pos >= slots) pos = slots - 1;
     }
-    return;
-  }
-  if (pos >= slots) pos = slots - 1;
+    // A part whose first chunk lies past the row's cached slots (and that does not append)
+    // has nothing to attend: it only takes part in the merge, with an empty state.
+    const int64_t cached = APPEND ? pos : pos + 1;
+    if (live && ((int64_t)part * CH < cached || (APPEND && part == 0))) {
+      const size_t base = ((size_t)row * heads + head) * (size_t)slots * DH + sub * E;
+      const KS* kb = keys + base;
+      const KS* vb = values + base;
+      float qv[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        qv[e] = QT::to_float(q[query * q_stride + head * DH + sub * E + e]);
 
-  const size_t base = ((size_t)row * heads + head) * (size_t)slots * DH + sub * E;
-  const KS* kb = keys + base;
-  const KS* vb = values + base;
+      const int64_t limit = cached;  // cache slots read: [0, limit)
+      if constexpr (APPEND) {
+        // The new key/value goes to slot `pos` (cugo_seq50.py:317-318) and is attended from
+        // registers by part 0; the cache loop reads slots [0, pos).
+        if (part == 0) {
+          const int64_t at = query * new_stride + head * DH + sub * E;
+          const uint4 kn = *reinterpret_cast<const uint4*>(k_new + at);
+          const uint4 vn = *reinterpret_cast<const uint4*>(v_new + at);
+          if (srow == 0) {
+            *reinterpret_cast<uint4*>(keys + base + (size_t)pos * DH) = kn;
+            *reinterpret_cast<uint4*>(values + base + (size_t)pos * DH) = vn;
+          }
+          float kf[E], vf[E];
+          KT::unpack(kn, kf);
+          KT::unpack(vn, vf);
+          float s = 0.f;
+#pragma unroll
+          for (int e = 0; e < E; ++e) s = __builtin_fmaf(qv[e], kf[e], s);
+          s = reduce_lanes<L>(s) * scale_log2;
+          if (srow == 0) {
+            st.m = s;
+            st.l = 1.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) st.acc[e] = vf[e];
+          }
+        }
+      }
 
-  float qv[E];
+      int64_t c = (int64_t)part * CH;
+      // Full chunks: U loads of S slots each, every slot valid.
+      for (; c + CH <= limit; c += (int64_t)P * CH) {
+        uint4 kr[U], vr[U];
+        bool valid[U];
 #pragma unroll
-  for (int e = 0; e < E; ++e) qv[e] = QT::to_float(q[query * q_stride + head * DH + sub * E + e]);
+        for (int u = 0; u < U; ++u) {
+          const size_t off = (size_t)(c + u * S + srow) * DH;
+          kr[u] = *reinterpret_cast<const uint4*>(kb + off);
+          vr[u] = *reinterpret_cast<const uint4*>(vb + off);
+          valid[u] = true;
+        }
+        fold_chunk<KT, E, L, U>(st, qv, kr, vr, valid, scale_log2);
+      }
+      // The row's last, partial chunk (at most one, on one part): one masked set of U
+      // loads (slots >= limit skipped), so a short row costs one round trip to memory
+      // rather than one per S slots.
+      if (c < limit) {
+        uint4 kr[U], vr[U];
+        bool valid[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t slot = c + u * S + srow;
+          valid[u] = slot < limit;  // uniform over a slot's L lanes
+          kr[u] = make_uint4(0, 0, 0, 0);
+          vr[u] = make_uint4(0, 0, 0, 0);
+          if (valid[u]) {
+            kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)slot * DH);
+            vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)slot * DH);
+          }
+        }
+        fold_chunk<KT, E, L, U>(st, qv, kr, vr, valid, scale_log2);
+      }
 
-  float m = kNegInf, l = 0.f, acc[E];
+      // Merge the S slot groups of each head (lanes with the same `sub`): log-sum-exp
+      // butterfly inside the head's W lanes.
 #pragma unroll
-  for (int e = 0; e < E; ++e) acc[e] = 0.f;
-
-  int64_t limit = pos + 1;  // cache slots read: [0, limit)
-  if constexpr (APPEND) {
-    // The new key/value goes to slot `pos` (cugo_seq50.py:317-318) and is attended from
-    // registers; the cache loop reads slots [0, pos).
-    limit = pos;
-    const int64_t at = query * new_stride + head * DH + sub * E;
-    const uint4 kn = *reinterpret_cast<const uint4*>(k_new + at);
-    const uint4 vn = *reinterpret_cast<const uint4*>(v_new + at);
-    if (srow == 0) {
-      *reinterpret_cast<uint4*>(keys + base + (size_t)pos * DH) = kn;
-      *reinterpret_cast<uint4*>(values + base + (size_t)pos * DH) = vn;
-    }
-    float kf[E], vf[E];
-    KT::unpack(kn, kf);
-    KT::unpack(vn, vf);
-    float s = 0.f;
+      for (int off = L; off < W; off <<= 1) {
+        const float mo = __shfl_xor(st.m, off, 64);
+        const float lo = __shfl_xor(st.l, off, 64);
+        float ao[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) s = __builtin_fmaf(qv[e], kf[e], s);
-    s = reduce_lanes<L>(s) * scale_log2;
-    if (srow == 0) {
-      m = s;
-      l = 1.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] = vf[e];
-    }
-  }
-
-  int64_t c = 0;
-  // Full chunks: U loads of S slots each, every slot valid.
-  for (; c + (int64_t)S * U <= limit; c += (int64_t)S * U) {
-    uint4 kr[U], vr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const size_t off = (size_t)(c + u * S + srow) * DH;
-      kr[u] = *reinterpret_cast<const uint4*>(kb + off);
-      vr[u] = *reinterpret_cast<const uint4*>(vb + off);
-    }
-    float s[U];
-    float mx = kNegInf;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float kf[E];
-      KT::unpack(kr[u], kf);
-      float d = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) d = __builtin_fmaf(qv[e], kf[e], d);
-      s[u] = reduce_lanes<L>(d) * scale_log2;
-      mx = fmaxf(mx, s[u]);
-    }
-    const float mn = fmaxf(m, mx);
-    const float alpha = rescale(m, mn);
-    l *= alpha;
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] *= alpha;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float p = exp2_fast(s[u] - mn);
-      l += p;
-      float vf[E];
-      KT::unpack(vr[u], vf);
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e]);
-    }
-    m = mn;
-  }
-  // Tail: one masked chunk of U loads (slots >= limit skipped), so a short row costs one
-  // round trip to memory rather than one per S slots.
-  if (c < limit) {
-    uint4 kr[U], vr[U];
-    bool valid[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t slot = c + u * S + srow;
-      valid[u] = slot < limit;  // uniform over a slot's L lanes
-      kr[u] = make_uint4(0, 0, 0, 0);
-      vr[u] = make_uint4(0, 0, 0, 0);
-      if (valid[u]) {
-        kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)slot * DH);
-        vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)slot * DH);
+        for (int e = 0; e < E; ++e) ao[e] = __shfl_xor(st.acc[e], off, 64);
+        merge<E>(st, mo, lo, ao);
       }
     }
-    float s[U];
-    float mx = kNegInf;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float kf[E];
-      KT::unpack(kr[u], kf);
-      float d = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) d = __builtin_fmaf(qv[e], kf[e], d);
-      // every lane takes part in the shuffles, valid or not
-      const float r = reduce_lanes<L>(d) * scale_log2;
-      s[u] = valid[u] ? r : kNegInf;
-      mx = fmaxf(mx, s[u]);
-    }
-    const float mn = fmaxf(m, mx);
-    const float alpha = rescale(m, mn);
-    l *= alpha;
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] *= alpha;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float p = valid[u] ? exp2_fast(s[u] - mn) : 0.f;
-      l += p;
-      float vf[E];
-      KT::unpack(vr[u], vf);
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] = __builtin_fmaf(p, vf[e], acc[e]);
-    }
-    m = mn;
   }
-
-  // Merge the S slot groups of each head (lanes with the same `sub`): log-sum-exp
-  // butterfly inside the head's W lanes.
+  if constexpr (P > 1) {
+    // Lanes with srow == 0 hold their head's state for one 16-byte part; parts 1..P-1
+    // hand theirs to part 0 through LDS.
+    __shared__ float shared_state[kWaves][G * L][E + 2];
+    const int slot_idx = (lane / W) * L + sub;
+    if (live && part != 0 && srow == 0) {
+      float* d = shared_state[wave][slot_idx];
+      d[0] = st.m;
+      d[1] = st.l;
 #pragma unroll
-  for (int off = L; off < W; off <<= 1) {
-    const float mo = __shfl_xor(m, off, 64);
-    const float lo = __shfl_xor(l, off, 64);
-    const float mn = fmaxf(m, mo);
-    const float a = rescale(m, mn);
-    const float b = rescale(mo, mn);
-    l = l * a + lo * b;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float ao = __shfl_xor(acc[e], off, 64);
-      acc[e] = acc[e] * a + ao * b;
+      for (int e = 0; e < E; ++e) d[2 + e] = st.acc[e];
     }
-    m = mn;
-  }
-  if (srow == 0) {
-    const float inv = 1.f / l;
+    __syncthreads();
+    if (live && part == 0 && srow == 0) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) o[e] = QT::from_float(acc[e] * inv);
+      for (int p = 1; p < P; ++p) {
+        const float* d = shared_state[wave + p][slot_idx];
+        float ao[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) ao[e] = d[2 + e];
+        merge<E>(st, d[0], d[1], ao);
+      }
+    }
+  }
+  if (part == 0 && srow == 0 && (live || nan_out)) {
+    typename QT::storage* o = out + pair * DH + sub * E;
+    if (nan_out) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = QT::from_float(__builtin_nanf(""));
+    } else {
+      const float inv = 1.f / st.l;
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = QT::from_float(st.acc[e] * inv);
+    }
   }
 }
 
-template <class QT, class KT, int DH, bool APPEND, int G>
+template <class QT, class KT, int DH, bool APPEND, int G, int P>
 int launch_group(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
                  const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
                  int64_t slots, int64_t cache_rows, float scale, int64_t q_stride,
@@ -298,15 +343,46 @@ int launch_group(const void* q, void* keys, void* values, const void* k_new, con
   using QS = typename QT::storage;
   using KS = typename KT::storage;
   const int64_t groups = n * heads / G;
-  const int64_t blocks = (groups + kWaves - 1) / kWaves;
+  constexpr int kGroupsPerBlock = kWaves / P;
+  const int64_t blocks = (groups + kGroupsPerBlock - 1) / kGroupsPerBlock;
   const float scale_log2 = scale * 1.4426950408889634f;  // softmax in base 2
-  hipLaunchKernelGGL((decode_kernel<QT, KT, DH, APPEND, G>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((decode_kernel<QT, KT, DH, APPEND, G, P>), dim3((unsigned)blocks),
                      dim3(64 * kWaves), 0, stream, static_cast<const QS*>(q),
                      static_cast<KS*>(keys), static_cast<KS*>(values),
                      static_cast<const KS*>(k_new), static_cast<const KS*>(v_new), pos, rows,
                      static_cast<QS*>(out), groups, (int)heads, slots, cache_rows, scale_log2,
                      q_stride, new_stride);
   return (int)hipGetLastError();
+}
+
+// Wavefronts per group: P = 2 for caches longer than 64 slots, whose rows may be long and
+// ragged, 1 otherwise.  Measured on MI355X at 4,096 queries x 8 heads on a 320-slot cache
+// (rows from seeded games; ms per launch for P = 1 / 2 / 4): rows up to a uniform target in
+// [1, 320] 0.156 / 0.150 / 0.143, rows filled to ~308 slots 0.241 / 0.233 / 0.232, one
+// game a row (~20 slots) 0.0185 / 0.0178 / 0.0212.  Four parts quadruple the wavefronts,
+// which short rows pay for in dispatch rounds; two parts are faster on all three.
+// CUGO_DECODE_FORCE_PARTS (a compile-time define) pins P for tuning builds.
+inline bool split_rows(int64_t slots) { return slots > 64; }
+
+template <class QT, class KT, int DH, bool APPEND, int G>
+int launch_parts(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
+                 const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
+                 int64_t slots, int64_t cache_rows, float scale, int64_t q_stride,
+                 int64_t new_stride, hipStream_t stream) {
+#ifdef CUGO_DECODE_FORCE_PARTS
+  (void)split_rows;
+  return launch_group<QT, KT, DH, APPEND, G, CUGO_DECODE_FORCE_PARTS>(
+      q, keys, values, k_new, v_new, pos, rows, out, n, heads, slots, cache_rows, scale,
+      q_stride, new_stride, stream);
+#else
+  if (split_rows(slots))
+    return launch_group<QT, KT, DH, APPEND, G, 2>(q, keys, values, k_new, v_new, pos, rows, out,
+                                                  n, heads, slots, cache_rows, scale, q_stride,
+                                                  new_stride, stream);
+  return launch_group<QT, KT, DH, APPEND, G, 1>(q, keys, values, k_new, v_new, pos, rows, out,
+                                                n, heads, slots, cache_rows, scale, q_stride,
+                                                new_stride, stream);
+#endif
 }
 
 // Heads per wavefront.  Measured on MI355X (4,096 queries x 8 heads, dh 32 bf16): rows of
@@ -339,7 +415,7 @@ int launch(const void* q, void* keys, void* values, const void* k_new, const voi
 #define CUGO_GROUP(GG)                                                                        \
   case GG:                                                                                    \
     if constexpr (GG * L <= 64)                                                               \
-      return launch_group<QT, KT, DH, APPEND, GG>(q, keys, values, k_new, v_new, pos, rows,   \
+      return launch_parts<QT, KT, DH, APPEND, GG>(q, keys, values, k_new, v_new, pos, rows,   \
                                                   out, n, heads, slots, cache_rows, scale,    \
                                                   q_stride, new_stride, stream);              \
     return -3;
@@ -348,7 +424,7 @@ int launch(const void* q, void* keys, void* values, const void* k_new, const voi
     CUGO_GROUP(8)
 #undef CUGO_GROUP
     default:
-      return launch_group<QT, KT, DH, APPEND, 1>(q, keys, values, k_new, v_new, pos, rows, out,
+      return launch_parts<QT, KT, DH, APPEND, 1>(q, keys, values, k_new, v_new, pos, rows, out,
                                                  n, heads, slots, cache_rows, scale, q_stride,
                                                  new_stride, stream);
   }
