@@ -734,12 +734,13 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
     Gumbel-max sampling over the legal actions, a `horizon`-step buffer (bf16 features,
     mask, action, log-prob, value, reward, done), finished games re-dealt from pre-dealt
     spares inside the step.  Reports env steps/s, the engine's and the actor's shares of
-    the step time and a roofline for each: the actor's FLOPs over its forward time
-    against the bf16 MFMA peak, the engine's bytes (observe 3,311 B a row, step with
-    auto-reset 513 B a row) over its time against HBM.  The rollout runs as one HIP graph
-    per horizon; the shares come from graphs of the engine's and the actor's launches
-    alone."""
-    from cugo_amd.rollout import MlpRollout, ResidualMlpActor, fused_forward
+    the step time and a roofline for each: the actor's FLOPs over its forward time (the
+    one-launch MFMA forward, `mlp_forward`, that the rollout runs) against the bf16 MFMA
+    peak, the engine's bytes (observe 3,311 B a row, step with auto-reset 513 B a row)
+    over its time against HBM.  The rollout runs as one HIP graph per horizon; the shares
+    come from graphs of the engine's and the actor's launches alone."""
+    from cugo_amd.rollout import (MlpRollout, ResidualMlpActor, fused_forward, mlp_forward,
+                                  pack_actor)
 
     dev = torch.device("cuda")
     torch.manual_seed(0)
@@ -805,17 +806,27 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
             ro.act(0)
         actor_step_ms = graph_ms(ag, 10, "c4.actor")
         del ag
-        # the forward pass alone, 20 back-to-back passes on the last step's input
+        # the forward pass alone, a graph of 20 back-to-back passes on the last step's
+        # input (bf16), replayed 3 times: the rollout's one-launch forward, and the
+        # layer-by-layer form (hipBLASLt GEMMs + HIP add + LayerNorm) for comparison
         x = ro.buffer.features[horizon - 1]
-        fused_forward(ext, actor, x)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with region("c4.forward"):
-            e0.record(stream)
-            for _ in range(20):
-                fused_forward(ext, actor, x)
-            e1.record(stream)
+        packed = ro.packed if ro.fused_kernel else pack_actor(ext, actor)
+
+        def forward_graph(fn) -> "torch.cuda.CUDAGraph":
+            fn()
             torch.cuda.synchronize()
-        forward_ms = e0.elapsed_time(e1) / 20
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(20):
+                    fn()
+            return g
+
+        fg = forward_graph(lambda: mlp_forward(ext, packed, x))
+        forward_ms = graph_ms(fg, 3, "c4.forward") / 20
+        del fg
+        lg = forward_graph(lambda: fused_forward(ext, actor, x))
+        layered_ms = graph_ms(lg, 3, "c4.forward_layers") / 20
+        del lg
     flops_row = actor.flops_per_row()
     tflops = flops_row * batch / (forward_ms * 1e-3) / 1e12
     engine_bytes = batch * (OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW)
@@ -827,11 +838,14 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
             "actor_share": round(actor_step_ms / step_ms, 4),
             "engine_step_ms": round(engine_step_ms, 4), "actor_step_ms": round(actor_step_ms, 4),
             "hip_graph": "one graph per rollout of horizon steps",
-            "roofline": {"kernel": "actor forward (hipBLASLt GEMMs + HIP add_layernorm)",
+            "roofline": {"kernel": "actor_kernel (mlp_forward: the whole actor in one launch)",
                          "bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
                          "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
                          "traffic": None, "flops_per_row": flops_row,
-                         "avg_forward_ms": round(forward_ms, 4)},
+                         "avg_forward_ms": round(forward_ms, 4),
+                         "layered_forward_ms": round(layered_ms, 4),
+                         "layered_tflops": round(flops_row * batch / (layered_ms * 1e-3)
+                                                 / 1e12, 1)},
             "engine_roofline": {"kernel": "observe + step_reset_spares (+ refill_spares)",
                                 "bound": "hbm", "achieved": round(engine_gbs, 2),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",

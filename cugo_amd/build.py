@@ -115,7 +115,7 @@ def build_library() -> Path:
     generate_stop_bits()
     out = PKG / "libcugo_hip.so"
     _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "kernels.hip"), str(CSRC / "decode.hip"),
-          str(CSRC / "selfplay.hip"),
+          str(CSRC / "selfplay.hip"), str(CSRC / "mlp.hip"),
           "-o", str(out)])
     check_no_packed_fp32(out)
     return out

@@ -778,6 +778,105 @@ std::vector<torch::Tensor> gumbel_sample(torch::Tensor logits, torch::Tensor leg
   return {actions, logp};
 }
 
+// mlp_pack_weight(w bf16 [rows, cols], rows_pad, cols_pad) -> packed bf16 [rows_pad *
+// cols_pad]: w in the order the actor kernel reads its MFMA operands
+// (cugo_mlp_pack_weight).
+torch::Tensor mlp_pack_weight(torch::Tensor w, int64_t rows_pad, int64_t cols_pad) {
+  TORCH_CHECK(w.is_cuda() && w.is_contiguous() && w.dim() == 2 &&
+                  w.scalar_type() == at::kBFloat16,
+              "w must be a contiguous CUDA bfloat16 [rows, cols] tensor");
+  TORCH_CHECK(w.size(0) <= rows_pad && w.size(1) <= cols_pad && rows_pad % 16 == 0 &&
+                  cols_pad % 32 == 0,
+              "rows_pad (a multiple of 16) and cols_pad (of 32) must cover w");
+  const DeviceGuard guard(w.device());
+  auto packed = torch::empty({rows_pad * cols_pad}, on(w, at::kBFloat16));
+  check_call(cugo_mlp_pack_weight(w.data_ptr(), w.size(0), w.size(1), rows_pad, cols_pad,
+                                  packed.data_ptr(), stream()),
+             "mlp_pack_weight");
+  return packed;
+}
+
+// mlp_actor_forward(x [n, F] f32 or bf16, x_copy bf16 [n, F] or None, packed weights and
+// bf16 vectors, actions, eps) -> (logits bf16 [n, actions], value f32 [n]): the residual
+// MLP actor's forward pass in one launch (cugo_mlp_actor_forward).  ln_w / ln_b hold the
+// blocks' LayerNorms then the final one; w_in, w1, w2 and w_head come from
+// mlp_pack_weight (w_head: the logits weight with the value weight as its last row).
+std::vector<torch::Tensor> mlp_actor_forward(
+    torch::Tensor x, c10::optional<torch::Tensor> x_copy, torch::Tensor w_in,
+    torch::Tensor b_in, std::vector<torch::Tensor> ln_w, std::vector<torch::Tensor> ln_b,
+    std::vector<torch::Tensor> w1, std::vector<torch::Tensor> b1, std::vector<torch::Tensor> w2,
+    std::vector<torch::Tensor> b2, torch::Tensor w_head, torch::Tensor b_head, int64_t actions,
+    double eps) {
+  TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.dim() == 2 &&
+                  (x.scalar_type() == at::kFloat || x.scalar_type() == at::kBFloat16),
+              "x must be a contiguous CUDA float32 or bfloat16 [n, F] tensor");
+  const int64_t n = x.size(0), f = x.size(1);
+  const int64_t blocks = static_cast<int64_t>(w1.size());
+  TORCH_CHECK(blocks <= CUGO_MLP_MAX_BLOCKS, "at most ", CUGO_MLP_MAX_BLOCKS, " blocks");
+  TORCH_CHECK(b1.size() == w1.size() && w2.size() == w1.size() && b2.size() == w1.size() &&
+                  ln_w.size() == w1.size() + 1 && ln_b.size() == w1.size() + 1,
+              "one fc1, fc2 and LayerNorm per block and a final LayerNorm");
+  const int64_t d = b_in.dim() == 1 ? b_in.size(0) : -1;
+  auto check_w = [&](const torch::Tensor& t, std::vector<int64_t> shape, const char* name) {
+    TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.scalar_type() == at::kBFloat16 &&
+                    t.sizes() == at::IntArrayRef(shape),
+                name, " must be a contiguous CUDA bfloat16 tensor of shape ", shape);
+    check_same_device(x, t, "x", name);
+  };
+  check_w(w_in, {d * CUGO_MLP_MAX_FEATURES}, "w_in (packed)");
+  check_w(b_in, {d}, "b_in");
+  for (int64_t b = 0; b <= blocks; ++b) {
+    check_w(ln_w[b], {d}, "ln_w");
+    check_w(ln_b[b], {d}, "ln_b");
+  }
+  for (int64_t b = 0; b < blocks; ++b) {
+    check_w(w1[b], {d * d}, "w1 (packed)");
+    check_w(b1[b], {d}, "b1");
+    check_w(w2[b], {d * d}, "w2 (packed)");
+    check_w(b2[b], {d}, "b2");
+  }
+  check_w(w_head, {CUGO_MLP_HEAD_ROWS * d}, "w_head (packed)");
+  check_w(b_head, {actions + 1}, "b_head");
+  if (x_copy.has_value()) {
+    TORCH_CHECK(x_copy->is_contiguous() && x_copy->scalar_type() == at::kBFloat16 &&
+                    x_copy->sizes() == x.sizes(),
+                "x_copy must be a contiguous bfloat16 tensor shaped like x");
+    check_same_device(x, *x_copy, "x", "x_copy");
+  }
+  CugoMlpWeights w{};
+  w.hidden = static_cast<int>(d);
+  w.blocks = static_cast<int>(blocks);
+  w.features = static_cast<int>(f);
+  w.actions = static_cast<int>(actions);
+  w.eps = static_cast<float>(eps);
+  w.w_in = w_in.data_ptr();
+  w.b_in = b_in.data_ptr();
+  for (int64_t b = 0; b <= blocks; ++b) {
+    w.ln_w[b] = ln_w[b].data_ptr();
+    w.ln_b[b] = ln_b[b].data_ptr();
+  }
+  for (int64_t b = 0; b < blocks; ++b) {
+    w.w1[b] = w1[b].data_ptr();
+    w.b1[b] = b1[b].data_ptr();
+    w.w2[b] = w2[b].data_ptr();
+    w.b2[b] = b2[b].data_ptr();
+  }
+  w.w_head = w_head.data_ptr();
+  w.b_head = b_head.data_ptr();
+  const DeviceGuard guard(x.device());
+  auto logits = torch::empty({n, actions}, on(x, at::kBFloat16));
+  auto value = torch::empty({n}, on(x, at::kFloat));
+  const int rc = cugo_mlp_actor_forward(
+      x.scalar_type() == at::kFloat ? CUGO_DTYPE_F32 : CUGO_DTYPE_BF16, x.data_ptr(),
+      x_copy.has_value() ? x_copy->data_ptr() : nullptr, n, &w, logits.data_ptr(),
+      value.data_ptr<float>(), stream());
+  TORCH_CHECK(rc != -3, "mlp_actor_forward: unsupported shape (hidden 512, at most ",
+              CUGO_MLP_MAX_BLOCKS, " blocks, features a multiple of 8 up to ",
+              CUGO_MLP_MAX_FEATURES, ", at most ", CUGO_MLP_HEAD_ROWS - 1, " actions)");
+  check_call(rc, "mlp_actor_forward");
+  return {logits, value};
+}
+
 // The tensors of one self-play wave, held for the wave's life, and the step's two
 // bookkeeping launches (cugo_selfplay_prepare / _advance).
 class SelfPlayState {
@@ -1010,6 +1109,16 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
       .def("prepare", &SelfPlayState::prepare)
       .def("advance", &SelfPlayState::advance);
   m.def("masked_argmax", &masked_argmax, "Greedy action: argmax of the legal logits");
+  m.def("mlp_pack_weight", &mlp_pack_weight,
+        "bf16 matrix in the actor kernel's MFMA operand order", pybind11::arg("w"),
+        pybind11::arg("rows_pad"), pybind11::arg("cols_pad"));
+  m.def("mlp_actor_forward", &mlp_actor_forward,
+        "residual MLP actor forward in one launch -> (logits bf16, value f32)",
+        pybind11::arg("x"), pybind11::arg("x_copy"), pybind11::arg("w_in"),
+        pybind11::arg("b_in"), pybind11::arg("ln_w"), pybind11::arg("ln_b"),
+        pybind11::arg("w1"), pybind11::arg("b1"), pybind11::arg("w2"), pybind11::arg("b2"),
+        pybind11::arg("w_head"), pybind11::arg("b_head"), pybind11::arg("actions"),
+        pybind11::arg("eps"));
   m.def("gumbel_sample", &gumbel_sample, "Masked Gumbel-max action and its log-softmax probability");
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),

@@ -9,15 +9,17 @@ over a resident batch of games with auto-reset, for a residual MLP actor:
     every game and gives each finished row its next game (seed base + i + B * generation,
     first player i & 1) from a pre-dealt spare (`refill_spares` every REFILL steps; a
     stale spare is dealt inline), so a finished game costs no separate reset launch;
-  * actor: bf16 GEMMs through PyTorch-ROCm (hipBLASLt), the bias and ReLU of each block's
-    first Linear fused into its GEMM (`torch._addmm_activation`), each residual add fused
-    with the next LayerNorm (`add_layernorm`, one HIP launch);
+  * actor: one HIP launch for the whole forward pass (`mlp_forward`: MFMA GEMMs with the
+    64-row tile's activations kept on chip from the input layer to the heads; it also
+    writes the bf16 copy of the observation into the buffer), for the 512-wide actor; any
+    other width runs `fused_forward`: bf16 GEMMs through PyTorch-ROCm (hipBLASLt), the bias
+    and ReLU of each block's first Linear fused into its GEMM, each residual add fused with
+    the next LayerNorm (`add_layernorm`, one HIP launch);
   * sampling: the Gumbel-max draw over the legal actions and its log-probability in one
     HIP launch (`gumbel_sample`), on uniforms from torch's generator (the reference draws
     with torch as well, cugo_seq_selfplay50.py:125-130).
 
-The observation's cast to bf16 is written straight into the rollout buffer, and the actor
-reads its input from there.
+The observation's cast to bf16 is written straight into the rollout buffer.
 """
 
 from __future__ import annotations
@@ -89,6 +91,72 @@ def fused_forward(ext, actor: ResidualMlpActor, x: torch.Tensor):
     return logits, value
 
 
+def mlp_kernel_fits(actor: ResidualMlpActor) -> bool:
+    """Whether `mlp_forward` serves this actor (hidden width 512, at most 4 blocks, the
+    input width a multiple of 8 up to 768, at most 255 actions)."""
+    return (actor.inp.out_features == 512 and len(actor.blocks) <= 4
+            and actor.inp.in_features % 8 == 0 and actor.inp.in_features <= 768
+            and actor.logits.out_features <= 255)
+
+
+@dataclass
+class PackedActor:
+    """A bf16 ResidualMlpActor's parameters as `mlp_forward` reads them: the matrices in
+    the kernel's MFMA operand order (`mlp_pack_weight`), the head as one matrix (the logits
+    weight with the value weight as its last row) and one bias."""
+
+    w_in: torch.Tensor
+    b_in: torch.Tensor
+    ln_w: list
+    ln_b: list
+    w1: list
+    b1: list
+    w2: list
+    b2: list
+    w_head: torch.Tensor
+    b_head: torch.Tensor
+    actions: int
+    eps: float
+
+
+MAX_FEATURES = 768  # the kernel's padded input width
+HEAD_ROWS = 256     # the kernel's padded head width
+
+
+@torch.no_grad()
+def pack_actor(ext, actor: ResidualMlpActor) -> PackedActor:
+    """The actor's parameters packed for `mlp_forward`; pack again after they change."""
+    d = actor.inp.out_features
+
+    def pack(w: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+        return ext.mlp_pack_weight(w.contiguous(), rows, cols)
+
+    blocks = actor.blocks
+    head = torch.cat([actor.logits.weight, actor.value.weight]).contiguous()
+    return PackedActor(
+        w_in=pack(actor.inp.weight, d, MAX_FEATURES), b_in=actor.inp.bias.contiguous(),
+        ln_w=[b.norm.weight.contiguous() for b in blocks] + [actor.norm.weight.contiguous()],
+        ln_b=[b.norm.bias.contiguous() for b in blocks] + [actor.norm.bias.contiguous()],
+        w1=[pack(b.fc1.weight, d, d) for b in blocks],
+        b1=[b.fc1.bias.contiguous() for b in blocks],
+        w2=[pack(b.fc2.weight, d, d) for b in blocks],
+        b2=[b.fc2.bias.contiguous() for b in blocks],
+        w_head=pack(head, HEAD_ROWS, d),
+        b_head=torch.cat([actor.logits.bias, actor.value.bias]).contiguous(),
+        actions=actor.logits.out_features, eps=actor.norm.eps)
+
+
+def mlp_forward(ext, packed: PackedActor, x: torch.Tensor,
+                x_copy: torch.Tensor | None = None):
+    """The actor's forward pass in one HIP launch (`pack_actor` of a bf16 actor): x [n, F]
+    float32 or bf16 (contiguous); x_copy, if given, receives x rounded to bf16.  Returns
+    (logits bf16 [n, A], value f32 [n]).  bf16 operands with fp32 accumulation; the
+    residual stream stays fp32 between blocks."""
+    p = packed
+    return ext.mlp_actor_forward(x, x_copy, p.w_in, p.b_in, p.ln_w, p.ln_b, p.w1, p.b1, p.w2,
+                                 p.b2, p.w_head, p.b_head, p.actions, p.eps)
+
+
 @dataclass
 class RolloutBuffer:
     """`horizon` steps of B games: the actor's bf16 input, the legal mask, the sampled
@@ -138,6 +206,9 @@ class MlpRollout:
         self.generator = generator
         self.noise: torch.Tensor | None = None
         self.graph: torch.cuda.CUDAGraph | None = None
+        # the one-launch forward where it fits the actor, else the layer-by-layer one
+        self.fused_kernel = mlp_kernel_fits(actor)
+        self.packed = pack_actor(ext, actor) if self.fused_kernel else None
         self.observation = None  # the last step's observe outputs
         self.step_out = None     # the last step's step outputs
 
@@ -153,9 +224,12 @@ class MlpRollout:
         of the buffer."""
         features, legal = self.observation[0], self.observation[1]
         buf = self.buffer
-        x = buf.features[t]
-        x.copy_(features)
-        logits, value = fused_forward(self.ext, self.actor, x)
+        if self.fused_kernel:
+            logits, value = mlp_forward(self.ext, self.packed, features, buf.features[t])
+        else:
+            x = buf.features[t]
+            x.copy_(features)
+            logits, value = fused_forward(self.ext, self.actor, x)
         u = self.noise if self.noise is not None else torch.rand(
             logits.shape, generator=self.generator, device=logits.device)
         action, logp = self.ext.gumbel_sample(logits, legal, u)
@@ -164,6 +238,20 @@ class MlpRollout:
         buf.logp[t].copy_(logp)
         buf.value[t].copy_(value)
         return action
+
+    def repack(self) -> None:
+        """Re-reads the actor's parameters after they changed (the one-launch forward reads
+        a packed copy; a captured graph reads the same tensors, updated in place)."""
+        if self.fused_kernel:
+            fresh = pack_actor(self.ext, self.actor)
+            if self.packed is None:
+                self.packed = fresh
+                return
+            for name in ("w_in", "b_in", "w_head", "b_head"):
+                getattr(self.packed, name).copy_(getattr(fresh, name))
+            for name in ("ln_w", "ln_b", "w1", "b1", "w2", "b2"):
+                for old, new in zip(getattr(self.packed, name), getattr(fresh, name)):
+                    old.copy_(new)
 
     def step(self, t: int, action: torch.Tensor):
         self.step_out = self.ext.step_reset_spares(

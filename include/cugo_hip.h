@@ -331,6 +331,52 @@ int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* lega
                        const float* uniforms, int64_t n, int64_t actions_count, int64_t* actions,
                        float* logp, hipStream_t stream);
 
+/* The weights of a residual MLP actor (bf16 device pointers): h = x W_in^T + b_in; per
+ * block h += W2 relu(W1 LN_b(h) + b1) + b2; z = LN_blocks(h); [logits, value] = z W_head^T
+ * + b_head.  The matrices are packed by cugo_mlp_pack_weight (Linear weights [out, in]):
+ * w_in [hidden, features] padded to [hidden, CUGO_MLP_MAX_FEATURES]; w1, w2 [hidden,
+ * hidden]; w_head = the logits weight [actions, hidden] with the value weight [1, hidden]
+ * as row `actions`, padded to [CUGO_MLP_HEAD_ROWS, hidden].  b_head [actions + 1]: the
+ * logits biases, then the value bias. */
+#define CUGO_MLP_MAX_BLOCKS 4
+#define CUGO_MLP_MAX_FEATURES 768
+#define CUGO_MLP_HEAD_ROWS 256
+typedef struct CugoMlpWeights {
+  int hidden;   /* must be 512 */
+  int blocks;   /* 0 .. CUGO_MLP_MAX_BLOCKS */
+  int features; /* multiple of 8, at most CUGO_MLP_MAX_FEATURES */
+  int actions;  /* logits; actions + 1 <= CUGO_MLP_HEAD_ROWS */
+  float eps;    /* LayerNorm epsilon */
+  const void* w_in;
+  const void* b_in;
+  const void* ln_w[CUGO_MLP_MAX_BLOCKS + 1]; /* block LayerNorms, then the final one */
+  const void* ln_b[CUGO_MLP_MAX_BLOCKS + 1];
+  const void* w1[CUGO_MLP_MAX_BLOCKS];
+  const void* b1[CUGO_MLP_MAX_BLOCKS];
+  const void* w2[CUGO_MLP_MAX_BLOCKS];
+  const void* b2[CUGO_MLP_MAX_BLOCKS];
+  const void* w_head;
+  const void* b_head;
+} CugoMlpWeights;
+
+/* cugo_mlp_pack_weight: a bf16 matrix w [rows, cols] (row major) in the order the actor
+ * kernel reads its MFMA B operands: packed[((t * S + s) * 64 + 16 q + r) * 8 + i] =
+ * w[16 t + r][32 s + 8 q + i] with S = cols_pad / 32, zero outside [rows, cols).
+ * rows_pad a multiple of 16, cols_pad of 32; packed holds rows_pad * cols_pad values.
+ * Run once per weight update. */
+int cugo_mlp_pack_weight(const void* w, int64_t rows, int64_t cols, int64_t rows_pad,
+                         int64_t cols_pad, void* packed, hipStream_t stream);
+
+/* cugo_mlp_actor_forward: the PPO rollout actor's forward pass in one launch (no reference
+ * counterpart: the reference's collector, python/cugo_ppo50.py:321-450, runs its actor as
+ * torch layers).  x [n, features] of x_dtype (F32 or BF16); x_copy, if not NULL, receives
+ * x rounded to bf16 [n, features]; logits bf16 [n, actions]; value f32 [n].  bf16
+ * operands, fp32 accumulation, the residual stream kept in fp32 between blocks.  Returns
+ * -3 for an unsupported shape. */
+int cugo_mlp_actor_forward(int x_dtype, const void* x, void* x_copy, int64_t n,
+                           const CugoMlpWeights* weights, void* logits, float* value,
+                           hipStream_t stream);
+
 /* The tensors of one self-play wave (WaveCollector, cugo_seq_selfplay50.py:45-76), w games,
  * max_steps recorded steps; every pointer is device memory. */
 typedef struct CugoSelfPlayWave {

@@ -110,6 +110,74 @@ def test_fused_forward_matches_float32(ext):
     assert agree >= 0.97, agree
 
 
+def _features(n: int, seed: int) -> torch.Tensor:
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = (torch.rand(n, 720, generator=g, device=DEV) < 0.2).float()
+    x[:, 453:479] = torch.rand(n, 26, generator=g, device=DEV)
+    return x
+
+
+@pytest.mark.parametrize("n,dtype,blocks", [(4096 + 37, torch.float32, 3),
+                                            (1000, torch.bfloat16, 3),
+                                            (130, torch.float32, 1)])
+def test_mlp_kernel_matches_float32(ext, n, dtype, blocks):
+    """mlp_forward (the whole actor in one launch: MFMA GEMMs, LayerNorms and the heads on a
+    64-row tile) against the module's own forward in float32 on the same bf16 inputs:
+    relative Frobenius error of the logits and values at most 2e-2, the greedy actions
+    agree on at least 97 % of the rows, and the bf16 copy of the input equals torch's
+    rounding.  Row counts that leave a partial last tile; float32 and bf16 inputs; one and
+    three blocks."""
+    from cugo_amd.rollout import ResidualMlpActor, fused_forward, mlp_forward, pack_actor
+
+    announce(f"MLP actor kernel vs float32 (n={n}, {dtype}, {blocks} blocks)")
+    torch.manual_seed(11)
+    base = ResidualMlpActor(blocks=blocks)
+    with torch.no_grad():
+        for p in base.parameters():
+            p.normal_(0.0, 0.05)
+    actor16 = base.to(DEV).to(torch.bfloat16).eval()
+    actor32 = ResidualMlpActor(blocks=blocks).to(DEV)
+    actor32.load_state_dict({k: v.float() for k, v in actor16.state_dict().items()})
+    x = _features(n, 5)
+    xb = x.to(torch.bfloat16)
+    copy = torch.full_like(xb, float("nan"))
+    packed = pack_actor(ext, actor16)
+    with torch.no_grad():
+        want_l, want_v = actor32.eval()(xb.float())
+        got_l, got_v = mlp_forward(ext, packed, (x if dtype == torch.float32 else xb).contiguous(),
+                                   copy)
+        layered_l, layered_v = fused_forward(ext, actor16, xb.contiguous())
+    assert got_l.dtype == torch.bfloat16 and got_v.dtype == torch.float32
+    assert tuple(got_l.shape) == (n, 179) and tuple(got_v.shape) == (n,)
+    assert torch.equal(copy, xb)
+    for got, want in ((got_l, want_l), (got_v, want_v)):
+        rel = float((got.float() - want).norm() / want.norm())
+        assert rel <= 2e-2, rel
+    assert float((layered_l.float() - want_l).norm() / want_l.norm()) <= 2e-2
+    agree = float((got_l.float().argmax(1) == want_l.argmax(1)).float().mean())
+    assert agree >= 0.97, agree
+    # repeatable, and an empty batch is a no-op
+    with torch.no_grad():
+        again_l, again_v = mlp_forward(ext, packed, (x if dtype == torch.float32 else xb).contiguous())
+        empty_l, empty_v = mlp_forward(ext, packed, x[:0].contiguous())
+    assert torch.equal(again_l, got_l) and torch.equal(again_v, got_v)
+    assert tuple(empty_l.shape) == (0, 179) and tuple(empty_v.shape) == (0,)
+
+
+def test_mlp_kernel_rejects_other_shapes(ext):
+    """Widths the kernel does not serve raise instead of running: hidden 256, or an input
+    width that is not a multiple of 8."""
+    from cugo_amd.rollout import ResidualMlpActor, mlp_forward, mlp_kernel_fits, pack_actor
+
+    narrow = ResidualMlpActor(d=256).to(DEV).to(torch.bfloat16)
+    odd = ResidualMlpActor(features=722).to(DEV).to(torch.bfloat16)
+    assert not mlp_kernel_fits(narrow) and not mlp_kernel_fits(odd)
+    with pytest.raises(RuntimeError):
+        mlp_forward(ext, pack_actor(ext, narrow), _features(64, 1))
+    with pytest.raises(RuntimeError):
+        mlp_forward(ext, pack_actor(ext, odd), torch.zeros(64, 722, device=DEV))
+
+
 def test_rollout_graph_replay_equals_eager(ext):
     """capture() + replay() plays what collect() plays: two rollouts from the same deals
     with the same fixed noise, one eager and one from the captured graph, for two horizons
