@@ -716,10 +716,12 @@ def paired_workload(ext, torch, pairs: int = 4096) -> dict:
             "mean_pair_score_a": round(s.mean_pair_score_a, 4)}
 
 
-def engine_traffic(batch: int) -> int | None:
-    """HBM bytes of one engine step of the rollout (observe with the draw, step with
-    auto-reset, and a 32nd of the spares' refill) from the committed counter summary."""
-    parts = [measured_traffic("observe_sample_kernel", str(batch)),
+def engine_traffic(batch: int, bf16: bool) -> int | None:
+    """HBM bytes of one engine step of the rollout (observe with the draw, float32 or bf16
+    features, step with auto-reset, and a 32nd of the spares' refill) from the committed
+    counter summary."""
+    parts = [measured_traffic("observe_bf16_sample_kernel" if bf16 else "observe_sample_kernel",
+                              str(batch)),
              measured_traffic("step_reset_spares_kernel", str(batch)),
              measured_traffic("refill_kernel", str(batch))]
     if None in parts:
@@ -783,11 +785,15 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         # Gumbel-max draw and the buffer writes of one step, one graph.
         st, g2, smp = ro.states.clone(), ro.generation.clone(), ro.sampler.clone()
         sp, sg = ro.spares.clone(), ro.spare_gen.clone()
+        feats = torch.empty((batch, 720), dtype=torch.bfloat16, device=dev)
 
         def engine_block():
             ext.refill_spares(sp, sg, g2, SEED_BASE + 0xC4)
             for _ in range(32):
-                _, _, _, _, _, acts = ext.observe_sample(st, smp)
+                if ro.fused_kernel:  # the rollout's bf16 observation, with the draw
+                    acts = ext.observe_bf16(st, feats, smp)[5]
+                else:
+                    acts = ext.observe_sample(st, smp)[5]
                 ext.step_reset_spares(st, acts, SEED_BASE + 0xC4, g2, smp, sp, sg)
 
         engine_block()
@@ -829,7 +835,8 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         del lg
     flops_row = actor.flops_per_row()
     tflops = flops_row * batch / (forward_ms * 1e-3) / 1e12
-    engine_bytes = batch * (OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW)
+    observe_bytes = OBSERVE_BYTES_PER_ROW - (720 * 2 if ro.fused_kernel else 0)
+    engine_bytes = batch * (observe_bytes + STEP_BYTES_PER_ROW)
     engine_gbs = engine_bytes / (engine_step_ms * 1e-3) / 1e9
     return {"env_steps_per_s": round(batch * reps * horizon / wall, 1),
             "games_per_s": round(games / wall, 1),
@@ -846,12 +853,13 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
                          "layered_forward_ms": round(layered_ms, 4),
                          "layered_tflops": round(flops_row * batch / (layered_ms * 1e-3)
                                                  / 1e12, 1)},
-            "engine_roofline": {"kernel": "observe + step_reset_spares (+ refill_spares)",
+            "engine_roofline": {"kernel": ("observe_bf16" if ro.fused_kernel else "observe")
+                                          + " + step_reset_spares (+ refill_spares)",
                                 "bound": "hbm", "achieved": round(engine_gbs, 2),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(engine_gbs / HBM_PEAK_GBS, 4),
-                                "traffic": engine_traffic(batch),
-                                "bytes_per_row_step": OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW,
+                                "traffic": engine_traffic(batch, ro.fused_kernel),
+                                "bytes_per_row_step": observe_bytes + STEP_BYTES_PER_ROW,
                                 "ms_per_step": round(engine_step_ms, 4)},
             "games_completed": games,
             "batch": batch, "horizon": horizon, "dtype": "bf16"}

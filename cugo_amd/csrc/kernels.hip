@@ -164,9 +164,26 @@ __device__ inline u32 spread4(u32 x) {
 // so every wave leaves the loop.  A claim is kClaim items: a claim of kClaim feature rows
 // issues all its LDS reads before its 3 x kClaim stores, so more rows a claim keep more
 // stores in flight per wave, at the cost of 20 VGPRs a row.
-template <int kClaim>
+// bf16 bits of a finite float's bits, rounded to nearest even (torch's float -> bfloat16).
+__device__ inline u32 bf16_bits(u32 f) { return (f + 0x7fffu + ((f >> 16) & 1u)) >> 16; }
+
+// Four features (float bits) of a row's float4 column `quad` (index row * kQuads + quad),
+// as float32 or, with kBf16, rounded to bfloat16.
+template <bool kBf16>
+__device__ inline void store_quad(void* features, i64 index, const uint4& v) {
+  if constexpr (kBf16) {
+    uint2 p;
+    p.x = bf16_bits(v.x) | (bf16_bits(v.y) << 16);
+    p.y = bf16_bits(v.z) | (bf16_bits(v.w) << 16);
+    reinterpret_cast<uint2*>(features)[index] = p;
+  } else {
+    reinterpret_cast<uint4*>(features)[index] = v;
+  }
+}
+
+template <int kClaim, bool kBf16 = false>
 __device__ inline void store_observation(const RecordBuffer& t, i64 base, int count,
-                                         float* features, u8* legal, int* next) {
+                                         void* features, u8* legal, int* next) {
   const int lane = threadIdx.x & (kTile - 1);
   constexpr int kQuads = kFeatureCount / 4;  // 180
   // Each of the lane's columns 1 and 2: its features' dense dwords, or the record's zero
@@ -179,7 +196,7 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
       const int pos = q < kQuads ? dense_pos((u32)(4 * q + k)) : -1;
       dpos[c][k] = kRecBits + (pos >= 0 ? pos : kRecDense);
     }
-  uint4* fout = reinterpret_cast<uint4*>(features + base * kFeatureCount);
+  const i64 fbase = base * kQuads;  // the tile's first float4 column
   // Legal mask: count x 179 bytes from a 4-byte aligned base (64 * 179 % 4 == 0); word
   // w holds tile bytes 4w..4w+3, i.e. actions a..a+3 of row r unless it straddles rows.
   u8* lout = legal + base * kActionCount;
@@ -226,7 +243,7 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
             v.z |= dv[j][c][2];
             v.w |= dv[j][c][3];
           }
-          if (q < kQuads) fout[(item0 + j) * kQuads + q] = v;
+          if (q < kQuads) store_quad<kBf16>(features, fbase + (item0 + j) * kQuads + q, v);
         }
       }
       continue;
@@ -250,7 +267,7 @@ __device__ inline void store_observation(const RecordBuffer& t, i64 base, int co
             v.z |= rec[dpos[c][2]];
             v.w |= rec[dpos[c][3]];
           }
-          fout[r * kQuads + q] = v;
+          store_quad<kBf16>(features, fbase + r * kQuads + q, v);
         }
       }
     } else if (item < count + chunks) {
@@ -326,10 +343,12 @@ __device__ inline i64 draw_legal(u64 m0, u64 m1, u64 m2, u64& x) {
 // kSample: also draw each row's random-policy action from its legal mask while the mask
 // is in registers (draw_legal with sampler[i], into actions[i]), as sample_kernel would
 // from the stored mask.
-template <bool kIndexed, bool kSample = false>
+// kBf16: the features are written rounded to bfloat16 (uint16 [n, 720]), as torch's
+// conversion of the float32 features rounds them.
+template <bool kIndexed, bool kSample = false, bool kBf16 = false>
 __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states, i64 env_count,
                                                               const i64* ids, i64 n,
-                                                              float* features, u8* legal,
+                                                              void* features, u8* legal,
                                                               u8* player, u8* done,
                                                               i16* status, u64* sampler = nullptr,
                                                               i64* actions = nullptr) {
@@ -382,7 +401,7 @@ __global__ __launch_bounds__(kObsThreads) void observe_kernel(const u64* states,
     }
   }
   __syncthreads();
-  store_observation<2>(t.out, base, count, features, legal, &next_item);
+  store_observation<2, kBf16>(t.out, base, count, features, legal, &next_item);
 }
 
 // --------------------------------------------------------------------- step ----
@@ -1123,6 +1142,24 @@ int cugo_observe(const uint8_t* states, int64_t n, float* features, uint8_t* leg
   observe_kernel<false><<<tiles(n), kObsThreads, 0, stream>>>(
       reinterpret_cast<const u64*>(states), n, nullptr, n, features, legal, player, done,
       status);
+  return launched();
+}
+
+int cugo_observe_bf16(const uint8_t* states, int64_t n, uint16_t* features, uint8_t* legal,
+                      uint8_t* player, uint8_t* done, int16_t* status, uint64_t* sampler,
+                      int64_t* actions, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!states || !features || !legal || !player || !done || !status)) ||
+      (sampler == nullptr) != (actions == nullptr))
+    return kBadArgument;
+  if (n == 0) return 0;
+  if (sampler != nullptr)
+    observe_kernel<false, true, true><<<tiles(n), kObsThreads, 0, stream>>>(
+        reinterpret_cast<const u64*>(states), n, nullptr, n, features, legal, player, done,
+        status, reinterpret_cast<u64*>(sampler), actions);
+  else
+    observe_kernel<false, false, true><<<tiles(n), kObsThreads, 0, stream>>>(
+        reinterpret_cast<const u64*>(states), n, nullptr, n, features, legal, player, done,
+        status);
   return launched();
 }
 

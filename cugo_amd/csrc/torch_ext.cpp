@@ -95,6 +95,39 @@ std::vector<torch::Tensor> observe(torch::Tensor states) {
   return o;
 }
 
+// observe with the features written rounded to bfloat16 into `features` (a contiguous
+// bf16 [N, 720] tensor, e.g. a row block of a rollout buffer): (features, legal, player,
+// done, status), features equal to observe's rounded as torch rounds float32 to bfloat16;
+// with a sampler, also observe_sample's draw (actions last).
+std::vector<torch::Tensor> observe_bf16(torch::Tensor states, torch::Tensor features,
+                                        c10::optional<torch::Tensor> sampler) {
+  check_states(states);
+  const int64_t n = states.size(0);
+  TORCH_CHECK(features.is_contiguous() && features.scalar_type() == at::kBFloat16 &&
+                  features.dim() == 2 && features.size(0) == n &&
+                  features.size(1) == CUGO_FEATURE_COUNT,
+              "features must be a contiguous bfloat16 [N, 720] tensor");
+  check_same_device(states, features, "states", "features");
+  if (sampler.has_value()) {
+    check_1d(*sampler, at::kLong, "sampler");
+    TORCH_CHECK(sampler->numel() == n, "sampler must have one entry per state row");
+    check_same_device(states, *sampler, "states", "sampler");
+  }
+  const DeviceGuard guard(states.device());
+  std::vector<torch::Tensor> o{features, torch::empty({n, CUGO_ACTION_COUNT}, on(states, at::kBool)),
+                               torch::empty({n}, on(states, at::kByte)),
+                               torch::empty({n}, on(states, at::kBool)),
+                               torch::empty({n}, on(states, at::kShort))};
+  if (sampler.has_value()) o.push_back(torch::empty({n}, on(states, at::kLong)));
+  check_call(cugo_observe_bf16(
+                 u8p(states), n, reinterpret_cast<uint16_t*>(features.data_ptr()), u8p(o[1]),
+                 u8p(o[2]), u8p(o[3]), o[4].data_ptr<int16_t>(),
+                 sampler.has_value() ? reinterpret_cast<uint64_t*>(sampler->data_ptr()) : nullptr,
+                 sampler.has_value() ? o[5].data_ptr<int64_t>() : nullptr, stream()),
+             "observe_bf16");
+  return o;
+}
+
 // observe plus sample_uniform's draw in one launch: (features, legal, player, done,
 // status, actions); sampler advances in place as sample_uniform advances it.
 std::vector<torch::Tensor> observe_sample(torch::Tensor states, torch::Tensor sampler) {
@@ -1119,6 +1152,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("w1"), pybind11::arg("b1"), pybind11::arg("w2"), pybind11::arg("b2"),
         pybind11::arg("w_head"), pybind11::arg("b_head"), pybind11::arg("actions"),
         pybind11::arg("eps"));
+  m.def("observe_bf16", &observe_bf16,
+        "observe (and observe_sample's draw, given a sampler) with bfloat16 features written "
+        "into a given tensor",
+        pybind11::arg("states"), pybind11::arg("features"),
+        pybind11::arg("sampler") = pybind11::none());
   m.def("gumbel_sample", &gumbel_sample, "Masked Gumbel-max action and its log-softmax probability");
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),

@@ -5,21 +5,21 @@ observe -> actor forward -> masked sampling -> step, records (features, legal, a
 logp) per decision and the settled reward at the end.  This module plays the same loop
 over a resident batch of games with auto-reset, for a residual MLP actor:
 
-  * engine: `observe` (720 features + 179-way mask), then `step_reset_spares`, which steps
+  * engine: `observe_bf16` (720 features, written as bf16 straight into the rollout
+    buffer, + the 179-way mask; `observe` with float32 features for other actors), then
+    `step_reset_spares`, which steps
     every game and gives each finished row its next game (seed base + i + B * generation,
     first player i & 1) from a pre-dealt spare (`refill_spares` every REFILL steps; a
     stale spare is dealt inline), so a finished game costs no separate reset launch;
   * actor: one HIP launch for the whole forward pass (`mlp_forward`: MFMA GEMMs with the
-    64-row tile's activations kept on chip from the input layer to the heads; it also
-    writes the bf16 copy of the observation into the buffer), for the 512-wide actor; any
+    64-row tile's activations kept on chip from the input layer to the heads, reading the
+    buffer's bf16 features), for the 512-wide actor; any
     other width runs `fused_forward`: bf16 GEMMs through PyTorch-ROCm (hipBLASLt), the bias
     and ReLU of each block's first Linear fused into its GEMM, each residual add fused with
     the next LayerNorm (`add_layernorm`, one HIP launch);
   * sampling: the Gumbel-max draw over the legal actions and its log-probability in one
     HIP launch (`gumbel_sample`), on uniforms from torch's generator (the reference draws
     with torch as well, cugo_seq_selfplay50.py:125-130).
-
-The observation's cast to bf16 is written straight into the rollout buffer.
 """
 
 from __future__ import annotations
@@ -213,10 +213,16 @@ class MlpRollout:
         self.step_out = None     # the last step's step outputs
 
     def observe(self, t: int):
-        """Step t's observation (the next games are pre-dealt every REFILL steps)."""
+        """Step t's observation (the next games are pre-dealt every REFILL steps).  With the
+        one-launch actor, the features are written as bf16 straight into the buffer's row
+        t (`observe_bf16`: the float32 features rounded as torch rounds them), which the
+        actor reads."""
         if t % REFILL == 0:
             self.ext.refill_spares(self.spares, self.spare_gen, self.generation, self.base)
-        self.observation = self.ext.observe(self.states)
+        if self.fused_kernel:
+            self.observation = self.ext.observe_bf16(self.states, self.buffer.features[t])
+        else:
+            self.observation = self.ext.observe(self.states)
         return self.observation
 
     def act(self, t: int):
@@ -224,8 +230,8 @@ class MlpRollout:
         of the buffer."""
         features, legal = self.observation[0], self.observation[1]
         buf = self.buffer
-        if self.fused_kernel:
-            logits, value = mlp_forward(self.ext, self.packed, features, buf.features[t])
+        if self.fused_kernel:  # features is buf.features[t]
+            logits, value = mlp_forward(self.ext, self.packed, features)
         else:
             x = buf.features[t]
             x.copy_(features)

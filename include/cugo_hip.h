@@ -112,6 +112,13 @@ int cugo_stock_indexed(const uint8_t* states, int64_t env_count, const int64_t* 
  */
 int cugo_sample_uniform(const uint8_t* legal, int64_t n, uint64_t* sampler, int64_t* actions,
                         hipStream_t stream);
+/* cugo_observe_bf16: cugo_observe with the features rounded to bfloat16 (uint16 bits
+ * [n, CUGO_FEATURE_COUNT], round to nearest even, as torch converts float32), for callers
+ * that keep bf16 observations (the PPO rollout's buffer); with sampler and actions (both
+ * or neither NULL) also cugo_observe_sample's draw.  No reference counterpart. */
+int cugo_observe_bf16(const uint8_t* states, int64_t n, uint16_t* features, uint8_t* legal,
+                      uint8_t* player, uint8_t* done, int16_t* status, uint64_t* sampler,
+                      int64_t* actions, hipStream_t stream);
 int cugo_observe_sample(const uint8_t* states, int64_t n, float* features, uint8_t* legal,
                         uint8_t* player, uint8_t* done, int16_t* status, uint64_t* sampler,
                         int64_t* actions, hipStream_t stream);

@@ -34,7 +34,8 @@ def _actor(seed: int, std: float):
 
 def test_rollout_engine_matches_oracle(ext, ref):
     """C4's loop at its full batch, 32,768 games, for 40 steps (the spares are refilled
-    at steps 0 and 32): observation, actions drawn from the legal set, step outputs and
+    at steps 0 and 32): observation (bf16 features equal to the oracle's float32 ones
+    rounded as torch rounds them), actions drawn from the legal set, step outputs and
     the rows after every step's auto-reset, against the oracle stepping the same
     actions and re-dealing finished rows from seed base + i + 32,768 * generation."""
     from cugo_amd.rollout import MlpRollout
@@ -52,7 +53,13 @@ def test_rollout_engine_matches_oracle(ext, ref):
         for t in range(steps):
             obs = ro.observe(t)
             robs = ref.observe(host)
-            assert_observe_equal(obs, robs, f"observation, step {t}")
+            # the rollout keeps bf16 features: the oracle's float32 features, rounded
+            want = torch.from_numpy(robs[0]).to(torch.bfloat16).view(torch.int16)
+            assert obs[0].dtype == torch.bfloat16
+            assert torch.equal(obs[0].view(torch.int16).cpu(), want), f"features, step {t}"
+            assert_observe_equal((obs[0].float(),) + tuple(obs[1:]),
+                                 (obs[0].float().cpu().numpy(),) + tuple(robs[1:]),
+                                 f"observation, step {t}")
             action = ro.act(t)
             a = to_np(action)
             legal = robs[1]
@@ -72,7 +79,7 @@ def test_rollout_engine_matches_oracle(ext, ref):
                                   rout[0].view(np.uint32)), t
             assert np.array_equal(to_np(buf.done[t]), rout[1]), t
             assert np.array_equal(to_np(buf.legal[t]), legal), t
-            assert torch.equal(buf.features[t], obs[0].to(torch.bfloat16)), t
+            assert buf.features[t].data_ptr() == obs[0].data_ptr(), t
             lp = to_np(buf.logp[t])
             assert (lp[live] <= 1e-6).all() and np.isfinite(lp[live]).all(), t
     assert np.array_equal(to_np(ro.generation), hgen)
