@@ -61,6 +61,18 @@ std::vector<torch::Tensor> observation_outputs(int64_t n, const torch::Tensor& l
           torch::empty({n}, on(like, at::kShort))};
 }
 
+// `out` if given (a contiguous tensor of `dtype` and `shape` on like's device: a caller's
+// buffer the kernel writes into), else a new tensor.
+torch::Tensor out_or_new(const c10::optional<torch::Tensor>& out, std::vector<int64_t> shape,
+                         at::ScalarType dtype, const torch::Tensor& like, const char* name) {
+  if (!out.has_value()) return torch::empty(shape, on(like, dtype));
+  TORCH_CHECK(out->is_contiguous() && out->scalar_type() == dtype &&
+                  out->sizes() == at::IntArrayRef(shape),
+              name, " must be a contiguous ", c10::toString(dtype), " tensor of shape ", shape);
+  check_same_device(like, *out, "input", name);
+  return *out;
+}
+
 std::vector<torch::Tensor> step_outputs(int64_t n, const torch::Tensor& like) {
   return {torch::empty({n}, on(like, at::kFloat)), torch::empty({n}, on(like, at::kBool)),
           torch::empty({n}, on(like, at::kBool)), torch::empty({n}, on(like, at::kShort)),
@@ -100,7 +112,8 @@ std::vector<torch::Tensor> observe(torch::Tensor states) {
 // done, status), features equal to observe's rounded as torch rounds float32 to bfloat16;
 // with a sampler, also observe_sample's draw (actions last).
 std::vector<torch::Tensor> observe_bf16(torch::Tensor states, torch::Tensor features,
-                                        c10::optional<torch::Tensor> sampler) {
+                                        c10::optional<torch::Tensor> sampler,
+                                        c10::optional<torch::Tensor> legal) {
   check_states(states);
   const int64_t n = states.size(0);
   TORCH_CHECK(features.is_contiguous() && features.scalar_type() == at::kBFloat16 &&
@@ -114,7 +127,8 @@ std::vector<torch::Tensor> observe_bf16(torch::Tensor states, torch::Tensor feat
     check_same_device(states, *sampler, "states", "sampler");
   }
   const DeviceGuard guard(states.device());
-  std::vector<torch::Tensor> o{features, torch::empty({n, CUGO_ACTION_COUNT}, on(states, at::kBool)),
+  std::vector<torch::Tensor> o{features,
+                               out_or_new(legal, {n, CUGO_ACTION_COUNT}, at::kBool, states, "legal"),
                                torch::empty({n}, on(states, at::kByte)),
                                torch::empty({n}, on(states, at::kBool)),
                                torch::empty({n}, on(states, at::kShort))};
@@ -479,7 +493,9 @@ std::vector<torch::Tensor> play_random(torch::Tensor states, torch::Tensor sampl
 std::vector<torch::Tensor> step_reset_spares(torch::Tensor states, torch::Tensor actions,
                                              int64_t base_seed, torch::Tensor generation,
                                              torch::Tensor sampler, torch::Tensor spares,
-                                             torch::Tensor spare_gen, int64_t seed_stride) {
+                                             torch::Tensor spare_gen, int64_t seed_stride,
+                                             c10::optional<torch::Tensor> reward,
+                                             c10::optional<torch::Tensor> done) {
   check_states(states);
   check_states(spares);
   const int64_t n = states.size(0);
@@ -497,6 +513,8 @@ std::vector<torch::Tensor> step_reset_spares(torch::Tensor states, torch::Tensor
   check_same_device(states, spare_gen, "states", "spare_gen");
   const DeviceGuard guard(states.device());
   auto o = step_outputs(n, states);
+  if (reward.has_value()) o[0] = out_or_new(reward, {n}, at::kFloat, states, "reward");
+  if (done.has_value()) o[1] = out_or_new(done, {n}, at::kBool, states, "done");
   check_call(cugo_step_reset_spares(
                  u8p(states), actions.data_ptr<int64_t>(), n, o[0].data_ptr<float>(), u8p(o[1]),
                  u8p(o[2]), o[3].data_ptr<int16_t>(), u8p(o[4]),
@@ -787,7 +805,9 @@ torch::Tensor masked_argmax(torch::Tensor logits, torch::Tensor legal) {
 // int64 [n], logp f32 [n]): the sampling of WaveCollector._step
 // (python/cugo_seq_selfplay50.py:125-130) with the uniforms supplied.
 std::vector<torch::Tensor> gumbel_sample(torch::Tensor logits, torch::Tensor legal,
-                                         torch::Tensor uniforms) {
+                                         torch::Tensor uniforms,
+                                         c10::optional<torch::Tensor> actions_out,
+                                         c10::optional<torch::Tensor> logp_out) {
   TORCH_CHECK(logits.is_cuda() && logits.is_contiguous() && logits.dim() == 2 &&
                   (logits.scalar_type() == at::kFloat || logits.scalar_type() == at::kBFloat16),
               "logits must be a contiguous CUDA float32 or bfloat16 [n, A] tensor");
@@ -801,8 +821,8 @@ std::vector<torch::Tensor> gumbel_sample(torch::Tensor logits, torch::Tensor leg
   check_same_device(logits, uniforms, "logits", "uniforms");
   const DeviceGuard guard(logits.device());
   const int64_t n = logits.size(0);
-  auto actions = torch::empty({n}, on(logits, at::kLong));
-  auto logp = torch::empty({n}, on(logits, at::kFloat));
+  auto actions = out_or_new(actions_out, {n}, at::kLong, logits, "actions");
+  auto logp = out_or_new(logp_out, {n}, at::kFloat, logits, "logp");
   check_call(cugo_gumbel_sample(logits.scalar_type() == at::kFloat ? CUGO_DTYPE_F32 : CUGO_DTYPE_BF16,
                                 logits.data_ptr(), u8p(legal), uniforms.data_ptr<float>(),
                                 n, logits.size(1), actions.data_ptr<int64_t>(),
@@ -839,7 +859,7 @@ std::vector<torch::Tensor> mlp_actor_forward(
     torch::Tensor b_in, std::vector<torch::Tensor> ln_w, std::vector<torch::Tensor> ln_b,
     std::vector<torch::Tensor> w1, std::vector<torch::Tensor> b1, std::vector<torch::Tensor> w2,
     std::vector<torch::Tensor> b2, torch::Tensor w_head, torch::Tensor b_head, int64_t actions,
-    double eps) {
+    double eps, c10::optional<torch::Tensor> value_out) {
   TORCH_CHECK(x.is_cuda() && x.is_contiguous() && x.dim() == 2 &&
                   (x.scalar_type() == at::kFloat || x.scalar_type() == at::kBFloat16),
               "x must be a contiguous CUDA float32 or bfloat16 [n, F] tensor");
@@ -898,7 +918,7 @@ std::vector<torch::Tensor> mlp_actor_forward(
   w.b_head = b_head.data_ptr();
   const DeviceGuard guard(x.device());
   auto logits = torch::empty({n, actions}, on(x, at::kBFloat16));
-  auto value = torch::empty({n}, on(x, at::kFloat));
+  auto value = out_or_new(value_out, {n}, at::kFloat, x, "value");
   const int rc = cugo_mlp_actor_forward(
       x.scalar_type() == at::kFloat ? CUGO_DTYPE_F32 : CUGO_DTYPE_BF16, x.data_ptr(),
       x_copy.has_value() ? x_copy->data_ptr() : nullptr, n, &w, logits.data_ptr(),
@@ -1124,7 +1144,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "step, then reset_done_spares of the finished rows, in one launch",
         pybind11::arg("states"), pybind11::arg("actions"), pybind11::arg("base_seed"),
         pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("spares"),
-        pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1);
+        pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1,
+        pybind11::arg("reward") = pybind11::none(), pybind11::arg("done") = pybind11::none());
   m.def("event_tokens", &event_tokens, "SeqNet.event_token: event_in(encode_events) + position + type");
   m.def("start_tokens", &start_tokens, "SeqNet.start_token: start_in(encode_start) + position + type");
   m.def("add_layernorm", &add_layernorm, "x + y and LayerNorm(x + y) in one launch",
@@ -1151,13 +1172,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("b_in"), pybind11::arg("ln_w"), pybind11::arg("ln_b"),
         pybind11::arg("w1"), pybind11::arg("b1"), pybind11::arg("w2"), pybind11::arg("b2"),
         pybind11::arg("w_head"), pybind11::arg("b_head"), pybind11::arg("actions"),
-        pybind11::arg("eps"));
+        pybind11::arg("eps"), pybind11::arg("value") = pybind11::none());
   m.def("observe_bf16", &observe_bf16,
         "observe (and observe_sample's draw, given a sampler) with bfloat16 features written "
         "into a given tensor",
         pybind11::arg("states"), pybind11::arg("features"),
-        pybind11::arg("sampler") = pybind11::none());
-  m.def("gumbel_sample", &gumbel_sample, "Masked Gumbel-max action and its log-softmax probability");
+        pybind11::arg("sampler") = pybind11::none(), pybind11::arg("legal") = pybind11::none());
+  m.def("gumbel_sample", &gumbel_sample, "Masked Gumbel-max action and its log-softmax probability",
+        pybind11::arg("logits"), pybind11::arg("legal"), pybind11::arg("uniforms"),
+        pybind11::arg("actions") = pybind11::none(), pybind11::arg("logp") = pybind11::none());
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
         pybind11::arg("rows") = pybind11::none());

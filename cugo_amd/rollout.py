@@ -147,14 +147,15 @@ def pack_actor(ext, actor: ResidualMlpActor) -> PackedActor:
 
 
 def mlp_forward(ext, packed: PackedActor, x: torch.Tensor,
-                x_copy: torch.Tensor | None = None):
+                x_copy: torch.Tensor | None = None, value: torch.Tensor | None = None):
     """The actor's forward pass in one HIP launch (`pack_actor` of a bf16 actor): x [n, F]
-    float32 or bf16 (contiguous); x_copy, if given, receives x rounded to bf16.  Returns
-    (logits bf16 [n, A], value f32 [n]).  bf16 operands with fp32 accumulation; the
-    residual stream stays fp32 between blocks."""
+    float32 or bf16 (contiguous); x_copy, if given, receives x rounded to bf16; `value`, if
+    given, receives the values (f32 [n]).  Returns (logits bf16 [n, A], value f32 [n]).
+    bf16 operands with fp32 accumulation; the residual stream stays fp32 between
+    blocks."""
     p = packed
     return ext.mlp_actor_forward(x, x_copy, p.w_in, p.b_in, p.ln_w, p.ln_b, p.w1, p.b1, p.w2,
-                                 p.b2, p.w_head, p.b_head, p.actions, p.eps)
+                                 p.b2, p.w_head, p.b_head, p.actions, p.eps, value)
 
 
 @dataclass
@@ -219,8 +220,9 @@ class MlpRollout:
         actor reads."""
         if t % REFILL == 0:
             self.ext.refill_spares(self.spares, self.spare_gen, self.generation, self.base)
-        if self.fused_kernel:
-            self.observation = self.ext.observe_bf16(self.states, self.buffer.features[t])
+        if self.fused_kernel:  # features and mask straight into the buffer's row t
+            self.observation = self.ext.observe_bf16(self.states, self.buffer.features[t],
+                                                     legal=self.buffer.legal[t])
         else:
             self.observation = self.ext.observe(self.states)
         return self.observation
@@ -230,20 +232,20 @@ class MlpRollout:
         of the buffer."""
         features, legal = self.observation[0], self.observation[1]
         buf = self.buffer
-        if self.fused_kernel:  # features is buf.features[t]
-            logits, value = mlp_forward(self.ext, self.packed, features)
+        if self.fused_kernel:
+            # features and legal are the buffer's rows t; the value, action and
+            # log-probability are written into theirs
+            logits, _ = mlp_forward(self.ext, self.packed, features, value=buf.value[t])
         else:
             x = buf.features[t]
             x.copy_(features)
             logits, value = fused_forward(self.ext, self.actor, x)
+            buf.legal[t].copy_(legal)
+            buf.value[t].copy_(value)
         u = self.noise if self.noise is not None else torch.rand(
             logits.shape, generator=self.generator, device=logits.device)
-        action, logp = self.ext.gumbel_sample(logits, legal, u)
-        buf.legal[t].copy_(legal)
-        buf.action[t].copy_(action)
-        buf.logp[t].copy_(logp)
-        buf.value[t].copy_(value)
-        return action
+        self.ext.gumbel_sample(logits, legal, u, actions=buf.action[t], logp=buf.logp[t])
+        return buf.action[t]
 
     def repack(self) -> None:
         """Re-reads the actor's parameters after they changed (the one-launch forward reads
@@ -260,11 +262,11 @@ class MlpRollout:
                     old.copy_(new)
 
     def step(self, t: int, action: torch.Tensor):
+        """Steps every game with `action` (re-dealing finished ones); the reward and done
+        flag go straight into the buffer's row t."""
         self.step_out = self.ext.step_reset_spares(
             self.states, action, self.base, self.generation, self.sampler, self.spares,
-            self.spare_gen)
-        self.buffer.reward[t].copy_(self.step_out[0])
-        self.buffer.done[t].copy_(self.step_out[1])
+            self.spare_gen, reward=self.buffer.reward[t], done=self.buffer.done[t])
         return self.step_out
 
     def _steps(self) -> None:
