@@ -848,7 +848,9 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
             "roofline": {"kernel": "actor_kernel (mlp_forward: the whole actor in one launch)",
                          "bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
                          "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
-                         "traffic": None, "flops_per_row": flops_row,
+                         "traffic": (measured_traffic("actor_kernel", str(batch))
+                                     if ro.fused_kernel else None),
+                         "flops_per_row": flops_row,
                          "avg_forward_ms": round(forward_ms, 4),
                          "layered_forward_ms": round(layered_ms, 4),
                          "layered_tflops": round(flops_row * batch / (layered_ms * 1e-3)
