@@ -531,46 +531,61 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
 }
 
 // ------------------------------------------------------------------ branch ----
-// branch_indexed (torch50_ext.cu:288-314) without LDS: each lane reads its parent row
-// straight from global memory (branching children of one root read the same row, so a
-// wave's loads are broadcasts from L2), steps it in registers and writes its child row
-// from registers.  The transition holds ~200 VGPRs, which allows two waves per SIMD;
-// capping registers for three or four waves spills 144 / 356 bytes a lane and measured
-// 1.35x / 2.7x slower on 1,048,576 children, and staging the rows through LDS as the other
-// step kernels do measured 1.13x slower.
+// branch_indexed (torch50_ext.cu:288-314): each lane reads its parent row straight from
+// global memory (branching children of one root read the same row, so a wave's loads are
+// broadcasts from L2), steps it in registers, and the wave's 64 child rows go out through
+// LDS as one contiguous block.  The transition holds ~200 VGPRs, which allows two waves
+// per SIMD; capping registers for three or four waves spills 144 / 356 bytes a lane and
+// measured 1.35x / 2.7x slower on 1,048,576 children, and staging the parents through LDS
+// as well, as the other step kernels do, measured 1.13x slower.
 __global__ __launch_bounds__(kTile) void branch_kernel(const u64* parents, i64 env_count,
                                                        const i64* ids, const i64* actions,
                                                        i64 n, u64* children, float* reward,
                                                        u8* done, u8* nagari, i16* status,
                                                        u8* committed) {
-  const i64 i = (i64)blockIdx.x * kTile + threadIdx.x;
-  if (i >= n) return;
-  const i64 id = ids[i];
-  u64 row[kRowWords];
-  if (valid_id(id, env_count)) {
-    const u64* src = parents + id * kRowWords;
+  __shared__ u64 tile[kTile * kRowWords];
+  const int lane = threadIdx.x;
+  const i64 base = (i64)blockIdx.x * kTile;
+  const i64 i = base + lane;
+  const int count = n - base < kTile ? (int)(n - base) : kTile;
+  if (i < n) {
+    const i64 id = ids[i];
+    u64 row[kRowWords];
+    if (valid_id(id, env_count)) {
+      const u64* src = parents + id * kRowWords;
 #pragma unroll
-    for (int k = 0; k < kRowWords; ++k) row[k] = src[k];
-    Env e = unpack_row(row);
-    const StepOut so = torch_step(e, clamp_action(actions[i]));
-    pack_row(e, row);
-    reward[i] = (float)so.reward0;
-    done[i] = so.done;
-    nagari[i] = so.nagari;
-    status[i] = (i16)so.status;
-    committed[i] = so.committed;
-  } else {  // torch50_ext.cu:108-118: a zero child
+      for (int k = 0; k < kRowWords; ++k) row[k] = src[k];
+      Env e = unpack_row(row);
+      const StepOut so = torch_step(e, clamp_action(actions[i]));
+      pack_row(e, row);
+      reward[i] = (float)so.reward0;
+      done[i] = so.done;
+      nagari[i] = so.nagari;
+      status[i] = (i16)so.status;
+      committed[i] = so.committed;
+    } else {  // torch50_ext.cu:108-118: a zero child
 #pragma unroll
-    for (int k = 0; k < kRowWords; ++k) row[k] = 0;
-    reward[i] = 0.0f;
-    done[i] = 1;
-    nagari[i] = 0;
-    status[i] = CUGO_INVALID_INDEX_STATUS;
-    committed[i] = 0;
+      for (int k = 0; k < kRowWords; ++k) row[k] = 0;
+      reward[i] = 0.0f;
+      done[i] = 1;
+      nagari[i] = 0;
+      status[i] = CUGO_INVALID_INDEX_STATUS;
+      committed[i] = 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kRowWords; ++k) tile[lane * kRowWords + k] = row[k];
   }
-  u64* out = children + i * kRowWords;
+  // The tile's child rows leave as one contiguous block: stored from registers, a store
+  // instruction wrote 8 bytes into each of 64 rows 248 bytes apart, and the L1's queue of
+  // partial-line writes stalled the wave most of the time.
+  __syncthreads();
+  u64* out = children + base * kRowWords;
+  const int words = count * kRowWords;
 #pragma unroll
-  for (int k = 0; k < kRowWords; ++k) out[k] = row[k];
+  for (int j = 0; j < kRowWords; ++j) {
+    const int w = j * kTile + lane;
+    if (w < words) out[w] = tile[w];
+  }
 }
 
 // ------------------------------------------------------------ random play ----
@@ -785,6 +800,8 @@ __global__ __launch_bounds__(kPlayThreads) void branch_observe_kernel(
       for (int k = 0; k < kRowWords; ++k) out[k] = row[k];
     }
   }
+  // (Staging these rows through LDS as branch_kernel does measured 5 % slower here: wave
+  // 0 joins the observation's stores later.)
   store_observation<2>(t.out, base, count, features, legal, &next_item);  // wave 0 after its rows
 }
 
