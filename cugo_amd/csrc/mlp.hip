@@ -6,29 +6,39 @@
 //   z = LN(h);  logits = z W_l^T + b_l;  value = z w_v + b_v
 // With one GEMM per layer through a library, every layer reads and writes a [B, 512]
 // activation tensor in HBM and each residual add + LayerNorm is another pass over two of
-// them.  Here a workgroup owns 64 rows for the whole network: the residual stream h stays
-// in the wavefronts' MFMA accumulators (fp32), each layer's bf16 input (x, LN(h) or
-// relu(...)) sits in LDS, and only the weights stream in from L2.
+// them.  Here a workgroup owns 128 rows for the whole network: the residual stream h stays
+// in the wavefronts' MFMA accumulators (fp32), each layer's bf16 input sits in LDS, and
+// only the weights stream in from L2.
 //
-// Layout of the work (512 threads, 8 wavefronts, two per SIMD, one workgroup per CU):
-//   * wavefront w computes output columns [64 w, 64 w + 64) of every 512-wide layer for
-//     all 64 rows: 4 x 4 tiles of 16 x 16, v_mfma_f32_16x16x32_bf16 over K in steps of 32
+// Why 128 rows: every workgroup reads all 4.07 MB of weights once, so the weight bytes a
+// CU pulls through its L1 per FLOP fall as the rows of a tile grow.  With 64-row tiles the
+// L1's fill rate (about 17 bytes a cycle per CU, its miss queue full a third of the time)
+// bounded the kernel with the MFMA pipe a quarter busy.
+//
+// Layout of the work (512 threads, 8 wavefronts, two per SIMD, one workgroup per CU; 256
+// registers a lane, the accumulators in AGPRs):
+//   * wavefront w owns columns [64 w, 64 w + 64) of h for all 128 rows: 8 x 4 tiles of
+//     16 x 16 (128 accumulator registers), v_mfma_f32_16x16x32_bf16 over K in steps of 32
 //     (lane l holds A[l % 16][8 (l / 16) + 0..7], B[8 (l / 16) + 0..7][l % 16] and
 //     D[4 (l / 16) + 0..3][l % 16]);
-//   * A fragments are 16-byte LDS reads of the row-major bf16 activation (row stride 520
-//     elements, so the 16 rows of a fragment start on different banks);
+//   * LDS holds Z, the 128 x 512 bf16 input of the current layer (128 KiB), and U, one
+//     128-column chunk of relu(fc1) (32 KiB): fc1 and fc2 run chunk by chunk, fc1's chunk
+//     on a 2 x 4 grid of wavefronts (64 rows x 32 columns each) into U, then h += U W2's
+//     matching K slice.  Z and U store 16-byte group g of row r at g ^ (r & 7), so the 16
+//     rows of an A fragment read 8 different bank slots without padding (160 KiB in all);
+//   * the input x passes through Z in two column slices ([0, 512) and [512, 768));
 //   * B fragments come from weights packed once in fragment order (cugo_mlp_pack_weight):
 //     the 64 lanes' 8 values of one (16-row tile, K step) are 1 KiB of contiguous memory,
-//     so one load instruction is a contiguous 1 KiB read.  Read straight from the Linear
-//     weight [out, in], the 16 lanes of a quarter-wave would touch 16 rows, 16 cache
-//     lines per quarter-wave: the L1's tag lookups, not the MFMAs, bounded that form
-//     (0.29 ms for 32,768 rows);
-//   * the B fragments sit in a ring of registers kDepth K steps ahead of the MFMAs (the K
-//     loop is unrolled, so the ring is indexed statically);
+//     so one load instruction is a contiguous 1 KiB read; they sit in a ring of registers
+//     a few K steps ahead of the MFMAs, and the next step's A fragments are read from LDS
+//     while the current step's MFMAs issue;
 //   * LayerNorm: per-row sum and sum of squares over a wavefront's 64 columns by
-//     shuffles, across the 8 wavefronts through LDS;
+//     shuffles, across the 8 wavefronts through LDS (over U, which is free then);
 //   * the head (up to 255 logits + the value) is one 256-wide layer, 32 columns a
 //     wavefront.
+// Why not four wavefronts of 128 columns each: h alone would then fill the 256
+// accumulator registers a lane can address, and the compiler gives every MFMA of a kernel
+// the same accumulator file, so fc1's accumulators would have nowhere to go.
 // Arithmetic: bf16 operands, fp32 accumulation; h is kept in fp32 between blocks (the
 // layer-by-layer path rounds it to bf16), LN statistics in fp32.
 #include <hip/hip_runtime.h>
@@ -44,30 +54,36 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 512;                  // hidden width
-constexpr int kM = 64;                   // rows per workgroup
+constexpr int kM = 128;                  // rows per workgroup
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMT = kM / 16;             // row tiles
-constexpr int kNT = kD / (16 * kWaves);  // column tiles per wavefront
+constexpr int kNT = kD / (16 * kWaves);  // column tiles of h per wavefront
 constexpr int kK = 32;                   // K per MFMA
 constexpr int kFrag = 64 * 8;            // elements of one packed B fragment
-constexpr int kZS = kD + 8;              // LDS row stride (elements) of the activations
+constexpr int kSteps = kD / kK;          // K steps of a 512-wide layer
+constexpr int kChunk = 128;              // fc1 columns per chunk
+constexpr int kChunks = kD / kChunk;
+constexpr int kZGroups = kD / 8;         // 16-byte groups in a row of Z
 constexpr int kHeadN = CUGO_MLP_HEAD_ROWS;  // logits + value, padded
 constexpr int kHeadNT = kHeadN / (16 * kWaves);
 constexpr int kMaxIn = CUGO_MLP_MAX_FEATURES;
 constexpr int kMaxBlocks = CUGO_MLP_MAX_BLOCKS;
 constexpr int kInSteps = kMaxIn / kK;    // K steps of the input layer (zero-padded)
-// K steps of weights in flight ahead of the MFMAs (CUGO_MLP_DEPTH pins it for tuning
-// builds).
-#ifdef CUGO_MLP_DEPTH
-constexpr int kDepth = CUGO_MLP_DEPTH;
-#else
-constexpr int kDepth = 4;
-#endif
-constexpr int kActBytes = kM * kZS * 2;                  // one activation buffer
-constexpr int kSmemBytes = 2 * kActBytes;                // Z and U (x overlays both)
-static_assert(kM * (kMaxIn + 8) * 2 <= kSmemBytes, "the input tile must fit in Z and U");
-static_assert(kMaxIn % kK == 0 && kHeadN % (16 * kWaves) == 0, "whole tiles");
+constexpr int kInSlice2 = kInSteps - kSteps;  // K steps of the input's second slice
+// K steps of weights in flight ahead of the MFMAs: the ring costs (depth + 1) x NT x 4
+// registers.
+constexpr int kDepthWide = 2;    // the 4-tile GEMMs (h's columns, the head)
+constexpr int kDepthNarrow = 3;  // fc1's 2-tile chunk GEMM
+// fc1's grid of wavefronts over a 128 x 128 chunk
+constexpr int kGridRows = 2;
+constexpr int kGridCols = kWaves / kGridRows;
+constexpr int kU_MT = kMT / kGridRows;                // 4 row tiles
+constexpr int kU_NT = kChunk / (16 * kGridCols);      // 2 column tiles
+static_assert(kMaxIn % kK == 0 && kInSlice2 > 0 && kInSlice2 <= kSteps, "input slices");
+static_assert(kHeadN % (16 * kWaves) == 0 && kChunk % (16 * 2) == 0, "whole tiles");
+static_assert((kM * kD + kM * kChunk) * 2 <= 160 * 1024, "Z and U fit the LDS");
+static_assert((kWaves + 1) * kM * 2 * 4 <= kM * kChunk * 2, "the LayerNorm sums fit in U");
 
 struct Weights {
   const __bf16* w_in;  // packed, kD x kMaxIn
@@ -84,73 +100,155 @@ struct Weights {
   float eps;
 };
 
-// acc[mt][t] += A[16 mt .., 0..32 STEPS) x B[.., 16 (tile0 + t) ..], A a row-major bf16
-// LDS tile, B packed in fragment order: fragment (n tile, K step) at (tile * STEPS +
-// step) * kFrag, lane l's 8 values at l * 8.  The K steps run from step `rot` round to
-// `rot` - 1: workgroups that start together read the same weights, and a different
-// starting step per workgroup spreads their reads over the matrix.
-template <int NT, int STEPS>
-__device__ inline void gemm(f32x4 (&acc)[kMT][NT], const __bf16* A, int a_stride,
-                            const __bf16* packed, int tile0, int lane, int l16, int q4,
-                            int rot) {
-  constexpr int R = kDepth + 1;
-  rot %= STEPS;
-  const __bf16* base = packed + (size_t)tile0 * STEPS * kFrag + lane * 8;
-  const __bf16* a_base = A + l16 * a_stride + 8 * q4;
-  auto step_of = [rot](int s) {  // uniform over the workgroup
-    int sk = s + rot;
-    return sk - (sk >= STEPS ? STEPS : 0);
+// Element offset of (row r, column k) in an LDS activation tile of kM rows: K step by K
+// step ([k / 32][r][32]), so one MFMA A fragment (16 rows, one K step) is 1 KiB and the
+// next row tile 1 KiB further; within a row's 64 bytes, 16-byte group g sits at
+// g ^ ((r >> 1) & 3), so the 16 rows of a fragment read at one group cover every bank.
+__device__ inline int swz(int r, int k) {
+  return ((k >> 5) * kM + r) * 32 + (((((k >> 3) & 3) ^ ((r >> 1) & 3))) << 3) + (k & 7);
+}
+
+// Where the accumulator layout lands in a swz() tile: element (r0 + 16 mt + 4 q4 + i,
+// c0 + 16 t + l16), r0 a multiple of 8 and c0 of 32, is at
+//   base[2 (t & 1) + (i >> 1)] + (c0 / 32 + t / 2) * 32 kM + 32 r0 + 512 mt + 32 i,
+// base[c] = 128 q4 + (l16 & 7) + 8 (((2 (q4 & 1)) | (l16 >> 3)) ^ c): four lane bases and
+// static offsets, so a layer's stores hold four address registers.
+struct StoreBases {
+  int base[4];
+  __device__ StoreBases(int q4, int l16) {
+    const int xl = (2 * (q4 & 1)) | (l16 >> 3);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) base[c] = 128 * q4 + (l16 & 7) + ((xl ^ c) << 3);
+  }
+  __device__ int at(int r0, int c0, int mt, int t, int i) const {
+    return base[(2 * (t & 1)) | (i >> 1)] + (c0 / 32 + t / 2) * 32 * kM + 32 * r0 + 512 * mt +
+           32 * i;
+  }
+};
+
+// A GEMM's B operand: a matrix packed in fragment order with steps_total K steps a tile
+// (fragment (tile, step) at (tile * steps_total + step) * kFrag, lane l's 8 values at l * 8),
+// from n tile tile0 and K step kbase on.  It is read through a buffer resource: the lane's
+// byte offset is one register for every load and the rest of the offset is a scalar, so
+// the loads hold no 64-bit address registers.
+struct BSrc {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int b0, ts;  // bytes: the first fragment, the distance between n tiles
+  __device__ BSrc(__amdgpu_buffer_rsrc_t r, int steps_total, int tile0, int kbase)
+      : rsrc(r), b0((tile0 * steps_total + kbase) * kFrag * 2), ts(steps_total * kFrag * 2) {}
+  __device__ bf16x8 at(int t, int s, int lane_off) const {
+    return __builtin_bit_cast(
+        bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off, b0 + t * ts + s * kFrag * 2, 0));
+  }
+};
+
+// The first DEPTH K steps of a GEMM's B fragments, into its ring: issued ahead of the
+// GEMM (before a barrier or an LDS phase), so their latency is not the GEMM's first wait.
+template <int NT, int NSTEPS, int DEPTH>
+__device__ inline void ring_fill(bf16x8 (&b)[DEPTH + 1][NT], const BSrc& src, int lane) {
+#pragma unroll
+  for (int j = 0; j < DEPTH; ++j)
+    if (j < NSTEPS) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) b[j][t] = src.at(t, j, lane * 16);
+    }
+}
+
+// acc[mt][t] += A[rows a_row0 + 16 mt .., K steps 0 .. NSTEPS) x B[K steps .., n tile t],
+// with the ring b filled by ring_fill.  A is an LDS tile laid out by swz(); its fragments
+// are one lane base plus static offsets.
+template <int MT, int NT, int NSTEPS, int DEPTH, int ABUF>
+__device__ inline void gemm_run(f32x4 (&acc)[MT][NT], bf16x8 (&b)[DEPTH + 1][NT],
+                                const BSrc& src, const __bf16* A, int a_row0, int lane,
+                                int l16, int q4) {
+  constexpr int R = DEPTH + 1;
+  const int lane_off = lane * 16;
+  // swz(a_row0 + 16 mt + l16, 32 s + 8 q4) = a_lane + s * 32 kM + mt * 512.  K steps from 8
+  // on are past a DS read's 16-bit byte offset, so they get a second base, kept opaque:
+  // otherwise the compiler makes one address register per (step, row tile) and shares them
+  // between GEMMs, and they spill.
+  const int a_lane = (a_row0 + l16) * 32 + ((q4 ^ ((l16 >> 1) & 3)) << 3);
+  int a_hi = a_lane + 8 * 32 * kM;
+  asm volatile("" : "+v"(a_hi));
+  auto a_at = [&](int mt, int s) {
+    const int at = s < 8 ? a_lane + s * 32 * kM : a_hi + (s - 8) * 32 * kM;
+    return *reinterpret_cast<const bf16x8*>(A + at + mt * 512);
   };
-  bf16x8 b[R][NT];
+  // ABUF = 2: the next step's A fragments are read while this step's MFMAs issue; 1: each
+  // step reads its own (the other wavefront of the SIMD covers the LDS latency).
+  bf16x8 a[ABUF][MT];
 #pragma unroll
-  for (int j = 0; j < kDepth; ++j)
-    if (j < STEPS) {
-      const int sk = step_of(j);
+  for (int mt = 0; mt < MT; ++mt) a[0][mt] = a_at(mt, 0);
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        b[j][t] = *reinterpret_cast<const bf16x8*>(base + (size_t)(t * STEPS + sk) * kFrag);
+  for (int s = 0; s < NSTEPS; ++s) {
+    if (s + DEPTH < NSTEPS) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) b[(s + DEPTH) % R][t] = src.at(t, s + DEPTH, lane_off);
+    }
+    if (ABUF == 2 && s + 1 < NSTEPS) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) a[(s + 1) % ABUF][mt] = a_at(mt, s + 1);
+    }
+    if (ABUF == 1 && s > 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) a[0][mt] = a_at(mt, s);
     }
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    if (s + kDepth < STEPS) {
-      const int sk = step_of(s + kDepth);
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        b[(s + kDepth) % R][t] =
-            *reinterpret_cast<const bf16x8*>(base + (size_t)(t * STEPS + sk) * kFrag);
-    }
-    const int k = step_of(s) * kK;
-    bf16x8 a[kMT];
-#pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
-      a[mt] = *reinterpret_cast<const bf16x8*>(a_base + 16 * mt * a_stride + k);
-#pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        acc[mt][t] =
-            __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], b[s % R][t], acc[mt][t], 0, 0, 0);
+        acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s % ABUF][mt], b[s % R][t],
+                                                             acc[mt][t], 0, 0, 0);
+    // Keep the ring: without a fence the scheduler hoists every K step's loads to the top
+    // of the unrolled loop, and their registers spill.
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
+// ring_fill + gemm_run.
+template <int MT, int NT, int NSTEPS, int DEPTH, int ABUF>
+__device__ inline void gemm(f32x4 (&acc)[MT][NT], const BSrc& src, const __bf16* A, int a_row0,
+                            int lane, int l16, int q4) {
+  bf16x8 b[DEPTH + 1][NT];
+  ring_fill<NT, NSTEPS, DEPTH>(b, src, lane);
+  gemm_run<MT, NT, NSTEPS, DEPTH, ABUF>(acc, b, src, A, a_row0, lane, l16, q4);
+}
+
 // acc[..][t][i] = bias[n0 + 16 t + l16] (every row).
-template <int NT>
-__device__ inline void set_bias(f32x4 (&acc)[kMT][NT], const __bf16* bias, int n0, int l16) {
+template <int MT, int NT>
+__device__ inline void set_bias(f32x4 (&acc)[MT][NT], const __bf16* bias, int n0, int l16) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const float v = (float)bias[n0 + 16 * t + l16];
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt) acc[mt][t] = f32x4{v, v, v, v};
+    for (int mt = 0; mt < MT; ++mt) acc[mt][t] = f32x4{v, v, v, v};
   }
 }
 
+// Sum over the 16 lanes of a DPP row (lanes 16 k .. 16 k + 15), left in every one of them:
+// xor 1 and xor 2 within quads, then the half-row and row mirrors.
+template <int kCtrl>
+__device__ inline float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl,
+                                                            0xf, 0xf, true));
+}
+__device__ inline float row16_sum(float v) {
+  v += dpp_mov<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return v;
+}
+
 // Z[r][n] = bf16(LN(h)[r][n] * gamma[n] + beta[n]) for the wavefront's columns; every
-// wavefront calls it (one barrier inside: the per-row partial sums cross wavefronts in
-// `red`).
+// wavefront calls it.  Per-row partial sums (sum, sum of squares over a wavefront's
+// columns) go to `red` (over U); after a barrier, thread r < kM turns row r's into
+// (rstd, -mean * rstd) once; after a second barrier every lane reads its rows' pair and
+// normalises with two FMAs a value.
 __device__ inline void layer_norm(const f32x4 (&h)[kMT][kNT], const __bf16* gamma,
                                   const __bf16* beta, float eps, __bf16* Z, float* red,
-                                  int wave, int l16, int q4) {
-  float s[kMT][4], ss[kMT][4];
+                                  int wave, int l16, int q4, int tid) {
+  float* stats = red + kWaves * kM * 2;  // [kM][2]
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
@@ -162,56 +260,46 @@ __device__ inline void layer_norm(const f32x4 (&h)[kMT][kNT], const __bf16* gamm
         a += v;
         b = __builtin_fmaf(v, v, b);
       }
-      s[mt][i] = a;
-      ss[mt][i] = b;
-    }
-  // the 16 lanes with the same q4 hold the same rows
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1)
-#pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        s[mt][i] += __shfl_xor(s[mt][i], off, 64);
-        ss[mt][i] += __shfl_xor(ss[mt][i], off, 64);
-      }
-  if (l16 == 0) {
-#pragma unroll
-    for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      // the 16 lanes with the same q4 hold the same rows
+      a = row16_sum(a);
+      b = row16_sum(b);
+      if (l16 == 0) {
         const int r = 16 * mt + 4 * q4 + i;
-        red[(wave * kM + r) * 2] = s[mt][i];
-        red[(wave * kM + r) * 2 + 1] = ss[mt][i];
+        *reinterpret_cast<float2*>(red + (wave * kM + r) * 2) = make_float2(a, b);
       }
+    }
+  __syncthreads();
+  if (tid < kM) {
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float2 p = *reinterpret_cast<const float2*>(red + (w * kM + tid) * 2);
+      a += p.x;
+      b += p.y;
+    }
+    const float mean = a * (1.f / kD);
+    const float var = fmaxf(b * (1.f / kD) - mean * mean, 0.f);
+    const float rstd = __builtin_amdgcn_rsqf(var + eps);  // hardware reciprocal square root
+    *reinterpret_cast<float2*>(stats + tid * 2) = make_float2(rstd, -mean * rstd);
   }
   __syncthreads();
+  const int n0 = wave * (16 * kNT);
+  const StoreBases sb(q4, l16);
   float g[kNT], be[kNT];
 #pragma unroll
   for (int t = 0; t < kNT; ++t) {
-    const int n = wave * (16 * kNT) + 16 * t + l16;
-    g[t] = (float)gamma[n];
-    be[t] = (float)beta[n];
+    g[t] = (float)gamma[n0 + 16 * t + l16];
+    be[t] = (float)beta[n0 + 16 * t + l16];
   }
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * mt + 4 * q4 + i;
-      float a = 0.f, b = 0.f;
+      const float2 st = *reinterpret_cast<const float2*>(stats + (16 * mt + 4 * q4 + i) * 2);
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        a += red[(w * kM + r) * 2];
-        b += red[(w * kM + r) * 2 + 1];
-      }
-      const float mean = a * (1.f / kD);
-      const float var = fmaxf(b * (1.f / kD) - mean * mean, 0.f);
-      const float rstd = 1.f / sqrtf(var + eps);
-#pragma unroll
-      for (int t = 0; t < kNT; ++t) {
-        const int n = wave * (16 * kNT) + 16 * t + l16;
-        Z[r * kZS + n] = (__bf16)((h[mt][t][i] - mean) * rstd * g[t] + be[t]);
-      }
+      for (int t = 0; t < kNT; ++t)
+        Z[sb.at(0, n0, mt, t, i)] = (__bf16)__builtin_fmaf(
+            __builtin_fmaf(h[mt][t][i], st.x, st.y), g[t], be[t]);
     }
 }
 
@@ -219,127 +307,138 @@ template <class TIn>
 struct Input;
 template <>
 struct Input<float> {
-  // four elements as bf16
-  __device__ static uint2 load4(const float* p) {
-    const float4 v = *reinterpret_cast<const float4*>(p);
-    uint2 r;
-    r.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v.x) |
-          ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v.y) << 16);
-    r.y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v.z) |
-          ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v.w) << 16);
-    return r;
+  // eight elements as bf16 (round to nearest even, as torch's conversion)
+  __device__ static uint4 load8(const float* p) {
+    const float4 v0 = *reinterpret_cast<const float4*>(p);
+    const float4 v1 = *reinterpret_cast<const float4*>(p + 4);
+    auto two = [](float lo, float hi) {
+      return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+    };
+    return make_uint4(two(v0.x, v0.y), two(v0.z, v0.w), two(v1.x, v1.y), two(v1.z, v1.w));
   }
 };
 template <>
 struct Input<__bf16> {
-  __device__ static uint2 load4(const __bf16* p) { return *reinterpret_cast<const uint2*>(p); }
+  __device__ static uint4 load8(const __bf16* p) { return *reinterpret_cast<const uint4*>(p); }
 };
 
+// Columns [c0, c0 + 8 GROUPS) of the tile's rows of x -> Z's groups 0 .. GROUPS (bf16;
+// zero past the features and past the last row), and their bf16 copy to x_copy.  Loads at
+// clamped indices are issued eight at a time before any is used.
+template <class TIn, int GROUPS>
+__device__ inline void load_input(const TIn* __restrict__ x, __bf16* __restrict__ x_copy,
+                                  int64_t n, int F, int64_t row0, int c0, __bf16* Z, int tid) {
+  constexpr int kTotal = kM * GROUPS;
+  static_assert(kTotal % (kThreads * 8) == 0, "whole batches");
+#pragma unroll 1
+  for (int j0 = 0; j0 < kTotal; j0 += kThreads * 8) {
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u * kThreads + tid;
+      const int r = j / GROUPS;
+      const int col = c0 + 8 * (j - r * GROUPS);
+      const int64_t g = row0 + r < n ? row0 + r : n - 1;
+      v[u] = Input<TIn>::load8(x + g * F + (col < F ? col : F - 8));
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + u * kThreads + tid;
+      const int r = j / GROUPS;
+      const int col = c0 + 8 * (j - r * GROUPS);
+      const bool valid = row0 + r < n && col < F;
+      const uint4 val = valid ? v[u] : make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4*>(Z + swz(r, col - c0)) = val;
+      if (x_copy != nullptr && valid)
+        *reinterpret_cast<uint4*>(x_copy + (row0 + r) * F + col) = val;
+    }
+  }
+}
+
 template <class TIn>
-__global__ __launch_bounds__(kThreads, 1) void actor_kernel(const TIn* __restrict__ x,
+__global__ __launch_bounds__(kThreads) void actor_kernel(const TIn* __restrict__ x,
                                                             __bf16* __restrict__ x_copy,
                                                             int64_t n, Weights w,
                                                             __bf16* __restrict__ logits,
                                                             float* __restrict__ value) {
-  __shared__ __attribute__((aligned(16))) __bf16 smem[kSmemBytes / 2];
-  __shared__ float red[kWaves * kM * 2];
+  __shared__ __attribute__((aligned(16))) __bf16 smem[kM * kD + kM * kChunk];
   __bf16* Z = smem;
-  __bf16* U = smem + kActBytes / 2;
-  __bf16* X = smem;  // the input tile, before the first LayerNorm
+  __bf16* U = smem + kM * kD;
+  float* red = reinterpret_cast<float*>(U);  // LayerNorm sums, while U is free
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
   const int64_t row0 = (int64_t)blockIdx.x * kM;
   const int F = w.features;
-  constexpr int xs = kMaxIn + 8;  // LDS row stride of the input tile
-
-  // ---- input tile -> LDS (bf16, zero columns up to kMaxIn), and its bf16 copy to x_copy
-  {
-    const int quads = F / 4;
-    const int total = kM * quads;
-    for (int j0 = 0; j0 < total; j0 += kThreads * 8) {
-      uint2 v[8];
-      int r[8], c[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u * kThreads + tid;
-        const int jj = j < total ? j : total - 1;
-        r[u] = jj / quads;
-        c[u] = jj - r[u] * quads;
-        const int64_t g = row0 + r[u] < n ? row0 + r[u] : n - 1;
-        v[u] = Input<TIn>::load4(x + g * F + 4 * c[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u * kThreads + tid;
-        if (j >= total) continue;
-        const bool valid = row0 + r[u] < n;
-        const uint2 val = valid ? v[u] : make_uint2(0u, 0u);
-        *reinterpret_cast<uint2*>(X + r[u] * xs + 4 * c[u]) = val;
-        if (x_copy != nullptr && valid)
-          *reinterpret_cast<uint2*>(x_copy + (row0 + r[u]) * F + 4 * c[u]) = val;
-      }
-    }
-    const int pad = kMaxIn - F;
-    if (pad > 0)
-      for (int j = tid; j < kM * pad; j += kThreads)
-        X[(j / pad) * xs + F + j % pad] = (__bf16)0.f;
-  }
-  __syncthreads();
-
-  const int n0 = wave * (16 * kNT);  // this wavefront's first column of a 512-wide layer
+  const int n0 = wave * (16 * kNT);  // this wavefront's first column of h
   const int tile0 = n0 / 16;
-  const int rot = (int)(blockIdx.x % 64u);  // first K step of this workgroup's GEMMs
-  f32x4 h[kMT][kNT];
-  set_bias<kNT>(h, w.b_in, n0, l16);
-  gemm<kNT, kInSteps>(h, X, xs, w.w_in, tile0, lane, l16, q4, rot);
+  // fc1's grid: rows [64 wr, 64 wr + 64), chunk columns [32 wc, 32 wc + 32)
+  const int wr = wave / kGridCols, wc = wave % kGridCols;
+  const StoreBases sb(q4, l16);
 
+  auto rsrc = [](const __bf16* p, int rows, int cols) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(p), (short)0, rows * cols * 2,
+                                             0x00020000);
+  };
+
+  // ---- input layer, x in two column slices through Z
+  f32x4 h[kMT][kNT];
+  set_bias<kMT, kNT>(h, w.b_in, n0, l16);
+  const auto w_in = rsrc(w.w_in, kD, kMaxIn);
+  load_input<TIn, kZGroups>(x, x_copy, n, F, row0, 0, Z, tid);
+  __syncthreads();
+  gemm<kMT, kNT, kSteps, kDepthWide, 1>(h, BSrc(w_in, kInSteps, tile0, 0), Z, 0, lane, l16, q4);
+  __syncthreads();  // Z read
+  load_input<TIn, kInSlice2 * kK / 8>(x, x_copy, n, F, row0, kD, Z, tid);
+  __syncthreads();
+  gemm<kMT, kNT, kInSlice2, kDepthWide, 1>(h, BSrc(w_in, kInSteps, tile0, kSteps), Z, 0, lane,
+                                           l16, q4);
+
+  const int ucol = 16 * kU_NT * wc;  // this wavefront's columns within a chunk
+  const int urow = 16 * kU_MT * wr;
   for (int b = 0; b < w.blocks; ++b) {
-    // z = LN(h) -> Z.  The barrier inside comes after every wavefront's last read of the
-    // previous layer's input (X or Z), so Z can be overwritten after it.
-    layer_norm(h, w.ln_w[b], w.ln_b[b], w.eps, Z, red, wave, l16, q4);
+    const auto w1 = rsrc(w.w1[b], kD, kD);
+    const auto w2 = rsrc(w.w2[b], kD, kD);
+    // z = LN(h) -> Z.  The barriers inside come after every wavefront's last read of the
+    // previous layer's input (Z) and of U, so both can be overwritten after them.
+    layer_norm(h, w.ln_w[b], w.ln_b[b], w.eps, Z, red, wave, l16, q4, tid);
     __syncthreads();  // Z complete
-    // fc1 in two halves of the wavefront's columns, so that its accumulators, h and the
-    // weight ring fit the 256 registers two wavefronts per SIMD allow.  relu(u) -> U (last
-    // read by the previous block's second layer, before the barrier above).
-    constexpr int kHalf = kNT / 2;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int c0 = n0 + 16 * kHalf * half;
-      f32x4 u[kMT][kHalf];
-      set_bias<kHalf>(u, w.b1[b], c0, l16);
-      gemm<kHalf, kD / kK>(u, Z, kZS, w.w1[b], c0 / 16, lane, l16, q4, rot);
+    for (int c = 0; c < kChunks; ++c) {
+      f32x4 u[kU_MT][kU_NT];
+      set_bias<kU_MT, kU_NT>(u, w.b1[b], kChunk * c + ucol, l16);
+      gemm<kU_MT, kU_NT, kSteps, kDepthNarrow, 2>(u, BSrc(w1, kSteps, (kChunk * c + ucol) / 16, 0),
+                                                   Z, urow, lane, l16, q4);
 #pragma unroll
-      for (int mt = 0; mt < kMT; ++mt)
+      for (int mt = 0; mt < kU_MT; ++mt)
 #pragma unroll
-        for (int t = 0; t < kHalf; ++t)
+        for (int t = 0; t < kU_NT; ++t)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            U[(16 * mt + 4 * q4 + i) * kZS + c0 + 16 * t + l16] =
-                (__bf16)fmaxf(u[mt][t][i], 0.f);
+            U[sb.at(urow, ucol, mt, t, i)] = (__bf16)fmaxf(u[mt][t][i], 0.f);
+      __syncthreads();  // U complete
+      gemm<kMT, kNT, kChunk / kK, kDepthWide, 1>(h, BSrc(w2, kSteps, tile0, c * (kChunk / kK)), U,
+                                                 0, lane, l16, q4);
+      __syncthreads();  // U read
     }
-    __syncthreads();  // U complete
-    {
-      const __bf16* b2 = w.b2[b];
+    const __bf16* b2 = w.b2[b];
 #pragma unroll
-      for (int t = 0; t < kNT; ++t) {
-        const float v = (float)b2[n0 + 16 * t + l16];
+    for (int t = 0; t < kNT; ++t) {
+      const float v = (float)b2[n0 + 16 * t + l16];
 #pragma unroll
-        for (int mt = 0; mt < kMT; ++mt) h[mt][t] += f32x4{v, v, v, v};
-      }
-      gemm<kNT, kD / kK>(h, U, kZS, w.w2[b], tile0, lane, l16, q4, rot);
+      for (int mt = 0; mt < kMT; ++mt) h[mt][t] += f32x4{v, v, v, v};
     }
   }
-
-  layer_norm(h, w.ln_w[w.blocks], w.ln_b[w.blocks], w.eps, Z, red, wave, l16, q4);
-  __syncthreads();  // Z complete
 
   // ---- head: columns [0, A) logits, A the value, the rest padding (zero weights)
   const int A = w.actions;
   const int hn0 = wave * (16 * kHeadNT);
+  layer_norm(h, w.ln_w[w.blocks], w.ln_b[w.blocks], w.eps, Z, red, wave, l16, q4, tid);
+  __syncthreads();  // Z complete
   f32x4 o[kMT][kHeadNT];
 #pragma unroll
   for (int t = 0; t < kHeadNT; ++t) {
@@ -348,7 +447,8 @@ __global__ __launch_bounds__(kThreads, 1) void actor_kernel(const TIn* __restric
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt) o[mt][t] = f32x4{v, v, v, v};
   }
-  gemm<kHeadNT, kD / kK>(o, Z, kZS, w.w_head, hn0 / 16, lane, l16, q4, rot);
+  gemm<kMT, kHeadNT, kSteps, kDepthNarrow, 1>(o, BSrc(rsrc(w.w_head, kHeadN, kD), kSteps, hn0 / 16, 0),
+                                              Z, 0, lane, l16, q4);
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
