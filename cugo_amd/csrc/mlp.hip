@@ -135,7 +135,11 @@ struct BSrc {
   __amdgpu_buffer_rsrc_t rsrc;
   int b0, ts;  // bytes: the first fragment, the distance between n tiles
   __device__ BSrc(__amdgpu_buffer_rsrc_t r, int steps_total, int tile0, int kbase)
-      : rsrc(r), b0((tile0 * steps_total + kbase) * kFrag * 2), ts(steps_total * kFrag * 2) {}
+      : rsrc(r), b0((tile0 * steps_total + kbase) * kFrag * 2), ts(steps_total * kFrag * 2) {
+    // Opaque where the GEMM starts: otherwise the scalar offsets of every load of the
+    // unrolled chunk loop are hoisted out of the blocks loop together, and they spill.
+    asm volatile("" : "+s"(b0));
+  }
   __device__ bf16x8 at(int t, int s, int lane_off) const {
     return __builtin_bit_cast(
         bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off, b0 + t * ts + s * kFrag * 2, 0));
@@ -232,12 +236,18 @@ __device__ inline float dpp_mov(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl,
                                                             0xf, 0xf, true));
 }
-__device__ inline float row16_sum(float v) {
-  v += dpp_mov<0xb1>(v);   // quad_perm [1, 0, 3, 2]
-  v += dpp_mov<0x4e>(v);   // quad_perm [2, 3, 0, 1]
-  v += dpp_mov<0x141>(v);  // row_half_mirror
-  v += dpp_mov<0x140>(v);  // row_mirror
-  return v;
+// v[j] = its sum over the 16 lanes of a DPP row (lanes 16 k .. 16 k + 15), left in every
+// one of them: xor 1 and xor 2 within quads, then the half-row and row mirrors.
+template <int N>
+__device__ inline void row16_sums(float (&v)[N]) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] += dpp_mov<0xb1>(v[j]);   // quad_perm [1, 0, 3, 2]
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] += dpp_mov<0x4e>(v[j]);   // quad_perm [2, 3, 0, 1]
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] += dpp_mov<0x141>(v[j]);  // row_half_mirror
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] += dpp_mov<0x140>(v[j]);  // row_mirror
 }
 
 // Z[r][n] = bf16(LN(h)[r][n] * gamma[n] + beta[n]) for the wavefront's columns; every
@@ -249,25 +259,41 @@ __device__ inline void layer_norm(const f32x4 (&h)[kMT][kNT], const __bf16* gamm
                                   const __bf16* beta, float eps, __bf16* Z, float* red,
                                   int wave, int l16, int q4, int tid) {
   float* stats = red + kWaves * kM * 2;  // [kM][2]
+  // per (row tile, row) partial sums, half the row tiles at a time; their DPP reductions
+  // run stage by stage, so consecutive DPP reads never depend on the instruction just
+  // before them
+  constexpr int kHalf = kMT / 2;
 #pragma unroll
-  for (int mt = 0; mt < kMT; ++mt)
+  for (int half = 0; half < 2; ++half) {
+    float a[kHalf * 4], b[kHalf * 4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float a = 0.f, b = 0.f;
+    for (int m = 0; m < kHalf; ++m)
 #pragma unroll
-      for (int t = 0; t < kNT; ++t) {
-        const float v = h[mt][t][i];
-        a += v;
-        b = __builtin_fmaf(v, v, b);
+      for (int i = 0; i < 4; ++i) {
+        float x = 0.f, y = 0.f;
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) {
+          const float v = h[half * kHalf + m][t][i];
+          x += v;
+          y = __builtin_fmaf(v, v, y);
+        }
+        a[m * 4 + i] = x;
+        b[m * 4 + i] = y;
       }
-      // the 16 lanes with the same q4 hold the same rows
-      a = row16_sum(a);
-      b = row16_sum(b);
-      if (l16 == 0) {
-        const int r = 16 * mt + 4 * q4 + i;
-        *reinterpret_cast<float2*>(red + (wave * kM + r) * 2) = make_float2(a, b);
-      }
+    // the 16 lanes with the same q4 hold the same rows
+    row16_sums<kHalf * 4>(a);
+    row16_sums<kHalf * 4>(b);
+    if (l16 == 0) {
+#pragma unroll
+      for (int m = 0; m < kHalf; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * (half * kHalf + m) + 4 * q4 + i;
+          *reinterpret_cast<float2*>(red + (wave * kM + r) * 2) =
+              make_float2(a[m * 4 + i], b[m * 4 + i]);
+        }
     }
+  }
   __syncthreads();
   if (tid < kM) {
     float a = 0.f, b = 0.f;
