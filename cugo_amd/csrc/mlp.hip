@@ -178,31 +178,37 @@ __device__ inline void gemm_run(f32x4 (&acc)[MT][NT], bf16x8 (&b)[DEPTH + 1][NT]
     const int at = s < 8 ? a_lane + s * 32 * kM : a_hi + (s - 8) * 32 * kM;
     return *reinterpret_cast<const bf16x8*>(A + at + mt * 512);
   };
-  // ABUF = 2: the next step's A fragments are read while this step's MFMAs issue; 1: each
-  // step reads its own (the other wavefront of the SIMD covers the LDS latency).
-  bf16x8 a[ABUF][MT];
+  // ABUF = 2: the next step's A fragments are read while this step's MFMAs issue.  ABUF = 1:
+  // the same in half steps (half the row tiles' fragments at a time), for the same
+  // registers as one step's fragments.
+  constexpr int AH = ABUF == 2 ? MT : MT / 2;  // fragments a stage holds
+  static_assert(ABUF == 2 || MT % 2 == 0, "half steps need an even row tile count");
+  bf16x8 a[2][AH];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) a[0][mt] = a_at(mt, 0);
+  for (int m = 0; m < AH; ++m) a[0][m] = a_at(m, 0);
+  constexpr int kStages = ABUF == 2 ? 1 : 2;  // stages a step
 #pragma unroll
   for (int s = 0; s < NSTEPS; ++s) {
     if (s + DEPTH < NSTEPS) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) b[(s + DEPTH) % R][t] = src.at(t, s + DEPTH, lane_off);
     }
-    if (ABUF == 2 && s + 1 < NSTEPS) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) a[(s + 1) % ABUF][mt] = a_at(mt, s + 1);
+    for (int h = 0; h < kStages; ++h) {
+      const int stage = s * kStages + h;
+      const int next = stage + 1;  // the stage whose fragments load now
+      if (next < NSTEPS * kStages) {
+        const int ns = next / kStages, nh = next % kStages;
+#pragma unroll
+        for (int m = 0; m < AH; ++m) a[next & 1][m] = a_at(nh * AH + m, ns);
+      }
+#pragma unroll
+      for (int m = 0; m < AH; ++m)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          acc[h * AH + m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              a[stage & 1][m], b[s % R][t], acc[h * AH + m][t], 0, 0, 0);
     }
-    if (ABUF == 1 && s > 0) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) a[0][mt] = a_at(mt, s);
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-        acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s % ABUF][mt], b[s % R][t],
-                                                             acc[mt][t], 0, 0, 0);
     // Keep the ring: without a fence the scheduler hoists every K step's loads to the top
     // of the unrolled loop, and their registers spill.
     __builtin_amdgcn_sched_barrier(0);
