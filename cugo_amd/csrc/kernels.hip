@@ -724,6 +724,69 @@ void play_kernel(
   }
 }
 
+// ------------------------------------------------------------ step + observe ----
+// step_kernel<3> (step with the caller's actions, then the auto-reset of finished rows)
+// followed by observe_kernel of the new states, in one launch: the PPO rollout's engine
+// between two actor passes.  Two waves per tile of 64 games: both stage the rows in;
+// wave 0 steps its games, deals the finished ones their next game (the pre-dealt spare,
+// dealt into its slot first if stale, as play_kernel does), builds the new states'
+// observation records in LDS and packs the rows; then both waves store the observation
+// and the rows.  The rows are read and written once, where the two launches read them
+// twice and wrote them once more.
+template <bool kBf16>
+__global__ __launch_bounds__(kPlayThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void step_observe_kernel(u64* states, i64 n, const i64* actions, float* reward, u8* done,
+                         u8* nagari, i16* status, u8* committed, AutoReset ar, void* features,
+                         u8* legal, u8* player, u8* obs_done, i16* obs_status) {
+  __shared__ ObserveTile t;   // the rows in, the new rows out
+  __shared__ RecordBuffer rb;  // the new states' observation records
+  __shared__ int next_item;    // store_observation's work counter
+  const i64 base = tile_base();
+  const int count = tile_count(base, n);
+  const int tid = threadIdx.x;
+  const int lane = tid & (kTile - 1);
+  const int wave = tid / kTile;
+  const i64 i = base + lane;
+  if (tid == 0) next_item = 0;
+  stage_in<kPlayThreads>(t.rows, states, nullptr, base, count, n);
+  __syncthreads();
+  if (wave == 0 && lane < count) {
+    u32 gen = ar.generation[i];
+    const i64 srow = spare_row(ar, i, gen + 1u);
+    const u32 sgen = ar.spare_gen[srow];  // issued before the step so its latency hides
+    u64* row = t.rows + lane * kRowWords;
+    Env e = unpack_row(row);
+    const StepOut so = torch_step(e, clamp_action(actions[i]));
+    reward[i] = (float)so.reward0;
+    done[i] = so.done;
+    nagari[i] = so.nagari;
+    status[i] = (i16)so.status;
+    committed[i] = so.committed;
+    if (so.done) {  // the next game: its spare, dealt into the slot first if stale
+      ++gen;
+      ar.generation[i] = gen;
+      const u64 seed = ar.base_seed + (u64)i + ar.stride * gen;
+      ar.sampler[i] = sampler_seed(seed);
+      if (sgen != gen) deal_into(seed, (u32)(i & 1), ar.spares + srow * kRowWords);
+      e = unpack_row(ar.spares + srow * kRowWords);
+    }
+    const Packet pk = make_packet(e);
+    FeatRow fr;
+    feature_row(pk, c_stop_bits, fr);
+    feature_record(fr, rb.rec[lane]);
+    rb.legal[lane][0] = pk.head.legal.w0;
+    rb.legal[lane][1] = pk.head.legal.w1;
+    rb.legal[lane][2] = pk.head.legal.w2;
+    player[i] = pk.head.player;
+    obs_done[i] = e.done != 0;
+    obs_status[i] = (i16)pk.head.status;
+    pack_row(e, row);
+  }
+  __syncthreads();
+  store_observation<kPlayClaim, kBf16>(rb, base, count, features, legal, &next_item);
+  stage_out<kPlayThreads>(t.rows, states, nullptr, base, count, n);
+}
+
 // ---------------------------------------------------------- branch + observe ----
 // branch_indexed then observe_indexed of the children (the reference's callers do exactly
 // this, python/cugo_ppo50.py:96-98), in one launch with the same outputs.  Two waves per
@@ -1309,6 +1372,33 @@ int cugo_step_reset_spares(uint8_t* states, const int64_t* actions, int64_t n, f
                      (u32)(spare_slots - 1)};
   launch_step<3, false>(n, stream, reinterpret_cast<u64*>(states), n, nullptr, actions, n,
                         reward, done, nagari, status, committed, nullptr, ar);
+  return launched();
+}
+
+int cugo_step_observe_spares(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
+                             uint8_t* done, uint8_t* nagari, int16_t* status,
+                             uint8_t* committed, uint64_t base_seed, int64_t seed_stride,
+                             uint32_t* generation, uint64_t* sampler, uint8_t* spares,
+                             const uint32_t* spare_gen, int64_t spare_slots, int features_dtype,
+                             void* features, uint8_t* legal, uint8_t* player,
+                             uint8_t* obs_done, int16_t* obs_status, hipStream_t stream) {
+  if (n < 0 || seed_stride < 0 || !valid_slots(spare_slots) ||
+      (features_dtype != CUGO_DTYPE_F32 && features_dtype != CUGO_DTYPE_BF16) ||
+      (n > 0 && (!states || !actions || !reward || !done || !nagari || !status || !committed ||
+                 !generation || !sampler || !spares || !spare_gen || !features || !legal ||
+                 !player || !obs_done || !obs_status)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  const AutoReset ar{base_seed, (u64)seed_stride, generation, reinterpret_cast<u64*>(sampler),
+                     reinterpret_cast<u64*>(spares), spare_gen, n, (u32)(spare_slots - 1)};
+  if (features_dtype == CUGO_DTYPE_BF16)
+    step_observe_kernel<true><<<tiles(n), kPlayThreads, 0, stream>>>(
+        reinterpret_cast<u64*>(states), n, actions, reward, done, nagari, status, committed, ar,
+        features, legal, player, obs_done, obs_status);
+  else
+    step_observe_kernel<false><<<tiles(n), kPlayThreads, 0, stream>>>(
+        reinterpret_cast<u64*>(states), n, actions, reward, done, nagari, status, committed, ar,
+        features, legal, player, obs_done, obs_status);
   return launched();
 }
 

@@ -526,6 +526,63 @@ std::vector<torch::Tensor> step_reset_spares(torch::Tensor states, torch::Tensor
   return o;
 }
 
+// step_reset_spares then observe (float32 features) or observe_bf16 (bfloat16) of the new
+// states in one launch, the features written into `features` (a contiguous [N, 720]
+// tensor, e.g. a row block of a rollout buffer); returns the step outputs then the
+// observation's: (reward, done, nagari, status, committed, features, legal, player,
+// obs_done, obs_status).  A stale spare is dealt into its slot before it is taken.
+std::vector<torch::Tensor> step_observe_spares(torch::Tensor states, torch::Tensor actions,
+                                               int64_t base_seed, torch::Tensor generation,
+                                               torch::Tensor sampler, torch::Tensor spares,
+                                               torch::Tensor spare_gen, torch::Tensor features,
+                                               int64_t seed_stride,
+                                               c10::optional<torch::Tensor> reward,
+                                               c10::optional<torch::Tensor> done,
+                                               c10::optional<torch::Tensor> legal) {
+  check_states(states);
+  check_states(spares);
+  const int64_t n = states.size(0);
+  check_1d(actions, at::kLong, "actions");
+  check_1d(generation, at::kInt, "generation");
+  check_1d(sampler, at::kLong, "sampler");
+  check_1d(spare_gen, at::kInt, "spare_gen");
+  TORCH_CHECK(actions.numel() == n && generation.numel() == n && sampler.numel() == n,
+              "actions, generation and sampler must have one entry per row");
+  const int64_t slots = spare_slots(spares, spare_gen, n);
+  TORCH_CHECK(features.is_contiguous() && features.dim() == 2 && features.size(0) == n &&
+                  features.size(1) == CUGO_FEATURE_COUNT &&
+                  (features.scalar_type() == at::kBFloat16 ||
+                   features.scalar_type() == at::kFloat),
+              "features must be a contiguous float32 or bfloat16 [N, 720] tensor");
+  check_same_device(states, actions, "states", "actions");
+  check_same_device(states, generation, "states", "generation");
+  check_same_device(states, sampler, "states", "sampler");
+  check_same_device(states, spares, "states", "spares");
+  check_same_device(states, spare_gen, "states", "spare_gen");
+  check_same_device(states, features, "states", "features");
+  const DeviceGuard guard(states.device());
+  auto o = step_outputs(n, states);
+  if (reward.has_value()) o[0] = out_or_new(reward, {n}, at::kFloat, states, "reward");
+  if (done.has_value()) o[1] = out_or_new(done, {n}, at::kBool, states, "done");
+  o.push_back(features);
+  o.push_back(out_or_new(legal, {n, CUGO_ACTION_COUNT}, at::kBool, states, "legal"));
+  o.push_back(torch::empty({n}, on(states, at::kByte)));
+  o.push_back(torch::empty({n}, on(states, at::kBool)));
+  o.push_back(torch::empty({n}, on(states, at::kShort)));
+  const bool bf16 = features.scalar_type() == at::kBFloat16;
+  check_call(cugo_step_observe_spares(
+                 u8p(states), actions.data_ptr<int64_t>(), n, o[0].data_ptr<float>(), u8p(o[1]),
+                 u8p(o[2]), o[3].data_ptr<int16_t>(), u8p(o[4]),
+                 static_cast<uint64_t>(base_seed), seed_stride < 0 ? n : seed_stride,
+                 reinterpret_cast<uint32_t*>(generation.data_ptr()),
+                 reinterpret_cast<uint64_t*>(sampler.data_ptr()), u8p(spares),
+                 reinterpret_cast<const uint32_t*>(spare_gen.data_ptr()), slots,
+                 bf16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32, features.data_ptr(), u8p(o[6]),
+                 u8p(o[7]), u8p(o[8]), o[9].data_ptr<int16_t>(), stream()),
+             "step_observe_spares");
+  return o;
+}
+
 // redeal(states, seat, keys, rng): in place (python/cugo_ppo50.py:122-148 given its draws).
 void redeal(torch::Tensor states, torch::Tensor seat, torch::Tensor keys, torch::Tensor rng) {
   check_states(states);
@@ -1146,6 +1203,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("spares"),
         pybind11::arg("spare_gen"), pybind11::arg("seed_stride") = -1,
         pybind11::arg("reward") = pybind11::none(), pybind11::arg("done") = pybind11::none());
+  m.def("step_observe_spares", &step_observe_spares,
+        "step_reset_spares, then observe (float32 or bfloat16 features, into `features`) of the "
+        "new states, in one launch",
+        pybind11::arg("states"), pybind11::arg("actions"), pybind11::arg("base_seed"),
+        pybind11::arg("generation"), pybind11::arg("sampler"), pybind11::arg("spares"),
+        pybind11::arg("spare_gen"), pybind11::arg("features"), pybind11::arg("seed_stride") = -1,
+        pybind11::arg("reward") = pybind11::none(), pybind11::arg("done") = pybind11::none(),
+        pybind11::arg("legal") = pybind11::none());
   m.def("event_tokens", &event_tokens, "SeqNet.event_token: event_in(encode_events) + position + type");
   m.def("start_tokens", &start_tokens, "SeqNet.start_token: start_in(encode_start) + position + type");
   m.def("add_layernorm", &add_layernorm, "x + y and LayerNorm(x + y) in one launch",

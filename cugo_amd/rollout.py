@@ -5,15 +5,17 @@ observe -> actor forward -> masked sampling -> step, records (features, legal, a
 logp) per decision and the settled reward at the end.  This module plays the same loop
 over a resident batch of games with auto-reset, for a residual MLP actor:
 
-  * engine: `observe_bf16` (720 features, written as bf16 straight into the rollout
-    buffer, + the 179-way mask; `observe` with float32 features for other actors), then
-    `step_reset_spares`, which steps
-    every game and gives each finished row its next game (seed base + i + B * generation,
-    first player i & 1) from a pre-dealt spare (`refill_spares` every REFILL steps; a
-    stale spare is dealt inline), so a finished game costs no separate reset launch;
-  * actor: one HIP launch for the whole forward pass (`mlp_forward`: MFMA GEMMs with the
-    64-row tile's activations kept on chip from the input layer to the heads, reading the
-    buffer's bf16 features), for the 512-wide actor; any
+  * engine: `step_observe_spares` in one launch per step: the step of every game with the
+    sampled actions, each finished row given its next game (seed base + i + B *
+    generation, first player i & 1) from a pre-dealt spare (`refill_spares` every REFILL
+    steps; a stale spare is dealt into its slot first), then the next step's observation
+    of the new states (720 features written as bf16 straight into the rollout buffer, +
+    the 179-way mask).  The horizon's first observation is `observe_bf16`; an actor the
+    one-launch forward does not serve gets `observe` (float32 features) and
+    `step_reset_spares` as two launches;
+  * actor: one HIP launch for the whole forward pass (`mlp_forward`: MFMA GEMMs with a
+    128-row tile's activations kept on chip from the input layer to the heads, reading
+    the buffer's bf16 features), for the 512-wide actor; any
     other width runs `fused_forward`: bf16 GEMMs through PyTorch-ROCm (hipBLASLt), the bias
     and ReLU of each block's first Linear fused into its GEMM, each residual add fused with
     the next LayerNorm (`add_layernorm`, one HIP launch);
@@ -269,10 +271,30 @@ class MlpRollout:
             self.spare_gen, reward=self.buffer.reward[t], done=self.buffer.done[t])
         return self.step_out
 
+    def step_observe(self, t: int, action: torch.Tensor):
+        """step(t, action), then step t + 1's observation of the new states, in one launch
+        (`step_observe_spares`): the reward and done flag go into the buffer's row t, the
+        bf16 features and mask into row t + 1."""
+        if (t + 1) % REFILL == 0:
+            self.ext.refill_spares(self.spares, self.spare_gen, self.generation, self.base)
+        buf = self.buffer
+        out = self.ext.step_observe_spares(
+            self.states, action, self.base, self.generation, self.sampler, self.spares,
+            self.spare_gen, buf.features[t + 1], reward=buf.reward[t], done=buf.done[t],
+            legal=buf.legal[t + 1])
+        self.step_out, self.observation = out[:5], out[5:]
+        return self.step_out
+
     def _steps(self) -> None:
+        self.observe(0)
         for t in range(self.horizon):
-            self.observe(t)
-            self.step(t, self.act(t))
+            action = self.act(t)
+            if self.fused_kernel and t + 1 < self.horizon:
+                self.step_observe(t, action)
+            else:
+                self.step(t, action)
+                if t + 1 < self.horizon:
+                    self.observe(t + 1)
 
     @torch.no_grad()
     def collect(self) -> RolloutBuffer:

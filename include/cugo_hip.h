@@ -197,6 +197,19 @@ int cugo_step_reset_spares(uint8_t* states, const int64_t* actions, int64_t n, f
                            uint64_t base_seed, int64_t seed_stride, uint32_t* generation,
                            uint64_t* sampler, const uint8_t* spares, const uint32_t* spare_gen,
                            int64_t spare_slots, hipStream_t stream);
+/* cugo_step_observe_spares: cugo_step_reset_spares followed by cugo_observe (features_dtype
+ * CUGO_DTYPE_F32, float [n, CUGO_FEATURE_COUNT]) or cugo_observe_bf16 (CUGO_DTYPE_BF16,
+ * uint16 bits) of the new states, in one launch, with the outputs of both calls.  A
+ * finished row whose spare is stale gets its next game dealt into the spare's slot first
+ * (so spares is written; spare_gen is not).  No reference counterpart: the PPO rollout's
+ * engine between two actor passes (python/cugo_ppo50.py:321-450 steps, then observes). */
+int cugo_step_observe_spares(uint8_t* states, const int64_t* actions, int64_t n, float* reward,
+                             uint8_t* done, uint8_t* nagari, int16_t* status,
+                             uint8_t* committed, uint64_t base_seed, int64_t seed_stride,
+                             uint32_t* generation, uint64_t* sampler, uint8_t* spares,
+                             const uint32_t* spare_gen, int64_t spare_slots, int features_dtype,
+                             void* features, uint8_t* legal, uint8_t* player,
+                             uint8_t* obs_done, int16_t* obs_status, hipStream_t stream);
 /* redeal (python/cugo_ppo50.py:122-148, `_redeal`) in place on rows [n, CUGO_STATE_BYTES]
  * for observer seat[i], given the reference's random draws: keys f32 [n, 50]
  * (torch.rand(n, 50)) rank the unknown cards (the opponent's cards not shown by a shake,

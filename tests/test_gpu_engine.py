@@ -367,6 +367,47 @@ def test_step_reset_spares_matches_step_then_reset(ext):
     assert int(gen_a.sum().item()) > n
 
 
+@pytest.mark.parametrize("bf16", [True, False])
+def test_step_observe_spares_matches_step_then_observe(ext, bf16):
+    """step_observe_spares == step_reset_spares followed by observe (float32 features) or
+    observe_bf16 of the new states: the five step outputs, the five observation outputs,
+    the rows, generations and samplers, bit for bit, over 60 steps with spares refilled
+    every few steps (spare copies and stale spares both occur), at a partial last tile."""
+    announce(f"step_observe_spares (bf16={bf16})")
+    n = 2500
+    base = 0x5772156
+    seeds = (np.uint64(base) + np.arange(n, dtype=np.uint64)).view(np.int64)
+    a = ext.create(torch.from_numpy(seeds).to(DEV), torch.from_numpy(np.arange(n) & 1).to(DEV))
+    gen_a = torch.zeros(n, dtype=torch.int32, device=DEV)
+    smp_a = ext.seed_samplers(n, base, gen_a)
+    sp_a = torch.zeros((2 * n, 248), dtype=torch.uint8, device=DEV)
+    sg_a = torch.zeros(2 * n, dtype=torch.int32, device=DEV)
+    b, gen_b, smp_b, sp_b, sg_b = (t.clone() for t in (a, gen_a, smp_a, sp_a, sg_a))
+    feats = torch.full((n, 720), float("nan"), device=DEV,
+                       dtype=torch.bfloat16 if bf16 else torch.float32)
+    for step in range(60):
+        if step % 7 == 0:
+            ext.refill_spares(sp_a, sg_a, gen_a, base)
+            ext.refill_spares(sp_b, sg_b, gen_b, base)
+        _, _, _, _, _, actions = ext.observe_sample(a, smp_a)
+        smp_b.copy_(smp_a)
+        st = ext.step_reset_spares(a, actions, base, gen_a, smp_a, sp_a, sg_a)
+        if bf16:
+            ob = ext.observe_bf16(a, torch.empty_like(feats))
+        else:
+            ob = ext.observe(a)
+        fused = ext.step_observe_spares(b, actions, base, gen_b, smp_b, sp_b, sg_b, feats)
+        assert fused[5].data_ptr() == feats.data_ptr()
+        for k, want in enumerate(list(st) + list(ob)):
+            got = fused[k]
+            if got.is_floating_point():  # bit patterns (NaN-safe)
+                got, want = got.view(torch.int16 if bf16 and k == 5 else torch.int32), \
+                    want.view(torch.int16 if bf16 and k == 5 else torch.int32)
+            assert torch.equal(got, want), (step, k)
+        assert torch.equal(a, b) and torch.equal(gen_a, gen_b) and torch.equal(smp_a, smp_b), step
+    assert int(gen_a.sum().item()) > n
+
+
 def test_branch_observe_matches_branch_then_observe(ext):
     """branch_observe_indexed == branch_indexed followed by observe_indexed of the children:
     every output bit-identical, with invalid and duplicate parent ids, wild actions and a

@@ -33,11 +33,12 @@ def _actor(seed: int, std: float):
 
 
 def test_rollout_engine_matches_oracle(ext, ref):
-    """C4's loop at its full batch, 32,768 games, for 40 steps (the spares are refilled
-    at steps 0 and 32): observation (bf16 features equal to the oracle's float32 ones
-    rounded as torch rounds them), actions drawn from the legal set, step outputs and
-    the rows after every step's auto-reset, against the oracle stepping the same
-    actions and re-dealing finished rows from seed base + i + 32,768 * generation."""
+    """C4's loop at its full batch, 32,768 games, for 40 steps, the step alone and the
+    fused step + next observation on alternate steps: observation (bf16 features equal
+    to the oracle's float32 ones rounded as torch rounds them), actions drawn from the
+    legal set, step outputs and the rows after every step's auto-reset, against the
+    oracle stepping the same actions and re-dealing finished rows from seed base + i +
+    32,768 * generation."""
     from cugo_amd.rollout import MlpRollout
 
     announce("MLP rollout engine vs oracle (32,768 x 40)")
@@ -50,8 +51,8 @@ def test_rollout_engine_matches_oracle(ext, ref):
     assert np.array_equal(to_np(ro.states), host)
     hgen = np.zeros(n, dtype=np.int64)
     with torch.no_grad():
+        obs = ro.observe(0)
         for t in range(steps):
-            obs = ro.observe(t)
             robs = ref.observe(host)
             # the rollout keeps bf16 features: the oracle's float32 features, rounded
             want = torch.from_numpy(robs[0]).to(torch.bfloat16).view(torch.int16)
@@ -65,7 +66,10 @@ def test_rollout_engine_matches_oracle(ext, ref):
             legal = robs[1]
             live = ~robs[3]
             assert legal[np.arange(n)[live], a[live]].all(), f"illegal action, step {t}"
-            out = ro.step(t, action)
+            # odd steps: the fused step + next observation the rollout loop uses; even
+            # steps: the step alone, then observe
+            fused = t % 2 == 1 and t + 1 < steps
+            out = ro.step_observe(t, action) if fused else ro.step(t, action)
             rout = ref.step(host, a)
             assert_step_equal(out, rout, f"step {t}")
             ended = np.nonzero(rout[1])[0]
@@ -82,6 +86,8 @@ def test_rollout_engine_matches_oracle(ext, ref):
             assert buf.features[t].data_ptr() == obs[0].data_ptr(), t
             lp = to_np(buf.logp[t])
             assert (lp[live] <= 1e-6).all() and np.isfinite(lp[live]).all(), t
+            if t + 1 < steps:
+                obs = ro.observation if fused else ro.observe(t + 1)
     assert np.array_equal(to_np(ro.generation), hgen)
     # the re-seeded sampler words of finished rows (unused by the actor) are the
     # driver's: SplitMix64 of the row's current seed
@@ -129,7 +135,7 @@ def _features(n: int, seed: int) -> torch.Tensor:
                                             (130, torch.float32, 1)])
 def test_mlp_kernel_matches_float32(ext, n, dtype, blocks):
     """mlp_forward (the whole actor in one launch: MFMA GEMMs, LayerNorms and the heads on a
-    64-row tile) against the module's own forward in float32 on the same bf16 inputs:
+    128-row tile) against the module's own forward in float32 on the same bf16 inputs:
     relative Frobenius error of the logits and values at most 2e-2, the greedy actions
     agree on at least 97 % of the rows, and the bf16 copy of the input equals torch's
     rounding.  Row counts that leave a partial last tile; float32 and bf16 inputs; one and
