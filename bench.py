@@ -716,17 +716,21 @@ def paired_workload(ext, torch, pairs: int = 4096) -> dict:
             "mean_pair_score_a": round(s.mean_pair_score_a, 4)}
 
 
-def engine_traffic(batch: int, bf16: bool) -> int | None:
-    """HBM bytes of one engine step of the rollout (observe with the draw, float32 or bf16
-    features, step with auto-reset, and a 32nd of the spares' refill) from the committed
-    counter summary."""
-    parts = [measured_traffic("observe_bf16_sample_kernel" if bf16 else "observe_sample_kernel",
-                              str(batch)),
-             measured_traffic("step_reset_spares_kernel", str(batch)),
-             measured_traffic("refill_kernel", str(batch))]
+def engine_traffic(batch: int, fused: bool) -> int | None:
+    """HBM bytes of one engine step of the rollout from the committed counter summary: the
+    fused step + observation (bf16 features) and a 32nd of the spares' refill, or observe
+    with the draw and the step with auto-reset for an actor the one-launch forward does
+    not serve."""
+    if fused:
+        parts = [measured_traffic("step_observe_kernel", str(batch)),
+                 measured_traffic("refill_kernel", str(batch))]
+    else:
+        parts = [measured_traffic("observe_sample_kernel", str(batch)),
+                 measured_traffic("step_reset_spares_kernel", str(batch)),
+                 measured_traffic("refill_kernel", str(batch))]
     if None in parts:
         return None
-    return parts[0] + parts[1] + parts[2] // 32
+    return sum(parts[:-1]) + parts[-1] // 32
 
 
 def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict:
@@ -738,7 +742,8 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
     spares inside the step.  Reports env steps/s, the engine's and the actor's shares of
     the step time and a roofline for each: the actor's FLOPs over its forward time (the
     one-launch MFMA forward, `mlp_forward`, that the rollout runs) against the bf16 MFMA
-    peak, the engine's bytes (observe 3,311 B a row, step with auto-reset 513 B a row)
+    peak, the engine's bytes (the fused step + next observation: the rows read and
+    written once, the action, the step outputs and the bf16 observation, 2,136 B a row)
     over its time against HBM.  The rollout runs as one HIP graph per horizon; the shares
     come from graphs of the engine's and the actor's launches alone."""
     from cugo_amd.rollout import (MlpRollout, ResidualMlpActor, fused_forward, mlp_forward,
@@ -779,30 +784,51 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
             wall = time.perf_counter() - t0
         games = ro.games_completed() - games0
         step_ms = wall * 1e3 / (reps * horizon)
-        # The engine's share: its launches alone (observe with the random policy's draw,
-        # then step_reset_spares, the spares refilled every 32 steps) on a copy of the
-        # games, 32 steps in one graph; the actor's: its forward pass, the uniforms, the
-        # Gumbel-max draw and the buffer writes of one step, one graph.
-        st, g2, smp = ro.states.clone(), ro.generation.clone(), ro.sampler.clone()
-        sp, sg = ro.spares.clone(), ro.spare_gen.clone()
+        # The engine's share: its launches alone on a copy of the games, 32 steps in one
+        # graph (the spares refilled once), with the uniform legal actions a first eager
+        # pass from the same rows drew (they stand in for the actor's): the rollout's fused
+        # step + next observation (bf16 features), or observe and step_reset_spares for an
+        # actor the one-launch forward does not serve.  Each replay first restores the rows,
+        # generations, samplers and spares; a graph of the restore alone is subtracted.
+        # The actor's share: its forward pass, the uniforms, the Gumbel-max draw and the
+        # buffer writes of one step, one graph.
+        start = [t.clone() for t in (ro.states, ro.generation, ro.sampler, ro.spares,
+                                     ro.spare_gen)]
+        st, g2, smp, sp, sg = (t.clone() for t in start)
         feats = torch.empty((batch, 720), dtype=torch.bfloat16, device=dev)
+        legal = ext.observe_bf16(st, feats)[1]
+        acts = []
+        ext.refill_spares(sp, sg, g2, SEED_BASE + 0xC4)
+        for _ in range(32):
+            acts.append(ext.sample_uniform(legal, smp))
+            legal = ext.step_observe_spares(st, acts[-1], SEED_BASE + 0xC4, g2, smp, sp, sg,
+                                            feats)[6]
 
-        def engine_block():
+        def engine_block(engine: bool):
+            for dst, src in zip((st, g2, smp, sp, sg), start):
+                dst.copy_(src)
+            if not engine:
+                return
             ext.refill_spares(sp, sg, g2, SEED_BASE + 0xC4)
-            for _ in range(32):
-                if ro.fused_kernel:  # the rollout's bf16 observation, with the draw
-                    acts = ext.observe_bf16(st, feats, smp)[5]
+            for k in range(32):
+                if ro.fused_kernel:
+                    ext.step_observe_spares(st, acts[k], SEED_BASE + 0xC4, g2, smp, sp, sg, feats)
                 else:
-                    acts = ext.observe_sample(st, smp)[5]
-                ext.step_reset_spares(st, acts, SEED_BASE + 0xC4, g2, smp, sp, sg)
+                    ext.step_reset_spares(st, acts[k], SEED_BASE + 0xC4, g2, smp, sp, sg)
+                    ext.observe(st)
 
-        engine_block()
-        torch.cuda.synchronize()
-        eg = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(eg):
-            engine_block()
-        engine_step_ms = graph_ms(eg, 3, "c4.engine") / 32
-        del eg
+        def block_ms(engine: bool, name: str) -> float:
+            engine_block(engine)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                engine_block(engine)
+            ms = graph_ms(g, 3, name)
+            del g
+            return ms
+
+        engine_step_ms = (block_ms(True, "c4.engine") - block_ms(False, "c4.restore")) / 32
+        del start, st, g2, smp, sp, sg, feats, acts
         ro.observe(0)
         ro.act(0)
         torch.cuda.synchronize()
@@ -835,8 +861,11 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         del lg
     flops_row = actor.flops_per_row()
     tflops = flops_row * batch / (forward_ms * 1e-3) / 1e12
-    observe_bytes = OBSERVE_BYTES_PER_ROW - (720 * 2 if ro.fused_kernel else 0)
-    engine_bytes = batch * (observe_bytes + STEP_BYTES_PER_ROW)
+    # fused: the rows read and written once, the action, the step outputs and the bf16
+    # observation; else observe (float32 features) and the step, the rows read twice
+    engine_row = (STEP_BYTES_PER_ROW + 720 * 2 + 179 + 4 if ro.fused_kernel
+                  else OBSERVE_BYTES_PER_ROW + STEP_BYTES_PER_ROW)
+    engine_bytes = batch * engine_row
     engine_gbs = engine_bytes / (engine_step_ms * 1e-3) / 1e9
     return {"env_steps_per_s": round(batch * reps * horizon / wall, 1),
             "games_per_s": round(games / wall, 1),
@@ -855,13 +884,14 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
                          "layered_forward_ms": round(layered_ms, 4),
                          "layered_tflops": round(flops_row * batch / (layered_ms * 1e-3)
                                                  / 1e12, 1)},
-            "engine_roofline": {"kernel": ("observe_bf16" if ro.fused_kernel else "observe")
-                                          + " + step_reset_spares (+ refill_spares)",
+            "engine_roofline": {"kernel": ("step_observe_spares" if ro.fused_kernel
+                                           else "observe + step_reset_spares")
+                                          + " (+ refill_spares)",
                                 "bound": "hbm", "achieved": round(engine_gbs, 2),
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(engine_gbs / HBM_PEAK_GBS, 4),
                                 "traffic": engine_traffic(batch, ro.fused_kernel),
-                                "bytes_per_row_step": observe_bytes + STEP_BYTES_PER_ROW,
+                                "bytes_per_row_step": engine_row,
                                 "ms_per_step": round(engine_step_ms, 4)},
             "games_completed": games,
             "batch": batch, "horizon": horizon, "dtype": "bf16"}
