@@ -790,8 +790,8 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         # step + next observation (bf16 features), or observe and step_reset_spares for an
         # actor the one-launch forward does not serve.  Each replay first restores the rows,
         # generations, samplers and spares; a graph of the restore alone is subtracted.
-        # The actor's share: its forward pass, the uniforms, the Gumbel-max draw and the
-        # buffer writes of one step, one graph.
+        # The actor's share: its forward pass, the Gumbel-max draw (uniforms from Philox in
+        # the kernel) and the buffer writes of one step, one graph.
         start = [t.clone() for t in (ro.states, ro.generation, ro.sampler, ro.spares,
                                      ro.spare_gen)]
         st, g2, smp, sp, sg = (t.clone() for t in start)
@@ -833,7 +833,6 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         ro.act(0)
         torch.cuda.synchronize()
         ag = torch.cuda.CUDAGraph()
-        ag.register_generator_state(gen)
         with torch.cuda.graph(ag):
             ro.act(0)
         actor_step_ms = graph_ms(ag, 10, "c4.actor")

@@ -269,19 +269,55 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void gumbel_kernel(
   }
 }
 
+// Philox4x32-10 (Salmon, Moraes, Dror and Shaw, "Parallel random numbers: as easy as 1,
+// 2, 3", SC 2011): ten rounds, each mapping the counter (c0, c1, c2, c3) under the key
+// (k0, k1) to (hi(M1 c2) ^ c1 ^ k0, lo(M1 c2), hi(M0 c0) ^ c3 ^ k1, lo(M0 c0)), the key
+// bumped by the Weyl constants between rounds.
+struct Philox4 {
+  uint32_t x[4];
+};
+__device__ inline Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                        uint32_t k0, uint32_t k1) {
+  constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = M0 * c0, hi0 = __umulhi(M0, c0);
+    const uint32_t lo1 = M1 * c2, hi1 = __umulhi(M1, c2);
+    c0 = hi1 ^ c1 ^ k0;
+    c1 = lo1;
+    c2 = hi0 ^ c3 ^ k1;
+    c3 = lo0;
+    k0 += W0;
+    k1 += W1;
+  }
+  return {{c0, c1, c2, c3}};
+}
+
+// The uniforms of cugo_gumbel_sample_philox: for row r and action a, word (a / 16) % 4 of
+// Philox4x32-10 at counter (r mod 2^32, (a % 16) + 64 (a / 64) + 256 (r / 2^32), offset,
+// *epoch mod 2^32) under the key (seed mod 2^32, seed / 2^32), as (word >> 8) * 2^-24, in
+// [0, 1).  A lane of gumbel_rows_kernel holds actions j + 16 k (k < 12): three counters.
+struct PhiloxNoise {
+  uint32_t k0, k1, offset;
+  const uint64_t* epoch;
+  float* u_out;  // if not NULL, the uniforms drawn, [n, A] (for tests)
+};
+
 // The same sampling with 16 lanes per row and four rows per wavefront, for rows of at
 // most kGumbelLanes * kGumbelPer actions: lane j of a row takes actions j, j + 16, ...,
 // issues all of its loads before any arithmetic, and keeps its masked logits in
 // registers for the softmax sum, so a row costs one round of memory latency.  Ties and
 // the reductions follow gumbel_kernel (the largest value, the first index among equal
-// ones); only the order of the fp32 softmax sum differs.
+// ones); only the order of the fp32 softmax sum differs.  kNoise: 0 no noise (greedy),
+// 1 the uniforms u [n, A], 2 uniforms drawn here from Philox (PhiloxNoise).
 constexpr int kGumbelLanes = 16;
 constexpr int kGumbelPer = 12;  // up to 192 actions
+static_assert(kGumbelPer == 12, "a Philox lane draws three blocks of four uniforms");
 
-template <class T, bool kNoise>
+template <class T, int kNoise>
 __global__ __launch_bounds__(256) void gumbel_rows_kernel(
     const typename T::storage* logits, const uint8_t* legal, const float* u, i64 n,
-    int actions_count, i64* actions, float* logp) {
+    int actions_count, i64* actions, float* logp, PhiloxNoise px) {
   const int j = threadIdx.x & (kGumbelLanes - 1);
   const i64 r = (i64)blockIdx.x * (256 / kGumbelLanes) + (threadIdx.x / kGumbelLanes);
   const bool row_ok = r < n;
@@ -291,7 +327,7 @@ __global__ __launch_bounds__(256) void gumbel_rows_kernel(
   const i64 rr = row_ok ? r : n - 1;
   const typename T::storage* lr = logits + rr * actions_count;
   const uint8_t* gr = legal + rr * actions_count;
-  const float* ur = kNoise ? u + rr * actions_count : nullptr;
+  const float* ur = kNoise == 1 ? u + rr * actions_count : nullptr;
   uint8_t gb[kGumbelPer];
   typename T::storage lv[kGumbelPer];
   float uv[kGumbelPer];
@@ -301,7 +337,25 @@ __global__ __launch_bounds__(256) void gumbel_rows_kernel(
     const int ac = a < actions_count ? a : actions_count - 1;
     gb[k] = gr[ac];
     lv[k] = lr[ac];
-    uv[k] = kNoise ? ur[ac] : 0.0f;
+    uv[k] = kNoise == 1 ? ur[ac] : 0.0f;
+  }
+  if constexpr (kNoise == 2) {
+    const uint32_t epoch = (uint32_t)*px.epoch;
+    const uint32_t row_hi = (uint32_t)((uint64_t)rr >> 32) << 8;
+#pragma unroll
+    for (int g = 0; g < kGumbelPer / 4; ++g) {
+      const Philox4 w = philox4x32_10((uint32_t)rr, (uint32_t)(j + 64 * g) + row_hi, px.offset,
+                                      epoch, px.k0, px.k1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) uv[4 * g + q] = (float)(w.x[q] >> 8) * 0x1.0p-24f;
+    }
+    if (px.u_out != nullptr && row_ok) {
+#pragma unroll
+      for (int k = 0; k < kGumbelPer; ++k) {
+        const int a = j + kGumbelLanes * k;
+        if (a < actions_count) px.u_out[r * actions_count + a] = uv[k];
+      }
+    }
   }
   bool ok[kGumbelPer];
   float m[kGumbelPer], uc[kGumbelPer];
@@ -322,7 +376,7 @@ __global__ __launch_bounds__(256) void gumbel_rows_kernel(
     if (!row_ok || a >= actions_count) continue;
     any |= ok[k];
     float v = m[k];
-    if (kNoise) {
+    if (kNoise != 0) {
       if (ok[k]) v = m[k] + -logf(-logf(uc[k]));
       else if (uc[k] >= 1.0f) v = INFINITY;
     }
@@ -658,11 +712,11 @@ int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* lega
     const unsigned grid = (unsigned)((n + 256 / kGumbelLanes - 1) / (256 / kGumbelLanes));
 #define CUGO_GUMBEL_ROWS(TT, NOISE, PTR)                                                   \
   gumbel_rows_kernel<TT, NOISE><<<grid, 256, 0, stream>>>(                                  \
-      (PTR)logits, legal, uniforms, n, (int)actions_count, actions, logp)
-    if (f32 && uniforms) CUGO_GUMBEL_ROWS(F32, true, const float*);
-    else if (f32) CUGO_GUMBEL_ROWS(F32, false, const float*);
-    else if (uniforms) CUGO_GUMBEL_ROWS(BF16, true, const uint16_t*);
-    else CUGO_GUMBEL_ROWS(BF16, false, const uint16_t*);
+      (PTR)logits, legal, uniforms, n, (int)actions_count, actions, logp, PhiloxNoise{})
+    if (f32 && uniforms) CUGO_GUMBEL_ROWS(F32, 1, const float*);
+    else if (f32) CUGO_GUMBEL_ROWS(F32, 0, const float*);
+    else if (uniforms) CUGO_GUMBEL_ROWS(BF16, 1, const uint16_t*);
+    else CUGO_GUMBEL_ROWS(BF16, 0, const uint16_t*);
 #undef CUGO_GUMBEL_ROWS
     return (int)hipGetLastError();
   }
@@ -673,6 +727,26 @@ int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* lega
   else
     gumbel_kernel<BF16><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
         (const uint16_t*)logits, legal, uniforms, n, (int)actions_count, actions, logp);
+  return (int)hipGetLastError();
+}
+
+int cugo_gumbel_sample_philox(int logits_dtype, const void* logits, const uint8_t* legal,
+                              uint64_t seed, const uint64_t* epoch, uint32_t offset, int64_t n,
+                              int64_t actions_count, int64_t* actions, float* logp,
+                              float* uniforms_out, hipStream_t stream) {
+  if (n < 0 || actions_count < 1 || actions_count > kGumbelLanes * kGumbelPer ||
+      (n > 0 && (!logits || !legal || !actions || !epoch)))
+    return -1;
+  if (n == 0) return 0;
+  if (logits_dtype != CUGO_DTYPE_F32 && logits_dtype != CUGO_DTYPE_BF16) return -2;
+  const PhiloxNoise px{(uint32_t)seed, (uint32_t)(seed >> 32), offset, epoch, uniforms_out};
+  const unsigned grid = (unsigned)((n + 256 / kGumbelLanes - 1) / (256 / kGumbelLanes));
+  if (logits_dtype == CUGO_DTYPE_F32)
+    gumbel_rows_kernel<F32, 2><<<grid, 256, 0, stream>>>(
+        (const float*)logits, legal, nullptr, n, (int)actions_count, actions, logp, px);
+  else
+    gumbel_rows_kernel<BF16, 2><<<grid, 256, 0, stream>>>(
+        (const uint16_t*)logits, legal, nullptr, n, (int)actions_count, actions, logp, px);
   return (int)hipGetLastError();
 }
 

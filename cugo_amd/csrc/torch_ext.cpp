@@ -888,6 +888,50 @@ std::vector<torch::Tensor> gumbel_sample(torch::Tensor logits, torch::Tensor leg
   return {actions, logp};
 }
 
+// gumbel_sample_philox(logits f32 or bf16 [n, A], legal bool [n, A], seed, epoch int64 [1]
+// (device), offset) -> (actions int64 [n], logp f32 [n]): gumbel_sample with uniforms drawn
+// in the kernel from Philox4x32-10 (cugo_gumbel_sample_philox); uniforms_out, if given,
+// receives them.
+std::vector<torch::Tensor> gumbel_sample_philox(torch::Tensor logits, torch::Tensor legal,
+                                                int64_t seed, torch::Tensor epoch,
+                                                int64_t offset,
+                                                c10::optional<torch::Tensor> actions_out,
+                                                c10::optional<torch::Tensor> logp_out,
+                                                c10::optional<torch::Tensor> uniforms_out) {
+  TORCH_CHECK(logits.is_cuda() && logits.is_contiguous() && logits.dim() == 2 &&
+                  (logits.scalar_type() == at::kFloat || logits.scalar_type() == at::kBFloat16),
+              "logits must be a contiguous CUDA float32 or bfloat16 [n, A] tensor");
+  TORCH_CHECK(legal.is_contiguous() && legal.sizes() == logits.sizes() &&
+                  legal.scalar_type() == at::kBool,
+              "legal must be a contiguous bool tensor shaped like logits");
+  TORCH_CHECK(logits.size(1) <= 192, "at most 192 actions");
+  TORCH_CHECK(epoch.numel() == 1 && epoch.scalar_type() == at::kLong,
+              "epoch must be a one-element int64 tensor");
+  TORCH_CHECK(offset >= 0 && offset <= 0xFFFFFFFFll, "offset must fit 32 bits");
+  check_same_device(logits, legal, "logits", "legal");
+  check_same_device(logits, epoch, "logits", "epoch");
+  const DeviceGuard guard(logits.device());
+  const int64_t n = logits.size(0);
+  auto actions = out_or_new(actions_out, {n}, at::kLong, logits, "actions");
+  auto logp = out_or_new(logp_out, {n}, at::kFloat, logits, "logp");
+  float* u = nullptr;
+  if (uniforms_out.has_value()) {
+    TORCH_CHECK(uniforms_out->is_contiguous() && uniforms_out->sizes() == logits.sizes() &&
+                    uniforms_out->scalar_type() == at::kFloat,
+                "uniforms_out must be a contiguous float32 tensor shaped like logits");
+    check_same_device(logits, *uniforms_out, "logits", "uniforms_out");
+    u = uniforms_out->data_ptr<float>();
+  }
+  check_call(cugo_gumbel_sample_philox(
+                 logits.scalar_type() == at::kFloat ? CUGO_DTYPE_F32 : CUGO_DTYPE_BF16,
+                 logits.data_ptr(), u8p(legal), static_cast<uint64_t>(seed),
+                 reinterpret_cast<const uint64_t*>(epoch.data_ptr()), (uint32_t)offset, n,
+                 logits.size(1), actions.data_ptr<int64_t>(), logp.data_ptr<float>(), u,
+                 stream()),
+             "gumbel_sample_philox");
+  return {actions, logp};
+}
+
 // mlp_pack_weight(w bf16 [rows, cols], rows_pad, cols_pad) -> packed bf16 [rows_pad *
 // cols_pad]: w in the order the actor kernel reads its MFMA operands
 // (cugo_mlp_pack_weight).
@@ -1211,6 +1255,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("spare_gen"), pybind11::arg("features"), pybind11::arg("seed_stride") = -1,
         pybind11::arg("reward") = pybind11::none(), pybind11::arg("done") = pybind11::none(),
         pybind11::arg("legal") = pybind11::none());
+  m.def("gumbel_sample_philox", &gumbel_sample_philox,
+        "gumbel_sample with uniforms drawn in the kernel from Philox4x32-10",
+        pybind11::arg("logits"), pybind11::arg("legal"), pybind11::arg("seed"),
+        pybind11::arg("epoch"), pybind11::arg("offset"), pybind11::arg("actions") = pybind11::none(),
+        pybind11::arg("logp") = pybind11::none(), pybind11::arg("uniforms_out") = pybind11::none());
   m.def("event_tokens", &event_tokens, "SeqNet.event_token: event_in(encode_events) + position + type");
   m.def("start_tokens", &start_tokens, "SeqNet.start_token: start_in(encode_start) + position + type");
   m.def("add_layernorm", &add_layernorm, "x + y and LayerNorm(x + y) in one launch",

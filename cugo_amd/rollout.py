@@ -20,8 +20,11 @@ over a resident batch of games with auto-reset, for a residual MLP actor:
     and ReLU of each block's first Linear fused into its GEMM, each residual add fused with
     the next LayerNorm (`add_layernorm`, one HIP launch);
   * sampling: the Gumbel-max draw over the legal actions and its log-probability in one
-    HIP launch (`gumbel_sample`), on uniforms from torch's generator (the reference draws
-    with torch as well, cugo_seq_selfplay50.py:125-130).
+    HIP launch (`gumbel_sample_philox`), its uniforms drawn in the kernel from
+    Philox4x32-10 keyed by a seed taken once from the caller's generator, the rollout's
+    epoch (a device counter raised once per horizon, so a captured graph draws fresh
+    noise on every replay) and the step; with fixed `noise` [B, 179], `gumbel_sample` on
+    those uniforms.
 """
 
 from __future__ import annotations
@@ -189,8 +192,9 @@ class MlpRollout:
 
     `collect()` plays `horizon` steps eagerly; `capture()` records those steps once as a
     HIP graph and `replay()` plays the next `horizon` steps from it (no per-op launch cost
-    on the host).  Uniforms come from `generator` (registered with the graph), or from
-    `noise` [B, 179] when set, which every step then reads."""
+    on the host).  The sampler's uniforms come from Philox4x32-10 (seeded from
+    `generator`, or torch's default generator), or from `noise` [B, 179] when set, which
+    every step then reads."""
 
     def __init__(self, ext, actor: ResidualMlpActor, batch: int, horizon: int,
                  base_seed: int, generator: torch.Generator | None = None) -> None:
@@ -208,6 +212,9 @@ class MlpRollout:
         self.buffer = RolloutBuffer.empty(horizon, batch, dev)
         self.generator = generator
         self.noise: torch.Tensor | None = None
+        # the Philox key and the horizon counter (device memory, raised by _steps)
+        self.seed = int(torch.randint(0, 2**62, (1,), generator=generator, device=dev).item())
+        self.epoch = torch.zeros(1, dtype=torch.int64, device=dev)
         self.graph: torch.cuda.CUDAGraph | None = None
         # the one-launch forward where it fits the actor, else the layer-by-layer one
         self.fused_kernel = mlp_kernel_fits(actor)
@@ -244,9 +251,12 @@ class MlpRollout:
             logits, value = fused_forward(self.ext, self.actor, x)
             buf.legal[t].copy_(legal)
             buf.value[t].copy_(value)
-        u = self.noise if self.noise is not None else torch.rand(
-            logits.shape, generator=self.generator, device=logits.device)
-        self.ext.gumbel_sample(logits, legal, u, actions=buf.action[t], logp=buf.logp[t])
+        if self.noise is not None:
+            self.ext.gumbel_sample(logits, legal, self.noise, actions=buf.action[t],
+                                   logp=buf.logp[t])
+        else:
+            self.ext.gumbel_sample_philox(logits, legal, self.seed, self.epoch, t,
+                                          actions=buf.action[t], logp=buf.logp[t])
         return buf.action[t]
 
     def repack(self) -> None:
@@ -286,6 +296,7 @@ class MlpRollout:
         return self.step_out
 
     def _steps(self) -> None:
+        self.epoch.add_(1)  # fresh sampler noise for this horizon (a kernel: graph-safe)
         self.observe(0)
         for t in range(self.horizon):
             action = self.act(t)
@@ -315,8 +326,6 @@ class MlpRollout:
                 self.step(t, self.act(t))
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        if self.generator is not None and self.noise is None:
-            graph.register_generator_state(self.generator)
         with torch.cuda.graph(graph):
             self._steps()
         self.graph = graph

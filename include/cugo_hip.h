@@ -351,6 +351,20 @@ int cugo_gumbel_sample(int logits_dtype, const void* logits, const uint8_t* lega
                        const float* uniforms, int64_t n, int64_t actions_count, int64_t* actions,
                        float* logp, hipStream_t stream);
 
+/* cugo_gumbel_sample_philox: cugo_gumbel_sample with its uniforms drawn in the kernel
+ * from Philox4x32-10 (Salmon et al., SC 2011) instead of read from memory: for row r and
+ * action a, word (a / 16) % 4 of the generator at counter (r mod 2^32, (a % 16) + 64 (a / 64)
+ * + 256 (r / 2^32), offset, *epoch mod 2^32) under the key (seed mod 2^32, seed / 2^32), as
+ * (word >> 8) * 2^-24.  epoch is device memory (read at run time, so a captured graph can
+ * advance it between replays); offset tells apart the calls of one epoch (e.g. the step
+ * of a rollout).  actions_count <= 192.  uniforms_out, if not NULL, receives the uniforms
+ * f32 [n, A].  No reference counterpart: the PPO rollout's sampler, whose uniforms the
+ * reference draws with torch (python/cugo_ppo50.py:321-450). */
+int cugo_gumbel_sample_philox(int logits_dtype, const void* logits, const uint8_t* legal,
+                              uint64_t seed, const uint64_t* epoch, uint32_t offset, int64_t n,
+                              int64_t actions_count, int64_t* actions, float* logp,
+                              float* uniforms_out, hipStream_t stream);
+
 /* The weights of a residual MLP actor (bf16 device pointers): h = x W_in^T + b_in; per
  * block h += W2 relu(W1 LN_b(h) + b1) + b2; z = LN_blocks(h); [logits, value] = z W_head^T
  * + b_head.  The matrices are packed by cugo_mlp_pack_weight (Linear weights [out, in]):

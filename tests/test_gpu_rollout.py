@@ -97,6 +97,41 @@ def test_rollout_engine_matches_oracle(ext, ref):
     assert hgen.sum() > n  # most games finished at least once in 40 steps
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gumbel_sample_philox(ext, dtype):
+    """gumbel_sample_philox draws exactly the oracle's Philox4x32-10 uniforms (bit for bit,
+    every row and action, at a partial last block of rows), and its actions and
+    log-probabilities equal gumbel_sample's on those uniforms; the epoch is read from
+    device memory at run time (a new epoch, new noise), and a repeat call draws the same."""
+    from oracle.philox_ref import gumbel_uniforms
+
+    announce(f"Gumbel-max with Philox uniforms ({dtype})")
+    n, a = 3001, 179
+    g = torch.Generator(device=DEV).manual_seed(3)
+    logits = (torch.randn(n, a, generator=g, device=DEV) * 3).to(dtype)
+    legal = torch.rand(n, a, generator=g, device=DEV) < 0.3
+    legal[5] = False  # a row with no legal action
+    legal[6] = False
+    legal[6, 178] = True
+    seed = 0x5EED1234ABCD9876
+    epoch = torch.tensor([41], dtype=torch.int64, device=DEV)
+    u = torch.full((n, a), float("nan"), device=DEV)
+    act, lp = ext.gumbel_sample_philox(logits, legal, seed, epoch, 9, uniforms_out=u)
+    want_u = gumbel_uniforms(seed, 41, 9, np.arange(n), a)
+    assert np.array_equal(u.cpu().numpy().view(np.uint32), want_u.view(np.uint32))
+    ref_act, ref_lp = ext.gumbel_sample(logits, legal, u)
+    assert torch.equal(act, ref_act)
+    assert torch.equal(lp.view(torch.int32), ref_lp.view(torch.int32))
+    assert int(act[6]) == 178
+    again = ext.gumbel_sample_philox(logits, legal, seed, epoch, 9)
+    assert torch.equal(again[0], act) and torch.equal(again[1].view(torch.int32), lp.view(torch.int32))
+    epoch.fill_(42)
+    u2 = torch.empty_like(u)
+    ext.gumbel_sample_philox(logits, legal, seed, epoch, 9, uniforms_out=u2)
+    assert np.array_equal(u2.cpu().numpy(), gumbel_uniforms(seed, 42, 9, np.arange(n), a))
+    assert float((u2 == u).float().mean()) < 1e-3
+
+
 def test_fused_forward_matches_float32(ext):
     """fused_forward (bf16 GEMMs with the bias + ReLU epilogue, fused add + LayerNorm)
     against the module's own forward in float32 on the same bf16 inputs: relative
