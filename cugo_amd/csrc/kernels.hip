@@ -40,10 +40,10 @@ __device__ inline bool valid_id(i64 id, i64 env_count) { return id >= 0 && id < 
 // thread first loads all of its words into registers, at indices clamped into the rows
 // that exist, and only then writes LDS: loads guarded by a branch, or a store of each
 // load before the next, would each wait out a full memory round trip.
-template <int kThreads = kTile>
+template <int kThreads = kTile, int kMaxRows = kTile>
 __device__ inline void stage_in(u64* lds, const u64* states, const i64* ids_lds, i64 base,
                                 int count, i64 env_count) {
-  constexpr int kPer = (kTileWords + kThreads - 1) / kThreads;
+  constexpr int kPer = (kMaxRows * kRowWords + kThreads - 1) / kThreads;
   constexpr int kBatch = kPer < 16 ? kPer : 16;  // words in flight per thread
   const int words = count * kRowWords;  // count >= 1 in every launched tile
   const bool gather = ids_lds != nullptr;
@@ -82,10 +82,10 @@ __device__ inline void stage_in(u64* lds, const u64* states, const i64* ids_lds,
 // Stores the tile's rows from LDS with kThreads threads: to dst rows base + r
 // (contiguous) or, when ids_lds is given, to rows ids[r] with a valid id (scatter, in
 // place).  All of a thread's LDS reads come before its stores.
-template <int kThreads = kTile>
+template <int kThreads = kTile, int kMaxRows = kTile>
 __device__ inline void stage_out(const u64* lds, u64* dst, const i64* ids_lds, i64 base,
                                  int count, i64 env_count) {
-  constexpr int kPer = (kTileWords + kThreads - 1) / kThreads;
+  constexpr int kPer = (kMaxRows * kRowWords + kThreads - 1) / kThreads;
   const int words = count * kRowWords;
   u64 v[kPer];
 #pragma unroll
@@ -136,10 +136,12 @@ __global__ __launch_bounds__(kTile) void create_kernel(const i64* seeds, const i
 // LDS of one observe tile: the staged rows are dead once every lane has unpacked its
 // row, so the per-row feature records and masks reuse the same bytes.
 constexpr int kRecStride = kFeatRecord + 1;  // + the zero pad; odd: no bank conflicts
-struct RecordBuffer {  // one step's observation of a tile, before it is stored
-  u32 rec[kTile][kRecStride];
-  u64 legal[kTile][3];
+template <int kRows>
+struct RecordBufferOf {  // one step's observation of a tile of kRows games, before it is stored
+  u32 rec[kRows][kRecStride];
+  u64 legal[kRows][3];
 };
+using RecordBuffer = RecordBufferOf<kTile>;
 struct ObserveTile {
   union {
     u64 rows[kTileWords];
@@ -181,8 +183,8 @@ __device__ inline void store_quad(void* features, i64 index, const uint4& v) {
   }
 }
 
-template <int kClaim, bool kBf16 = false>
-__device__ inline void store_observation(const RecordBuffer& t, i64 base, int count,
+template <int kClaim, bool kBf16 = false, int kRows = kTile>
+__device__ inline void store_observation(const RecordBufferOf<kRows>& t, i64 base, int count,
                                          void* features, u8* legal, int* next) {
   const int lane = threadIdx.x & (kTile - 1);
   constexpr int kQuads = kFeatureCount / 4;  // 180
@@ -538,17 +540,21 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
 // per SIMD; capping registers for three or four waves spills 144 / 356 bytes a lane and
 // measured 1.35x / 2.7x slower on 1,048,576 children, and staging the parents through LDS
 // as well, as the other step kernels do, measured 1.13x slower.
+// kRows children a wavefront: at 1,048,576 children (16,384 wavefronts, many rounds) 64
+// took 0.103 ms, 48 0.126 and 32 0.153: fewer children a wavefront run fewer divergent
+// rule paths each, but the launch issues more wavefronts of the same length.
+template <int kRows>
 __global__ __launch_bounds__(kTile) void branch_kernel(const u64* parents, i64 env_count,
                                                        const i64* ids, const i64* actions,
                                                        i64 n, u64* children, float* reward,
                                                        u8* done, u8* nagari, i16* status,
                                                        u8* committed) {
-  __shared__ u64 tile[kTile * kRowWords];
+  __shared__ u64 tile[kRows * kRowWords];
   const int lane = threadIdx.x;
-  const i64 base = (i64)blockIdx.x * kTile;
+  const i64 base = (i64)blockIdx.x * kRows;
   const i64 i = base + lane;
-  const int count = n - base < kTile ? (int)(n - base) : kTile;
-  if (i < n) {
+  const int count = n - base < kRows ? (int)(n - base) : kRows;
+  if (lane < kRows && i < n) {
     const i64 id = ids[i];
     u64 row[kRowWords];
     if (valid_id(id, env_count)) {
@@ -582,7 +588,7 @@ __global__ __launch_bounds__(kTile) void branch_kernel(const u64* parents, i64 e
   u64* out = children + base * kRowWords;
   const int words = count * kRowWords;
 #pragma unroll
-  for (int j = 0; j < kRowWords; ++j) {
+  for (int j = 0; j < (kRows * kRowWords + kTile - 1) / kTile; ++j) {
     const int w = j * kTile + lane;
     if (w < words) out[w] = tile[w];
   }
@@ -727,34 +733,37 @@ void play_kernel(
 // ------------------------------------------------------------ step + observe ----
 // step_kernel<3> (step with the caller's actions, then the auto-reset of finished rows)
 // followed by observe_kernel of the new states, in one launch: the PPO rollout's engine
-// between two actor passes.  Two waves per tile of 64 games: both stage the rows in;
+// between two actor passes.  Two waves per tile of kRows games: both stage the rows in;
 // wave 0 steps its games, deals the finished ones their next game (the pre-dealt spare,
 // dealt into its slot first if stale, as play_kernel does), builds the new states'
 // observation records in LDS and packs the rows; then both waves store the observation
 // and the rows.  The rows are read and written once, where the two launches read them
 // twice and wrote them once more.
-template <bool kBf16>
-__global__ __launch_bounds__(kPlayThreads) __attribute__((amdgpu_waves_per_eu(2)))
+constexpr int kStepObserveRows = 32;  // games a tile (see cugo_step_observe_spares)
+
+template <bool kBf16, int kRows, int kThreads>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void step_observe_kernel(u64* states, i64 n, const i64* actions, float* reward, u8* done,
                          u8* nagari, i16* status, u8* committed, AutoReset ar, void* features,
                          u8* legal, u8* player, u8* obs_done, i16* obs_status) {
-  __shared__ ObserveTile t;   // the rows in, the new rows out
-  __shared__ RecordBuffer rb;  // the new states' observation records
-  __shared__ int next_item;    // store_observation's work counter
-  const i64 base = tile_base();
-  const int count = tile_count(base, n);
+  static_assert(kRows >= 1 && kRows <= kTile, "a tile is at most one wavefront of games");
+  __shared__ u64 rows[kRows * kRowWords];     // the rows in, the new rows out
+  __shared__ RecordBufferOf<kRows> rb;        // the new states' observation records
+  __shared__ int next_item;                   // store_observation's work counter
+  const i64 base = (i64)blockIdx.x * kRows;
+  const int count = n - base < kRows ? (int)(n - base) : kRows;
   const int tid = threadIdx.x;
   const int lane = tid & (kTile - 1);
   const int wave = tid / kTile;
   const i64 i = base + lane;
   if (tid == 0) next_item = 0;
-  stage_in<kPlayThreads>(t.rows, states, nullptr, base, count, n);
+  stage_in<kThreads, kRows>(rows, states, nullptr, base, count, n);
   __syncthreads();
   if (wave == 0 && lane < count) {
     u32 gen = ar.generation[i];
     const i64 srow = spare_row(ar, i, gen + 1u);
     const u32 sgen = ar.spare_gen[srow];  // issued before the step so its latency hides
-    u64* row = t.rows + lane * kRowWords;
+    u64* row = rows + lane * kRowWords;
     Env e = unpack_row(row);
     const StepOut so = torch_step(e, clamp_action(actions[i]));
     reward[i] = (float)so.reward0;
@@ -783,8 +792,8 @@ void step_observe_kernel(u64* states, i64 n, const i64* actions, float* reward, 
     pack_row(e, row);
   }
   __syncthreads();
-  store_observation<kPlayClaim, kBf16>(rb, base, count, features, legal, &next_item);
-  stage_out<kPlayThreads>(t.rows, states, nullptr, base, count, n);
+  store_observation<kPlayClaim, kBf16, kRows>(rb, base, count, features, legal, &next_item);
+  stage_out<kThreads, kRows>(rows, states, nullptr, base, count, n);
 }
 
 // ---------------------------------------------------------- branch + observe ----
@@ -1391,12 +1400,20 @@ int cugo_step_observe_spares(uint8_t* states, const int64_t* actions, int64_t n,
   if (n == 0) return 0;
   const AutoReset ar{base_seed, (u64)seed_stride, generation, reinterpret_cast<u64*>(sampler),
                      reinterpret_cast<u64*>(spares), spare_gen, n, (u32)(spare_slots - 1)};
+  // Games a tile: measured on MI355X at 32,768 rows (the PPO rollout's batch), us a launch
+  // for (games, threads): (64, 128) 54.0, (32, 128) 44.2, (32, 64) 50.3, (24, 64) 50.1,
+  // (16, 64) 45.5, (16, 128) 71.9.  A wavefront runs the union of its games' rule paths, so
+  // fewer games a wavefront execute fewer divergent branches, while more wavefronts than
+  // the ~210 VGPRs let a SIMD hold (two) cost a second round.
+  constexpr int kRows = kStepObserveRows, kThreads = kPlayThreads;
   if (features_dtype == CUGO_DTYPE_BF16)
-    step_observe_kernel<true><<<tiles(n), kPlayThreads, 0, stream>>>(
+    step_observe_kernel<true, kRows, kThreads><<<(unsigned)((n + kRows - 1) / kRows), kThreads,
+                                                0, stream>>>(
         reinterpret_cast<u64*>(states), n, actions, reward, done, nagari, status, committed, ar,
         features, legal, player, obs_done, obs_status);
   else
-    step_observe_kernel<false><<<tiles(n), kPlayThreads, 0, stream>>>(
+    step_observe_kernel<false, kRows, kThreads><<<(unsigned)((n + kRows - 1) / kRows), kThreads,
+                                                 0, stream>>>(
         reinterpret_cast<u64*>(states), n, actions, reward, done, nagari, status, committed, ar,
         features, legal, player, obs_done, obs_status);
   return launched();
@@ -1460,7 +1477,7 @@ int cugo_branch_indexed(const uint8_t* states, int64_t env_count, const int64_t*
                  !committed)))
     return kBadArgument;
   if (n == 0) return 0;
-  branch_kernel<<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<const u64*>(states),
+  branch_kernel<kTile><<<tiles(n), kTile, 0, stream>>>(reinterpret_cast<const u64*>(states),
                                                 env_count, ids, actions, n,
                                                 reinterpret_cast<u64*>(children), reward,
                                                 done, nagari, status, committed);
