@@ -111,13 +111,32 @@ def check_no_packed_fp32(lib: Path) -> None:
           "device code", flush=True)
 
 
-def build_library() -> Path:
-    generate_stop_bits()
+SOURCES = ("kernels.hip", "decode.hip", "selfplay.hip", "mlp.hip", "linear.hip")
+HEADERS = (CSRC / "engine.h", REPO / "include" / "cugo_hip.h")
+
+
+def build_library(force: bool = True) -> Path:
+    """Compiles each source to an object under _build/ (in parallel; with force=False only
+    those older than their source or a shared header), then links the library."""
+    generate_stop_bits(force=force)
     out = PKG / "libcugo_hip.so"
-    _run([HIPCC, *HIP_FLAGS, "-shared", str(CSRC / "kernels.hip"), str(CSRC / "decode.hip"),
-          str(CSRC / "selfplay.hip"), str(CSRC / "mlp.hip"),
-          "-o", str(out)])
-    check_no_packed_fp32(out)
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    shared = [*HEADERS, CSRC / "stop_bits.inc"]
+    procs, objs = [], []
+    for name in SOURCES:
+        src, obj = CSRC / name, objdir / (name + ".o")
+        objs.append(obj)
+        if force or not _newer(obj, [src, *shared]):
+            cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+            print("+", " ".join(cmd), flush=True)
+            procs.append((name, subprocess.Popen(cmd)))
+    failed = [name for name, p in procs if p.wait() != 0]
+    if failed:
+        raise RuntimeError(f"hipcc failed for {failed}")
+    if procs or not _newer(out, objs):
+        _run([HIPCC, *HIP_FLAGS, "-shared", *map(str, objs), "-o", str(out)])
+        check_no_packed_fp32(out)
     return out
 
 
@@ -171,4 +190,4 @@ if __name__ == "__main__":
     what = sys.argv[1:] or ["all"]
     for item in what:
         {"all": build_all, "lib": build_library, "ext": build_extension,
-         "oracle": build_oracle}[item]()
+         "oracle": build_oracle, "lib-changed": lambda: build_library(force=False)}[item]()

@@ -1,0 +1,297 @@
+// bf16 linear layers on MFMA for gfx950: Y = act(X W^T + b), optionally with GELU.
+//
+// The sequence policy's decoder step (cugo_amd/seq_decode.py, the reference's
+// SeqNet.cached_step, python/cugo_seq50.py:291-322) runs its nn.Linear layers over one
+// token a row: 4,096 query rows and 8,192 event rows a self-play step, K = 256 (1,024 for
+// linear2), N = 256-1,024.  At these sizes a library GEMM reaches a fraction of HBM
+// bandwidth on its operand bytes, and the feed-forward's GELU is one more pass over the
+// widest activation (N = 1,024).  This kernel is sized for them.
+//
+// What bounds it is the vector memory path of a CU, not the MFMA pipe: a load instruction
+// costs the texture addresser a cycle for every cache line each 16-lane quarter of the
+// wavefront touches.  An MFMA operand fragment read straight from a row-major matrix puts
+// 16 rows (16 lines, 16 bytes of each) in every quarter-wave: 16 bytes a cycle.  So:
+//   * W is packed once in fragment order (cugo_mlp_pack_weight: 64 lanes x 16 bytes of one
+//     fragment are 1 KiB of contiguous memory), and each wavefront loads its fragments
+//     straight into a register ring D K steps ahead of the MFMAs;
+//   * the workgroup's X panel (BM rows x all of K, at most 128 KiB) is copied into LDS
+//     once with row-contiguous loads (a quarter-wave reads 256 contiguous bytes), in
+//     K-step-major order with the 16-byte groups of a row XOR-swizzled, so one fragment
+//     (16 rows x 64 bytes) is a conflict-free 1 KiB read; one barrier, then the
+//     wavefronts read their X fragments from LDS;
+//   * a workgroup is a WR x WC grid of wavefronts, each owning 16 TM rows x 16 TN columns
+//     of the tile (BM = 16 TM WR, BN = 16 TN WC): wavefronts of one grid column load the
+//     same W fragments, the second from L1;
+//   * v_mfma_f32_16x16x32_bf16 with W as the A operand and X as the B operand, i.e. the
+//     product is formed transposed: lane l then holds Y[16 mt + l % 16][16 nt + 4 (l / 16)
+//     + 0..3], four adjacent columns;
+//   * the epilogue adds the bias, rounds to bf16 (what the library layer stores), and for
+//     GELU evaluates x / 2 (1 + erf(x / sqrt 2)) in fp32 on that bf16 value and rounds
+//     again, the two steps nn.Linear + nn.GELU() take in bf16; the tile then goes through
+//     the LDS (over the dead X panel) so that it leaves in 16-byte row pieces, whole lines
+//     a quarter-wave (stored from the accumulator layout, a quarter-wave would write 8
+//     bytes into each of 16 rows).
+// Workgroup ids are remapped so that consecutive tiles run on one XCD (the dispatcher
+// deals workgroups to the 8 XCDs in turn), keeping a row panel's reads in one L2.
+//
+// Arithmetic: bf16 operands, fp32 accumulation in K order; partial rows and columns are
+// clamped on load and masked on store.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "../../include/cugo_hip.h"
+
+namespace cugo_amd {
+namespace linear {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kK = 32;  // K per MFMA
+constexpr int kFragBytes = 64 * 16;
+
+struct Args {
+  const __bf16* x;
+  const __bf16* w;     // packed: fragment (tile, step) at (tile * KS + step) * 1 KiB
+  const __bf16* bias;  // [n] or NULL
+  __bf16* y;
+  int m, n, ldx, ldy;
+  int col_blocks;  // workgroups along n
+  int wtiles;      // 16-row tiles of the packed W
+};
+
+__device__ inline float gelu(float v) {
+  return v * 0.5f * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
+// Element offset of (row r, column k) in the LDS X panel of BM rows: K step major
+// ([k / 32][r][32]), the 16-byte group g of a row's 64 bytes at g ^ ((r >> 1) & 3).
+template <int BM>
+__device__ inline int xs_at(int r, int k) {
+  return ((k >> 5) * BM + r) * 32 + ((((k >> 3) & 3) ^ ((r >> 1) & 3)) << 3) + (k & 7);
+}
+
+template <int TM, int TN, int WR, int WC, int D, int KS, int ACT>
+__global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
+  constexpr int kT = 64 * WR * WC;         // threads
+  constexpr int BM = 16 * TM * WR;         // rows of the workgroup's tile
+  constexpr int BN = 16 * TN * WC;         // columns
+  constexpr int R = D + 1;                 // ring slots
+  constexpr int kGroups = BM * KS * 4;     // 16-byte groups of the X panel
+  constexpr int kBatch = 8;                // loads in flight a thread while staging
+  constexpr int kOutStride = BN + 16;      // elements a row of the staged output tile
+  constexpr int kXsElems = BM * KS * kK;
+  constexpr int kLds = kXsElems > BM * kOutStride ? kXsElems : BM * kOutStride;
+  static_assert(kGroups % kT == 0, "whole staging rounds");
+  static_assert(kLds * 2 <= 160 * 1024, "the tile fits the LDS");
+  __shared__ __attribute__((aligned(16))) __bf16 xs[kLds];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wr = wave / WC, wc = wave % WC;
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  const int rb = bid / a.col_blocks;
+  const int m0 = rb * BM;
+  const int nb0 = (bid - rb * a.col_blocks) * BN;  // the workgroup's first column
+  const int n0 = nb0 + wc * 16 * TN;               // this wavefront's
+  const int r0 = wr * 16 * TM;                     // this wavefront's first row in the tile
+  const int l16 = lane & 15, q4 = lane >> 4;
+
+  // W's first D K steps, issued before the X panel's copy so both are in flight.
+  const auto wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(a.w), (short)0,
+                                                     a.wtiles * KS * kFragBytes, 0x00020000);
+  int wt[TN];  // byte offset of fragment (tile, 0); tiles past the end read the last one
+#pragma unroll
+  for (int t = 0; t < TN; ++t) wt[t] = min(n0 / 16 + t, a.wtiles - 1) * KS * kFragBytes;
+  bf16x8 wb[R][TN];
+  auto load_w = [&](int s, int slot) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+      wb[slot][t] = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(wrs, lane * 16, wt[t] + s * kFragBytes, 0));
+  };
+#pragma unroll
+  for (int j = 0; j < D; ++j)
+    if (j < KS) load_w(j, j);
+
+  // The X panel: thread tid copies 16-byte groups tid, tid + kT, ... (row-major order,
+  // so a quarter-wave reads 256 contiguous bytes of one row).
+  const auto xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__bf16*>(a.x), (short)0, ((a.m - 1) * a.ldx + KS * kK) * 2, 0x00020000);
+#pragma unroll
+  for (int b0 = 0; b0 < kGroups; b0 += kT * kBatch) {
+    uint4 v[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int gi = b0 + j * kT + tid;
+      if (gi < kGroups) {
+        const int r = gi / (KS * 4), c = gi % (KS * 4);
+        const int row = min(m0 + r, a.m - 1);
+        v[j] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, (row * a.ldx + 8 * c) * 2, 0, 0));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int gi = b0 + j * kT + tid;
+      if (gi < kGroups) {
+        const int r = gi / (KS * 4), c = gi % (KS * 4);
+        *reinterpret_cast<uint4*>(xs + xs_at<BM>(r, 8 * c)) = v[j];
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int t = 0; t < TN; ++t) acc[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // The K loop is unrolled whole (KS is a template argument): with a run-time trip count
+  // the compiler cannot count the loads in flight across the loop's branches and waits
+  // for all of them before every step's MFMAs.
+  const int x_lane = xs_at<BM>(r0 + l16, 8 * q4);
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (s + D < KS) load_w(s + D, (s + D) % R);
+    bf16x8 xa[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      xa[i] = *reinterpret_cast<const bf16x8*>(xs + x_lane + (s * BM + 16 * i) * 32);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[s % R][t], xa[i], acc[i][t],
+                                                            0, 0, 0);
+    // Keep the ring: without a fence the scheduler hoists later K steps' loads.
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Epilogue: bias, bf16, GELU, into the LDS as a row-major BM x BN tile (the X panel is
+  // dead once every wavefront is past the barrier), then out in 16-byte row pieces: a
+  // quarter-wave writes whole lines instead of 16 rows' 8 bytes each.
+  float bias[TN][4];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int col = n0 + 16 * t + 4 * q4;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) bias[t][c] = 0.f;
+    if (a.bias != nullptr && col < a.n) {
+      const bf16x4 bv = *reinterpret_cast<const bf16x4*>(a.bias + col);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) bias[t][c] = (float)bv[c];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      bf16x4 out;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const __bf16 v = (__bf16)(acc[i][t][c] + bias[t][c]);
+        out[c] = ACT == CUGO_LINEAR_GELU ? (__bf16)gelu((float)v) : v;
+      }
+      const int r = r0 + 16 * i + l16, c = wc * 16 * TN + 16 * t + 4 * q4;
+      *reinterpret_cast<bf16x4*>(xs + r * kOutStride + c) = out;
+    }
+  __syncthreads();
+  constexpr int kPieces = BM * BN / 8;  // 16-byte pieces of the tile
+  const bool wide = (a.ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+#pragma unroll
+  for (int p0 = 0; p0 < kPieces; p0 += kT) {
+    const int p = p0 + tid;
+    if (p < kPieces) {
+      const int r = p / (BN / 8), c = (p % (BN / 8)) * 8;
+      const int row = m0 + r, col = nb0 + c;
+      if (row < a.m && col < a.n) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xs + r * kOutStride + c);
+        __bf16* dst = a.y + (int64_t)row * a.ldy + col;
+        if (wide && col + 8 <= a.n) {
+          *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+          *reinterpret_cast<uint2*>(dst) = uint2{v.x, v.y};
+          if (col + 8 <= a.n) *reinterpret_cast<uint2*>(dst + 4) = uint2{v.z, v.w};
+        }
+      }
+    }
+  }
+}
+
+template <int TM, int TN, int WR, int WC, int D, int KS>
+int launch_ks(const Args& a, int act, hipStream_t stream) {
+  constexpr int BM = 16 * TM * WR;
+  if constexpr (BM * KS * kK * 2 > 160 * 1024) {
+    return -7;  // the X panel does not fit the LDS at this depth
+  } else {
+    const unsigned grid = (unsigned)(((a.m + BM - 1) / BM) * a.col_blocks);
+    if (act == CUGO_LINEAR_GELU)
+      linear_kernel<TM, TN, WR, WC, D, KS, CUGO_LINEAR_GELU>
+          <<<grid, 64 * WR * WC, 0, stream>>>(a);
+    else
+      linear_kernel<TM, TN, WR, WC, D, KS, CUGO_LINEAR_NONE>
+          <<<grid, 64 * WR * WC, 0, stream>>>(a);
+    return (int)hipGetLastError();
+  }
+}
+
+template <int TM, int TN, int WR, int WC, int D>
+int launch(const Args& base, int k, int act, hipStream_t stream) {
+  Args a = base;
+  a.col_blocks = (a.n + 16 * TN * WC - 1) / (16 * TN * WC);
+  switch (k / kK) {
+    case 2: return launch_ks<TM, TN, WR, WC, D, 2>(a, act, stream);
+    case 4: return launch_ks<TM, TN, WR, WC, D, 4>(a, act, stream);
+    case 8: return launch_ks<TM, TN, WR, WC, D, 8>(a, act, stream);
+    case 16: return launch_ks<TM, TN, WR, WC, D, 16>(a, act, stream);
+    case 32: return launch_ks<TM, TN, WR, WC, D, 32>(a, act, stream);
+    default: return -3;
+  }
+}
+
+}  // namespace linear
+}  // namespace cugo_amd
+
+using namespace cugo_amd::linear;
+
+extern "C" {
+
+int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const void* bias,
+                int64_t m, int64_t n, int64_t k, void* y, int64_t ldy, int tile,
+                hipStream_t stream) {
+  if (m < 0 || n < 1 || k < 1 || (m > 0 && (!x || !w_packed || !y))) return -1;
+  if (act != CUGO_LINEAR_NONE && act != CUGO_LINEAR_GELU) return -2;
+  const bool k_ok = k == 64 || k == 128 || k == 256 || k == 512 || k == 1024;
+  if (!k_ok || n % 4 != 0 || ldx < k || ldx % 8 != 0 || ldy < n || ldy % 4 != 0) return -3;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed)) % 16 != 0 ||
+      (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(bias)) % 8 != 0)
+    return -4;
+  // Buffer offsets are 32-bit byte offsets.
+  if (m * ldx >= (int64_t(1) << 30) || (n + 15) * k >= (int64_t(1) << 30)) return -5;
+  if (m == 0) return 0;
+  const Args a{static_cast<const __bf16*>(x), static_cast<const __bf16*>(w_packed),
+               static_cast<const __bf16*>(bias), static_cast<__bf16*>(y),
+               (int)m, (int)n, (int)ldx, (int)ldy, 0, (int)((n + 15) / 16)};
+  if (tile == 0) {  // by the decoder step's shapes: 64-row tiles once 32-row ones pass
+    const int64_t blocks32 = ((m + 31) / 32) * ((n + 127) / 128);  // ~4 a CU
+    tile = blocks32 > 1024 ? 2 : 1;
+  }
+  switch (tile) {
+    case 1: return launch<2, 2, 1, 4, 3>(a, (int)k, act, stream);  // 32 rows x 128 columns
+    case 2: return launch<2, 2, 2, 4, 3>(a, (int)k, act, stream);  // 64 x 128, 8 wavefronts
+    case 3: return launch<2, 4, 2, 2, 2>(a, (int)k, act, stream);  // 64 x 128
+    case 4: return launch<4, 2, 2, 4, 2>(a, (int)k, act, stream);  // 128 x 128, 8 wavefronts
+    case 5: return launch<2, 2, 2, 2, 3>(a, (int)k, act, stream);  // 64 x 64
+    default: return -6;
+  }
+}
+
+}  // extern "C"

@@ -839,6 +839,35 @@ std::vector<torch::Tensor> add_layernorm(torch::Tensor x, c10::optional<torch::T
   return {x_out, ln};
 }
 
+// linear(x [m, k] bf16, w_packed, n, bias [n] bf16 or None, gelu, tile) -> y [m, n] bf16:
+// nn.Linear (and with gelu=True the nn.GELU() after it) of the decoder step
+// (python/cugo_seq50.py:291-322) in one launch.  w_packed is the layer's weight [n, k] as
+// mlp_pack_weight(weight, roundup(n, 16), k) lays it out.  x may be a row-strided view
+// (unit stride along k).
+torch::Tensor linear(torch::Tensor x, torch::Tensor w_packed, int64_t n,
+                     c10::optional<torch::Tensor> bias, bool gelu, int64_t tile) {
+  TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16 && x.stride(1) == 1,
+              "x must be a CUDA bfloat16 [m, k] tensor with unit stride along k");
+  const int64_t m = x.size(0), k = x.size(1);
+  TORCH_CHECK(n > 0 && w_packed.scalar_type() == at::kBFloat16 && w_packed.is_contiguous() &&
+                  w_packed.numel() == (n + 15) / 16 * 16 * k,
+              "w_packed must be a contiguous bfloat16 tensor of roundup(n, 16) * k elements");
+  check_same_device(x, w_packed, "x", "w_packed");
+  if (bias.has_value()) {
+    TORCH_CHECK(bias->scalar_type() == at::kBFloat16 && bias->is_contiguous() && bias->numel() == n,
+                "bias must be a contiguous bfloat16 [n] tensor");
+    check_same_device(x, *bias, "x", "bias");
+  }
+  const DeviceGuard guard(x.device());
+  auto y = torch::empty({m, n}, x.options());
+  const int64_t ldx = m > 1 ? x.stride(0) : k;
+  check_call(cugo_linear(gelu ? CUGO_LINEAR_GELU : CUGO_LINEAR_NONE, x.data_ptr(), ldx,
+                         w_packed.data_ptr(), bias.has_value() ? bias->data_ptr() : nullptr, m, n,
+                         k, y.data_ptr(), n, static_cast<int>(tile), stream()),
+             "linear");
+  return y;
+}
+
 // masked_argmax(logits [n, A] f32/bf16, legal bool [n, A]) -> int64 [n]: the greedy
 // action of python/cugo_eval50.py:125-127 (argmax of logits.float() masked with -1e30).
 torch::Tensor masked_argmax(torch::Tensor logits, torch::Tensor legal) {
@@ -1265,6 +1294,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("add_layernorm", &add_layernorm, "x + y and LayerNorm(x + y) in one launch",
         pybind11::arg("x"), pybind11::arg("y"), pybind11::arg("weight"), pybind11::arg("bias"),
         pybind11::arg("eps"));
+  m.def("linear", &linear, "bf16 x weight^T + bias, optionally followed by GELU, in one launch",
+        pybind11::arg("x"), pybind11::arg("w_packed"), pybind11::arg("n"),
+        pybind11::arg("bias") = pybind11::none(), pybind11::arg("gelu") = false,
+        pybind11::arg("tile") = 0);
   pybind11::class_<SelfPlayState>(m, "SelfPlayState",
                                    "A self-play wave's tensors and its step bookkeeping")
       .def(pybind11::init<int64_t, int64_t, torch::Tensor, torch::Tensor, torch::Tensor,

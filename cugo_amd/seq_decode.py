@@ -7,14 +7,17 @@ like it: `model.encoder.layers` of pre-norm `nn.TransformerEncoderLayer`s
 -> linear2) and a cache with `k`, `v` ([layers, rows, heads, slots, dh]), `length`,
 `heads`, `slots`, `row_ids`.  The per-layer `index_put_` of the new key/value and the
 decode attention run as one HIP launch (`decode_attention_append`, reading q, k and v in
-place from the packed in-projection), and each residual add with the pre-norm that
-follows it as another (`add_layernorm`).
+place from the packed in-projection), each residual add with the pre-norm that follows
+it as another (`add_layernorm`), and each bf16 linear layer as one (`linear`), linear1
+with the GELU after it.
 
 `KVCache` mirrors the reference cache (python/cugo_seq50.py:325-339) with the slot count
 as a parameter (the reference fixes it at MAX_EVENTS + 2 = 50).
 """
 
 from __future__ import annotations
+
+import weakref
 
 import torch
 import torch.nn.functional as F
@@ -49,7 +52,7 @@ def _ext():
     return _EXT
 
 
-def _add_norm(x: torch.Tensor, y: torch.Tensor | None, norm: nn.Module):
+def add_norm(x: torch.Tensor, y: torch.Tensor | None, norm: nn.Module):
     """(x + y, norm(x + y)), or (x, norm(x)) for y None: one HIP launch
     (`add_layernorm`) for an affine LayerNorm over the last dim of a bf16/fp32 row of a
     supported width, torch's two ops otherwise."""
@@ -64,6 +67,63 @@ def _add_norm(x: torch.Tensor, y: torch.Tensor | None, norm: nn.Module):
     return x, norm(x)
 
 
+def is_exact_gelu(act) -> bool:
+    """The exact (erf) GELU, as a function or a module."""
+    return act is F.gelu or (isinstance(act, nn.GELU) and act.approximate == "none")
+
+
+def _fits_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> bool:
+    """The shapes and alignments `linear` takes (include/cugo_hip.h, cugo_linear)."""
+    return (x.dim() == 2 and x.is_cuda and x.dtype == torch.bfloat16 and x.stride(1) == 1
+            and weight.dtype == torch.bfloat16 and weight.dim() == 2
+            and weight.shape[1] == x.shape[1] and x.shape[1] in (64, 128, 256, 512, 1024)
+            and weight.shape[0] % 4 == 0 and (x.shape[0] <= 1 or x.stride(0) % 8 == 0)
+            and x.data_ptr() % 16 == 0
+            and (bias is None or (bias.dtype == torch.bfloat16 and bias.is_contiguous()
+                                  and bias.data_ptr() % 8 == 0)))
+
+
+_PACKED: dict[int, tuple] = {}
+
+
+def packed_weight(weight: torch.Tensor) -> torch.Tensor:
+    """`weight` [n, k] in the fragment order `linear` reads (mlp_pack_weight with n padded
+    to 16), built on first use and rebuilt into the same buffer when the weight changes
+    in place (its version), so a captured HIP graph reads the new values."""
+    n, k = weight.shape
+    key = (weight.data_ptr(), weight._version)
+    hit = _PACKED.get(id(weight))
+    if (hit is None or hit[0]() is not weight or hit[2].device != weight.device
+            or hit[2].numel() != (n + 15) // 16 * 16 * k):
+        hit = (weakref.ref(weight), key,
+               _ext().mlp_pack_weight(weight.detach().contiguous(), (n + 15) // 16 * 16, k))
+    elif hit[1] != key:
+        hit[2].copy_(_ext().mlp_pack_weight(weight.detach().contiguous(), (n + 15) // 16 * 16, k))
+        hit = (hit[0], key, hit[2])
+    _PACKED[id(weight)] = hit
+    return hit[2]
+
+
+def prepare_linears(model: nn.Module) -> None:
+    """Packs every encoder layer's linear weights now (before a HIP-graph capture)."""
+    for layer in model.encoder.layers:
+        for w in (layer.self_attn.in_proj_weight, layer.self_attn.out_proj.weight,
+                  layer.linear1.weight, layer.linear2.weight):
+            if w.dtype == torch.bfloat16 and w.is_cuda:
+                packed_weight(w)
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+           gelu: bool = False) -> torch.Tensor:
+    """F.linear(x, weight, bias), then F.gelu when `gelu`: one HIP launch (`linear`) for
+    bf16 rows with K in {64, ..., 1,024} and N a multiple of 4, torch's ops otherwise."""
+    if _fits_linear(x, weight, bias):
+        return _ext().linear(x, packed_weight(weight), weight.shape[0],
+                             None if bias is None else bias.detach(), gelu)
+    y = F.linear(x, weight, bias)
+    return F.gelu(y) if gelu else y
+
+
 def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = None,
                 rows: torch.Tensor | None = None) -> torch.Tensor:
     """One token per cache row (x [n, d]); its key/value go to slot cache.length[row].
@@ -71,8 +131,8 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
     Each token attends every cached slot plus itself; `slots` bounds the slot index;
     `rows` names each token's cache row (default: every row in order).  Returns the
     final hidden state [n, d].  Same steps as python/cugo_seq50.py:291-322; each residual
-    add and the pre-norm after it run as one launch, and q, k and v are read in place from
-    the packed in-projection."""
+    add and the pre-norm after it run as one launch, q, k and v are read in place from
+    the packed in-projection, and linear1 + GELU is one launch."""
     n, d = x.shape
     heads = cache.heads
     dh = d // heads
@@ -81,17 +141,22 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
     length = cache.length if rows is None else cache.length.index_select(0, row_ids)
     pos = length.clamp_max(t - 1)
     layers = model.encoder.layers
-    x, h = _add_norm(x, None, layers[0].norm1)
+    x, h = add_norm(x, None, layers[0].norm1)
     for i, layer in enumerate(layers):
         attn = layer.self_attn
-        q, k, v = F.linear(h, attn.in_proj_weight, attn.in_proj_bias).chunk(3, -1)
+        q, k, v = linear(h, attn.in_proj_weight, attn.in_proj_bias).chunk(3, -1)
         a = decode_attention_append(q.reshape(n, heads, dh), k.reshape(n, heads, dh),
                                     v.reshape(n, heads, dh), cache.k[i], cache.v[i], pos,
                                     row_ids)
-        x, h = _add_norm(x, attn.out_proj(a.reshape(n, d)), layer.norm2)
-        m = layer.linear2(layer.activation(layer.linear1(h)))
+        x, h = add_norm(x, linear(a.reshape(n, d), attn.out_proj.weight, attn.out_proj.bias),
+                         layer.norm2)
+        if is_exact_gelu(layer.activation):
+            u = linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True)
+        else:
+            u = layer.activation(linear(h, layer.linear1.weight, layer.linear1.bias))
+        m = linear(u, layer.linear2.weight, layer.linear2.bias)
         if i + 1 < len(layers):
-            x, h = _add_norm(x, m, layers[i + 1].norm1)
+            x, h = add_norm(x, m, layers[i + 1].norm1)
         else:
             x = x + m
     return x

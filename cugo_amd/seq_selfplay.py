@@ -25,7 +25,8 @@ import torch
 from torch import nn
 
 from .cugo_torch50_ext import load_extension
-from .seq_decode import KVCache, cached_step
+from .seq_decode import (KVCache, add_norm, cached_step, is_exact_gelu, linear,
+                         packed_weight, prepare_linears)
 
 FEATURES = 720
 ACTIONS = 179
@@ -109,9 +110,13 @@ class SeqPolicy(nn.Module):
         return hit[1]
 
     def prepare(self) -> None:
-        """Build the transposed token weights now (before a HIP-graph capture)."""
+        """Build the transposed token weights and the packed encoder weights now (before a
+        HIP-graph capture)."""
         self._weight_t("event_in")
         self._weight_t("start_in")
+        prepare_linears(self)
+        if self.head[0].weight.dtype == torch.bfloat16 and self.head[0].weight.is_cuda:
+            packed_weight(self.head[0].weight)
 
     def start_token(self, start: torch.Tensor, seat: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:271-274: start_in(encode_start) + position[0] + token_type[0]."""
@@ -145,8 +150,13 @@ class SeqPolicy(nn.Module):
         return self.query_in(q_in) + self.token_type[2]
 
     def readout(self, h: torch.Tensor) -> torch.Tensor:
-        """cugo_seq50.py:187-189 and :288-289."""
-        out = self.head(self.norm(h))
+        """cugo_seq50.py:187-189 and :288-289: head(norm(h)), the norm as one HIP launch
+        and the head's first Linear with its GELU as another where they fit."""
+        if h.dim() == 2 and is_exact_gelu(self.head[1]):
+            _, z = add_norm(h, None, self.norm)
+            out = self.head[2](linear(z, self.head[0].weight, self.head[0].bias, gelu=True))
+        else:
+            out = self.head(self.norm(h))
         return out.squeeze(-1) if out.shape[-1] == 1 else out
 
     def cached_step(self, cache: KVCache, x: torch.Tensor, slots: int | None = None,

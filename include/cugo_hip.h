@@ -340,6 +340,22 @@ int cugo_start_tokens(int dtype, const int64_t* start, const int64_t* seat, int6
 int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weight,
                        const void* bias, float eps, int64_t n, int64_t d, void* x_out, void* ln,
                        hipStream_t stream);
+/* cugo_linear: the nn.Linear layers of SeqNet.cached_step (cugo_seq50.py:291-322: the
+ * packed in-projection, out_proj, linear1 followed by the layer's GELU, linear2), bf16:
+ * y = act(x w^T + bias), each element rounded to bf16 after the bias and, with
+ * CUGO_LINEAR_GELU, GELU(v) = v / 2 (1 + erf(v / sqrt 2)) of that value rounded again.
+ * x [m, k] with row stride ldx; w [n, k] (nn.Linear's layout) given as w_packed, its
+ * cugo_mlp_pack_weight form with rows_pad = roundup(n, 16) and cols_pad = k; bias [n] or
+ * NULL; y [m, n] with row stride ldy; fp32 accumulation.  Requires k in {64, 128, 256,
+ * 512, 1024}, n % 4 == 0, ldx % 8 == 0, ldy % 4 == 0, x and w_packed 16-byte aligned, y
+ * and bias 8-byte aligned.  tile: 0 chooses the workgroup tile from k; 1-4 force 32 x 256,
+ * 32 x 128, 64 x 128 or 64 x 256 (rows x columns).  Returns -3 for an unsupported shape,
+ * -4 for misaligned pointers, -5 for sizes beyond 32-bit byte offsets. */
+#define CUGO_LINEAR_NONE 0
+#define CUGO_LINEAR_GELU 1
+int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const void* bias,
+                int64_t m, int64_t n, int64_t k, void* y, int64_t ldy, int tile,
+                hipStream_t stream);
 /* cugo_gumbel_sample: the sampling of WaveCollector._step (cugo_seq_selfplay50.py:125-130)
  * given the uniforms torch.rand_like drew: masked = legal ? logits : -1e30;
  * actions[i] = argmax_a(masked - log(-log(clamp(u, 1e-20, 1)))) (first index on ties);

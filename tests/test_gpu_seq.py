@@ -165,6 +165,71 @@ def test_add_layernorm_matches_torch(ext, dtype, d):
             assert same >= 0.98, same
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 768, 256), (8192, 1024, 256), (4096, 256, 1024),
+                                   (1001, 260, 128), (1, 4, 64), (70, 1028, 512)])
+def test_linear_matches_float64(ext, m, n, k):
+    """`linear` against the float64 product of the same bf16 operands, + bias, rounded to
+    bf16: every element within the bound of an fp32 sum of k products (k 2^-24 times the
+    sum of their magnitudes) rounded to bf16 (one unit), 98 % bit-identical; its GELU
+    form equals torch's F.gelu of its plain form bit for bit; every workgroup tile gives
+    identical bits (the same K order); a row-strided x, no bias, the packed-weight
+    cache (rebuilt in place when the weight changes), and the shape checks."""
+    from cugo_amd.seq_decode import linear, packed_weight
+
+    announce(f"linear m={m} n={n} k={k}")
+    g = torch.Generator(device="cpu").manual_seed(m + n + k)
+    x = (torch.randn(m, k, generator=g)).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(n, k, generator=g) * k ** -0.5).to(torch.bfloat16).to(DEV)
+    b = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    wp = ext.mlp_pack_weight(w, (n + 15) // 16 * 16, k)
+
+    def check(got, bias):
+        exact = x.double() @ w.double().T
+        mag = x.double().abs() @ w.double().abs().T
+        if bias is not None:
+            exact = exact + bias.double()
+            mag = mag + bias.double().abs()
+        delta = mag * (k + 1) * 2.0 ** -24
+        excess = (got.double() - exact).abs() - (exact.abs() * 2.0 ** -7 + 2 * delta)
+        assert float(excess.max()) <= 0.0, (int((excess > 0).sum()), float(excess.max()))
+        want = exact.to(torch.bfloat16)
+        same = float((got.view(torch.int16) == want.view(torch.int16)).float().mean())
+        assert same >= 0.98, same
+
+    got = ext.linear(x, wp, n, b)
+    assert got.shape == (m, n) and got.dtype == torch.bfloat16
+    check(got, b)
+    assert torch.equal(ext.linear(x, wp, n, b, gelu=True), torch.nn.functional.gelu(got))
+    for tile, rows in ((1, 32), (2, 64), (3, 64), (4, 128), (5, 64)):
+        if rows * k * 2 <= 160 * 1024:  # the X panel fits the LDS
+            assert torch.equal(ext.linear(x, wp, n, b, tile=tile), got), tile
+        else:
+            with pytest.raises(RuntimeError):
+                ext.linear(x, wp, n, b, tile=tile)
+    check(ext.linear(x, wp, n, None), None)
+    wide = torch.zeros(m, k + 40, dtype=torch.bfloat16, device=DEV)
+    wide[:, 8:8 + k] = x
+    assert torch.equal(ext.linear(wide[:, 8:8 + k], wp, n, b), got)
+    # the module-level wrapper packs the weight once and repacks it when it changes
+    assert torch.equal(linear(x, w, b), got)
+    p0 = packed_weight(w)
+    assert torch.equal(p0, wp) and packed_weight(w) is p0
+    w.mul_(-1.0)
+    assert packed_weight(w) is p0 and torch.equal(linear(x, w, b), ext.linear(x, p0, n, b))
+    assert torch.equal(p0, ext.mlp_pack_weight(w, (n + 15) // 16 * 16, k))
+    if m == 1:
+        with pytest.raises(RuntimeError):  # k = 96 is not a supported depth
+            ext.linear(torch.zeros(4, 96, dtype=torch.bfloat16, device=DEV),
+                       ext.mlp_pack_weight(torch.zeros(4, 96, dtype=torch.bfloat16,
+                                                       device=DEV), 16, 96), 4)
+        with pytest.raises(RuntimeError):  # n % 4
+            ext.linear(x, ext.mlp_pack_weight(w[:3].contiguous(), 16, k), 3)
+        with pytest.raises(RuntimeError):  # packed size does not match n
+            ext.linear(x, wp, n + 16, None)
+        with pytest.raises(RuntimeError):
+            ext.linear(x, wp, n, b, tile=6)
+
+
 def test_gumbel_sample_matches_reference(ext):
     announce("gumbel_sample")
     g = torch.Generator(device=DEV).manual_seed(3)
@@ -232,12 +297,13 @@ def _reference_step(policy, ref, actions_from=None):
     player = players.long()
     q = policy.query_token(features, legal)
     hidden = reference_cached_step(policy, ref["cache"], q, (player & 1) * w + ids)
-    logits = policy.readout(hidden).float()
+    logits = policy.head(policy.norm(hidden)).float()  # cugo_seq50.py:187-189, torch ops
     learner_move = torch.ones_like(active)
     if p:
         pids = torch.arange(p, device=DEV)
         opp_q = opp.query_token(features[:p], legal[:p])
-        opp_logits = opp.readout(reference_cached_step(opp, ref["opp_cache"], opp_q, pids)).float()
+        opp_h = reference_cached_step(opp, ref["opp_cache"], opp_q, pids)
+        opp_logits = opp.head(opp.norm(opp_h)).float()
         opp_move = player[:p] != ref["learner_seat"][:p]
         logits = torch.cat((torch.where(opp_move.unsqueeze(1), opp_logits, logits[:p]), logits[p:]))
         learner_move = torch.cat((~opp_move, learner_move[p:]))
