@@ -56,11 +56,21 @@ struct Args {
   const __bf16* x;
   const __bf16* w;     // packed: fragment (tile, step) at (tile * KS + step) * 1 KiB
   const __bf16* bias;  // [n] or NULL
-  __bf16* y;
+  __bf16* y;           // with kAddNorm: x_out = res + (x W^T + b)
   int m, n, ldx, ldy;
   int col_blocks;  // workgroups along n
   int wtiles;      // 16-row tiles of the packed W
+  // kAddNorm only (rows of n = BN elements, row stride ldy)
+  const __bf16* res;
+  const __bf16* ln_w;
+  const __bf16* ln_b;
+  __bf16* ln;
+  float eps;
 };
+
+// Epilogues beyond CUGO_LINEAR_NONE / CUGO_LINEAR_GELU: the residual add and the
+// LayerNorm after it (a pre-norm layer's out_proj or linear2 followed by the next norm).
+constexpr int kAddNorm = 2;
 
 __device__ inline float gelu(float v) {
   return v * 0.5f * (1.0f + erff(v * 0.70710678118654752440f));
@@ -84,7 +94,6 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
   constexpr int kOutStride = BN + 16;      // elements a row of the staged output tile
   constexpr int kXsElems = BM * KS * kK;
   constexpr int kLds = kXsElems > BM * kOutStride ? kXsElems : BM * kOutStride;
-  static_assert(kGroups % kT == 0, "whole staging rounds");
   static_assert(kLds * 2 <= 160 * 1024, "the tile fits the LDS");
   __shared__ __attribute__((aligned(16))) __bf16 xs[kLds];
 
@@ -118,6 +127,18 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
 #pragma unroll
   for (int j = 0; j < D; ++j)
     if (j < KS) load_w(j, j);
+
+  // kAddNorm: the residual rows this wavefront normalises (row wave + WR WC j of the
+  // tile), loaded now so their latency hides behind the GEMM.
+  constexpr int kNormRows = ACT == kAddNorm ? BM / (WR * WC) : 1;
+  bf16x4 res_v[kNormRows];
+  if constexpr (ACT == kAddNorm) {
+#pragma unroll
+    for (int j = 0; j < kNormRows; ++j) {
+      const int row = min(m0 + wave + WR * WC * j, a.m - 1);
+      res_v[j] = *reinterpret_cast<const bf16x4*>(a.res + (int64_t)row * a.ldy + lane * 4);
+    }
+  }
 
   // The X panel: thread tid copies 16-byte groups tid, tid + kT, ... (row-major order,
   // so a quarter-wave reads 256 contiguous bytes of one row).
@@ -204,6 +225,52 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
       *reinterpret_cast<bf16x4*>(xs + r * kOutStride + c) = out;
     }
   __syncthreads();
+  if constexpr (ACT == kAddNorm) {
+    // One wavefront a row, 4 elements a lane, in the order and arithmetic of
+    // add_layernorm_kernel (selfplay.hip): x_out = bf16(res + y); two-pass fp32 mean and
+    // variance by lane sums and xor shuffles; ln = bf16((v - mean) rstd w + b).
+    static_assert(BN == 256, "a workgroup holds whole 256-wide rows");
+    constexpr int KE = BN / 64;
+    static_assert(BM % (WR * WC) == 0, "whole rows a wavefront");
+    const bf16x4 wv4 = *reinterpret_cast<const bf16x4*>(a.ln_w + lane * KE);
+    const bf16x4 bv4 = *reinterpret_cast<const bf16x4*>(a.ln_b + lane * KE);
+#pragma unroll
+    for (int j = 0; j < kNormRows; ++j) {
+      const int r = wave + WR * WC * j;
+      const int row = m0 + r;
+      if (row >= a.m) break;
+      const bf16x4 yv = *reinterpret_cast<const bf16x4*>(xs + r * kOutStride + lane * KE);
+      const int64_t at = (int64_t)row * a.ldy + lane * KE;
+      const bf16x4 xv = res_v[j];
+      float v[KE];
+      bf16x4 xo;
+#pragma unroll
+      for (int k = 0; k < KE; ++k) {
+        xo[k] = (__bf16)((float)xv[k] + (float)yv[k]);
+        v[k] = (float)xo[k];
+      }
+      *reinterpret_cast<bf16x4*>(a.y + at) = xo;
+      float sum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KE; ++k) sum += v[k];
+      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+      const float mean = sum / (float)BN;
+      float sq = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KE; ++k) {
+        const float c = v[k] - mean;
+        sq += c * c;
+      }
+      for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+      const float rstd = 1.0f / sqrtf(sq / (float)BN + a.eps);
+      bf16x4 o;
+#pragma unroll
+      for (int k = 0; k < KE; ++k)
+        o[k] = (__bf16)((v[k] - mean) * rstd * (float)wv4[k] + (float)bv4[k]);
+      *reinterpret_cast<bf16x4*>(a.ln + at) = o;
+    }
+    return;
+  }
   constexpr int kPieces = BM * BN / 8;  // 16-byte pieces of the tile
   const bool wide = (a.ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
 #pragma unroll
@@ -231,11 +298,23 @@ int launch_ks(const Args& a, int act, hipStream_t stream) {
   constexpr int BM = 16 * TM * WR;
   if constexpr (BM * KS * kK * 2 > 160 * 1024) {
     return -7;  // the X panel does not fit the LDS at this depth
+  } else if constexpr (16 * TN * WC != 256) {
+    if (act == kAddNorm) return -3;
+    const unsigned grid = (unsigned)(((a.m + BM - 1) / BM) * a.col_blocks);
+    if (act == CUGO_LINEAR_GELU)
+      linear_kernel<TM, TN, WR, WC, D, KS, CUGO_LINEAR_GELU>
+          <<<grid, 64 * WR * WC, 0, stream>>>(a);
+    else
+      linear_kernel<TM, TN, WR, WC, D, KS, CUGO_LINEAR_NONE>
+          <<<grid, 64 * WR * WC, 0, stream>>>(a);
+    return (int)hipGetLastError();
   } else {
     const unsigned grid = (unsigned)(((a.m + BM - 1) / BM) * a.col_blocks);
     if (act == CUGO_LINEAR_GELU)
       linear_kernel<TM, TN, WR, WC, D, KS, CUGO_LINEAR_GELU>
           <<<grid, 64 * WR * WC, 0, stream>>>(a);
+    else if (act == kAddNorm)
+      linear_kernel<TM, TN, WR, WC, D, KS, kAddNorm><<<grid, 64 * WR * WC, 0, stream>>>(a);
     else
       linear_kernel<TM, TN, WR, WC, D, KS, CUGO_LINEAR_NONE>
           <<<grid, 64 * WR * WC, 0, stream>>>(a);
@@ -277,9 +356,16 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
   // Buffer offsets are 32-bit byte offsets.
   if (m * ldx >= (int64_t(1) << 30) || (n + 15) * k >= (int64_t(1) << 30)) return -5;
   if (m == 0) return 0;
-  const Args a{static_cast<const __bf16*>(x), static_cast<const __bf16*>(w_packed),
-               static_cast<const __bf16*>(bias), static_cast<__bf16*>(y),
-               (int)m, (int)n, (int)ldx, (int)ldy, 0, (int)((n + 15) / 16)};
+  Args a{};
+  a.x = static_cast<const __bf16*>(x);
+  a.w = static_cast<const __bf16*>(w_packed);
+  a.bias = static_cast<const __bf16*>(bias);
+  a.y = static_cast<__bf16*>(y);
+  a.m = (int)m;
+  a.n = (int)n;
+  a.ldx = (int)ldx;
+  a.ldy = (int)ldy;
+  a.wtiles = (int)((n + 15) / 16);
   if (tile == 0) {  // by the decoder step's shapes: 64-row tiles once 32-row ones pass
     const int64_t blocks32 = ((m + 31) / 32) * ((n + 127) / 128);  // ~4 a CU
     tile = blocks32 > 1024 ? 2 : 1;
@@ -290,6 +376,46 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
     case 3: return launch<2, 4, 2, 2, 2>(a, (int)k, act, stream);  // 64 x 128
     case 4: return launch<4, 2, 2, 4, 2>(a, (int)k, act, stream);  // 128 x 128, 8 wavefronts
     case 5: return launch<2, 2, 2, 2, 3>(a, (int)k, act, stream);  // 64 x 64
+    default: return -6;
+  }
+}
+
+int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
+                              const void* bias, int64_t m, int64_t n, int64_t k, const void* res,
+                              const void* ln_weight, const void* ln_bias, float eps,
+                              void* x_out, void* ln, int tile, hipStream_t stream) {
+  if (m < 0 || (m > 0 && (!x || !w_packed || !res || !ln_weight || !ln_bias || !x_out || !ln)))
+    return -1;
+  const bool k_ok = k == 64 || k == 128 || k == 256 || k == 512 || k == 1024;
+  if (!k_ok || n != 256 || ldx < k || ldx % 8 != 0) return -3;
+  const uintptr_t p16 = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed);
+  const uintptr_t p8 = reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(res) |
+                       reinterpret_cast<uintptr_t>(ln_weight) |
+                       reinterpret_cast<uintptr_t>(ln_bias) | reinterpret_cast<uintptr_t>(x_out) |
+                       reinterpret_cast<uintptr_t>(ln);
+  if (p16 % 16 != 0 || p8 % 8 != 0) return -4;
+  if (m * ldx >= (int64_t(1) << 30) || (n + 15) * k >= (int64_t(1) << 30)) return -5;
+  if (m == 0) return 0;
+  Args a{};
+  a.x = static_cast<const __bf16*>(x);
+  a.w = static_cast<const __bf16*>(w_packed);
+  a.bias = static_cast<const __bf16*>(bias);
+  a.y = static_cast<__bf16*>(x_out);
+  a.m = (int)m;
+  a.n = (int)n;
+  a.ldx = (int)ldx;
+  a.ldy = (int)n;
+  a.wtiles = (int)((n + 15) / 16);
+  a.res = static_cast<const __bf16*>(res);
+  a.ln_w = static_cast<const __bf16*>(ln_weight);
+  a.ln_b = static_cast<const __bf16*>(ln_bias);
+  a.ln = static_cast<__bf16*>(ln);
+  a.eps = eps;
+  switch (tile) {
+    case 1: return launch<2, 4, 1, 4, 2>(a, (int)k, kAddNorm, stream);  // 32 x 256, 4 waves
+    case 0:  // measured fastest at 4,096 and 8,192 rows, k = 256 and 1,024
+    case 2: return launch<2, 2, 1, 8, 3>(a, (int)k, kAddNorm, stream);  // 32 x 256, 8 waves
+    case 3: return launch<1, 4, 1, 4, 2>(a, (int)k, kAddNorm, stream);  // 16 x 256, 4 waves
     default: return -6;
   }
 }

@@ -868,6 +868,50 @@ torch::Tensor linear(torch::Tensor x, torch::Tensor w_packed, int64_t n,
   return y;
 }
 
+// linear_add_layernorm(x [m, k], w_packed, bias, res [m, 256], ln_weight, ln_bias, eps)
+// -> (x_out, ln): linear then add_layernorm(res, y, ...) in one launch (the out_proj /
+// linear2 of a pre-norm layer with the residual add and the next norm,
+// python/cugo_seq50.py:316-322); all bf16.
+std::vector<torch::Tensor> linear_add_layernorm(torch::Tensor x, torch::Tensor w_packed,
+                                                c10::optional<torch::Tensor> bias,
+                                                torch::Tensor res, torch::Tensor ln_weight,
+                                                torch::Tensor ln_bias, double eps,
+                                                int64_t tile) {
+  TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16 && x.stride(1) == 1,
+              "x must be a CUDA bfloat16 [m, k] tensor with unit stride along k");
+  const int64_t m = x.size(0), k = x.size(1), n = 256;
+  TORCH_CHECK(res.is_contiguous() && res.dim() == 2 && res.size(0) == m && res.size(1) == n &&
+                  res.scalar_type() == at::kBFloat16,
+              "res must be a contiguous bfloat16 [m, 256] tensor");
+  TORCH_CHECK(w_packed.scalar_type() == at::kBFloat16 && w_packed.is_contiguous() &&
+                  w_packed.numel() == n * k,
+              "w_packed must be the packed bfloat16 [256, k] weight");
+  TORCH_CHECK(ln_weight.scalar_type() == at::kBFloat16 && ln_bias.scalar_type() == at::kBFloat16 &&
+                  ln_weight.numel() == n && ln_bias.numel() == n && ln_weight.is_contiguous() &&
+                  ln_bias.is_contiguous(),
+              "ln_weight and ln_bias must be contiguous bfloat16 [256] tensors");
+  check_same_device(x, w_packed, "x", "w_packed");
+  check_same_device(x, res, "x", "res");
+  check_same_device(x, ln_weight, "x", "ln_weight");
+  check_same_device(x, ln_bias, "x", "ln_bias");
+  if (bias.has_value()) {
+    TORCH_CHECK(bias->scalar_type() == at::kBFloat16 && bias->is_contiguous() && bias->numel() == n,
+                "bias must be a contiguous bfloat16 [256] tensor");
+    check_same_device(x, *bias, "x", "bias");
+  }
+  const DeviceGuard guard(x.device());
+  auto x_out = torch::empty_like(res);
+  auto ln = torch::empty_like(res);
+  const int64_t ldx = m > 1 ? x.stride(0) : k;
+  check_call(cugo_linear_add_layernorm(x.data_ptr(), ldx, w_packed.data_ptr(),
+                                       bias.has_value() ? bias->data_ptr() : nullptr, m, n, k,
+                                       res.data_ptr(), ln_weight.data_ptr(), ln_bias.data_ptr(),
+                                       static_cast<float>(eps), x_out.data_ptr(), ln.data_ptr(),
+                                       static_cast<int>(tile), stream()),
+             "linear_add_layernorm");
+  return {x_out, ln};
+}
+
 // masked_argmax(logits [n, A] f32/bf16, legal bool [n, A]) -> int64 [n]: the greedy
 // action of python/cugo_eval50.py:125-127 (argmax of logits.float() masked with -1e30).
 torch::Tensor masked_argmax(torch::Tensor logits, torch::Tensor legal) {
@@ -1297,6 +1341,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("linear", &linear, "bf16 x weight^T + bias, optionally followed by GELU, in one launch",
         pybind11::arg("x"), pybind11::arg("w_packed"), pybind11::arg("n"),
         pybind11::arg("bias") = pybind11::none(), pybind11::arg("gelu") = false,
+        pybind11::arg("tile") = 0);
+  m.def("linear_add_layernorm", &linear_add_layernorm,
+        "linear, then the residual add and LayerNorm of add_layernorm, in one launch",
+        pybind11::arg("x"), pybind11::arg("w_packed"), pybind11::arg("bias"), pybind11::arg("res"),
+        pybind11::arg("ln_weight"), pybind11::arg("ln_bias"), pybind11::arg("eps"),
         pybind11::arg("tile") = 0);
   pybind11::class_<SelfPlayState>(m, "SelfPlayState",
                                    "A self-play wave's tensors and its step bookkeeping")

@@ -7,9 +7,9 @@ like it: `model.encoder.layers` of pre-norm `nn.TransformerEncoderLayer`s
 -> linear2) and a cache with `k`, `v` ([layers, rows, heads, slots, dh]), `length`,
 `heads`, `slots`, `row_ids`.  The per-layer `index_put_` of the new key/value and the
 decode attention run as one HIP launch (`decode_attention_append`, reading q, k and v in
-place from the packed in-projection), each residual add with the pre-norm that follows
-it as another (`add_layernorm`), and each bf16 linear layer as one (`linear`), linear1
-with the GELU after it.
+place from the packed in-projection), each bf16 linear layer as one (`linear`, linear1
+with the GELU after it), and out_proj / linear2 with the residual add and the pre-norm
+that follows them as one (`linear_add_layernorm`).
 
 `KVCache` mirrors the reference cache (python/cugo_seq50.py:325-339) with the slot count
 as a parameter (the reference fixes it at MAX_EVENTS + 2 = 50).
@@ -124,6 +124,23 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
     return F.gelu(y) if gelu else y
 
 
+def linear_add_norm(u: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                    x: torch.Tensor, norm: nn.Module):
+    """add_norm(x, F.linear(u, weight, bias), norm): one HIP launch
+    (`linear_add_layernorm`) for bf16 rows 256 wide, `linear` and `add_norm` otherwise."""
+    if (_fits_linear(u, weight, bias) and weight.shape[0] == 256 and x.dim() == 2
+            and x.dtype == torch.bfloat16 and x.shape == (u.shape[0], 256)
+            and isinstance(norm, nn.LayerNorm) and norm.weight is not None
+            and norm.bias is not None and norm.weight.dtype == torch.bfloat16
+            and tuple(norm.normalized_shape) == (256,)):
+        out = _ext().linear_add_layernorm(u, packed_weight(weight),
+                                          None if bias is None else bias.detach(),
+                                          x.contiguous(), norm.weight.detach(),
+                                          norm.bias.detach(), norm.eps)
+        return out[0], out[1]
+    return add_norm(x, linear(u, weight, bias), norm)
+
+
 def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = None,
                 rows: torch.Tensor | None = None) -> torch.Tensor:
     """One token per cache row (x [n, d]); its key/value go to slot cache.length[row].
@@ -131,8 +148,9 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
     Each token attends every cached slot plus itself; `slots` bounds the slot index;
     `rows` names each token's cache row (default: every row in order).  Returns the
     final hidden state [n, d].  Same steps as python/cugo_seq50.py:291-322; each residual
-    add and the pre-norm after it run as one launch, q, k and v are read in place from
-    the packed in-projection, and linear1 + GELU is one launch."""
+    add and the pre-norm after it run in the launch of the linear layer before them, q, k
+    and v are read in place from the packed in-projection, and linear1 + GELU is one
+    launch."""
     n, d = x.shape
     heads = cache.heads
     dh = d // heads
@@ -148,15 +166,15 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
         a = decode_attention_append(q.reshape(n, heads, dh), k.reshape(n, heads, dh),
                                     v.reshape(n, heads, dh), cache.k[i], cache.v[i], pos,
                                     row_ids)
-        x, h = add_norm(x, linear(a.reshape(n, d), attn.out_proj.weight, attn.out_proj.bias),
-                         layer.norm2)
+        x, h = linear_add_norm(a.reshape(n, d), attn.out_proj.weight, attn.out_proj.bias, x,
+                               layer.norm2)
         if is_exact_gelu(layer.activation):
             u = linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True)
         else:
             u = layer.activation(linear(h, layer.linear1.weight, layer.linear1.bias))
-        m = linear(u, layer.linear2.weight, layer.linear2.bias)
         if i + 1 < len(layers):
-            x, h = add_norm(x, m, layers[i + 1].norm1)
+            x, h = linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x,
+                                   layers[i + 1].norm1)
         else:
-            x = x + m
+            x = x + linear(u, layer.linear2.weight, layer.linear2.bias)
     return x

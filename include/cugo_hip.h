@@ -356,6 +356,17 @@ int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weig
 int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const void* bias,
                 int64_t m, int64_t n, int64_t k, void* y, int64_t ldy, int tile,
                 hipStream_t stream);
+/* cugo_linear_add_layernorm: cugo_linear (no activation) followed by cugo_add_layernorm of
+ * its output onto res, in one launch: the out_proj / linear2 of a pre-norm encoder layer
+ * with the residual add and the next LayerNorm (cugo_seq50.py:316-322).  y = bf16(x w^T +
+ * bias); x_out = bf16(res + y); ln = LayerNorm(x_out) * ln_weight + ln_bias, with the
+ * statistics and roundings of cugo_add_layernorm.  n must be 256; res, x_out, ln
+ * contiguous [m, 256] (x_out may alias res); other requirements as cugo_linear.  tile: 1
+ * for 32-row tiles on 4 wavefronts, 0 or 2 on 8, 3 for 16-row tiles on 4. */
+int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
+                              const void* bias, int64_t m, int64_t n, int64_t k, const void* res,
+                              const void* ln_weight, const void* ln_bias, float eps,
+                              void* x_out, void* ln, int tile, hipStream_t stream);
 /* cugo_gumbel_sample: the sampling of WaveCollector._step (cugo_seq_selfplay50.py:125-130)
  * given the uniforms torch.rand_like drew: masked = legal ? logits : -1e30;
  * actions[i] = argmax_a(masked - log(-log(clamp(u, 1e-20, 1)))) (first index on ties);

@@ -230,6 +230,43 @@ def test_linear_matches_float64(ext, m, n, k):
             ext.linear(x, wp, n, b, tile=6)
 
 
+@pytest.mark.parametrize("m,k", [(4096, 256), (8192, 1024), (1001, 256), (1, 64)])
+def test_linear_add_layernorm_equals_its_two_launches(ext, m, k):
+    """linear_add_layernorm == add_layernorm(res, linear(x)) bit for bit (x_out and ln),
+    with and without bias, on every tile; within torch's bf16 LayerNorm tolerance of the
+    torch ops; the module-level wrapper; only 256-wide rows."""
+    from cugo_amd.seq_decode import linear_add_norm
+
+    announce(f"linear_add_layernorm m={m} k={k}")
+    g = torch.Generator(device="cpu").manual_seed(m * 7 + k)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(256, k, generator=g) * k ** -0.5).to(torch.bfloat16).to(DEV)
+    b = (torch.randn(256, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    res = (torch.randn(m, 256, generator=g) * 2.0).to(torch.bfloat16).to(DEV)
+    norm = torch.nn.LayerNorm(256).to(DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_((torch.randn(256, generator=g) * 0.3 + 1.0).to(torch.bfloat16))
+        norm.bias.copy_((torch.randn(256, generator=g) * 0.1).to(torch.bfloat16))
+        wp = ext.mlp_pack_weight(w, 256, k)
+        for bias in (b, None):
+            xo, ln = ext.linear_add_layernorm(x, wp, bias, res, norm.weight, norm.bias, norm.eps)
+            y = ext.linear(x, wp, 256, bias)
+            want_x, want_ln = ext.add_layernorm(res, y, norm.weight, norm.bias, norm.eps)
+            assert torch.equal(xo, want_x) and torch.equal(ln, want_ln)
+        xo, ln = ext.linear_add_layernorm(x, wp, b, res, norm.weight, norm.bias, norm.eps)
+        for tile in (1, 2, 3):
+            got = ext.linear_add_layernorm(x, wp, b, res, norm.weight, norm.bias, norm.eps,
+                                           tile=tile)
+            assert torch.equal(got[0], xo) and torch.equal(got[1], ln), tile
+        assert rel_err(ln, norm(res + torch.nn.functional.linear(x, w, b))) <= 1e-2
+        got = linear_add_norm(x, w, b, res, norm)
+        assert torch.equal(got[0], xo) and torch.equal(got[1], ln)
+        if m == 1:
+            with pytest.raises(RuntimeError):  # only 256-wide rows
+                ext.linear_add_layernorm(x, ext.mlp_pack_weight(w[:128].contiguous(), 128, k),
+                                         None, res, norm.weight, norm.bias, norm.eps)
+
+
 def test_gumbel_sample_matches_reference(ext):
     announce("gumbel_sample")
     g = torch.Generator(device=DEV).manual_seed(3)
