@@ -177,20 +177,26 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
   // The K loop is unrolled whole (KS is a template argument): with a run-time trip count
   // the compiler cannot count the loads in flight across the loop's branches and waits
   // for all of them before every step's MFMAs.
+  // X fragments are double-buffered: step s + 1's are read from LDS before step s's MFMAs
+  // issue, so the MFMAs do not wait on the LDS every step.
   const int x_lane = xs_at<BM>(r0 + l16, 8 * q4);
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    if (s + D < KS) load_w(s + D, (s + D) % R);
-    bf16x8 xa[TM];
+  auto load_x = [&](bf16x8 (&xa)[TM], int s) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
       xa[i] = *reinterpret_cast<const bf16x8*>(xs + x_lane + (s * BM + 16 * i) * 32);
+  };
+  bf16x8 xa[2][TM];
+  load_x(xa[0], 0);
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (s + D < KS) load_w(s + D, (s + D) % R);
+    if (s + 1 < KS) load_x(xa[(s + 1) & 1], s + 1);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int t = 0; t < TN; ++t)
-        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[s % R][t], xa[i], acc[i][t],
-                                                            0, 0, 0);
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb[s % R][t], xa[s & 1][i],
+                                                            acc[i][t], 0, 0, 0);
     // Keep the ring: without a fence the scheduler hoists later K steps' loads.
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -376,6 +382,8 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
     case 3: return launch<2, 4, 2, 2, 2>(a, (int)k, act, stream);  // 64 x 128
     case 4: return launch<4, 2, 2, 4, 2>(a, (int)k, act, stream);  // 128 x 128, 8 wavefronts
     case 5: return launch<2, 2, 2, 2, 3>(a, (int)k, act, stream);  // 64 x 64
+    case 6: return launch<4, 4, 2, 2, 2>(a, (int)k, act, stream);  // 128 x 128, 4 waves
+    case 7: return launch<2, 4, 1, 4, 2>(a, (int)k, act, stream);  // 32 x 256
     default: return -6;
   }
 }

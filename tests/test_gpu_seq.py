@@ -200,7 +200,7 @@ def test_linear_matches_float64(ext, m, n, k):
     assert got.shape == (m, n) and got.dtype == torch.bfloat16
     check(got, b)
     assert torch.equal(ext.linear(x, wp, n, b, gelu=True), torch.nn.functional.gelu(got))
-    for tile, rows in ((1, 32), (2, 64), (3, 64), (4, 128), (5, 64)):
+    for tile, rows in ((1, 32), (2, 64), (3, 64), (4, 128), (5, 64), (6, 128), (7, 32)):
         if rows * k * 2 <= 160 * 1024:  # the X panel fits the LDS
             assert torch.equal(ext.linear(x, wp, n, b, tile=tile), got), tile
         else:
@@ -227,7 +227,7 @@ def test_linear_matches_float64(ext, m, n, k):
         with pytest.raises(RuntimeError):  # packed size does not match n
             ext.linear(x, wp, n + 16, None)
         with pytest.raises(RuntimeError):
-            ext.linear(x, wp, n, b, tile=6)
+            ext.linear(x, wp, n, b, tile=8)
 
 
 @pytest.mark.parametrize("m,k", [(4096, 256), (8192, 1024), (1001, 256), (1, 64)])
