@@ -60,7 +60,8 @@ struct Args {
   int m, n, ldx, ldy;
   int col_blocks;  // workgroups along n
   int wtiles;      // 16-row tiles of the packed W
-  // kAddNorm only (rows of n = BN elements, row stride ldy)
+  // the residual (row stride ldy), added to the output after its rounding (NULL: none);
+  // kAddNorm's residual, with rows of n = BN elements
   const __bf16* res;
   const __bf16* ln_w;
   const __bf16* ln_b;
@@ -71,6 +72,15 @@ struct Args {
 // Epilogues beyond CUGO_LINEAR_NONE / CUGO_LINEAR_GELU: the residual add and the
 // LayerNorm after it (a pre-norm layer's out_proj or linear2 followed by the next norm).
 constexpr int kAddNorm = 2;
+
+// Eight bf16 sums, each rounded from fp32 as torch adds bf16 tensors.
+__device__ inline uint4 add_bf16(uint4 a, uint4 b) {
+  const bf16x8 x = __builtin_bit_cast(bf16x8, a), y = __builtin_bit_cast(bf16x8, b);
+  bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (__bf16)((float)x[i] + (float)y[i]);
+  return __builtin_bit_cast(uint4, z);
+}
 
 __device__ inline float gelu(float v) {
   return v * 0.5f * (1.0f + erff(v * 0.70710678118654752440f));
@@ -286,11 +296,19 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
       const int r = p / (BN / 8), c = (p % (BN / 8)) * 8;
       const int row = m0 + r, col = nb0 + c;
       if (row < a.m && col < a.n) {
-        const uint4 v = *reinterpret_cast<const uint4*>(xs + r * kOutStride + c);
-        __bf16* dst = a.y + (int64_t)row * a.ldy + col;
+        uint4 v = *reinterpret_cast<const uint4*>(xs + r * kOutStride + c);
+        const int64_t at = (int64_t)row * a.ldy + col;
+        __bf16* dst = a.y + at;
         if (wide && col + 8 <= a.n) {
+          if (a.res != nullptr) v = add_bf16(v, *reinterpret_cast<const uint4*>(a.res + at));
           *reinterpret_cast<uint4*>(dst) = v;
         } else {
+          if (a.res != nullptr) {
+            const uint2 lo = *reinterpret_cast<const uint2*>(a.res + at);
+            const uint2 hi = col + 8 <= a.n ? *reinterpret_cast<const uint2*>(a.res + at + 4)
+                                            : uint2{0u, 0u};
+            v = add_bf16(v, uint4{lo.x, lo.y, hi.x, hi.y});
+          }
           *reinterpret_cast<uint2*>(dst) = uint2{v.x, v.y};
           if (col + 8 <= a.n) *reinterpret_cast<uint2*>(dst + 4) = uint2{v.z, v.w};
         }
@@ -350,14 +368,15 @@ using namespace cugo_amd::linear;
 extern "C" {
 
 int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const void* bias,
-                int64_t m, int64_t n, int64_t k, void* y, int64_t ldy, int tile,
-                hipStream_t stream) {
+                const void* residual, int64_t m, int64_t n, int64_t k, void* y, int64_t ldy,
+                int tile, hipStream_t stream) {
   if (m < 0 || n < 1 || k < 1 || (m > 0 && (!x || !w_packed || !y))) return -1;
   if (act != CUGO_LINEAR_NONE && act != CUGO_LINEAR_GELU) return -2;
   const bool k_ok = k == 64 || k == 128 || k == 256 || k == 512 || k == 1024;
   if (!k_ok || n % 4 != 0 || ldx < k || ldx % 8 != 0 || ldy < n || ldy % 4 != 0) return -3;
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed)) % 16 != 0 ||
-      (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(bias)) % 8 != 0)
+      (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(bias) |
+       reinterpret_cast<uintptr_t>(residual)) % 8 != 0)
     return -4;
   // Buffer offsets are 32-bit byte offsets.
   if (m * ldx >= (int64_t(1) << 30) || (n + 15) * k >= (int64_t(1) << 30)) return -5;
@@ -366,6 +385,7 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
   a.x = static_cast<const __bf16*>(x);
   a.w = static_cast<const __bf16*>(w_packed);
   a.bias = static_cast<const __bf16*>(bias);
+  a.res = static_cast<const __bf16*>(residual);
   a.y = static_cast<__bf16*>(y);
   a.m = (int)m;
   a.n = (int)n;

@@ -839,13 +839,15 @@ std::vector<torch::Tensor> add_layernorm(torch::Tensor x, c10::optional<torch::T
   return {x_out, ln};
 }
 
-// linear(x [m, k] bf16, w_packed, n, bias [n] bf16 or None, gelu, tile) -> y [m, n] bf16:
-// nn.Linear (and with gelu=True the nn.GELU() after it) of the decoder step
+// linear(x [m, k] bf16, w_packed, n, bias [n] bf16 or None, gelu, tile, residual [m, n] or
+// None) -> y [m, n] bf16: nn.Linear (and with gelu=True the nn.GELU() after it; with a
+// residual, residual + that) of the decoder step
 // (python/cugo_seq50.py:291-322) in one launch.  w_packed is the layer's weight [n, k] as
 // mlp_pack_weight(weight, roundup(n, 16), k) lays it out.  x may be a row-strided view
 // (unit stride along k).
 torch::Tensor linear(torch::Tensor x, torch::Tensor w_packed, int64_t n,
-                     c10::optional<torch::Tensor> bias, bool gelu, int64_t tile) {
+                     c10::optional<torch::Tensor> bias, bool gelu, int64_t tile,
+                     c10::optional<torch::Tensor> residual) {
   TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16 && x.stride(1) == 1,
               "x must be a CUDA bfloat16 [m, k] tensor with unit stride along k");
   const int64_t m = x.size(0), k = x.size(1);
@@ -858,12 +860,19 @@ torch::Tensor linear(torch::Tensor x, torch::Tensor w_packed, int64_t n,
                 "bias must be a contiguous bfloat16 [n] tensor");
     check_same_device(x, *bias, "x", "bias");
   }
+  if (residual.has_value()) {
+    TORCH_CHECK(residual->scalar_type() == at::kBFloat16 && residual->is_contiguous() &&
+                    residual->dim() == 2 && residual->size(0) == m && residual->size(1) == n,
+                "residual must be a contiguous bfloat16 [m, n] tensor");
+    check_same_device(x, *residual, "x", "residual");
+  }
   const DeviceGuard guard(x.device());
   auto y = torch::empty({m, n}, x.options());
   const int64_t ldx = m > 1 ? x.stride(0) : k;
   check_call(cugo_linear(gelu ? CUGO_LINEAR_GELU : CUGO_LINEAR_NONE, x.data_ptr(), ldx,
-                         w_packed.data_ptr(), bias.has_value() ? bias->data_ptr() : nullptr, m, n,
-                         k, y.data_ptr(), n, static_cast<int>(tile), stream()),
+                         w_packed.data_ptr(), bias.has_value() ? bias->data_ptr() : nullptr,
+                         residual.has_value() ? residual->data_ptr() : nullptr, m, n, k,
+                         y.data_ptr(), n, static_cast<int>(tile), stream()),
              "linear");
   return y;
 }
@@ -1341,7 +1350,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("linear", &linear, "bf16 x weight^T + bias, optionally followed by GELU, in one launch",
         pybind11::arg("x"), pybind11::arg("w_packed"), pybind11::arg("n"),
         pybind11::arg("bias") = pybind11::none(), pybind11::arg("gelu") = false,
-        pybind11::arg("tile") = 0);
+        pybind11::arg("tile") = 0, pybind11::arg("residual") = pybind11::none());
   m.def("linear_add_layernorm", &linear_add_layernorm,
         "linear, then the residual add and LayerNorm of add_layernorm, in one launch",
         pybind11::arg("x"), pybind11::arg("w_packed"), pybind11::arg("bias"), pybind11::arg("res"),

@@ -114,14 +114,19 @@ def prepare_linears(model: nn.Module) -> None:
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
-           gelu: bool = False) -> torch.Tensor:
-    """F.linear(x, weight, bias), then F.gelu when `gelu`: one HIP launch (`linear`) for
-    bf16 rows with K in {64, ..., 1,024} and N a multiple of 4, torch's ops otherwise."""
-    if _fits_linear(x, weight, bias):
+           gelu: bool = False, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear(x, weight, bias), then F.gelu when `gelu`, then residual + that when a
+    residual is given: one HIP launch (`linear`) for bf16 rows with K in {64, ..., 1,024}
+    and N a multiple of 4, torch's ops otherwise."""
+    if _fits_linear(x, weight, bias) and (
+            residual is None or (residual.dtype == torch.bfloat16 and residual.is_contiguous()
+                                 and residual.shape == (x.shape[0], weight.shape[0]))):
         return _ext().linear(x, packed_weight(weight), weight.shape[0],
-                             None if bias is None else bias.detach(), gelu)
+                             None if bias is None else bias.detach(), gelu,
+                             residual=residual)
     y = F.linear(x, weight, bias)
-    return F.gelu(y) if gelu else y
+    y = F.gelu(y) if gelu else y
+    return y if residual is None else residual + y
 
 
 def linear_add_norm(u: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
@@ -157,7 +162,8 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
     t = cache.slots if slots is None else min(slots, cache.slots)
     row_ids = cache.row_ids if rows is None else rows
     length = cache.length if rows is None else cache.length.index_select(0, row_ids)
-    pos = length.clamp_max(t - 1)
+    # The decode kernel takes positions past the last slot as the last slot itself.
+    pos = length if t == cache.slots else length.clamp_max(t - 1)
     layers = model.encoder.layers
     x, h = add_norm(x, None, layers[0].norm1)
     for i, layer in enumerate(layers):
@@ -176,5 +182,5 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
             x, h = linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x,
                                    layers[i + 1].norm1)
         else:
-            x = x + linear(u, layer.linear2.weight, layer.linear2.bias)
+            x = linear(u, layer.linear2.weight, layer.linear2.bias, residual=x)
     return x

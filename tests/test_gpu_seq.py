@@ -172,8 +172,9 @@ def test_linear_matches_float64(ext, m, n, k):
     bf16: every element within the bound of an fp32 sum of k products (k 2^-24 times the
     sum of their magnitudes) rounded to bf16 (one unit), 98 % bit-identical; its GELU
     form equals torch's F.gelu of its plain form bit for bit; every workgroup tile gives
-    identical bits (the same K order); a row-strided x, no bias, the packed-weight
-    cache (rebuilt in place when the weight changes), and the shape checks."""
+    identical bits (the same K order); with a residual, torch's bf16 add of the two; a
+    row-strided x, no bias, the packed-weight cache (rebuilt in place when the weight
+    changes), and the shape checks."""
     from cugo_amd.seq_decode import linear, packed_weight
 
     announce(f"linear m={m} n={n} k={k}")
@@ -207,11 +208,16 @@ def test_linear_matches_float64(ext, m, n, k):
             with pytest.raises(RuntimeError):
                 ext.linear(x, wp, n, b, tile=tile)
     check(ext.linear(x, wp, n, None), None)
+    r = torch.randn(m, n, generator=g).to(torch.bfloat16).to(DEV)  # residual, torch's bf16 add
+    assert torch.equal(ext.linear(x, wp, n, b, residual=r), r + got)
+    assert torch.equal(ext.linear(x, wp, n, b, gelu=True, residual=r),
+                       r + torch.nn.functional.gelu(got))
     wide = torch.zeros(m, k + 40, dtype=torch.bfloat16, device=DEV)
     wide[:, 8:8 + k] = x
     assert torch.equal(ext.linear(wide[:, 8:8 + k], wp, n, b), got)
     # the module-level wrapper packs the weight once and repacks it when it changes
     assert torch.equal(linear(x, w, b), got)
+    assert torch.equal(linear(x, w, b, residual=r), r + got)
     p0 = packed_weight(w)
     assert torch.equal(p0, wp) and packed_weight(w) is p0
     w.mul_(-1.0)
