@@ -683,12 +683,14 @@ torch::Tensor decode_attention(torch::Tensor q, torch::Tensor keys, torch::Tenso
   return out;
 }
 
-// decode_attention_append(q, k_new, v_new, keys, values, pos, rows=None): writes k_new and
-// v_new ([n, heads, dh], cast to the cache dtype) to slot pos of each query's row, in place,
-// then attends as decode_attention (python/cugo_seq50.py:313-320 in one launch).
+// decode_attention_append(q, k_new, v_new, keys, values, pos, rows=None, out=None): writes
+// k_new and v_new ([n, heads, dh], cast to the cache dtype) to slot pos of each query's row,
+// in place, then attends as decode_attention (python/cugo_seq50.py:313-320 in one launch),
+// into `out` when given.
 torch::Tensor decode_attention_append(torch::Tensor q, torch::Tensor k_new, torch::Tensor v_new,
                                       torch::Tensor keys, torch::Tensor values, torch::Tensor pos,
-                                      c10::optional<torch::Tensor> rows) {
+                                      c10::optional<torch::Tensor> rows,
+                                      c10::optional<torch::Tensor> out_opt) {
   check_decode(q, keys, values, pos, rows);
   TORCH_CHECK(k_new.sizes() == q.sizes() && v_new.sizes() == q.sizes(),
               "k_new and v_new must have q's shape [n, heads, dh]");
@@ -705,7 +707,16 @@ torch::Tensor decode_attention_append(torch::Tensor q, torch::Tensor k_new, torc
     k_new = k_new.contiguous();
     v_new = v_new.contiguous();
   }
-  auto out = torch::empty(q.sizes(), q.options());
+  torch::Tensor out;
+  if (out_opt.has_value()) {
+    out = *out_opt;
+    TORCH_CHECK(out.is_contiguous() && out.sizes() == q.sizes() &&
+                    out.scalar_type() == q.scalar_type(),
+                "out must be a contiguous tensor of q's shape and dtype");
+    check_same_device(q, out, "q", "out");
+  } else {
+    out = torch::empty(q.sizes(), q.options());
+  }
   const int64_t dh = q.size(2);
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(dh)));
   check_call(cugo_decode_attention_append(
@@ -753,10 +764,11 @@ int token_dtype(const torch::Tensor& w) {
 }
 
 // event_tokens(words [n, 9], seat [n], index [n], weight_t [414, d], bias, position,
-// token_type) -> [n, d]: SeqNet.event_token (python/cugo_seq50.py:276-282).
+// token_type, out=None) -> [n, d]: SeqNet.event_token (python/cugo_seq50.py:276-282),
+// written into `out` (contiguous [n, d]) when given.
 torch::Tensor event_tokens(torch::Tensor words, torch::Tensor seat, torch::Tensor index,
                            torch::Tensor weight_t, torch::Tensor bias, torch::Tensor position,
-                           torch::Tensor token_type) {
+                           torch::Tensor token_type, c10::optional<torch::Tensor> out_opt) {
   TORCH_CHECK(words.is_cuda() && words.is_contiguous() && words.dim() == 2 &&
                   words.size(1) == CUGO_EVENT_WORDS && words.scalar_type() == at::kLong,
               "words must be a contiguous CUDA int64 [n, EVENT_WORDS] tensor");
@@ -772,7 +784,7 @@ torch::Tensor event_tokens(torch::Tensor words, torch::Tensor seat, torch::Tenso
   check_same_device(words, index, "words", "index");
   check_token_weights(weight_t, bias, position, token_type, 8 * 50 + 12 + 2, words);
   const DeviceGuard guard(words.device());
-  auto out = torch::empty({n, weight_t.size(1)}, on(words, weight_t.scalar_type()));
+  auto out = out_or_new(out_opt, {n, weight_t.size(1)}, weight_t.scalar_type(), words, "out");
   check_call(cugo_event_tokens(token_dtype(weight_t), words.data_ptr<int64_t>(), word_rows,
                                seat.data_ptr<int64_t>(), index.data_ptr<int64_t>(), n,
                                weight_t.data_ptr(), bias.data_ptr(), position.data_ptr(),
@@ -1342,7 +1354,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("logits"), pybind11::arg("legal"), pybind11::arg("seed"),
         pybind11::arg("epoch"), pybind11::arg("offset"), pybind11::arg("actions") = pybind11::none(),
         pybind11::arg("logp") = pybind11::none(), pybind11::arg("uniforms_out") = pybind11::none());
-  m.def("event_tokens", &event_tokens, "SeqNet.event_token: event_in(encode_events) + position + type");
+  m.def("event_tokens", &event_tokens, "SeqNet.event_token: event_in(encode_events) + position + type",
+        pybind11::arg("words"), pybind11::arg("seat"), pybind11::arg("index"),
+        pybind11::arg("weight_t"), pybind11::arg("bias"), pybind11::arg("position"),
+        pybind11::arg("token_type"), pybind11::arg("out") = pybind11::none());
   m.def("start_tokens", &start_tokens, "SeqNet.start_token: start_in(encode_start) + position + type");
   m.def("add_layernorm", &add_layernorm, "x + y and LayerNorm(x + y) in one launch",
         pybind11::arg("x"), pybind11::arg("y"), pybind11::arg("weight"), pybind11::arg("bias"),
@@ -1393,7 +1408,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Write the new key/value at slot pos, then single-query attention",
         pybind11::arg("q"), pybind11::arg("k_new"), pybind11::arg("v_new"),
         pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
-        pybind11::arg("rows") = pybind11::none());
+        pybind11::arg("rows") = pybind11::none(), pybind11::arg("out") = pybind11::none());
   m.attr("FEATURE_COUNT") = pybind11::int_(CUGO_FEATURE_COUNT);
   m.attr("ACTION_COUNT") = pybind11::int_(CUGO_ACTION_COUNT);
   m.attr("PRIMARY_ACTION_COUNT") = pybind11::int_(CUGO_PRIMARY_ACTION_COUNT);

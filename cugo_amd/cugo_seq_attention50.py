@@ -47,8 +47,10 @@ def decode_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, 
 
 def decode_attention_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                             keys: torch.Tensor, values: torch.Tensor, pos: torch.Tensor,
-                            rows: torch.Tensor | None = None) -> torch.Tensor:
+                            rows: torch.Tensor | None = None,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
     """Writes k_new/v_new [n, heads, dh] to slot pos[i] of row rows[i] of keys/values (in
-    place, cast to the cache dtype), then returns decode_attention over slots 0..pos."""
+    place, cast to the cache dtype), then returns decode_attention over slots 0..pos
+    (written into `out`, contiguous [n, heads, dh], when given)."""
     _check_device(q, k_new, v_new, keys, values, pos)
-    return _ext().decode_attention_append(q, k_new, v_new, keys, values, pos, rows)
+    return _ext().decode_attention_append(q, k_new, v_new, keys, values, pos, rows, out)

@@ -147,11 +147,12 @@ def linear_add_norm(u: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | 
 
 
 def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = None,
-                rows: torch.Tensor | None = None) -> torch.Tensor:
+                rows: torch.Tensor | None = None, pos: torch.Tensor | None = None) -> torch.Tensor:
     """One token per cache row (x [n, d]); its key/value go to slot cache.length[row].
 
     Each token attends every cached slot plus itself; `slots` bounds the slot index;
-    `rows` names each token's cache row (default: every row in order).  Returns the
+    `rows` names each token's cache row (default: every row in order); `pos`, if given,
+    the slot of each token in place of its row's length.  Returns the
     final hidden state [n, d].  Same steps as python/cugo_seq50.py:291-322; each residual
     add and the pre-norm after it run in the launch of the linear layer before them, q, k
     and v are read in place from the packed in-projection, and linear1 + GELU is one
@@ -161,9 +162,10 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
     dh = d // heads
     t = cache.slots if slots is None else min(slots, cache.slots)
     row_ids = cache.row_ids if rows is None else rows
-    length = cache.length if rows is None else cache.length.index_select(0, row_ids)
+    if pos is None:
+        pos = cache.length if rows is None else cache.length.index_select(0, row_ids)
     # The decode kernel takes positions past the last slot as the last slot itself.
-    pos = length if t == cache.slots else length.clamp_max(t - 1)
+    pos = pos if t == cache.slots else pos.clamp_max(t - 1)
     layers = model.encoder.layers
     x, h = add_norm(x, None, layers[0].norm1)
     for i, layer in enumerate(layers):
@@ -173,6 +175,44 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
                                     v.reshape(n, heads, dh), cache.k[i], cache.v[i], pos,
                                     row_ids)
         x, h = linear_add_norm(a.reshape(n, d), attn.out_proj.weight, attn.out_proj.bias, x,
+                               layer.norm2)
+        if is_exact_gelu(layer.activation):
+            u = linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True)
+        else:
+            u = layer.activation(linear(h, layer.linear1.weight, layer.linear1.bias))
+        if i + 1 < len(layers):
+            x, h = linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x,
+                                   layers[i + 1].norm1)
+        else:
+            x = linear(u, layer.linear2.weight, layer.linear2.bias, residual=x)
+    return x
+
+
+def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a: torch.Tensor,
+                     pos_b: torch.Tensor, rows_b: torch.Tensor) -> torch.Tensor:
+    """cached_step for two groups of tokens at once: rows [0, split) of x (group a, one
+    token for each of the cache rows 0 .. split - 1, written at slot pos_a[r]) and rows
+    [split, n) (group b, one token for cache row rows_b[j], at slot pos_b[j]).  At every
+    layer group a's keys and values are appended before group b attends, so b sees what
+    it would see had a been through every layer first (cached_step(a), then
+    cached_step(b)); a reads no slot of b (a token reads the slots below its own, and b
+    writes at or above a's).  The linear layers run once over both groups.  Positions past
+    the last slot are taken as the last slot.  Returns the final hidden states [n, d]."""
+    n, d = x.shape
+    heads = cache.heads
+    dh = d // heads
+    layers = model.encoder.layers
+    x, h = add_norm(x, None, layers[0].norm1)
+    att = torch.empty((n, heads, dh), dtype=x.dtype, device=x.device)
+    for i, layer in enumerate(layers):
+        sa = layer.self_attn
+        q, k, v = (t.reshape(n, heads, dh)
+                   for t in linear(h, sa.in_proj_weight, sa.in_proj_bias).chunk(3, -1))
+        decode_attention_append(q[:split], k[:split], v[:split], cache.k[i], cache.v[i], pos_a,
+                                None, out=att[:split])
+        decode_attention_append(q[split:], k[split:], v[split:], cache.k[i], cache.v[i], pos_b,
+                                rows_b, out=att[split:])
+        x, h = linear_add_norm(att.view(n, d), sa.out_proj.weight, sa.out_proj.bias, x,
                                layer.norm2)
         if is_exact_gelu(layer.activation):
             u = linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True)

@@ -25,8 +25,8 @@ import torch
 from torch import nn
 
 from .cugo_torch50_ext import load_extension
-from .seq_decode import (KVCache, add_norm, cached_step, is_exact_gelu, linear,
-                         packed_weight, prepare_linears)
+from .seq_decode import (KVCache, add_norm, cached_step, cached_step_pair, is_exact_gelu,
+                         linear, packed_weight, prepare_linears)
 
 FEATURES = 720
 ACTIONS = 179
@@ -124,14 +124,15 @@ class SeqPolicy(nn.Module):
                                        self._weight_t("start_in"), self.start_in.bias.detach(),
                                        self.position.detach(), self.token_type.detach())
 
-    def event_token(self, words: torch.Tensor, seat: torch.Tensor,
-                    index: torch.Tensor) -> torch.Tensor:
+    def event_token(self, words: torch.Tensor, seat: torch.Tensor, index: torch.Tensor,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
         """cugo_seq50.py:276-282: event_in(encode_events) + position[1 + min(index, 47)]
         + token_type[1].  Row r reads words[r % len(words)] and index[r % len(words)], so one
-        copy of the events serves every seat that observes them."""
+        copy of the events serves every seat that observes them.  Written into `out` when
+        given."""
         return self.ext().event_tokens(words.contiguous(), seat.contiguous(), index.contiguous(),
                                        self._weight_t("event_in"), self.event_in.bias.detach(),
-                                       self.position.detach(), self.token_type.detach())
+                                       self.position.detach(), self.token_type.detach(), out)
 
     def query_token(self, features: torch.Tensor, legal: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:166-180: query_in(features ++ legal) + token_type[2]; events mode
@@ -145,9 +146,11 @@ class SeqPolicy(nn.Module):
         """Feature columns a rollout keeps for this mode (cugo_seq50.py:342-344)."""
         return None if self.mode == "hybrid" else CONTEXT_INDEX
 
-    def query_from_input(self, q_in: torch.Tensor) -> torch.Tensor:
-        """query_token on the already concatenated input [n, 720 + 179]."""
-        return self.query_in(q_in) + self.token_type[2]
+    def query_from_input(self, q_in: torch.Tensor,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+        """query_token on the already concatenated input [n, 720 + 179] (into `out` when
+        given)."""
+        return torch.add(self.query_in(q_in), self.token_type[2], out=out)
 
     def readout(self, h: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:187-189 and :288-289: head(norm(h)), the norm as one HIP launch
@@ -239,6 +242,13 @@ class SelfPlayWave:
         self.graph: torch.cuda.CUDAGraph | None = None  # one step, for `pool` below
         self.graph_pool: bool | None = None
         self._done_flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
+        # The learner's event tokens of a step wait in rows [0, 2 w) of `pair` and go
+        # through the layers with the next step's queries (rows [2 w, 3 w)), in one pass
+        # (cached_step_pair); event_pos holds the slots they go to.  flush() runs them
+        # alone.
+        d = actor.position.shape[1]
+        self.pair = torch.zeros((3 * wave, d), dtype=actor.event_in.weight.dtype, device=dev)
+        self.event_pos = torch.zeros(2 * wave, dtype=torch.int64, device=dev)
 
     # the reference's tensor names, for callers of the wave's outcome
     def __getattr__(self, name: str):
@@ -281,22 +291,31 @@ class SelfPlayWave:
         if pool and self.p:
             self._open(self.opponent, self.opp_cache, t.start[:self.p],
                        1 - t.learner_seat[:self.p])
+        # no events wait: the first step's event rows write the query's own scratch slot
+        self.pair[:2 * self.w].zero_()
+        self.event_pos.copy_(self.cache.length)
 
     @torch.no_grad()
     def step(self, pool: bool = False) -> None:
         """One decision of every game (the reference's _step,
         cugo_seq_selfplay50.py:108-163); the bookkeeping around the policy is two HIP
         launches (SelfPlayState.prepare before the query, .advance after the event
-        tokens)."""
-        ext, actor, t = self.ext, self.actor, self.t
+        tokens).  The learner's event tokens of this step enter its cache at the next
+        step (with that step's queries) or at flush(); until then the cache holds the
+        step's query in their slots, which no later token reads."""
+        ext, actor, t, w = self.ext, self.actor, self.t, self.w
         pool = pool and self.p > 0
         native = self.native[pool]
         features, legal, players, done, status = ext.observe_indexed(self.states, self.ids)
         stock = ext.stock_indexed(self.states, self.ids)
         q_in, query_rows = native.prepare(self.states, features, legal, players, done, status,
                                           stock, actor.event_in.weight.dtype)
-        logits = actor.readout(actor.cached_step(self.cache, actor.query_from_input(q_in),
-                                                 rows=query_rows))
+        # the last step's event tokens (both seats' rows) and this step's queries through
+        # the layers together; the queries attend the events' new keys at every layer
+        actor.query_from_input(q_in, out=self.pair[2 * w:])
+        hidden = cached_step_pair(actor, self.cache, self.pair, 2 * w, self.event_pos,
+                                  self.cache.length.index_select(0, query_rows), query_rows)
+        logits = actor.readout(hidden[2 * w:])
         if pool:
             p, opp = self.p, self.opponent
             theirs = opp.readout(opp.cached_step(self.opp_cache, opp.query_from_input(q_in[:p])))
@@ -309,13 +328,20 @@ class SelfPlayWave:
         actions, logp = ext.gumbel_sample(logits.contiguous(), legal, noise)
         reward0, new_done, nagari, step_status, committed, events = ext.step_events_indexed(
             self.states, self.ids, actions)
-        actor.cached_step(self.cache, actor.event_token(events, self.seats2, t.count))
+        actor.event_token(events, self.seats2, t.count, out=self.pair[:2 * w])
+        self.event_pos.copy_(self.cache.length)  # before advance counts the committed ones
         if pool:
             opp.cached_step(self.opp_cache,
                             opp.event_token(events[:p], 1 - t.learner_seat[:p], t.count[:p]))
         native.advance(done, reward0, new_done, nagari, step_status, committed, events, actions,
                        logp)
         t.step_index += 1
+
+    @torch.no_grad()
+    def flush(self) -> None:
+        """Runs the last step's waiting event tokens through the learner's layers, so its
+        cache holds every event as the reference's does after the same steps."""
+        cached_step(self.actor, self.cache, self.pair[:2 * self.w], pos=self.event_pos)
 
     def _capture_step(self, pool: bool) -> torch.cuda.CUDAGraph:
         """step(pool) as a HIP graph.  Library handles, the caching allocator's blocks and
@@ -373,6 +399,7 @@ class SelfPlayWave:
                     break
                 if behind[1] == self.max_steps:
                     raise RuntimeError(f"a wave ran {self.max_steps} steps with games left")
+        self.flush()
         problems = int(t.bad)
         if problems:
             raise RuntimeError(f"{problems} observe or step results of active games were "

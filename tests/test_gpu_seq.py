@@ -484,10 +484,12 @@ def test_selfplay_step_matches_reference_formulation(ext, mode, pool):
         for name in names:
             want = torch.stack(ref["rec"][name])
             assert torch.equal(recs[name][:steps], want), name
+        # The last step's event tokens wait for the next step's queries: flush them.
         # Live slots only (below each row's length): slots past it still hold keys of
         # the games played while capturing, which no query reads.  Layer 0's keys come
         # from the tokens alone; deeper layers also carry the reference's bf16 rounding
         # of attention scores and probabilities (the HIP decode keeps them in fp32).
+        wave.flush()
         live = (torch.arange(wave.cache.slots, device=DEV).view(1, -1)
                 < wave.cache.length.view(-1, 1)).view(1, -1, 1, wave.cache.slots, 1)
         errs = [rel_err((wave.cache.k[i] * live[0]).float(), (ref["cache"].k[i] * live[0]).float())
