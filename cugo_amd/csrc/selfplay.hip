@@ -441,7 +441,9 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   const i64 rec = step * w + i;
   const float* f = features + i * kFeatures;
   const int width = (int)wave.width;
-  typename T::storage* q = q_in + i * (width + kActions);
+  const int q_stride = wave.q_stride > 0 ? (int)wave.q_stride : width + kActions;
+  typename T::storage* q = q_in + i * q_stride;
+  for (int j = width + kActions + lane; j < q_stride; j += 64) q[j] = T::from_float(0.0f);
   for (int j = lane; j < width; j += 64) {
     const float x = f[wave.columns != nullptr ? wave.columns[j] : j];
     q[j] = T::from_float(x);
@@ -757,7 +759,8 @@ int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8
   if (!wave || wave->w < 0 || wave->max_steps < 0 || wave->width < 1 ||
       wave->width > kFeatures || (wave->columns == nullptr && wave->width != kFeatures) ||
       wave->pool_games < 0 || wave->pool_games > wave->w ||
-      (wave->pool_games > 0 && !wave->learner_seat))
+      (wave->pool_games > 0 && !wave->learner_seat) ||
+      (wave->q_stride != 0 && wave->q_stride < wave->width + kActions))
     return -1;
   const int64_t w = wave->w;
   if (w > 0 && (!states || !features || !legal || !player || !done || !status || !stock ||

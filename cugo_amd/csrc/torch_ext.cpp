@@ -1222,11 +1222,13 @@ class SelfPlayState {
                           u8p(rec_valid)};
   }
 
-  // -> (q_in [w, width + 179] of q_dtype, query_rows int64 [w])
+  // -> (q_in [w, q_stride or width + 179] of q_dtype, query_rows int64 [w]); with
+  // q_stride > 0 the columns past width + 179 are zeros (a padded query input)
   std::vector<torch::Tensor> prepare(torch::Tensor states, torch::Tensor features,
                                      torch::Tensor legal, torch::Tensor player,
                                      torch::Tensor done, torch::Tensor status,
-                                     torch::Tensor stock, at::ScalarType q_dtype) {
+                                     torch::Tensor stock, at::ScalarType q_dtype,
+                                     int64_t q_stride) {
     const int64_t w = c_.w;
     check_states(states);
     TORCH_CHECK(states.size(0) == w, "states must hold the wave's w rows");
@@ -1246,7 +1248,11 @@ class SelfPlayState {
     for (const auto* t : {&states, &features, &legal, &player, &done, &status, &stock})
       TORCH_CHECK(t->device() == keep_[0].device(), "inputs must be on the wave's device");
     const DeviceGuard guard(states.device());
-    auto q_in = torch::empty({w, c_.width + CUGO_ACTION_COUNT}, on(states, q_dtype));
+    TORCH_CHECK(q_stride == 0 || q_stride >= c_.width + CUGO_ACTION_COUNT,
+                "q_stride must be 0 or at least width + ACTION_COUNT");
+    c_.q_stride = q_stride;
+    auto q_in = torch::empty({w, q_stride > 0 ? q_stride : c_.width + CUGO_ACTION_COUNT},
+                             on(states, q_dtype));
     auto rows = torch::empty({w}, on(states, at::kLong));
     check_call(cugo_selfplay_prepare(&c_, q_dtype == at::kBFloat16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32,
                                      u8p(states), features.data_ptr<float>(), u8p(legal),
@@ -1380,7 +1386,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                           torch::Tensor, torch::Tensor, torch::Tensor,
                           c10::optional<torch::Tensor>, int64_t, torch::Tensor,
                           c10::optional<torch::Tensor>>())
-      .def("prepare", &SelfPlayState::prepare)
+      .def("prepare", &SelfPlayState::prepare, pybind11::arg("states"), pybind11::arg("features"),
+           pybind11::arg("legal"), pybind11::arg("player"), pybind11::arg("done"),
+           pybind11::arg("status"), pybind11::arg("stock"), pybind11::arg("q_dtype"),
+           pybind11::arg("q_stride") = 0)
       .def("advance", &SelfPlayState::advance);
   m.def("masked_argmax", &masked_argmax, "Greedy action: argmax of the legal logits");
   m.def("mlp_pack_weight", &mlp_pack_weight,

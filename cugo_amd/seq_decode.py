@@ -76,7 +76,7 @@ def _fits_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | Non
     """The shapes and alignments `linear` takes (include/cugo_hip.h, cugo_linear)."""
     return (x.dim() == 2 and x.is_cuda and x.dtype == torch.bfloat16 and x.stride(1) == 1
             and weight.dtype == torch.bfloat16 and weight.dim() == 2
-            and weight.shape[1] == x.shape[1] and x.shape[1] in (64, 128, 256, 512, 1024)
+            and weight.shape[1] <= x.shape[1] and x.shape[1] in (64, 128, 256, 512, 1024)
             and weight.shape[0] % 4 == 0 and (x.shape[0] <= 1 or x.stride(0) % 8 == 0)
             and x.data_ptr() % 16 == 0
             and (bias is None or (bias.dtype == torch.bfloat16 and bias.is_contiguous()
@@ -86,21 +86,25 @@ def _fits_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | Non
 _PACKED: dict[int, tuple] = {}
 
 
-def packed_weight(weight: torch.Tensor) -> torch.Tensor:
+def packed_weight(weight: torch.Tensor, k_pad: int | None = None) -> torch.Tensor:
     """`weight` [n, k] in the fragment order `linear` reads (mlp_pack_weight with n padded
-    to 16), built on first use and rebuilt into the same buffer when the weight changes
-    in place (its version), so a captured HIP graph reads the new values."""
+    to 16 and k to k_pad, zeros past k), built on first use and rebuilt into the same
+    buffer when the weight changes in place (its version), so a captured HIP graph reads
+    the new values."""
     n, k = weight.shape
+    kp = k if k_pad is None else k_pad
     key = (weight.data_ptr(), weight._version)
-    hit = _PACKED.get(id(weight))
+    slot = (id(weight), kp)
+    hit = _PACKED.get(slot)
+    rows = (n + 15) // 16 * 16
     if (hit is None or hit[0]() is not weight or hit[2].device != weight.device
-            or hit[2].numel() != (n + 15) // 16 * 16 * k):
+            or hit[2].numel() != rows * kp):
         hit = (weakref.ref(weight), key,
-               _ext().mlp_pack_weight(weight.detach().contiguous(), (n + 15) // 16 * 16, k))
+               _ext().mlp_pack_weight(weight.detach().contiguous(), rows, kp))
     elif hit[1] != key:
-        hit[2].copy_(_ext().mlp_pack_weight(weight.detach().contiguous(), (n + 15) // 16 * 16, k))
+        hit[2].copy_(_ext().mlp_pack_weight(weight.detach().contiguous(), rows, kp))
         hit = (hit[0], key, hit[2])
-    _PACKED[id(weight)] = hit
+    _PACKED[slot] = hit
     return hit[2]
 
 
@@ -117,11 +121,14 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
            gelu: bool = False, residual: torch.Tensor | None = None) -> torch.Tensor:
     """F.linear(x, weight, bias), then F.gelu when `gelu`, then residual + that when a
     residual is given: one HIP launch (`linear`) for bf16 rows with K in {64, ..., 1,024}
-    and N a multiple of 4, torch's ops otherwise."""
+    and N a multiple of 4, torch's ops otherwise.  x may be wider than the weight's K when
+    its extra columns are zeros (a padded input: the packed weight is zero there too)."""
+    if x.shape[-1] != weight.shape[1] and not _fits_linear(x, weight, bias):
+        x = x[..., :weight.shape[1]]
     if _fits_linear(x, weight, bias) and (
             residual is None or (residual.dtype == torch.bfloat16 and residual.is_contiguous()
                                  and residual.shape == (x.shape[0], weight.shape[0]))):
-        return _ext().linear(x, packed_weight(weight), weight.shape[0],
+        return _ext().linear(x, packed_weight(weight, x.shape[1]), weight.shape[0],
                              None if bias is None else bias.detach(), gelu,
                              residual=residual)
     y = F.linear(x, weight, bias)

@@ -149,8 +149,14 @@ class SeqPolicy(nn.Module):
     def query_from_input(self, q_in: torch.Tensor,
                          out: torch.Tensor | None = None) -> torch.Tensor:
         """query_token on the already concatenated input [n, 720 + 179] (into `out` when
-        given)."""
-        return torch.add(self.query_in(q_in), self.token_type[2], out=out)
+        given); q_in may carry zero columns past the input width (SelfPlayState.prepare's
+        padded rows), so that the first layer and its GELU run as one `linear` launch."""
+        first, act, second = self.query_in
+        if is_exact_gelu(act):
+            h = linear(q_in, first.weight, first.bias, gelu=True)
+        else:
+            h = act(linear(q_in, first.weight, first.bias))
+        return torch.add(linear(h, second.weight, second.bias), self.token_type[2], out=out)
 
     def readout(self, h: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:187-189 and :288-289: head(norm(h)), the norm as one HIP launch
@@ -248,6 +254,10 @@ class SelfPlayWave:
         # alone.
         d = actor.position.shape[1]
         self.pair = torch.zeros((3 * wave, d), dtype=actor.event_in.weight.dtype, device=dev)
+        # The query input's rows padded with zeros to a depth `linear` takes (1,024 for the
+        # 899 columns of the hybrid mode), or unpadded where none fits.
+        q_width = (FEATURES if cols is None else len(cols)) + ACTIONS
+        self.q_stride = next((k for k in (64, 128, 256, 512, 1024) if k >= q_width), 0)
         self.event_pos = torch.zeros(2 * wave, dtype=torch.int64, device=dev)
 
     # the reference's tensor names, for callers of the wave's outcome
@@ -309,7 +319,7 @@ class SelfPlayWave:
         features, legal, players, done, status = ext.observe_indexed(self.states, self.ids)
         stock = ext.stock_indexed(self.states, self.ids)
         q_in, query_rows = native.prepare(self.states, features, legal, players, done, status,
-                                          stock, actor.event_in.weight.dtype)
+                                          stock, actor.event_in.weight.dtype, self.q_stride)
         # the last step's event tokens (both seats' rows) and this step's queries through
         # the layers together; the queries attend the events' new keys at every layer
         actor.query_from_input(q_in, out=self.pair[2 * w:])

@@ -469,12 +469,15 @@ typedef struct CugoSelfPlayWave {
   int64_t* rec_seat;
   int64_t* rec_count;
   uint8_t* rec_valid;             /* [max_steps, w] bool */
+  int64_t q_stride;               /* elements between q_in rows, >= width + 179 (the
+                                     columns past width + 179 are written as zeros); 0 means
+                                     width + 179 */
 } CugoSelfPlayWave;
 
 /* cugo_selfplay_prepare: the step's work between observe and the policy
  * (cugo_seq_selfplay50.py:110-140): bad += active & (status != OK or no legal action);
- * q_in [w, width + 179] of q_dtype = (the kept feature columns, legal as 0/1), the
- * policy's query input; records of step step_index (skipped outside [0, max_steps)): the
+ * q_in [w, width + 179] of q_dtype (row stride q_stride, zero padded) = (the kept feature
+ * columns, legal as 0/1), the policy's query input; records of step step_index (skipped outside [0, max_steps)): the
  * kept features as bf16, legal, opponent hand (hands word 1 - player of the state row),
  * stock, stop points (round(exp2(12 f[471]) - 1), cugo_contract50.py:40-42), seat, count,
  * valid = active and the learner moves (a pool game's mover may be the opponent);

@@ -236,6 +236,33 @@ def test_linear_matches_float64(ext, m, n, k):
             ext.linear(x, wp, n, b, tile=8)
 
 
+def test_linear_on_a_zero_padded_input(ext):
+    """The query MLP's first layer (K = 899) on prepare's zero-padded 1,024-column rows:
+    the wrapper packs the weight with zero columns to 1,024, so the result equals the
+    kernel on the explicitly padded weight bit for bit, and torch's F.gelu(F.linear) on
+    the unpadded input within the bf16 bar; an unpadded 899-column input falls back to
+    torch."""
+    from cugo_amd.seq_decode import linear
+
+    announce("linear on a zero-padded input (899 of 1,024 columns)")
+    g = torch.Generator(device="cpu").manual_seed(899)
+    x = torch.randn(1000, 899, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(512, 899, generator=g) * 0.03).to(torch.bfloat16).to(DEV)
+    b = (torch.randn(512, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    xpad = torch.zeros(1000, 1024, dtype=torch.bfloat16, device=DEV)
+    xpad[:, :899] = x
+    wpad = torch.zeros(512, 1024, dtype=torch.bfloat16, device=DEV)
+    wpad[:, :899] = w
+    got = linear(xpad, w, b, gelu=True)
+    assert torch.equal(got, ext.linear(xpad, ext.mlp_pack_weight(wpad, 512, 1024), 512, b,
+                                       gelu=True))
+    want = torch.nn.functional.gelu(torch.nn.functional.linear(x, w, b))
+    assert rel_err(got, want) <= 1e-2
+    same = float((got.view(torch.int16) == want.view(torch.int16)).float().mean())
+    assert same >= 0.98, same
+    assert torch.equal(linear(x, w, b, gelu=True), want)
+
+
 @pytest.mark.parametrize("m,k", [(4096, 256), (8192, 1024), (1001, 256), (1, 64)])
 def test_linear_add_layernorm_equals_its_two_launches(ext, m, k):
     """linear_add_layernorm == add_layernorm(res, linear(x)) bit for bit (x_out and ln),
@@ -338,13 +365,16 @@ def _reference_step(policy, ref, actions_from=None):
     active = ~done
     ref["bad"] += (active & ((status != 0) | ~legal.any(1))).sum()
     player = players.long()
-    q = policy.query_token(features, legal)
+    kept = features if policy.mode == "hybrid" else features.index_select(1, policy.context_index)
+    dt = policy.event_in.weight.dtype
+    # cugo_seq50.py:166-180 in torch ops
+    q = policy.query_in(torch.cat((kept.to(dt), legal.to(dt)), -1)) + policy.token_type[2]
     hidden = reference_cached_step(policy, ref["cache"], q, (player & 1) * w + ids)
     logits = policy.head(policy.norm(hidden)).float()  # cugo_seq50.py:187-189, torch ops
     learner_move = torch.ones_like(active)
     if p:
         pids = torch.arange(p, device=DEV)
-        opp_q = opp.query_token(features[:p], legal[:p])
+        opp_q = opp.query_in(torch.cat((kept[:p].to(dt), legal[:p].to(dt)), -1)) + opp.token_type[2]
         opp_h = reference_cached_step(opp, ref["opp_cache"], opp_q, pids)
         opp_logits = opp.head(opp.norm(opp_h)).float()
         opp_move = player[:p] != ref["learner_seat"][:p]
@@ -356,7 +386,6 @@ def _reference_step(policy, ref, actions_from=None):
     stock = ext.stock_indexed(ref["states"], ids)
     stop = torch.round(torch.exp2(12.0 * features[:, 471].float()) - 1.0).long()
     rec = ref["rec"]
-    kept = features if policy.mode == "hybrid" else features.index_select(1, policy.context_index)
     rec["features"].append(kept.to(torch.bfloat16))
     rec["legal"].append(legal)
     rec["seat"].append(player)
