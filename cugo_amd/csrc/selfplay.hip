@@ -484,6 +484,7 @@ __global__ __launch_bounds__(256) void advance_kernel(
     const i64* events, const i64* actions, const float* logp) {
   const i64 w = wave.w;
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0 && wave.noise_epoch != nullptr) wave.noise_epoch[0] += 1;  // read by no one here
   const bool in = i < w;
   const bool active = in && done[i] == 0;
   const u64 bad = __ballot(active && step_status[i] != 0);

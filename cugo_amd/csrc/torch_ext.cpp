@@ -1263,6 +1263,15 @@ class SelfPlayState {
     return {q_in, rows};
   }
 
+  // The counter every advance raises by one (the Philox noise epoch of the next step).
+  void set_noise_epoch(torch::Tensor epoch) {
+    TORCH_CHECK(epoch.numel() == 1 && epoch.scalar_type() == at::kLong && epoch.is_cuda() &&
+                    epoch.device() == keep_[0].device(),
+                "epoch must be a one-element int64 tensor on the wave's device");
+    keep_.push_back(epoch);
+    c_.noise_epoch = reinterpret_cast<uint64_t*>(epoch.data_ptr());
+  }
+
   void advance(torch::Tensor done, torch::Tensor reward0, torch::Tensor new_done,
                torch::Tensor nagari, torch::Tensor step_status, torch::Tensor committed,
                torch::Tensor events, torch::Tensor actions, torch::Tensor logp) {
@@ -1390,7 +1399,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            pybind11::arg("legal"), pybind11::arg("player"), pybind11::arg("done"),
            pybind11::arg("status"), pybind11::arg("stock"), pybind11::arg("q_dtype"),
            pybind11::arg("q_stride") = 0)
-      .def("advance", &SelfPlayState::advance);
+      .def("advance", &SelfPlayState::advance)
+      .def("set_noise_epoch", &SelfPlayState::set_noise_epoch);
   m.def("masked_argmax", &masked_argmax, "Greedy action: argmax of the legal logits");
   m.def("mlp_pack_weight", &mlp_pack_weight,
         "bf16 matrix in the actor kernel's MFMA operand order", pybind11::arg("w"),

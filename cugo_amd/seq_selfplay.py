@@ -241,9 +241,15 @@ class SelfPlayWave:
         self.opp_cache = None if opponent is None else policy_cache(opponent, max(1, self.p), dev)
         self.columns = None if cols is None else torch.tensor(cols, dtype=torch.int32, device=dev)
         self.native = {pool: self._native(pool) for pool in ((False, True) if self.p else (False,))}
-        # Gumbel noise: None draws torch.rand inside each step; a [wave, 179] float32
-        # tensor is read instead (its caller refills it between replays).
+        # Gumbel noise: None draws Philox4x32-10 uniforms in the sampling kernel (seeded
+        # once from torch's generator; the epoch advances with every step, in the advance
+        # kernel); a [wave, 179] float32 tensor is read instead (its caller refills it
+        # between replays).
         self.noise: torch.Tensor | None = None
+        self.seed = int(torch.randint(0, 2**62, (1,)).item())
+        self.noise_epoch = torch.zeros(1, dtype=torch.int64, device=dev)
+        for native in self.native.values():
+            native.set_noise_epoch(self.noise_epoch)
         self.logits: torch.Tensor | None = None  # the last step's logits
         self.graph: torch.cuda.CUDAGraph | None = None  # one step, for `pool` below
         self.graph_pool: bool | None = None
@@ -333,9 +339,11 @@ class SelfPlayWave:
             logits = torch.cat((torch.where(their_turn, theirs.to(logits.dtype), logits[:p]),
                                 logits[p:]))
         self.logits = logits
-        noise = self.noise if self.noise is not None else torch.rand(
-            logits.shape, dtype=torch.float32, device=logits.device)
-        actions, logp = ext.gumbel_sample(logits.contiguous(), legal, noise)
+        if self.noise is not None:
+            actions, logp = ext.gumbel_sample(logits.contiguous(), legal, self.noise)
+        else:
+            actions, logp = ext.gumbel_sample_philox(logits.contiguous(), legal, self.seed,
+                                                     self.noise_epoch, 0)
         reward0, new_done, nagari, step_status, committed, events = ext.step_events_indexed(
             self.states, self.ids, actions)
         actor.event_token(events, self.seats2, t.count, out=self.pair[:2 * w])

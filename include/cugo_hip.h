@@ -472,6 +472,9 @@ typedef struct CugoSelfPlayWave {
   int64_t q_stride;               /* elements between q_in rows, >= width + 179 (the
                                      columns past width + 179 are written as zeros); 0 means
                                      width + 179 */
+  uint64_t* noise_epoch;          /* [1] or NULL: advanced by one by every
+                                     cugo_selfplay_advance (the epoch of the step's Philox
+                                     noise, cugo_gumbel_sample_philox) */
 } CugoSelfPlayWave;
 
 /* cugo_selfplay_prepare: the step's work between observe and the policy

@@ -567,6 +567,8 @@ def test_selfplay_graph_replays_equal_eager_steps(ext, pool):
 
 
 def test_selfplay_wave_plays_to_the_end(ext):
+    """A wave with the default noise (Philox uniforms drawn in the sampling kernel) plays
+    to the end with only legal actions; the noise epoch advances once a step."""
     announce("selfplay wave to the end")
     from cugo_amd.seq_selfplay import SelfPlayWave, make_seeds
 
@@ -575,7 +577,11 @@ def test_selfplay_wave_plays_to_the_end(ext):
     wave = SelfPlayWave(ext, policy, w, max_steps=64)
     seeds, first = make_seeds(w, 4242, DEV)
     with torch.no_grad():
+        wave.capture()
+        epoch0 = int(wave.noise_epoch)
         steps = wave.play(seeds, first, torch.zeros(w, dtype=torch.int64, device=DEV))
+    # the Philox noise's epoch advanced once per replayed step (fresh uniforms each step)
+    assert int(wave.noise_epoch) - epoch0 == steps
     assert 16 <= steps <= 64
     assert bool(wave.finished.all())
     assert int(wave.bad) == 0
