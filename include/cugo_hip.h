@@ -363,8 +363,9 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
  * with the residual add and the next LayerNorm (cugo_seq50.py:316-322).  y = bf16(x w^T +
  * bias); x_out = bf16(res + y); ln = LayerNorm(x_out) * ln_weight + ln_bias, with the
  * statistics and roundings of cugo_add_layernorm.  n must be 256; res, x_out, ln
- * contiguous [m, 256] (x_out may alias res); other requirements as cugo_linear.  tile: 1
- * for 32-row tiles on 4 wavefronts, 0 or 2 on 8, 3 for 16-row tiles on 4. */
+ * contiguous [m, 256] (x_out may alias res); other requirements as cugo_linear.  tile: 0
+ * by shape; 1 for 32-row tiles on 4 wavefronts, 2 on 8, 3 for 16-row tiles on 4, 4 for
+ * 64-row tiles on 8. */
 int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
                               const void* bias, int64_t m, int64_t n, int64_t k, const void* res,
                               const void* ln_weight, const void* ln_bias, float eps,

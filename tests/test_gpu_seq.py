@@ -287,7 +287,9 @@ def test_linear_add_layernorm_equals_its_two_launches(ext, m, k):
             want_x, want_ln = ext.add_layernorm(res, y, norm.weight, norm.bias, norm.eps)
             assert torch.equal(xo, want_x) and torch.equal(ln, want_ln)
         xo, ln = ext.linear_add_layernorm(x, wp, b, res, norm.weight, norm.bias, norm.eps)
-        for tile in (1, 2, 3):
+        for tile, rows in ((1, 32), (2, 32), (3, 16), (4, 64)):
+            if rows * k * 2 > 160 * 1024:  # the X panel does not fit the LDS
+                continue
             got = ext.linear_add_layernorm(x, wp, b, res, norm.weight, norm.bias, norm.eps,
                                            tile=tile)
             assert torch.equal(got[0], xo) and torch.equal(got[1], ln), tile
