@@ -60,9 +60,10 @@ struct Args {
   int m, n, ldx, ldy;
   int col_blocks;  // workgroups along n
   int wtiles;      // 16-row tiles of the packed W
-  // the residual (row stride ldy), added to the output after its rounding (NULL: none);
-  // kAddNorm's residual, with rows of n = BN elements
+  // the residual (row stride ldr, 0: one row for all), added to the output after its
+  // rounding (NULL: none); kAddNorm's residual (row stride ldy), rows of n = BN elements
   const __bf16* res;
+  int ldr;
   const __bf16* ln_w;
   const __bf16* ln_b;
   __bf16* ln;
@@ -288,7 +289,9 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
     return;
   }
   constexpr int kPieces = BM * BN / 8;  // 16-byte pieces of the tile
-  const bool wide = (a.ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+  const bool wide = (a.ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
+                    (a.res == nullptr ||
+                     ((a.ldr & 7) == 0 && (reinterpret_cast<uintptr_t>(a.res) & 15) == 0));
 #pragma unroll
   for (int p0 = 0; p0 < kPieces; p0 += kT) {
     const int p = p0 + tid;
@@ -297,15 +300,15 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
       const int row = m0 + r, col = nb0 + c;
       if (row < a.m && col < a.n) {
         uint4 v = *reinterpret_cast<const uint4*>(xs + r * kOutStride + c);
-        const int64_t at = (int64_t)row * a.ldy + col;
-        __bf16* dst = a.y + at;
+        __bf16* dst = a.y + (int64_t)row * a.ldy + col;
+        const __bf16* rsrc = a.res + (int64_t)row * a.ldr + col;
         if (wide && col + 8 <= a.n) {
-          if (a.res != nullptr) v = add_bf16(v, *reinterpret_cast<const uint4*>(a.res + at));
+          if (a.res != nullptr) v = add_bf16(v, *reinterpret_cast<const uint4*>(rsrc));
           *reinterpret_cast<uint4*>(dst) = v;
         } else {
           if (a.res != nullptr) {
-            const uint2 lo = *reinterpret_cast<const uint2*>(a.res + at);
-            const uint2 hi = col + 8 <= a.n ? *reinterpret_cast<const uint2*>(a.res + at + 4)
+            const uint2 lo = *reinterpret_cast<const uint2*>(rsrc);
+            const uint2 hi = col + 8 <= a.n ? *reinterpret_cast<const uint2*>(rsrc + 4)
                                             : uint2{0u, 0u};
             v = add_bf16(v, uint4{lo.x, lo.y, hi.x, hi.y});
           }
@@ -368,12 +371,14 @@ using namespace cugo_amd::linear;
 extern "C" {
 
 int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const void* bias,
-                const void* residual, int64_t m, int64_t n, int64_t k, void* y, int64_t ldy,
-                int tile, hipStream_t stream) {
+                const void* residual, int64_t ldr, int64_t m, int64_t n, int64_t k, void* y,
+                int64_t ldy, int tile, hipStream_t stream) {
   if (m < 0 || n < 1 || k < 1 || (m > 0 && (!x || !w_packed || !y))) return -1;
   if (act != CUGO_LINEAR_NONE && act != CUGO_LINEAR_GELU) return -2;
   const bool k_ok = k == 64 || k == 128 || k == 256 || k == 512 || k == 1024;
-  if (!k_ok || n % 4 != 0 || ldx < k || ldx % 8 != 0 || ldy < n || ldy % 4 != 0) return -3;
+  if (!k_ok || n % 4 != 0 || ldx < k || ldx % 8 != 0 || ldy < n || ldy % 4 != 0 ||
+      (residual != nullptr && ldr != 0 && (ldr < n || ldr % 4 != 0)))
+    return -3;
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed)) % 16 != 0 ||
       (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(bias) |
        reinterpret_cast<uintptr_t>(residual)) % 8 != 0)
@@ -386,6 +391,7 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
   a.w = static_cast<const __bf16*>(w_packed);
   a.bias = static_cast<const __bf16*>(bias);
   a.res = static_cast<const __bf16*>(residual);
+  a.ldr = (int)ldr;
   a.y = static_cast<__bf16*>(y);
   a.m = (int)m;
   a.n = (int)n;

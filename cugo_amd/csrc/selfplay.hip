@@ -463,6 +463,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   if (active && (status[i] != 0 || !any)) atomicAdd(wave.bad, 1ull);
   const i64 p = (i64)player[i];
   query_rows[i] = (p & 1) * w + i;
+  if (wave.query_pos != nullptr) wave.query_pos[i] = wave.cache_length[(p & 1) * w + i];
   if (!record) return;
   wave.rec_seat[rec] = p;
   wave.rec_count[rec] = wave.count[i];

@@ -859,7 +859,7 @@ std::vector<torch::Tensor> add_layernorm(torch::Tensor x, c10::optional<torch::T
 // (unit stride along k).
 torch::Tensor linear(torch::Tensor x, torch::Tensor w_packed, int64_t n,
                      c10::optional<torch::Tensor> bias, bool gelu, int64_t tile,
-                     c10::optional<torch::Tensor> residual) {
+                     c10::optional<torch::Tensor> residual, c10::optional<torch::Tensor> out) {
   TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16 && x.stride(1) == 1,
               "x must be a CUDA bfloat16 [m, k] tensor with unit stride along k");
   const int64_t m = x.size(0), k = x.size(1);
@@ -872,18 +872,21 @@ torch::Tensor linear(torch::Tensor x, torch::Tensor w_packed, int64_t n,
                 "bias must be a contiguous bfloat16 [n] tensor");
     check_same_device(x, *bias, "x", "bias");
   }
+  int64_t ldr = 0;
   if (residual.has_value()) {
     TORCH_CHECK(residual->scalar_type() == at::kBFloat16 && residual->is_contiguous() &&
-                    residual->dim() == 2 && residual->size(0) == m && residual->size(1) == n,
-                "residual must be a contiguous bfloat16 [m, n] tensor");
+                    ((residual->dim() == 2 && residual->size(0) == m && residual->size(1) == n) ||
+                     (residual->dim() == 1 && residual->size(0) == n)),
+                "residual must be a contiguous bfloat16 [m, n] tensor or an [n] row for all");
     check_same_device(x, *residual, "x", "residual");
+    ldr = residual->dim() == 2 ? n : 0;
   }
   const DeviceGuard guard(x.device());
-  auto y = torch::empty({m, n}, x.options());
+  auto y = out_or_new(out, {m, n}, at::kBFloat16, x, "out");
   const int64_t ldx = m > 1 ? x.stride(0) : k;
   check_call(cugo_linear(gelu ? CUGO_LINEAR_GELU : CUGO_LINEAR_NONE, x.data_ptr(), ldx,
                          w_packed.data_ptr(), bias.has_value() ? bias->data_ptr() : nullptr,
-                         residual.has_value() ? residual->data_ptr() : nullptr, m, n, k,
+                         residual.has_value() ? residual->data_ptr() : nullptr, ldr, m, n, k,
                          y.data_ptr(), n, static_cast<int>(tile), stream()),
              "linear");
   return y;
@@ -1222,8 +1225,9 @@ class SelfPlayState {
                           u8p(rec_valid)};
   }
 
-  // -> (q_in [w, q_stride or width + 179] of q_dtype, query_rows int64 [w]); with
-  // q_stride > 0 the columns past width + 179 are zeros (a padded query input)
+  // -> (q_in [w, q_stride or width + 179] of q_dtype, query_rows int64 [w], query_pos int64
+  // [w] = the cache length of each query row); with q_stride > 0 the columns past
+  // width + 179 are zeros (a padded query input)
   std::vector<torch::Tensor> prepare(torch::Tensor states, torch::Tensor features,
                                      torch::Tensor legal, torch::Tensor player,
                                      torch::Tensor done, torch::Tensor status,
@@ -1254,13 +1258,15 @@ class SelfPlayState {
     auto q_in = torch::empty({w, q_stride > 0 ? q_stride : c_.width + CUGO_ACTION_COUNT},
                              on(states, q_dtype));
     auto rows = torch::empty({w}, on(states, at::kLong));
+    auto pos = torch::empty({w}, on(states, at::kLong));
+    c_.query_pos = pos.data_ptr<int64_t>();
     check_call(cugo_selfplay_prepare(&c_, q_dtype == at::kBFloat16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32,
                                      u8p(states), features.data_ptr<float>(), u8p(legal),
                                      u8p(player), u8p(done), status.data_ptr<int16_t>(),
                                      stock.data_ptr<int64_t>(), q_in.data_ptr(),
                                      rows.data_ptr<int64_t>(), stream()),
                "selfplay_prepare");
-    return {q_in, rows};
+    return {q_in, rows, pos};
   }
 
   // The counter every advance raises by one (the Philox noise epoch of the next step).
@@ -1380,7 +1386,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("linear", &linear, "bf16 x weight^T + bias, optionally followed by GELU, in one launch",
         pybind11::arg("x"), pybind11::arg("w_packed"), pybind11::arg("n"),
         pybind11::arg("bias") = pybind11::none(), pybind11::arg("gelu") = false,
-        pybind11::arg("tile") = 0, pybind11::arg("residual") = pybind11::none());
+        pybind11::arg("tile") = 0, pybind11::arg("residual") = pybind11::none(),
+        pybind11::arg("out") = pybind11::none());
   m.def("linear_add_layernorm", &linear_add_layernorm,
         "linear, then the residual add and LayerNorm of add_layernorm, in one launch",
         pybind11::arg("x"), pybind11::arg("w_packed"), pybind11::arg("bias"), pybind11::arg("res"),

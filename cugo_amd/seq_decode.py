@@ -118,22 +118,26 @@ def prepare_linears(model: nn.Module) -> None:
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
-           gelu: bool = False, residual: torch.Tensor | None = None) -> torch.Tensor:
+           gelu: bool = False, residual: torch.Tensor | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
     """F.linear(x, weight, bias), then F.gelu when `gelu`, then residual + that when a
-    residual is given: one HIP launch (`linear`) for bf16 rows with K in {64, ..., 1,024}
-    and N a multiple of 4, torch's ops otherwise.  x may be wider than the weight's K when
-    its extra columns are zeros (a padded input: the packed weight is zero there too)."""
+    residual is given ([rows, N], or an [N] row for every row): one HIP launch (`linear`)
+    for bf16 rows with K in {64, ..., 1,024} and N a multiple of 4, torch's ops otherwise;
+    into `out` when given.  x may be wider than the weight's K when its extra columns are
+    zeros (a padded input: the packed weight is zero there too)."""
     if x.shape[-1] != weight.shape[1] and not _fits_linear(x, weight, bias):
         x = x[..., :weight.shape[1]]
+    n = weight.shape[0]
     if _fits_linear(x, weight, bias) and (
             residual is None or (residual.dtype == torch.bfloat16 and residual.is_contiguous()
-                                 and residual.shape == (x.shape[0], weight.shape[0]))):
-        return _ext().linear(x, packed_weight(weight, x.shape[1]), weight.shape[0],
+                                 and residual.shape in ((x.shape[0], n), (n,)))):
+        return _ext().linear(x, packed_weight(weight, x.shape[1]), n,
                              None if bias is None else bias.detach(), gelu,
-                             residual=residual)
+                             residual=None if residual is None else residual.detach(), out=out)
     y = F.linear(x, weight, bias)
     y = F.gelu(y) if gelu else y
-    return y if residual is None else residual + y
+    y = y if residual is None else residual + y
+    return y if out is None else out.copy_(y)
 
 
 def linear_add_norm(u: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,

@@ -156,7 +156,8 @@ class SeqPolicy(nn.Module):
             h = linear(q_in, first.weight, first.bias, gelu=True)
         else:
             h = act(linear(q_in, first.weight, first.bias))
-        return torch.add(linear(h, second.weight, second.bias), self.token_type[2], out=out)
+        # + token_type[2] rounded after the layer's own rounding, as torch adds the two
+        return linear(h, second.weight, second.bias, residual=self.token_type[2], out=out)
 
     def readout(self, h: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:187-189 and :288-289: head(norm(h)), the norm as one HIP launch
@@ -324,13 +325,14 @@ class SelfPlayWave:
         native = self.native[pool]
         features, legal, players, done, status = ext.observe_indexed(self.states, self.ids)
         stock = ext.stock_indexed(self.states, self.ids)
-        q_in, query_rows = native.prepare(self.states, features, legal, players, done, status,
-                                          stock, actor.event_in.weight.dtype, self.q_stride)
+        q_in, query_rows, query_pos = native.prepare(self.states, features, legal, players, done,
+                                                     status, stock, actor.event_in.weight.dtype,
+                                                     self.q_stride)
         # the last step's event tokens (both seats' rows) and this step's queries through
         # the layers together; the queries attend the events' new keys at every layer
         actor.query_from_input(q_in, out=self.pair[2 * w:])
         hidden = cached_step_pair(actor, self.cache, self.pair, 2 * w, self.event_pos,
-                                  self.cache.length.index_select(0, query_rows), query_rows)
+                                  query_pos, query_rows)
         logits = actor.readout(hidden[2 * w:])
         if pool:
             p, opp = self.p, self.opponent

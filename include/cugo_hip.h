@@ -346,9 +346,10 @@ int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weig
  * CUGO_LINEAR_GELU, GELU(v) = v / 2 (1 + erf(v / sqrt 2)) of that value rounded again.
  * x [m, k] with row stride ldx; w [n, k] (nn.Linear's layout) given as w_packed, its
  * cugo_mlp_pack_weight form with rows_pad = roundup(n, 16) and cols_pad = k; bias [n] or
- * NULL; y [m, n] with row stride ldy; residual NULL or [m, n] with row stride ldy, added
- * to each output after its rounding and rounded again (the last layer's x + linear2(u),
- * cugo_seq50.py:322); y may alias residual; fp32 accumulation.  Requires k in {64, 128, 256,
+ * NULL; y [m, n] with row stride ldy; residual NULL or [m, n] with row stride ldr (0: one
+ * [n] row for every row), added to each output after its rounding and rounded again (the
+ * last layer's x + linear2(u), cugo_seq50.py:322; the query token's + token_type[2],
+ * :166-180); y may alias residual; fp32 accumulation.  Requires k in {64, 128, 256,
  * 512, 1024}, n % 4 == 0, ldx % 8 == 0, ldy % 4 == 0, x and w_packed 16-byte aligned, y
  * and bias 8-byte aligned.  tile: 0 chooses the workgroup tile from k; 1-4 force 32 x 256,
  * 32 x 128, 64 x 128 or 64 x 256 (rows x columns).  Returns -3 for an unsupported shape,
@@ -356,8 +357,8 @@ int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weig
 #define CUGO_LINEAR_NONE 0
 #define CUGO_LINEAR_GELU 1
 int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const void* bias,
-                const void* residual, int64_t m, int64_t n, int64_t k, void* y, int64_t ldy,
-                int tile, hipStream_t stream);
+                const void* residual, int64_t ldr, int64_t m, int64_t n, int64_t k, void* y,
+                int64_t ldy, int tile, hipStream_t stream);
 /* cugo_linear_add_layernorm: cugo_linear (no activation) followed by cugo_add_layernorm of
  * its output onto res, in one launch: the out_proj / linear2 of a pre-norm encoder layer
  * with the residual add and the next LayerNorm (cugo_seq50.py:316-322).  y = bf16(x w^T +
@@ -476,6 +477,8 @@ typedef struct CugoSelfPlayWave {
   uint64_t* noise_epoch;          /* [1] or NULL: advanced by one by every
                                      cugo_selfplay_advance (the epoch of the step's Philox
                                      noise, cugo_gumbel_sample_philox) */
+  int64_t* query_pos;             /* [w] or NULL: cugo_selfplay_prepare writes
+                                     cache_length[query_rows[i]], the query's cache slot */
 } CugoSelfPlayWave;
 
 /* cugo_selfplay_prepare: the step's work between observe and the policy

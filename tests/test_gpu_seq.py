@@ -212,6 +212,10 @@ def test_linear_matches_float64(ext, m, n, k):
     assert torch.equal(ext.linear(x, wp, n, b, residual=r), r + got)
     assert torch.equal(ext.linear(x, wp, n, b, gelu=True, residual=r),
                        r + torch.nn.functional.gelu(got))
+    row = r[-1].contiguous()  # one row added to every row (the query token's + token_type)
+    into = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    assert ext.linear(x, wp, n, b, residual=row, out=into).data_ptr() == into.data_ptr()
+    assert torch.equal(into, got + row)
     wide = torch.zeros(m, k + 40, dtype=torch.bfloat16, device=DEV)
     wide[:, 8:8 + k] = x
     assert torch.equal(ext.linear(wide[:, 8:8 + k], wp, n, b), got)
