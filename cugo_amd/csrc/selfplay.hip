@@ -497,6 +497,10 @@ __global__ __launch_bounds__(256) void advance_kernel(
     if (nagari[i]) wave.final_nagari[i] = 1;
     wave.finished[i] = 1;
   }
+  if (wave.event_pos != nullptr) {  // the slots of this step's event tokens
+    wave.event_pos[i] = wave.cache_length[i];
+    wave.event_pos[w + i] = wave.cache_length[w + i];
+  }
   const i64 c = wave.count[i];
   if (active && committed[i]) {
     const i64 slot = c < kMaxEvents - 1 ? c : kMaxEvents - 1;

@@ -1278,6 +1278,15 @@ class SelfPlayState {
     c_.noise_epoch = reinterpret_cast<uint64_t*>(epoch.data_ptr());
   }
 
+  // Where every advance writes each cache row's length before the step's events count.
+  void set_event_pos(torch::Tensor event_pos) {
+    TORCH_CHECK(event_pos.numel() == 2 * c_.w && event_pos.scalar_type() == at::kLong &&
+                    event_pos.is_contiguous() && event_pos.device() == keep_[0].device(),
+                "event_pos must be a contiguous int64 [2 w] tensor on the wave's device");
+    keep_.push_back(event_pos);
+    c_.event_pos = event_pos.data_ptr<int64_t>();
+  }
+
   void advance(torch::Tensor done, torch::Tensor reward0, torch::Tensor new_done,
                torch::Tensor nagari, torch::Tensor step_status, torch::Tensor committed,
                torch::Tensor events, torch::Tensor actions, torch::Tensor logp) {
@@ -1407,7 +1416,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            pybind11::arg("status"), pybind11::arg("stock"), pybind11::arg("q_dtype"),
            pybind11::arg("q_stride") = 0)
       .def("advance", &SelfPlayState::advance)
-      .def("set_noise_epoch", &SelfPlayState::set_noise_epoch);
+      .def("set_noise_epoch", &SelfPlayState::set_noise_epoch)
+      .def("set_event_pos", &SelfPlayState::set_event_pos);
   m.def("masked_argmax", &masked_argmax, "Greedy action: argmax of the legal logits");
   m.def("mlp_pack_weight", &mlp_pack_weight,
         "bf16 matrix in the actor kernel's MFMA operand order", pybind11::arg("w"),

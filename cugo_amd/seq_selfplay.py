@@ -266,6 +266,8 @@ class SelfPlayWave:
         q_width = (FEATURES if cols is None else len(cols)) + ACTIONS
         self.q_stride = next((k for k in (64, 128, 256, 512, 1024) if k >= q_width), 0)
         self.event_pos = torch.zeros(2 * wave, dtype=torch.int64, device=dev)
+        for native in self.native.values():  # advance writes the slots of a step's events
+            native.set_event_pos(self.event_pos)
 
     # the reference's tensor names, for callers of the wave's outcome
     def __getattr__(self, name: str):
@@ -349,7 +351,6 @@ class SelfPlayWave:
         reward0, new_done, nagari, step_status, committed, events = ext.step_events_indexed(
             self.states, self.ids, actions)
         actor.event_token(events, self.seats2, t.count, out=self.pair[:2 * w])
-        self.event_pos.copy_(self.cache.length)  # before advance counts the committed ones
         if pool:
             opp.cached_step(self.opp_cache,
                             opp.event_token(events[:p], 1 - t.learner_seat[:p], t.count[:p]))

@@ -479,6 +479,9 @@ typedef struct CugoSelfPlayWave {
                                      noise, cugo_gumbel_sample_philox) */
   int64_t* query_pos;             /* [w] or NULL: cugo_selfplay_prepare writes
                                      cache_length[query_rows[i]], the query's cache slot */
+  int64_t* event_pos;             /* [2 w] or NULL: cugo_selfplay_advance writes each cache
+                                     row's length before the step's events are counted (the
+                                     slots the step's event tokens go to) */
 } CugoSelfPlayWave;
 
 /* cugo_selfplay_prepare: the step's work between observe and the policy
