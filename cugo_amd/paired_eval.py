@@ -1,10 +1,10 @@
 """Paired evaluation on the HIP engine (python/cugo_eval50.py:137-361, `evaluate_paired`).
 
 Every deal is played twice, model A on seat 0 in game i and on seat 1 in game pairs + i,
-so deal luck cancels in the pair score.  A decision step observes the games still
-running, evaluates each model on the rows where its seat moves, takes the greedy action
-(the `masked_argmax` kernel: argmax of the fp32 logits with illegal actions at -1e30) or
-samples from the softmax, steps the engine, and drops finished games.  Summary fields and
+so deal luck cancels in the pair score.  A decision step observes the games, evaluates
+each model, takes for every game the greedy action of the model whose seat moves (the
+`masked_argmax` kernel: argmax of the fp32 logits with illegal actions at -1e30) or a
+sample from its softmax, and steps the engine; finished games stay resident, masked.  Summary fields and
 their meaning are the reference's `EvalSummary` (cugo_eval50.py:27-61).
 
 Policies are modules mapping the [n, 720] features to logits (or a tuple whose first
@@ -82,7 +82,14 @@ def _mean(x: torch.Tensor) -> float:
 
 def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, seed_offset: int,
                     max_steps: int, use_amp: bool, sample_a: bool = False,
-                    sample_b: bool = False) -> EvalSummary:
+                    sample_b: bool = False, graph: bool = True) -> EvalSummary:
+    """cugo_eval50.py:137-361 on resident games: every step observes all 2 pairs games,
+    evaluates both models on every row, keeps model A's action where A's seat moves and
+    B's elsewhere, and steps every game; rows of games that are over are masked out of
+    the outcome and the checks (the reference drops them instead, which needs the count of
+    survivors on the host every step).  The per-row decisions are the reference's; the
+    step is one HIP-graph replay (greedy policies; `graph=False` or sampling: eager), and
+    the host reads whether games are left one step behind, so the GPU never waits."""
     if pairs <= 0:
         raise ValueError("pairs must be positive")
     if max_steps <= 0:
@@ -95,55 +102,79 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
     final_reward0 = torch.zeros(games, device=dev)
     final_nagari = torch.zeros(games, dtype=torch.bool, device=dev)
     excluded = torch.zeros(games, dtype=torch.bool, device=dev)  # over before any decision
+    active = torch.zeros(games, dtype=torch.bool, device=dev)   # games still being played
     bad = torch.zeros(3, dtype=torch.int64, device=dev)  # observe, legal, step
+    steps_dev = torch.zeros((), dtype=torch.int64, device=dev)  # decision steps
     ok = int(ext.STATUS_OK)
     model_a.eval()
     model_b.eval()
-    ids = torch.arange(games, device=dev)
-    decision_steps = 0
-    finished_all = False
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
+
+    def step() -> None:
+        features, legal, players, done, status = ext.observe(states)
+        fine = status == ok
+        bad[0] += (active & ~fine).sum()
+        bad[1] += (active & fine & (done | ~legal.any(1))).sum()
+        steps_dev.add_(active.any().long())
+        a_moves = players.long() == a_seat
+        actions = torch.where(a_moves, _actions(ext, model_a, features, legal, use_amp, sample_a),
+                              _actions(ext, model_b, features, legal, use_amp, sample_b))
+        reward0, new_done, nagari, step_status, _ = ext.step(states, actions)
+        step_ok = step_status == ok
+        bad[2] += (active & ~step_ok).sum()
+        ended = active & step_ok & new_done
+        final_reward0.copy_(torch.where(ended, reward0, final_reward0))
+        final_nagari.logical_or_(ended & nagari)
+        active.logical_and_(step_ok & ~new_done)
+
+    replay = step
+    flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
     with torch.inference_mode():
-        for step in range(max_steps):
-            if ids.numel() == 0:
-                finished_all = True
-                break
-            features, legal, players, done, status = ext.observe_indexed(states, ids)
-            fine = status == ok
-            any_legal = legal.any(1)
-            if step == 0:
-                # games already over, or unplayable, at the deal leave the evaluation
-                excluded.index_fill_(0, ids[done], True)
-                live = ~done
-                bad[0] += (live & ~fine).sum()
-                bad[1] += (live & fine & ~any_legal).sum()
-                keep = live & fine & any_legal
-                ids, features, legal, players = ids[keep], features[keep], legal[keep], players[keep]
-                if ids.numel() == 0:
+        if graph and not (sample_a or sample_b):
+            # warm-up steps on a side stream (library handles, allocator blocks), then the
+            # capture; the state they touched is put back
+            kept = [states, final_reward0, final_nagari, active, bad, steps_dev]
+            saved = [t.clone() for t in kept]
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                step()
+                step()
+            torch.cuda.current_stream().wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step()
+            for t, v in zip(kept, saved):
+                t.copy_(v)
+            replay = g.replay
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        # the deal: games over already, or unplayable, leave the evaluation before step 0
+        _, legal, _, done, status = ext.observe(states)
+        fine = status == ok
+        any_legal = legal.any(1)
+        excluded.copy_(done)
+        bad[0] += (~done & ~fine).sum()
+        bad[1] += (~done & fine & ~any_legal).sum()
+        active.copy_(~done & fine & any_legal)
+        stream = torch.cuda.current_stream()
+        finished_all = False
+        behind = None  # (event, flag slot) of the step before the latest
+        for k in range(max_steps):
+            replay()
+            flags[k & 1].copy_(active.any(), non_blocking=True)
+            queued = (torch.cuda.Event(), k & 1)
+            queued[0].record(stream)
+            if behind is not None:
+                behind[0].synchronize()
+                if not bool(flags[behind[1]]):
                     finished_all = True
                     break
-            else:
-                bad[0] += (~fine).sum()
-                bad[1] += (fine & (done | ~any_legal)).sum()
-            decision_steps += 1
-            a_moves = players.long() == a_seat.index_select(0, ids)
-            actions = torch.empty(ids.numel(), dtype=torch.int64, device=dev)
-            for model, rows, sample in ((model_a, a_moves, sample_a), (model_b, ~a_moves, sample_b)):
-                at = torch.nonzero(rows).squeeze(1)
-                if at.numel():
-                    actions[at] = _actions(ext, model, features[at], legal[at], use_amp, sample)
-            reward0, new_done, nagari, step_status, _ = ext.step_indexed(states, ids, actions)
-            step_ok = step_status == ok
-            bad[2] += (~step_ok).sum()
-            ended = step_ok & new_done
-            final_reward0[ids] = torch.where(ended, reward0, torch.zeros_like(reward0))
-            final_nagari[ids] = ended & nagari
-            ids = ids[step_ok & ~new_done]
+            behind = queued
         else:
-            finished_all = ids.numel() == 0
+            finished_all = not bool(active.any())
     torch.cuda.synchronize()
     seconds = time.perf_counter() - t0
+    decision_steps = int(steps_dev)
 
     observe_bad, legal_bad, step_bad = (int(x) for x in bad.tolist())
     if observe_bad:

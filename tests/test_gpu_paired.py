@@ -129,3 +129,25 @@ def test_paired_self_play_scores_zero(ext):
     s = evaluate_paired(ext, model, model, 100, seed_offset=3, max_steps=128, use_amp=True,
                         sample_a=True, sample_b=True)
     assert s.a_wins + s.b_wins + s.draws == s.evaluated_games
+
+
+def test_paired_eval_graph_equals_eager(ext):
+    """The captured step and the eager one play the same games: identical summaries (all
+    fields but the time) for two different MLP policies under fp16 autocast."""
+    announce("paired eval: graph replay vs eager steps")
+    from dataclasses import asdict
+
+    from cugo_amd.paired_eval import evaluate_paired
+
+    def mlp(seed):
+        torch.manual_seed(seed)
+        return torch.nn.Sequential(torch.nn.Linear(720, 256), torch.nn.ReLU(),
+                                   torch.nn.Linear(256, 179)).to(DEV)
+
+    a, b = mlp(5), mlp(6)
+    runs = [asdict(evaluate_paired(ext, a, b, 300, seed_offset=41, max_steps=128, use_amp=True,
+                                   graph=g)) for g in (True, False, True)]
+    for r in runs:
+        r.pop("seconds")
+    assert runs[0] == runs[1] == runs[2]
+    assert runs[0]["evaluated_games"] > 0 and runs[0]["decision_steps"] > 10
