@@ -72,6 +72,21 @@ def _actions(ext, model: nn.Module, features, legal, use_amp: bool, sample: bool
     return ext.masked_argmax(logits, legal)
 
 
+def _half_linears(model: nn.Module) -> nn.Module:
+    """A copy of `model` whose nn.Linear weights and biases are already float16: under fp16
+    autocast a Linear casts them at every call (a cast launch per parameter and step), to
+    exactly these values, so the copy computes what the model computes without them."""
+    import copy
+
+    twin = copy.deepcopy(model)
+    for m in twin.modules():
+        if isinstance(m, nn.Linear):
+            m.weight.data = m.weight.data.half()
+            if m.bias is not None:
+                m.bias.data = m.bias.data.half()
+    return twin
+
+
 def _wdl(x: torch.Tensor) -> tuple[int, int, int]:
     return int((x > 0).sum()), int((x < 0).sum()), int((x == 0).sum())
 
@@ -108,6 +123,10 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
     ok = int(ext.STATUS_OK)
     model_a.eval()
     model_b.eval()
+    if use_amp:
+        same = model_b is model_a
+        model_a = _half_linears(model_a)
+        model_b = model_a if same else _half_linears(model_b)
 
     def step() -> None:
         features, legal, players, done, status = ext.observe(states)

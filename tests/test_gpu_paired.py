@@ -133,7 +133,8 @@ def test_paired_self_play_scores_zero(ext):
 
 def test_paired_eval_graph_equals_eager(ext):
     """The captured step and the eager one play the same games: identical summaries (all
-    fields but the time) for two different MLP policies under fp16 autocast."""
+    fields but the time) for two different MLP policies under fp16 autocast; the Linear
+    weights cast to fp16 once give autocast's own outputs bit for bit."""
     announce("paired eval: graph replay vs eager steps")
     from dataclasses import asdict
 
@@ -145,6 +146,12 @@ def test_paired_eval_graph_equals_eager(ext):
                                    torch.nn.Linear(256, 179)).to(DEV)
 
     a, b = mlp(5), mlp(6)
+    # the fp16 copy of the Linear weights computes what autocast computes, bit for bit
+    from cugo_amd.paired_eval import _half_linears
+
+    x = torch.randn(1000, 720, device=DEV)
+    with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.float16):
+        assert torch.equal(_half_linears(a)(x), a(x))
     runs = [asdict(evaluate_paired(ext, a, b, 300, seed_offset=41, max_steps=128, use_amp=True,
                                    graph=g)) for g in (True, False, True)]
     for r in runs:
