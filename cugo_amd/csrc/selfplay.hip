@@ -518,6 +518,54 @@ __global__ __launch_bounds__(256) void advance_kernel(
   }
 }
 
+// Paired evaluation on resident games (cugo_eval50.py:137-361 without dropping finished
+// games): the bookkeeping of a step around the models and the engine step.  Before the
+// step: the observe checks of the active games, the decision-step count, and each game's
+// action from the model whose seat moves.  After it: the step check, the final reward and
+// nagari flag of games that end now, and the active mask.
+__global__ __launch_bounds__(256) void paired_select_kernel(
+    const uint8_t* active, const int16_t* status, const uint8_t* done,
+    const uint8_t* any_legal, const uint8_t* player, const i64* a_seat, const i64* act_a,
+    const i64* act_b, i64 n, i64* actions, i64* bad, int* any_active) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in = i < n;
+  const bool act = in && active[i] != 0;
+  const bool fine = in && status[i] == 0;
+  const u64 obs_bad = __ballot(act && !fine);
+  const u64 legal_bad = __ballot(act && fine && (done[i] != 0 || any_legal[i] == 0));
+  const u64 live = __ballot(act);
+  if ((threadIdx.x & 63) == 0) {
+    if (obs_bad != 0) atomicAdd(reinterpret_cast<unsigned long long*>(bad), (unsigned long long)__popcll(obs_bad));
+    if (legal_bad != 0)
+      atomicAdd(reinterpret_cast<unsigned long long*>(bad + 1), (unsigned long long)__popcll(legal_bad));
+    if (live != 0) *any_active = 1;
+  }
+  if (in) actions[i] = (i64)player[i] == a_seat[i] ? act_a[i] : act_b[i];
+}
+
+__global__ __launch_bounds__(256) void paired_update_kernel(
+    uint8_t* active, const int16_t* step_status, const uint8_t* new_done, const float* reward0,
+    const uint8_t* nagari, i64 n, float* final_reward0, uint8_t* final_nagari, i64* bad,
+    int* any_active, i64* steps) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0 && *any_active != 0) {  // one decision step more; the flag is read by no one else
+    *steps += 1;
+    *any_active = 0;
+  }
+  const bool in = i < n;
+  const bool act = in && active[i] != 0;
+  const bool ok = in && step_status[i] == 0;
+  const u64 step_bad = __ballot(act && !ok);
+  if ((threadIdx.x & 63) == 0 && step_bad != 0)
+    atomicAdd(reinterpret_cast<unsigned long long*>(bad + 2), (unsigned long long)__popcll(step_bad));
+  if (!act) return;
+  if (ok && new_done[i] != 0) {
+    final_reward0[i] = reward0[i];
+    if (nagari[i] != 0) final_nagari[i] = 1;
+  }
+  active[i] = ok && new_done[i] == 0;
+}
+
 // Pre-norm transformer residual step (nn.TransformerEncoderLayer with norm_first,
 // python/cugo_seq50.py:318-322): x_out = x + y rounded to the dtype (y == nullptr: x_out is
 // not written and x is normalised as is), then ln = LayerNorm(x_out) with fp32 mean and
@@ -787,6 +835,34 @@ int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8
         stock, (float*)q_in, query_rows);
   else
     return -2;
+  return (int)hipGetLastError();
+}
+
+int cugo_paired_select(const uint8_t* active, const int16_t* status, const uint8_t* done,
+                       const uint8_t* any_legal, const uint8_t* player, const int64_t* a_seat,
+                       const int64_t* act_a, const int64_t* act_b, int64_t n, int64_t* actions,
+                       int64_t* bad, int32_t* any_active, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!active || !status || !done || !any_legal || !player || !a_seat ||
+                          !act_a || !act_b || !actions || !bad || !any_active)))
+    return -1;
+  if (n == 0) return 0;
+  paired_select_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+      active, status, done, any_legal, player, a_seat, act_a, act_b, n, actions, bad,
+      any_active);
+  return (int)hipGetLastError();
+}
+
+int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_t* new_done,
+                       const float* reward0, const uint8_t* nagari, int64_t n,
+                       float* final_reward0, uint8_t* final_nagari, int64_t* bad,
+                       int32_t* any_active, int64_t* steps, hipStream_t stream) {
+  if (n < 0 || !bad || !any_active || !steps ||
+      (n > 0 && (!active || !step_status || !new_done || !reward0 || !nagari || !final_reward0 ||
+                 !final_nagari)))
+    return -1;
+  paired_update_kernel<<<(unsigned)((n + 255) / 256 > 0 ? (n + 255) / 256 : 1), 256, 0, stream>>>(
+      active, step_status, new_done, reward0, nagari, n, final_reward0, final_nagari, bad,
+      any_active, steps);
   return (int)hipGetLastError();
 }
 

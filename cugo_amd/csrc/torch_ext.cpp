@@ -936,6 +936,73 @@ std::vector<torch::Tensor> linear_add_layernorm(torch::Tensor x, torch::Tensor w
   return {x_out, ln};
 }
 
+// paired_select(active, status, done, any_legal, player, a_seat, act_a, act_b, bad,
+// any_active) -> actions int64 [n]; paired_update(active, step_status, new_done, reward0,
+// nagari, final_reward0, final_nagari, bad, any_active, steps): the bookkeeping of a
+// resident paired-evaluation step (cugo_paired_select / cugo_paired_update).
+namespace {
+void check_n(const torch::Tensor& t, int64_t n, at::ScalarType dt, const char* name) {
+  TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.numel() == n && t.scalar_type() == dt,
+              name, " must be a contiguous CUDA ", c10::toString(dt), " tensor of ", n,
+              " elements");
+}
+}  // namespace
+
+torch::Tensor paired_select(torch::Tensor active, torch::Tensor status, torch::Tensor done,
+                            torch::Tensor any_legal, torch::Tensor player, torch::Tensor a_seat,
+                            torch::Tensor act_a, torch::Tensor act_b, torch::Tensor bad,
+                            torch::Tensor any_active) {
+  const int64_t n = active.numel();
+  check_n(active, n, at::kBool, "active");
+  check_n(status, n, at::kShort, "status");
+  check_n(done, n, at::kBool, "done");
+  check_n(any_legal, n, at::kBool, "any_legal");
+  check_n(player, n, at::kByte, "player");
+  check_n(a_seat, n, at::kLong, "a_seat");
+  check_n(act_a, n, at::kLong, "act_a");
+  check_n(act_b, n, at::kLong, "act_b");
+  check_n(bad, 3, at::kLong, "bad");
+  check_n(any_active, 1, at::kInt, "any_active");
+  for (const auto* t : {&status, &done, &any_legal, &player, &a_seat, &act_a, &act_b, &bad,
+                        &any_active})
+    check_same_device(active, *t, "active", "an input");
+  const DeviceGuard guard(active.device());
+  auto actions = torch::empty({n}, on(active, at::kLong));
+  check_call(cugo_paired_select(u8p(active), status.data_ptr<int16_t>(), u8p(done), u8p(any_legal),
+                                u8p(player), a_seat.data_ptr<int64_t>(), act_a.data_ptr<int64_t>(),
+                                act_b.data_ptr<int64_t>(), n, actions.data_ptr<int64_t>(),
+                                bad.data_ptr<int64_t>(), any_active.data_ptr<int32_t>(), stream()),
+             "paired_select");
+  return actions;
+}
+
+void paired_update(torch::Tensor active, torch::Tensor step_status, torch::Tensor new_done,
+                   torch::Tensor reward0, torch::Tensor nagari, torch::Tensor final_reward0,
+                   torch::Tensor final_nagari, torch::Tensor bad, torch::Tensor any_active,
+                   torch::Tensor steps) {
+  const int64_t n = active.numel();
+  check_n(active, n, at::kBool, "active");
+  check_n(step_status, n, at::kShort, "step_status");
+  check_n(new_done, n, at::kBool, "new_done");
+  check_n(reward0, n, at::kFloat, "reward0");
+  check_n(nagari, n, at::kBool, "nagari");
+  check_n(final_reward0, n, at::kFloat, "final_reward0");
+  check_n(final_nagari, n, at::kBool, "final_nagari");
+  check_n(bad, 3, at::kLong, "bad");
+  check_n(any_active, 1, at::kInt, "any_active");
+  check_n(steps, 1, at::kLong, "steps");
+  for (const auto* t : {&step_status, &new_done, &reward0, &nagari, &final_reward0,
+                        &final_nagari, &bad, &any_active, &steps})
+    check_same_device(active, *t, "active", "an input");
+  const DeviceGuard guard(active.device());
+  check_call(cugo_paired_update(u8p(active), step_status.data_ptr<int16_t>(), u8p(new_done),
+                                reward0.data_ptr<float>(), u8p(nagari), n,
+                                final_reward0.data_ptr<float>(), u8p(final_nagari),
+                                bad.data_ptr<int64_t>(), any_active.data_ptr<int32_t>(),
+                                steps.data_ptr<int64_t>(), stream()),
+             "paired_update");
+}
+
 // masked_argmax(logits [n, A] f32/bf16, legal bool [n, A]) -> int64 [n]: the greedy
 // action of python/cugo_eval50.py:125-127 (argmax of logits.float() masked with -1e30).
 torch::Tensor masked_argmax(torch::Tensor logits, torch::Tensor legal) {
@@ -1418,6 +1485,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
       .def("advance", &SelfPlayState::advance)
       .def("set_noise_epoch", &SelfPlayState::set_noise_epoch)
       .def("set_event_pos", &SelfPlayState::set_event_pos);
+  m.def("paired_select", &paired_select,
+        "paired evaluation: observe checks and each game's action from its mover's model");
+  m.def("paired_update", &paired_update,
+        "paired evaluation: step checks, final rewards and the active mask after a step");
   m.def("masked_argmax", &masked_argmax, "Greedy action: argmax of the legal logits");
   m.def("mlp_pack_weight", &mlp_pack_weight,
         "bf16 matrix in the actor kernel's MFMA operand order", pybind11::arg("w"),

@@ -128,22 +128,19 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         model_a = _half_linears(model_a)
         model_b = model_a if same else _half_linears(model_b)
 
+    any_active = torch.zeros(1, dtype=torch.int32, device=dev)  # set in a step, counted after
+
     def step() -> None:
+        # the checks, the count and the per-game choice of model are one launch before the
+        # step and one after it (paired_select / paired_update, selfplay.hip)
         features, legal, players, done, status = ext.observe(states)
-        fine = status == ok
-        bad[0] += (active & ~fine).sum()
-        bad[1] += (active & fine & (done | ~legal.any(1))).sum()
-        steps_dev.add_(active.any().long())
-        a_moves = players.long() == a_seat
-        actions = torch.where(a_moves, _actions(ext, model_a, features, legal, use_amp, sample_a),
-                              _actions(ext, model_b, features, legal, use_amp, sample_b))
+        act_a = _actions(ext, model_a, features, legal, use_amp, sample_a)
+        act_b = _actions(ext, model_b, features, legal, use_amp, sample_b)
+        actions = ext.paired_select(active, status, done, legal.any(1), players, a_seat, act_a,
+                                    act_b, bad, any_active)
         reward0, new_done, nagari, step_status, _ = ext.step(states, actions)
-        step_ok = step_status == ok
-        bad[2] += (active & ~step_ok).sum()
-        ended = active & step_ok & new_done
-        final_reward0.copy_(torch.where(ended, reward0, final_reward0))
-        final_nagari.logical_or_(ended & nagari)
-        active.logical_and_(step_ok & ~new_done)
+        ext.paired_update(active, step_status, new_done, reward0, nagari, final_reward0,
+                          final_nagari, bad, any_active, steps_dev.view(1))
 
     replay = step
     flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
@@ -151,7 +148,7 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         if graph and not (sample_a or sample_b):
             # warm-up steps on a side stream (library handles, allocator blocks), then the
             # capture; the state they touched is put back
-            kept = [states, final_reward0, final_nagari, active, bad, steps_dev]
+            kept = [states, final_reward0, final_nagari, active, bad, steps_dev, any_active]
             saved = [t.clone() for t in kept]
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
