@@ -627,7 +627,31 @@ def selfplay_workload(ext, torch, wave: int = 4096, waves: int = 3) -> dict:
         sp.step()
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t1) / reps * 1e3
+    # the step's largest linear launch on its own: linear1 + GELU over the paired pass's
+    # 3 w rows (events of both seats and the queries), HIP events around 20 launches
+    from cugo_amd.seq_decode import linear, packed_weight
+
+    lin = policy.encoder.layers[0].linear1
+    h = torch.randn(3 * wave, lin.in_features, device=dev).to(torch.bfloat16)
+    packed_weight(lin.weight)
+    linear(h, lin.weight, lin.bias, gelu=True)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with region("f1.linear"):
+        e0.record(stream)
+        for _ in range(20):
+            linear(h, lin.weight, lin.bias, gelu=True)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    lin_us = e0.elapsed_time(e1) * 1e3 / 20
+    m, k, nn_ = 3 * wave, lin.in_features, lin.out_features
+    lin_bytes = 2 * (m * k + nn_ * k + m * nn_) + 2 * nn_
     return {"games_per_s": round(wave * waves / wall, 1),
+            "linear_roofline": {"kernel": f"linear_kernel (linear1 + GELU, {m} x {nn_} x {k} bf16)",
+                                "bound": "hbm", "achieved": round(lin_bytes / lin_us / 1e3, 1),
+                                "peak": 8000.0, "unit": "GB/s",
+                                "frac": round(lin_bytes / lin_us / 1e3 / 8000.0, 4),
+                                "us_per_launch": round(lin_us, 2), "traffic": None},
             "steps_per_wave": round(steps / waves, 2),
             "decision_steps_per_s": round(wave * steps / wall, 1),
             "tokens_per_s": round(3 * wave * steps / wall, 1),

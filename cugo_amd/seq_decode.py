@@ -200,7 +200,8 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
 
 
 def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a: torch.Tensor,
-                     pos_b: torch.Tensor, rows_b: torch.Tensor) -> torch.Tensor:
+                     pos_b: torch.Tensor, rows_b: torch.Tensor,
+                     final_norm: nn.Module | None = None):
     """cached_step for two groups of tokens at once: rows [0, split) of x (group a, one
     token for each of the cache rows 0 .. split - 1, written at slot pos_a[r]) and rows
     [split, n) (group b, one token for cache row rows_b[j], at slot pos_b[j]).  At every
@@ -208,7 +209,8 @@ def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a
     it would see had a been through every layer first (cached_step(a), then
     cached_step(b)); a reads no slot of b (a token reads the slots below its own, and b
     writes at or above a's).  The linear layers run once over both groups.  Positions past
-    the last slot are taken as the last slot.  Returns the final hidden states [n, d]."""
+    the last slot are taken as the last slot.  Returns the final hidden states [n, d], and
+    with `final_norm` also final_norm of them (in the last layer's launch)."""
     n, d = x.shape
     heads = cache.heads
     dh = d // heads
@@ -232,6 +234,8 @@ def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a
         if i + 1 < len(layers):
             x, h = linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x,
                                    layers[i + 1].norm1)
+        elif final_norm is not None:
+            return linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x, final_norm)
         else:
             x = linear(u, layer.linear2.weight, layer.linear2.bias, residual=x)
     return x

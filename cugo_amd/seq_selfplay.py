@@ -159,11 +159,12 @@ class SeqPolicy(nn.Module):
         # + token_type[2] rounded after the layer's own rounding, as torch adds the two
         return linear(h, second.weight, second.bias, residual=self.token_type[2], out=out)
 
-    def readout(self, h: torch.Tensor) -> torch.Tensor:
+    def readout(self, h: torch.Tensor, normed: torch.Tensor | None = None) -> torch.Tensor:
         """cugo_seq50.py:187-189 and :288-289: head(norm(h)), the norm as one HIP launch
-        and the head's first Linear with its GELU as another where they fit."""
+        (or `normed`, norm(h) already computed) and the head's first Linear with its GELU
+        as another where they fit."""
         if h.dim() == 2 and is_exact_gelu(self.head[1]):
-            _, z = add_norm(h, None, self.norm)
+            z = add_norm(h, None, self.norm)[1] if normed is None else normed
             out = self.head[2](linear(z, self.head[0].weight, self.head[0].bias, gelu=True))
         else:
             out = self.head(self.norm(h))
@@ -333,9 +334,9 @@ class SelfPlayWave:
         # the last step's event tokens (both seats' rows) and this step's queries through
         # the layers together; the queries attend the events' new keys at every layer
         actor.query_from_input(q_in, out=self.pair[2 * w:])
-        hidden = cached_step_pair(actor, self.cache, self.pair, 2 * w, self.event_pos,
-                                  query_pos, query_rows)
-        logits = actor.readout(hidden[2 * w:])
+        hidden, normed = cached_step_pair(actor, self.cache, self.pair, 2 * w, self.event_pos,
+                                          query_pos, query_rows, final_norm=actor.norm)
+        logits = actor.readout(hidden[2 * w:], normed[2 * w:])
         if pool:
             p, opp = self.p, self.opponent
             theirs = opp.readout(opp.cached_step(self.opp_cache, opp.query_from_input(q_in[:p])))
