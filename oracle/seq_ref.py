@@ -16,9 +16,12 @@ uses:
   those vectors with the reference's bf16 roundings: the Linear in float64, rounded to
   the weight dtype, then + position, rounded, then + token_type, rounded.
 * `reference_cached_step` - SeqNet.cached_step (cugo_seq50.py:291-322): index_put_ of the
-  new key/value, then the matmul decode path (oracle.decode_ref.matmul_path).
+  new key/value, then the matmul decode path (oracle.decode_ref.matmul_path).  Pinned by
+  the fact that incremental decoding must equal the full causal forward of the same
+  prefix (tests/test_cpu_seq_step_pins.py, float64, ragged rows, the slot clamp).
 * `gumbel_reference` - the sampling lines of WaveCollector._step
-  (cugo_seq_selfplay50.py:125-130) on supplied uniforms, in torch.
+  (cugo_seq_selfplay50.py:125-130) on supplied uniforms, in torch.  Pinned by closed
+  forms and sampled frequencies (same test file).
 """
 
 from __future__ import annotations
@@ -100,14 +103,21 @@ def token_reference(tokens: np.ndarray, weight, bias, position_row, token_type_r
     return (r2.to(torch.float64) + token_type_row.to(torch.float64)).to(dt)
 
 
-def reference_cached_step(model, cache, x, rows):
-    """cugo_seq50.py:291-322 restated with the matmul decode path."""
+def reference_cached_step(model, cache, x, rows=None, slots=None):
+    """cugo_seq50.py:291-322 restated with the matmul decode path: token i goes to cache
+    row rows[i] (default: row i) at slot min(length[row], t - 1), t = min(slots,
+    cache.slots), and attends slots 0..that slot; returns the last layer's residual
+    stream [n, d].  Pinned in tests/test_cpu_seq_step_pins.py against the full causal
+    forward of nn.TransformerEncoder."""
     import torch
     import torch.nn.functional as F
 
     n, d = x.shape
     heads, dh = cache.heads, d // cache.heads
-    pos = cache.length.index_select(0, rows).clamp_max(cache.slots - 1)
+    t = cache.slots if slots is None else min(slots, cache.slots)
+    if rows is None:
+        rows = torch.arange(n, device=x.device)
+    pos = cache.length.index_select(0, rows).clamp_max(t - 1)
     head_ids = torch.arange(heads, device=x.device).view(1, heads)
     flat_rows = (rows.view(n, 1) * heads + head_ids).flatten()
     flat_pos = pos.repeat_interleave(heads)
@@ -127,7 +137,9 @@ def reference_cached_step(model, cache, x, rows):
 
 def gumbel_reference(logits, legal, uniforms):
     """cugo_seq_selfplay50.py:125-130 with `torch.rand_like(masked)` replaced by the
-    supplied uniforms: (actions, logp)."""
+    supplied uniforms: (actions, logp).  Pinned in tests/test_cpu_seq_step_pins.py by
+    closed forms (one legal action, k equal logits, a dominant draw) and by the action
+    frequencies of many draws against the legal softmax."""
     import torch
 
     masked = logits.masked_fill(~legal, -1.0e30)

@@ -15,6 +15,7 @@ import torch
 
 from cugo_amd.cugo_seq_attention50 import decode_attention, decode_attention_append
 from oracle.decode_ref import brute_force, matmul_path
+from oracle.seq_ref import reference_cached_step
 from tests.conftest import announce
 
 pytestmark = pytest.mark.gpu
@@ -213,27 +214,6 @@ def _layered_model(layers=4, d=256, heads=8, seed=0):
     return model.to(DEV).to(torch.bfloat16).eval()
 
 
-def _reference_cached_step(model, cache, x, rows):
-    """python/cugo_seq50.py:291-322 restated with the matmul decode path."""
-    import torch.nn.functional as F
-
-    n, d = x.shape
-    heads, dh = cache.heads, d // cache.heads
-    pos = cache.length.index_select(0, rows).clamp_max(cache.slots - 1)
-    flat_rows = (rows.view(n, 1) * heads + torch.arange(heads, device=DEV).view(1, heads)).flatten()
-    flat_pos = pos.repeat_interleave(heads)
-    for i, layer in enumerate(model.encoder.layers):
-        attn = layer.self_attn
-        q, k, v = F.linear(layer.norm1(x), attn.in_proj_weight, attn.in_proj_bias).chunk(3, -1)
-        kc, vc = cache.k[i], cache.v[i]
-        kc.view(-1, cache.slots, dh).index_put_((flat_rows, flat_pos), k.reshape(n * heads, dh).to(kc.dtype))
-        vc.view(-1, cache.slots, dh).index_put_((flat_rows, flat_pos), v.reshape(n * heads, dh).to(vc.dtype))
-        a = matmul_path(q.reshape(n, heads, dh), kc, vc, pos, rows)
-        x = x + attn.out_proj(a.reshape(n, d))
-        x = x + layer.linear2(layer.activation(layer.linear1(layer.norm2(x))))
-    return x
-
-
 def test_cached_step_matches_reference_and_replays_in_a_graph(ext):
     """Four steps of the 4-layer d256 policy decode through the fused HIP step and the
     reference formulation; then the fused step captured in a HIP graph and replayed."""
@@ -250,7 +230,7 @@ def test_cached_step_matches_reference_and_replays_in_a_graph(ext):
             rows = torch.randperm(rows_n, generator=g)[:n].to(DEV)
             x = (torch.randn(n, 256, generator=g) * 0.5).to(torch.bfloat16).to(DEV)
             ha = cached_step(model, ca, x, rows=rows)
-            hb = _reference_cached_step(model, cb, x, rows)
+            hb = reference_cached_step(model, cb, x, rows)
             assert rel_err(ha, hb.float()) <= 1e-2, step
             ca.length.index_add_(0, rows, torch.ones_like(rows))
             cb.length.index_add_(0, rows, torch.ones_like(rows))
@@ -305,7 +285,6 @@ def test_cached_step_full_cache_with_game_lengths(ext, lengths):
     states within 1e-2 relative, and the appended key/value slots within 1e-2."""
     from bench import decode_lengths
     from cugo_amd.seq_decode import KVCache, cached_step
-    from oracle.seq_ref import reference_cached_step
 
     announce(f"cached_step full cache [4, 4096, 8, 320, 32], {lengths} lengths")
     rows, slots, per_row = 4096, 320, 24
