@@ -757,6 +757,26 @@ def engine_traffic(batch: int, fused: bool) -> int | None:
     return sum(parts[:-1]) + parts[-1] // 32
 
 
+ROLLOUT_BASE = SEED_BASE + 0xC4  # the MLP rollout's deal seeds
+
+
+def make_rollout(ext, torch, batch: int = 32768, horizon: int = 128):
+    """The MLP rollout the `rollout` leg times: the residual MLP actor (720 -> 512, three
+    blocks, bf16, N(0, 0.02) weights from seed 0), B games dealt from ROLLOUT_BASE + i, the
+    sampler's Philox key drawn from a generator seeded 1."""
+    from cugo_amd.rollout import MlpRollout, ResidualMlpActor
+
+    dev = torch.device("cuda")
+    torch.manual_seed(0)
+    actor = ResidualMlpActor()
+    with torch.no_grad():
+        for prm in actor.parameters():
+            prm.normal_(0.0, 0.02)
+    actor = actor.to(dev).to(torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(1)
+    return MlpRollout(ext, actor, batch, horizon, ROLLOUT_BASE, generator=gen)
+
+
 def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict:
     """MLP PPO self-play rollout (cugo_amd/rollout.py): B games, a residual MLP actor
     (720 features -> Linear 512 -> 3 blocks of h + Linear(ReLU(Linear(LayerNorm(h)))) ->
@@ -770,18 +790,11 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
     written once, the action, the step outputs and the bf16 observation, 2,136 B a row)
     over its time against HBM.  The rollout runs as one HIP graph per horizon; the shares
     come from graphs of the engine's and the actor's launches alone."""
-    from cugo_amd.rollout import (MlpRollout, ResidualMlpActor, fused_forward, mlp_forward,
-                                  pack_actor)
+    from cugo_amd.rollout import fused_forward, mlp_forward, pack_actor
 
     dev = torch.device("cuda")
-    torch.manual_seed(0)
-    actor = ResidualMlpActor()
-    with torch.no_grad():
-        for prm in actor.parameters():
-            prm.normal_(0.0, 0.02)
-    actor = actor.to(dev).to(torch.bfloat16).eval()
-    gen = torch.Generator(device=dev).manual_seed(1)
-    ro = MlpRollout(ext, actor, batch, horizon, SEED_BASE + 0xC4, generator=gen)
+    ro = make_rollout(ext, torch, batch, horizon)
+    actor = ro.actor
     stream = torch.cuda.current_stream()
 
     def graph_ms(g, reps: int, name: str) -> float:
@@ -822,10 +835,10 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
         feats = torch.empty((batch, 720), dtype=torch.bfloat16, device=dev)
         legal = ext.observe_bf16(st, feats)[1]
         acts = []
-        ext.refill_spares(sp, sg, g2, SEED_BASE + 0xC4)
+        ext.refill_spares(sp, sg, g2, ROLLOUT_BASE)
         for _ in range(32):
             acts.append(ext.sample_uniform(legal, smp))
-            legal = ext.step_observe_spares(st, acts[-1], SEED_BASE + 0xC4, g2, smp, sp, sg,
+            legal = ext.step_observe_spares(st, acts[-1], ROLLOUT_BASE, g2, smp, sp, sg,
                                             feats)[6]
 
         def engine_block(engine: bool):
@@ -833,12 +846,12 @@ def rollout_workload(ext, torch, batch: int = 32768, horizon: int = 128) -> dict
                 dst.copy_(src)
             if not engine:
                 return
-            ext.refill_spares(sp, sg, g2, SEED_BASE + 0xC4)
+            ext.refill_spares(sp, sg, g2, ROLLOUT_BASE)
             for k in range(32):
                 if ro.fused_kernel:
-                    ext.step_observe_spares(st, acts[k], SEED_BASE + 0xC4, g2, smp, sp, sg, feats)
+                    ext.step_observe_spares(st, acts[k], ROLLOUT_BASE, g2, smp, sp, sg, feats)
                 else:
-                    ext.step_reset_spares(st, acts[k], SEED_BASE + 0xC4, g2, smp, sp, sg)
+                    ext.step_reset_spares(st, acts[k], ROLLOUT_BASE, g2, smp, sp, sg)
                     ext.observe(st)
 
         def block_ms(engine: bool, name: str) -> float:

@@ -566,6 +566,31 @@ __global__ __launch_bounds__(256) void paired_update_kernel(
   active[i] = ok && new_done[i] == 0;
 }
 
+// The event log of a paired evaluation of sequence policies (History.record,
+// cugo_seq50.py:62-67, called at cugo_eval50.py:258-263), kept as each policy's cache
+// length: after the engine step and the event tokens (which read the old count), before
+// paired_update clears the active flags.  Every game's event token went to slot
+// length_m[i] of policy m's cache row i (event_pos_m records it for the next step's pass);
+// an active game whose step is OK and committed keeps it: count[i] and every length_m[i]
+// advance.  One thread per game.
+__global__ __launch_bounds__(256) void paired_events_kernel(
+    const uint8_t* active, const int16_t* step_status, const uint8_t* committed, i64 n,
+    i64* count, i64* length_a, i64* event_pos_a, i64* length_b, i64* event_pos_b) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const i64 la = length_a[i];
+  event_pos_a[i] = la;
+  i64 lb = 0;
+  if (length_b != nullptr) {
+    lb = length_b[i];
+    event_pos_b[i] = lb;
+  }
+  if (active[i] == 0 || step_status[i] != 0 || committed[i] == 0) return;
+  count[i] += 1;
+  length_a[i] = la + 1;
+  if (length_b != nullptr) length_b[i] = lb + 1;
+}
+
 // Pre-norm transformer residual step (nn.TransformerEncoderLayer with norm_first,
 // python/cugo_seq50.py:318-322): x_out = x + y rounded to the dtype (y == nullptr: x_out is
 // not written and x is normalised as is), then ln = LayerNorm(x_out) with fp32 mean and
@@ -863,6 +888,20 @@ int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_
   paired_update_kernel<<<(unsigned)((n + 255) / 256 > 0 ? (n + 255) / 256 : 1), 256, 0, stream>>>(
       active, step_status, new_done, reward0, nagari, n, final_reward0, final_nagari, bad,
       any_active, steps);
+  return (int)hipGetLastError();
+}
+
+int cugo_paired_events(const uint8_t* active, const int16_t* step_status,
+                       const uint8_t* committed, int64_t n, int64_t* count, int64_t* length_a,
+                       int64_t* event_pos_a, int64_t* length_b, int64_t* event_pos_b,
+                       hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!active || !step_status || !committed || !count || !length_a ||
+                          !event_pos_a)) ||
+      (length_b == nullptr) != (event_pos_b == nullptr))
+    return -1;
+  if (n == 0) return 0;
+  paired_events_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+      active, step_status, committed, n, count, length_a, event_pos_a, length_b, event_pos_b);
   return (int)hipGetLastError();
 }
 

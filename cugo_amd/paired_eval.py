@@ -4,12 +4,25 @@ Every deal is played twice, model A on seat 0 in game i and on seat 1 in game pa
 so deal luck cancels in the pair score.  A decision step observes the games, evaluates
 each model, takes for every game the greedy action of the model whose seat moves (the
 `masked_argmax` kernel: argmax of the fp32 logits with illegal actions at -1e30) or a
-sample from its softmax, and steps the engine; finished games stay resident, masked.  Summary fields and
-their meaning are the reference's `EvalSummary` (cugo_eval50.py:27-61).
+sample from its softmax, and steps the engine; finished games stay resident, masked.
+Summary fields and their meaning are the reference's `EvalSummary`
+(cugo_eval50.py:27-61).
 
-Policies are modules mapping the [n, 720] features to logits (or a tuple whose first
-item is the logits), like the reference's PpoActor; sequence policies with event
-histories are not handled here.
+Two kinds of policy, as in the reference (`policy_logits`, cugo_seq50.py:347-365):
+
+* features-only modules mapping the [n, 720] features to logits (or a tuple whose first
+  item is the logits), like the reference's PpoActor, under fp16 autocast with use_amp;
+* sequence policies (`uses_history`, cugo_amd.seq_selfplay.SeqPolicy, into which a
+  reference SeqNet state_dict loads), run in bf16 with use_amp as the reference does
+  (cugo_eval50.py:120-121).  The reference builds a History of every game's opening and
+  committed events (cugo_eval50.py:169, :258-263) and runs the dense forward over
+  [opening, events, query] for each mover (`SeqNet.forward`, cugo_seq50.py:208-224).  Here
+  each sequence policy keeps one KV-cache row per game, for the seat it plays there: the
+  opening token at slot 0, one event token per committed event of either seat (its own
+  view of it), and each step a query token in the slot after them.  A step's event
+  tokens go through the layers with the next step's queries, in one pass
+  (`cached_step_pair`), as the sequence self-play does; incremental decoding computes
+  what the dense forward computes at the query.
 """
 
 from __future__ import annotations
@@ -21,7 +34,7 @@ from dataclasses import dataclass
 import torch
 from torch import nn
 
-from .seq_selfplay import make_seeds
+from .seq_selfplay import MAX_EVENTS, make_seeds
 
 
 @dataclass
@@ -61,15 +74,83 @@ class EvalSummary:
         return self.games / self.seconds
 
 
-def _actions(ext, model: nn.Module, features, legal, use_amp: bool, sample: bool):
-    """cugo_eval50.py:112-127 for a features-only policy."""
-    with torch.autocast(device_type="cuda", dtype=torch.float16, enabled=use_amp):
-        out = model(features)
-    logits = (out[0] if isinstance(out, tuple) else out).float().contiguous()
+def _choose(ext, logits: torch.Tensor, legal: torch.Tensor, sample: bool) -> torch.Tensor:
+    """The greedy action (argmax of the legal logits as float32) or a softmax sample
+    (cugo_eval50.py:124-127)."""
     if sample:
-        masked = logits.masked_fill(~legal, -1.0e30)
+        masked = logits.float().masked_fill(~legal, -1.0e30)
         return torch.multinomial(torch.softmax(masked, dim=1), 1).squeeze(1)
-    return ext.masked_argmax(logits, legal)
+    return ext.masked_argmax(logits.contiguous(), legal)
+
+
+class _SequenceSeat:
+    """A sequence policy's part of the resident games: one KV-cache row per game for the
+    seat the policy plays in it (`seat`), the rows of the step's pass (the last step's
+    event tokens in [0, games), this step's queries in [games, 2 games)), the slots the
+    waiting event tokens go to, and the query input rows (features ++ legal in the policy
+    dtype, zero-padded to a width `linear` takes)."""
+
+    def __init__(self, model: nn.Module, seat: torch.Tensor, games: int, dev) -> None:
+        from .seq_selfplay import ACTIONS, FEATURES, policy_cache
+
+        for name in ("query_from_input", "event_token", "start_token", "readout", "prepare"):
+            if not hasattr(model, name):
+                raise TypeError("a sequence policy must be a cugo_amd.seq_selfplay.SeqPolicy "
+                                "(a reference SeqNet state_dict loads into one)")
+        self.model, self.seat, self.games = model, seat, games
+        dtype = model.event_in.weight.dtype
+        d = model.position.shape[1]
+        self.cache = policy_cache(model, games, dev)
+        self.pair = torch.zeros((2 * games, d), dtype=dtype, device=dev)
+        self.event_pos = torch.ones(games, dtype=torch.int64, device=dev)
+        cols = model.kept_columns()
+        self.columns = None if cols is None else torch.tensor(cols, device=dev)
+        self.width = FEATURES if cols is None else len(cols)
+        need = self.width + ACTIONS
+        stride = next((k for k in (64, 128, 256, 512, 1024) if k >= need), need)
+        self.q_in = torch.zeros((games, stride), dtype=dtype, device=dev)
+        self.ids = torch.arange(games, device=dev)
+        model.prepare()
+
+    def open(self, start: torch.Tensor) -> None:
+        """Every game's opening token (cugo_seq50.py:271-274, seen from `seat`) into slot 0;
+        no event waits (the first pass writes zeros into the queries' own slots)."""
+        m, cache = self.model, self.cache
+        cache.length.zero_()
+        m.cached_step(cache, m.start_token(start, self.seat), 1)
+        cache.length.fill_(1)
+        self.event_pos.fill_(1)
+        self.pair[:self.games].zero_()
+
+    def logits(self, features: torch.Tensor, legal: torch.Tensor) -> torch.Tensor:
+        """The last step's event tokens and every game's query through the layers together
+        (the queries attend the events' keys at every layer), then the readout of the
+        queries: [games, 179] logits in the policy dtype."""
+        from .seq_decode import cached_step_pair
+
+        m, g = self.model, self.games
+        kept = features if self.columns is None else features.index_select(1, self.columns)
+        self.q_in[:, :self.width].copy_(kept)
+        self.q_in[:, self.width:self.width + legal.shape[1]].copy_(legal)
+        m.query_from_input(self.q_in, out=self.pair[g:])
+        hidden, normed = cached_step_pair(m, self.cache, self.pair, g, self.event_pos,
+                                          self.cache.length, self.ids, final_norm=m.norm)
+        return m.readout(hidden[g:], normed[g:])
+
+    def events(self, events: torch.Tensor, count: torch.Tensor) -> None:
+        """This step's event tokens, each game's from `seat`'s view at position 1 + count
+        (cugo_seq50.py:276-282), waiting for the next step's pass."""
+        self.model.event_token(events, self.seat, count, out=self.pair[:self.games])
+
+
+def _bf16_twin(model: nn.Module) -> nn.Module:
+    """The policy in bf16: fp16 autocast is not used for sequence models, which run in
+    bf16 (cugo_eval50.py:120-121); parameters that are bf16 already are kept as they are."""
+    import copy
+
+    if next(model.parameters()).dtype == torch.bfloat16:
+        return model
+    return copy.deepcopy(model).to(torch.bfloat16).eval()
 
 
 def _half_linears(model: nn.Module) -> nn.Module:
@@ -97,14 +178,18 @@ def _mean(x: torch.Tensor) -> float:
 
 def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, seed_offset: int,
                     max_steps: int, use_amp: bool, sample_a: bool = False,
-                    sample_b: bool = False, graph: bool = True) -> EvalSummary:
+                    sample_b: bool = False, graph: bool = True,
+                    trace: list | None = None) -> EvalSummary:
     """cugo_eval50.py:137-361 on resident games: every step observes all 2 pairs games,
     evaluates both models on every row, keeps model A's action where A's seat moves and
     B's elsewhere, and steps every game; rows of games that are over are masked out of
     the outcome and the checks (the reference drops them instead, which needs the count of
     survivors on the host every step).  The per-row decisions are the reference's; the
     step is one HIP-graph replay (greedy policies; `graph=False` or sampling: eager), and
-    the host reads whether games are left one step behind, so the GPU never waits."""
+    the host reads whether games are left one step behind, so the GPU never waits.
+    Either model may be a sequence policy (`uses_history`, a SeqPolicy).  `trace`, when
+    given, receives one dict a decision step: copies of every game's chosen action and
+    of both models' logits ("actions", "logits_a", "logits_b")."""
     if pairs <= 0:
         raise ValueError("pairs must be positive")
     if max_steps <= 0:
@@ -123,22 +208,55 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
     ok = int(ext.STATUS_OK)
     model_a.eval()
     model_b.eval()
+    same = model_b is model_a
+    seq = [bool(getattr(m, "uses_history", False)) for m in (model_a, model_b)]
     if use_amp:
-        same = model_b is model_a
-        model_a = _half_linears(model_a)
-        model_b = model_a if same else _half_linears(model_b)
+        # features-only policies: the Linear weights cast to fp16 once; sequence
+        # policies: bf16 (cugo_eval50.py:120-121)
+        model_a = _bf16_twin(model_a) if seq[0] else _half_linears(model_a)
+        model_b = model_a if same else (_bf16_twin(model_b) if seq[1] else
+                                        _half_linears(model_b))
+    # Sequence policies keep their event histories as KV caches, one row per game for the
+    # seat they play (A: a_seat, B: the other); both models may be one module.
+    ids = torch.arange(games, device=dev)
+    seq_seats = [(_SequenceSeat(m, a_seat if k == 0 else 1 - a_seat, games, dev)
+                  if seq[k] else None) for k, m in enumerate((model_a, model_b))]
+    histories = [s for s in seq_seats if s is not None]
+    count = torch.zeros(games, dtype=torch.int64, device=dev)  # committed events per game
+    start = ext.start(states) if histories else None  # the openings (History, cugo_seq50.py:56)
 
     any_active = torch.zeros(1, dtype=torch.int32, device=dev)  # set in a step, counted after
+
+    last: dict[str, torch.Tensor] = {}  # the latest step's outputs, for `trace`
+
+    def logits_actions(k: int, model, features, legal, sample: bool):
+        if seq_seats[k] is not None:
+            logits = seq_seats[k].logits(features, legal)
+        else:
+            with torch.autocast(device_type="cuda", dtype=torch.float16, enabled=use_amp):
+                out = model(features)
+            logits = (out[0] if isinstance(out, tuple) else out).float()
+        last[("logits_a", "logits_b")[k]] = logits
+        return _choose(ext, logits, legal, sample)
 
     def step() -> None:
         # the checks, the count and the per-game choice of model are one launch before the
         # step and one after it (paired_select / paired_update, selfplay.hip)
         features, legal, players, done, status = ext.observe(states)
-        act_a = _actions(ext, model_a, features, legal, use_amp, sample_a)
-        act_b = _actions(ext, model_b, features, legal, use_amp, sample_b)
+        act_a = logits_actions(0, model_a, features, legal, sample_a)
+        act_b = logits_actions(1, model_b, features, legal, sample_b)
         actions = ext.paired_select(active, status, done, legal.any(1), players, a_seat, act_a,
                                     act_b, bad, any_active)
-        reward0, new_done, nagari, step_status, _ = ext.step(states, actions)
+        last["actions"] = actions
+        if histories:
+            reward0, new_done, nagari, step_status, committed, events = (
+                ext.step_events_indexed(states, ids, actions))
+            for h in histories:
+                h.events(events, count)
+            lengths = [x for h in histories for x in (h.cache.length, h.event_pos)]
+            ext.paired_events(active, step_status, committed, count, *lengths)
+        else:
+            reward0, new_done, nagari, step_status, _ = ext.step(states, actions)
         ext.paired_update(active, step_status, new_done, reward0, nagari, final_reward0,
                           final_nagari, bad, any_active, steps_dev.view(1))
 
@@ -148,7 +266,10 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         if graph and not (sample_a or sample_b):
             # warm-up steps on a side stream (library handles, allocator blocks), then the
             # capture; the state they touched is put back
-            kept = [states, final_reward0, final_nagari, active, bad, steps_dev, any_active]
+            kept = [states, final_reward0, final_nagari, active, bad, steps_dev, any_active,
+                    count]
+            for h in histories:
+                kept += [h.cache.length, h.event_pos, h.pair]
             saved = [t.clone() for t in kept]
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
@@ -172,11 +293,15 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         bad[0] += (~done & ~fine).sum()
         bad[1] += (~done & fine & ~any_legal).sum()
         active.copy_(~done & fine & any_legal)
+        for h in histories:
+            h.open(start)
         stream = torch.cuda.current_stream()
         finished_all = False
         behind = None  # (event, flag slot) of the step before the latest
         for k in range(max_steps):
             replay()
+            if trace is not None:
+                trace.append({name: t.clone() for name, t in last.items()})
             flags[k & 1].copy_(active.any(), non_blocking=True)
             queued = (torch.cuda.Event(), k & 1)
             queued[0].record(stream)
@@ -201,6 +326,8 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         raise RuntimeError(f"step failed on {step_bad} active visits")
     if not finished_all:
         raise RuntimeError(f"not all games finished within {max_steps} decision steps")
+    if histories and int(count.max()) > MAX_EVENTS:
+        raise RuntimeError(f"a game committed more than {MAX_EVENTS} events")
 
     score = torch.where(a_seat == 0, final_reward0, -final_reward0)  # A's points
     s0, s1 = score[:pairs], score[pairs:]

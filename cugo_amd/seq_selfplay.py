@@ -61,6 +61,8 @@ class SeqPolicy(nn.Module):
     and the readout head.  mode "hybrid": the query carries all 720 features; "events":
     only the CONTEXT_INDEX columns (cugo_seq50.py:143-150)."""
 
+    uses_history = True  # cugo_seq50.py:134: callers feed it event histories
+
     def __init__(self, mode: str = "hybrid", outputs: int = ACTIONS, d_model: int = 256,
                  layers: int = 4, heads: int = 8) -> None:
         super().__init__()

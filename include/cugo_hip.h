@@ -517,6 +517,18 @@ int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_
                        const float* reward0, const uint8_t* nagari, int64_t n,
                        float* final_reward0, uint8_t* final_nagari, int64_t* bad,
                        int32_t* any_active, int64_t* steps, hipStream_t stream);
+/* cugo_paired_events: the event log of a paired evaluation of sequence policies, which the
+ * reference keeps in a History (History.record, cugo_seq50.py:62-67, called at
+ * cugo_eval50.py:258-263; no counterpart as one call), as each policy's KV-cache lengths.
+ * After the engine step (step_events_indexed) and the event tokens, before
+ * cugo_paired_update: event_pos_a[i] = length_a[i] (and event_pos_b[i] = length_b[i]) for
+ * every game; a game that is active, whose step status is OK and whose action committed
+ * advances count[i], length_a[i] and length_b[i] by one.  length_b and event_pos_b are both
+ * NULL when one policy keeps a cache.  int64 arrays of n entries; bool arrays one byte. */
+int cugo_paired_events(const uint8_t* active, const int16_t* step_status,
+                       const uint8_t* committed, int64_t n, int64_t* count, int64_t* length_a,
+                       int64_t* event_pos_a, int64_t* length_b, int64_t* event_pos_b,
+                       hipStream_t stream);
 
 /* cugo_selfplay_advance: the step's work after the engine step (cugo_seq_selfplay50.py:
  * 146-163): bad += active & (step status != OK); games that finished now keep reward0 and

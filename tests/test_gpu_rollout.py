@@ -256,3 +256,94 @@ def test_rollout_graph_replay_equals_eager(ext):
             for name in ("features", "legal", "action", "logp", "value", "reward", "done"):
                 assert torch.equal(getattr(a.buffer, name), getattr(b.buffer, name)), name
     assert a.games_completed() > n
+
+
+def test_rollout_captured_horizons_match_oracle(ext, ref):
+    """C4 in the form bench.py times it (bench.make_rollout: B = 32,768, the 3 x 512 bf16
+    actor, a 128-step horizon captured once as a HIP graph and replayed, Philox uniforms
+    drawn in the sampler).  The capture's two eager warm-up steps and two replayed
+    horizons (refills at steps 0, 32, 64 and 96 of each; the epoch raised by each replay)
+    against the oracle stepping the recorded actions: every one of the 256 steps' bf16
+    features, mask, reward and done flag, the rows, generations and re-seeded sampler
+    words after each horizon, every action legal.  The sampler's draw is checked on a
+    1,024-row sample at steps 0, 31, 32, 95 and 127 of each horizon: the Philox uniforms
+    of (seed, epoch, step) from the oracle's Philox, the actor's logits on the recorded
+    features, and the oracle's Gumbel-max give the recorded action, value and
+    log-probability."""
+    from bench import ROLLOUT_BASE, make_rollout
+    from cugo_amd.rollout import mlp_forward
+    from oracle.philox_ref import gumbel_uniforms
+    from oracle.seq_ref import gumbel_reference
+
+    announce("MLP rollout: two captured 128-step horizons at 32,768 games vs oracle")
+    n, horizon, base = 32768, 128, ROLLOUT_BASE
+    ro = make_rollout(ext, torch, n, horizon)
+    assert ro.fused_kernel and ro.noise is None
+    idx = np.arange(n, dtype=np.uint64)
+    host = ref.create((np.uint64(base) + idx).view(np.int64), np.arange(n, dtype=np.int64) & 1)
+    assert np.array_equal(to_np(ro.states), host)
+    hgen = np.zeros(n, dtype=np.int64)
+
+    def oracle_step(actions: np.ndarray, label: str):
+        rout = ref.step(host, actions)
+        ended = np.nonzero(rout[1])[0]
+        hgen[ended] += 1
+        seeds = (np.uint64(base) + ended.astype(np.uint64)
+                 + np.uint64(n) * hgen[ended].astype(np.uint64)).view(np.int64)
+        host[ended] = ref.create(seeds, ended & 1)
+        return rout
+
+    def rows_match(label: str):
+        assert np.array_equal(to_np(ro.states), host), f"rows after {label}"
+        assert np.array_equal(to_np(ro.generation), hgen), f"generations after {label}"
+        done_rows = np.nonzero(hgen)[0][:256]
+        want = [splitmix_first(int(base + i + n * hgen[i]) & (2**64 - 1)) for i in done_rows]
+        assert np.array_equal(to_np(ro.sampler).view(np.uint64)[done_rows],
+                              np.array(want, np.uint64)), f"samplers after {label}"
+
+    buf = ro.buffer
+    with torch.no_grad():
+        ro.capture()  # records the horizon; its two eager warm-up steps run first
+        torch.cuda.synchronize()
+        for t in range(2):
+            oracle_step(to_np(buf.action[t]), f"warm-up step {t}")
+        rows_match("the warm-up steps")
+        sample_rows = np.sort(np.random.default_rng(41).choice(n, 1024, replace=False))
+        rows_dev = torch.from_numpy(sample_rows).to(DEV)
+        for epoch in (1, 2):
+            ro.replay()
+            torch.cuda.synchronize()
+            assert int(ro.epoch) == epoch
+            for t in range(horizon):
+                label = f"horizon {epoch}, step {t}"
+                if t % 32 == 0:
+                    print(f"  {label}", flush=True)
+                robs = ref.observe(host)
+                want = torch.from_numpy(robs[0]).to(torch.bfloat16).view(torch.int16)
+                assert torch.equal(buf.features[t].view(torch.int16).cpu(), want), \
+                    f"features, {label}"
+                legal = robs[1]
+                assert np.array_equal(to_np(buf.legal[t]), legal), f"legal, {label}"
+                a = to_np(buf.action[t])
+                live = ~robs[3]
+                assert legal[np.arange(n)[live], a[live]].all(), f"illegal action, {label}"
+                lp = to_np(buf.logp[t])
+                assert (lp[live] <= 1e-6).all() and np.isfinite(lp[live]).all(), label
+                if t in (0, 31, 32, 95, 127):
+                    x = buf.features[t].index_select(0, rows_dev).contiguous()
+                    logits, value = mlp_forward(ext, ro.packed, x)
+                    u = torch.from_numpy(gumbel_uniforms(ro.seed, epoch, t, sample_rows, 179))
+                    legal_s = buf.legal[t].index_select(0, rows_dev)
+                    act, logp = gumbel_reference(logits.float(), legal_s, u.to(DEV))
+                    assert torch.equal(act, buf.action[t].index_select(0, rows_dev)), \
+                        f"sampled actions, {label}"
+                    assert torch.allclose(logp, buf.logp[t].index_select(0, rows_dev),
+                                          atol=1e-5), f"log-probabilities, {label}"
+                    assert torch.equal(value, buf.value[t].index_select(0, rows_dev)), \
+                        f"values, {label}"
+                rout = oracle_step(a, label)
+                assert np.array_equal(to_np(buf.reward[t]).view(np.uint32),
+                                      rout[0].view(np.uint32)), f"reward, {label}"
+                assert np.array_equal(to_np(buf.done[t]), rout[1]), f"done, {label}"
+            rows_match(f"horizon {epoch}")
+    assert hgen.sum() > 4 * n  # about 13 games a row in 258 steps
