@@ -110,6 +110,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-selfplay", action="store_true")
     p.add_argument("--no-redeal", action="store_true")
     p.add_argument("--no-paired", action="store_true")
+    p.add_argument("--no-published", action="store_true",
+                   help="skip the reference's own two published-figure harnesses")
     p.add_argument("--streams", type=int, default=1,
                    help="slices of the batch stepped on their own streams")
     p.add_argument("--no-graph", action="store_true", help="issue the loop eagerly")
@@ -300,6 +302,35 @@ def mid_game_roots(ext, torch, n: int, base: int):
     return roots.index_select(0, live).contiguous(), player.long().index_select(0, live)
 
 
+# Host threads for the CPU baselines: one per core this process may run on, at most 16
+# (the host cores that go with one GPU on the MI355X boxes this runs on: each of a node's
+# GPUs has a 16-core share of the host, however many cores the OS reports).
+CPU_THREAD_CAP = 16
+
+
+def host_cores() -> dict:
+    """The host the CPU baselines run on: the OS's core count, the cores this process may
+    run on (its affinity), the CPU model, and the threads used (the affinity count, capped
+    at CPU_THREAD_CAP)."""
+    count = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = count
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    threads = max(1, min(affinity, CPU_THREAD_CAP))
+    return {"threads": threads, "os_cpu_count": count, "affinity_cores": affinity,
+            "cpu_model": model, "thread_cap": CPU_THREAD_CAP,
+            "cap_reason": "16 host cores go with each GPU of the node"}
+
+
 def branch_cpu_baseline(roots, parent, actions, seconds: float) -> dict:
     """The same children on the host's cores: the reference engine's own build
     (oracle/_ref; the oracle's C restatement where it is absent) clones each child's root
@@ -311,9 +342,10 @@ def branch_cpu_baseline(roots, parent, actions, seconds: float) -> dict:
 
     reference = REF_LIB.exists()
     ref = RefEngine(reference=reference)
-    threads = min(os.cpu_count() or 1, 16)
+    host = host_cores()
+    threads = host["threads"]
     r, ids, acts = (t.cpu().numpy() for t in (roots, parent, actions))
-    out = {"cores": threads, "kind": "reference" if reference else "port"}
+    out = {"cores": threads, "kind": "reference" if reference else "port", "host": host}
     for name, observe in (("branch", False), ("branch_observe", True)):
         reps, dt = 0, 0.0
         t0 = time.perf_counter()
@@ -740,6 +772,200 @@ def paired_workload(ext, torch, pairs: int = 4096) -> dict:
             "mean_pair_score_a": round(s.mean_pair_score_a, 4)}
 
 
+def paired_seq_workload(ext, torch, pairs: int = 4096) -> dict:
+    """Paired evaluation of two sequence policies (evaluate_paired with a History,
+    cugo_eval50.py:169): 4,096 deals played twice with the seats swapped, two hybrid-mode
+    4-layer d256 SeqPolicy models (fp32 weights from N(0, 0.02), seeds 1 and 2, run in bf16
+    as use_amp does), greedy actions; complete games/s."""
+    from cugo_amd.paired_eval import evaluate_paired
+    from cugo_amd.seq_selfplay import SeqPolicy
+
+    dev = torch.device("cuda")
+
+    def policy(seed: int):
+        torch.manual_seed(seed)
+        m = SeqPolicy("hybrid")
+        with torch.no_grad():
+            for prm in m.parameters():
+                prm.normal_(0.0, 0.02)
+        return m.to(dev).eval()
+
+    a, b = policy(1), policy(2)
+    evaluate_paired(ext, a, b, 256, seed_offset=0, max_steps=128, use_amp=True)  # warm
+    with region("f4.paired_seq"):
+        s = evaluate_paired(ext, a, b, pairs, seed_offset=1 << 20, max_steps=128,
+                            use_amp=True)
+    return {"games_per_s": round(s.games / s.seconds, 1), "seconds": round(s.seconds, 4),
+            "decision_steps": s.decision_steps, "pairs": pairs,
+            "ms_per_decision_step": round(1e3 * s.seconds / max(1, s.decision_steps), 4),
+            "mean_pair_score_a": round(s.mean_pair_score_a, 4)}
+
+
+PUBLISHED_GAMES_PER_S = 100_000.0      # README.md:22-23, torch50_smoke.py on one RTX 5080
+PUBLISHED_BRANCHES_PER_S = 100_000_000.0  # README.md:23, branch50_smoke.py on one RTX 5080
+
+
+def published_smoke_workload(ext, torch, batch: int = 32768, iters: int = 3,
+                             max_steps: int = 128) -> dict:
+    """The workload of the reference's published games/s figure (torch50_smoke.py:62-134,
+    run_games): each batch of B = 32,768 games is dealt from make_seeds(B, offset) and
+    played to the end by PpoActor(256, blocks=1, norm="none") in fp16 (seed 12345: Linear
+    720 -> 256, one residual block x + fc2(SiLU(fc1(x))) with fc2 zero-initialised, then
+    out(SiLU(h)) with out zero-initialised) and the masked argmax; every step observes and
+    steps all B games.  Timed as the reference times it: a warm-up batch, then `iters`
+    batches (offsets 2,000,000 + i B), games/s = B / seconds per batch, their mean.  Here a
+    step is one HIP-graph replay (observe -> the model's GEMMs -> masked argmax -> the
+    status checks on the device -> step) and the host reads the all-done flag one step
+    behind instead of synchronising on every step's checks."""
+    from torch import nn
+    from torch.nn import functional as F
+
+    from cugo_amd.seq_selfplay import make_seeds
+
+    dev = torch.device("cuda")
+
+    class SmokeActor(nn.Module):
+        """PpoActor(256, blocks=1, norm="none") (cugo_ppo_nets50.py:22-64)."""
+
+        def __init__(self, hidden: int = 256) -> None:
+            super().__init__()
+            self.inp = nn.Linear(720, hidden)
+            self.fc1 = nn.Linear(hidden, hidden)
+            self.fc2 = nn.Linear(hidden, hidden)
+            self.out = nn.Linear(hidden, 179)
+            for lin in (self.fc2, self.out):
+                nn.init.zeros_(lin.weight)
+                nn.init.zeros_(lin.bias)
+
+        def forward(self, x):
+            h = self.inp(x)
+            h = h + self.fc2(F.silu(self.fc1(h)))
+            return self.out(F.silu(h))
+
+    torch.manual_seed(12345)
+    torch.cuda.manual_seed_all(12345)
+    model = SmokeActor().to(dev).half().eval()
+    states = torch.empty((batch, 248), dtype=torch.uint8, device=dev)
+    a_seat = torch.zeros(batch, dtype=torch.int64, device=dev)
+    active = torch.zeros(batch, dtype=torch.bool, device=dev)
+    final_reward = torch.zeros(batch, device=dev)
+    final_nagari = torch.zeros(batch, dtype=torch.bool, device=dev)
+    bad = torch.zeros(3, dtype=torch.int64, device=dev)
+    steps = torch.zeros(1, dtype=torch.int64, device=dev)
+    any_active = torch.zeros(1, dtype=torch.int32, device=dev)
+    flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
+
+    def step() -> None:
+        features, legal, players, done, status = ext.observe(states)
+        logits = model(features.to(torch.float16))
+        actions = ext.masked_argmax(logits.float(), legal)
+        actions = ext.paired_select(active, status, done, legal.any(1), players, a_seat,
+                                    actions, actions, bad, any_active)
+        reward, new_done, nagari, step_status, _ = ext.step(states, actions)
+        ext.paired_update(active, step_status, new_done, reward, nagari, final_reward,
+                          final_nagari, bad, any_active, steps)
+
+    def deal(offset: int) -> None:
+        seeds, first = make_seeds(batch, offset, dev)
+        states.copy_(ext.create(seeds, first))
+        done = ext.observe(states)[3]
+        active.copy_(~done)
+        final_reward.zero_()
+        final_nagari.zero_()
+
+    def run(offset: int, replay) -> tuple[float, int]:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        deal(offset)
+        stream = torch.cuda.current_stream()
+        behind = None
+        for k in range(max_steps):
+            replay()
+            flags[k & 1].copy_(active.any(), non_blocking=True)
+            queued = (torch.cuda.Event(), k & 1, k + 1)
+            queued[0].record(stream)
+            if behind is not None:
+                behind[0].synchronize()
+                if not bool(flags[behind[1]]):
+                    break
+            behind = queued
+        else:
+            raise RuntimeError(f"not all games finished within {max_steps} decision steps")
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, behind[2]
+
+    with torch.inference_mode():
+        deal(0)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        run(1_000_000, graph.replay)  # warm-up batch
+        bad.zero_()
+        seconds, step_counts = [], []
+        with region("published.smoke"):
+            for i in range(iters):
+                dt, n_steps = run(2_000_000 + i * batch, graph.replay)
+                seconds.append(dt)
+                step_counts.append(n_steps)
+    problems = [int(x) for x in bad.tolist()]
+    if any(problems):
+        raise RuntimeError(f"observe/legal/step checks failed: {problems}")
+    mean_s = sum(seconds) / len(seconds)
+    gps = batch / mean_s
+    return {"games_per_s": round(gps, 1), "best_games_per_s": round(batch / min(seconds), 1),
+            "mean_ms_per_batch": round(1e3 * mean_s, 4), "batch": batch, "iters": iters,
+            "decision_steps": step_counts,
+            "published_games_per_s": PUBLISHED_GAMES_PER_S,
+            "vs_published": round(gps / PUBLISHED_GAMES_PER_S, 2),
+            "published_on": "1x RTX 5080 (README.md:22-23)",
+            "model": "PpoActor(256, blocks=1, norm=none) fp16, masked argmax"}
+
+
+def published_branch_workload(ext, torch, batch: int = 262144, parents_n: int = 4096,
+                              warmup: int = 5, iters: int = 20) -> dict:
+    """The workload of the reference's published branches/s figure (branch50_smoke.py:
+    68-191): 4,096 games dealt from make_seeds, each stepped once with its first legal
+    action, the live ones kept as parents; 262,144 children, child j of parent j mod P,
+    each taking its parent's first legal action; branch_indexed timed over 20 calls after
+    5, branches/s = children x calls / seconds."""
+    from cugo_amd.seq_selfplay import make_seeds
+
+    dev = torch.device("cuda")
+
+    def live(rows):
+        _, legal, _, done, status = ext.observe(rows)
+        keep = torch.nonzero(~done & (status == 0)).flatten()
+        return rows.index_select(0, keep).contiguous(), legal.index_select(0, keep)
+
+    parents, legal = live(ext.create(*make_seeds(parents_n, 0, dev)))
+    ext.step(parents, legal.to(torch.int64).argmax(1))
+    parents, legal = live(parents)
+    n_parents = parents.shape[0]
+    ids = torch.arange(batch, dtype=torch.int64, device=dev).remainder(n_parents)
+    actions = legal.to(torch.int64).argmax(1).index_select(0, ids)
+    for _ in range(warmup):
+        ext.branch_indexed(parents, ids, actions)
+    torch.cuda.synchronize()
+    with region("published.branch"):
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            ext.branch_indexed(parents, ids, actions)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+    rate = batch * iters / dt
+    return {"branches_per_s": round(rate, 1), "ms_per_call": round(1e3 * dt / iters, 4),
+            "children": batch, "parents": int(n_parents), "iters": iters,
+            "published_branches_per_s": PUBLISHED_BRANCHES_PER_S,
+            "vs_published": round(rate / PUBLISHED_BRANCHES_PER_S, 2),
+            "published_on": "1x RTX 5080 (README.md:23)"}
+
+
 def engine_traffic(batch: int, fused: bool) -> int | None:
     """HBM bytes of one engine step of the rollout from the committed counter summary: the
     fused step + observation (bf16 features) and a 32nd of the spares' refill, or observe
@@ -941,7 +1167,8 @@ def cpu_baseline(seconds: float) -> dict:
 
     reference = REF_LIB.exists()
     ref = RefEngine(reference=reference)
-    threads = min(os.cpu_count() or 1, 16)
+    host = host_cores()
+    threads = host["threads"]
     n = 4096
     while True:
         t0 = time.perf_counter()
@@ -953,7 +1180,7 @@ def cpu_baseline(seconds: float) -> dict:
     return {"value": n / dt, "unit": "games/s", "cores": threads,
             "kind": "reference" if reference else "port",
             "sample": f"{n} random-policy games ({decisions} decisions) in {dt:.1f} s",
-            "steps_per_s": decisions / dt}
+            "steps_per_s": decisions / dt, "host": host}
 
 
 def store_ceiling(torch) -> dict:
@@ -1106,6 +1333,10 @@ def main() -> None:
         result["redeal"] = redeal_workload(ext, torch)
     if not args.no_paired:
         result["paired"] = paired_workload(ext, torch)
+        result["paired_seq"] = paired_seq_workload(ext, torch)
+    if not args.no_published:
+        result["published_smoke"] = published_smoke_workload(ext, torch)
+        result["published_branch"] = published_branch_workload(ext, torch)
     if not args.no_rollout:
         with tuned_gemms(torch, not args.no_tunable):
             result["rollout"] = rollout_workload(ext, torch)
