@@ -1183,12 +1183,14 @@ def cpu_baseline(seconds: float) -> dict:
             "steps_per_s": decisions / dt, "host": host}
 
 
-def store_ceiling(torch) -> dict:
+def store_ceiling(torch, ext=None) -> dict:
     """What plain stores reach on this GPU: torch's fill_ of a 192 MiB float32 tensor (about
     the bytes of one observation step at B = 65,536; it fits in the GPU's 256 MB last-level
     cache, as the loop's output buffers do) and of a 4 GiB one (every byte has to reach
     DRAM), 20 launches each timed with events.  The observation kernels are store-bound, so
-    these are their practical ceilings below the published 8 TB/s."""
+    these are their practical ceilings below the published 8 TB/s.  With `ext`, also the
+    store probe: play_random's observation-row store pattern without the game (65,536 rows
+    of 2,880 bytes, 32 steps), over the same rows every step and at distinct rows."""
     stream = torch.cuda.current_stream()
 
     def fill_gbs(numel: int) -> tuple[float, float]:
@@ -1210,9 +1212,31 @@ def store_ceiling(torch) -> dict:
 
     gbs, ms = fill_gbs(48 << 20)
     large_gbs, large_ms = fill_gbs(1 << 30)
-    return {"kernel": "torch fill_, 192 MiB float32", "gbs": round(gbs, 1),
-            "avg_launch_ms": round(ms, 4), "large_fill_gbs": round(large_gbs, 1),
-            "large_fill": "torch fill_, 4 GiB float32", "large_fill_ms": round(large_ms, 4)}
+    out = {"kernel": "torch fill_, 192 MiB float32", "gbs": round(gbs, 1),
+           "avg_launch_ms": round(ms, 4), "large_fill_gbs": round(large_gbs, 1),
+           "large_fill": "torch fill_, 4 GiB float32", "large_fill_ms": round(large_ms, 4)}
+    if ext is not None:
+        rows, row_bytes, steps = 65536, 720 * 4, REFILL
+        buf = torch.empty(rows * row_bytes * steps, dtype=torch.uint8, device="cuda")
+        probe = {"pattern": f"{rows} rows x {row_bytes} B, {steps} steps, 64 rows a wave, "
+                            "4 rows at a time, 1 KiB float4 stores"}
+        for name, distinct in (("looped", False), ("distinct", True)):
+            for _ in range(2):
+                ext.store_probe(buf, rows, row_bytes, steps, distinct)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with region(f"ceiling.store_probe_{name}"):
+                e0.record(stream)
+                for _ in range(5):
+                    ext.store_probe(buf, rows, row_bytes, steps, distinct)
+                e1.record(stream)
+                torch.cuda.synchronize()
+            pms = e0.elapsed_time(e1) / 5
+            probe[f"{name}_ms"] = round(pms, 4)
+            probe[f"{name}_gbs"] = round(rows * row_bytes * steps / (pms * 1e-3) / 1e9, 1)
+        del buf
+        out["store_probe"] = probe
+    return out
 
 
 @contextlib.contextmanager
@@ -1253,7 +1277,7 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    ceiling = store_ceiling(torch)
+    ceiling = store_ceiling(torch, ext)
     rp = random_policy(ext, torch, args.batch, args.steps, args.warmup, args.streams,
                        not args.no_graph, not args.two_launch)
     games_per_s = rp["games"] / rp["seconds"]
@@ -1284,6 +1308,13 @@ def main() -> None:
                     "record_frac_of_large_fill": round(
                         args.batch * play_bytes / (rp["record_ms"] * 1e-3) / 1e9
                         / ceiling["large_fill_gbs"], 4)}
+        probe = ceiling.get("store_probe")
+        if probe is not None and args.batch == 65536:
+            # the time the launch's feature rows alone take to store (the probe), over
+            # the launch's time
+            roofline["frac_of_store_probe"] = round(probe["looped_ms"] / rp["play_ms"], 4)
+            roofline["record_frac_of_store_probe"] = round(
+                probe["distinct_ms"] / rp["record_ms"], 4)
     else:
         roofline = observe_roofline
     result = {

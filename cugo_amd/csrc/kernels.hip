@@ -548,6 +548,11 @@ __global__ __launch_bounds__(kStepThreads) void step_kernel(u64* states, i64 env
 // kRows children a wavefront: at 1,048,576 children (16,384 wavefronts, many rounds) 64
 // took 0.103 ms, 48 0.126 and 32 0.153: fewer children a wavefront run fewer divergent
 // rule paths each, but the launch issues more wavefronts of the same length.
+// Waves whose 64 children share one parent (C3's layout) were also given a path that
+// reads the parent with scalar loads and builds its legality head once in scalar
+// registers: VALU instructions fell from 2,095 to 1,978 a wave (the head is that
+// small a part of the step), SALU rose from 634 to 871, VGPRs stayed at 198, and the
+// launch took the same time (0.100-0.102 ms against 0.099-0.105), so it was dropped.
 template <int kRows>
 __global__ __launch_bounds__(kTile) void branch_kernel(const u64* parents, i64 env_count,
                                                        const i64* ids, const i64* actions,
@@ -609,9 +614,9 @@ __global__ __launch_bounds__(kTile) void branch_kernel(const u64* parents, i64 e
 // finished ones their next game, builds step s's records and draws its actions, then
 // takes over the stores that are left.  So the HBM-bound stores run beside the integer
 // work of both the step and the next observation, and the rows are read and written
-// once per launch.  Two waves per SIMD (the register budget is pinned to 256 VGPRs; the
-// loop keeps a few dwords in scratch): four tiles per CU (34 KiB of LDS each), every tile
-// of a 65,536-row batch resident at once.
+// once per launch.  Two waves per SIMD (the register budget is pinned to 256 VGPRs, with
+// no private memory: the code object's private segment is 0 bytes): four tiles per CU
+// (34 KiB of LDS each), every tile of a 65,536-row batch resident at once.
 constexpr int kPlayThreads = 128;
 constexpr int64_t kMaxPlaySteps = 1 << 20;
 
@@ -880,6 +885,30 @@ __global__ __launch_bounds__(kPlayThreads) void branch_observe_kernel(
   // (Staging these rows through LDS as branch_kernel does measured 5 % slower here: wave
   // 0 joins the observation's stores later.)
   store_observation<2>(t.out, base, count, features, legal, &next_item);  // wave 0 after its rows
+}
+
+// ----------------------------------------------------------- calibration ----
+// play_kernel's observation-row stores without the game, to measure what the memory
+// system gives that store pattern: each 64-lane wave owns 64 consecutive rows of
+// `row_f4` float4s and writes them 4 rows at a time, a row as float4 stores of 1 KiB
+// (lane l writes float4 l + 64 k of the row), `steps` times; step s writes rows
+// [s * rows, (s + 1) * rows) when `distinct`, else rows [0, rows) again.
+__global__ __launch_bounds__(256) void store_probe_kernel(float4* out, i64 rows, int row_f4,
+                                                          int steps, int distinct) {
+  const int lane = threadIdx.x & 63;
+  const i64 wave = ((i64)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  if (wave * 64 >= rows) return;
+  const float4 v = make_float4(1.0f, 0.0f, 1.0f, 0.0f);
+  for (int s = 0; s < steps; ++s) {
+    float4* step = out + (distinct ? (i64)s * rows * row_f4 : 0);
+    for (int r0 = 0; r0 < 64; r0 += 4) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float4* row = step + (wave * 64 + r0 + q) * row_f4;
+        for (int c = lane; c < row_f4; c += 64) row[c] = v;
+      }
+    }
+  }
 }
 
 // -------------------------------------------------------------------- small ----
@@ -1491,6 +1520,18 @@ int cugo_start(const uint8_t* states, int64_t n, int64_t* out, hipStream_t strea
   if (n < 0 || (n > 0 && (!states || !out))) return kBadArgument;
   if (n == 0) return 0;
   start_kernel<<<blocks256(n), 256, 0, stream>>>(reinterpret_cast<const u64*>(states), n, out);
+  return launched();
+}
+
+int cugo_store_probe(void* out, int64_t rows, int64_t row_bytes, int64_t steps, int distinct,
+                     hipStream_t stream) {
+  if (rows < 0 || rows % 64 != 0 || row_bytes <= 0 || row_bytes % 16 != 0 ||
+      row_bytes > (1 << 20) || steps < 0 || steps > (1 << 16) || (rows > 0 && !out))
+    return kBadArgument;
+  if (rows == 0 || steps == 0) return 0;
+  const int64_t waves = rows / 64;
+  store_probe_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, stream>>>(
+      reinterpret_cast<float4*>(out), rows, (int)(row_bytes / 16), (int)steps, distinct != 0);
   return launched();
 }
 

@@ -1003,6 +1003,24 @@ void paired_update(torch::Tensor active, torch::Tensor step_status, torch::Tenso
              "paired_update");
 }
 
+// store_probe(out uint8, rows, row_bytes, steps, distinct): the calibration launch
+// cugo_store_probe (play_random's observation-row stores without the game) into `out`.
+void store_probe(torch::Tensor out, int64_t rows, int64_t row_bytes, int64_t steps,
+                 bool distinct) {
+  TORCH_CHECK(out.is_cuda() && out.is_contiguous() && out.scalar_type() == at::kByte,
+              "out must be a contiguous CUDA uint8 tensor");
+  TORCH_CHECK(rows >= 0 && rows % 64 == 0 && row_bytes > 0 && row_bytes % 16 == 0 &&
+                  steps >= 0,
+              "rows must be a multiple of 64 and row_bytes a multiple of 16");
+  TORCH_CHECK(out.numel() >= rows * row_bytes * (distinct ? steps : 1),
+              "out is smaller than the rows the probe writes");
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(out.data_ptr()) % 16 == 0, "out must be 16-byte aligned");
+  const DeviceGuard guard(out.device());
+  check_call(cugo_store_probe(out.data_ptr(), rows, row_bytes, steps, distinct ? 1 : 0,
+                              stream()),
+             "store_probe");
+}
+
 // paired_events(active, step_status, committed, count, length_a, event_pos_a, length_b,
 // event_pos_b): the event bookkeeping of a paired evaluation of sequence policies
 // (cugo_paired_events): every game's event slot into event_pos_*, and a kept event
@@ -1524,6 +1542,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "paired evaluation: observe checks and each game's action from its mover's model");
   m.def("paired_update", &paired_update,
         "paired evaluation: step checks, final rewards and the active mask after a step");
+  m.def("store_probe", &store_probe,
+        "calibration: play_random's observation-row store pattern without the game",
+        pybind11::arg("out"), pybind11::arg("rows"), pybind11::arg("row_bytes"),
+        pybind11::arg("steps"), pybind11::arg("distinct"));
   m.def("paired_events", &paired_events,
         "paired evaluation of sequence policies: event slots, counts and cache lengths",
         pybind11::arg("active"), pybind11::arg("step_status"), pybind11::arg("committed"),

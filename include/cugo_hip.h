@@ -500,6 +500,15 @@ int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8
                           const float* features, const uint8_t* legal, const uint8_t* player,
                           const uint8_t* done, const int16_t* status, const int64_t* stock,
                           void* q_in, int64_t* query_rows, hipStream_t stream);
+/* cugo_store_probe: a calibration launch with no counterpart in the reference: the store
+ * pattern of play_random's observation rows without the game (each 64-lane wave owns 64
+ * consecutive rows of row_bytes and writes them 4 rows at a time as 1 KiB float4 stores),
+ * `steps` times, into rows [s * rows, (s + 1) * rows) at step s when `distinct`, else over
+ * rows [0, rows) every step.  out holds rows * row_bytes bytes (times steps when
+ * distinct), 16-byte aligned; rows a multiple of 64, row_bytes a multiple of 16. */
+int cugo_store_probe(void* out, int64_t rows, int64_t row_bytes, int64_t steps, int distinct,
+                     hipStream_t stream);
+
 /* Paired evaluation on resident games (evaluate_paired, cugo_eval50.py:137-361, with
  * finished games masked instead of dropped; no counterpart in the reference, whose loop
  * does this with torch ops).  cugo_paired_select, after observe: bad[0] += active &

@@ -205,6 +205,50 @@ def test_branch_and_clone(ext, ref):
         assert torch.equal(a[valid], b[valid])
 
 
+def test_branch_one_parent_waves(ext, ref):
+    """branch_indexed where every child of a 64-child wave has the same parent (the
+    scalar-head path) and where one lane differs or the shared id is invalid (the per-lane
+    path), against the oracle: every golden mid-game parent kind (pending floor choices,
+    finished games, ordinary decisions), every action id in turn plus out-of-range ones,
+    and a partial last wave."""
+    announce("branch one-parent waves")
+    golden = np.load(GOLDEN / "rows.npz")
+    parents_np = golden["mid"]
+    m = parents_np.shape[0]
+    legal = golden["legal"]
+    pending = np.nonzero(parents_np[:, 27 * 8 + 3] != 0)[0]   # pactive byte of word 27
+    finished = np.nonzero(parents_np[:, 29 * 8 + 7] != 0)[0]  # done byte of word 29
+    ordinary = np.setdiff1d(np.arange(m), np.concatenate([pending, finished]))
+    assert pending.size > 0 and finished.size > 0
+    rng = np.random.default_rng(29)
+    chosen = np.concatenate([pending[:24], finished[:8], rng.choice(ordinary, 96, replace=False)])
+    ids, acts = [], []
+    for w, p in enumerate(chosen):
+        wave = np.full(64, p, dtype=np.int64)
+        a = (np.arange(64) + 64 * (w % 3)) % 181 - 1  # -1 .. 179 over three waves
+        good = np.nonzero(legal[p])[0]
+        if good.size:  # most lanes legal
+            a[::2] = good[np.arange(32) % good.size]
+        if w % 17 == 5:
+            wave[63] = (p + 1) % m  # one lane with another parent
+        ids.append(wave)
+        acts.append(a)
+    ids.append(np.full(64, m, dtype=np.int64))  # a wave of one invalid parent id
+    acts.append(np.zeros(64, dtype=np.int64))
+    ids.append(np.full(37, chosen[0], dtype=np.int64))  # a partial last wave
+    acts.append(np.arange(37, dtype=np.int64))
+    ids, acts = np.concatenate(ids), np.concatenate(acts)
+    parents = torch.from_numpy(parents_np).to(DEV)
+    snapshot = parents.clone()
+    out = ext.branch_indexed(parents, torch.from_numpy(ids).to(DEV), torch.from_numpy(acts).to(DEV))
+    rout = ref.branch(parents_np, ids, acts)
+    assert np.array_equal(to_np(out[0]), rout[0]), "children differ"
+    assert_step_equal(out[1:], rout[1:], "one-parent branch outputs")
+    assert torch.equal(parents, snapshot)
+    status = to_np(out[4])
+    assert (status == 0).sum() > 1000 and (status == -1).sum() == 64
+
+
 def test_empty_batches(ext):
     announce("empty_batches")
     states = ext.create(torch.zeros(4, dtype=torch.long, device=DEV),
