@@ -463,7 +463,9 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   if (active && (status[i] != 0 || !any)) atomicAdd(wave.bad, 1ull);
   const i64 p = (i64)player[i];
   query_rows[i] = (p & 1) * w + i;
-  if (wave.query_pos != nullptr) wave.query_pos[i] = wave.cache_length[(p & 1) * w + i];
+  // a finished game's query attends nothing (its row is skipped: no cache read or write,
+  // a NaN output that nothing uses)
+  if (wave.query_pos != nullptr) wave.query_pos[i] = active ? wave.cache_length[(p & 1) * w + i] : -1;
   if (!record) return;
   wave.rec_seat[rec] = p;
   wave.rec_count[rec] = wave.count[i];
@@ -497,12 +499,15 @@ __global__ __launch_bounds__(256) void advance_kernel(
     if (nagari[i]) wave.final_nagari[i] = 1;
     wave.finished[i] = 1;
   }
-  if (wave.event_pos != nullptr) {  // the slots of this step's event tokens
-    wave.event_pos[i] = wave.cache_length[i];
-    wave.event_pos[w + i] = wave.cache_length[w + i];
+  // The slots of this step's event tokens; an event that is not kept (no committed action,
+  // or a game already over) goes nowhere: its row of the next pass is skipped.
+  const bool keep = active && committed[i];
+  if (wave.event_pos != nullptr) {
+    wave.event_pos[i] = keep ? wave.cache_length[i] : -1;
+    wave.event_pos[w + i] = keep ? wave.cache_length[w + i] : -1;
   }
   const i64 c = wave.count[i];
-  if (active && committed[i]) {
+  if (keep) {
     const i64 slot = c < kMaxEvents - 1 ? c : kMaxEvents - 1;
     i64* log = wave.events + (i * kMaxEvents + slot) * 9;
     for (int k = 0; k < 9; ++k) log[k] = events[i * 9 + k];
@@ -569,26 +574,33 @@ __global__ __launch_bounds__(256) void paired_update_kernel(
 // The event log of a paired evaluation of sequence policies (History.record,
 // cugo_seq50.py:62-67, called at cugo_eval50.py:258-263), kept as each policy's cache
 // length: after the engine step and the event tokens (which read the old count), before
-// paired_update clears the active flags.  Every game's event token went to slot
-// length_m[i] of policy m's cache row i (event_pos_m records it for the next step's pass);
-// an active game whose step is OK and committed keeps it: count[i] and every length_m[i]
-// advance.  One thread per game.
+// paired_update clears the active flags.  A game's event is kept when the game was active,
+// its step is OK and its action committed: its token goes to slot length_m[i] of policy
+// m's cache row i at the next step's pass (event_pos_m), and count[i] and every length_m[i]
+// advance; any other event's row is skipped at that pass (event_pos_m = -1).  The next
+// step's query of a game still playing (active, OK, not finished now) goes to slot
+// length_m[i] (query_pos_m); a finished game's query row is skipped (-1).  One thread per
+// game.
 __global__ __launch_bounds__(256) void paired_events_kernel(
-    const uint8_t* active, const int16_t* step_status, const uint8_t* committed, i64 n,
-    i64* count, i64* length_a, i64* event_pos_a, i64* length_b, i64* event_pos_b) {
+    const uint8_t* active, const int16_t* step_status, const uint8_t* committed,
+    const uint8_t* new_done, i64 n, i64* count, i64* length_a, i64* event_pos_a,
+    i64* query_pos_a, i64* length_b, i64* event_pos_b, i64* query_pos_b) {
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
+  const bool live = active[i] != 0 && step_status[i] == 0;
+  const bool keep = live && committed[i] != 0;
+  const bool next = live && new_done[i] == 0;
   const i64 la = length_a[i];
-  event_pos_a[i] = la;
-  i64 lb = 0;
+  event_pos_a[i] = keep ? la : -1;
+  query_pos_a[i] = next ? la + (keep ? 1 : 0) : -1;
+  if (keep) length_a[i] = la + 1;
   if (length_b != nullptr) {
-    lb = length_b[i];
-    event_pos_b[i] = lb;
+    const i64 lb = length_b[i];
+    event_pos_b[i] = keep ? lb : -1;
+    query_pos_b[i] = next ? lb + (keep ? 1 : 0) : -1;
+    if (keep) length_b[i] = lb + 1;
   }
-  if (active[i] == 0 || step_status[i] != 0 || committed[i] == 0) return;
-  count[i] += 1;
-  length_a[i] = la + 1;
-  if (length_b != nullptr) length_b[i] = lb + 1;
+  if (keep) count[i] += 1;
 }
 
 // Pre-norm transformer residual step (nn.TransformerEncoderLayer with norm_first,
@@ -892,16 +904,19 @@ int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_
 }
 
 int cugo_paired_events(const uint8_t* active, const int16_t* step_status,
-                       const uint8_t* committed, int64_t n, int64_t* count, int64_t* length_a,
-                       int64_t* event_pos_a, int64_t* length_b, int64_t* event_pos_b,
-                       hipStream_t stream) {
-  if (n < 0 || (n > 0 && (!active || !step_status || !committed || !count || !length_a ||
-                          !event_pos_a)) ||
-      (length_b == nullptr) != (event_pos_b == nullptr))
+                       const uint8_t* committed, const uint8_t* new_done, int64_t n,
+                       int64_t* count, int64_t* length_a, int64_t* event_pos_a,
+                       int64_t* query_pos_a, int64_t* length_b, int64_t* event_pos_b,
+                       int64_t* query_pos_b, hipStream_t stream) {
+  const bool has_b = length_b != nullptr;
+  if (n < 0 || (n > 0 && (!active || !step_status || !committed || !new_done || !count ||
+                          !length_a || !event_pos_a || !query_pos_a)) ||
+      (event_pos_b != nullptr) != has_b || (query_pos_b != nullptr) != has_b)
     return -1;
   if (n == 0) return 0;
   paired_events_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
-      active, step_status, committed, n, count, length_a, event_pos_a, length_b, event_pos_b);
+      active, step_status, committed, new_done, n, count, length_a, event_pos_a, query_pos_a,
+      length_b, event_pos_b, query_pos_b);
   return (int)hipGetLastError();
 }
 

@@ -1021,38 +1021,50 @@ void store_probe(torch::Tensor out, int64_t rows, int64_t row_bytes, int64_t ste
              "store_probe");
 }
 
-// paired_events(active, step_status, committed, count, length_a, event_pos_a, length_b,
-// event_pos_b): the event bookkeeping of a paired evaluation of sequence policies
-// (cugo_paired_events): every game's event slot into event_pos_*, and a kept event
-// (active, OK, committed) advances the count and the cache lengths.
+// paired_events(active, step_status, committed, new_done, count, length_a, event_pos_a,
+// query_pos_a, length_b, event_pos_b, query_pos_b): the event bookkeeping of a paired
+// evaluation of sequence policies (cugo_paired_events): a kept event's slot (or -1) into
+// event_pos_*, the next query's slot (or -1) into query_pos_*, and the counts and cache
+// lengths advanced.
 void paired_events(torch::Tensor active, torch::Tensor step_status, torch::Tensor committed,
-                   torch::Tensor count, torch::Tensor length_a, torch::Tensor event_pos_a,
-                   c10::optional<torch::Tensor> length_b, c10::optional<torch::Tensor> event_pos_b) {
+                   torch::Tensor new_done, torch::Tensor count, torch::Tensor length_a,
+                   torch::Tensor event_pos_a, torch::Tensor query_pos_a,
+                   c10::optional<torch::Tensor> length_b, c10::optional<torch::Tensor> event_pos_b,
+                   c10::optional<torch::Tensor> query_pos_b) {
   const int64_t n = active.numel();
   check_n(active, n, at::kBool, "active");
   check_n(step_status, n, at::kShort, "step_status");
   check_n(committed, n, at::kBool, "committed");
+  check_n(new_done, n, at::kBool, "new_done");
   check_n(count, n, at::kLong, "count");
   check_n(length_a, n, at::kLong, "length_a");
   check_n(event_pos_a, n, at::kLong, "event_pos_a");
-  for (const auto* t : {&step_status, &committed, &count, &length_a, &event_pos_a})
+  check_n(query_pos_a, n, at::kLong, "query_pos_a");
+  for (const auto* t : {&step_status, &committed, &new_done, &count, &length_a, &event_pos_a,
+                        &query_pos_a})
     check_same_device(active, *t, "active", "an input");
-  TORCH_CHECK(length_b.has_value() == event_pos_b.has_value(),
-              "length_b and event_pos_b go together");
+  TORCH_CHECK(length_b.has_value() == event_pos_b.has_value() &&
+                  length_b.has_value() == query_pos_b.has_value(),
+              "length_b, event_pos_b and query_pos_b go together");
   int64_t* lb = nullptr;
   int64_t* pb = nullptr;
+  int64_t* qb = nullptr;
   if (length_b.has_value()) {
     check_n(*length_b, n, at::kLong, "length_b");
     check_n(*event_pos_b, n, at::kLong, "event_pos_b");
+    check_n(*query_pos_b, n, at::kLong, "query_pos_b");
     check_same_device(active, *length_b, "active", "length_b");
     check_same_device(active, *event_pos_b, "active", "event_pos_b");
+    check_same_device(active, *query_pos_b, "active", "query_pos_b");
     lb = length_b->data_ptr<int64_t>();
     pb = event_pos_b->data_ptr<int64_t>();
+    qb = query_pos_b->data_ptr<int64_t>();
   }
   const DeviceGuard guard(active.device());
-  check_call(cugo_paired_events(u8p(active), step_status.data_ptr<int16_t>(), u8p(committed), n,
-                                count.data_ptr<int64_t>(), length_a.data_ptr<int64_t>(),
-                                event_pos_a.data_ptr<int64_t>(), lb, pb, stream()),
+  check_call(cugo_paired_events(u8p(active), step_status.data_ptr<int16_t>(), u8p(committed),
+                                u8p(new_done), n, count.data_ptr<int64_t>(),
+                                length_a.data_ptr<int64_t>(), event_pos_a.data_ptr<int64_t>(),
+                                query_pos_a.data_ptr<int64_t>(), lb, pb, qb, stream()),
              "paired_events");
 }
 
@@ -1547,11 +1559,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("out"), pybind11::arg("rows"), pybind11::arg("row_bytes"),
         pybind11::arg("steps"), pybind11::arg("distinct"));
   m.def("paired_events", &paired_events,
-        "paired evaluation of sequence policies: event slots, counts and cache lengths",
+        "paired evaluation of sequence policies: event and query slots, counts, cache lengths",
         pybind11::arg("active"), pybind11::arg("step_status"), pybind11::arg("committed"),
-        pybind11::arg("count"), pybind11::arg("length_a"), pybind11::arg("event_pos_a"),
+        pybind11::arg("new_done"), pybind11::arg("count"), pybind11::arg("length_a"),
+        pybind11::arg("event_pos_a"), pybind11::arg("query_pos_a"),
         pybind11::arg("length_b") = pybind11::none(),
-        pybind11::arg("event_pos_b") = pybind11::none());
+        pybind11::arg("event_pos_b") = pybind11::none(),
+        pybind11::arg("query_pos_b") = pybind11::none());
   m.def("masked_argmax", &masked_argmax, "Greedy action: argmax of the legal logits");
   m.def("mlp_pack_weight", &mlp_pack_weight,
         "bf16 matrix in the actor kernel's MFMA operand order", pybind11::arg("w"),

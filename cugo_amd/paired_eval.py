@@ -102,7 +102,10 @@ class _SequenceSeat:
         d = model.position.shape[1]
         self.cache = policy_cache(model, games, dev)
         self.pair = torch.zeros((2 * games, d), dtype=dtype, device=dev)
-        self.event_pos = torch.ones(games, dtype=torch.int64, device=dev)
+        # slots of the waiting event tokens and of the next queries; -1 skips a row (an
+        # event not kept, the query of a game that is over)
+        self.event_pos = torch.full((games,), -1, dtype=torch.int64, device=dev)
+        self.query_pos = torch.full((games,), -1, dtype=torch.int64, device=dev)
         cols = model.kept_columns()
         self.columns = None if cols is None else torch.tensor(cols, device=dev)
         self.width = FEATURES if cols is None else len(cols)
@@ -112,20 +115,22 @@ class _SequenceSeat:
         self.ids = torch.arange(games, device=dev)
         model.prepare()
 
-    def open(self, start: torch.Tensor) -> None:
+    def open(self, start: torch.Tensor, active: torch.Tensor) -> None:
         """Every game's opening token (cugo_seq50.py:271-274, seen from `seat`) into slot 0;
-        no event waits (the first pass writes zeros into the queries' own slots)."""
+        no event waits, and the first queries go to slot 1 of the games being played."""
         m, cache = self.model, self.cache
         cache.length.zero_()
         m.cached_step(cache, m.start_token(start, self.seat), 1)
         cache.length.fill_(1)
-        self.event_pos.fill_(1)
-        self.pair[:self.games].zero_()
+        self.event_pos.fill_(-1)
+        torch.where(active, cache.length, torch.full_like(cache.length, -1), out=self.query_pos)
 
     def logits(self, features: torch.Tensor, legal: torch.Tensor) -> torch.Tensor:
-        """The last step's event tokens and every game's query through the layers together
-        (the queries attend the events' keys at every layer), then the readout of the
-        queries: [games, 179] logits in the policy dtype."""
+        """The last step's kept event tokens and the query of every game still being played
+        through the layers together (the queries attend the events' keys at every layer),
+        then the readout of the queries: [games, 179] logits in the policy dtype (NaN in
+        the rows of games that are over, whose rows the decode skips: no cache read or
+        write; nothing reads those logits)."""
         from .seq_decode import cached_step_pair
 
         m, g = self.model, self.games
@@ -134,7 +139,7 @@ class _SequenceSeat:
         self.q_in[:, self.width:self.width + legal.shape[1]].copy_(legal)
         m.query_from_input(self.q_in, out=self.pair[g:])
         hidden, normed = cached_step_pair(m, self.cache, self.pair, g, self.event_pos,
-                                          self.cache.length, self.ids, final_norm=m.norm)
+                                          self.query_pos, self.ids, final_norm=m.norm)
         return m.readout(hidden[g:], normed[g:])
 
     def events(self, events: torch.Tensor, count: torch.Tensor) -> None:
@@ -253,8 +258,8 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
                 ext.step_events_indexed(states, ids, actions))
             for h in histories:
                 h.events(events, count)
-            lengths = [x for h in histories for x in (h.cache.length, h.event_pos)]
-            ext.paired_events(active, step_status, committed, count, *lengths)
+            slots = [x for h in histories for x in (h.cache.length, h.event_pos, h.query_pos)]
+            ext.paired_events(active, step_status, committed, new_done, count, *slots)
         else:
             reward0, new_done, nagari, step_status, _ = ext.step(states, actions)
         ext.paired_update(active, step_status, new_done, reward0, nagari, final_reward0,
@@ -269,7 +274,7 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
             kept = [states, final_reward0, final_nagari, active, bad, steps_dev, any_active,
                     count]
             for h in histories:
-                kept += [h.cache.length, h.event_pos, h.pair]
+                kept += [h.cache.length, h.event_pos, h.query_pos, h.pair]
             saved = [t.clone() for t in kept]
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
@@ -294,7 +299,7 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         bad[1] += (~done & fine & ~any_legal).sum()
         active.copy_(~done & fine & any_legal)
         for h in histories:
-            h.open(start)
+            h.open(start, active)
         stream = torch.cuda.current_stream()
         finished_all = False
         behind = None  # (event, flag slot) of the step before the latest

@@ -260,8 +260,9 @@ class SelfPlayWave:
         self._done_flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
         # The learner's event tokens of a step wait in rows [0, 2 w) of `pair` and go
         # through the layers with the next step's queries (rows [2 w, 3 w)), in one pass
-        # (cached_step_pair); event_pos holds the slots they go to.  flush() runs them
-        # alone.
+        # (cached_step_pair); event_pos holds the slots they go to (-1 for an event that
+        # is not kept: no committed action, or a game already over, whose row the decode
+        # skips, as it skips the query of a finished game).  flush() runs them alone.
         d = actor.position.shape[1]
         self.pair = torch.zeros((3 * wave, d), dtype=actor.event_in.weight.dtype, device=dev)
         # The query input's rows padded with zeros to a depth `linear` takes (1,024 for the
@@ -313,9 +314,9 @@ class SelfPlayWave:
         if pool and self.p:
             self._open(self.opponent, self.opp_cache, t.start[:self.p],
                        1 - t.learner_seat[:self.p])
-        # no events wait: the first step's event rows write the query's own scratch slot
+        # no events wait: the first step's event rows are skipped
         self.pair[:2 * self.w].zero_()
-        self.event_pos.copy_(self.cache.length)
+        self.event_pos.fill_(-1)
 
     @torch.no_grad()
     def step(self, pool: bool = False) -> None:
@@ -324,7 +325,9 @@ class SelfPlayWave:
         launches (SelfPlayState.prepare before the query, .advance after the event
         tokens).  The learner's event tokens of this step enter its cache at the next
         step (with that step's queries) or at flush(); until then the cache holds the
-        step's query in their slots, which no later token reads."""
+        step's query in their slots, which no later token reads.  Rows of finished games
+        and of events not kept are skipped by the decode (no cache read or write; their
+        hidden states and logits are NaN, and nothing reads them)."""
         ext, actor, t, w = self.ext, self.actor, self.t, self.w
         pool = pool and self.p > 0
         native = self.native[pool]

@@ -530,14 +530,19 @@ int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_
  * reference keeps in a History (History.record, cugo_seq50.py:62-67, called at
  * cugo_eval50.py:258-263; no counterpart as one call), as each policy's KV-cache lengths.
  * After the engine step (step_events_indexed) and the event tokens, before
- * cugo_paired_update: event_pos_a[i] = length_a[i] (and event_pos_b[i] = length_b[i]) for
- * every game; a game that is active, whose step status is OK and whose action committed
- * advances count[i], length_a[i] and length_b[i] by one.  length_b and event_pos_b are both
- * NULL when one policy keeps a cache.  int64 arrays of n entries; bool arrays one byte. */
+ * cugo_paired_update.  A game's event is kept when the game is active, its step status is
+ * OK and its action committed: event_pos_a[i] = length_a[i] (the slot its token takes at
+ * the next step's pass), then count[i] and length_a[i] advance by one; an event not kept
+ * gets event_pos_a[i] = -1 (its row of the pass is skipped).  query_pos_a[i] is the slot of
+ * the next step's query: the new length_a[i] for a game that is active, OK and not
+ * finished by this step, else -1 (skipped).  The same for policy b, whose three arrays are
+ * all NULL when one policy keeps a cache.  int64 arrays of n entries; bool arrays one
+ * byte. */
 int cugo_paired_events(const uint8_t* active, const int16_t* step_status,
-                       const uint8_t* committed, int64_t n, int64_t* count, int64_t* length_a,
-                       int64_t* event_pos_a, int64_t* length_b, int64_t* event_pos_b,
-                       hipStream_t stream);
+                       const uint8_t* committed, const uint8_t* new_done, int64_t n,
+                       int64_t* count, int64_t* length_a, int64_t* event_pos_a,
+                       int64_t* query_pos_a, int64_t* length_b, int64_t* event_pos_b,
+                       int64_t* query_pos_b, hipStream_t stream);
 
 /* cugo_selfplay_advance: the step's work after the engine step (cugo_seq_selfplay50.py:
  * 146-163): bad += active & (step status != OK); games that finished now keep reward0 and
