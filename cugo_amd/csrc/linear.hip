@@ -363,6 +363,307 @@ int launch(const Args& base, int k, int act, hipStream_t stream) {
   }
 }
 
+// ---------------------------------------------------------------- feed-forward ----
+// The feed-forward half of a pre-norm encoder layer in one launch (cugo_seq50.py:319-322:
+// x + linear2(GELU(linear1(h))), h = norm2(x), then the next layer's norm1 or the final
+// norm), for d = 256 and a 1,024-wide hidden layer.  The two-launch form writes the
+// [m, 1,024] GELU output to HBM and reads it back; here a workgroup owns 16 MT rows for
+// the whole block and the hidden layer never leaves the CU:
+//   * h's rows (256 columns) are copied into LDS once (the X panel layout of
+//     linear_kernel); the hidden layer runs in four 256-column chunks: each of the 8
+//     wavefronts computes 32 columns of the chunk for all rows (linear1, W1 as the MFMA A
+//     operand, K = 256), adds the bias, rounds, applies GELU and rounds again, and writes
+//     them to a chunk buffer in LDS (two buffers, so one barrier a chunk); then each
+//     wavefront adds the chunk's K slice of linear2 into its 32 output columns for all
+//     rows (accumulators in registers across the chunks, K order 0 .. 1,023 as the
+//     one-launch linear2 runs it);
+//   * the epilogue is linear_kernel's: bias, bf16, the residual add, the LayerNorm (or
+//     the plain residual), through LDS row-major.
+// Every rounding and every fp32 sum is in the order of linear (GELU) + linear_add_layernorm
+// (or linear with the residual), so the outputs are the same bits.
+// What bounds it: each workgroup streams all 1 MiB of W1 and W2 through its CU's L1 (the
+// FLOPs a weight byte buys are the tile's rows), ~20 bytes a cycle a CU when every CU
+// reads the same weights at once; the GELU's erff is ~5 us of VALU at 12,288 rows (the
+// launch without it: 20.5 against 26.1 us).  At 12,288 rows the launch takes 32 us
+// against 43 for the two launches it replaces.
+// Weights: linear_kernel's packed fragments, W1 [1,024, 256] (8 K steps a 16-row tile)
+// and W2 [256, 1,024] (32 K steps a tile), read through buffer loads a few K steps ahead
+// of the MFMAs.
+namespace ffn {
+
+constexpr int kD = 256;       // model width
+constexpr int kF = 1024;      // hidden width
+constexpr int kC = 256;       // hidden columns a chunk
+constexpr int kChunks = kF / kC;
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kS1 = kD / kK;  // K steps of linear1 (8)
+constexpr int kSc = kC / kK;  // K steps of linear2 a chunk (8)
+constexpr int kS2 = kF / kK;  // K steps of linear2 (32)
+
+struct Args {
+  const __bf16* h;  // [m, 256], row stride ldh
+  const __bf16* x;  // residual [m, 256], contiguous
+  const __bf16* w1;
+  const __bf16* b1;
+  const __bf16* w2;
+  const __bf16* b2;
+  const __bf16* ln_w;  // NULL: x_out = x + y only
+  const __bf16* ln_b;
+  float eps;
+  __bf16* x_out;  // [m, 256] contiguous (may alias x)
+  __bf16* ln;     // [m, 256] contiguous, with ln_w
+  int m, ldh;
+};
+
+template <int MT, int kDepth>
+__global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
+  constexpr int kR = kDepth + 1;  // ring slots: K steps of weights in flight ahead of MFMAs
+  constexpr int BM = 16 * MT;
+  constexpr int kPanel = BM * kD;            // elements of h's panel, and of a chunk buffer
+  constexpr int kOutStride = kD + 16;        // elements a row of the staged output
+  static_assert(BM * kOutStride <= 2 * kPanel, "the staged output fits two panels");
+  static_assert(3 * kPanel * 2 <= 160 * 1024, "the panel and two chunks fit the LDS");
+  __shared__ __attribute__((aligned(16))) __bf16 smem[3 * kPanel];
+  __bf16* hs = smem;               // h's rows (xs_at layout, BM rows, K = 256)
+  __bf16* us = smem + kPanel;      // chunk buffers 0 and 1 (xs_at layout, K = 256)
+  __bf16* staged = smem;           // the output tile, after the last chunk (hs + us[0])
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, q4 = lane >> 4;
+  const int m0 = blockIdx.x * BM;
+  const int c0 = wave * 32;  // this wavefront's columns: of each chunk, and of the output
+
+  const auto w1r = __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(a.w1), (short)0,
+                                                     (kF / 16) * kS1 * kFragBytes, 0x00020000);
+  const auto w2r = __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(a.w2), (short)0,
+                                                     (kD / 16) * kS2 * kFragBytes, 0x00020000);
+  // W1 fragment (chunk c, tile t, step s): hidden columns 256 c + 32 wave + 16 t;
+  // W2 fragment (tile t, step s): output columns 32 wave + 16 t, K step s of 32.
+  auto w1_at = [&](int c, int t, int s) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+        w1r, lane * 16, ((16 * c + 2 * wave + t) * kS1 + s) * kFragBytes, 0));
+  };
+  auto w2_at = [&](int t, int s) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+        w2r, lane * 16, ((2 * wave + t) * kS2 + s) * kFragBytes, 0));
+  };
+
+  bf16x8 r1[kR][2];  // W1 ring
+  bf16x8 r2[kR][2];  // W2 ring
+#pragma unroll
+  for (int j = 0; j < kDepth; ++j)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) r1[j][t] = w1_at(0, t, j);
+
+  constexpr int kNormRows = BM / kWaves;  // rows a wavefront finishes in the epilogue
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+  // h's panel: thread tid copies 16-byte groups tid, tid + kThreads, ... (row-major).
+  {
+    constexpr int kGroups = BM * kD / 8;
+    const auto hr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<__bf16*>(a.h), (short)0, ((a.m - 1) * a.ldh + kD) * 2, 0x00020000);
+    constexpr int kBatch = 8;
+#pragma unroll
+    for (int b0 = 0; b0 < kGroups; b0 += kThreads * kBatch) {
+      uint4 v[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int gi = b0 + j * kThreads + tid;
+        if (gi < kGroups) {
+          const int r = gi / (kD / 8), c = gi % (kD / 8);
+          const int row = min(m0 + r, a.m - 1);
+          v[j] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(hr, (row * a.ldh + 8 * c) * 2, 0, 0));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int gi = b0 + j * kThreads + tid;
+        if (gi < kGroups) {
+          const int r = gi / (kD / 8), c = gi % (kD / 8);
+          *reinterpret_cast<uint4*>(hs + xs_at<BM>(r, 8 * c)) = v[j];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const int x_lane = xs_at<BM>(l16, 8 * q4);  // B fragments: row tile i, K step s at
+                                              // x_lane + (s * BM + 16 i) * 32
+  f32x4 y[MT][2];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) y[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    __bf16* ub = us + (c & 1) * kPanel;
+    bf16x4_t b1v[2];  // linear1's bias at this lane's columns of the chunk
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      b1v[t] = *reinterpret_cast<const bf16x4_t*>(a.b1 + kC * c + c0 + 16 * t + 4 * q4);
+    // ---- linear1 of the chunk: u[i][t] = W1 (32 of the chunk's columns) x h (row tile i)
+    f32x4 u[MT][2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) u[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 xa[2][MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      xa[0][i] = *reinterpret_cast<const bf16x8*>(hs + x_lane + 16 * i * 32);
+#pragma unroll
+    for (int s = 0; s < kS1; ++s) {
+      if (s + kDepth < kS1) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) r1[(s + kDepth) % kR][t] = w1_at(c, t, s + kDepth);
+      } else if (s + kDepth - kS1 < kDepth) {
+        // the ring's next steps: linear2's first of this chunk
+        const int s2 = s + kDepth - kS1;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) r2[s2 % kR][t] = w2_at(t, kSc * c + s2);
+      }
+      if (s + 1 < kS1) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          xa[(s + 1) & 1][i] =
+              *reinterpret_cast<const bf16x8*>(hs + x_lane + ((s + 1) * BM + 16 * i) * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          u[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r1[s % kR][t], xa[s & 1][i],
+                                                            u[i][t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // bias, bf16, GELU, bf16 (linear_kernel's GELU epilogue) into the chunk buffer: lane l
+    // holds hidden columns c0 + 16 t + 4 q4 + 0..3 of row 16 i + l16
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        bf16x4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const __bf16 v = (__bf16)(u[i][t][e] + (float)b1v[t][e]);
+          o[e] = (__bf16)gelu((float)v);
+        }
+        *reinterpret_cast<bf16x4_t*>(ub + xs_at<BM>(16 * i + l16, c0 + 16 * t + 4 * q4)) = o;
+      }
+    __syncthreads();  // the chunk is complete (and the other buffer's readers are done)
+    // ---- linear2's K slice of the chunk: y[i][t] += W2 (32 output columns) x u (row tile i)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      xa[0][i] = *reinterpret_cast<const bf16x8*>(ub + x_lane + 16 * i * 32);
+#pragma unroll
+    for (int s = 0; s < kSc; ++s) {
+      if (s + kDepth < kSc) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) r2[(s + kDepth) % kR][t] = w2_at(t, kSc * c + s + kDepth);
+      } else if (c + 1 < kChunks) {
+        // the ring's next steps: the next chunk's linear1
+        const int s1 = s + kDepth - kSc;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) r1[s1 % kR][t] = w1_at(c + 1, t, s1);
+      }
+      if (s + 1 < kSc) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          xa[(s + 1) & 1][i] =
+              *reinterpret_cast<const bf16x8*>(ub + x_lane + ((s + 1) * BM + 16 * i) * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          y[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r2[s % kR][t], xa[s & 1][i],
+                                                            y[i][t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // ---- epilogue: bias, bf16, staged row-major over h's panel and chunk buffer 0 (both
+  // dead: every wavefront passed the last chunk's barrier after its last read of them)
+  float b2v[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const bf16x4_t bv = *reinterpret_cast<const bf16x4_t*>(a.b2 + c0 + 16 * t + 4 * q4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) b2v[t][e] = (float)bv[e];
+  }
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      bf16x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (__bf16)(y[i][t][e] + b2v[t][e]);
+      *reinterpret_cast<bf16x4_t*>(staged + (16 * i + l16) * kOutStride + c0 + 16 * t +
+                                   4 * q4) = o;
+    }
+  // the residual rows this wavefront finishes (row wave + 8 j)
+  bf16x4_t res_v[kNormRows];
+#pragma unroll
+  for (int j = 0; j < kNormRows; ++j) {
+    const int row = min(m0 + wave + kWaves * j, a.m - 1);
+    res_v[j] = *reinterpret_cast<const bf16x4_t*>(a.x + (int64_t)row * kD + lane * 4);
+  }
+  __syncthreads();
+  // one wavefront a row, 4 elements a lane: x_out = bf16(res + y); with ln_w, the
+  // LayerNorm of linear_kernel's kAddNorm epilogue
+  constexpr int KE = kD / 64;
+  const bool norm = a.ln_w != nullptr;
+  bf16x4_t wv4, bv4;
+  if (norm) {
+    wv4 = *reinterpret_cast<const bf16x4_t*>(a.ln_w + lane * KE);
+    bv4 = *reinterpret_cast<const bf16x4_t*>(a.ln_b + lane * KE);
+  }
+#pragma unroll
+  for (int j = 0; j < kNormRows; ++j) {
+    const int r = wave + kWaves * j;
+    const int row = m0 + r;
+    if (row >= a.m) break;
+    const bf16x4_t yv = *reinterpret_cast<const bf16x4_t*>(staged + r * kOutStride + lane * KE);
+    const int64_t at = (int64_t)row * kD + lane * KE;
+    const bf16x4_t xv = res_v[j];
+    float v[KE];
+    bf16x4_t xo;
+#pragma unroll
+    for (int k = 0; k < KE; ++k) {
+      xo[k] = (__bf16)((float)xv[k] + (float)yv[k]);
+      v[k] = (float)xo[k];
+    }
+    *reinterpret_cast<bf16x4_t*>(a.x_out + at) = xo;
+    if (!norm) continue;
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KE; ++k) sum += v[k];
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float mean = sum / (float)kD;
+    float sq = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KE; ++k) {
+      const float d = v[k] - mean;
+      sq += d * d;
+    }
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+    const float rstd = 1.0f / sqrtf(sq / (float)kD + a.eps);
+    bf16x4_t o;
+#pragma unroll
+    for (int k = 0; k < KE; ++k)
+      o[k] = (__bf16)((v[k] - mean) * rstd * (float)wv4[k] + (float)bv4[k]);
+    *reinterpret_cast<bf16x4_t*>(a.ln + at) = o;
+  }
+}
+
+}  // namespace ffn
+
 }  // namespace linear
 }  // namespace cugo_amd
 
@@ -455,6 +756,72 @@ int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
     case 4: return launch<4, 2, 1, 8, 2>(a, (int)k, kAddNorm, stream);  // 64 x 256, 8 waves
     default: return -6;
   }
+}
+
+
+int cugo_ffn(const void* h, int64_t ldh, const void* x, const void* w1_packed, const void* b1,
+             const void* w2_packed, const void* b2, const void* ln_weight, const void* ln_bias,
+             float eps, int64_t m, void* x_out, void* ln, int rows, hipStream_t stream) {
+  if (m < 0 || (m > 0 && (!h || !x || !w1_packed || !b1 || !w2_packed || !b2 || !x_out)) ||
+      (ln_weight == nullptr) != (ln_bias == nullptr) || (ln_weight != nullptr && !ln))
+    return -1;
+  if (ldh < 256 || ldh % 8 != 0) return -3;
+  const uintptr_t p16 = reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(w1_packed) |
+                        reinterpret_cast<uintptr_t>(w2_packed);
+  const uintptr_t p8 = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(b1) |
+                       reinterpret_cast<uintptr_t>(b2) | reinterpret_cast<uintptr_t>(x_out) |
+                       reinterpret_cast<uintptr_t>(ln_weight) |
+                       reinterpret_cast<uintptr_t>(ln_bias) | reinterpret_cast<uintptr_t>(ln);
+  if (p16 % 16 != 0 || p8 % 8 != 0) return -4;
+  if (m * ldh >= (int64_t(1) << 30)) return -5;
+  if (m == 0) return 0;
+  ffn::Args a{};
+  a.h = static_cast<const __bf16*>(h);
+  a.x = static_cast<const __bf16*>(x);
+  a.w1 = static_cast<const __bf16*>(w1_packed);
+  a.b1 = static_cast<const __bf16*>(b1);
+  a.w2 = static_cast<const __bf16*>(w2_packed);
+  a.b2 = static_cast<const __bf16*>(b2);
+  a.ln_w = static_cast<const __bf16*>(ln_weight);
+  a.ln_b = static_cast<const __bf16*>(ln_bias);
+  a.eps = eps;
+  a.x_out = static_cast<__bf16*>(x_out);
+  a.ln = static_cast<__bf16*>(ln);
+  a.m = (int)m;
+  a.ldh = (int)ldh;
+  if (rows == 0) {
+    // Rows a workgroup: every workgroup streams all 1 MiB of weights through its CU's
+    // L1, which bounds the kernel, so the tile that leaves each CU the fewest rows (rounds
+    // of one workgroup a CU x rows), the smaller on a tie.  Measured (us, 32 / 48 / 64
+    // rows): 8,192 rows 24.9 / 29.6 / 36.1; 12,288: 33.6 / 31.9 / 37.3; 16,384: 36.5 / 44.1
+    // / 39.9.
+    int cus = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) {
+      int n = 0;
+      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+          n > 0)
+        cus = n;
+    }
+    int64_t best = -1;
+    for (int r : {32, 48, 64}) {
+      const int64_t load = ((m + r - 1) / r + cus - 1) / cus * r;
+      if (best < 0 || load < best) {
+        best = load;
+        rows = r;
+      }
+    }
+  }
+  // K steps of weights in flight: 3 -> 5 took 12,288 rows from 33.2 to 31.9 us (48-row
+  // tiles), 7 no further
+  const auto grid = [&](int r) { return (unsigned)((m + r - 1) / r); };
+  switch (rows) {
+    case 32: ffn::ffn_kernel<2, 5><<<grid(32), ffn::kThreads, 0, stream>>>(a); break;
+    case 48: ffn::ffn_kernel<3, 5><<<grid(48), ffn::kThreads, 0, stream>>>(a); break;
+    case 64: ffn::ffn_kernel<4, 5><<<grid(64), ffn::kThreads, 0, stream>>>(a); break;
+    default: return -6;
+  }
+  return (int)hipGetLastError();
 }
 
 }  // extern "C"

@@ -936,6 +936,56 @@ std::vector<torch::Tensor> linear_add_layernorm(torch::Tensor x, torch::Tensor w
   return {x_out, ln};
 }
 
+// ffn(h [m, 256], x [m, 256], w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, rows,
+// out) -> (x_out, ln): the feed-forward half of a pre-norm layer with the residual add and
+// the next norm (python/cugo_seq50.py:319-322) in one launch (cugo_ffn); without
+// ln_weight, ln is an empty tensor and x_out = x + linear2(GELU(linear1(h))).  `out`, if
+// given, receives x_out (it may be x).
+std::vector<torch::Tensor> ffn(torch::Tensor h, torch::Tensor x, torch::Tensor w1_packed,
+                               torch::Tensor b1, torch::Tensor w2_packed, torch::Tensor b2,
+                               c10::optional<torch::Tensor> ln_weight,
+                               c10::optional<torch::Tensor> ln_bias, double eps, int64_t rows,
+                               c10::optional<torch::Tensor> out) {
+  TORCH_CHECK(h.is_cuda() && h.dim() == 2 && h.size(1) == 256 && h.scalar_type() == at::kBFloat16 &&
+                  h.stride(1) == 1,
+              "h must be a CUDA bfloat16 [m, 256] tensor with unit stride along its columns");
+  const int64_t m = h.size(0);
+  TORCH_CHECK(x.is_contiguous() && x.dim() == 2 && x.size(0) == m && x.size(1) == 256 &&
+                  x.scalar_type() == at::kBFloat16,
+              "x must be a contiguous bfloat16 [m, 256] tensor");
+  TORCH_CHECK(w1_packed.scalar_type() == at::kBFloat16 && w1_packed.is_contiguous() &&
+                  w1_packed.numel() == 1024 * 256 && w2_packed.scalar_type() == at::kBFloat16 &&
+                  w2_packed.is_contiguous() && w2_packed.numel() == 256 * 1024,
+              "w1_packed and w2_packed must be the packed bfloat16 [1024, 256] and [256, 1024] "
+              "weights");
+  TORCH_CHECK(b1.scalar_type() == at::kBFloat16 && b1.is_contiguous() && b1.numel() == 1024 &&
+                  b2.scalar_type() == at::kBFloat16 && b2.is_contiguous() && b2.numel() == 256,
+              "b1 and b2 must be contiguous bfloat16 [1024] and [256] tensors");
+  TORCH_CHECK(ln_weight.has_value() == ln_bias.has_value(), "ln_weight and ln_bias go together");
+  for (const auto* t : {&x, &w1_packed, &b1, &w2_packed, &b2}) check_same_device(h, *t, "h", "an input");
+  if (ln_weight.has_value()) {
+    TORCH_CHECK(ln_weight->scalar_type() == at::kBFloat16 && ln_bias->scalar_type() == at::kBFloat16 &&
+                    ln_weight->numel() == 256 && ln_bias->numel() == 256 &&
+                    ln_weight->is_contiguous() && ln_bias->is_contiguous(),
+                "ln_weight and ln_bias must be contiguous bfloat16 [256] tensors");
+    check_same_device(h, *ln_weight, "h", "ln_weight");
+    check_same_device(h, *ln_bias, "h", "ln_bias");
+  }
+  const DeviceGuard guard(h.device());
+  auto x_out = out_or_new(out, {m, 256}, at::kBFloat16, h, "out");
+  auto ln = ln_weight.has_value() ? torch::empty({m, 256}, on(h, at::kBFloat16))
+                                  : torch::empty({0}, on(h, at::kBFloat16));
+  const int64_t ldh = m > 1 ? h.stride(0) : 256;
+  check_call(cugo_ffn(h.data_ptr(), ldh, x.data_ptr(), w1_packed.data_ptr(), b1.data_ptr(),
+                      w2_packed.data_ptr(), b2.data_ptr(),
+                      ln_weight.has_value() ? ln_weight->data_ptr() : nullptr,
+                      ln_bias.has_value() ? ln_bias->data_ptr() : nullptr, static_cast<float>(eps),
+                      m, x_out.data_ptr(), ln_weight.has_value() ? ln.data_ptr() : nullptr,
+                      static_cast<int>(rows), stream()),
+             "ffn");
+  return {x_out, ln};
+}
+
 // paired_select(active, status, done, any_legal, player, a_seat, act_a, act_b, bad,
 // any_active) -> actions int64 [n]; paired_update(active, step_status, new_done, reward0,
 // nagari, final_reward0, final_nagari, bad, any_active, steps): the bookkeeping of a
@@ -1550,6 +1600,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
       .def("advance", &SelfPlayState::advance)
       .def("set_noise_epoch", &SelfPlayState::set_noise_epoch)
       .def("set_event_pos", &SelfPlayState::set_event_pos);
+  m.def("ffn", &ffn,
+        "linear1 + GELU + linear2 + residual add (+ the next LayerNorm) in one launch",
+        pybind11::arg("h"), pybind11::arg("x"), pybind11::arg("w1_packed"), pybind11::arg("b1"),
+        pybind11::arg("w2_packed"), pybind11::arg("b2"),
+        pybind11::arg("ln_weight") = pybind11::none(), pybind11::arg("ln_bias") = pybind11::none(),
+        pybind11::arg("eps") = 1e-5, pybind11::arg("rows") = 0,
+        pybind11::arg("out") = pybind11::none());
   m.def("paired_select", &paired_select,
         "paired evaluation: observe checks and each game's action from its mover's model");
   m.def("paired_update", &paired_update,

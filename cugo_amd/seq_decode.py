@@ -7,9 +7,10 @@ like it: `model.encoder.layers` of pre-norm `nn.TransformerEncoderLayer`s
 -> linear2) and a cache with `k`, `v` ([layers, rows, heads, slots, dh]), `length`,
 `heads`, `slots`, `row_ids`.  The per-layer `index_put_` of the new key/value and the
 decode attention run as one HIP launch (`decode_attention_append`, reading q, k and v in
-place from the packed in-projection), each bf16 linear layer as one (`linear`, linear1
-with the GELU after it), and out_proj / linear2 with the residual add and the pre-norm
-that follows them as one (`linear_add_layernorm`).
+place from the packed in-projection), each bf16 linear layer as one (`linear`), out_proj
+with the residual add and the pre-norm that follows it as one (`linear_add_layernorm`), and
+the feed-forward half (linear1, GELU, linear2, the residual add and the next norm) as one
+(`ffn`, the hidden layer kept on chip).
 
 `KVCache` mirrors the reference cache (python/cugo_seq50.py:325-339) with the slot count
 as a parameter (the reference fixes it at MAX_EVENTS + 2 = 50).
@@ -157,6 +158,47 @@ def linear_add_norm(u: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | 
     return add_norm(x, linear(u, weight, bias), norm)
 
 
+def _fits_ffn(layer, h: torch.Tensor, x: torch.Tensor, norm: nn.Module | None) -> bool:
+    """The shapes `ffn` takes: bf16 rows 256 wide, a 1,024-wide hidden layer with the exact
+    GELU, and (when given) an affine bf16 LayerNorm over 256 columns."""
+    l1, l2 = layer.linear1, layer.linear2
+    return (h.dim() == 2 and h.is_cuda and h.dtype == torch.bfloat16 and h.shape[1] == 256
+            and h.stride(1) == 1 and (h.shape[0] <= 1 or h.stride(0) % 8 == 0)
+            and h.data_ptr() % 16 == 0 and x.dtype == torch.bfloat16 and x.is_contiguous()
+            and x.shape == h.shape and is_exact_gelu(layer.activation)
+            and tuple(l1.weight.shape) == (1024, 256) and tuple(l2.weight.shape) == (256, 1024)
+            and l1.weight.dtype == torch.bfloat16 and l2.weight.dtype == torch.bfloat16
+            and l1.bias is not None and l2.bias is not None
+            and l1.bias.dtype == torch.bfloat16 and l2.bias.dtype == torch.bfloat16
+            and (norm is None or (isinstance(norm, nn.LayerNorm) and norm.weight is not None
+                                  and norm.bias is not None
+                                  and norm.weight.dtype == torch.bfloat16
+                                  and tuple(norm.normalized_shape) == (256,))))
+
+
+def feed_forward(layer, h: torch.Tensor, x: torch.Tensor, norm: nn.Module | None = None):
+    """x + linear2(activation(linear1(h))) of a pre-norm encoder layer
+    (python/cugo_seq50.py:319-322), h = norm2(x), and with `norm` also norm of that:
+    returns x_out, or (x_out, norm(x_out)).  One HIP launch (`ffn`, the hidden layer kept
+    on chip) for the d = 256, 1,024-wide bf16 layer; linear (GELU) and linear_add_norm /
+    linear with the residual otherwise, which give the same bits."""
+    if _fits_ffn(layer, h, x, norm):
+        l1, l2 = layer.linear1, layer.linear2
+        out = _ext().ffn(h, x, packed_weight(l1.weight), l1.bias.detach(),
+                         packed_weight(l2.weight), l2.bias.detach(),
+                         None if norm is None else norm.weight.detach(),
+                         None if norm is None else norm.bias.detach(),
+                         1e-5 if norm is None else norm.eps)
+        return out[0] if norm is None else (out[0], out[1])
+    if is_exact_gelu(layer.activation):
+        u = linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True)
+    else:
+        u = layer.activation(linear(h, layer.linear1.weight, layer.linear1.bias))
+    if norm is None:
+        return linear(u, layer.linear2.weight, layer.linear2.bias, residual=x)
+    return linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x, norm)
+
+
 def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = None,
                 rows: torch.Tensor | None = None, pos: torch.Tensor | None = None) -> torch.Tensor:
     """One token per cache row (x [n, d]); its key/value go to slot cache.length[row].
@@ -187,15 +229,10 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
                                     row_ids)
         x, h = linear_add_norm(a.reshape(n, d), attn.out_proj.weight, attn.out_proj.bias, x,
                                layer.norm2)
-        if is_exact_gelu(layer.activation):
-            u = linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True)
-        else:
-            u = layer.activation(linear(h, layer.linear1.weight, layer.linear1.bias))
         if i + 1 < len(layers):
-            x, h = linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x,
-                                   layers[i + 1].norm1)
+            x, h = feed_forward(layer, h, x, layers[i + 1].norm1)
         else:
-            x = linear(u, layer.linear2.weight, layer.linear2.bias, residual=x)
+            x = feed_forward(layer, h, x)
     return x
 
 
@@ -227,15 +264,10 @@ def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a
                                 rows_b, out=att[split:])
         x, h = linear_add_norm(att.view(n, d), sa.out_proj.weight, sa.out_proj.bias, x,
                                layer.norm2)
-        if is_exact_gelu(layer.activation):
-            u = linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True)
-        else:
-            u = layer.activation(linear(h, layer.linear1.weight, layer.linear1.bias))
         if i + 1 < len(layers):
-            x, h = linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x,
-                                   layers[i + 1].norm1)
+            x, h = feed_forward(layer, h, x, layers[i + 1].norm1)
         elif final_norm is not None:
-            return linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x, final_norm)
+            return feed_forward(layer, h, x, final_norm)
         else:
-            x = linear(u, layer.linear2.weight, layer.linear2.bias, residual=x)
+            x = feed_forward(layer, h, x)
     return x

@@ -373,6 +373,22 @@ int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
                               const void* bias, int64_t m, int64_t n, int64_t k, const void* res,
                               const void* ln_weight, const void* ln_bias, float eps,
                               void* x_out, void* ln, int tile, hipStream_t stream);
+/* cugo_ffn: the feed-forward half of a pre-norm encoder layer of SeqNet.cached_step
+ * (cugo_seq50.py:319-322) with the norm after it, in one launch, for d_model 256 and a
+ * 1,024-wide hidden layer: u = GELU(h w1^T + b1) (each rounded to bf16 as cugo_linear
+ * with CUGO_LINEAR_GELU), y = bf16(u w2^T + b2), x_out = bf16(x + y), and with ln_weight
+ * ln = LayerNorm(x_out) * ln_weight + ln_bias (the next layer's norm1 or the final norm,
+ * as cugo_linear_add_layernorm).  The same bits as cugo_linear (GELU) followed by
+ * cugo_linear_add_layernorm (or by cugo_linear with the residual, when ln_weight and
+ * ln_bias are NULL); the hidden layer never leaves the chip.  h [m, 256] with row stride
+ * ldh (16-byte aligned); x, x_out, ln contiguous [m, 256] (x_out may alias x); w1_packed
+ * the [1,024, 256] linear1 weight and w2_packed the [256, 1,024] linear2 weight in
+ * cugo_mlp_pack_weight form (rows_pad = rows, cols_pad = cols); b1 [1,024], b2 [256],
+ * ln_weight / ln_bias [256]; all bf16.  rows: rows a workgroup (32, 48 or 64; 0 chooses by
+ * m).  No reference counterpart as one call. */
+int cugo_ffn(const void* h, int64_t ldh, const void* x, const void* w1_packed, const void* b1,
+             const void* w2_packed, const void* b2, const void* ln_weight, const void* ln_bias,
+             float eps, int64_t m, void* x_out, void* ln, int rows, hipStream_t stream);
 /* cugo_gumbel_sample: the sampling of WaveCollector._step (cugo_seq_selfplay50.py:125-130)
  * given the uniforms torch.rand_like drew: masked = legal ? logits : -1e30;
  * actions[i] = argmax_a(masked - log(-log(clamp(u, 1e-20, 1)))) (first index on ties);

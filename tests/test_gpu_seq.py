@@ -306,6 +306,57 @@ def test_linear_add_layernorm_equals_its_two_launches(ext, m, k):
                                          None, res, norm.weight, norm.bias, norm.eps)
 
 
+@pytest.mark.parametrize("m", [1, 37, 4096 + 5, 12288])
+def test_ffn_equals_its_two_launches(ext, m):
+    """ffn (linear1 + GELU + linear2 + residual add + next LayerNorm in one launch) ==
+    linear(gelu=True) then linear_add_layernorm, bit for bit (x_out and ln), on every row
+    tile; without the norm == linear(gelu=True) then linear with the residual; in place
+    (x_out over x); and within bf16 tolerance of the torch layer; through the module-level
+    feed_forward of a torch encoder layer."""
+    from cugo_amd.seq_decode import feed_forward
+
+    announce(f"ffn m={m}")
+    g = torch.Generator(device="cpu").manual_seed(m + 3)
+    h = torch.randn(m, 256, generator=g).to(torch.bfloat16).to(DEV)
+    x = (torch.randn(m, 256, generator=g) * 2.0).to(torch.bfloat16).to(DEV)
+    w1 = (torch.randn(1024, 256, generator=g) * 256 ** -0.5).to(torch.bfloat16).to(DEV)
+    b1 = (torch.randn(1024, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    w2 = (torch.randn(256, 1024, generator=g) * 1024 ** -0.5).to(torch.bfloat16).to(DEV)
+    b2 = (torch.randn(256, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    norm = torch.nn.LayerNorm(256).to(DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_((torch.randn(256, generator=g) * 0.3 + 1.0).to(torch.bfloat16))
+        norm.bias.copy_((torch.randn(256, generator=g) * 0.1).to(torch.bfloat16))
+        w1p, w2p = ext.mlp_pack_weight(w1, 1024, 256), ext.mlp_pack_weight(w2, 256, 1024)
+        u = ext.linear(h, w1p, 1024, b1, True)
+        want_x, want_ln = ext.linear_add_layernorm(u, w2p, b2, x, norm.weight, norm.bias, norm.eps)
+        want_plain = ext.linear(u, w2p, 256, b2, False, residual=x)
+        for rows in (0, 32, 48, 64):
+            xo, ln = ext.ffn(h, x, w1p, b1, w2p, b2, norm.weight, norm.bias, norm.eps, rows)
+            assert torch.equal(xo, want_x) and torch.equal(ln, want_ln), rows
+            plain, empty = ext.ffn(h, x, w1p, b1, w2p, b2, rows=rows)
+            assert torch.equal(plain, want_plain) and empty.numel() == 0, rows
+        inplace = x.clone()
+        got = ext.ffn(h, inplace, w1p, b1, w2p, b2, norm.weight, norm.bias, norm.eps,
+                      out=inplace)
+        assert got[0].data_ptr() == inplace.data_ptr() and torch.equal(inplace, want_x)
+        # the torch layer, float32 from the same bf16 values
+        ref_u = torch.nn.functional.gelu(h.float() @ w1.float().T + b1.float())
+        ref_x = x.float() + ref_u @ w2.float().T + b2.float()
+        assert rel_err(want_x, ref_x) <= 1e-2
+        # the module-level form on a torch encoder layer's parameters
+        layer = torch.nn.TransformerEncoderLayer(256, 8, 1024, dropout=0.0, activation="gelu",
+                                                 batch_first=True, norm_first=True)
+        layer = layer.to(DEV).to(torch.bfloat16)
+        layer.linear1.weight.copy_(w1)
+        layer.linear1.bias.copy_(b1)
+        layer.linear2.weight.copy_(w2)
+        layer.linear2.bias.copy_(b2)
+        fx, fln = feed_forward(layer, h, x, norm)
+        assert torch.equal(fx, want_x) and torch.equal(fln, want_ln)
+        assert torch.equal(feed_forward(layer, h, x), want_plain)
+
+
 def test_gumbel_sample_matches_reference(ext):
     announce("gumbel_sample")
     g = torch.Generator(device=DEV).manual_seed(3)
