@@ -659,31 +659,53 @@ def selfplay_workload(ext, torch, wave: int = 4096, waves: int = 3) -> dict:
         sp.step()
     torch.cuda.synchronize()
     eager_ms = (time.perf_counter() - t1) / reps * 1e3
-    # the step's largest linear launch on its own: linear1 + GELU over the paired pass's
-    # 3 w rows (events of both seats and the queries), HIP events around 20 launches
-    from cugo_amd.seq_decode import linear, packed_weight
+    # the step's largest launch on its own: a layer's feed-forward half (ffn: linear1,
+    # GELU, linear2, the residual add and the next norm) over the paired pass's 3 w rows
+    # (events of both seats and the queries), HIP events around 20 launches; beside it the
+    # two launches it replaces (linear + GELU, linear_add_layernorm)
+    from cugo_amd.seq_decode import feed_forward, linear, linear_add_norm
 
-    lin = policy.encoder.layers[0].linear1
-    h = torch.randn(3 * wave, lin.in_features, device=dev).to(torch.bfloat16)
-    packed_weight(lin.weight)
-    linear(h, lin.weight, lin.bias, gelu=True)
+    layer, nxt = policy.encoder.layers[0], policy.encoder.layers[1].norm1
+    m = 3 * wave
+    h = torch.randn(m, 256, device=dev).to(torch.bfloat16)
+    x = torch.randn(m, 256, device=dev).to(torch.bfloat16)
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with region("f1.linear"):
-        e0.record(stream)
-        for _ in range(20):
-            linear(h, lin.weight, lin.bias, gelu=True)
-        e1.record(stream)
+
+    def launch_us(fn, name: str) -> float:
+        fn()
         torch.cuda.synchronize()
-    lin_us = e0.elapsed_time(e1) * 1e3 / 20
-    m, k, nn_ = 3 * wave, lin.in_features, lin.out_features
-    lin_bytes = 2 * (m * k + nn_ * k + m * nn_) + 2 * nn_
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with region(name):
+            e0.record(stream)
+            for _ in range(20):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / 20
+
+    ffn_us = launch_us(lambda: feed_forward(layer, h, x, nxt), "f1.ffn")
+    u = linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True)
+    two_us = (launch_us(lambda: linear(h, layer.linear1.weight, layer.linear1.bias, gelu=True),
+                        "f1.linear1")
+              + launch_us(lambda: linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x,
+                                                  nxt), "f1.linear2"))
+    ffn_flops = 2 * m * (256 * 1024 + 1024 * 256)
+    ffn_hbm = 2 * (4 * m * 256 + 2 * 256 * 1024 + 1024 + 3 * 256)
+    rows_wg = 48 if m == 12288 else None
+    wgs = (m + 47) // 48 if rows_wg else None
     return {"games_per_s": round(wave * waves / wall, 1),
-            "linear_roofline": {"kernel": f"linear_kernel (linear1 + GELU, {m} x {nn_} x {k} bf16)",
-                                "bound": "hbm", "achieved": round(lin_bytes / lin_us / 1e3, 1),
-                                "peak": 8000.0, "unit": "GB/s",
-                                "frac": round(lin_bytes / lin_us / 1e3 / 8000.0, 4),
-                                "us_per_launch": round(lin_us, 2), "traffic": None},
+            "ffn_roofline": {
+                "kernel": f"ffn_kernel (linear1 + GELU + linear2 + residual + LayerNorm, {m} "
+                          "rows, 256 -> 1024 -> 256, bf16)",
+                "bound": "mfma", "achieved": round(ffn_flops / ffn_us / 1e6, 1),
+                "peak": 2500.0, "unit": "TFLOP/s",
+                "frac": round(ffn_flops / ffn_us / 1e6 / 2500.0, 4), "traffic": None,
+                "us_per_launch": round(ffn_us, 2),
+                "two_launch_us": round(two_us, 2),
+                "hbm_gbs": round(ffn_hbm / ffn_us / 1e3, 1),
+                # every workgroup streams all of W1 and W2 (1 MiB) through its CU's L1
+                "l1_weight_gbs": (round(wgs * (1 << 20) / ffn_us / 1e3, 1) if wgs else None),
+                "workgroups": wgs},
             "steps_per_wave": round(steps / waves, 2),
             "decision_steps_per_s": round(wave * steps / wall, 1),
             "tokens_per_s": round(3 * wave * steps / wall, 1),

@@ -385,7 +385,9 @@ int launch(const Args& base, int k, int act, hipStream_t stream) {
 // FLOPs a weight byte buys are the tile's rows), ~20 bytes a cycle a CU when every CU
 // reads the same weights at once; the GELU's erff is ~5 us of VALU at 12,288 rows (the
 // launch without it: 20.5 against 26.1 us).  At 12,288 rows the launch takes 32 us
-// against 43 for the two launches it replaces.
+// against 43 for the two launches it replaces.  A GELU table in LDS (gelu() of the 4,736
+// bf16 inputs without a closed form, built by each workgroup, then looked up; the same bits
+// on every finite input) made the launch slower: 39.6 against 31.9 us at 12,288 rows.
 // Weights: linear_kernel's packed fragments, W1 [1,024, 256] (8 K steps a 16-row tile)
 // and W2 [256, 1,024] (32 K steps a tile), read through buffer loads a few K steps ahead
 // of the MFMAs.
