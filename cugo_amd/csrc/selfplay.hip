@@ -476,6 +476,27 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   wave.rec_valid[rec] = active && (i >= wave.pool_games || p == wave.learner_seat[i]);
 }
 
+// cugo_query_input: [features (the kept columns), legal as 0/1] in the policy dtype,
+// zero-padded to q_stride columns (SeqNet._query's input, cugo_seq50.py:166-180).  One
+// wavefront per row; a column index outside [0, 720) gives NaN (no read outside the row).
+template <class T>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void query_input_kernel(
+    const float* features, const uint8_t* legal, const int32_t* columns, int width,
+    int q_stride, i64 n, typename T::storage* q_in) {
+  const int lane = threadIdx.x & 63;
+  const i64 i = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
+  if (i >= n) return;
+  const float* f = features + i * kFeatures;
+  typename T::storage* q = q_in + i * q_stride;
+  for (int j = lane; j < width; j += 64) {
+    const int c = columns != nullptr ? columns[j] : j;  // a column outside the features: NaN
+    q[j] = T::from_float(c >= 0 && c < kFeatures ? f[c] : __builtin_nanf(""));
+  }
+  const uint8_t* g = legal + i * kActions;
+  for (int j = lane; j < kActions; j += 64) q[width + j] = T::from_float(g[j] != 0 ? 1.0f : 0.0f);
+  for (int j = width + kActions + lane; j < q_stride; j += 64) q[j] = T::from_float(0.0f);
+}
+
 // After the engine step (:146-163): bad += active & (step status != OK); a game that
 // finished now keeps its reward and nagari flag and is marked finished; a committed
 // action's event goes to slot min(count, 47) of the log, and both seats' cache lengths
@@ -870,6 +891,26 @@ int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8
     prepare_kernel<F32><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
         *wave, reinterpret_cast<const u64*>(states), features, legal, player, done, status,
         stock, (float*)q_in, query_rows);
+  else
+    return -2;
+  return (int)hipGetLastError();
+}
+
+int cugo_query_input(int q_dtype, const float* features, const uint8_t* legal,
+                     const int32_t* columns, int64_t width, int64_t n, void* q_in,
+                     int64_t q_stride, hipStream_t stream) {
+  if (n < 0 || width < 1 || width > kFeatures || (columns == nullptr && width != kFeatures) ||
+      q_stride < width + kActions || q_stride > (1 << 16) ||
+      (n > 0 && (!features || !legal || !q_in)))
+    return -1;
+  if (n == 0) return 0;
+  const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
+  if (q_dtype == CUGO_DTYPE_BF16)
+    query_input_kernel<BF16><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
+        features, legal, columns, (int)width, (int)q_stride, n, (uint16_t*)q_in);
+  else if (q_dtype == CUGO_DTYPE_F32)
+    query_input_kernel<F32><<<grid, 64 * kRowsPerBlock, 0, stream>>>(
+        features, legal, columns, (int)width, (int)q_stride, n, (float*)q_in);
   else
     return -2;
   return (int)hipGetLastError();

@@ -936,6 +936,41 @@ std::vector<torch::Tensor> linear_add_layernorm(torch::Tensor x, torch::Tensor w
   return {x_out, ln};
 }
 
+// query_input(features f32 [n, 720], legal bool [n, 179], columns int32 [width] or None,
+// q_in [n, q_stride] bf16/f32): SeqNet._query's input rows, zero-padded (cugo_query_input).
+void query_input(torch::Tensor features, torch::Tensor legal, c10::optional<torch::Tensor> columns,
+                 torch::Tensor q_in) {
+  TORCH_CHECK(features.is_cuda() && features.is_contiguous() && features.dim() == 2 &&
+                  features.size(1) == CUGO_FEATURE_COUNT && features.scalar_type() == at::kFloat,
+              "features must be a contiguous CUDA float32 [n, 720] tensor");
+  const int64_t n = features.size(0);
+  TORCH_CHECK(legal.is_contiguous() && legal.dim() == 2 && legal.size(0) == n &&
+                  legal.size(1) == CUGO_ACTION_COUNT && legal.scalar_type() == at::kBool,
+              "legal must be a contiguous bool [n, 179] tensor");
+  int64_t width = CUGO_FEATURE_COUNT;
+  const int32_t* cols = nullptr;
+  if (columns.has_value()) {
+    TORCH_CHECK(columns->is_contiguous() && columns->dim() == 1 &&
+                    columns->scalar_type() == at::kInt && columns->numel() >= 1 &&
+                    columns->numel() <= CUGO_FEATURE_COUNT,
+                "columns must be a contiguous int32 vector of at most 720 feature columns");
+    check_same_device(features, *columns, "features", "columns");
+    width = columns->numel();
+    cols = columns->data_ptr<int32_t>();
+  }
+  TORCH_CHECK(q_in.is_contiguous() && q_in.dim() == 2 && q_in.size(0) == n &&
+                  q_in.size(1) >= width + CUGO_ACTION_COUNT &&
+                  (q_in.scalar_type() == at::kBFloat16 || q_in.scalar_type() == at::kFloat),
+              "q_in must be a contiguous bfloat16 or float32 [n, >= width + 179] tensor");
+  check_same_device(features, legal, "features", "legal");
+  check_same_device(features, q_in, "features", "q_in");
+  const DeviceGuard guard(features.device());
+  check_call(cugo_query_input(q_in.scalar_type() == at::kBFloat16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32,
+                              features.data_ptr<float>(), u8p(legal), cols, width, n,
+                              q_in.data_ptr(), q_in.size(1), stream()),
+             "query_input");
+}
+
 // ffn(h [m, 256], x [m, 256], w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, rows,
 // out) -> (x_out, ln): the feed-forward half of a pre-norm layer with the residual add and
 // the next norm (python/cugo_seq50.py:319-322) in one launch (cugo_ffn); without
@@ -1600,6 +1635,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
       .def("advance", &SelfPlayState::advance)
       .def("set_noise_epoch", &SelfPlayState::set_noise_epoch)
       .def("set_event_pos", &SelfPlayState::set_event_pos);
+  m.def("query_input", &query_input, "SeqNet._query's input rows, zero-padded, into q_in",
+        pybind11::arg("features"), pybind11::arg("legal"), pybind11::arg("columns"),
+        pybind11::arg("q_in"));
   m.def("ffn", &ffn,
         "linear1 + GELU + linear2 + residual add (+ the next LayerNorm) in one launch",
         pybind11::arg("h"), pybind11::arg("x"), pybind11::arg("w1_packed"), pybind11::arg("b1"),

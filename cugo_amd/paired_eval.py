@@ -90,7 +90,8 @@ class _SequenceSeat:
     waiting event tokens go to, and the query input rows (features ++ legal in the policy
     dtype, zero-padded to a width `linear` takes)."""
 
-    def __init__(self, model: nn.Module, seat: torch.Tensor, games: int, dev) -> None:
+    def __init__(self, model: nn.Module, seat: torch.Tensor, games: int, dev,
+                 q_inputs: dict) -> None:
         from .seq_selfplay import ACTIONS, FEATURES, policy_cache
 
         for name in ("query_from_input", "event_token", "start_token", "readout", "prepare"):
@@ -107,11 +108,17 @@ class _SequenceSeat:
         self.event_pos = torch.full((games,), -1, dtype=torch.int64, device=dev)
         self.query_pos = torch.full((games,), -1, dtype=torch.int64, device=dev)
         cols = model.kept_columns()
-        self.columns = None if cols is None else torch.tensor(cols, device=dev)
-        self.width = FEATURES if cols is None else len(cols)
-        need = self.width + ACTIONS
+        width = FEATURES if cols is None else len(cols)
+        need = width + ACTIONS
         stride = next((k for k in (64, 128, 256, 512, 1024) if k >= need), need)
-        self.q_in = torch.zeros((games, stride), dtype=dtype, device=dev)
+        # the query input rows, shared by the policies that read the same columns in the
+        # same dtype (filled once a step)
+        key = (None if cols is None else tuple(cols), dtype, stride)
+        if key not in q_inputs:
+            q_inputs[key] = (None if cols is None else
+                             torch.tensor(cols, dtype=torch.int32, device=dev),
+                             torch.zeros((games, stride), dtype=dtype, device=dev))
+        self.columns, self.q_in = q_inputs[key]
         self.ids = torch.arange(games, device=dev)
         model.prepare()
 
@@ -125,18 +132,16 @@ class _SequenceSeat:
         self.event_pos.fill_(-1)
         torch.where(active, cache.length, torch.full_like(cache.length, -1), out=self.query_pos)
 
-    def logits(self, features: torch.Tensor, legal: torch.Tensor) -> torch.Tensor:
+    def logits(self) -> torch.Tensor:
         """The last step's kept event tokens and the query of every game still being played
-        through the layers together (the queries attend the events' keys at every layer),
-        then the readout of the queries: [games, 179] logits in the policy dtype (NaN in
-        the rows of games that are over, whose rows the decode skips: no cache read or
-        write; nothing reads those logits)."""
+        (its input rows in `q_in`, filled this step) through the layers together (the
+        queries attend the events' keys at every layer), then the readout of the queries:
+        [games, 179] logits in the policy dtype (NaN in the rows of games that are over,
+        whose rows the decode skips: no cache read or write; nothing reads those
+        logits)."""
         from .seq_decode import cached_step_pair
 
         m, g = self.model, self.games
-        kept = features if self.columns is None else features.index_select(1, self.columns)
-        self.q_in[:, :self.width].copy_(kept)
-        self.q_in[:, self.width:self.width + legal.shape[1]].copy_(legal)
         m.query_from_input(self.q_in, out=self.pair[g:])
         hidden, normed = cached_step_pair(m, self.cache, self.pair, g, self.event_pos,
                                           self.query_pos, self.ids, final_norm=m.norm)
@@ -224,7 +229,8 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
     # Sequence policies keep their event histories as KV caches, one row per game for the
     # seat they play (A: a_seat, B: the other); both models may be one module.
     ids = torch.arange(games, device=dev)
-    seq_seats = [(_SequenceSeat(m, a_seat if k == 0 else 1 - a_seat, games, dev)
+    q_inputs: dict = {}  # (columns, dtype, stride) -> (int32 columns, query input rows)
+    seq_seats = [(_SequenceSeat(m, a_seat if k == 0 else 1 - a_seat, games, dev, q_inputs)
                   if seq[k] else None) for k, m in enumerate((model_a, model_b))]
     histories = [s for s in seq_seats if s is not None]
     count = torch.zeros(games, dtype=torch.int64, device=dev)  # committed events per game
@@ -236,7 +242,7 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
 
     def logits_actions(k: int, model, features, legal, sample: bool):
         if seq_seats[k] is not None:
-            logits = seq_seats[k].logits(features, legal)
+            logits = seq_seats[k].logits()
         else:
             with torch.autocast(device_type="cuda", dtype=torch.float16, enabled=use_amp):
                 out = model(features)
@@ -248,6 +254,8 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         # the checks, the count and the per-game choice of model are one launch before the
         # step and one after it (paired_select / paired_update, selfplay.hip)
         features, legal, players, done, status = ext.observe(states)
+        for columns, q_in in q_inputs.values():  # the sequence policies' query input rows
+            ext.query_input(features, legal, columns, q_in)
         act_a = logits_actions(0, model_a, features, legal, sample_a)
         act_b = logits_actions(1, model_b, features, legal, sample_b)
         actions = ext.paired_select(active, status, done, legal.any(1), players, a_seat, act_a,

@@ -496,10 +496,13 @@ typedef struct CugoSelfPlayWave {
                                      cugo_selfplay_advance (the epoch of the step's Philox
                                      noise, cugo_gumbel_sample_philox) */
   int64_t* query_pos;             /* [w] or NULL: cugo_selfplay_prepare writes
-                                     cache_length[query_rows[i]], the query's cache slot */
+                                     cache_length[query_rows[i]], the query's cache slot,
+                                     or -1 for a game that is over (the decode skips it) */
   int64_t* event_pos;             /* [2 w] or NULL: cugo_selfplay_advance writes each cache
                                      row's length before the step's events are counted (the
-                                     slots the step's event tokens go to) */
+                                     slots the step's event tokens go to), or -1 where the
+                                     step's event is not kept (no committed action, or a
+                                     game already over: the decode skips the row) */
 } CugoSelfPlayWave;
 
 /* cugo_selfplay_prepare: the step's work between observe and the policy
@@ -524,6 +527,17 @@ int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8
  * distinct), 16-byte aligned; rows a multiple of 64, row_bytes a multiple of 16. */
 int cugo_store_probe(void* out, int64_t rows, int64_t row_bytes, int64_t steps, int distinct,
                      hipStream_t stream);
+
+/* cugo_query_input: the query token's input row of SeqNet._query (cugo_seq50.py:166-180)
+ * for callers outside the self-play step: q_in[i] = [features[i][columns] (or all 720),
+ * legal[i] as 0/1] in q_dtype (CUGO_DTYPE_BF16 rounded to nearest even, or CUGO_DTYPE_F32),
+ * zero-padded to q_stride >= width + 179 columns.  features f32 [n, 720], legal bool
+ * [n, 179], columns int32 [width] or NULL (width 720); a column index outside [0, 720)
+ * writes NaN.  No reference counterpart as one call (the reference concatenates with torch
+ * ops). */
+int cugo_query_input(int q_dtype, const float* features, const uint8_t* legal,
+                     const int32_t* columns, int64_t width, int64_t n, void* q_in,
+                     int64_t q_stride, hipStream_t stream);
 
 /* Paired evaluation on resident games (evaluate_paired, cugo_eval50.py:137-361, with
  * finished games masked instead of dropped; no counterpart in the reference, whose loop

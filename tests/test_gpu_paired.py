@@ -171,6 +171,32 @@ def _seq_policy(seed: int, mode: str):
     return p.to(DEV).to(torch.bfloat16).eval()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("kept", ["all", "some"])
+def test_query_input_equals_concat(ext, dtype, kept):
+    """query_input's rows equal torch's concat of the kept feature columns and the legal
+    mask, cast to the policy dtype, with the padding zeroed (the rows start as garbage)."""
+    announce(f"query_input {kept} {dtype}")
+    g = torch.Generator(device="cpu").manual_seed(5)
+    n = 3001
+    features = torch.randn((n, 720), generator=g).to(DEV)
+    legal = (torch.rand((n, 179), generator=g) < 0.3).to(DEV)
+    cols = None
+    if kept == "some":
+        cols = torch.randperm(720, generator=g)[:433].sort().values.to(torch.int32).to(DEV)
+    width = 720 if cols is None else cols.numel()
+    stride = 1024 if cols is None else 640
+    q_in = torch.full((n, stride), 7.0, dtype=dtype, device=DEV)
+    ext.query_input(features, legal, cols, q_in)
+    kept_f = features if cols is None else features.index_select(1, cols.long())
+    want = torch.zeros((n, stride), dtype=dtype, device=DEV)
+    want[:, :width] = kept_f.to(dtype)
+    want[:, width:width + 179] = legal.to(dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(q_in.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                       want.view(torch.int16 if dtype == torch.bfloat16 else torch.int32))
+
+
 def _summary(pairs, reward, nagari, excluded, steps):
     """EvalSummary's fields (cugo_eval50.py:287-361) from finished games, in numpy."""
     n = 2 * pairs
