@@ -535,11 +535,13 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
     concatenates the event logs of games i, i + 4,096, i + 8,192, ... (one opening token
     plus each game's events) until a per-row target drawn uniformly from [1, 320] is
     reached ("stress", mean pos ~170), or while they fit below 320 slots ("full", pos
-    ~300), or holds one game (the reference's 50-slot regime, "natural")."""
+    ~300), or holds one game (the reference's 50-slot regime, "natural").  The step takes
+    the queries longest first (`decode_order`, one launch a step for its 4 layers); the
+    decode kernel alone is timed with that order and in index order."""
     from torch import nn
 
-    from cugo_amd.seq_decode import KVCache, cached_step
-    from cugo_amd.cugo_seq_attention50 import decode_attention_append
+    from cugo_amd.seq_decode import KVCache, order_pays, cached_step
+    from cugo_amd.cugo_seq_attention50 import decode_attention_append, decode_order
 
     dev = torch.device("cuda")
     layers, d, heads = 4, 256, 8
@@ -577,21 +579,39 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
                     cached_step(model, cache, x)
                 torch.cuda.synchronize()
                 step_s = (time.perf_counter() - t0) / steps
-            # The decode kernel alone, same call as inside the step (layer 0's cache).
+            # The decode kernel alone, same call as inside the step (layer 0's cache, the
+            # step's query order: longest first, one order launch a step for 4 layers).
             q = (torch.randn(rows, heads, dh, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
             kn, vn = q.clone(), q.clone()
             pos = lengths[name].clamp_max(slots - 1)
-            for _ in range(3):
-                decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos)
-            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            order = decode_order(pos, slots) if order_pays(rows, slots) else None
             reps = 50
-            with region(f"c5.decode_{name}"):
+
+            def burst(label, order):
+                for _ in range(3):
+                    decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos, order=order)
+                ev0 = torch.cuda.Event(enable_timing=True)
+                ev1 = torch.cuda.Event(enable_timing=True)
+                with region(label):
+                    ev0.record(stream)
+                    for _ in range(reps):
+                        decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos,
+                                                order=order)
+                    ev1.record(stream)
+                    torch.cuda.synchronize()
+                return ev0.elapsed_time(ev1) / reps
+
+            kernel_ms = burst(f"c5.decode_{name}", order)
+            unordered_ms = burst(f"c5.decode_{name}_unordered", None) if order is not None else None
+            order_ms = None
+            if order is not None:
+                ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 ev0.record(stream)
                 for _ in range(reps):
-                    decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos)
+                    decode_order(pos, slots)
                 ev1.record(stream)
                 torch.cuda.synchronize()
-            kernel_ms = ev0.elapsed_time(ev1) / reps
+                order_ms = ev0.elapsed_time(ev1) / reps
             # cache reads (slots < pos; slot pos comes from registers) + q, k_new, v_new
             # reads + k/v slot writes + out writes + pos
             row_bytes = heads * dh * 2
@@ -607,6 +627,9 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
                          "mean_pos": round(float(pos.float().mean()), 2),
                          "max_pos": int(pos.max()),
                          "decode_kernel_ms": round(kernel_ms, 4),
+                         "decode_kernel_ms_index_order": (round(unordered_ms, 4)
+                                                          if unordered_ms is not None else None),
+                         "order_ms": round(order_ms, 4) if order_ms is not None else None,
                          "decode_bytes": nbytes,
                          }
     out["cache"] = [layers, rows, heads, slots, dh]

@@ -163,14 +163,19 @@ __device__ inline void merge(Partial<E>& a, float mo, float lo, const float (&ao
 // a wavefront's work is its row's length, so on ragged rows the longest rows end the launch
 // with few loads in flight; with P > 1 a row's chunks spread over P wavefronts and a launch
 // holds P times as many, which the dispatcher starts as others finish.
+// `order`, when given, is a permutation of the queries: the g-th group of the launch serves
+// query order[g / (heads / G)] instead of g / (heads / G).  Which workgroup serves a query
+// changes nothing in its result (the same wavefronts in the same roles); the dispatcher
+// starts workgroups in index order as others finish, so queries ordered longest first
+// (cugo_decode_order) end a ragged launch with short work.
 template <class QT, class KT, int DH, bool APPEND, int G, int P, int U = kUnroll>
 __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
     const typename QT::storage* __restrict__ q, typename KT::storage* __restrict__ keys,
     typename KT::storage* __restrict__ values, const typename KT::storage* __restrict__ k_new,
     const typename KT::storage* __restrict__ v_new, const int64_t* __restrict__ pos_in,
-    const int64_t* __restrict__ rows, typename QT::storage* __restrict__ out, int64_t groups,
-    int heads, int64_t slots, int64_t cache_rows, float scale_log2, int64_t q_stride,
-    int64_t new_stride) {
+    const int64_t* __restrict__ rows, const int32_t* __restrict__ order,
+    typename QT::storage* __restrict__ out, int64_t groups, int heads, int64_t slots,
+    int64_t cache_rows, float scale_log2, int64_t q_stride, int64_t new_stride) {
   using KS = typename KT::storage;
   constexpr int E = 16 / (int)sizeof(KS);  // elements per 16-byte part
   constexpr int L = DH / E;                // lanes per slot
@@ -196,11 +201,13 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 #pragma unroll
   for (int e = 0; e < E; ++e) st.acc[e] = 0.f;
   int64_t pair = 0;
-  if (group < groups) {  // uniform over the wavefront (and over the group's P wavefronts)
-    const int64_t pair0 = group * G;
-    const int64_t query = pair0 / heads;
-    pair = pair0 + lane / W;
-    const int head = (int)(pair - query * heads);
+  // uniform over the wavefront (and over the group's P wavefronts)
+  const int64_t slot_q = group * G / heads;  // the query's place in the launch
+  const int64_t n = groups * G / heads;
+  const int64_t query = order != nullptr && group < groups ? (int64_t)order[slot_q] : slot_q;
+  if (group < groups && query >= 0 && query < n) {  // an order entry outside [0, n): no work
+    const int head = (int)(group * G - slot_q * heads) + lane / W;
+    pair = query * heads + head;
     const int64_t row = rows ? rows[query] : query;
     int64_t pos = pos_in[query];
     if (row < 0 || row >= cache_rows || pos < 0) {
@@ -337,9 +344,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 
 template <class QT, class KT, int DH, bool APPEND, int G, int P>
 int launch_group(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
-                 const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
-                 int64_t slots, int64_t cache_rows, float scale, int64_t q_stride,
-                 int64_t new_stride, hipStream_t stream) {
+                 const int64_t* pos, const int64_t* rows, const int32_t* order, void* out,
+                 int64_t n, int64_t heads, int64_t slots, int64_t cache_rows, float scale,
+                 int64_t q_stride, int64_t new_stride, hipStream_t stream) {
   using QS = typename QT::storage;
   using KS = typename KT::storage;
   const int64_t groups = n * heads / G;
@@ -350,8 +357,8 @@ int launch_group(const void* q, void* keys, void* values, const void* k_new, con
                      dim3(64 * kWaves), 0, stream, static_cast<const QS*>(q),
                      static_cast<KS*>(keys), static_cast<KS*>(values),
                      static_cast<const KS*>(k_new), static_cast<const KS*>(v_new), pos, rows,
-                     static_cast<QS*>(out), groups, (int)heads, slots, cache_rows, scale_log2,
-                     q_stride, new_stride);
+                     order, static_cast<QS*>(out), groups, (int)heads, slots, cache_rows,
+                     scale_log2, q_stride, new_stride);
   return (int)hipGetLastError();
 }
 
@@ -366,21 +373,21 @@ inline bool split_rows(int64_t slots) { return slots > 64; }
 
 template <class QT, class KT, int DH, bool APPEND, int G>
 int launch_parts(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
-                 const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
-                 int64_t slots, int64_t cache_rows, float scale, int64_t q_stride,
-                 int64_t new_stride, hipStream_t stream) {
+                 const int64_t* pos, const int64_t* rows, const int32_t* order, void* out,
+                 int64_t n, int64_t heads, int64_t slots, int64_t cache_rows, float scale,
+                 int64_t q_stride, int64_t new_stride, hipStream_t stream) {
 #ifdef CUGO_DECODE_FORCE_PARTS
   (void)split_rows;
   return launch_group<QT, KT, DH, APPEND, G, CUGO_DECODE_FORCE_PARTS>(
-      q, keys, values, k_new, v_new, pos, rows, out, n, heads, slots, cache_rows, scale,
+      q, keys, values, k_new, v_new, pos, rows, order, out, n, heads, slots, cache_rows, scale,
       q_stride, new_stride, stream);
 #else
   if (split_rows(slots))
-    return launch_group<QT, KT, DH, APPEND, G, 2>(q, keys, values, k_new, v_new, pos, rows, out,
-                                                  n, heads, slots, cache_rows, scale, q_stride,
-                                                  new_stride, stream);
-  return launch_group<QT, KT, DH, APPEND, G, 1>(q, keys, values, k_new, v_new, pos, rows, out,
-                                                n, heads, slots, cache_rows, scale, q_stride,
+    return launch_group<QT, KT, DH, APPEND, G, 2>(q, keys, values, k_new, v_new, pos, rows,
+                                                  order, out, n, heads, slots, cache_rows, scale,
+                                                  q_stride, new_stride, stream);
+  return launch_group<QT, KT, DH, APPEND, G, 1>(q, keys, values, k_new, v_new, pos, rows, order,
+                                                out, n, heads, slots, cache_rows, scale, q_stride,
                                                 new_stride, stream);
 #endif
 }
@@ -407,41 +414,41 @@ int pick_group(int64_t heads, int64_t slots) {
 
 template <class QT, class KT, int DH, bool APPEND>
 int launch(const void* q, void* keys, void* values, const void* k_new, const void* v_new,
-           const int64_t* pos, const int64_t* rows, void* out, int64_t n, int64_t heads,
-           int64_t slots, int64_t cache_rows, float scale, int64_t q_stride, int64_t new_stride,
-           hipStream_t stream) {
+           const int64_t* pos, const int64_t* rows, const int32_t* order, void* out, int64_t n,
+           int64_t heads, int64_t slots, int64_t cache_rows, float scale, int64_t q_stride,
+           int64_t new_stride, hipStream_t stream) {
   constexpr int L = DH / (16 / (int)sizeof(typename KT::storage));
   switch (pick_group<L>(heads, slots)) {
 #define CUGO_GROUP(GG)                                                                        \
   case GG:                                                                                    \
     if constexpr (GG * L <= 64)                                                               \
       return launch_parts<QT, KT, DH, APPEND, GG>(q, keys, values, k_new, v_new, pos, rows,   \
-                                                  out, n, heads, slots, cache_rows, scale,    \
-                                                  q_stride, new_stride, stream);              \
+                                                  order, out, n, heads, slots, cache_rows,    \
+                                                  scale, q_stride, new_stride, stream);       \
     return -3;
     CUGO_GROUP(2)
     CUGO_GROUP(4)
     CUGO_GROUP(8)
 #undef CUGO_GROUP
     default:
-      return launch_parts<QT, KT, DH, APPEND, 1>(q, keys, values, k_new, v_new, pos, rows, out,
-                                                 n, heads, slots, cache_rows, scale, q_stride,
-                                                 new_stride, stream);
+      return launch_parts<QT, KT, DH, APPEND, 1>(q, keys, values, k_new, v_new, pos, rows,
+                                                 order, out, n, heads, slots, cache_rows, scale,
+                                                 q_stride, new_stride, stream);
   }
 }
 
 template <class QT, class KT, bool APPEND>
 int by_dh(int64_t dh, const void* q, void* keys, void* values, const void* k_new,
-          const void* v_new, const int64_t* pos, const int64_t* rows, void* out, int64_t n,
-          int64_t heads, int64_t slots, int64_t cache_rows, float scale, int64_t q_stride,
-          int64_t new_stride, hipStream_t stream) {
+          const void* v_new, const int64_t* pos, const int64_t* rows, const int32_t* order,
+          void* out, int64_t n, int64_t heads, int64_t slots, int64_t cache_rows, float scale,
+          int64_t q_stride, int64_t new_stride, hipStream_t stream) {
   switch (dh) {
 #define CUGO_DH(D)                                                                       \
   case D:                                                                                \
     if constexpr (16 / sizeof(typename KT::storage) <= D)                                \
-      return launch<QT, KT, D, APPEND>(q, keys, values, k_new, v_new, pos, rows, out, n, \
-                                       heads, slots, cache_rows, scale, q_stride,        \
-                                       new_stride, stream);                              \
+      return launch<QT, KT, D, APPEND>(q, keys, values, k_new, v_new, pos, rows, order, \
+                                       out, n, heads, slots, cache_rows, scale,          \
+                                       q_stride, new_stride, stream);                    \
     return -3;
     CUGO_DH(16)
     CUGO_DH(32)
@@ -456,24 +463,25 @@ int by_dh(int64_t dh, const void* q, void* keys, void* values, const void* k_new
 template <bool APPEND>
 int dispatch(int q_dtype, int kv_dtype, int64_t dh, const void* q, void* keys, void* values,
              const void* k_new, const void* v_new, const int64_t* pos, const int64_t* rows,
-             void* out, int64_t n, int64_t heads, int64_t slots, int64_t cache_rows,
-             float scale, int64_t q_stride, int64_t new_stride, hipStream_t stream) {
-#define CUGO_KV(QTYPE)                                                                      \
-  switch (kv_dtype) {                                                                       \
-    case CUGO_DTYPE_BF16:                                                                   \
-      return by_dh<QTYPE, BF16, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, out, \
-                                        n, heads, slots, cache_rows, scale, q_stride,      \
-                                        new_stride, stream);                               \
-    case CUGO_DTYPE_F16:                                                                    \
-      return by_dh<QTYPE, F16, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, out,  \
-                                       n, heads, slots, cache_rows, scale, q_stride,       \
-                                       new_stride, stream);                                \
-    case CUGO_DTYPE_F32:                                                                    \
-      return by_dh<QTYPE, F32, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, out,  \
-                                       n, heads, slots, cache_rows, scale, q_stride,       \
-                                       new_stride, stream);                                \
-    default:                                                                                \
-      return -2;                                                                            \
+             const int32_t* order, void* out, int64_t n, int64_t heads, int64_t slots,
+             int64_t cache_rows, float scale, int64_t q_stride, int64_t new_stride,
+             hipStream_t stream) {
+#define CUGO_KV(QTYPE)                                                                        \
+  switch (kv_dtype) {                                                                         \
+    case CUGO_DTYPE_BF16:                                                                     \
+      return by_dh<QTYPE, BF16, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, order,  \
+                                        out, n, heads, slots, cache_rows, scale, q_stride,    \
+                                        new_stride, stream);                                  \
+    case CUGO_DTYPE_F16:                                                                      \
+      return by_dh<QTYPE, F16, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, order,   \
+                                       out, n, heads, slots, cache_rows, scale, q_stride,     \
+                                       new_stride, stream);                                   \
+    case CUGO_DTYPE_F32:                                                                      \
+      return by_dh<QTYPE, F32, APPEND>(dh, q, keys, values, k_new, v_new, pos, rows, order,   \
+                                       out, n, heads, slots, cache_rows, scale, q_stride,     \
+                                       new_stride, stream);                                   \
+    default:                                                                                  \
+      return -2;                                                                              \
   }
   switch (q_dtype) {
     case CUGO_DTYPE_BF16:
@@ -486,6 +494,57 @@ int dispatch(int q_dtype, int kv_dtype, int64_t dh, const void* q, void* keys, v
       return -2;
   }
 #undef CUGO_KV
+}
+
+// cugo_decode_order: the queries longest first (by min(pos, slots - 1); a negative pos
+// last), binned by length: bin b holds the rows with slots - 1 - clamp(pos) in
+// [b << shift, (b + 1) << shift).  One workgroup: a histogram of the bins in LDS, an
+// exclusive scan over it, then every query takes the next place of its bin.  Places within
+// a bin go in the order the LDS atomics return them, which may differ between calls; the
+// decode's results do not depend on the order.
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderBins = 4096;
+
+__global__ __launch_bounds__(kOrderThreads) void order_kernel(const int64_t* __restrict__ pos,
+                                                              int64_t n, int64_t slots, int shift,
+                                                              int32_t* __restrict__ order) {
+  __shared__ int next[kOrderBins];  // the bins' counts, then their next free place
+  __shared__ int partial[kOrderThreads];
+  const int tid = threadIdx.x;
+  for (int b = tid; b < kOrderBins; b += kOrderThreads) next[b] = 0;
+  __syncthreads();
+  auto bin_of = [&](int64_t i) {
+    int64_t p = pos[i];
+    p = p < 0 ? -1 : (p >= slots ? slots - 1 : p);
+    return (int)((slots - 1 - p) >> shift);  // < kOrderBins by the choice of shift
+  };
+  for (int64_t i = tid; i < n; i += kOrderThreads) atomicAdd(&next[bin_of(i)], 1);
+  __syncthreads();
+  constexpr int kPer = kOrderBins / kOrderThreads;  // consecutive bins a thread scans
+  int count[kPer];
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    count[k] = next[tid * kPer + k];
+    sum += count[k];
+  }
+  partial[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < kOrderThreads; off <<= 1) {  // inclusive scan of the sums
+    const int v = tid >= off ? partial[tid - off] : 0;
+    __syncthreads();
+    partial[tid] += v;
+    __syncthreads();
+  }
+  int start = partial[tid] - sum;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    next[tid * kPer + k] = start;
+    start += count[k];
+  }
+  __syncthreads();
+  for (int64_t i = tid; i < n; i += kOrderThreads)
+    order[atomicAdd(&next[bin_of(i)], 1)] = (int32_t)i;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -506,8 +565,8 @@ extern "C" {
 
 int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, int64_t q_stride,
                           const void* keys, const void* values, const int64_t* pos,
-                          const int64_t* rows, int64_t n, int64_t heads, int64_t dh,
-                          int64_t slots, int64_t cache_rows, float scale, void* out,
+                          const int64_t* rows, const int32_t* order, int64_t n, int64_t heads,
+                          int64_t dh, int64_t slots, int64_t cache_rows, float scale, void* out,
                           hipStream_t stream) {
   using namespace cugo_amd::decode;
   const int bad = check_args(q, keys, values, pos, out, n, heads, dh, slots, cache_rows);
@@ -515,16 +574,16 @@ int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, int64_t q_st
   if (q_stride < heads * dh) return -1;
   if (n == 0) return 0;
   return dispatch<false>(q_dtype, kv_dtype, dh, q, const_cast<void*>(keys),
-                         const_cast<void*>(values), nullptr, nullptr, pos, rows, out, n, heads,
-                         slots, cache_rows, scale, q_stride, 0, stream);
+                         const_cast<void*>(values), nullptr, nullptr, pos, rows, order, out, n,
+                         heads, slots, cache_rows, scale, q_stride, 0, stream);
 }
 
 int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, int64_t q_stride,
                                  const void* k_new, const void* v_new, int64_t new_stride,
                                  void* keys, void* values, const int64_t* pos,
-                                 const int64_t* rows, int64_t n, int64_t heads, int64_t dh,
-                                 int64_t slots, int64_t cache_rows, float scale, void* out,
-                                 hipStream_t stream) {
+                                 const int64_t* rows, const int32_t* order, int64_t n,
+                                 int64_t heads, int64_t dh, int64_t slots, int64_t cache_rows,
+                                 float scale, void* out, hipStream_t stream) {
   using namespace cugo_amd::decode;
   const int bad = check_args(q, keys, values, pos, out, n, heads, dh, slots, cache_rows);
   if (bad) return bad;
@@ -533,8 +592,20 @@ int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, int64
   const int64_t kv_size = kv_dtype == CUGO_DTYPE_F32 ? 4 : 2;
   if (!aligned16(k_new) || !aligned16(v_new) || (new_stride * kv_size) % 16 != 0) return -4;
   if (n == 0) return 0;
-  return dispatch<true>(q_dtype, kv_dtype, dh, q, keys, values, k_new, v_new, pos, rows, out,
-                        n, heads, slots, cache_rows, scale, q_stride, new_stride, stream);
+  return dispatch<true>(q_dtype, kv_dtype, dh, q, keys, values, k_new, v_new, pos, rows, order,
+                        out, n, heads, slots, cache_rows, scale, q_stride, new_stride, stream);
+}
+
+int cugo_decode_order(const int64_t* pos, int64_t n, int64_t slots, int32_t* order,
+                      hipStream_t stream) {
+  using namespace cugo_amd::decode;
+  if (n < 0 || n > INT32_MAX || slots <= 0 || (n > 0 && (!pos || !order))) return -1;
+  if (n == 0) return 0;
+  int shift = 0;  // bins of 2^shift consecutive lengths, at most kOrderBins of them
+  while ((slots >> shift) >= kOrderBins) ++shift;
+  hipLaunchKernelGGL(order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, pos, n, slots, shift,
+                     order);
+  return (int)hipGetLastError();
 }
 
 }  // extern "C"

@@ -650,9 +650,11 @@ void check_decode(const torch::Tensor& q, const torch::Tensor& keys, const torch
   }
 }
 
-// decode_attention(q, keys, values, pos, rows=None)
+// decode_attention(q, keys, values, pos, rows=None, order=None)
 // (python/cugo_seq_attention50.py:43-62): q [n, heads, dh]; keys/values
-// [rows, heads, slots, dh]; pos/rows int64 [n] -> [n, heads, dh] in q's dtype.
+// [rows, heads, slots, dh]; pos/rows int64 [n] -> [n, heads, dh] in q's dtype; `order`
+// (int32 [n], a permutation of the queries, e.g. decode_order's) only changes which
+// workgroups serve which queries.
 // [n, heads, dh] rows read in place when each row's [heads, dh] block is contiguous (a
 // column slice of a packed [n, 3 d] projection is); otherwise a contiguous copy.
 torch::Tensor row_blocks(const torch::Tensor& t) {
@@ -665,9 +667,19 @@ int64_t block_stride(const torch::Tensor& t) {
   return t.size(0) <= 1 ? t.size(1) * t.size(2) : t.stride(0);
 }
 
+const int32_t* order_ptr(const c10::optional<torch::Tensor>& order, const torch::Tensor& q) {
+  if (!order.has_value()) return nullptr;
+  check_1d(*order, at::kInt, "order");
+  TORCH_CHECK(order->numel() == q.size(0), "order must have one entry per query");
+  check_same_device(q, *order, "q", "order");
+  return order->data_ptr<int32_t>();
+}
+
 torch::Tensor decode_attention(torch::Tensor q, torch::Tensor keys, torch::Tensor values,
-                               torch::Tensor pos, c10::optional<torch::Tensor> rows) {
+                               torch::Tensor pos, c10::optional<torch::Tensor> rows,
+                               c10::optional<torch::Tensor> order) {
   check_decode(q, keys, values, pos, rows);
+  const int32_t* ord = order_ptr(order, q);
   const DeviceGuard guard(q.device());
   q = row_blocks(q);
   auto out = torch::empty(q.sizes(), q.options());
@@ -676,22 +688,38 @@ torch::Tensor decode_attention(torch::Tensor q, torch::Tensor keys, torch::Tenso
   check_call(cugo_decode_attention(dtype_code(q.scalar_type()), dtype_code(keys.scalar_type()),
                                    q.data_ptr(), block_stride(q), keys.data_ptr(),
                                    values.data_ptr(), pos.data_ptr<int64_t>(),
-                                   rows.has_value() ? rows->data_ptr<int64_t>() : nullptr,
+                                   rows.has_value() ? rows->data_ptr<int64_t>() : nullptr, ord,
                                    q.size(0), q.size(1), dh, keys.size(2), keys.size(0), scale,
                                    out.data_ptr(), stream()),
              "decode_attention");
   return out;
 }
 
-// decode_attention_append(q, k_new, v_new, keys, values, pos, rows=None, out=None): writes
-// k_new and v_new ([n, heads, dh], cast to the cache dtype) to slot pos of each query's row,
-// in place, then attends as decode_attention (python/cugo_seq50.py:313-320 in one launch),
-// into `out` when given.
+// decode_order(pos int64 [n], slots) -> int32 [n]: the queries longest first by
+// min(pos, slots - 1) (cugo_decode_order), for decode_attention's `order`.
+torch::Tensor decode_order(torch::Tensor pos, int64_t slots) {
+  check_1d(pos, at::kLong, "pos");
+  TORCH_CHECK(pos.is_cuda(), "pos must be a CUDA tensor");
+  TORCH_CHECK(slots > 0, "slots must be positive");
+  const DeviceGuard guard(pos.device());
+  auto order = torch::empty({pos.numel()}, on(pos, at::kInt));
+  check_call(cugo_decode_order(pos.data_ptr<int64_t>(), pos.numel(), slots,
+                               order.data_ptr<int32_t>(), stream()),
+             "decode_order");
+  return order;
+}
+
+// decode_attention_append(q, k_new, v_new, keys, values, pos, rows=None, out=None,
+// order=None): writes k_new and v_new ([n, heads, dh], cast to the cache dtype) to slot pos
+// of each query's row, in place, then attends as decode_attention
+// (python/cugo_seq50.py:313-320 in one launch), into `out` when given.
 torch::Tensor decode_attention_append(torch::Tensor q, torch::Tensor k_new, torch::Tensor v_new,
                                       torch::Tensor keys, torch::Tensor values, torch::Tensor pos,
                                       c10::optional<torch::Tensor> rows,
-                                      c10::optional<torch::Tensor> out_opt) {
+                                      c10::optional<torch::Tensor> out_opt,
+                                      c10::optional<torch::Tensor> order) {
   check_decode(q, keys, values, pos, rows);
+  const int32_t* ord = order_ptr(order, q);
   TORCH_CHECK(k_new.sizes() == q.sizes() && v_new.sizes() == q.sizes(),
               "k_new and v_new must have q's shape [n, heads, dh]");
   check_same_device(q, k_new, "q", "k_new");
@@ -724,7 +752,7 @@ torch::Tensor decode_attention_append(torch::Tensor q, torch::Tensor k_new, torc
                  block_stride(q), k_new.data_ptr(), v_new.data_ptr(), block_stride(k_new),
                  keys.data_ptr(), values.data_ptr(),
                  pos.data_ptr<int64_t>(), rows.has_value() ? rows->data_ptr<int64_t>() : nullptr,
-                 q.size(0), q.size(1), dh, keys.size(2), keys.size(0), scale, out.data_ptr(),
+                 ord, q.size(0), q.size(1), dh, keys.size(2), keys.size(0), scale, out.data_ptr(),
                  stream()),
              "decode_attention_append");
   return out;
@@ -1682,12 +1710,16 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("actions") = pybind11::none(), pybind11::arg("logp") = pybind11::none());
   m.def("decode_attention", &decode_attention, "Single-query attention over a KV cache",
         pybind11::arg("q"), pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
-        pybind11::arg("rows") = pybind11::none());
+        pybind11::arg("rows") = pybind11::none(), pybind11::arg("order") = pybind11::none());
   m.def("decode_attention_append", &decode_attention_append,
         "Write the new key/value at slot pos, then single-query attention",
         pybind11::arg("q"), pybind11::arg("k_new"), pybind11::arg("v_new"),
         pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
-        pybind11::arg("rows") = pybind11::none(), pybind11::arg("out") = pybind11::none());
+        pybind11::arg("rows") = pybind11::none(), pybind11::arg("out") = pybind11::none(),
+        pybind11::arg("order") = pybind11::none());
+  m.def("decode_order", &decode_order,
+        "The queries longest first (int32 permutation) for the decode calls' `order`",
+        pybind11::arg("pos"), pybind11::arg("slots"));
   m.attr("FEATURE_COUNT") = pybind11::int_(CUGO_FEATURE_COUNT);
   m.attr("ACTION_COUNT") = pybind11::int_(CUGO_ACTION_COUNT);
   m.attr("PRIMARY_ACTION_COUNT") = pybind11::int_(CUGO_PRIMARY_ACTION_COUNT);

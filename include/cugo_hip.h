@@ -273,6 +273,10 @@ int cugo_play_random_noalloc(uint8_t* states, int64_t n, uint64_t* sampler, floa
  *   out           [n, heads, dh] of q_dtype, contiguous
  *   keys, values  [cache_rows, heads, slots, dh] of kv_dtype, contiguous, 16-byte aligned
  *   pos, rows     int64 [n]
+ *   order         int32 [n] or NULL: the order in which the launch takes the queries (a
+ *                 permutation of 0 .. n - 1, e.g. cugo_decode_order's); it changes no
+ *                 result, only which queries the last workgroups serve (an entry outside
+ *                 [0, n) is skipped: its query is not computed)
  * Softmax and accumulation are fp32; out is rounded to q_dtype.  dh is 16, 32, 64 or 128
  * (dh * element size >= 16 bytes).  A query whose pos is negative, or whose row is outside
  * [0, cache_rows), gets a NaN output (the reference's softmax over no slot is NaN) and
@@ -285,8 +289,8 @@ int cugo_play_random_noalloc(uint8_t* states, int64_t n, uint64_t* sampler, floa
 
 int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, int64_t q_stride,
                           const void* keys, const void* values, const int64_t* pos,
-                          const int64_t* rows, int64_t n, int64_t heads, int64_t dh,
-                          int64_t slots, int64_t cache_rows, float scale, void* out,
+                          const int64_t* rows, const int32_t* order, int64_t n, int64_t heads,
+                          int64_t dh, int64_t slots, int64_t cache_rows, float scale, void* out,
                           hipStream_t stream);
 
 /*
@@ -301,9 +305,24 @@ int cugo_decode_attention(int q_dtype, int kv_dtype, const void* q, int64_t q_st
 int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, int64_t q_stride,
                                  const void* k_new, const void* v_new, int64_t new_stride,
                                  void* keys, void* values, const int64_t* pos,
-                                 const int64_t* rows, int64_t n, int64_t heads, int64_t dh,
-                                 int64_t slots, int64_t cache_rows, float scale, void* out,
-                                 hipStream_t stream);
+                                 const int64_t* rows, const int32_t* order, int64_t n,
+                                 int64_t heads, int64_t dh, int64_t slots, int64_t cache_rows,
+                                 float scale, void* out, hipStream_t stream);
+
+/*
+ * The order for the two calls above that takes ragged rows longest first: order (int32
+ * [n]) receives a permutation of 0 .. n - 1 sorted by min(pos, slots - 1), longest first
+ * (negative pos last), in bins of 2^s lengths where slots >> s < 4,096 (s = 0 below 4,096
+ * slots).  The dispatcher starts workgroups in index order as others finish, so the long
+ * rows start first and the short ones fill in at the end of the launch.  A row's place
+ * within its bin may differ between calls; no decode result depends on it.  One
+ * workgroup; computed once, it serves every layer of a step and, while lengths grow
+ * together, the following steps.  Returns -1 for n outside [0, 2^31), slots <= 0 or a
+ * null pointer.  No reference counterpart (the reference's Triton grid takes the rows in
+ * index order, cugo_seq_attention50.py:43-56).
+ */
+int cugo_decode_order(const int64_t* pos, int64_t n, int64_t slots, int32_t* order,
+                      hipStream_t stream);
 
 /*
  * Event-sequence policy self-play (python/cugo_seq50.py, python/cugo_seq_selfplay50.py).

@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 import torch
 
-from cugo_amd.cugo_seq_attention50 import decode_attention, decode_attention_append
+from cugo_amd.cugo_seq_attention50 import (decode_attention, decode_attention_append,
+                                           decode_order)
 from oracle.decode_ref import brute_force, matmul_path
 from oracle.seq_ref import reference_cached_step
 from tests.conftest import announce
@@ -199,6 +200,70 @@ def test_argument_errors(ext):
     q48, k48, v48 = make_case(2, 2, 2, 4, 48, seed=15)
     with pytest.raises(RuntimeError):
         decode_attention(q48, k48, v48, pos[:2])  # dh = 48 is not supported
+
+
+@pytest.mark.parametrize("slots", [320, 10_000])
+def test_decode_order_is_longest_first(ext, slots):
+    """decode_order: a permutation of the queries, non-increasing in min(pos, slots - 1)
+    (negative pos last), exactly below 4,096 slots and by bins of 2^s lengths above
+    (10,000 slots: s = 2)."""
+    announce(f"decode_order, {slots} slots")
+    g = np.random.default_rng(slots)
+    n = 5000
+    pos = torch.from_numpy(g.integers(-3, slots + 40, n)).to(DEV)
+    order = decode_order(pos, slots)
+    assert order.dtype == torch.int32 and order.shape == (n,)
+    o = order.long().cpu()
+    assert torch.equal(o.sort().values, torch.arange(n))
+    clamped = pos.cpu().clamp(-1, slots - 1)
+    shift = 0 if slots < 4096 else 2
+    key = (slots - 1 - clamped[o]) >> shift
+    assert bool((key[1:] >= key[:-1]).all())
+    assert decode_order(pos[:0], slots).shape == (0,)
+    assert int(decode_order(pos[:1], slots)[0]) == 0
+
+
+@pytest.mark.parametrize("slots", [320, 50])
+def test_decode_order_changes_no_result(ext, slots):
+    """The same queries served in another order (decode_order's, a reversal, a random
+    permutation) give bit-identical outputs and cache writes, with and without the append;
+    an order entry outside [0, n) leaves its query's output unwritten.  4,096 queries on
+    ragged rows: more workgroups than the chip holds at once."""
+    announce(f"decode order invariance, {slots}-slot cache")
+    n, rows, heads, dh = 4096, 4096, 8, 32
+    q, k, v = make_case(n, rows, heads, slots, dh, seed=31 + slots)
+    g = np.random.default_rng(32)
+    row_ids = torch.from_numpy(g.permutation(rows)).to(DEV)
+    pos = torch.from_numpy(g.integers(0, slots, n)).to(DEV)
+    pos[:3] = torch.tensor([-1, slots + 7, 0], device=DEV)
+    k_new = (torch.randn(n, heads, dh, generator=torch.Generator().manual_seed(33)) * 0.5).to(
+        torch.bfloat16).to(DEV)
+    v_new = k_new.flip(0).contiguous()
+    want = decode_attention(q, k, v, pos, rows=row_ids)
+    k0, v0 = k.clone(), v.clone()
+    want_app = decode_attention_append(q, k_new, v_new, k0, v0, pos, rows=row_ids)
+    orders = [decode_order(pos, slots), torch.arange(n - 1, -1, -1, device=DEV, dtype=torch.int32),
+              torch.from_numpy(g.permutation(n).astype(np.int32)).to(DEV)]
+    for order in orders:
+        got = decode_attention(q, k, v, pos, rows=row_ids, order=order)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        k1, v1 = k.clone(), v.clone()
+        got = decode_attention_append(q, k_new, v_new, k1, v1, pos, rows=row_ids, order=order)
+        assert torch.equal(got.view(torch.int16), want_app.view(torch.int16))
+        assert torch.equal(k1, k0) and torch.equal(v1, v0)
+    order = orders[2].clone()
+    skipped = int(order[17])
+    order[17] = -1
+    out = torch.full_like(q, 3.0)
+    decode_attention_append(q, k_new, v_new, k.clone(), v.clone(), pos, rows=row_ids, out=out,
+                            order=order)
+    assert bool((out[skipped] == 3.0).all())
+    keep = torch.arange(n, device=DEV) != skipped
+    assert torch.equal(out[keep].view(torch.int16), want_app[keep].view(torch.int16))
+    with pytest.raises(RuntimeError):
+        decode_attention(q, k, v, pos, rows=row_ids, order=order.long())
+    with pytest.raises(RuntimeError):
+        decode_attention(q, k, v, pos, rows=row_ids, order=order[:-1])
 
 
 def _layered_model(layers=4, d=256, heads=8, seed=0):
