@@ -367,7 +367,9 @@ int launch_group(const void* q, void* keys, void* values, const void* k_new, con
 // (rows from seeded games; ms per launch for P = 1 / 2 / 4): rows up to a uniform target in
 // [1, 320] 0.156 / 0.150 / 0.143, rows filled to ~308 slots 0.241 / 0.233 / 0.232, one
 // game a row (~20 slots) 0.0185 / 0.0178 / 0.0212.  Four parts quadruple the wavefronts,
-// which short rows pay for in dispatch rounds; two parts are faster on all three.
+// which short rows pay for in dispatch rounds; two parts are faster on all three.  On the
+// self-play policy's 50-slot cache (events then queries of 4,096 games, rows of 0-40
+// slots) two parts took the whole decision step from 0.483 to 0.516 ms: one there.
 // CUGO_DECODE_FORCE_PARTS (a compile-time define) pins P for tuning builds.
 inline bool split_rows(int64_t slots) { return slots > 64; }
 
