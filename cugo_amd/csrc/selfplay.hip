@@ -592,6 +592,17 @@ __global__ __launch_bounds__(256) void paired_update_kernel(
   active[i] = ok && new_done[i] == 0;
 }
 
+// A paired evaluation's policy answers only for the games whose mover sits in its seat
+// (cugo_eval50.py:130-135 feeds each model its movers): the query of every other game is
+// skipped by the step's decode (query_pos = -1: no cache read or write, NaN logits that
+// nothing reads).  After the observation, before the policy's pass.  One thread per game.
+__global__ __launch_bounds__(256) void paired_movers_kernel(const uint8_t* player,
+                                                            const i64* seat, i64 n,
+                                                            i64* query_pos) {
+  const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n && (i64)player[i] != seat[i]) query_pos[i] = -1;
+}
+
 // The event log of a paired evaluation of sequence policies (History.record,
 // cugo_seq50.py:62-67, called at cugo_eval50.py:258-263), kept as each policy's cache
 // length: after the engine step and the event tokens (which read the old count), before
@@ -941,6 +952,15 @@ int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_
   paired_update_kernel<<<(unsigned)((n + 255) / 256 > 0 ? (n + 255) / 256 : 1), 256, 0, stream>>>(
       active, step_status, new_done, reward0, nagari, n, final_reward0, final_nagari, bad,
       any_active, steps);
+  return (int)hipGetLastError();
+}
+
+int cugo_paired_movers(const uint8_t* player, const int64_t* seat, int64_t n,
+                       int64_t* query_pos, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!player || !seat || !query_pos))) return -1;
+  if (n == 0) return 0;
+  paired_movers_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(player, seat, n,
+                                                                        query_pos);
   return (int)hipGetLastError();
 }
 

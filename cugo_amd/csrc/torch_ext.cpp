@@ -1138,6 +1138,23 @@ void store_probe(torch::Tensor out, int64_t rows, int64_t row_bytes, int64_t ste
 // query_pos_a, length_b, event_pos_b, query_pos_b): the event bookkeeping of a paired
 // evaluation of sequence policies (cugo_paired_events): a kept event's slot (or -1) into
 // event_pos_*, the next query's slot (or -1) into query_pos_*, and the counts and cache
+// paired_movers(player uint8 [n], seat int64 [n], query_pos int64 [n]): query_pos = -1
+// where the mover is not in `seat` (cugo_paired_movers).
+void paired_movers(torch::Tensor player, torch::Tensor seat, torch::Tensor query_pos) {
+  check_1d(player, at::kByte, "player");
+  check_1d(seat, at::kLong, "seat");
+  check_1d(query_pos, at::kLong, "query_pos");
+  const int64_t n = player.numel();
+  TORCH_CHECK(seat.numel() == n && query_pos.numel() == n,
+              "player, seat and query_pos must have one entry per game");
+  check_same_device(player, seat, "player", "seat");
+  check_same_device(player, query_pos, "player", "query_pos");
+  const DeviceGuard guard(player.device());
+  check_call(cugo_paired_movers(player.data_ptr<uint8_t>(), seat.data_ptr<int64_t>(), n,
+                                query_pos.data_ptr<int64_t>(), stream()),
+             "paired_movers");
+}
+
 // lengths advanced.
 void paired_events(torch::Tensor active, torch::Tensor step_status, torch::Tensor committed,
                    torch::Tensor new_done, torch::Tensor count, torch::Tensor length_a,
@@ -1681,6 +1698,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "calibration: play_random's observation-row store pattern without the game",
         pybind11::arg("out"), pybind11::arg("rows"), pybind11::arg("row_bytes"),
         pybind11::arg("steps"), pybind11::arg("distinct"));
+  m.def("paired_movers", &paired_movers,
+        "query_pos = -1 for the games whose mover is not in the policy's seat",
+        pybind11::arg("player"), pybind11::arg("seat"), pybind11::arg("query_pos"));
   m.def("paired_events", &paired_events,
         "paired evaluation of sequence policies: event and query slots, counts, cache lengths",
         pybind11::arg("active"), pybind11::arg("step_status"), pybind11::arg("committed"),

@@ -22,7 +22,9 @@ Two kinds of policy, as in the reference (`policy_logits`, cugo_seq50.py:347-365
   view of it), and each step a query token in the slot after them.  A step's event
   tokens go through the layers with the next step's queries, in one pass
   (`cached_step_pair`), as the sequence self-play does; incremental decoding computes
-  what the dense forward computes at the query.
+  what the dense forward computes at the query.  A policy's pass keeps the queries of its
+  movers only (`paired_movers`): the others' rows are skipped by the decode, as the
+  reference feeds each model its movers (cugo_eval50.py:130-135).
 """
 
 from __future__ import annotations
@@ -134,11 +136,11 @@ class _SequenceSeat:
 
     def logits(self) -> torch.Tensor:
         """The last step's kept event tokens and the query of every game still being played
-        (its input rows in `q_in`, filled this step) through the layers together (the
-        queries attend the events' keys at every layer), then the readout of the queries:
-        [games, 179] logits in the policy dtype (NaN in the rows of games that are over,
-        whose rows the decode skips: no cache read or write; nothing reads those
-        logits)."""
+        whose mover sits in this policy's seat (its input rows in `q_in`, filled this step)
+        through the layers together (the queries attend the events' keys at every layer),
+        then the readout of the queries: [games, 179] logits in the policy dtype (NaN in the
+        rows of the other games, whose rows the decode skips: no cache read or write;
+        nothing reads those logits)."""
         from .seq_decode import cached_step_pair
 
         m, g = self.model, self.games
@@ -256,6 +258,8 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         features, legal, players, done, status = ext.observe(states)
         for columns, q_in in q_inputs.values():  # the sequence policies' query input rows
             ext.query_input(features, legal, columns, q_in)
+        for h in histories:  # a sequence policy answers for its movers only (the others'
+            ext.paired_movers(players, h.seat, h.query_pos)  # queries are skipped)
         act_a = logits_actions(0, model_a, features, legal, sample_a)
         act_b = logits_actions(1, model_b, features, legal, sample_b)
         actions = ext.paired_select(active, status, done, legal.any(1), players, a_seat, act_a,

@@ -575,6 +575,13 @@ int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_
                        const float* reward0, const uint8_t* nagari, int64_t n,
                        float* final_reward0, uint8_t* final_nagari, int64_t* bad,
                        int32_t* any_active, int64_t* steps, hipStream_t stream);
+/* cugo_paired_movers: query_pos[i] = -1 for every game whose mover (player[i], the
+ * observation's) is not in seat[i], the seat a sequence policy plays: that policy's pass
+ * then skips those games' queries, as the reference feeds each model only its movers
+ * (cugo_eval50.py:130-135). */
+int cugo_paired_movers(const uint8_t* player, const int64_t* seat, int64_t n,
+                       int64_t* query_pos, hipStream_t stream);
+
 /* cugo_paired_events: the event log of a paired evaluation of sequence policies, which the
  * reference keeps in a History (History.record, cugo_seq50.py:62-67, called at
  * cugo_eval50.py:258-263; no counterpart as one call), as each policy's KV-cache lengths.
