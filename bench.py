@@ -537,7 +537,8 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
     reached ("stress", mean pos ~170), or while they fit below 320 slots ("full", pos
     ~300), or holds one game (the reference's 50-slot regime, "natural").  The step takes
     the queries longest first (`decode_order`, one launch a step for its 4 layers); the
-    decode kernel alone is timed with that order and in index order."""
+    decode kernel alone is timed over the 4 layers' caches in turn (as the step reads
+    them) with that order, in index order, and on one layer's cache."""
     from torch import nn
 
     from cugo_amd.seq_decode import KVCache, order_pays, cached_step
@@ -579,29 +580,33 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
                     cached_step(model, cache, x)
                 torch.cuda.synchronize()
                 step_s = (time.perf_counter() - t0) / steps
-            # The decode kernel alone, same call as inside the step (layer 0's cache, the
-            # step's query order: longest first, one order launch a step for 4 layers).
+            # The decode kernel alone, same call as inside the step: the layers' caches in
+            # turn, as the step reads them (a burst on one layer's cache also times how much
+            # of a launch's reads the last-level cache keeps from the launch before), with
+            # the step's query order (longest first, one order launch a step for 4 layers).
             q = (torch.randn(rows, heads, dh, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
             kn, vn = q.clone(), q.clone()
             pos = lengths[name].clamp_max(slots - 1)
             order = decode_order(pos, slots) if order_pays(rows, slots) else None
-            reps = 50
+            reps = 52
 
-            def burst(label, order):
-                for _ in range(3):
-                    decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos, order=order)
+            def burst(label, order, layer_of=lambda r: r % layers):
+                for r in range(4):
+                    decode_attention_append(q, kn, vn, cache.k[layer_of(r)],
+                                            cache.v[layer_of(r)], pos, order=order)
                 ev0 = torch.cuda.Event(enable_timing=True)
                 ev1 = torch.cuda.Event(enable_timing=True)
                 with region(label):
                     ev0.record(stream)
-                    for _ in range(reps):
-                        decode_attention_append(q, kn, vn, cache.k[0], cache.v[0], pos,
-                                                order=order)
+                    for r in range(reps):
+                        decode_attention_append(q, kn, vn, cache.k[layer_of(r)],
+                                                cache.v[layer_of(r)], pos, order=order)
                     ev1.record(stream)
                     torch.cuda.synchronize()
                 return ev0.elapsed_time(ev1) / reps
 
             kernel_ms = burst(f"c5.decode_{name}", order)
+            one_layer_ms = burst(f"c5.decode_{name}_one_layer", order, lambda r: 0)
             unordered_ms = burst(f"c5.decode_{name}_unordered", None) if order is not None else None
             order_ms = None
             if order is not None:
@@ -627,6 +632,7 @@ def decode_workload(ext, torch, steps: int, rows: int = 4096, slots: int = 320) 
                          "mean_pos": round(float(pos.float().mean()), 2),
                          "max_pos": int(pos.max()),
                          "decode_kernel_ms": round(kernel_ms, 4),
+                         "decode_kernel_ms_one_layer": round(one_layer_ms, 4),
                          "decode_kernel_ms_index_order": (round(unordered_ms, 4)
                                                           if unordered_ms is not None else None),
                          "order_ms": round(order_ms, 4) if order_ms is not None else None,

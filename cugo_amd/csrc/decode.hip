@@ -85,6 +85,29 @@ struct F32 {
   }
 };
 
+// A cache load: non-temporal on the long caches (kStream: P > 1), whose launches stream
+// through more cache than the last-level cache holds, and whose plain loads would evict
+// what the layer's linear launches keep there.  Measured on the [4, 4,096, 8, 320, 32]
+// cache, ms a 4-layer step plain / non-temporal: rows to a uniform target in [1, 320]
+// 0.751 / 0.667, rows filled to ~308 slots 1.162 / 1.050, one game a row (~20 slots)
+// 0.270 / 0.246 (plain loads on rows of at most 64 slots only: 0.271).  The decode launch
+// alone on one layer's cache, us: 141 / 125, 244 / 222, and one game a row 18.9 / 23.5,
+// the last-level cache keeping those rows (95 MB) from launch to launch; over the 4
+// layers' caches in turn, as the step reads them, one game a row takes 25.6 with plain
+// loads on its short rows and 24.2 non-temporal.  Short caches keep plain loads: the
+// self-play step's query launch re-reads, from the last-level cache, the rows its event
+// launch has just read.
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+template <bool kStream, class T>
+__device__ inline uint4 load_slot(const T* p) {
+  if constexpr (kStream) {
+    const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+}
+
 constexpr float kNegInf = -__builtin_inff();
 constexpr int kWaves = 4;   // wavefronts per workgroup
 constexpr int kUnroll = 8;  // loads of K (and of V) in flight per lane
@@ -266,8 +289,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const size_t off = (size_t)(c + u * S + srow) * DH;
-          kr[u] = *reinterpret_cast<const uint4*>(kb + off);
-          vr[u] = *reinterpret_cast<const uint4*>(vb + off);
+          kr[u] = load_slot<(P > 1)>(kb + off);
+          vr[u] = load_slot<(P > 1)>(vb + off);
           valid[u] = true;
         }
         fold_chunk<KT, E, L, U>(st, qv, kr, vr, valid, scale_log2);
@@ -285,8 +308,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_kernel(
           kr[u] = make_uint4(0, 0, 0, 0);
           vr[u] = make_uint4(0, 0, 0, 0);
           if (valid[u]) {
-            kr[u] = *reinterpret_cast<const uint4*>(kb + (size_t)slot * DH);
-            vr[u] = *reinterpret_cast<const uint4*>(vb + (size_t)slot * DH);
+            kr[u] = load_slot<(P > 1)>(kb + (size_t)slot * DH);
+            vr[u] = load_slot<(P > 1)>(vb + (size_t)slot * DH);
           }
         }
         fold_chunk<KT, E, L, U>(st, qv, kr, vr, valid, scale_log2);
