@@ -436,6 +436,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   const i64 i = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
   const i64 w = wave.w;
   if (i >= w) return;
+  if (i == 0 && lane == 0 && wave.playing != nullptr) wave.playing[0] = 0;  // advance sets it
   const i64 step = wave.step_index[0];
   const bool record = step >= 0 && step < wave.max_steps;
   const i64 rec = step * w + i;
@@ -514,6 +515,9 @@ __global__ __launch_bounds__(256) void advance_kernel(
   const u64 bad = __ballot(active && step_status[i] != 0);
   if ((threadIdx.x & 63) == 0 && bad != 0)
     atomicAdd(wave.bad, (unsigned long long)__popcll(bad));
+  // a game still being played after this step: the wave goes on (prepare cleared the flag)
+  const u64 playing = __ballot(active && new_done[i] == 0);
+  if ((threadIdx.x & 63) == 0 && playing != 0 && wave.playing != nullptr) wave.playing[0] = 1;
   if (!in) return;
   if (active && new_done[i]) {
     wave.final_reward0[i] = reward0[i];

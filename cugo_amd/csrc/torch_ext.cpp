@@ -1540,6 +1540,15 @@ class SelfPlayState {
     c_.noise_epoch = reinterpret_cast<uint64_t*>(epoch.data_ptr());
   }
 
+  // The flag every prepare clears and every advance sets while a game is still played.
+  void set_playing(torch::Tensor playing) {
+    TORCH_CHECK(playing.numel() == 1 && playing.scalar_type() == at::kInt && playing.is_cuda() &&
+                    playing.device() == keep_[0].device(),
+                "playing must be a one-element int32 tensor on the wave's device");
+    keep_.push_back(playing);
+    c_.playing = playing.data_ptr<int32_t>();
+  }
+
   // Where every advance writes each cache row's length before the step's events count.
   void set_event_pos(torch::Tensor event_pos) {
     TORCH_CHECK(event_pos.numel() == 2 * c_.w && event_pos.scalar_type() == at::kLong &&
@@ -1679,7 +1688,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
            pybind11::arg("q_stride") = 0)
       .def("advance", &SelfPlayState::advance)
       .def("set_noise_epoch", &SelfPlayState::set_noise_epoch)
-      .def("set_event_pos", &SelfPlayState::set_event_pos);
+      .def("set_event_pos", &SelfPlayState::set_event_pos)
+      .def("set_playing", &SelfPlayState::set_playing);
   m.def("query_input", &query_input, "SeqNet._query's input rows, zero-padded, into q_in",
         pybind11::arg("features"), pybind11::arg("legal"), pybind11::arg("columns"),
         pybind11::arg("q_in"));

@@ -257,7 +257,12 @@ class SelfPlayWave:
         self.logits: torch.Tensor | None = None  # the last step's logits
         self.graph: torch.cuda.CUDAGraph | None = None  # one step, for `pool` below
         self.graph_pool: bool | None = None
-        self._done_flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
+        # 1 while a game is still being played after a step (prepare clears it, advance
+        # sets it); copied behind each replay into pinned host memory
+        self.playing = torch.zeros(1, dtype=torch.int32, device=dev)
+        for native in self.native.values():
+            native.set_playing(self.playing)
+        self._done_flags = torch.zeros(2, dtype=torch.int32, pin_memory=True)
         # The learner's event tokens of a step wait in rows [0, 2 w) of `pair` and go
         # through the layers with the next step's queries (rows [2 w, 3 w)), in one pass
         # (cached_step_pair); event_pos holds the slots they go to (-1 for an event that
@@ -402,10 +407,10 @@ class SelfPlayWave:
     def play(self, seeds: torch.Tensor, first: torch.Tensor, learner_seat: torch.Tensor,
              pool: bool = False) -> int:
         """Deals a wave and replays the step until every game has finished; returns the
-        number of steps run.  After each replay the finished flag is copied to pinned
-        host memory behind it, and the host reads the flag of the replay before the one
-        it has just queued, so the GPU never waits for the host: the wave runs at most
-        one step past its end."""
+        number of steps run.  After each replay the step's playing flag (set by its
+        advance launch while a game is left) is copied to pinned host memory behind it,
+        and the host reads the flag of the replay before the one it has just queued, so
+        the GPU never waits for the host: the wave runs at most one step past its end."""
         self.capture(pool)
         self.reset(seeds, first, learner_seat, pool)
         flags, t = self._done_flags, self.t
@@ -417,12 +422,12 @@ class SelfPlayWave:
             if steps < self.max_steps:
                 self.graph.replay()
                 steps += 1
-                flags[steps & 1].copy_(t.finished.all(), non_blocking=True)
+                flags[steps & 1].copy_(self.playing[0], non_blocking=True)
                 queued = (torch.cuda.Event(), steps, steps & 1)
                 queued[0].record(stream)
             if behind is not None:
                 behind[0].synchronize()
-                if bool(flags[behind[2]]):
+                if not int(flags[behind[2]]):  # no game left after that step
                     break
                 if behind[1] == self.max_steps:
                     raise RuntimeError(f"a wave ran {self.max_steps} steps with games left")

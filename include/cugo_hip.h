@@ -522,6 +522,10 @@ typedef struct CugoSelfPlayWave {
                                      slots the step's event tokens go to), or -1 where the
                                      step's event is not kept (no committed action, or a
                                      game already over: the decode skips the row) */
+  int32_t* playing;               /* [1] or NULL: cugo_selfplay_prepare clears it and
+                                     cugo_selfplay_advance sets it to 1 when a game is still
+                                     being played after the step (the host's stop test,
+                                     without a reduction launch) */
 } CugoSelfPlayWave;
 
 /* cugo_selfplay_prepare: the step's work between observe and the policy
