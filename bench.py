@@ -904,17 +904,18 @@ def published_smoke_workload(ext, torch, batch: int = 32768, iters: int = 3,
     bad = torch.zeros(3, dtype=torch.int64, device=dev)
     steps = torch.zeros(1, dtype=torch.int64, device=dev)
     any_active = torch.zeros(1, dtype=torch.int32, device=dev)
-    flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
+    playing = torch.zeros(1, dtype=torch.int32, device=dev)  # 1 while a game is left
+    flags = torch.zeros(2, dtype=torch.int32, pin_memory=True)
 
     def step() -> None:
         features, legal, players, done, status = ext.observe(states)
         logits = model(features.to(torch.float16))
         actions = ext.masked_argmax(logits.float(), legal)
         actions = ext.paired_select(active, status, done, legal.any(1), players, a_seat,
-                                    actions, actions, bad, any_active)
+                                    actions, actions, bad, any_active, playing)
         reward, new_done, nagari, step_status, _ = ext.step(states, actions)
         ext.paired_update(active, step_status, new_done, reward, nagari, final_reward,
-                          final_nagari, bad, any_active, steps)
+                          final_nagari, bad, any_active, steps, playing)
 
     def deal(offset: int) -> None:
         seeds, first = make_seeds(batch, offset, dev)
@@ -932,12 +933,12 @@ def published_smoke_workload(ext, torch, batch: int = 32768, iters: int = 3,
         behind = None
         for k in range(max_steps):
             replay()
-            flags[k & 1].copy_(active.any(), non_blocking=True)
+            flags[k & 1].copy_(playing[0], non_blocking=True)
             queued = (torch.cuda.Event(), k & 1, k + 1)
             queued[0].record(stream)
             if behind is not None:
                 behind[0].synchronize()
-                if not bool(flags[behind[1]]):
+                if not int(flags[behind[1]]):
                     break
             behind = queued
         else:

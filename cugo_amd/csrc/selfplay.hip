@@ -556,8 +556,9 @@ __global__ __launch_bounds__(256) void advance_kernel(
 __global__ __launch_bounds__(256) void paired_select_kernel(
     const uint8_t* active, const int16_t* status, const uint8_t* done,
     const uint8_t* any_legal, const uint8_t* player, const i64* a_seat, const i64* act_a,
-    const i64* act_b, i64 n, i64* actions, i64* bad, int* any_active) {
+    const i64* act_b, i64 n, i64* actions, i64* bad, int* any_active, int* playing) {
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0 && playing != nullptr) *playing = 0;  // paired_update sets it
   const bool in = i < n;
   const bool act = in && active[i] != 0;
   const bool fine = in && status[i] == 0;
@@ -576,7 +577,7 @@ __global__ __launch_bounds__(256) void paired_select_kernel(
 __global__ __launch_bounds__(256) void paired_update_kernel(
     uint8_t* active, const int16_t* step_status, const uint8_t* new_done, const float* reward0,
     const uint8_t* nagari, i64 n, float* final_reward0, uint8_t* final_nagari, i64* bad,
-    int* any_active, i64* steps) {
+    int* any_active, i64* steps, int* playing) {
   const i64 i = (i64)blockIdx.x * blockDim.x + threadIdx.x;
   if (i == 0 && *any_active != 0) {  // one decision step more; the flag is read by no one else
     *steps += 1;
@@ -588,6 +589,9 @@ __global__ __launch_bounds__(256) void paired_update_kernel(
   const u64 step_bad = __ballot(act && !ok);
   if ((threadIdx.x & 63) == 0 && step_bad != 0)
     atomicAdd(reinterpret_cast<unsigned long long*>(bad + 2), (unsigned long long)__popcll(step_bad));
+  // a game still active after the update: the evaluation goes on (paired_select cleared it)
+  const u64 left = __ballot(act && ok && new_done[i] == 0);
+  if ((threadIdx.x & 63) == 0 && left != 0 && playing != nullptr) *playing = 1;
   if (!act) return;
   if (ok && new_done[i] != 0) {
     final_reward0[i] = reward0[i];
@@ -934,28 +938,30 @@ int cugo_query_input(int q_dtype, const float* features, const uint8_t* legal,
 int cugo_paired_select(const uint8_t* active, const int16_t* status, const uint8_t* done,
                        const uint8_t* any_legal, const uint8_t* player, const int64_t* a_seat,
                        const int64_t* act_a, const int64_t* act_b, int64_t n, int64_t* actions,
-                       int64_t* bad, int32_t* any_active, hipStream_t stream) {
+                       int64_t* bad, int32_t* any_active, int32_t* playing,
+                       hipStream_t stream) {
   if (n < 0 || (n > 0 && (!active || !status || !done || !any_legal || !player || !a_seat ||
                           !act_a || !act_b || !actions || !bad || !any_active)))
     return -1;
   if (n == 0) return 0;
   paired_select_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
       active, status, done, any_legal, player, a_seat, act_a, act_b, n, actions, bad,
-      any_active);
+      any_active, playing);
   return (int)hipGetLastError();
 }
 
 int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_t* new_done,
                        const float* reward0, const uint8_t* nagari, int64_t n,
                        float* final_reward0, uint8_t* final_nagari, int64_t* bad,
-                       int32_t* any_active, int64_t* steps, hipStream_t stream) {
+                       int32_t* any_active, int64_t* steps, int32_t* playing,
+                       hipStream_t stream) {
   if (n < 0 || !bad || !any_active || !steps ||
       (n > 0 && (!active || !step_status || !new_done || !reward0 || !nagari || !final_reward0 ||
                  !final_nagari)))
     return -1;
   paired_update_kernel<<<(unsigned)((n + 255) / 256 > 0 ? (n + 255) / 256 : 1), 256, 0, stream>>>(
       active, step_status, new_done, reward0, nagari, n, final_reward0, final_nagari, bad,
-      any_active, steps);
+      any_active, steps, playing);
   return (int)hipGetLastError();
 }
 

@@ -1050,9 +1050,10 @@ std::vector<torch::Tensor> ffn(torch::Tensor h, torch::Tensor x, torch::Tensor w
 }
 
 // paired_select(active, status, done, any_legal, player, a_seat, act_a, act_b, bad,
-// any_active) -> actions int64 [n]; paired_update(active, step_status, new_done, reward0,
-// nagari, final_reward0, final_nagari, bad, any_active, steps): the bookkeeping of a
-// resident paired-evaluation step (cugo_paired_select / cugo_paired_update).
+// any_active, playing=None) -> actions int64 [n]; paired_update(active, step_status,
+// new_done, reward0, nagari, final_reward0, final_nagari, bad, any_active, steps,
+// playing=None): the bookkeeping of a resident paired-evaluation step (cugo_paired_select
+// / cugo_paired_update); `playing` (int32 [1]) ends a step at 1 while a game is active.
 namespace {
 void check_n(const torch::Tensor& t, int64_t n, at::ScalarType dt, const char* name) {
   TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.numel() == n && t.scalar_type() == dt,
@@ -1061,10 +1062,17 @@ void check_n(const torch::Tensor& t, int64_t n, at::ScalarType dt, const char* n
 }
 }  // namespace
 
+int32_t* playing_ptr(const c10::optional<torch::Tensor>& playing, const torch::Tensor& like) {
+  if (!playing.has_value()) return nullptr;
+  check_n(*playing, 1, at::kInt, "playing");
+  check_same_device(like, *playing, "active", "playing");
+  return playing->data_ptr<int32_t>();
+}
+
 torch::Tensor paired_select(torch::Tensor active, torch::Tensor status, torch::Tensor done,
                             torch::Tensor any_legal, torch::Tensor player, torch::Tensor a_seat,
                             torch::Tensor act_a, torch::Tensor act_b, torch::Tensor bad,
-                            torch::Tensor any_active) {
+                            torch::Tensor any_active, c10::optional<torch::Tensor> playing) {
   const int64_t n = active.numel();
   check_n(active, n, at::kBool, "active");
   check_n(status, n, at::kShort, "status");
@@ -1084,7 +1092,8 @@ torch::Tensor paired_select(torch::Tensor active, torch::Tensor status, torch::T
   check_call(cugo_paired_select(u8p(active), status.data_ptr<int16_t>(), u8p(done), u8p(any_legal),
                                 u8p(player), a_seat.data_ptr<int64_t>(), act_a.data_ptr<int64_t>(),
                                 act_b.data_ptr<int64_t>(), n, actions.data_ptr<int64_t>(),
-                                bad.data_ptr<int64_t>(), any_active.data_ptr<int32_t>(), stream()),
+                                bad.data_ptr<int64_t>(), any_active.data_ptr<int32_t>(),
+                                playing_ptr(playing, active), stream()),
              "paired_select");
   return actions;
 }
@@ -1092,7 +1101,7 @@ torch::Tensor paired_select(torch::Tensor active, torch::Tensor status, torch::T
 void paired_update(torch::Tensor active, torch::Tensor step_status, torch::Tensor new_done,
                    torch::Tensor reward0, torch::Tensor nagari, torch::Tensor final_reward0,
                    torch::Tensor final_nagari, torch::Tensor bad, torch::Tensor any_active,
-                   torch::Tensor steps) {
+                   torch::Tensor steps, c10::optional<torch::Tensor> playing) {
   const int64_t n = active.numel();
   check_n(active, n, at::kBool, "active");
   check_n(step_status, n, at::kShort, "step_status");
@@ -1112,7 +1121,8 @@ void paired_update(torch::Tensor active, torch::Tensor step_status, torch::Tenso
                                 reward0.data_ptr<float>(), u8p(nagari), n,
                                 final_reward0.data_ptr<float>(), u8p(final_nagari),
                                 bad.data_ptr<int64_t>(), any_active.data_ptr<int32_t>(),
-                                steps.data_ptr<int64_t>(), stream()),
+                                steps.data_ptr<int64_t>(), playing_ptr(playing, active),
+                                stream()),
              "paired_update");
 }
 
@@ -1701,9 +1711,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("eps") = 1e-5, pybind11::arg("rows") = 0,
         pybind11::arg("out") = pybind11::none());
   m.def("paired_select", &paired_select,
-        "paired evaluation: observe checks and each game's action from its mover's model");
+        "paired evaluation: observe checks and each game's action from its mover's model",
+        pybind11::arg("active"), pybind11::arg("status"), pybind11::arg("done"),
+        pybind11::arg("any_legal"), pybind11::arg("player"), pybind11::arg("a_seat"),
+        pybind11::arg("act_a"), pybind11::arg("act_b"), pybind11::arg("bad"),
+        pybind11::arg("any_active"), pybind11::arg("playing") = pybind11::none());
   m.def("paired_update", &paired_update,
-        "paired evaluation: step checks, final rewards and the active mask after a step");
+        "paired evaluation: step checks, final rewards and the active mask after a step",
+        pybind11::arg("active"), pybind11::arg("step_status"), pybind11::arg("new_done"),
+        pybind11::arg("reward0"), pybind11::arg("nagari"), pybind11::arg("final_reward0"),
+        pybind11::arg("final_nagari"), pybind11::arg("bad"), pybind11::arg("any_active"),
+        pybind11::arg("steps"), pybind11::arg("playing") = pybind11::none());
   m.def("store_probe", &store_probe,
         "calibration: play_random's observation-row store pattern without the game",
         pybind11::arg("out"), pybind11::arg("rows"), pybind11::arg("row_bytes"),

@@ -239,6 +239,7 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
     start = ext.start(states) if histories else None  # the openings (History, cugo_seq50.py:56)
 
     any_active = torch.zeros(1, dtype=torch.int32, device=dev)  # set in a step, counted after
+    playing = torch.zeros(1, dtype=torch.int32, device=dev)  # 1 after a step with games left
 
     last: dict[str, torch.Tensor] = {}  # the latest step's outputs, for `trace`
 
@@ -263,7 +264,7 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         act_a = logits_actions(0, model_a, features, legal, sample_a)
         act_b = logits_actions(1, model_b, features, legal, sample_b)
         actions = ext.paired_select(active, status, done, legal.any(1), players, a_seat, act_a,
-                                    act_b, bad, any_active)
+                                    act_b, bad, any_active, playing)
         last["actions"] = actions
         if histories:
             reward0, new_done, nagari, step_status, committed, events = (
@@ -275,10 +276,10 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
         else:
             reward0, new_done, nagari, step_status, _ = ext.step(states, actions)
         ext.paired_update(active, step_status, new_done, reward0, nagari, final_reward0,
-                          final_nagari, bad, any_active, steps_dev.view(1))
+                          final_nagari, bad, any_active, steps_dev.view(1), playing)
 
     replay = step
-    flags = torch.zeros(2, dtype=torch.bool, pin_memory=True)
+    flags = torch.zeros(2, dtype=torch.int32, pin_memory=True)
     with torch.inference_mode():
         if graph and not (sample_a or sample_b):
             # warm-up steps on a side stream (library handles, allocator blocks), then the
@@ -319,12 +320,12 @@ def evaluate_paired(ext, model_a: nn.Module, model_b: nn.Module, pairs: int, see
             replay()
             if trace is not None:
                 trace.append({name: t.clone() for name, t in last.items()})
-            flags[k & 1].copy_(active.any(), non_blocking=True)
+            flags[k & 1].copy_(playing[0], non_blocking=True)
             queued = (torch.cuda.Event(), k & 1)
             queued[0].record(stream)
             if behind is not None:
                 behind[0].synchronize()
-                if not bool(flags[behind[1]]):
+                if not int(flags[behind[1]]):
                     finished_all = True
                     break
             behind = queued

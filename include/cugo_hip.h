@@ -566,19 +566,23 @@ int cugo_query_input(int q_dtype, const float* features, const uint8_t* legal,
  * finished games masked instead of dropped; no counterpart in the reference, whose loop
  * does this with torch ops).  cugo_paired_select, after observe: bad[0] += active &
  * status != OK, bad[1] += active & status == OK & (done | !any_legal), *any_active = 1 if
- * any game is active, actions[i] = player[i] == a_seat[i] ? act_a[i] : act_b[i].
+ * any game is active, actions[i] = player[i] == a_seat[i] ? act_a[i] : act_b[i];
+ * *playing = 0 when playing is not NULL.
  * cugo_paired_update, after the engine step: *steps += 1 and *any_active = 0 if it was set;
  * bad[2] += active & step_status != OK; games that end now (active, OK, new_done) keep
- * reward0 and nagari in final_reward0 / final_nagari; active &= OK & !new_done.  bool
+ * reward0 and nagari in final_reward0 / final_nagari; active &= OK & !new_done; *playing =
+ * 1 when a game is still active (the host's stop test without a reduction launch).  bool
  * arrays are one byte; bad int64 [3]. */
 int cugo_paired_select(const uint8_t* active, const int16_t* status, const uint8_t* done,
                        const uint8_t* any_legal, const uint8_t* player, const int64_t* a_seat,
                        const int64_t* act_a, const int64_t* act_b, int64_t n, int64_t* actions,
-                       int64_t* bad, int32_t* any_active, hipStream_t stream);
+                       int64_t* bad, int32_t* any_active, int32_t* playing,
+                       hipStream_t stream);
 int cugo_paired_update(uint8_t* active, const int16_t* step_status, const uint8_t* new_done,
                        const float* reward0, const uint8_t* nagari, int64_t n,
                        float* final_reward0, uint8_t* final_nagari, int64_t* bad,
-                       int32_t* any_active, int64_t* steps, hipStream_t stream);
+                       int32_t* any_active, int64_t* steps, int32_t* playing,
+                       hipStream_t stream);
 /* cugo_paired_movers: query_pos[i] = -1 for every game whose mover (player[i], the
  * observation's) is not in seat[i], the seat a sequence policy plays: that policy's pass
  * then skips those games' queries, as the reference feeds each model only its movers
