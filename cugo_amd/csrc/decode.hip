@@ -521,6 +521,62 @@ int dispatch(int q_dtype, int kv_dtype, int64_t dh, const void* q, void* keys, v
 #undef CUGO_KV
 }
 
+// The KV append alone (cugo_seq50.py:317-318, the index_put_ of a token's new key and
+// value), for tokens whose attention output nothing reads: one thread per 16-byte part of
+// a (token, head) row, keys[rows[i], h, min(pos[i], slots - 1)] = k_new[i, h] and likewise
+// for values; a token with pos < 0 or a row outside the cache writes nothing.
+template <class KT, int DH>
+__global__ __launch_bounds__(256) void kv_append_kernel(
+    const typename KT::storage* __restrict__ k_new, const typename KT::storage* __restrict__ v_new,
+    int64_t new_stride, typename KT::storage* __restrict__ keys,
+    typename KT::storage* __restrict__ values, const int64_t* __restrict__ pos_in,
+    const int64_t* __restrict__ rows, int64_t n, int heads, int64_t slots, int64_t cache_rows) {
+  constexpr int E = 16 / (int)sizeof(typename KT::storage);
+  constexpr int kParts = DH / E;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n * heads * kParts) return;
+  const int64_t i = t / (heads * kParts);
+  const int rest = (int)(t - i * heads * kParts);
+  const int head = rest / kParts, part = rest % kParts;
+  int64_t pos = pos_in[i];
+  const int64_t row = rows ? rows[i] : i;
+  if (pos < 0 || row < 0 || row >= cache_rows) return;
+  if (pos >= slots) pos = slots - 1;
+  const int64_t src = i * new_stride + head * DH + part * E;
+  const size_t dst = (((size_t)row * heads + head) * (size_t)slots + pos) * DH + part * E;
+  *reinterpret_cast<uint4*>(keys + dst) = *reinterpret_cast<const uint4*>(k_new + src);
+  *reinterpret_cast<uint4*>(values + dst) = *reinterpret_cast<const uint4*>(v_new + src);
+}
+
+template <class KT>
+int kv_append_by_dh(int64_t dh, const void* k_new, const void* v_new, int64_t new_stride,
+                    void* keys, void* values, const int64_t* pos, const int64_t* rows,
+                    int64_t n, int64_t heads, int64_t slots, int64_t cache_rows,
+                    hipStream_t stream) {
+  using KS = typename KT::storage;
+  const int64_t parts = dh * (int64_t)sizeof(KS) / 16;
+  const unsigned blocks = (unsigned)((n * heads * parts + 255) / 256);
+  switch (dh) {
+#define CUGO_APPEND_DH(D)                                                                    \
+  case D:                                                                                    \
+    if constexpr (16 / sizeof(KS) <= D) {                                                    \
+      hipLaunchKernelGGL((kv_append_kernel<KT, D>), dim3(blocks), dim3(256), 0, stream,     \
+                         static_cast<const KS*>(k_new), static_cast<const KS*>(v_new),       \
+                         new_stride, static_cast<KS*>(keys), static_cast<KS*>(values), pos,  \
+                         rows, n, (int)heads, slots, cache_rows);                            \
+      return (int)hipGetLastError();                                                         \
+    }                                                                                        \
+    return -3;
+    CUGO_APPEND_DH(16)
+    CUGO_APPEND_DH(32)
+    CUGO_APPEND_DH(64)
+    CUGO_APPEND_DH(128)
+#undef CUGO_APPEND_DH
+    default:
+      return -3;
+  }
+}
+
 // cugo_decode_order: the queries longest first (by min(pos, slots - 1); a negative pos
 // last), binned by length: bin b holds the rows with slots - 1 - clamp(pos) in
 // [b << shift, (b + 1) << shift).  One workgroup: a histogram of the bins in LDS, an
@@ -619,6 +675,34 @@ int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, int64
   if (n == 0) return 0;
   return dispatch<true>(q_dtype, kv_dtype, dh, q, keys, values, k_new, v_new, pos, rows, order,
                         out, n, heads, slots, cache_rows, scale, q_stride, new_stride, stream);
+}
+
+int cugo_kv_append(int kv_dtype, const void* k_new, const void* v_new, int64_t new_stride,
+                   void* keys, void* values, const int64_t* pos, const int64_t* rows,
+                   int64_t n, int64_t heads, int64_t dh, int64_t slots, int64_t cache_rows,
+                   hipStream_t stream) {
+  using namespace cugo_amd::decode;
+  if (n < 0 || heads <= 0 || dh <= 0 || slots <= 0 || cache_rows < 0 || new_stride < heads * dh)
+    return -1;
+  if (n > 0 && (!k_new || !v_new || !keys || !values || !pos)) return -1;
+  const int64_t kv_size = kv_dtype == CUGO_DTYPE_F32 ? 4 : 2;
+  if (!aligned16(keys) || !aligned16(values) || !aligned16(k_new) || !aligned16(v_new) ||
+      (new_stride * kv_size) % 16 != 0)
+    return -4;
+  if (n == 0) return 0;
+  switch (kv_dtype) {
+    case CUGO_DTYPE_BF16:
+      return kv_append_by_dh<BF16>(dh, k_new, v_new, new_stride, keys, values, pos, rows, n,
+                                   heads, slots, cache_rows, stream);
+    case CUGO_DTYPE_F16:
+      return kv_append_by_dh<F16>(dh, k_new, v_new, new_stride, keys, values, pos, rows, n,
+                                  heads, slots, cache_rows, stream);
+    case CUGO_DTYPE_F32:
+      return kv_append_by_dh<F32>(dh, k_new, v_new, new_stride, keys, values, pos, rows, n,
+                                  heads, slots, cache_rows, stream);
+    default:
+      return -2;
+  }
 }
 
 int cugo_decode_order(const int64_t* pos, int64_t n, int64_t slots, int32_t* order,

@@ -695,6 +695,34 @@ torch::Tensor decode_attention(torch::Tensor q, torch::Tensor keys, torch::Tenso
   return out;
 }
 
+// kv_append(k_new, v_new, keys, values, pos, rows=None): the KV append of
+// decode_attention_append without the attention (cugo_kv_append), in place.
+void kv_append(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor keys,
+               torch::Tensor values, torch::Tensor pos, c10::optional<torch::Tensor> rows) {
+  check_decode(k_new, keys, values, pos, rows);
+  TORCH_CHECK(v_new.sizes() == k_new.sizes(), "k_new and v_new must have one shape");
+  TORCH_CHECK(k_new.scalar_type() == keys.scalar_type() && v_new.scalar_type() == keys.scalar_type(),
+              "k_new and v_new must have the cache's dtype");
+  check_same_device(k_new, v_new, "k_new", "v_new");
+  const DeviceGuard guard(k_new.device());
+  k_new = row_blocks(k_new);
+  v_new = row_blocks(v_new);
+  const int64_t elem = keys.element_size();
+  if (block_stride(k_new) != block_stride(v_new) || (block_stride(k_new) * elem) % 16 != 0 ||
+      (reinterpret_cast<uintptr_t>(k_new.data_ptr()) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(v_new.data_ptr()) & 15u) != 0) {
+    k_new = k_new.contiguous();
+    v_new = v_new.contiguous();
+  }
+  check_call(cugo_kv_append(dtype_code(keys.scalar_type()), k_new.data_ptr(), v_new.data_ptr(),
+                            block_stride(k_new), keys.data_ptr(), values.data_ptr(),
+                            pos.data_ptr<int64_t>(),
+                            rows.has_value() ? rows->data_ptr<int64_t>() : nullptr,
+                            k_new.size(0), k_new.size(1), k_new.size(2), keys.size(2),
+                            keys.size(0), stream()),
+             "kv_append");
+}
+
 // decode_order(pos int64 [n], slots) -> int32 [n]: the queries longest first by
 // min(pos, slots - 1) (cugo_decode_order), for decode_attention's `order`.
 torch::Tensor decode_order(torch::Tensor pos, int64_t slots) {
@@ -1765,6 +1793,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("keys"), pybind11::arg("values"), pybind11::arg("pos"),
         pybind11::arg("rows") = pybind11::none(), pybind11::arg("out") = pybind11::none(),
         pybind11::arg("order") = pybind11::none());
+  m.def("kv_append", &kv_append,
+        "the KV append of decode_attention_append without the attention, in place",
+        pybind11::arg("k_new"), pybind11::arg("v_new"), pybind11::arg("keys"),
+        pybind11::arg("values"), pybind11::arg("pos"), pybind11::arg("rows") = pybind11::none());
   m.def("decode_order", &decode_order,
         "The queries longest first (int32 permutation) for the decode calls' `order`",
         pybind11::arg("pos"), pybind11::arg("slots"));

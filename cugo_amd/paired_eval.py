@@ -147,7 +147,7 @@ class _SequenceSeat:
         m.query_from_input(self.q_in, out=self.pair[g:])
         hidden, normed = cached_step_pair(m, self.cache, self.pair, g, self.event_pos,
                                           self.query_pos, self.ids, final_norm=m.norm)
-        return m.readout(hidden[g:], normed[g:])
+        return m.readout(hidden, normed)  # the queries' (the events' are not kept)
 
     def events(self, events: torch.Tensor, count: torch.Tensor) -> None:
         """This step's event tokens, each game's from `seat`'s view at position 1 + count

@@ -252,7 +252,7 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
 
 def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a: torch.Tensor,
                      pos_b: torch.Tensor, rows_b: torch.Tensor,
-                     final_norm: nn.Module | None = None):
+                     final_norm: nn.Module | None = None, prune: bool = True):
     """cached_step for two groups of tokens at once: rows [0, split) of x (group a, one
     token for each of the cache rows 0 .. split - 1, written at slot pos_a[r]) and rows
     [split, n) (group b, one token for cache row rows_b[j], at slot pos_b[j]).  At every
@@ -260,8 +260,13 @@ def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a
     it would see had a been through every layer first (cached_step(a), then
     cached_step(b)); a reads no slot of b (a token reads the slots below its own, and b
     writes at or above a's).  The linear layers run once over both groups.  Positions past
-    the last slot are taken as the last slot.  Returns the final hidden states [n, d], and
-    with `final_norm` also final_norm of them (in the last layer's launch)."""
+    the last slot are taken as the last slot.  Returns group b's final hidden states
+    [n - split, d], and with `final_norm` also final_norm of them (in the last layer's
+    launch).  Group a's outputs are not returned: the callers' a tokens are event tokens,
+    whose outputs the reference discards (cugo_seq_selfplay50.py:156), so at the last layer
+    (`prune`) they only append their key and value (`kv_append`) and skip the attention,
+    out_proj and feed-forward; b's outputs and every cache slot are the bits of the full
+    pass (`prune=False`)."""
     n, d = x.shape
     heads = cache.heads
     dh = d // heads
@@ -270,18 +275,23 @@ def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a
     att = torch.empty((n, heads, dh), dtype=x.dtype, device=x.device)
     for i, layer in enumerate(layers):
         sa = layer.self_attn
+        last = i + 1 == len(layers)
         q, k, v = (t.reshape(n, heads, dh)
                    for t in linear(h, sa.in_proj_weight, sa.in_proj_bias).chunk(3, -1))
-        decode_attention_append(q[:split], k[:split], v[:split], cache.k[i], cache.v[i], pos_a,
-                                None, out=att[:split])
+        if last and prune:  # a's key and value only: nothing reads its outputs past here
+            _ext().kv_append(k[:split], v[:split], cache.k[i], cache.v[i], pos_a)
+        else:
+            decode_attention_append(q[:split], k[:split], v[:split], cache.k[i], cache.v[i],
+                                    pos_a, None, out=att[:split])
         decode_attention_append(q[split:], k[split:], v[split:], cache.k[i], cache.v[i], pos_b,
                                 rows_b, out=att[split:])
+        if last:  # b's rows only
+            x, h = linear_add_norm(att[split:].view(n - split, d), sa.out_proj.weight,
+                                   sa.out_proj.bias, x[split:], layer.norm2)
+            if final_norm is not None:
+                return feed_forward(layer, h, x, final_norm)
+            return feed_forward(layer, h, x)
         x, h = linear_add_norm(att.view(n, d), sa.out_proj.weight, sa.out_proj.bias, x,
                                layer.norm2)
-        if i + 1 < len(layers):
-            x, h = feed_forward(layer, h, x, layers[i + 1].norm1)
-        elif final_norm is not None:
-            return feed_forward(layer, h, x, final_norm)
-        else:
-            x = feed_forward(layer, h, x)
+        x, h = feed_forward(layer, h, x, layers[i + 1].norm1)
     return x

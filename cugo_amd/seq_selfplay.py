@@ -346,7 +346,7 @@ class SelfPlayWave:
         actor.query_from_input(q_in, out=self.pair[2 * w:])
         hidden, normed = cached_step_pair(actor, self.cache, self.pair, 2 * w, self.event_pos,
                                           query_pos, query_rows, final_norm=actor.norm)
-        logits = actor.readout(hidden[2 * w:], normed[2 * w:])
+        logits = actor.readout(hidden, normed)  # the queries' (the events' are not kept)
         if pool:
             p, opp = self.p, self.opponent
             theirs = opp.readout(opp.cached_step(self.opp_cache, opp.query_from_input(q_in[:p])))

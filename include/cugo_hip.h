@@ -310,7 +310,21 @@ int cugo_decode_attention_append(int q_dtype, int kv_dtype, const void* q, int64
                                  float scale, void* out, hipStream_t stream);
 
 /*
- * The order for the two calls above that takes ragged rows longest first: order (int32
+ * The KV append of cugo_decode_attention_append without the attention, for tokens whose
+ * attention output nothing reads (the event tokens at a sequence policy's last layer:
+ * the reference discards their outputs, cugo_seq_selfplay50.py:156): k_new / v_new
+ * [n, heads, dh] of kv_dtype (row i at i * new_stride elements, 16-byte aligned) to slot
+ * min(pos[i], slots - 1) of row rows[i] (rows NULL: row i) of keys / values, as
+ * index_put_ does (cugo_seq50.py:317-318); pos < 0 or a row outside [0, cache_rows)
+ * writes nothing.  Same return codes as cugo_decode_attention_append.
+ */
+int cugo_kv_append(int kv_dtype, const void* k_new, const void* v_new, int64_t new_stride,
+                   void* keys, void* values, const int64_t* pos, const int64_t* rows,
+                   int64_t n, int64_t heads, int64_t dh, int64_t slots, int64_t cache_rows,
+                   hipStream_t stream);
+
+/*
+ * The order for cugo_decode_attention / _append that takes ragged rows longest first: order (int32
  * [n]) receives a permutation of 0 .. n - 1 sorted by min(pos, slots - 1), longest first
  * (negative pos last), in bins of 2^s lengths where slots >> s < 4,096 (s = 0 below 4,096
  * slots).  The dispatcher starts workgroups in index order as others finish, so the long

@@ -171,6 +171,32 @@ def test_append_equals_index_put_then_decode(ext):
     assert rel_err(got, matmul_path(q, k1, v1, pos, row_ids).float()) <= 1e-2
 
 
+def test_kv_append_equals_index_put(ext):
+    """kv_append == index_put_ of k_new / v_new at slot min(pos, slots - 1) of each row
+    (the append of decode_attention_append without its attention), with strided inputs
+    (columns of a packed projection), skipped tokens (pos < 0) and rows outside the cache
+    writing nothing."""
+    announce("kv_append vs index_put_")
+    n, rows, heads, slots, dh = 1000, 2048, 8, 50, 32
+    _, k, v = make_case(n, rows, heads, slots, dh, seed=19)
+    g = torch.Generator(device="cpu").manual_seed(20)
+    packed = torch.randn(n, 3, heads, dh, generator=g).to(torch.bfloat16).to(DEV)
+    k_new, v_new = packed[:, 1], packed[:, 2]
+    row_ids = torch.from_numpy(np.random.default_rng(21).permutation(rows)[:n]).to(DEV)
+    pos = torch.from_numpy(np.random.default_rng(22).integers(0, slots + 3, n)).to(DEV)
+    pos[:3] = torch.tensor([-1, slots + 9, 0], device=DEV)
+    row_ids[3] = rows + 5
+    want_k, want_v = k.clone(), v.clone()
+    keep = (pos >= 0) & (row_ids < rows)
+    at = pos.clamp_max(slots - 1)
+    flat_rows = (row_ids[keep].view(-1, 1) * heads + torch.arange(heads, device=DEV)).flatten()
+    flat_pos = at[keep].repeat_interleave(heads)
+    want_k.view(-1, slots, dh).index_put_((flat_rows, flat_pos), k_new[keep].reshape(-1, dh))
+    want_v.view(-1, slots, dh).index_put_((flat_rows, flat_pos), v_new[keep].reshape(-1, dh))
+    ext.kv_append(k_new, v_new, k, v, pos, row_ids)
+    assert torch.equal(k, want_k) and torch.equal(v, want_v)
+
+
 def test_nan_and_clamp_semantics(ext):
     announce("decode NaN / clamp semantics")
     q, k, v = make_case(6, 4, 8, 10, 32, seed=13)

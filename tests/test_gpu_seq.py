@@ -410,6 +410,45 @@ def _policy(d=256, layers=4, heads=8, seed=0, mode="hybrid"):
     return p.to(DEV).to(torch.bfloat16).eval()
 
 
+@pytest.mark.parametrize("w", [4096, 333])
+def test_pair_step_pruned_equals_full(ext, w):
+    """cached_step_pair with the event rows' last layer pruned (their key and value
+    appended by kv_append, no attention, out_proj or feed-forward for them) against the
+    full pass: the queries' hidden states and their final norm bit for bit, and every
+    cache slot of every layer; events skipped on some rows, the queries on one of their
+    game's two seat rows (self-play's layout), some queries skipped."""
+    from cugo_amd.seq_decode import cached_step_pair
+    from cugo_amd.seq_selfplay import policy_cache
+
+    announce(f"pair step pruned vs full (w={w})")
+    policy = _policy(seed=3)
+    g = torch.Generator(device=DEV).manual_seed(w)
+    ca = policy_cache(policy, 2 * w, DEV)
+    for t in (ca.k, ca.v):
+        t.copy_((torch.randn(t.shape, generator=g, device=DEV) * 0.5).to(t.dtype))
+    cb_k, cb_v = ca.k.clone(), ca.v.clone()
+    length = torch.randint(0, 40, (2 * w,), generator=g, device=DEV)
+    pos_a = torch.where(torch.rand(2 * w, generator=g, device=DEV) < 0.2, -1, length)
+    seat = torch.randint(0, 2, (w,), generator=g, device=DEV)
+    rows_b = torch.arange(w, device=DEV) + w * seat
+    pos_b = torch.where(torch.rand(w, generator=g, device=DEV) < 0.1, -1,
+                        length[rows_b] + (pos_a[rows_b] >= 0).long())
+    x = (torch.randn(3 * w, 256, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    with torch.no_grad():
+        h1, n1 = cached_step_pair(policy, ca, x, 2 * w, pos_a, pos_b, rows_b,
+                                  final_norm=policy.norm)
+        ca.k, cb_k = cb_k, ca.k  # the full pass on the untouched copy
+        ca.v, cb_v = cb_v, ca.v
+        h2, n2 = cached_step_pair(policy, ca, x, 2 * w, pos_a, pos_b, rows_b,
+                                  final_norm=policy.norm, prune=False)
+    assert h1.shape == (w, 256)
+    live = pos_b >= 0
+    assert torch.equal(h1[live].view(torch.int16), h2[live].view(torch.int16))
+    assert torch.equal(n1[live].view(torch.int16), n2[live].view(torch.int16))
+    assert torch.equal(cb_k.view(torch.int16), ca.k.view(torch.int16))
+    assert torch.equal(cb_v.view(torch.int16), ca.v.view(torch.int16))
+
+
 def _reference_step(policy, ref, actions_from=None):
     """One WaveCollector step (cugo_seq_selfplay50.py:108-163, no pool) in the reference
     formulation: dense tokens from the oracle, index_put_ + matmul attention, the torch
