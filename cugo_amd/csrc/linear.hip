@@ -376,7 +376,9 @@ int launch(const Args& base, int k, int act, hipStream_t stream) {
 //     them to a chunk buffer in LDS (two buffers, so one barrier a chunk); then each
 //     wavefront adds the chunk's K slice of linear2 into its 32 output columns for all
 //     rows (accumulators in registers across the chunks, K order 0 .. 1,023 as the
-//     one-launch linear2 runs it);
+//     one-launch linear2 runs it); a chunk's GELU runs a 4-column group a K step beside
+//     the MFMAs of the next chunk's linear1 (the last chunk's beside the third linear2
+//     slice), which took 12,288 rows from 26.6 to 24.9 us;
 //   * the epilogue is linear_kernel's: bias, bf16, the residual add, the LayerNorm (or
 //     the plain residual), through LDS row-major.
 // Every rounding and every fp32 sum is in the order of linear (GELU) + linear_add_layernorm
@@ -402,6 +404,20 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kS1 = kD / kK;  // K steps of linear1 (8)
 constexpr int kSc = kC / kK;  // K steps of linear2 a chunk (8)
 constexpr int kS2 = kF / kK;  // K steps of linear2 (32)
+// The phases of ffn_kernel's loop: which weight (linear2's: true), which chunk, which
+// chunk's GELU runs beside it (-1: none), and whether a barrier follows it.
+constexpr int kPhases = 2 * kChunks;
+__host__ __device__ constexpr bool phase_w2(int p) { return p == 2 || p == 4 || p >= 6; }
+__host__ __device__ constexpr int phase_chunk(int p) {
+  return p == 0 ? 0 : p == 1 ? 1 : p == 2 ? 0 : p == 3 ? 2 : p == 4 ? 1 : p == 5 ? 3 : p == 6 ? 2 : 3;
+}
+__host__ __device__ constexpr int phase_gelu(int p) {
+  return p == 1 ? 0 : p == 3 ? 1 : p == 5 ? 2 : p == 6 ? 3 : -1;
+}
+__host__ __device__ constexpr bool phase_barrier(int p) {
+  return p == 1 || p == 3 || p == 5 || p == 6;
+}
+static_assert(kChunks == 4 && kS1 == kSc, "the phase table is written for four chunks");
 
 struct Args {
   const __bf16* h;  // [m, 256], row stride ldh
@@ -453,12 +469,17 @@ __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
         w2r, lane * 16, ((2 * wave + t) * kS2 + s) * kFragBytes, 0));
   };
 
-  bf16x8 r1[kR][2];  // W1 ring
-  bf16x8 r2[kR][2];  // W2 ring
+  // One ring for both weights, in the order the phases below use them (8 K steps a
+  // phase): step g of that sequence sits in slot g % kR.
+  bf16x8 ring[kR][2];
+  auto w_at = [&](int g, int t) {
+    const int p = g / kS1, s = g % kS1, c = phase_chunk(p);
+    return phase_w2(p) ? w2_at(t, kSc * c + s) : w1_at(c, t, s);
+  };
 #pragma unroll
   for (int j = 0; j < kDepth; ++j)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) r1[j][t] = w1_at(0, t, j);
+    for (int t = 0; t < 2; ++t) ring[j][t] = w_at(j, t);
 
   constexpr int kNormRows = BM / kWaves;  // rows a wavefront finishes in the epilogue
   typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -502,92 +523,74 @@ __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) y[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Phases of 8 K steps: A(c) = linear1 of chunk c into u[c & 1], B(c) = linear2's K
+  // slice of chunk c into y, G(c) = chunk c's bias + GELU into chunk buffer c & 1, in the
+  // order A0 | A1 G0 | bar | B0 | A2 G1 | bar | B1 | A3 G2 | bar | B2 G3 | bar | B3:
+  // each GELU runs on VALU beside another phase's MFMAs, and every chunk buffer is written
+  // only after the barrier that follows the last read of its previous contents.
+  f32x4 u[2][MT][2];
+  bf16x8 xa[2][MT];
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    __bf16* ub = us + (c & 1) * kPanel;
-    bf16x4_t b1v[2];  // linear1's bias at this lane's columns of the chunk
+  for (int p = 0; p < kPhases; ++p) {
+    const bool w2 = phase_w2(p);
+    const int c = phase_chunk(p);
+    const int gc = phase_gelu(p);  // the chunk whose GELU runs in this phase, or -1
+    const __bf16* src = w2 ? us + (c & 1) * kPanel : hs;  // the B operands' panel
+    bf16x4_t b1v[2];  // linear1's bias at this lane's columns of chunk gc
+    if (gc >= 0) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-      b1v[t] = *reinterpret_cast<const bf16x4_t*>(a.b1 + kC * c + c0 + 16 * t + 4 * q4);
-    // ---- linear1 of the chunk: u[i][t] = W1 (32 of the chunk's columns) x h (row tile i)
-    f32x4 u[MT][2];
+      for (int t = 0; t < 2; ++t)
+        b1v[t] = *reinterpret_cast<const bf16x4_t*>(a.b1 + kC * gc + c0 + 16 * t + 4 * q4);
+    }
+    if (!w2) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) u[c & 1][i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) u[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    bf16x8 xa[2][MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-      xa[0][i] = *reinterpret_cast<const bf16x8*>(hs + x_lane + 16 * i * 32);
+      xa[0][i] = *reinterpret_cast<const bf16x8*>(src + x_lane + 16 * i * 32);
 #pragma unroll
     for (int s = 0; s < kS1; ++s) {
-      if (s + kDepth < kS1) {
+      const int g = kS1 * p + s;
+      if (g + kDepth < kS1 * kPhases) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) r1[(s + kDepth) % kR][t] = w1_at(c, t, s + kDepth);
-      } else if (s + kDepth - kS1 < kDepth) {
-        // the ring's next steps: linear2's first of this chunk
-        const int s2 = s + kDepth - kS1;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) r2[s2 % kR][t] = w2_at(t, kSc * c + s2);
+        for (int t = 0; t < 2; ++t) ring[(g + kDepth) % kR][t] = w_at(g + kDepth, t);
       }
       if (s + 1 < kS1) {
 #pragma unroll
         for (int i = 0; i < MT; ++i)
           xa[(s + 1) & 1][i] =
-              *reinterpret_cast<const bf16x8*>(hs + x_lane + ((s + 1) * BM + 16 * i) * 32);
+              *reinterpret_cast<const bf16x8*>(src + x_lane + ((s + 1) * BM + 16 * i) * 32);
       }
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-          u[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r1[s % kR][t], xa[s & 1][i],
-                                                            u[i][t], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // bias, bf16, GELU, bf16 (linear_kernel's GELU epilogue) into the chunk buffer: lane l
-    // holds hidden columns c0 + 16 t + 4 q4 + 0..3 of row 16 i + l16
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < 2; ++t) {
+          if (w2)
+            y[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ring[g % kR][t], xa[s & 1][i],
+                                                              y[i][t], 0, 0, 0);
+          else
+            u[c & 1][i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                ring[g % kR][t], xa[s & 1][i], u[c & 1][i][t], 0, 0, 0);
+        }
+      // one 4-column group of G(gc) a step: bias, bf16, GELU, bf16 (linear_kernel's GELU
+      // epilogue); lane l holds hidden columns c0 + 16 t + 4 q4 + 0..3 of row 16 i + l16
+      if (gc >= 0 && s < 2 * MT) {
+        const int i = s / 2, t = s % 2;
         bf16x4_t o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const __bf16 v = (__bf16)(u[i][t][e] + (float)b1v[t][e]);
+          const __bf16 v = (__bf16)(u[gc & 1][i][t][e] + (float)b1v[t][e]);
           o[e] = (__bf16)gelu((float)v);
         }
-        *reinterpret_cast<bf16x4_t*>(ub + xs_at<BM>(16 * i + l16, c0 + 16 * t + 4 * q4)) = o;
+        *reinterpret_cast<bf16x4_t*>(us + (gc & 1) * kPanel +
+                                     xs_at<BM>(16 * i + l16, c0 + 16 * t + 4 * q4)) = o;
       }
-    __syncthreads();  // the chunk is complete (and the other buffer's readers are done)
-    // ---- linear2's K slice of the chunk: y[i][t] += W2 (32 output columns) x u (row tile i)
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-      xa[0][i] = *reinterpret_cast<const bf16x8*>(ub + x_lane + 16 * i * 32);
-#pragma unroll
-    for (int s = 0; s < kSc; ++s) {
-      if (s + kDepth < kSc) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) r2[(s + kDepth) % kR][t] = w2_at(t, kSc * c + s + kDepth);
-      } else if (c + 1 < kChunks) {
-        // the ring's next steps: the next chunk's linear1
-        const int s1 = s + kDepth - kSc;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) r1[s1 % kR][t] = w1_at(c + 1, t, s1);
-      }
-      if (s + 1 < kSc) {
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-          xa[(s + 1) & 1][i] =
-              *reinterpret_cast<const bf16x8*>(ub + x_lane + ((s + 1) * BM + 16 * i) * 32);
-      }
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          y[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r2[s % kR][t], xa[s & 1][i],
-                                                            y[i][t], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (phase_barrier(p)) __syncthreads();
   }
 
   // ---- epilogue: bias, bf16, staged row-major over h's panel and chunk buffer 0 (both
