@@ -420,8 +420,15 @@ __host__ __device__ constexpr bool phase_barrier(int p) {
 static_assert(kChunks == 4 && kS1 == kSc, "the phase table is written for four chunks");
 
 struct Args {
-  const __bf16* h;  // [m, 256], row stride ldh
+  const __bf16* h;  // [m, 256], row stride ldh (with wo: the attention output)
   const __bf16* x;  // residual [m, 256], contiguous
+  // With wo (kOut): h is computed here, x1 = x + bf16(h_in W_o^T + b_o), h = LN2(x1), and
+  // x1 is the feed-forward's residual (out_proj + add + norm2, linear_add_layernorm).
+  const __bf16* wo;
+  const __bf16* bo;
+  const __bf16* ln2_w;
+  const __bf16* ln2_b;
+  float eps2;
   const __bf16* w1;
   const __bf16* b1;
   const __bf16* w2;
@@ -434,7 +441,7 @@ struct Args {
   int m, ldh;
 };
 
-template <int MT, int kDepth>
+template <int MT, int kDepth, bool kOut>
 __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
   constexpr int kR = kDepth + 1;  // ring slots: K steps of weights in flight ahead of MFMAs
   constexpr int BM = 16 * MT;
@@ -468,12 +475,23 @@ __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
     return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
         w2r, lane * 16, ((2 * wave + t) * kS2 + s) * kFragBytes, 0));
   };
+  // W_o fragment (tile t, step s): out_proj's output columns 32 wave + 16 t
+  const auto wor = __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(a.wo), (short)0,
+                                                     kOut ? (kD / 16) * kS1 * kFragBytes : 0,
+                                                     0x00020000);
+  auto wo_at = [&](int t, int s) {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+        wor, lane * 16, ((2 * wave + t) * kS1 + s) * kFragBytes, 0));
+  };
+  constexpr int kPre = kOut ? kS1 : 0;  // ring steps of out_proj, before the phases
 
-  // One ring for both weights, in the order the phases below use them (8 K steps a
-  // phase): step g of that sequence sits in slot g % kR.
+  // One ring for the weights, in the order they are used (out_proj's 8 K steps first
+  // with kOut, then the phases below, 8 K steps each): step g of that sequence sits in
+  // slot g % kR.
   bf16x8 ring[kR][2];
   auto w_at = [&](int g, int t) {
-    const int p = g / kS1, s = g % kS1, c = phase_chunk(p);
+    if (kOut && g < kPre) return wo_at(t, g);
+    const int p = (g - kPre) / kS1, s = (g - kPre) % kS1, c = phase_chunk(p);
     return phase_w2(p) ? w2_at(t, kSc * c + s) : w1_at(c, t, s);
   };
 #pragma unroll
@@ -483,6 +501,16 @@ __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
 
   constexpr int kNormRows = BM / kWaves;  // rows a wavefront finishes in the epilogue
   typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  // the residual rows this wavefront finishes (row wave + 8 j, columns 4 lane + 0..3):
+  // with kOut, x's rows now (x1 replaces them after out_proj), else x's at the epilogue
+  bf16x4_t res_v[kNormRows];
+  if constexpr (kOut) {
+#pragma unroll
+    for (int j = 0; j < kNormRows; ++j) {
+      const int row = min(m0 + wave + kWaves * j, a.m - 1);
+      res_v[j] = *reinterpret_cast<const bf16x4_t*>(a.x + (int64_t)row * kD + lane * 4);
+    }
+  }
 
   // h's panel: thread tid copies 16-byte groups tid, tid + kThreads, ... (row-major).
   {
@@ -522,6 +550,87 @@ __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
   for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int t = 0; t < 2; ++t) y[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 xa[2][MT];
+
+  if constexpr (kOut) {
+    // ---- out_proj into y over the attention rows in hs (linear_kernel's K order), then
+    // linear_kernel's kAddNorm epilogue: bias, bf16, staged row-major over the chunk
+    // buffers, x1 = bf16(x + y) per row (kept in res_v), h = LN2(x1) into hs
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      xa[0][i] = *reinterpret_cast<const bf16x8*>(hs + x_lane + 16 * i * 32);
+#pragma unroll
+    for (int s = 0; s < kS1; ++s) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) ring[(s + kDepth) % kR][t] = w_at(s + kDepth, t);
+      if (s + 1 < kS1) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          xa[(s + 1) & 1][i] =
+              *reinterpret_cast<const bf16x8*>(hs + x_lane + ((s + 1) * BM + 16 * i) * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          y[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ring[s % kR][t], xa[s & 1][i],
+                                                            y[i][t], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    float bov[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const bf16x4_t bv = *reinterpret_cast<const bf16x4_t*>(a.bo + c0 + 16 * t + 4 * q4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bov[t][e] = (float)bv[e];
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        bf16x4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (__bf16)(y[i][t][e] + bov[t][e]);
+        *reinterpret_cast<bf16x4_t*>(us + (16 * i + l16) * kOutStride + c0 + 16 * t + 4 * q4) =
+            o;
+        y[i][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    __syncthreads();  // the tile is staged; every wavefront is past its reads of hs
+    const bf16x4_t wv4 = *reinterpret_cast<const bf16x4_t*>(a.ln2_w + lane * 4);
+    const bf16x4_t bv4 = *reinterpret_cast<const bf16x4_t*>(a.ln2_b + lane * 4);
+#pragma unroll
+    for (int j = 0; j < kNormRows; ++j) {  // every row of the tile: A phases read them all
+      const int r = wave + kWaves * j;
+      const bf16x4_t yv = *reinterpret_cast<const bf16x4_t*>(us + r * kOutStride + lane * 4);
+      float v[4];
+      bf16x4_t x1;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x1[k] = (__bf16)((float)res_v[j][k] + (float)yv[k]);
+        v[k] = (float)x1[k];
+      }
+      res_v[j] = x1;
+      float sum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sum += v[k];
+      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+      const float mean = sum / (float)kD;
+      float sq = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float d = v[k] - mean;
+        sq += d * d;
+      }
+      for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+      const float rstd = 1.0f / sqrtf(sq / (float)kD + a.eps2);
+      bf16x4_t o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        o[k] = (__bf16)((v[k] - mean) * rstd * (float)wv4[k] + (float)bv4[k]);
+      *reinterpret_cast<bf16x4_t*>(hs + xs_at<BM>(r, 4 * lane)) = o;
+    }
+    __syncthreads();  // h's panel is complete; the staged tile is dead
+  }
 
   // Phases of 8 K steps: A(c) = linear1 of chunk c into u[c & 1], B(c) = linear2's K
   // slice of chunk c into y, G(c) = chunk c's bias + GELU into chunk buffer c & 1, in the
@@ -529,7 +638,6 @@ __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
   // each GELU runs on VALU beside another phase's MFMAs, and every chunk buffer is written
   // only after the barrier that follows the last read of its previous contents.
   f32x4 u[2][MT][2];
-  bf16x8 xa[2][MT];
 #pragma unroll
   for (int p = 0; p < kPhases; ++p) {
     const bool w2 = phase_w2(p);
@@ -553,8 +661,8 @@ __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
       xa[0][i] = *reinterpret_cast<const bf16x8*>(src + x_lane + 16 * i * 32);
 #pragma unroll
     for (int s = 0; s < kS1; ++s) {
-      const int g = kS1 * p + s;
-      if (g + kDepth < kS1 * kPhases) {
+      const int g = kPre + kS1 * p + s;
+      if (g + kDepth < kPre + kS1 * kPhases) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) ring[(g + kDepth) % kR][t] = w_at(g + kDepth, t);
       }
@@ -612,12 +720,12 @@ __global__ __launch_bounds__(kThreads) void ffn_kernel(Args a) {
       *reinterpret_cast<bf16x4_t*>(staged + (16 * i + l16) * kOutStride + c0 + 16 * t +
                                    4 * q4) = o;
     }
-  // the residual rows this wavefront finishes (row wave + 8 j)
-  bf16x4_t res_v[kNormRows];
+  if constexpr (!kOut) {
 #pragma unroll
-  for (int j = 0; j < kNormRows; ++j) {
-    const int row = min(m0 + wave + kWaves * j, a.m - 1);
-    res_v[j] = *reinterpret_cast<const bf16x4_t*>(a.x + (int64_t)row * kD + lane * 4);
+    for (int j = 0; j < kNormRows; ++j) {
+      const int row = min(m0 + wave + kWaves * j, a.m - 1);
+      res_v[j] = *reinterpret_cast<const bf16x4_t*>(a.x + (int64_t)row * kD + lane * 4);
+    }
   }
   __syncthreads();
   // one wavefront a row, 4 elements a lane: x_out = bf16(res + y); with ln_w, the
@@ -764,9 +872,57 @@ int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
 }
 
 
-int cugo_ffn(const void* h, int64_t ldh, const void* x, const void* w1_packed, const void* b1,
-             const void* w2_packed, const void* b2, const void* ln_weight, const void* ln_bias,
-             float eps, int64_t m, void* x_out, void* ln, int rows, hipStream_t stream) {
+// The launch shared by cugo_ffn and cugo_out_proj_ffn: rows a workgroup (0: by m) and
+// the kernel with or without the out_proj prologue.
+static int ffn_launch(const ffn::Args& a, int rows, bool out, hipStream_t stream) {
+  const int64_t m = a.m;
+  if (rows == 0) {
+    // Rows a workgroup: every workgroup streams all 1 MiB of weights through its CU's
+    // L1, which bounds the kernel, so the tile that leaves each CU the fewest rows (rounds
+    // of one workgroup a CU x rows); on a tie the smaller, or with out_proj (128 KiB more
+    // a workgroup) the larger.  Measured (us, 32 / 48 / 64 rows): 8,192 rows 24.9 / 29.6 /
+    // 36.1; 12,288: 33.6 / 31.9 / 37.3; 16,384: 36.5 / 44.1 / 39.9; with out_proj, 16,384:
+    // 53.1 / 66.0 / 45.3.
+    int cus = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) {
+      int n = 0;
+      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+          n > 0)
+        cus = n;
+    }
+    int64_t best = -1;
+    for (int r : {32, 48, 64}) {
+      const int64_t load = ((m + r - 1) / r + cus - 1) / cus * r;
+      if (best < 0 || load < best || (out && load == best)) {
+        best = load;
+        rows = r;
+      }
+    }
+  }
+  // K steps of weights in flight: 3 -> 5 took 12,288 rows from 33.2 to 31.9 us (48-row
+  // tiles), 7 no further
+  const auto grid = [&](int r) { return (unsigned)((m + r - 1) / r); };
+#define CUGO_FFN_LAUNCH(MT, R)                                                            \
+  if (out)                                                                                \
+    ffn::ffn_kernel<MT, 5, true><<<grid(R), ffn::kThreads, 0, stream>>>(a);               \
+  else                                                                                    \
+    ffn::ffn_kernel<MT, 5, false><<<grid(R), ffn::kThreads, 0, stream>>>(a);              \
+  break;
+  switch (rows) {
+    case 32: CUGO_FFN_LAUNCH(2, 32)
+    case 48: CUGO_FFN_LAUNCH(3, 48)
+    case 64: CUGO_FFN_LAUNCH(4, 64)
+    default: return -6;
+  }
+#undef CUGO_FFN_LAUNCH
+  return (int)hipGetLastError();
+}
+
+// Argument checks of the feed-forward half, shared by both entry points.
+static int ffn_check(const void* h, int64_t ldh, const void* x, const void* w1_packed,
+                     const void* b1, const void* w2_packed, const void* b2, const void* ln_weight,
+                     const void* ln_bias, int64_t m, const void* x_out, const void* ln) {
   if (m < 0 || (m > 0 && (!h || !x || !w1_packed || !b1 || !w2_packed || !b2 || !x_out)) ||
       (ln_weight == nullptr) != (ln_bias == nullptr) || (ln_weight != nullptr && !ln))
     return -1;
@@ -779,7 +935,13 @@ int cugo_ffn(const void* h, int64_t ldh, const void* x, const void* w1_packed, c
                        reinterpret_cast<uintptr_t>(ln_bias) | reinterpret_cast<uintptr_t>(ln);
   if (p16 % 16 != 0 || p8 % 8 != 0) return -4;
   if (m * ldh >= (int64_t(1) << 30)) return -5;
-  if (m == 0) return 0;
+  return 0;
+}
+
+static ffn::Args ffn_args(const void* h, int64_t ldh, const void* x, const void* w1_packed,
+                          const void* b1, const void* w2_packed, const void* b2,
+                          const void* ln_weight, const void* ln_bias, float eps, int64_t m,
+                          void* x_out, void* ln) {
   ffn::Args a{};
   a.h = static_cast<const __bf16*>(h);
   a.x = static_cast<const __bf16*>(x);
@@ -794,39 +956,42 @@ int cugo_ffn(const void* h, int64_t ldh, const void* x, const void* w1_packed, c
   a.ln = static_cast<__bf16*>(ln);
   a.m = (int)m;
   a.ldh = (int)ldh;
-  if (rows == 0) {
-    // Rows a workgroup: every workgroup streams all 1 MiB of weights through its CU's
-    // L1, which bounds the kernel, so the tile that leaves each CU the fewest rows (rounds
-    // of one workgroup a CU x rows), the smaller on a tie.  Measured (us, 32 / 48 / 64
-    // rows): 8,192 rows 24.9 / 29.6 / 36.1; 12,288: 33.6 / 31.9 / 37.3; 16,384: 36.5 / 44.1
-    // / 39.9.
-    int cus = 256;
-    int dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess) {
-      int n = 0;
-      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-          n > 0)
-        cus = n;
-    }
-    int64_t best = -1;
-    for (int r : {32, 48, 64}) {
-      const int64_t load = ((m + r - 1) / r + cus - 1) / cus * r;
-      if (best < 0 || load < best) {
-        best = load;
-        rows = r;
-      }
-    }
-  }
-  // K steps of weights in flight: 3 -> 5 took 12,288 rows from 33.2 to 31.9 us (48-row
-  // tiles), 7 no further
-  const auto grid = [&](int r) { return (unsigned)((m + r - 1) / r); };
-  switch (rows) {
-    case 32: ffn::ffn_kernel<2, 5><<<grid(32), ffn::kThreads, 0, stream>>>(a); break;
-    case 48: ffn::ffn_kernel<3, 5><<<grid(48), ffn::kThreads, 0, stream>>>(a); break;
-    case 64: ffn::ffn_kernel<4, 5><<<grid(64), ffn::kThreads, 0, stream>>>(a); break;
-    default: return -6;
-  }
-  return (int)hipGetLastError();
+  return a;
+}
+
+int cugo_ffn(const void* h, int64_t ldh, const void* x, const void* w1_packed, const void* b1,
+             const void* w2_packed, const void* b2, const void* ln_weight, const void* ln_bias,
+             float eps, int64_t m, void* x_out, void* ln, int rows, hipStream_t stream) {
+  const int rc = ffn_check(h, ldh, x, w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, m,
+                           x_out, ln);
+  if (rc != 0 || m == 0) return rc;
+  return ffn_launch(
+      ffn_args(h, ldh, x, w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, m, x_out, ln),
+      rows, false, stream);
+}
+
+int cugo_out_proj_ffn(const void* att, int64_t ld_att, const void* x, const void* wo_packed,
+                      const void* bo, const void* ln2_weight, const void* ln2_bias, float eps2,
+                      const void* w1_packed, const void* b1, const void* w2_packed,
+                      const void* b2, const void* ln_weight, const void* ln_bias, float eps,
+                      int64_t m, void* x_out, void* ln, int rows, hipStream_t stream) {
+  int rc = ffn_check(att, ld_att, x, w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, m, x_out,
+                     ln);
+  if (rc != 0) return rc;
+  if (m > 0 && (!wo_packed || !bo || !ln2_weight || !ln2_bias)) return -1;
+  if ((reinterpret_cast<uintptr_t>(wo_packed) % 16) != 0 ||
+      ((reinterpret_cast<uintptr_t>(bo) | reinterpret_cast<uintptr_t>(ln2_weight) |
+        reinterpret_cast<uintptr_t>(ln2_bias)) % 8) != 0)
+    return -4;
+  if (m == 0) return 0;
+  ffn::Args a =
+      ffn_args(att, ld_att, x, w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, m, x_out, ln);
+  a.wo = static_cast<const __bf16*>(wo_packed);
+  a.bo = static_cast<const __bf16*>(bo);
+  a.ln2_w = static_cast<const __bf16*>(ln2_weight);
+  a.ln2_b = static_cast<const __bf16*>(ln2_bias);
+  a.eps2 = eps2;
+  return ffn_launch(a, rows, true, stream);
 }
 
 }  // extern "C"

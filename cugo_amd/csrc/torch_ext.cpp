@@ -1027,19 +1027,28 @@ void query_input(torch::Tensor features, torch::Tensor legal, c10::optional<torc
              "query_input");
 }
 
-// ffn(h [m, 256], x [m, 256], w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, rows,
-// out) -> (x_out, ln): the feed-forward half of a pre-norm layer with the residual add and
-// the next norm (python/cugo_seq50.py:319-322) in one launch (cugo_ffn); without
-// ln_weight, ln is an empty tensor and x_out = x + linear2(GELU(linear1(h))).  `out`, if
-// given, receives x_out (it may be x).
-std::vector<torch::Tensor> ffn(torch::Tensor h, torch::Tensor x, torch::Tensor w1_packed,
-                               torch::Tensor b1, torch::Tensor w2_packed, torch::Tensor b2,
-                               c10::optional<torch::Tensor> ln_weight,
-                               c10::optional<torch::Tensor> ln_bias, double eps, int64_t rows,
-                               c10::optional<torch::Tensor> out) {
+// out_proj's part of out_proj_ffn: the packed [256, 256] weight, its bias and norm2.
+struct OutProj {
+  const torch::Tensor* wo_packed;
+  const torch::Tensor* bo;
+  const torch::Tensor* ln2_weight;
+  const torch::Tensor* ln2_bias;
+  double eps2;
+};
+
+// The feed-forward half (cugo_ffn), or with `op` out_proj + add + norm2 before it
+// (cugo_out_proj_ffn, h then being the attention output).
+static std::vector<torch::Tensor> ffn_impl(torch::Tensor h, torch::Tensor x,
+                                           torch::Tensor w1_packed, torch::Tensor b1,
+                                           torch::Tensor w2_packed, torch::Tensor b2,
+                                           c10::optional<torch::Tensor> ln_weight,
+                                           c10::optional<torch::Tensor> ln_bias, double eps,
+                                           int64_t rows, c10::optional<torch::Tensor> out,
+                                           const OutProj* op) {
+  const char* hname = op != nullptr ? "att" : "h";
   TORCH_CHECK(h.is_cuda() && h.dim() == 2 && h.size(1) == 256 && h.scalar_type() == at::kBFloat16 &&
                   h.stride(1) == 1,
-              "h must be a CUDA bfloat16 [m, 256] tensor with unit stride along its columns");
+              hname, " must be a CUDA bfloat16 [m, 256] tensor with unit stride along its columns");
   const int64_t m = h.size(0);
   TORCH_CHECK(x.is_contiguous() && x.dim() == 2 && x.size(0) == m && x.size(1) == 256 &&
                   x.scalar_type() == at::kBFloat16,
@@ -1053,28 +1062,78 @@ std::vector<torch::Tensor> ffn(torch::Tensor h, torch::Tensor x, torch::Tensor w
                   b2.scalar_type() == at::kBFloat16 && b2.is_contiguous() && b2.numel() == 256,
               "b1 and b2 must be contiguous bfloat16 [1024] and [256] tensors");
   TORCH_CHECK(ln_weight.has_value() == ln_bias.has_value(), "ln_weight and ln_bias go together");
-  for (const auto* t : {&x, &w1_packed, &b1, &w2_packed, &b2}) check_same_device(h, *t, "h", "an input");
+  for (const auto* t : {&x, &w1_packed, &b1, &w2_packed, &b2}) check_same_device(h, *t, hname, "an input");
   if (ln_weight.has_value()) {
     TORCH_CHECK(ln_weight->scalar_type() == at::kBFloat16 && ln_bias->scalar_type() == at::kBFloat16 &&
                     ln_weight->numel() == 256 && ln_bias->numel() == 256 &&
                     ln_weight->is_contiguous() && ln_bias->is_contiguous(),
                 "ln_weight and ln_bias must be contiguous bfloat16 [256] tensors");
-    check_same_device(h, *ln_weight, "h", "ln_weight");
-    check_same_device(h, *ln_bias, "h", "ln_bias");
+    check_same_device(h, *ln_weight, hname, "ln_weight");
+    check_same_device(h, *ln_bias, hname, "ln_bias");
+  }
+  if (op != nullptr) {
+    TORCH_CHECK(op->wo_packed->scalar_type() == at::kBFloat16 && op->wo_packed->is_contiguous() &&
+                    op->wo_packed->numel() == 256 * 256,
+                "wo_packed must be the packed bfloat16 [256, 256] weight");
+    for (const auto* t : {op->bo, op->ln2_weight, op->ln2_bias})
+      TORCH_CHECK(t->scalar_type() == at::kBFloat16 && t->is_contiguous() && t->numel() == 256,
+                  "bo, ln2_weight and ln2_bias must be contiguous bfloat16 [256] tensors");
+    for (const auto* t : {op->wo_packed, op->bo, op->ln2_weight, op->ln2_bias})
+      check_same_device(h, *t, hname, "an input");
   }
   const DeviceGuard guard(h.device());
   auto x_out = out_or_new(out, {m, 256}, at::kBFloat16, h, "out");
   auto ln = ln_weight.has_value() ? torch::empty({m, 256}, on(h, at::kBFloat16))
                                   : torch::empty({0}, on(h, at::kBFloat16));
   const int64_t ldh = m > 1 ? h.stride(0) : 256;
-  check_call(cugo_ffn(h.data_ptr(), ldh, x.data_ptr(), w1_packed.data_ptr(), b1.data_ptr(),
-                      w2_packed.data_ptr(), b2.data_ptr(),
-                      ln_weight.has_value() ? ln_weight->data_ptr() : nullptr,
-                      ln_bias.has_value() ? ln_bias->data_ptr() : nullptr, static_cast<float>(eps),
-                      m, x_out.data_ptr(), ln_weight.has_value() ? ln.data_ptr() : nullptr,
-                      static_cast<int>(rows), stream()),
-             "ffn");
+  void* lw = ln_weight.has_value() ? ln_weight->data_ptr() : nullptr;
+  void* lb = ln_bias.has_value() ? ln_bias->data_ptr() : nullptr;
+  void* lnp = ln_weight.has_value() ? ln.data_ptr() : nullptr;
+  if (op == nullptr)
+    check_call(cugo_ffn(h.data_ptr(), ldh, x.data_ptr(), w1_packed.data_ptr(), b1.data_ptr(),
+                        w2_packed.data_ptr(), b2.data_ptr(), lw, lb, static_cast<float>(eps), m,
+                        x_out.data_ptr(), lnp, static_cast<int>(rows), stream()),
+               "ffn");
+  else
+    check_call(cugo_out_proj_ffn(h.data_ptr(), ldh, x.data_ptr(), op->wo_packed->data_ptr(),
+                                 op->bo->data_ptr(), op->ln2_weight->data_ptr(),
+                                 op->ln2_bias->data_ptr(), static_cast<float>(op->eps2),
+                                 w1_packed.data_ptr(), b1.data_ptr(), w2_packed.data_ptr(),
+                                 b2.data_ptr(), lw, lb, static_cast<float>(eps), m,
+                                 x_out.data_ptr(), lnp, static_cast<int>(rows), stream()),
+               "out_proj_ffn");
   return {x_out, ln};
+}
+
+// ffn(h [m, 256], x [m, 256], w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, rows,
+// out) -> (x_out, ln): the feed-forward half of a pre-norm layer with the residual add and
+// the next norm (python/cugo_seq50.py:319-322) in one launch (cugo_ffn); without
+// ln_weight, ln is an empty tensor and x_out = x + linear2(GELU(linear1(h))).  `out`, if
+// given, receives x_out (it may be x).
+std::vector<torch::Tensor> ffn(torch::Tensor h, torch::Tensor x, torch::Tensor w1_packed,
+                               torch::Tensor b1, torch::Tensor w2_packed, torch::Tensor b2,
+                               c10::optional<torch::Tensor> ln_weight,
+                               c10::optional<torch::Tensor> ln_bias, double eps, int64_t rows,
+                               c10::optional<torch::Tensor> out) {
+  return ffn_impl(h, x, w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, rows, out,
+                  nullptr);
+}
+
+// out_proj_ffn(att [m, 256], x [m, 256], wo_packed, bo, ln2_weight, ln2_bias, eps2,
+// w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, rows, out) -> (x_out, ln): the
+// layer after its attention (python/cugo_seq50.py:317-322) in one launch
+// (cugo_out_proj_ffn): x1 = x + out_proj(att), h = norm2(x1), x_out = x1 +
+// linear2(GELU(linear1(h))), ln = the next norm of x_out (empty without ln_weight).
+std::vector<torch::Tensor> out_proj_ffn(torch::Tensor att, torch::Tensor x,
+                                        torch::Tensor wo_packed, torch::Tensor bo,
+                                        torch::Tensor ln2_weight, torch::Tensor ln2_bias,
+                                        double eps2, torch::Tensor w1_packed, torch::Tensor b1,
+                                        torch::Tensor w2_packed, torch::Tensor b2,
+                                        c10::optional<torch::Tensor> ln_weight,
+                                        c10::optional<torch::Tensor> ln_bias, double eps,
+                                        int64_t rows, c10::optional<torch::Tensor> out) {
+  const OutProj op{&wo_packed, &bo, &ln2_weight, &ln2_bias, eps2};
+  return ffn_impl(att, x, w1_packed, b1, w2_packed, b2, ln_weight, ln_bias, eps, rows, out, &op);
 }
 
 // paired_select(active, status, done, any_legal, player, a_seat, act_a, act_b, bad,
@@ -1738,6 +1797,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         pybind11::arg("ln_weight") = pybind11::none(), pybind11::arg("ln_bias") = pybind11::none(),
         pybind11::arg("eps") = 1e-5, pybind11::arg("rows") = 0,
         pybind11::arg("out") = pybind11::none());
+  m.def("out_proj_ffn", &out_proj_ffn,
+        "out_proj + residual add + norm2, then ffn, in one launch",
+        pybind11::arg("att"), pybind11::arg("x"), pybind11::arg("wo_packed"), pybind11::arg("bo"),
+        pybind11::arg("ln2_weight"), pybind11::arg("ln2_bias"), pybind11::arg("eps2"),
+        pybind11::arg("w1_packed"), pybind11::arg("b1"), pybind11::arg("w2_packed"),
+        pybind11::arg("b2"), pybind11::arg("ln_weight") = pybind11::none(),
+        pybind11::arg("ln_bias") = pybind11::none(), pybind11::arg("eps") = 1e-5,
+        pybind11::arg("rows") = 0, pybind11::arg("out") = pybind11::none());
   m.def("paired_select", &paired_select,
         "paired evaluation: observe checks and each game's action from its mover's model",
         pybind11::arg("active"), pybind11::arg("status"), pybind11::arg("done"),

@@ -199,6 +199,31 @@ def feed_forward(layer, h: torch.Tensor, x: torch.Tensor, norm: nn.Module | None
     return linear_add_norm(u, layer.linear2.weight, layer.linear2.bias, x, norm)
 
 
+def attention_tail(layer, att: torch.Tensor, x: torch.Tensor, norm: nn.Module | None = None):
+    """The rest of a pre-norm encoder layer after its attention (python/cugo_seq50.py:
+    317-322): x1 = x + out_proj(att), then feed_forward(layer, norm2(x1), x1, norm).  One
+    HIP launch (`out_proj_ffn`: neither x1 nor norm2(x1) leaves the chip) for the d = 256
+    bf16 layer `feed_forward` fuses with a biased out_proj and an affine bf16 norm2;
+    linear_add_norm and feed_forward otherwise, which give the same bits."""
+    op, n2 = layer.self_attn.out_proj, layer.norm2
+    if (_fits_ffn(layer, att, x, norm) and _fits_linear(att, op.weight, op.bias)
+            and tuple(op.weight.shape) == (256, 256) and op.bias is not None
+            and isinstance(n2, nn.LayerNorm) and n2.weight is not None and n2.bias is not None
+            and n2.weight.dtype == torch.bfloat16 and n2.bias.dtype == torch.bfloat16
+            and tuple(n2.normalized_shape) == (256,)):
+        l1, l2 = layer.linear1, layer.linear2
+        out = _ext().out_proj_ffn(att, x, packed_weight(op.weight), op.bias.detach(),
+                                  n2.weight.detach(), n2.bias.detach(), n2.eps,
+                                  packed_weight(l1.weight), l1.bias.detach(),
+                                  packed_weight(l2.weight), l2.bias.detach(),
+                                  None if norm is None else norm.weight.detach(),
+                                  None if norm is None else norm.bias.detach(),
+                                  1e-5 if norm is None else norm.eps)
+        return out[0] if norm is None else (out[0], out[1])
+    x, h = linear_add_norm(att, op.weight, op.bias, x, n2)
+    return feed_forward(layer, h, x, norm)
+
+
 def order_pays(n: int, slots: int) -> bool:
     """Whether a longest-first query order (decode_order) is worth its launch: on caches
     longer than 64 slots the decode splits each query's slots over two wavefronts of a
@@ -241,12 +266,10 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
         a = decode_attention_append(q.reshape(n, heads, dh), k.reshape(n, heads, dh),
                                     v.reshape(n, heads, dh), cache.k[i], cache.v[i], pos,
                                     row_ids, order=order)
-        x, h = linear_add_norm(a.reshape(n, d), attn.out_proj.weight, attn.out_proj.bias, x,
-                               layer.norm2)
         if i + 1 < len(layers):
-            x, h = feed_forward(layer, h, x, layers[i + 1].norm1)
+            x, h = attention_tail(layer, a.reshape(n, d), x, layers[i + 1].norm1)
         else:
-            x = feed_forward(layer, h, x)
+            x = attention_tail(layer, a.reshape(n, d), x)
     return x
 
 
@@ -286,12 +309,6 @@ def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a
         decode_attention_append(q[split:], k[split:], v[split:], cache.k[i], cache.v[i], pos_b,
                                 rows_b, out=att[split:])
         if last:  # b's rows only
-            x, h = linear_add_norm(att[split:].view(n - split, d), sa.out_proj.weight,
-                                   sa.out_proj.bias, x[split:], layer.norm2)
-            if final_norm is not None:
-                return feed_forward(layer, h, x, final_norm)
-            return feed_forward(layer, h, x)
-        x, h = linear_add_norm(att.view(n, d), sa.out_proj.weight, sa.out_proj.bias, x,
-                               layer.norm2)
-        x, h = feed_forward(layer, h, x, layers[i + 1].norm1)
+            return attention_tail(layer, att[split:].view(n - split, d), x[split:], final_norm)
+        x, h = attention_tail(layer, att.view(n, d), x, layers[i + 1].norm1)
     return x

@@ -422,6 +422,19 @@ int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
 int cugo_ffn(const void* h, int64_t ldh, const void* x, const void* w1_packed, const void* b1,
              const void* w2_packed, const void* b2, const void* ln_weight, const void* ln_bias,
              float eps, int64_t m, void* x_out, void* ln, int rows, hipStream_t stream);
+/* cugo_out_proj_ffn: the rest of a pre-norm encoder layer of SeqNet.cached_step after the
+ * attention (cugo_seq50.py:317-322) in one launch: x1 = bf16(x + bf16(att wo^T + bo)),
+ * h = LayerNorm(x1) * ln2_weight + ln2_bias (norm2, eps2), then cugo_ffn of (h, x1): the
+ * same bits as cugo_linear_add_layernorm (out_proj + add + norm2) followed by cugo_ffn,
+ * with neither x1 nor h leaving the chip.  att [m, 256] with row stride ld_att (16-byte
+ * aligned), wo_packed the [256, 256] out_proj weight in cugo_mlp_pack_weight form, bo,
+ * ln2_weight, ln2_bias [256] bf16; the rest as cugo_ffn (x_out may alias x).  No reference
+ * counterpart as one call. */
+int cugo_out_proj_ffn(const void* att, int64_t ld_att, const void* x, const void* wo_packed,
+                      const void* bo, const void* ln2_weight, const void* ln2_bias, float eps2,
+                      const void* w1_packed, const void* b1, const void* w2_packed,
+                      const void* b2, const void* ln_weight, const void* ln_bias, float eps,
+                      int64_t m, void* x_out, void* ln, int rows, hipStream_t stream);
 /* cugo_gumbel_sample: the sampling of WaveCollector._step (cugo_seq_selfplay50.py:125-130)
  * given the uniforms torch.rand_like drew: masked = legal ? logits : -1e30;
  * actions[i] = argmax_a(masked - log(-log(clamp(u, 1e-20, 1)))) (first index on ties);

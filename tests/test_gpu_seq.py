@@ -357,6 +357,63 @@ def test_ffn_equals_its_two_launches(ext, m):
         assert torch.equal(feed_forward(layer, h, x), want_plain)
 
 
+@pytest.mark.parametrize("m", [1, 37, 4096 + 5, 12288, 16384])
+def test_out_proj_ffn_equals_its_launches(ext, m):
+    """out_proj_ffn (out_proj + residual add + norm2, then the feed-forward, one launch) ==
+    linear_add_layernorm (out_proj, norm2) then ffn, bit for bit (x_out and ln), on every
+    row tile, with and without the next norm, in place (x_out over x), on an attention
+    output with a row stride (a view of a wider buffer); and through attention_tail of a
+    torch encoder layer, against linear_add_norm + feed_forward; within bf16 tolerance of
+    the torch layer in float32."""
+    from cugo_amd.seq_decode import attention_tail, feed_forward, linear_add_norm
+
+    announce(f"out_proj_ffn m={m}")
+    g = torch.Generator(device="cpu").manual_seed(m + 11)
+    wide = torch.randn(m, 264, generator=g).to(torch.bfloat16).to(DEV)
+    att = wide[:, :256]  # row stride 264
+    x = (torch.randn(m, 256, generator=g) * 2.0).to(torch.bfloat16).to(DEV)
+    layer = torch.nn.TransformerEncoderLayer(256, 8, 1024, dropout=0.0, activation="gelu",
+                                             batch_first=True, norm_first=True)
+    layer = layer.to(DEV).to(torch.bfloat16)
+    nxt = torch.nn.LayerNorm(256).to(DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        for norm in (layer.norm2, nxt):
+            norm.weight.copy_((torch.randn(256, generator=g) * 0.3 + 1.0).to(torch.bfloat16))
+            norm.bias.copy_((torch.randn(256, generator=g) * 0.1).to(torch.bfloat16))
+        for lin in (layer.self_attn.out_proj, layer.linear1, layer.linear2):
+            lin.bias.copy_((torch.randn(lin.bias.shape, generator=g) * 0.1).to(torch.bfloat16))
+        op, n2, l1, l2 = layer.self_attn.out_proj, layer.norm2, layer.linear1, layer.linear2
+        wop = ext.mlp_pack_weight(op.weight.contiguous(), 256, 256)
+        w1p = ext.mlp_pack_weight(l1.weight.contiguous(), 1024, 256)
+        w2p = ext.mlp_pack_weight(l2.weight.contiguous(), 256, 1024)
+        x1, h = ext.linear_add_layernorm(att, wop, op.bias, x, n2.weight, n2.bias, n2.eps)
+        want_x, want_ln = ext.ffn(h, x1, w1p, l1.bias, w2p, l2.bias, nxt.weight, nxt.bias,
+                                  nxt.eps)
+        want_plain, _ = ext.ffn(h, x1, w1p, l1.bias, w2p, l2.bias)
+        args = (wop, op.bias, n2.weight, n2.bias, n2.eps, w1p, l1.bias, w2p, l2.bias)
+        for rows in (0, 32, 48, 64):
+            xo, ln = ext.out_proj_ffn(att, x, *args, nxt.weight, nxt.bias, nxt.eps, rows)
+            assert torch.equal(xo, want_x) and torch.equal(ln, want_ln), rows
+            plain, empty = ext.out_proj_ffn(att, x, *args, rows=rows)
+            assert torch.equal(plain, want_plain) and empty.numel() == 0, rows
+        inplace = x.clone()
+        got = ext.out_proj_ffn(att, inplace, *args, nxt.weight, nxt.bias, nxt.eps, out=inplace)
+        assert got[0].data_ptr() == inplace.data_ptr() and torch.equal(inplace, want_x)
+        tx, tln = attention_tail(layer, att, x, nxt)
+        assert torch.equal(tx, want_x) and torch.equal(tln, want_ln)
+        assert torch.equal(attention_tail(layer, att, x), want_plain)
+        # the two-launch path gives the same bits
+        sx, sh = linear_add_norm(att, op.weight, op.bias, x, n2)
+        assert torch.equal(feed_forward(layer, sh, sx, nxt)[0], want_x)
+        # the torch layer in float32 from the same bf16 values
+        f = {k: v.float() for k, v in layer.state_dict().items()}
+        r1 = x.float() + att.float() @ f["self_attn.out_proj.weight"].T + f["self_attn.out_proj.bias"]
+        rh = torch.nn.functional.layer_norm(r1, (256,), f["norm2.weight"], f["norm2.bias"], n2.eps)
+        ru = torch.nn.functional.gelu(rh @ f["linear1.weight"].T + f["linear1.bias"])
+        ref_x = r1 + ru @ f["linear2.weight"].T + f["linear2.bias"]
+        assert rel_err(want_x, ref_x) <= 1e-2
+
+
 def test_gumbel_sample_matches_reference(ext):
     announce("gumbel_sample")
     g = torch.Generator(device=DEV).manual_seed(3)
