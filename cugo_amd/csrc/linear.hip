@@ -221,10 +221,14 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
     const int col = n0 + 16 * t + 4 * q4;
 #pragma unroll
     for (int c = 0; c < 4; ++c) bias[t][c] = 0.f;
-    if (a.bias != nullptr && col < a.n) {
+    if (a.bias != nullptr && col + 4 <= a.n) {
       const bf16x4 bv = *reinterpret_cast<const bf16x4*>(a.bias + col);
 #pragma unroll
       for (int c = 0; c < 4; ++c) bias[t][c] = (float)bv[c];
+    } else if (a.bias != nullptr) {  // the last columns of an n that is not a multiple of 4
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (col + c < a.n) bias[t][c] = (float)a.bias[col + c];
     }
   }
   __syncthreads();
@@ -292,6 +296,8 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
   const bool wide = (a.ldy & 7) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
                     (a.res == nullptr ||
                      ((a.ldr & 7) == 0 && (reinterpret_cast<uintptr_t>(a.res) & 15) == 0));
+  // n or ldy not a multiple of 4 (e.g. 179 logits a row): element stores, no residual
+  const bool narrow = ((a.n | a.ldy) & 3) != 0;
 #pragma unroll
   for (int p0 = 0; p0 < kPieces; p0 += kT) {
     const int p = p0 + tid;
@@ -305,6 +311,11 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
         if (wide && col + 8 <= a.n) {
           if (a.res != nullptr) v = add_bf16(v, *reinterpret_cast<const uint4*>(rsrc));
           *reinterpret_cast<uint4*>(dst) = v;
+        } else if (narrow) {
+          const bf16x8 e8 = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (col + e < a.n) dst[e] = e8[e];
         } else {
           if (a.res != nullptr) {
             const uint2 lo = *reinterpret_cast<const uint2*>(rsrc);
@@ -790,8 +801,8 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
   if (m < 0 || n < 1 || k < 1 || (m > 0 && (!x || !w_packed || !y))) return -1;
   if (act != CUGO_LINEAR_NONE && act != CUGO_LINEAR_GELU) return -2;
   const bool k_ok = k == 64 || k == 128 || k == 256 || k == 512 || k == 1024;
-  if (!k_ok || n % 4 != 0 || ldx < k || ldx % 8 != 0 || ldy < n || ldy % 4 != 0 ||
-      (residual != nullptr && ldr != 0 && (ldr < n || ldr % 4 != 0)))
+  if (!k_ok || ldx < k || ldx % 8 != 0 || ldy < n ||
+      (residual != nullptr && (n % 4 != 0 || ldy % 4 != 0 || (ldr != 0 && (ldr < n || ldr % 4 != 0)))))
     return -3;
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed)) % 16 != 0 ||
       (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(bias) |

@@ -78,7 +78,7 @@ def _fits_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | Non
     return (x.dim() == 2 and x.is_cuda and x.dtype == torch.bfloat16 and x.stride(1) == 1
             and weight.dtype == torch.bfloat16 and weight.dim() == 2
             and weight.shape[1] <= x.shape[1] and x.shape[1] in (64, 128, 256, 512, 1024)
-            and weight.shape[0] % 4 == 0 and (x.shape[0] <= 1 or x.stride(0) % 8 == 0)
+            and (x.shape[0] <= 1 or x.stride(0) % 8 == 0)
             and x.data_ptr() % 16 == 0
             and (bias is None or (bias.dtype == torch.bfloat16 and bias.is_contiguous()
                                   and bias.data_ptr() % 8 == 0)))
@@ -123,15 +123,16 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
            out: torch.Tensor | None = None) -> torch.Tensor:
     """F.linear(x, weight, bias), then F.gelu when `gelu`, then residual + that when a
     residual is given ([rows, N], or an [N] row for every row): one HIP launch (`linear`)
-    for bf16 rows with K in {64, ..., 1,024} and N a multiple of 4, torch's ops otherwise;
-    into `out` when given.  x may be wider than the weight's K when its extra columns are
-    zeros (a padded input: the packed weight is zero there too)."""
+    for bf16 rows with K in {64, ..., 1,024} (with a residual, N a multiple of 4), torch's
+    ops otherwise; into `out` when given.  x may be wider than the weight's K when its
+    extra columns are zeros (a padded input: the packed weight is zero there too)."""
     if x.shape[-1] != weight.shape[1] and not _fits_linear(x, weight, bias):
         x = x[..., :weight.shape[1]]
     n = weight.shape[0]
     if _fits_linear(x, weight, bias) and (
             residual is None or (residual.dtype == torch.bfloat16 and residual.is_contiguous()
-                                 and residual.shape in ((x.shape[0], n), (n,)))):
+                                 and residual.shape in ((x.shape[0], n), (n,))
+                                 and n % 4 == 0)):
         return _ext().linear(x, packed_weight(weight, x.shape[1]), n,
                              None if bias is None else bias.detach(), gelu,
                              residual=None if residual is None else residual.detach(), out=out)

@@ -117,8 +117,9 @@ class SeqPolicy(nn.Module):
         self._weight_t("event_in")
         self._weight_t("start_in")
         prepare_linears(self)
-        if self.head[0].weight.dtype == torch.bfloat16 and self.head[0].weight.is_cuda:
-            packed_weight(self.head[0].weight)
+        for lin in (self.head[0], self.head[2]):
+            if lin.weight.dtype == torch.bfloat16 and lin.weight.is_cuda:
+                packed_weight(lin.weight)
 
     def start_token(self, start: torch.Tensor, seat: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:271-274: start_in(encode_start) + position[0] + token_type[0]."""
@@ -163,11 +164,12 @@ class SeqPolicy(nn.Module):
 
     def readout(self, h: torch.Tensor, normed: torch.Tensor | None = None) -> torch.Tensor:
         """cugo_seq50.py:187-189 and :288-289: head(norm(h)), the norm as one HIP launch
-        (or `normed`, norm(h) already computed) and the head's first Linear with its GELU
-        as another where they fit."""
+        (or `normed`, norm(h) already computed), the head's first Linear with its GELU as
+        another and its output Linear as a third where they fit."""
         if h.dim() == 2 and is_exact_gelu(self.head[1]):
             z = add_norm(h, None, self.norm)[1] if normed is None else normed
-            out = self.head[2](linear(z, self.head[0].weight, self.head[0].bias, gelu=True))
+            u = linear(z, self.head[0].weight, self.head[0].bias, gelu=True)
+            out = linear(u, self.head[2].weight, self.head[2].bias)
         else:
             out = self.head(self.norm(h))
         return out.squeeze(-1) if out.shape[-1] == 1 else out

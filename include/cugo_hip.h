@@ -383,8 +383,9 @@ int cugo_add_layernorm(int dtype, const void* x, const void* y, const void* weig
  * [n] row for every row), added to each output after its rounding and rounded again (the
  * last layer's x + linear2(u), cugo_seq50.py:322; the query token's + token_type[2],
  * :166-180); y may alias residual; fp32 accumulation.  Requires k in {64, 128, 256,
- * 512, 1024}, n % 4 == 0, ldx % 8 == 0, ldy % 4 == 0, x and w_packed 16-byte aligned, y
- * and bias 8-byte aligned.  tile: 0 chooses the workgroup tile from the shape; 1-7 force
+ * 512, 1024}, ldx % 8 == 0, ldy >= n, x and w_packed 16-byte aligned, y and bias 8-byte
+ * aligned, and with a residual n % 4 == 0 and ldy % 4 == 0 (any n without one: the
+ * head's 179 logits).  tile: 0 chooses the workgroup tile from the shape; 1-7 force
  * 32 x 128, 64 x 128 (8 wavefronts), 64 x 128, 128 x 128 (8), 64 x 64, 128 x 128 or
  * 32 x 256 (rows x columns; -7 where the X panel, rows x k, passes the LDS).  Returns -3
  * for an unsupported shape,

@@ -166,7 +166,8 @@ def test_add_layernorm_matches_torch(ext, dtype, d):
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 768, 256), (8192, 1024, 256), (4096, 256, 1024),
-                                   (1001, 260, 128), (1, 4, 64), (70, 1028, 512)])
+                                   (1001, 260, 128), (1, 4, 64), (70, 1028, 512),
+                                   (4096, 179, 256), (33, 7, 64)])
 def test_linear_matches_float64(ext, m, n, k):
     """`linear` against the float64 product of the same bf16 operands, + bias, rounded to
     bf16: every element within the bound of an fp32 sum of k products (k 2^-24 times the
@@ -174,7 +175,9 @@ def test_linear_matches_float64(ext, m, n, k):
     form equals torch's F.gelu of its plain form bit for bit; every workgroup tile gives
     identical bits (the same K order); with a residual, torch's bf16 add of the two; a
     row-strided x, no bias, the packed-weight cache (rebuilt in place when the weight
-    changes), and the shape checks."""
+    changes), and the shape checks.  An n that is not a multiple of 4 (the head's 179
+    logits) gives the first n columns of the same product over the zero-padded weight,
+    and takes no residual."""
     from cugo_amd.seq_decode import linear, packed_weight
 
     announce(f"linear m={m} n={n} k={k}")
@@ -209,6 +212,15 @@ def test_linear_matches_float64(ext, m, n, k):
                 ext.linear(x, wp, n, b, tile=tile)
     check(ext.linear(x, wp, n, None), None)
     r = torch.randn(m, n, generator=g).to(torch.bfloat16).to(DEV)  # residual, torch's bf16 add
+    if n % 4 != 0:
+        n16 = (n + 15) // 16 * 16
+        b16 = torch.zeros(n16, dtype=torch.bfloat16, device=DEV)
+        b16[:n] = b
+        assert torch.equal(ext.linear(x, wp, n16, b16)[:, :n], got)
+        assert torch.equal(linear(x, w, b), got)
+        with pytest.raises(RuntimeError):  # a residual needs n % 4 == 0
+            ext.linear(x, wp, n, b, residual=r)
+        return
     assert torch.equal(ext.linear(x, wp, n, b, residual=r), r + got)
     assert torch.equal(ext.linear(x, wp, n, b, gelu=True, residual=r),
                        r + torch.nn.functional.gelu(got))
@@ -232,8 +244,6 @@ def test_linear_matches_float64(ext, m, n, k):
             ext.linear(torch.zeros(4, 96, dtype=torch.bfloat16, device=DEV),
                        ext.mlp_pack_weight(torch.zeros(4, 96, dtype=torch.bfloat16,
                                                        device=DEV), 16, 96), 4)
-        with pytest.raises(RuntimeError):  # n % 4
-            ext.linear(x, ext.mlp_pack_weight(w[:3].contiguous(), 16, k), 3)
         with pytest.raises(RuntimeError):  # packed size does not match n
             ext.linear(x, wp, n + 16, None)
         with pytest.raises(RuntimeError):
