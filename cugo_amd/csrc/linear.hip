@@ -889,11 +889,12 @@ static int ffn_launch(const ffn::Args& a, int rows, bool out, hipStream_t stream
   const int64_t m = a.m;
   if (rows == 0) {
     // Rows a workgroup: every workgroup streams all 1 MiB of weights through its CU's
-    // L1, which bounds the kernel, so the tile that leaves each CU the fewest rows (rounds
-    // of one workgroup a CU x rows); on a tie the smaller, or with out_proj (128 KiB more
-    // a workgroup) the larger.  Measured (us, 32 / 48 / 64 rows): 8,192 rows 24.9 / 29.6 /
-    // 36.1; 12,288: 33.6 / 31.9 / 37.3; 16,384: 36.5 / 44.1 / 39.9; with out_proj, 16,384:
-    // 53.1 / 66.0 / 45.3.
+    // L1 (1.125 MiB with out_proj), which bounds the kernel, so the tile that leaves each
+    // CU the fewest rows (rounds of one workgroup a CU x rows), the larger on a tie (fewer
+    // workgroups streaming the weights).  Measured with out_proj (us, 16 / 32 / 48 / 64
+    // rows): 4,096 rows 19.7 / 24.7 / 33.2 / -; 8,192: 30.6 / 27.5 / 33.8 / -; 12,288:
+    // 42.9 / 48.8 / 36.0 / 43.4; 16,384: - / 53.4 / 65.8 / 45.7; without it, 12,288: 39.5 /
+    // 34.0 / 31.1 / 36.6.
     int cus = 256;
     int dev = 0;
     if (hipGetDevice(&dev) == hipSuccess) {
@@ -903,9 +904,9 @@ static int ffn_launch(const ffn::Args& a, int rows, bool out, hipStream_t stream
         cus = n;
     }
     int64_t best = -1;
-    for (int r : {32, 48, 64}) {
+    for (int r : {16, 32, 48, 64}) {
       const int64_t load = ((m + r - 1) / r + cus - 1) / cus * r;
-      if (best < 0 || load < best || (out && load == best)) {
+      if (best < 0 || load <= best) {
         best = load;
         rows = r;
       }
@@ -921,6 +922,7 @@ static int ffn_launch(const ffn::Args& a, int rows, bool out, hipStream_t stream
     ffn::ffn_kernel<MT, 5, false><<<grid(R), ffn::kThreads, 0, stream>>>(a);              \
   break;
   switch (rows) {
+    case 16: CUGO_FFN_LAUNCH(1, 16)
     case 32: CUGO_FFN_LAUNCH(2, 32)
     case 48: CUGO_FFN_LAUNCH(3, 48)
     case 64: CUGO_FFN_LAUNCH(4, 64)

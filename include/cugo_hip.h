@@ -418,7 +418,7 @@ int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
  * ldh (16-byte aligned); x, x_out, ln contiguous [m, 256] (x_out may alias x); w1_packed
  * the [1,024, 256] linear1 weight and w2_packed the [256, 1,024] linear2 weight in
  * cugo_mlp_pack_weight form (rows_pad = rows, cols_pad = cols); b1 [1,024], b2 [256],
- * ln_weight / ln_bias [256]; all bf16.  rows: rows a workgroup (32, 48 or 64; 0 chooses by
+ * ln_weight / ln_bias [256]; all bf16.  rows: rows a workgroup (16, 32, 48 or 64; 0 chooses by
  * m).  No reference counterpart as one call. */
 int cugo_ffn(const void* h, int64_t ldh, const void* x, const void* w1_packed, const void* b1,
              const void* w2_packed, const void* b2, const void* ln_weight, const void* ln_bias,

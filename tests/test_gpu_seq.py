@@ -341,7 +341,7 @@ def test_ffn_equals_its_two_launches(ext, m):
         u = ext.linear(h, w1p, 1024, b1, True)
         want_x, want_ln = ext.linear_add_layernorm(u, w2p, b2, x, norm.weight, norm.bias, norm.eps)
         want_plain = ext.linear(u, w2p, 256, b2, False, residual=x)
-        for rows in (0, 32, 48, 64):
+        for rows in (0, 16, 32, 48, 64):
             xo, ln = ext.ffn(h, x, w1p, b1, w2p, b2, norm.weight, norm.bias, norm.eps, rows)
             assert torch.equal(xo, want_x) and torch.equal(ln, want_ln), rows
             plain, empty = ext.ffn(h, x, w1p, b1, w2p, b2, rows=rows)
@@ -401,7 +401,7 @@ def test_out_proj_ffn_equals_its_launches(ext, m):
                                   nxt.eps)
         want_plain, _ = ext.ffn(h, x1, w1p, l1.bias, w2p, l2.bias)
         args = (wop, op.bias, n2.weight, n2.bias, n2.eps, w1p, l1.bias, w2p, l2.bias)
-        for rows in (0, 32, 48, 64):
+        for rows in (0, 16, 32, 48, 64):
             xo, ln = ext.out_proj_ffn(att, x, *args, nxt.weight, nxt.bias, nxt.eps, rows)
             assert torch.equal(xo, want_x) and torch.equal(ln, want_ln), rows
             plain, empty = ext.out_proj_ffn(att, x, *args, rows=rows)
