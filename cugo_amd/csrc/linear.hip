@@ -824,8 +824,10 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
   a.ldy = (int)ldy;
   a.wtiles = (int)((n + 15) / 16);
   if (tile == 0) {  // by the decoder step's shapes: 64-row tiles once 32-row ones pass
-    const int64_t blocks32 = ((m + 31) / 32) * ((n + 127) / 128);  // ~4 a CU
-    tile = blocks32 > 1024 ? 2 : 1;
+    // ~4 a CU, 128-row tiles past ~8 (in_proj, us by tile 1 / 2 / 4: 4,096 x 768 x 256
+    // 5.7 / 6.4 / 6.2; 12,288 rows 12.6 / 12.6 / 12.0; 16,384 rows 16.5 / 15.6 / 13.2)
+    const int64_t blocks32 = ((m + 31) / 32) * ((n + 127) / 128);
+    tile = blocks32 > 2048 && k <= 512 ? 4 : blocks32 > 1024 ? 2 : 1;
   }
   switch (tile) {
     case 1: return launch<2, 2, 1, 4, 3>(a, (int)k, act, stream);  // 32 rows x 128 columns
