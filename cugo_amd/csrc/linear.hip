@@ -38,6 +38,8 @@
 // clamped on load and masked on store.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <stdint.h>
 
 #include "../../include/cugo_hip.h"
@@ -61,7 +63,7 @@ struct Args {
   int col_blocks;  // workgroups along n
   int wtiles;      // 16-row tiles of the packed W
   // the residual (row stride ldr, 0: one row for all), added to the output after its
-  // rounding (NULL: none); kAddNorm's residual (row stride ldy), rows of n = BN elements
+  // rounding (NULL: none); kAddNorm's too, its rows of n = BN elements
   const __bf16* res;
   int ldr;
   const __bf16* ln_w;
@@ -147,7 +149,7 @@ __global__ __launch_bounds__(64 * WR * WC) void linear_kernel(Args a) {
 #pragma unroll
     for (int j = 0; j < kNormRows; ++j) {
       const int row = min(m0 + wave + WR * WC * j, a.m - 1);
-      res_v[j] = *reinterpret_cast<const bf16x4*>(a.res + (int64_t)row * a.ldy + lane * 4);
+      res_v[j] = *reinterpret_cast<const bf16x4*>(a.res + (int64_t)row * a.ldr + lane * 4);
     }
   }
 
@@ -843,12 +845,13 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
 
 int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
                               const void* bias, int64_t m, int64_t n, int64_t k, const void* res,
-                              const void* ln_weight, const void* ln_bias, float eps,
+                              int64_t ldr, const void* ln_weight, const void* ln_bias, float eps,
                               void* x_out, void* ln, int tile, hipStream_t stream) {
   if (m < 0 || (m > 0 && (!x || !w_packed || !res || !ln_weight || !ln_bias || !x_out || !ln)))
     return -1;
   const bool k_ok = k == 64 || k == 128 || k == 256 || k == 512 || k == 1024;
-  if (!k_ok || n != 256 || ldx < k || ldx % 8 != 0) return -3;
+  if (!k_ok || n != 256 || ldx < k || ldx % 8 != 0 || (ldr != 0 && (ldr < n || ldr % 4 != 0)))
+    return -3;
   const uintptr_t p16 = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed);
   const uintptr_t p8 = reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(res) |
                        reinterpret_cast<uintptr_t>(ln_weight) |
@@ -868,6 +871,7 @@ int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
   a.ldy = (int)n;
   a.wtiles = (int)((n + 15) / 16);
   a.res = static_cast<const __bf16*>(res);
+  a.ldr = (int)ldr;
   a.ln_w = static_cast<const __bf16*>(ln_weight);
   a.ln_b = static_cast<const __bf16*>(ln_bias);
   a.ln = static_cast<__bf16*>(ln);
@@ -897,13 +901,18 @@ static int ffn_launch(const ffn::Args& a, int rows, bool out, hipStream_t stream
     // rows): 4,096 rows 19.7 / 24.7 / 33.2 / -; 8,192: 30.6 / 27.5 / 33.8 / -; 12,288:
     // 42.9 / 48.8 / 36.0 / 43.4; 16,384: - / 53.4 / 65.8 / 45.7; without it, 12,288: 39.5 /
     // 34.0 / 31.1 / 36.6.
+    // the device's CU count, asked once a device (every caller stores the same answer)
+    static std::atomic<int> cus_of[64];
     int cus = 256;
     int dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess) {
-      int n = 0;
-      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-          n > 0)
-        cus = n;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+      cus = cus_of[dev].load(std::memory_order_relaxed);
+      if (cus == 0) {
+        int n = 0;
+        cus = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+                          hipSuccess && n > 0 ? n : 256;
+        cus_of[dev].store(cus, std::memory_order_relaxed);
+      }
     }
     int64_t best = -1;
     for (int r : {16, 32, 48, 64}) {

@@ -105,10 +105,50 @@ __device__ inline void add_scaled(float (&acc)[K], float x, int j,
   for (int k = 0; k < K; ++k) acc[k] += x * w[k];
 }
 
+// ln[lane's columns] = LayerNorm(v) * w + b of one row held K values a lane over a
+// wavefront: fp32 mean and variance (two passes, xor-shuffle sums), rounded to the dtype
+// (nn.LayerNorm on the dtype's values; add_layernorm_kernel below and the token kernels'
+// fused norm share it, so they give the same bits).
+template <class T, int K>
+__device__ inline void row_norm(const float (&v)[K], const typename T::storage* w,
+                                const typename T::storage* b, float eps, int d, int lane,
+                                typename T::storage* ln) {
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) sum += v[k];
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  const float mean = sum / (float)d;
+  float sq = 0.0f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float c = v[k] - mean;
+    sq += c * c;
+  }
+  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+  const float rstd = 1.0f / sqrtf(sq / (float)d + eps);
+  float wv[K], bv[K], o[K];
+  load_row<T, K>(w + lane * K, wv);
+  load_row<T, K>(b + lane * K, bv);
+#pragma unroll
+  for (int k = 0; k < K; ++k) o[k] = (v[k] - mean) * rstd * wv[k] + bv[k];
+  store_row<T, K>(ln + lane * K, o);
+}
+
+// The token's last two adds and its store; with `norm`, also LayerNorm of the stored
+// token into norm.out (the first layer's norm1, as add_layernorm would compute it).
+template <class T>
+struct TokenNorm {
+  const typename T::storage* w;
+  const typename T::storage* b;
+  float eps;
+  typename T::storage* out;  // NULL: no norm
+};
+
 template <class T, int K>
 __device__ inline void finish(float (&acc)[K], const typename T::storage* position,
                               const typename T::storage* token_type,
-                              typename T::storage* out, int d, int lane) {
+                              typename T::storage* out, int d, int lane,
+                              const TokenNorm<T>& norm = TokenNorm<T>{}, i64 row = 0) {
   float p[K], t[K], o[K];
   load_row<T, K>(position + lane * K, p);
   load_row<T, K>(token_type + lane * K, t);
@@ -119,6 +159,12 @@ __device__ inline void finish(float (&acc)[K], const typename T::storage* positi
     o[k] = r2 + t[k];
   }
   store_row<T, K>(out + lane * K, o);
+  if (norm.out != nullptr) {
+    float v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = T::round(o[k]);  // the stored token's values
+    row_norm<T, K>(v, norm.w, norm.b, norm.eps, d, lane, norm.out + row * d);
+  }
 }
 
 // SeqNet.event_token(words, seat, index) (cugo_seq50.py:276-282) with encode_events
@@ -131,7 +177,8 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void event_tokens_kernel(
     const i64* words, i64 word_rows, const i64* seat, const i64* index, i64 n,
     const typename T::storage* wt, const typename T::storage* bias,
     const typename T::storage* position, i64 position_rows,
-    const typename T::storage* token_type, int d, typename T::storage* out) {
+    const typename T::storage* token_type, int d, typename T::storage* out,
+    TokenNorm<T> norm) {
   const int lane = threadIdx.x & 63;
   const i64 r = (i64)blockIdx.x * kRowsPerBlock + uniform(threadIdx.x >> 6);
   if (r >= n) return;
@@ -164,7 +211,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void event_tokens_kernel(
   p = 1 + (p < kMaxEvents - 1 ? p : kMaxEvents - 1);
   if (p < 0) p = 0;
   if (p >= position_rows) p = position_rows - 1;
-  finish<T>(acc, position + p * d, token_type + d, out + r * d, d, lane);
+  finish<T>(acc, position + p * d, token_type + d, out + r * d, d, lane, norm, r);
 }
 
 // SeqNet.start_token(start, seat) (cugo_seq50.py:271-274) with encode_start (:113-128):
@@ -666,25 +713,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
     for (int k = 0; k < K; ++k) v[k] = T::round(v[k] + u[k]);
     store_row<T, K>(x_out + at, v);
   }
-  float sum = 0.0f;
-#pragma unroll
-  for (int k = 0; k < K; ++k) sum += v[k];
-  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-  const float mean = sum / (float)d;
-  float sq = 0.0f;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const float c = v[k] - mean;
-    sq += c * c;
-  }
-  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
-  const float rstd = 1.0f / sqrtf(sq / (float)d + eps);
-  float wv[K], bv[K], o[K];
-  load_row<T, K>(w + lane * K, wv);
-  load_row<T, K>(b + lane * K, bv);
-#pragma unroll
-  for (int k = 0; k < K; ++k) o[k] = (v[k] - mean) * rstd * wv[k] + bv[k];
-  store_row<T, K>(ln + at, o);
+  row_norm<T, K>(v, w, b, eps, d, lane, ln + r * d);
 }
 
 template <class T>
@@ -714,14 +743,16 @@ template <class T>
 int launch_event(const i64* words, i64 word_rows, const i64* seat, const i64* index, i64 n,
                  const void* wt,
                  const void* bias, const void* position, i64 position_rows,
-                 const void* token_type, int d, void* out, hipStream_t stream) {
+                 const void* token_type, int d, void* out, const void* ln_w, const void* ln_b,
+                 float eps, void* ln, hipStream_t stream) {
   using S = typename T::storage;
   const unsigned grid = (unsigned)((n + kRowsPerBlock - 1) / kRowsPerBlock);
+  const TokenNorm<T> norm{(const S*)ln_w, (const S*)ln_b, eps, (S*)ln};
 #define CUGO_EVENT_CASE(KK)                                                                 \
   case KK:                                                                                  \
     event_tokens_kernel<T, KK><<<grid, 64 * kRowsPerBlock, 0, stream>>>(                    \
         words, word_rows, seat, index, n, (const S*)wt, (const S*)bias, (const S*)position, \
-        position_rows, (const S*)token_type, d, (S*)out);                                   \
+        position_rows, (const S*)token_type, d, (S*)out, norm);                             \
     break;
   switch (d / 64) {
     CUGO_EVENT_CASE(1)
@@ -783,20 +814,25 @@ extern "C" {
 int cugo_event_tokens(int dtype, const int64_t* words, int64_t word_rows, const int64_t* seat,
                       const int64_t* index, int64_t n, const void* weight_t, const void* bias,
                       const void* position, int64_t position_rows, const void* token_type,
-                      int64_t d, void* out, hipStream_t stream) {
+                      int64_t d, void* out, const void* ln_weight, const void* ln_bias,
+                      float eps, void* ln, hipStream_t stream) {
   if (n < 0 || position_rows < 1 || (n > 0 && (word_rows < 1 || n % word_rows != 0)) ||
       (n > 0 && (!words || !seat || !index || !weight_t || !bias || !position ||
-                 !token_type || !out)))
+                 !token_type || !out)) ||
+      (ln != nullptr && (!ln_weight || !ln_bias)))
     return -1;
   if (!valid_width(d)) return -3;
-  if (!aligned_rows(dtype, d, {weight_t, bias, position, token_type, out})) return -4;
+  if (!aligned_rows(dtype, d, {weight_t, bias, position, token_type, out, ln_weight, ln_bias, ln}))
+    return -4;
   if (n == 0) return 0;
   if (dtype == CUGO_DTYPE_BF16)
     return launch_event<BF16>(words, word_rows, seat, index, n, weight_t, bias, position,
-                              position_rows, token_type, (int)d, out, stream);
+                              position_rows, token_type, (int)d, out, ln_weight, ln_bias, eps,
+                              ln, stream);
   if (dtype == CUGO_DTYPE_F32)
     return launch_event<F32>(words, word_rows, seat, index, n, weight_t, bias, position,
-                             position_rows, token_type, (int)d, out, stream);
+                             position_rows, token_type, (int)d, out, ln_weight, ln_bias, eps, ln,
+                             stream);
   return -2;
 }
 

@@ -824,7 +824,10 @@ int token_dtype(const torch::Tensor& w) {
 // written into `out` (contiguous [n, d]) when given.
 torch::Tensor event_tokens(torch::Tensor words, torch::Tensor seat, torch::Tensor index,
                            torch::Tensor weight_t, torch::Tensor bias, torch::Tensor position,
-                           torch::Tensor token_type, c10::optional<torch::Tensor> out_opt) {
+                           torch::Tensor token_type, c10::optional<torch::Tensor> out_opt,
+                           c10::optional<torch::Tensor> ln_weight,
+                           c10::optional<torch::Tensor> ln_bias, double eps,
+                           c10::optional<torch::Tensor> ln_out) {
   TORCH_CHECK(words.is_cuda() && words.is_contiguous() && words.dim() == 2 &&
                   words.size(1) == CUGO_EVENT_WORDS && words.scalar_type() == at::kLong,
               "words must be a contiguous CUDA int64 [n, EVENT_WORDS] tensor");
@@ -841,11 +844,30 @@ torch::Tensor event_tokens(torch::Tensor words, torch::Tensor seat, torch::Tenso
   check_token_weights(weight_t, bias, position, token_type, 8 * 50 + 12 + 2, words);
   const DeviceGuard guard(words.device());
   auto out = out_or_new(out_opt, {n, weight_t.size(1)}, weight_t.scalar_type(), words, "out");
+  // with ln_out: also the tokens' LayerNorm (the first layer's norm1) into ln_out
+  TORCH_CHECK(ln_out.has_value() == (ln_weight.has_value() && ln_bias.has_value()),
+              "ln_out goes with ln_weight and ln_bias");
+  const int64_t d = weight_t.size(1);
+  if (ln_out.has_value()) {
+    for (const auto* t : {&*ln_weight, &*ln_bias})
+      TORCH_CHECK(t->scalar_type() == weight_t.scalar_type() && t->is_contiguous() &&
+                      t->numel() == d,
+                  "ln_weight and ln_bias must be contiguous [d] tensors of the weights' dtype");
+    TORCH_CHECK(ln_out->scalar_type() == weight_t.scalar_type() && ln_out->is_contiguous() &&
+                    ln_out->dim() == 2 && ln_out->size(0) == n && ln_out->size(1) == d,
+                "ln_out must be a contiguous [n, d] tensor of the weights' dtype");
+    check_same_device(words, *ln_weight, "words", "ln_weight");
+    check_same_device(words, *ln_bias, "words", "ln_bias");
+    check_same_device(words, *ln_out, "words", "ln_out");
+  }
   check_call(cugo_event_tokens(token_dtype(weight_t), words.data_ptr<int64_t>(), word_rows,
                                seat.data_ptr<int64_t>(), index.data_ptr<int64_t>(), n,
                                weight_t.data_ptr(), bias.data_ptr(), position.data_ptr(),
-                               position.size(0), token_type.data_ptr(), weight_t.size(1),
-                               out.data_ptr(), stream()),
+                               position.size(0), token_type.data_ptr(), d, out.data_ptr(),
+                               ln_out.has_value() ? ln_weight->data_ptr() : nullptr,
+                               ln_out.has_value() ? ln_bias->data_ptr() : nullptr,
+                               static_cast<float>(eps),
+                               ln_out.has_value() ? ln_out->data_ptr() : nullptr, stream()),
              "event_tokens");
   return out;
 }
@@ -956,13 +978,15 @@ std::vector<torch::Tensor> linear_add_layernorm(torch::Tensor x, torch::Tensor w
                                                 c10::optional<torch::Tensor> bias,
                                                 torch::Tensor res, torch::Tensor ln_weight,
                                                 torch::Tensor ln_bias, double eps,
-                                                int64_t tile) {
+                                                int64_t tile, c10::optional<torch::Tensor> out,
+                                                c10::optional<torch::Tensor> ln_out) {
   TORCH_CHECK(x.is_cuda() && x.dim() == 2 && x.scalar_type() == at::kBFloat16 && x.stride(1) == 1,
               "x must be a CUDA bfloat16 [m, k] tensor with unit stride along k");
   const int64_t m = x.size(0), k = x.size(1), n = 256;
-  TORCH_CHECK(res.is_contiguous() && res.dim() == 2 && res.size(0) == m && res.size(1) == n &&
-                  res.scalar_type() == at::kBFloat16,
-              "res must be a contiguous bfloat16 [m, 256] tensor");
+  TORCH_CHECK(res.is_contiguous() && res.scalar_type() == at::kBFloat16 &&
+                  ((res.dim() == 2 && res.size(0) == m && res.size(1) == n) ||
+                   (res.dim() == 1 && res.size(0) == n)),
+              "res must be a contiguous bfloat16 [m, 256] tensor or a [256] row for all");
   TORCH_CHECK(w_packed.scalar_type() == at::kBFloat16 && w_packed.is_contiguous() &&
                   w_packed.numel() == n * k,
               "w_packed must be the packed bfloat16 [256, k] weight");
@@ -980,12 +1004,13 @@ std::vector<torch::Tensor> linear_add_layernorm(torch::Tensor x, torch::Tensor w
     check_same_device(x, *bias, "x", "bias");
   }
   const DeviceGuard guard(x.device());
-  auto x_out = torch::empty_like(res);
-  auto ln = torch::empty_like(res);
+  auto x_out = out_or_new(out, {m, n}, at::kBFloat16, x, "out");
+  auto ln = out_or_new(ln_out, {m, n}, at::kBFloat16, x, "ln_out");
   const int64_t ldx = m > 1 ? x.stride(0) : k;
   check_call(cugo_linear_add_layernorm(x.data_ptr(), ldx, w_packed.data_ptr(),
                                        bias.has_value() ? bias->data_ptr() : nullptr, m, n, k,
-                                       res.data_ptr(), ln_weight.data_ptr(), ln_bias.data_ptr(),
+                                       res.data_ptr(), res.dim() == 2 ? n : 0,
+                                       ln_weight.data_ptr(), ln_bias.data_ptr(),
                                        static_cast<float>(eps), x_out.data_ptr(), ln.data_ptr(),
                                        static_cast<int>(tile), stream()),
              "linear_add_layernorm");
@@ -1755,7 +1780,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("event_tokens", &event_tokens, "SeqNet.event_token: event_in(encode_events) + position + type",
         pybind11::arg("words"), pybind11::arg("seat"), pybind11::arg("index"),
         pybind11::arg("weight_t"), pybind11::arg("bias"), pybind11::arg("position"),
-        pybind11::arg("token_type"), pybind11::arg("out") = pybind11::none());
+        pybind11::arg("token_type"), pybind11::arg("out") = pybind11::none(),
+        pybind11::arg("ln_weight") = pybind11::none(), pybind11::arg("ln_bias") = pybind11::none(),
+        pybind11::arg("eps") = 1e-5, pybind11::arg("ln_out") = pybind11::none());
   m.def("start_tokens", &start_tokens, "SeqNet.start_token: start_in(encode_start) + position + type");
   m.def("add_layernorm", &add_layernorm, "x + y and LayerNorm(x + y) in one launch",
         pybind11::arg("x"), pybind11::arg("y"), pybind11::arg("weight"), pybind11::arg("bias"),
@@ -1769,7 +1796,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "linear, then the residual add and LayerNorm of add_layernorm, in one launch",
         pybind11::arg("x"), pybind11::arg("w_packed"), pybind11::arg("bias"), pybind11::arg("res"),
         pybind11::arg("ln_weight"), pybind11::arg("ln_bias"), pybind11::arg("eps"),
-        pybind11::arg("tile") = 0);
+        pybind11::arg("tile") = 0, pybind11::arg("out") = pybind11::none(),
+        pybind11::arg("ln_out") = pybind11::none());
   pybind11::class_<SelfPlayState>(m, "SelfPlayState",
                                    "A self-play wave's tensors and its step bookkeeping")
       .def(pybind11::init<int64_t, int64_t, torch::Tensor, torch::Tensor, torch::Tensor,

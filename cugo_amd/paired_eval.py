@@ -105,6 +105,7 @@ class _SequenceSeat:
         d = model.position.shape[1]
         self.cache = policy_cache(model, games, dev)
         self.pair = torch.zeros((2 * games, d), dtype=dtype, device=dev)
+        self.pair_h = torch.zeros_like(self.pair)  # norm1 of the rows, from their launches
         # slots of the waiting event tokens and of the next queries; -1 skips a row (an
         # event not kept, the query of a game that is over)
         self.event_pos = torch.full((games,), -1, dtype=torch.int64, device=dev)
@@ -144,15 +145,17 @@ class _SequenceSeat:
         from .seq_decode import cached_step_pair
 
         m, g = self.model, self.games
-        m.query_from_input(self.q_in, out=self.pair[g:])
+        m.query_from_input(self.q_in, out=self.pair[g:], norm_out=self.pair_h[g:])
         hidden, normed = cached_step_pair(m, self.cache, self.pair, g, self.event_pos,
-                                          self.query_pos, self.ids, final_norm=m.norm)
+                                          self.query_pos, self.ids, final_norm=m.norm,
+                                          h=self.pair_h)
         return m.readout(hidden, normed)  # the queries' (the events' are not kept)
 
     def events(self, events: torch.Tensor, count: torch.Tensor) -> None:
         """This step's event tokens, each game's from `seat`'s view at position 1 + count
         (cugo_seq50.py:276-282), waiting for the next step's pass."""
-        self.model.event_token(events, self.seat, count, out=self.pair[:self.games])
+        self.model.event_token(events, self.seat, count, out=self.pair[:self.games],
+                               norm_out=self.pair_h[:self.games])
 
 
 def _bf16_twin(model: nn.Module) -> nn.Module:

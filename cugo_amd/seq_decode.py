@@ -276,7 +276,8 @@ def cached_step(model: nn.Module, cache, x: torch.Tensor, slots: int | None = No
 
 def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a: torch.Tensor,
                      pos_b: torch.Tensor, rows_b: torch.Tensor,
-                     final_norm: nn.Module | None = None, prune: bool = True):
+                     final_norm: nn.Module | None = None, prune: bool = True,
+                     h: torch.Tensor | None = None):
     """cached_step for two groups of tokens at once: rows [0, split) of x (group a, one
     token for each of the cache rows 0 .. split - 1, written at slot pos_a[r]) and rows
     [split, n) (group b, one token for cache row rows_b[j], at slot pos_b[j]).  At every
@@ -290,12 +291,14 @@ def cached_step_pair(model: nn.Module, cache, x: torch.Tensor, split: int, pos_a
     whose outputs the reference discards (cugo_seq_selfplay50.py:156), so at the last layer
     (`prune`) they only append their key and value (`kv_append`) and skip the attention,
     out_proj and feed-forward; b's outputs and every cache slot are the bits of the full
-    pass (`prune=False`)."""
+    pass (`prune=False`).  `h`, if given, is the first layer's norm1 of x, already written
+    by the launches that made x."""
     n, d = x.shape
     heads = cache.heads
     dh = d // heads
     layers = model.encoder.layers
-    x, h = add_norm(x, None, layers[0].norm1)
+    if h is None:
+        x, h = add_norm(x, None, layers[0].norm1)
     att = torch.empty((n, heads, dh), dtype=x.dtype, device=x.device)
     for i, layer in enumerate(layers):
         sa = layer.self_attn

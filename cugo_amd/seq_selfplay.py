@@ -25,8 +25,8 @@ import torch
 from torch import nn
 
 from .cugo_torch50_ext import load_extension
-from .seq_decode import (KVCache, add_norm, cached_step, cached_step_pair, is_exact_gelu,
-                         linear, packed_weight, prepare_linears)
+from .seq_decode import (KVCache, _fits_linear, add_norm, cached_step, cached_step_pair,
+                         is_exact_gelu, linear, packed_weight, prepare_linears)
 
 FEATURES = 720
 ACTIONS = 179
@@ -127,15 +127,38 @@ class SeqPolicy(nn.Module):
                                        self._weight_t("start_in"), self.start_in.bias.detach(),
                                        self.position.detach(), self.token_type.detach())
 
+    def _norm1(self) -> nn.Module:
+        """The first encoder layer's norm1 (the pre-norm every token meets first)."""
+        return self.encoder.layers[0].norm1
+
+    def _fused_norm1(self) -> bool:
+        """Whether the token launches can write norm1 of their tokens themselves: an
+        affine LayerNorm over d in the tokens' dtype."""
+        n1 = self._norm1()
+        dt = self.event_in.weight.dtype
+        return (isinstance(n1, nn.LayerNorm) and n1.weight is not None and n1.bias is not None
+                and n1.weight.dtype == dt and n1.bias.dtype == dt
+                and tuple(n1.normalized_shape) == (self.position.shape[1],))
+
     def event_token(self, words: torch.Tensor, seat: torch.Tensor, index: torch.Tensor,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None,
+                    norm_out: torch.Tensor | None = None) -> torch.Tensor:
         """cugo_seq50.py:276-282: event_in(encode_events) + position[1 + min(index, 47)]
         + token_type[1].  Row r reads words[r % len(words)] and index[r % len(words)], so one
         copy of the events serves every seat that observes them.  Written into `out` when
-        given."""
-        return self.ext().event_tokens(words.contiguous(), seat.contiguous(), index.contiguous(),
-                                       self._weight_t("event_in"), self.event_in.bias.detach(),
-                                       self.position.detach(), self.token_type.detach(), out)
+        given; with `norm_out`, the first layer's norm1 of the tokens is written there too
+        (in the same launch where the norm allows)."""
+        fused = norm_out is not None and self._fused_norm1()
+        n1 = self._norm1()
+        x = self.ext().event_tokens(words.contiguous(), seat.contiguous(), index.contiguous(),
+                                    self._weight_t("event_in"), self.event_in.bias.detach(),
+                                    self.position.detach(), self.token_type.detach(), out,
+                                    n1.weight.detach() if fused else None,
+                                    n1.bias.detach() if fused else None,
+                                    n1.eps if fused else 1e-5, norm_out if fused else None)
+        if norm_out is not None and not fused:
+            norm_out.copy_(add_norm(x, None, n1)[1])
+        return x
 
     def query_token(self, features: torch.Tensor, legal: torch.Tensor) -> torch.Tensor:
         """cugo_seq50.py:166-180: query_in(features ++ legal) + token_type[2]; events mode
@@ -149,18 +172,32 @@ class SeqPolicy(nn.Module):
         """Feature columns a rollout keeps for this mode (cugo_seq50.py:342-344)."""
         return None if self.mode == "hybrid" else CONTEXT_INDEX
 
-    def query_from_input(self, q_in: torch.Tensor,
-                         out: torch.Tensor | None = None) -> torch.Tensor:
+    def query_from_input(self, q_in: torch.Tensor, out: torch.Tensor | None = None,
+                         norm_out: torch.Tensor | None = None) -> torch.Tensor:
         """query_token on the already concatenated input [n, 720 + 179] (into `out` when
         given); q_in may carry zero columns past the input width (SelfPlayState.prepare's
-        padded rows), so that the first layer and its GELU run as one `linear` launch."""
+        padded rows), so that the first layer and its GELU run as one `linear` launch.
+        With `norm_out`, the first layer's norm1 of the tokens is written there too (in the
+        second layer's launch where the shapes allow)."""
         first, act, second = self.query_in
         if is_exact_gelu(act):
             h = linear(q_in, first.weight, first.bias, gelu=True)
         else:
             h = act(linear(q_in, first.weight, first.bias))
         # + token_type[2] rounded after the layer's own rounding, as torch adds the two
-        return linear(h, second.weight, second.bias, residual=self.token_type[2], out=out)
+        tt = self.token_type[2]
+        if (norm_out is not None and self._fused_norm1() and tt.dtype == torch.bfloat16
+                and second.weight.shape[0] == 256 and second.bias is not None
+                and _fits_linear(h, second.weight, second.bias)):
+            n1 = self._norm1()
+            x, _ = self.ext().linear_add_layernorm(
+                h, packed_weight(second.weight, h.shape[1]), second.bias.detach(), tt.detach(),
+                n1.weight.detach(), n1.bias.detach(), n1.eps, out=out, ln_out=norm_out)
+            return x
+        x = linear(h, second.weight, second.bias, residual=tt, out=out)
+        if norm_out is not None:
+            norm_out.copy_(add_norm(x, None, self._norm1())[1])
+        return x
 
     def readout(self, h: torch.Tensor, normed: torch.Tensor | None = None) -> torch.Tensor:
         """cugo_seq50.py:187-189 and :288-289: head(norm(h)), the norm as one HIP launch
@@ -272,6 +309,8 @@ class SelfPlayWave:
         # skips, as it skips the query of a finished game).  flush() runs them alone.
         d = actor.position.shape[1]
         self.pair = torch.zeros((3 * wave, d), dtype=actor.event_in.weight.dtype, device=dev)
+        # the first layer's norm1 of those rows, written by the launches that make them
+        self.pair_h = torch.zeros_like(self.pair)
         # The query input's rows padded with zeros to a depth `linear` takes (1,024 for the
         # 899 columns of the hybrid mode), or unpadded where none fits.
         q_width = (FEATURES if cols is None else len(cols)) + ACTIONS
@@ -345,9 +384,10 @@ class SelfPlayWave:
                                                      self.q_stride)
         # the last step's event tokens (both seats' rows) and this step's queries through
         # the layers together; the queries attend the events' new keys at every layer
-        actor.query_from_input(q_in, out=self.pair[2 * w:])
+        actor.query_from_input(q_in, out=self.pair[2 * w:], norm_out=self.pair_h[2 * w:])
         hidden, normed = cached_step_pair(actor, self.cache, self.pair, 2 * w, self.event_pos,
-                                          query_pos, query_rows, final_norm=actor.norm)
+                                          query_pos, query_rows, final_norm=actor.norm,
+                                          h=self.pair_h)
         logits = actor.readout(hidden, normed)  # the queries' (the events' are not kept)
         if pool:
             p, opp = self.p, self.opponent
@@ -363,7 +403,8 @@ class SelfPlayWave:
                                                      self.noise_epoch, 0)
         reward0, new_done, nagari, step_status, committed, events = ext.step_events_indexed(
             self.states, self.ids, actions)
-        actor.event_token(events, self.seats2, t.count, out=self.pair[:2 * w])
+        actor.event_token(events, self.seats2, t.count, out=self.pair[:2 * w],
+                          norm_out=self.pair_h[:2 * w])
         if pool:
             opp.cached_step(self.opp_cache,
                             opp.event_token(events[:p], 1 - t.learner_seat[:p], t.count[:p]))

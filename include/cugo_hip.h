@@ -353,12 +353,15 @@ int cugo_decode_order(const int64_t* pos, int64_t n, int64_t slots, int32_t* ord
  *   47)] + token_type[1], with the reference's bf16 roundings (after the Linear, after
  *   each add).  words int64 [word_rows, 9] and index int64 [word_rows] (word_rows divides
  *   n: the self-play step passes each event once for both seats), seat int64 [n],
- *   weight_t [414, d], out [n, d].
+ *   weight_t [414, d], out [n, d].  With ln non-NULL, also ln[r] = LayerNorm(out[r]) *
+ *   ln_weight + ln_bias ([d] each; the first encoder layer's norm1, cugo_seq50.py:318),
+ *   the bits cugo_add_layernorm gives on out (ln NULL: ln_weight and ln_bias unused).
  */
 int cugo_event_tokens(int dtype, const int64_t* words, int64_t word_rows, const int64_t* seat,
                       const int64_t* index, int64_t n, const void* weight_t, const void* bias,
                       const void* position, int64_t position_rows, const void* token_type,
-                      int64_t d, void* out, hipStream_t stream);
+                      int64_t d, void* out, const void* ln_weight, const void* ln_bias,
+                      float eps, void* ln, hipStream_t stream);
 /* cugo_start_tokens: out[i] = SeqNet.start_token(start[i], seat[i]) (cugo_seq50.py:271-274
  * with encode_start :113-128): start_in of the 274-wide opening token + position[0] +
  * token_type[0].  start int64 [n, 8], seat int64 [n], weight_t [274, d], out [n, d]. */
@@ -399,13 +402,15 @@ int cugo_linear(int act, const void* x, int64_t ldx, const void* w_packed, const
  * its output onto res, in one launch: the out_proj / linear2 of a pre-norm encoder layer
  * with the residual add and the next LayerNorm (cugo_seq50.py:316-322).  y = bf16(x w^T +
  * bias); x_out = bf16(res + y); ln = LayerNorm(x_out) * ln_weight + ln_bias, with the
- * statistics and roundings of cugo_add_layernorm.  n must be 256; res, x_out, ln
- * contiguous [m, 256] (x_out may alias res); other requirements as cugo_linear.  tile: 0
- * by shape; 1 for 32-row tiles on 4 wavefronts, 2 on 8, 3 for 16-row tiles on 4, 4 for
- * 64-row tiles on 8. */
+ * statistics and roundings of cugo_add_layernorm.  n must be 256; res [m, 256] with row
+ * stride ldr (256 for contiguous rows; 0: one [256] row added to every row, the query
+ * token's + token_type[2], cugo_seq50.py:166-180, normalised by the first layer's norm1);
+ * x_out, ln contiguous [m, 256] (x_out may alias res); other requirements as
+ * cugo_linear.  tile: 0 by shape; 1 for 32-row tiles on 4 wavefronts, 2 on 8, 3 for
+ * 16-row tiles on 4, 4 for 64-row tiles on 8. */
 int cugo_linear_add_layernorm(const void* x, int64_t ldx, const void* w_packed,
                               const void* bias, int64_t m, int64_t n, int64_t k, const void* res,
-                              const void* ln_weight, const void* ln_bias, float eps,
+                              int64_t ldr, const void* ln_weight, const void* ln_bias, float eps,
                               void* x_out, void* ln, int tile, hipStream_t stream);
 /* cugo_ffn: the feed-forward half of a pre-norm encoder layer of SeqNet.cached_step
  * (cugo_seq50.py:319-322) with the norm after it, in one launch, for d_model 256 and a

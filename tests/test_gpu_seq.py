@@ -96,6 +96,14 @@ def test_event_tokens_against_oracle(ext, dtype, d):
         p = (1 + index.clamp(max=47)).clamp(min=0)
         want = token_reference(tok, w, b, pos[p], tt[1].expand(n, d))
         check_tokens(got, want, dtype)
+        # with the first layer's norm1 in the same launch: add_layernorm's bits
+        nw = (torch.randn(d, generator=torch.Generator().manual_seed(d)) * 0.3 + 1.0).to(dtype).to(DEV)
+        nb = (torch.randn(d, generator=torch.Generator().manual_seed(d + 1)) * 0.1).to(dtype).to(DEV)
+        ln = torch.full((n, d), float("nan"), dtype=dtype, device=DEV)
+        got_n = ext.event_tokens(words, seat, index, w.t().contiguous(), b, pos, tt,
+                                 ln_weight=nw, ln_bias=nb, eps=1e-5, ln_out=ln)
+        assert torch.equal(got_n, got)
+        assert torch.equal(ln, ext.add_layernorm(got, None, nw, nb, 1e-5)[1])
     # each event read once for both seats (rows r and r + n share event r)
     seats2 = torch.cat((torch.zeros(n, dtype=torch.int64, device=DEV),
                         torch.ones(n, dtype=torch.int64, device=DEV)))
@@ -280,8 +288,10 @@ def test_linear_on_a_zero_padded_input(ext):
 @pytest.mark.parametrize("m,k", [(4096, 256), (8192, 1024), (1001, 256), (1, 64)])
 def test_linear_add_layernorm_equals_its_two_launches(ext, m, k):
     """linear_add_layernorm == add_layernorm(res, linear(x)) bit for bit (x_out and ln),
-    with and without bias, on every tile; within torch's bf16 LayerNorm tolerance of the
-    torch ops; the module-level wrapper; only 256-wide rows."""
+    with and without bias, on every tile; with one residual row for every row (the query
+    token's + token_type[2]) == linear with that residual, then add_layernorm; into given
+    output tensors; within torch's bf16 LayerNorm tolerance of the torch ops; the
+    module-level wrapper; only 256-wide rows."""
     from cugo_amd.seq_decode import linear_add_norm
 
     announce(f"linear_add_layernorm m={m} k={k}")
@@ -310,6 +320,15 @@ def test_linear_add_layernorm_equals_its_two_launches(ext, m, k):
         assert rel_err(ln, norm(res + torch.nn.functional.linear(x, w, b))) <= 1e-2
         got = linear_add_norm(x, w, b, res, norm)
         assert torch.equal(got[0], xo) and torch.equal(got[1], ln)
+        row = res[-1].contiguous()  # one residual row for all
+        into = torch.full((m, 256), float("nan"), dtype=torch.bfloat16, device=DEV)
+        ln_into = torch.full((m, 256), float("nan"), dtype=torch.bfloat16, device=DEV)
+        bx, bln = ext.linear_add_layernorm(x, wp, b, row, norm.weight, norm.bias, norm.eps,
+                                           out=into, ln_out=ln_into)
+        assert bx.data_ptr() == into.data_ptr() and bln.data_ptr() == ln_into.data_ptr()
+        want_x = ext.linear(x, wp, 256, b, residual=row)
+        want_ln = ext.add_layernorm(want_x, None, norm.weight, norm.bias, norm.eps)[1]
+        assert torch.equal(into, want_x) and torch.equal(ln_into, want_ln)
         if m == 1:
             with pytest.raises(RuntimeError):  # only 256-wide rows
                 ext.linear_add_layernorm(x, ext.mlp_pack_weight(w[:128].contiguous(), 128, k),
