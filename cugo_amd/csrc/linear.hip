@@ -393,16 +393,21 @@ int launch(const Args& base, int k, int act, hipStream_t stream) {
 //     the MFMAs of the next chunk's linear1 (the last chunk's beside the third linear2
 //     slice), which took 12,288 rows from 26.6 to 24.9 us;
 //   * the epilogue is linear_kernel's: bias, bf16, the residual add, the LayerNorm (or
-//     the plain residual), through LDS row-major.
+//     the plain residual), through LDS row-major;
+//   * with kOut (cugo_out_proj_ffn) the layer's out_proj runs first, on the attention
+//     output's rows in the panel, with linear_kernel's kAddNorm epilogue (x1 = x +
+//     out_proj, kept in registers as the feed-forward's residual; h = norm2(x1) written
+//     over the panel), so neither x1 nor h leaves the CU.
 // Every rounding and every fp32 sum is in the order of linear (GELU) + linear_add_layernorm
-// (or linear with the residual), so the outputs are the same bits.
-// What bounds it: each workgroup streams all 1 MiB of W1 and W2 through its CU's L1 (the
-// FLOPs a weight byte buys are the tile's rows), ~20 bytes a cycle a CU when every CU
-// reads the same weights at once; the GELU's erff is ~5 us of VALU at 12,288 rows (the
-// launch without it: 20.5 against 26.1 us).  At 12,288 rows the launch takes 32 us
-// against 43 for the two launches it replaces.  A GELU table in LDS (gelu() of the 4,736
-// bf16 inputs without a closed form, built by each workgroup, then looked up; the same bits
-// on every finite input) made the launch slower: 39.6 against 31.9 us at 12,288 rows.
+// (or linear with the residual), and with kOut of linear_add_layernorm before them, so the
+// outputs are the same bits.
+// What bounds it: each workgroup streams all 1 MiB of W1 and W2 (and W_o's 128 KiB)
+// through its CU's L1 (the FLOPs a weight byte buys are the tile's rows), ~20 bytes a
+// cycle a CU when every CU reads the same weights at once; the GELU's erff is ~5 us of
+// VALU at 12,288 rows (the launch without it: 20.5 against 26.1 us).  A GELU table in LDS
+// (gelu() of the 4,736 bf16 inputs without a closed form, built by each workgroup, then
+// looked up; the same bits on every finite input) made the launch slower: 39.6 against
+// 31.9 us at 12,288 rows.
 // Weights: linear_kernel's packed fragments, W1 [1,024, 256] (8 K steps a 16-row tile)
 // and W2 [256, 1,024] (32 K steps a tile), read through buffer loads a few K steps ahead
 // of the MFMAs.
