@@ -1163,6 +1163,30 @@ __global__ __launch_bounds__(256) void redeal_kernel(u64* states, const i64* sea
   w[kWordRng] = (u64)rng[r];
 }
 
+// redeal_worlds' acceptance test and copy (python/cugo_ppo50.py:151-172): candidate j, a
+// redealt copy of row missing[j] % rows, is kept when its observer's features and legal
+// mask equal the real deal's value for value (torch's ==, then all over the row); a kept
+// candidate's row goes to row missing[j] of out (rows of out outside [0, out_rows) are
+// never written: such a candidate is reported as not kept).  One wavefront per candidate.
+__global__ __launch_bounds__(256) void accept_worlds_kernel(
+    const float* f, const u8* l, const float* f_real, const u8* l_real, const i64* missing,
+    i64 rows, i64 n, const u64* cand, u64* out, i64 out_rows, u8* same) {
+  const int lane = threadIdx.x & 63;
+  const i64 j = (i64)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (j >= n) return;
+  const i64 dst = missing[j];
+  const bool in = dst >= 0 && dst < out_rows;
+  const i64 r = in ? dst % rows : 0;
+  bool eq = in;
+  for (int k = lane; k < kFeatureCount; k += 64)
+    eq = eq && f[j * kFeatureCount + k] == f_real[r * kFeatureCount + k];
+  for (int k = lane; k < kActionCount; k += 64)
+    eq = eq && l[j * kActionCount + k] == l_real[r * kActionCount + k];
+  const bool all = __ballot(!eq) == 0;  // every lane of the row agrees
+  if (lane == 0) same[j] = all ? 1 : 0;
+  if (all && lane < kRowWords) out[dst * kRowWords + lane] = cand[j * kRowWords + lane];
+}
+
 // ------------------------------------------------------- canonical rollout ----
 // rollout_canonical_torch50 (torch50.h:598-619): each lane deals game i from seeds[i] /
 // first[i] and plays it to the end with the canonical action in registers, then writes
@@ -1638,6 +1662,20 @@ int cugo_redeal(uint8_t* states, const int64_t* seat, const float* keys, const i
   if (n == 0) return 0;
   redeal_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(reinterpret_cast<u64*>(states), seat,
                                                             keys, rng, n);
+  return launched();
+}
+
+int cugo_accept_worlds(const float* features, const uint8_t* legal, const float* real_features,
+                       const uint8_t* real_legal, const int64_t* missing, int64_t rows,
+                       int64_t n, const uint8_t* candidates, uint8_t* out, int64_t out_rows,
+                       uint8_t* same, hipStream_t stream) {
+  if (n < 0 || (n > 0 && (rows < 1 || !features || !legal || !real_features || !real_legal ||
+                          !missing || !candidates || !out || !same)))
+    return kBadArgument;
+  if (n == 0) return 0;
+  accept_worlds_kernel<<<(unsigned)((n + 3) / 4), 256, 0, stream>>>(
+      features, legal, real_features, real_legal, missing, rows, n,
+      reinterpret_cast<const u64*>(candidates), reinterpret_cast<u64*>(out), out_rows, same);
   return launched();
 }
 

@@ -602,6 +602,43 @@ void redeal(torch::Tensor states, torch::Tensor seat, torch::Tensor keys, torch:
              "redeal");
 }
 
+// accept_worlds(features, legal, real_features, real_legal, missing, candidates, out) ->
+// same bool [n]: one try of redeal_worlds (python/cugo_ppo50.py:151-172): candidate j is
+// kept when its observation equals the real row missing[j] % R's, and then copied to
+// row missing[j] of out, in place (cugo_accept_worlds).
+torch::Tensor accept_worlds(torch::Tensor features, torch::Tensor legal, torch::Tensor real_features,
+                            torch::Tensor real_legal, torch::Tensor missing, torch::Tensor candidates,
+                            torch::Tensor out) {
+  check_states(candidates);
+  check_states(out);
+  const int64_t n = candidates.size(0), rows = real_features.size(0);
+  check_1d(missing, at::kLong, "missing");
+  TORCH_CHECK(missing.numel() == n, "missing must have one entry per candidate");
+  TORCH_CHECK(features.is_contiguous() && features.scalar_type() == at::kFloat &&
+                  features.dim() == 2 && features.size(0) == n &&
+                  features.size(1) == CUGO_FEATURE_COUNT &&
+                  real_features.is_contiguous() && real_features.scalar_type() == at::kFloat &&
+                  real_features.dim() == 2 && real_features.size(1) == CUGO_FEATURE_COUNT,
+              "features and real_features must be contiguous float32 [*, FEATURE_COUNT] tensors");
+  TORCH_CHECK(legal.is_contiguous() && legal.scalar_type() == at::kBool && legal.dim() == 2 &&
+                  legal.size(0) == n && legal.size(1) == CUGO_ACTION_COUNT &&
+                  real_legal.is_contiguous() && real_legal.scalar_type() == at::kBool &&
+                  real_legal.dim() == 2 && real_legal.size(0) == rows &&
+                  real_legal.size(1) == CUGO_ACTION_COUNT,
+              "legal and real_legal must be contiguous bool [*, ACTION_COUNT] tensors");
+  TORCH_CHECK(n == 0 || rows > 0, "the real rows must not be empty");
+  for (const auto* t : {&features, &legal, &real_features, &real_legal, &missing, &out})
+    check_same_device(candidates, *t, "candidates", "an input");
+  const DeviceGuard guard(candidates.device());
+  auto same = torch::empty({n}, on(candidates, at::kBool));
+  check_call(cugo_accept_worlds(features.data_ptr<float>(), u8p(legal),
+                                real_features.data_ptr<float>(), u8p(real_legal),
+                                missing.data_ptr<int64_t>(), rows, n, u8p(candidates), u8p(out),
+                                out.size(0), u8p(same), stream()),
+             "accept_worlds");
+  return same;
+}
+
 torch::Tensor seed_samplers(int64_t n, int64_t base_seed, torch::Tensor generation) {
   check_1d(generation, at::kInt, "generation");
   TORCH_CHECK(generation.numel() == n, "generation must have n entries");
@@ -1892,6 +1929,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "the KV append of decode_attention_append without the attention, in place",
         pybind11::arg("k_new"), pybind11::arg("v_new"), pybind11::arg("keys"),
         pybind11::arg("values"), pybind11::arg("pos"), pybind11::arg("rows") = pybind11::none());
+  m.def("accept_worlds", &accept_worlds,
+        "redeal_worlds' acceptance test and copy of one try, in one launch");
   m.def("decode_order", &decode_order,
         "The queries longest first (int32 permutation) for the decode calls' `order`",
         pybind11::arg("pos"), pybind11::arg("slots"));

@@ -33,7 +33,10 @@ def redeal_worlds(ext, states: torch.Tensor, env_rows: torch.Tensor, seat: torch
                   worlds: int, tries: int = 8) -> torch.Tensor:
     """[worlds * R, 248] copies of the rows, world-major, each redealt so the observer's
     features and legal actions are unchanged (cugo_ppo50.py:151-172).  Each try redeals
-    and observes only the rows still without a world, from the real deal again."""
+    and observes only the rows still without a world, from the real deal again; the test
+    against the real observation and the copy of the accepted worlds are one launch
+    (`accept_worlds`), and the count of rows left is the try's one host read (the next
+    try's draws are sized by it, as the reference's are)."""
     if states.shape[1] != STATE_BYTES:
         raise RuntimeError("the state rows must be 248 bytes")
     base = states.index_select(0, env_rows)
@@ -50,9 +53,7 @@ def redeal_worlds(ext, states: torch.Tensor, env_rows: torch.Tensor, seat: torch
         cand = real.index_select(0, missing)
         redeal(ext, cand, seats.index_select(0, missing))
         f, l, _, _, _ = ext.observe_indexed(cand, torch.arange(missing.numel(), device=dev))
-        of = missing % rows  # world-major: copy k of row r is row k * rows + r
-        same = (f == f_real.index_select(0, of)).all(1)
-        same &= (l == l_real.index_select(0, of)).all(1)
-        out.index_copy_(0, missing[same], cand[same])
+        # world-major: copy k of row r is row k * rows + r, compared with real row r
+        same = ext.accept_worlds(f, l, f_real, l_real, missing, cand, out)
         missing = missing[~same]
     return out

@@ -218,6 +218,18 @@ int cugo_step_observe_spares(uint8_t* states, const int64_t* actions, int64_t n,
  * hand; the RNG word becomes rng[i] (torch.randint(-2**62, 2**62, (n,))). */
 int cugo_redeal(uint8_t* states, const int64_t* seat, const float* keys, const int64_t* rng,
                 int64_t n, hipStream_t stream);
+/* redeal_worlds' acceptance test and copy (python/cugo_ppo50.py:151-172, one try): the
+ * candidate rows [n, CUGO_STATE_BYTES] (redealt copies of rows missing[j] % rows) with
+ * their observations features f32 [n, CUGO_FEATURE_COUNT] and legal [n, CUGO_ACTION_COUNT];
+ * same[j] = 1 when candidate j's features and legal mask equal the real deal's
+ * (real_features / real_legal row missing[j] % rows, value for value as torch's ==), and
+ * then its row is copied to row missing[j] of out [out_rows, CUGO_STATE_BYTES]; a
+ * missing[j] outside [0, out_rows) is never written (same[j] = 0).  No reference
+ * counterpart as one call (the reference's torch ops compare, gather and copy). */
+int cugo_accept_worlds(const float* features, const uint8_t* legal, const float* real_features,
+                       const uint8_t* real_legal, const int64_t* missing, int64_t rows,
+                       int64_t n, const uint8_t* candidates, uint8_t* out, int64_t out_rows,
+                       uint8_t* same, hipStream_t stream);
 /* sampler[i] = SplitMix64(base_seed + i + batch * generation[i]).next(), never 0. */
 int cugo_seed_samplers(int64_t n, uint64_t base_seed, const uint32_t* generation,
                        uint64_t* sampler, hipStream_t stream);

@@ -109,3 +109,53 @@ def test_redeal_worlds_keep_the_observers_view(ext):
     torch.manual_seed(1)
     again = redeal_worlds(ext, states, env_rows, player, worlds)
     assert torch.equal(out, again)
+    # the same torch draws through the reference's loop in torch ops (cugo_ppo50.py:151-172:
+    # compare, gather and copy per try) give the same worlds
+    torch.manual_seed(1)
+    assert torch.equal(out, _worlds_in_torch_ops(ext, states, env_rows, player, worlds))
+
+
+def _worlds_in_torch_ops(ext, states, env_rows, seat, worlds, tries=8):
+    from cugo_amd.redeal import redeal
+
+    base = states.index_select(0, env_rows)
+    rows = base.shape[0]
+    f_real, l_real, _, _, _ = ext.observe_indexed(base, torch.arange(rows, device=DEV))
+    real = base.repeat(worlds, 1)
+    seats = seat.repeat(worlds)
+    out = real.clone()
+    missing = torch.arange(real.shape[0], device=DEV)
+    for _ in range(tries):
+        if missing.numel() == 0:
+            break
+        cand = real.index_select(0, missing)
+        redeal(ext, cand, seats.index_select(0, missing))
+        f, l, _, _, _ = ext.observe_indexed(cand, torch.arange(missing.numel(), device=DEV))
+        of = missing % rows
+        same = (f == f_real.index_select(0, of)).all(1) & (l == l_real.index_select(0, of)).all(1)
+        out.index_copy_(0, missing[same], cand[same])
+        missing = missing[~same]
+    return out
+
+
+def test_accept_worlds_edges(ext):
+    """accept_worlds: an empty try; a row index outside `out` is neither written nor kept;
+    a candidate differing in one feature or one legal bit is not kept."""
+    announce("accept_worlds edges")
+    states, player = _mid_game_rows(ext, 64, 0x78)
+    r = states.shape[0]
+    f, l, _, _, _ = ext.observe_indexed(states, torch.arange(r, device=DEV))
+    out = torch.zeros_like(states)
+    empty = ext.accept_worlds(f[:0], l[:0], f, l, torch.zeros(0, dtype=torch.int64, device=DEV),
+                              states[:0], out)
+    assert empty.shape == (0,) and not bool(out.any())
+    missing = torch.arange(r, device=DEV)
+    missing[0] = r + 5   # outside out
+    f2, l2 = f.clone(), l.clone()
+    f2[1, 7] += 1.0
+    l2[2, 3] = ~l2[2, 3]
+    same = ext.accept_worlds(f2, l2, f, l, missing, states, out)
+    want = torch.ones(r, dtype=torch.bool, device=DEV)
+    want[:3] = False
+    assert torch.equal(same, want)
+    assert not bool(out[:3].any()) and torch.equal(out[3:], states[3:])
