@@ -484,7 +484,10 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   const i64 w = wave.w;
   if (i >= w) return;
   if (i == 0 && lane == 0 && wave.playing != nullptr) wave.playing[0] = 0;  // advance sets it
-  const i64 step = wave.step_index[0];
+  // this step's index: the one advance left in step_index[1], kept in step_index[0] for
+  // advance (no thread here reads [0], none in advance writes it)
+  const i64 step = wave.step_index[1];
+  if (i == 0 && lane == 0) wave.step_index[0] = step;
   const bool record = step >= 0 && step < wave.max_steps;
   const i64 rec = step * w + i;
   const float* f = features + i * kFeatures;
@@ -589,6 +592,7 @@ __global__ __launch_bounds__(256) void advance_kernel(
     wave.count[i] = c + 1;
   }
   const i64 step = wave.step_index[0];
+  if (i == 0) wave.step_index[1] = step + 1;  // the next step's (no thread here reads [1])
   if (step >= 0 && step < wave.max_steps) {
     wave.rec_actions[step * w + i] = actions[i];
     wave.rec_logp[step * w + i] = logp[i];

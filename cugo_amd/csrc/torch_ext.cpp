@@ -1602,7 +1602,7 @@ class SelfPlayState {
                   " has the wrong dtype or shape");
     };
     const int64_t s = max_steps;
-    want(step_index, at::kLong, {1}, "step_index");
+    want(step_index, at::kLong, {2}, "step_index");
     want(count, at::kLong, {w}, "count");
     want(events, at::kLong, {w, 48, CUGO_EVENT_WORDS}, "events");
     want(cache_length, at::kLong, {2 * w}, "cache length");

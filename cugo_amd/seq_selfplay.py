@@ -241,7 +241,7 @@ class _WaveTensors:
             "start": ((w, START_WORDS), i64), "learner_seat": ((w,), i64),
             "rec_features": ((steps, w, width), torch.bfloat16),
             "rec_legal": ((steps, w, ACTIONS), b), "rec_logp": ((steps, w), f32),
-            "rec_valid": ((steps, w), b), "step_index": ((1,), i64),
+            "rec_valid": ((steps, w), b), "step_index": ((2,), i64),
             "final_reward0": ((w,), f32), "final_nagari": ((w,), b), "finished": ((w,), b),
             "started": ((w,), b), "bad": ((), i64),
         }
@@ -409,8 +409,7 @@ class SelfPlayWave:
             opp.cached_step(self.opp_cache,
                             opp.event_token(events[:p], 1 - t.learner_seat[:p], t.count[:p]))
         native.advance(done, reward0, new_done, nagari, step_status, committed, events, actions,
-                       logp)
-        t.step_index += 1
+                       logp)  # and the step counter (step_index[1])
 
     @torch.no_grad()
     def flush(self) -> None:

@@ -535,7 +535,9 @@ typedef struct CugoSelfPlayWave {
   const int64_t* learner_seat;    /* [w]: the learner's seat (read for pool games) */
   int64_t* opp_cache_length;      /* [max(1, pool_games)]: the opponent's cache lengths
                                      (NULL without a pool) */
-  const int64_t* step_index;      /* [1]: the step being recorded */
+  int64_t* step_index;            /* [2]: [0] the step being recorded (prepare copies [1]
+                                     into it), [1] the next one (advance writes [0] + 1);
+                                     both 0 at a wave's start */
   int64_t* count;                 /* [w]: events committed so far */
   int64_t* events;                /* [w, 48, 9]: event log */
   int64_t* cache_length;          /* [2 w]: KV-cache lengths, row = seat * w + game */
