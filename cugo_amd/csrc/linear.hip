@@ -953,7 +953,7 @@ static int ffn_check(const void* h, int64_t ldh, const void* x, const void* w1_p
                      const void* b1, const void* w2_packed, const void* b2, const void* ln_weight,
                      const void* ln_bias, int64_t m, const void* x_out, const void* ln) {
   if (m < 0 || (m > 0 && (!h || !x || !w1_packed || !b1 || !w2_packed || !b2 || !x_out)) ||
-      (ln_weight == nullptr) != (ln_bias == nullptr) || (ln_weight != nullptr && !ln))
+      (ln_weight == nullptr) != (ln_bias == nullptr) || (m > 0 && ln_weight != nullptr && !ln))
     return -1;
   if (ldh < 256 || ldh % 8 != 0) return -3;
   const uintptr_t p16 = reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(w1_packed) |

@@ -335,7 +335,7 @@ def test_linear_add_layernorm_equals_its_two_launches(ext, m, k):
                                          None, res, norm.weight, norm.bias, norm.eps)
 
 
-@pytest.mark.parametrize("m", [1, 37, 4096 + 5, 12288])
+@pytest.mark.parametrize("m", [0, 1, 37, 4096 + 5, 12288])
 def test_ffn_equals_its_two_launches(ext, m):
     """ffn (linear1 + GELU + linear2 + residual add + next LayerNorm in one launch) ==
     linear(gelu=True) then linear_add_layernorm, bit for bit (x_out and ln), on every row
@@ -386,7 +386,7 @@ def test_ffn_equals_its_two_launches(ext, m):
         assert torch.equal(feed_forward(layer, h, x), want_plain)
 
 
-@pytest.mark.parametrize("m", [1, 37, 4096 + 5, 12288, 16384])
+@pytest.mark.parametrize("m", [0, 1, 37, 4096 + 5, 12288, 16384])
 def test_out_proj_ffn_equals_its_launches(ext, m):
     """out_proj_ffn (out_proj + residual add + norm2, then the feed-forward, one launch) ==
     linear_add_layernorm (out_proj, norm2) then ffn, bit for bit (x_out and ln), on every
