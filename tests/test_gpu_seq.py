@@ -806,3 +806,44 @@ def test_selfplay_collect_with_pool(ext):
     assert int(out["log"]["count"].max()) <= 48
     w_t = wave.opponent._weight_t("event_in")
     assert torch.equal(w_t, other["event_in.weight"].t().to(w_t.dtype))
+
+
+def test_empty_batches_of_the_step_ops(ext):
+    """Every operation of the sequence policy's step and of the paired evaluation takes a
+    batch of no rows: no error, empty outputs of the right shape, nothing written."""
+    announce("empty batches")
+    bf, i64, u8 = torch.bfloat16, torch.int64, torch.bool
+    z = lambda *shape, dtype=bf: torch.zeros(shape, dtype=dtype, device=DEV)  # noqa: E731
+    w = (torch.randn(256, 256) * 0.05).to(bf).to(DEV)
+    wp = ext.mlp_pack_weight(w, 256, 256)
+    w179 = ext.mlp_pack_weight(w[:179].contiguous(), 192, 256)
+    b, ones = z(256), torch.ones(256, dtype=bf, device=DEV)
+    x = z(0, 256)
+    assert ext.linear(x, wp, 256, b, True).shape == (0, 256)
+    assert ext.linear(x, wp, 256, b, residual=z(0, 256)).shape == (0, 256)
+    assert ext.linear(x, w179, 179, b[:179]).shape == (0, 179)
+    xo, ln = ext.linear_add_layernorm(x, wp, b, z(0, 256), ones, b, 1e-5)
+    assert xo.shape == (0, 256) and ln.shape == (0, 256)
+    xo, ln = ext.linear_add_layernorm(x, wp, b, b, ones, b, 1e-5)  # one residual row for all
+    assert xo.shape == (0, 256) and ln.shape == (0, 256)
+    assert ext.add_layernorm(x, x, ones, b, 1e-5)[1].shape == (0, 256)
+    pos = torch.zeros(0, dtype=i64, device=DEV)
+    keys, values = z(4, 8, 16, 32), z(4, 8, 16, 32)
+    q = z(0, 8, 32)
+    assert ext.decode_attention_append(q, q, q, keys, values, pos).shape == (0, 8, 32)
+    ext.kv_append(q, q, keys, values, pos)
+    assert not bool(keys.any()) and not bool(values.any())
+    logits, legal = z(0, 179), z(0, 179, dtype=u8)
+    assert ext.masked_argmax(logits, legal).shape == (0,)
+    acts, logp = ext.gumbel_sample(logits.float(), legal, z(0, 179, dtype=torch.float32))
+    assert acts.shape == (0,) and logp.shape == (0,)
+    epoch = torch.zeros(1, dtype=i64, device=DEV)
+    acts, logp = ext.gumbel_sample_philox(logits, legal, 7, epoch, 0)
+    assert acts.shape == (0,) and logp.shape == (0,)
+    q_in = z(0, 1024)
+    ext.query_input(z(0, 720, dtype=torch.float32), legal, None, q_in)
+    wt = (torch.randn(274, 256) * 0.05).to(bf).to(DEV)
+    assert ext.start_tokens(z(0, 8, dtype=i64), pos, wt, b, z(49, 256), z(3, 256)).shape == (0, 256)
+    ext.paired_movers(z(0, dtype=torch.uint8), pos, pos)
+    flags = z(0, dtype=u8)
+    ext.paired_events(flags, z(0, dtype=torch.int16), flags, flags, pos, pos, pos, pos)
