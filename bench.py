@@ -1295,10 +1295,10 @@ def store_ceiling(torch, ext=None) -> dict:
 
 @contextlib.contextmanager
 def tuned_gemms(torch, enabled: bool):
-    """PyTorch-ROCm TunableOp for the legs whose eager warm-up runs every GEMM shape they
-    then capture into a HIP graph (self-play, rollout): each shape's first call times the
-    library's solutions (about 2 s in all) and the graph keeps the fastest.  Its results
-    file goes to the temporary directory."""
+    """PyTorch-ROCm TunableOp for a leg whose eager warm-up runs every library GEMM shape
+    it then captures into a HIP graph (the rollout leg's layer-by-layer baseline): each
+    shape's first call times the library's solutions and the graph keeps the fastest.
+    Its results file goes to the temporary directory."""
     tunable = torch.cuda.tunable
     if enabled:
         tunable.set_filename(os.path.join(os.environ.get("TMPDIR", "/tmp"),
@@ -1394,8 +1394,9 @@ def main() -> None:
                    "streams": args.streams, "hip_graph": not args.no_graph,
                    "spare_slots": SPARE_SLOTS,
                    "gemm_selection": ("hipBLASLt heuristics" if args.no_tunable else
-                                      "PyTorch-ROCm TunableOp for the self-play and "
-                                      "rollout legs")},
+                                      "PyTorch-ROCm TunableOp for the rollout leg's "
+                                      "layer-by-layer baseline (the self-play and decode "
+                                      "legs' layers run on this build's kernels)")},
         "kernel_ms_per_step": (round(rp["play_ms"] / REFILL, 4)
                                if rp["play_ms"] is not None else None),
         "steps_per_s": round(args.batch * args.steps / rp["seconds"], 1),
@@ -1412,8 +1413,7 @@ def main() -> None:
     if not args.no_decode:
         result["decode"] = decode_workload(ext, torch, args.decode_steps)
     if not args.no_selfplay:
-        with tuned_gemms(torch, not args.no_tunable):
-            result["selfplay"] = selfplay_workload(ext, torch)
+        result["selfplay"] = selfplay_workload(ext, torch)
     if not args.no_redeal:
         result["redeal"] = redeal_workload(ext, torch)
     if not args.no_paired:
