@@ -25,6 +25,7 @@
 #include <initializer_list>
 
 #include "../../include/cugo_hip.h"
+#include "engine.h"
 
 namespace cugo_amd {
 namespace tokens {
@@ -49,6 +50,12 @@ struct BF16 {
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
   }
   __device__ static float round(float f) { return to_float(from_float(f)); }
+  // 4 consecutive values (p 8-byte aligned)
+  __device__ static void store4(uint16_t* p, float4 x) {
+    *reinterpret_cast<uint2*>(p) =
+        make_uint2((uint32_t)from_float(x.x) | ((uint32_t)from_float(x.y) << 16),
+                   (uint32_t)from_float(x.z) | ((uint32_t)from_float(x.w) << 16));
+  }
 };
 
 struct F32 {
@@ -56,6 +63,7 @@ struct F32 {
   __device__ static float to_float(float x) { return x; }
   __device__ static float from_float(float f) { return f; }
   __device__ static float round(float f) { return f; }
+  __device__ static void store4(float* p, float4 x) { *reinterpret_cast<float4*>(p) = x; }
 };
 
 __device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -495,10 +503,25 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   const int q_stride = wave.q_stride > 0 ? (int)wave.q_stride : width + kActions;
   typename T::storage* q = q_in + i * q_stride;
   for (int j = width + kActions + lane; j < q_stride; j += 64) q[j] = T::from_float(0.0f);
-  for (int j = lane; j < width; j += 64) {
-    const float x = f[wave.columns != nullptr ? wave.columns[j] : j];
-    q[j] = T::from_float(x);
-    if (record) wave.rec_features[rec * width + j] = BF16::from_float(x);
+  const bool by4 = wave.columns == nullptr && wave.q_stride > 0 && wave.q_stride % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(q_in) | reinterpret_cast<uintptr_t>(features)) &
+                    15u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(wave.rec_features) & 7u) == 0;
+  if (by4) {
+    // every column in order, 4-element aligned rows: a lane converts 4 features at a time
+    // (one 16-byte load, 8- or 16-byte stores; width = 720 is a multiple of 4)
+    const float4* f4 = reinterpret_cast<const float4*>(f);
+    for (int j = lane; j < kFeatures / 4; j += 64) {
+      const float4 x = f4[j];
+      T::store4(q + 4 * j, x);
+      if (record) BF16::store4(wave.rec_features + rec * width + 4 * j, x);
+    }
+  } else {
+    for (int j = lane; j < width; j += 64) {
+      const float x = f[wave.columns != nullptr ? wave.columns[j] : j];
+      q[j] = T::from_float(x);
+      if (record) wave.rec_features[rec * width + j] = BF16::from_float(x);
+    }
   }
   const uint8_t* g = legal + i * kActions;
   bool any = false;
@@ -521,7 +544,14 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void prepare_kernel(
   wave.rec_seat[rec] = p;
   wave.rec_count[rec] = wave.count[i];
   wave.rec_opp_hand[rec] = (i64)states[i * kRowWords + (1 - p)];
-  wave.rec_stock[rec] = stock[i];
+  if (stock != nullptr) {
+    wave.rec_stock[rec] = stock[i];
+  } else {  // stock_indexed's value, from the row in hand (kernels.hip stock_kernel)
+    Env e;
+    e.stock = states[i * kRowWords + 3];
+    e.rng = states[i * kRowWords + 6];
+    wave.rec_stock[rec] = (i64)peek_stock(e);
+  }
   wave.rec_stop_points[rec] = (i64)rintf(exp2f(12.0f * f[kStopPointsColumn]) - 1.0f);
   // a pool game's decision belongs to the learner only when the learner's seat moves
   wave.rec_valid[rec] = active && (i >= wave.pool_games || p == wave.learner_seat[i]);
@@ -934,7 +964,7 @@ int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8
       (wave->q_stride != 0 && wave->q_stride < wave->width + kActions))
     return -1;
   const int64_t w = wave->w;
-  if (w > 0 && (!states || !features || !legal || !player || !done || !status || !stock ||
+  if (w > 0 && (!states || !features || !legal || !player || !done || !status ||
                 !q_in || !query_rows || !wave->step_index || !wave->count || !wave->bad ||
                 !wave->rec_features || !wave->rec_legal || !wave->rec_opp_hand ||
                 !wave->rec_stock || !wave->rec_stop_points || !wave->rec_seat ||

@@ -1652,8 +1652,8 @@ class SelfPlayState {
   std::vector<torch::Tensor> prepare(torch::Tensor states, torch::Tensor features,
                                      torch::Tensor legal, torch::Tensor player,
                                      torch::Tensor done, torch::Tensor status,
-                                     torch::Tensor stock, at::ScalarType q_dtype,
-                                     int64_t q_stride) {
+                                     c10::optional<torch::Tensor> stock,
+                                     at::ScalarType q_dtype, int64_t q_stride) {
     const int64_t w = c_.w;
     check_states(states);
     TORCH_CHECK(states.size(0) == w, "states must hold the wave's w rows");
@@ -1664,13 +1664,16 @@ class SelfPlayState {
                     legal.sizes() == torch::IntArrayRef({w, CUGO_ACTION_COUNT}),
                 "legal must be bool [w, ACTION_COUNT]");
     TORCH_CHECK(player.numel() == w && done.numel() == w && status.numel() == w &&
-                    stock.numel() == w && player.scalar_type() == at::kByte &&
-                    done.scalar_type() == at::kBool && status.scalar_type() == at::kShort &&
-                    stock.scalar_type() == at::kLong,
-                "player/done/status/stock must be observe's and stock_indexed's [w] outputs");
+                    player.scalar_type() == at::kByte && done.scalar_type() == at::kBool &&
+                    status.scalar_type() == at::kShort,
+                "player/done/status must be observe's [w] outputs");
+    TORCH_CHECK(!stock.has_value() ||
+                    (stock->numel() == w && stock->scalar_type() == at::kLong &&
+                     stock->is_contiguous() && stock->device() == keep_[0].device()),
+                "stock must be stock_indexed's [w] output");
     TORCH_CHECK(q_dtype == at::kBFloat16 || q_dtype == at::kFloat,
                 "the query dtype must be bfloat16 or float32");
-    for (const auto* t : {&states, &features, &legal, &player, &done, &status, &stock})
+    for (const auto* t : {&states, &features, &legal, &player, &done, &status})
       TORCH_CHECK(t->device() == keep_[0].device(), "inputs must be on the wave's device");
     const DeviceGuard guard(states.device());
     TORCH_CHECK(q_stride == 0 || q_stride >= c_.width + CUGO_ACTION_COUNT,
@@ -1684,7 +1687,8 @@ class SelfPlayState {
     check_call(cugo_selfplay_prepare(&c_, q_dtype == at::kBFloat16 ? CUGO_DTYPE_BF16 : CUGO_DTYPE_F32,
                                      u8p(states), features.data_ptr<float>(), u8p(legal),
                                      u8p(player), u8p(done), status.data_ptr<int16_t>(),
-                                     stock.data_ptr<int64_t>(), q_in.data_ptr(),
+                                     stock.has_value() ? stock->data_ptr<int64_t>() : nullptr,
+                                     q_in.data_ptr(),
                                      rows.data_ptr<int64_t>(), stream()),
                "selfplay_prepare");
     return {q_in, rows, pos};

@@ -378,9 +378,9 @@ class SelfPlayWave:
         pool = pool and self.p > 0
         native = self.native[pool]
         features, legal, players, done, status = ext.observe_indexed(self.states, self.ids)
-        stock = ext.stock_indexed(self.states, self.ids)
+        # stock None: prepare records stock_indexed's words from the state rows itself
         q_in, query_rows, query_pos = native.prepare(self.states, features, legal, players, done,
-                                                     status, stock, actor.event_in.weight.dtype,
+                                                     status, None, actor.event_in.weight.dtype,
                                                      self.q_stride)
         # the last step's event tokens (both seats' rows) and this step's queries through
         # the layers together; the queries attend the events' new keys at every layer

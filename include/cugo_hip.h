@@ -584,7 +584,8 @@ typedef struct CugoSelfPlayWave {
  * valid = active and the learner moves (a pool game's mover may be the opponent);
  * query_rows [w] = (player & 1) * w + game.  states [w, 248] (row = game), features
  * f32 [w, 720], legal bool [w, 179], player/done [w], status i16 [w] (observe outputs),
- * stock int64 [w] (stock_indexed before the step). */
+ * stock int64 [w] (stock_indexed before the step), or NULL: the same words taken from the
+ * state rows here (no stock_indexed launch). */
 int cugo_selfplay_prepare(const CugoSelfPlayWave* wave, int q_dtype, const uint8_t* states,
                           const float* features, const uint8_t* legal, const uint8_t* player,
                           const uint8_t* done, const int16_t* status, const int64_t* stock,
