@@ -712,6 +712,37 @@ def test_selfplay_step_matches_reference_formulation(ext, mode, pool):
         assert max(errs) <= 2e-2, errs
 
 
+def test_prepare_reads_the_stock_words_itself(ext):
+    """SelfPlayState.prepare with stock None (the self-play step's form) records the words
+    stock_indexed gives for the same rows, and writes the same query input, rows and slots
+    as with stock_indexed's tensor passed in."""
+    announce("selfplay prepare: stock words from the state rows")
+    from cugo_amd.seq_selfplay import SelfPlayWave, make_seeds
+
+    policy = _policy()
+    w = 300
+    wave = SelfPlayWave(ext, policy, w, max_steps=8)
+    seeds, first = make_seeds(w, 77, DEV)
+    with torch.no_grad():
+        wave.reset(seeds, first, torch.zeros(w, dtype=torch.int64, device=DEV))
+        # a few steps in, so the stock and its draws differ from the deal's
+        for _ in range(3):
+            wave.step()
+        step = int(wave.step_index[1])
+        native = wave.native[False]
+        obs = ext.observe_indexed(wave.states, wave.ids)
+        stock = ext.stock_indexed(wave.states, wave.ids)
+        dt = policy.event_in.weight.dtype
+        given = native.prepare(wave.states, *obs, stock, dt, wave.q_stride)
+        rec_given = wave.rec_long["stock"][step].clone()
+        wave.rec_long["stock"][step].zero_()
+        read = native.prepare(wave.states, *obs, None, dt, wave.q_stride)
+        rec_read = wave.rec_long["stock"][step].clone()
+    assert torch.equal(rec_given, stock) and torch.equal(rec_read, stock)
+    for x, y in zip(given, read):
+        assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize("pool", [False, True])
 def test_selfplay_graph_replays_equal_eager_steps(ext, pool):
     """Replays of the captured step == eager step() calls from the same start (same
