@@ -421,8 +421,9 @@ int launch_parts(const void* q, void* keys, void* values, const void* k_new, con
 // up to ~50 slots run 2-2.5x faster with 8 heads per wavefront than with one (fewer
 // wavefronts, each with all its loads in flight), and on a 320-slot cache 8 beats 2 both
 // for one game's rows (mean 20 slots: 18.5 against 23.5 us) and for full rows (mean 297:
-// 219 against 223 us).  So: up to 8, whatever the capacity (a grouping must divide
-// `heads` and fit G * L <= 64 lanes).
+// 219 against 223 us), and 4 loses to 8 on every set (one game a row 0.42 of HBM against
+// 0.49, full rows 0.73 against 0.75, the self-play step 0.459 against 0.428 ms).  So: up
+// to 8, whatever the capacity (a grouping must divide `heads` and fit G * L <= 64 lanes).
 template <int L>
 int pick_group(int64_t heads, int64_t slots) {
 #ifdef CUGO_DECODE_FORCE_GROUP
